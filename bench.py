@@ -1,0 +1,338 @@
+"""Decode-attention layer-step benchmark on one MI355X.
+
+A step is one decode step over every layer of the configuration.  Per layer it runs:
+- quantize-on-append of the new token's K/V (one HIP launch);
+- split-K quantized decode attention plus combine over the whole context.
+
+Caches are seeded synthetic data of the configured shape, one distinct cache per
+layer, built on the GPU with the same HIP append kernel.  Each step rewrites the
+last slot and attends over the full context, so every step does identical work.
+
+The timed region replays a HIP graph of W warm-up and then K timed steps, bracketed
+by hipEvents on the launch stream.  ``value`` is the mean microseconds per
+layer-step (append + attention).  The line also carries:
+- ``roofline``: algorithmic bytes of the attention kernel / its measured time;
+- ``cpu_baseline``: the CPU oracle (the reference's torch path restated) timed on a
+  bounded sample on this host's cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--chunk", type=int, default=0)
+    ap.add_argument("--layers", type=int, default=0, help="override the layer count (debug only)")
+    return ap.parse_args()
+
+
+def algorithmic_bytes(cfg, ctx_list):
+    """Bytes one layer-step must move: codes (+ fp16 outlier channels / per-token
+    scales the format stores) for every context token, plus q in and out."""
+    tok = sum(int(c) for c in ctx_list)
+    per_tok_head = 0
+    per_tok_head += 128 if cfg.k_format == "int8" else 64
+    per_tok_head += 128 if cfg.v_format == "int8" else 64
+    if cfg.outlier_channels:
+        per_tok_head += 4 * 2
+    return tok * cfg.kv_heads * per_tok_head + 2 * cfg.batch * cfg.q_heads * 128 * 2
+
+
+class Layer:
+    """Device buffers and prepared C-ABI calls of one layer."""
+
+    def __init__(self, cfg, layer, device, ctx, gen, chunk):
+        from llm_kvcache_quantization_amd import _capi as C
+        from llm_kvcache_quantization_amd import synthetic as SY
+        from llm_kvcache_quantization_amd.kernels import DecodePlan, kv_view_static, kv_view_tok
+
+        self.C = C
+        B, Hkv, Hq = cfg.batch, cfg.kv_heads, cfg.q_heads
+        cap = int(max(ctx))
+        t = SY.calibrate(cfg, layer)
+        self.tables = t
+        ch = SY.outlier_channels(cfg, layer)
+        kb = 128 if cfg.k_format == "int8" else 64
+        vb = 128 if cfg.v_format == "int8" else 64
+        self.k = torch.empty(B, Hkv, cap, kb, dtype=torch.uint8, device=device)
+        self.v = torch.empty(B, Hkv, cap, vb, dtype=torch.uint8, device=device)
+        self.ko = None
+        dev = lambda x: None if x is None else x.to(device)
+        self.ks, self.kz = dev(t.k_scale), dev(t.k_zp)
+        self.vs, self.vz = dev(t.v_scale), dev(t.v_zp)
+        self.oidx = dev(t.k_outlier_idx)
+        if cfg.outlier_channels:
+            self.ko = torch.empty(B, Hkv, cap, 4, dtype=torch.float16, device=device)
+        self.ctx = torch.tensor(ctx, dtype=torch.int32, device=device)
+        self.q = SY.draw_q(cfg, B, gen, device=device)
+        self.inv_tau = SY.inv_tau(cfg)[layer].to(device)
+        # prefill: every slot [0, cap) gets quantized seeded data (chunks bound the temporaries)
+        step = 8192
+        for s0 in range(0, cap, step):
+            n = min(step, cap - s0)
+            kx, vx = SY.draw_kv(cfg, layer, B, n, gen, device=device, ch=ch)
+            pk, pv = self._append_params(cfg, kx, vx, s0)
+            C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
+                                             ctypes.c_void_p(C.stream_handle(torch.device(device)))))
+            del kx, vx
+        # the decode-step token: rewrites slot cap-1 of every sequence each step
+        self.k_new, self.v_new = SY.draw_kv(cfg, layer, B, 1, gen, device=device, ch=ch)
+        self.step_slot = cap - 1
+        self.pk, self.pv = self._append_params(cfg, self.k_new, self.v_new, self.step_slot)
+        self._pk, self._pv = ctypes.byref(self.pk), ctypes.byref(self.pv)
+        ks_view = None
+        if cfg.k_format == "int8":
+            self.ks_tok = self.ks.clamp(min=1e-5).to(torch.float16)[None, :, None, :].expand(B, Hkv, cap, 4)
+            kview = kv_view_tok(self.k, self.ks_tok)
+            kfmt = C.KVQ_FMT_INT8_SYM
+        else:
+            kview = kv_view_static(self.k, self.ks, self.kz, self.oidx, self.ko)
+            kfmt = C.KVQ_FMT_INT4_ASYM
+        if cfg.v_format == "int8":
+            self.vs_tok = self.vs.clamp(min=1e-5).to(torch.float16)[None, :, None, :].expand(B, Hkv, cap, 4)
+            vview = kv_view_tok(self.v, self.vs_tok)
+            vfmt = C.KVQ_FMT_INT8_SYM
+        else:
+            vview = kv_view_static(self.v, self.vs, self.vz)
+            vfmt = C.KVQ_FMT_INT4_ASYM
+        del ks_view
+        self.plan = DecodePlan(self.q, kfmt, kview, vfmt, vview, self.ctx, Hkv, cap,
+                               1.0 / math.sqrt(128), 32, inv_tau=self.inv_tau, chunk_tokens=chunk)
+
+    def _append_params(self, cfg, kx, vx, pos):
+        C = self.C
+        out = []
+        for x, codes, fmt, s, z, side in ((kx, self.k, cfg.k_format, self.ks, self.kz, "k"),
+                                          (vx, self.v, cfg.v_format, self.vs, self.vz, "v")):
+            p = C.AppendParams()
+            B, H, S, D = x.shape
+            p.format = C.KVQ_FMT_INT8_SYM if fmt == "int8" else C.KVQ_FMT_INT4_ASYM
+            p.x = x.data_ptr()
+            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride(0), x.stride(1), x.stride(2)
+            p.batch, p.heads, p.seq_new, p.head_dim, p.group_size = B, H, S, D, 32
+            p.static_scale = s.data_ptr()
+            p.static_scale_dtype = C.KVQ_DTYPE_F16
+            p.static_stride_h, p.static_stride_g = s.stride()
+            if z is not None:
+                p.static_zp = z.data_ptr()
+            p.codes = codes.data_ptr()
+            p.codes_stride_b, p.codes_stride_h, p.codes_stride_t = codes.stride(0), codes.stride(1), codes.stride(2)
+            p.write_pos = pos
+            p.capacity = codes.shape[2]
+            if side == "k" and self.ko is not None:
+                p.n_outlier = 4
+                p.outlier_idx = self.oidx.data_ptr()
+                p.outlier_out = self.ko.data_ptr()
+                p.oo_stride_b, p.oo_stride_h, p.oo_stride_t = self.ko.stride(0), self.ko.stride(1), self.ko.stride(2)
+            p._keep = (x,)
+            out.append(p)
+        return out
+
+    def append(self, stream):
+        self.C.check(self.C.lib().kvq_quant_append(self._pk, self._pv, ctypes.c_void_p(stream)))
+
+    def attend(self, stream):
+        self.plan.launch(stream)
+
+
+def time_region(fn, stream, steps, warmup, use_graph):
+    """Mean ms per call of fn(stream) over `steps` calls, timed with HIP events."""
+    s = torch.cuda.current_stream()
+    for _ in range(2):
+        fn(s.cuda_stream)
+    torch.cuda.synchronize()
+    graph = None
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn(torch.cuda.current_stream().cuda_stream)
+        run = graph.replay
+    else:
+        run = lambda: fn(s.cuda_stream)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, graph
+
+
+def cpu_baseline(cfg, layers_dev):
+    """The CPU oracle (reference torch path) on a bounded sample of the workload:
+    one layer, `rows` batch rows at the full context, quantize-on-append of one token
+    + fp16-dequant fp32 attention; scaled to microseconds per layer-step."""
+    from oracle import attn as OA
+    from oracle import quant as OQ
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    L0 = layers_dev[0]
+    rows = 1
+    sl = slice(0, rows)
+    t = L0.tables
+    ctx = L0.ctx[sl].cpu()
+    q = L0.q[sl].cpu()
+    tau = L0.inv_tau.cpu()
+    k_new, v_new = L0.k_new[sl].cpu(), L0.v_new[sl].cpu()
+    if cfg.k_format == "int8":
+        kc = L0.k[sl].cpu().view(torch.int8)
+        ks = L0.ks_tok[sl].cpu()
+    else:
+        kc = L0.k[sl].cpu()
+        ko = L0.ko[sl].cpu() if L0.ko is not None else None
+    vc = L0.v[sl].cpu() if cfg.v_format != "int8" else L0.v[sl].cpu().view(torch.int8)
+
+    def one():
+        if cfg.k_format == "int8":
+            OQ.quantize_symmetric_int8_with_scale(k_new, t.k_scale, 32)
+        else:
+            OQ.quantize_asymmetric_static(k_new, t.k_scale, t.k_zp)
+        if cfg.v_format == "int8":
+            OQ.quantize_symmetric_int8_with_scale(v_new, t.v_scale, 32)
+            return OA.decode_attn_int8_torch_ref(OA.prescale_q(q, tau), kc, vc, ks, L0.vs_tok[sl].cpu(),
+                                                 ctx, 1 / math.sqrt(128))
+        OQ.quantize_asymmetric_static(v_new, t.v_scale, t.v_zp)
+        if cfg.k_format == "int8":
+            return OA.decode_attn_k8v4_ref(q, kc, ks, vc, t.v_scale, t.v_zp, ctx, 1 / math.sqrt(128), inv_tau=tau)
+        return OA.decode_attn_asym_ref(q, kc, vc, t.k_scale, t.k_zp, t.v_scale, t.v_zp, ctx,
+                                       1 / math.sqrt(128), inv_tau=tau, k_outlier_idx=t.k_outlier_idx,
+                                       k_outlier_val=ko)
+
+    one()  # warm-up
+    times = []
+    budget = 20.0
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < budget or len(times) < 2:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    us_per_layer_step = med * 1e6 * (cfg.batch / rows)
+    return {
+        "value": round(us_per_layer_step, 1),
+        "unit": "us/layer-step",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle (reference torch path restated, fp16 dequant + fp32 softmax) on "
+                   f"{rows} of {cfg.batch} batch rows of layer 0 at full context, median of "
+                   f"{len(times)} runs, scaled x{cfg.batch // rows} to the full layer-step; "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the decode path is "
+                          "measured on one MI355X (see DESIGN.md for how it would shard)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    from llm_kvcache_quantization_amd import _capi as C
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    C.lib()
+    cfg = SY.CONFIGS[args.config]
+    nl = args.layers or cfg.layers
+    device = "cuda:0"
+    torch.cuda.set_device(0)
+    ctx = SY.context_lengths(cfg).tolist()
+    gen = torch.Generator(device=device).manual_seed(SY.seed_for(cfg.index, 0))
+    print(f"[bench] building {nl} layer caches for config {cfg.index} ({cfg.name})", file=sys.stderr, flush=True)
+    t0 = time.time()
+    layers = [Layer(cfg, l, device, ctx, gen, args.chunk) for l in range(nl)]
+    torch.cuda.synchronize()
+    print(f"[bench] caches ready in {time.time() - t0:.1f}s; chunk={layers[0].plan.chunk_tokens}",
+          file=sys.stderr, flush=True)
+
+    use_graph = not args.no_graph
+    step_fn = lambda s: [(L.append(s), L.attend(s)) for L in layers]
+    attn_fn = lambda s: [L.attend(s) for L in layers]
+    app_fn = lambda s: [L.append(s) for L in layers]
+    ms_step, g_step = time_region(step_fn, None, args.steps, args.warmup, use_graph)
+    ms_attn, _ = time_region(attn_fn, None, args.steps, args.warmup, use_graph)
+    ms_app, _ = time_region(app_fn, None, args.steps, args.warmup, use_graph)
+    us_layer = ms_step * 1000.0 / nl
+    us_attn = ms_attn * 1000.0 / nl
+    us_app = ms_app * 1000.0 / nl
+    nbytes = algorithmic_bytes(cfg, ctx)
+    achieved = nbytes / (us_attn * 1e-6) / 1e9
+    print(f"[bench] step {ms_step:.3f} ms = {us_layer:.2f} us/layer-step "
+          f"(attention {us_attn:.2f} us, append {us_app:.2f} us); attention {achieved:.0f} GB/s",
+          file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(cfg, layers)
+    line = {
+        "metric": "decode-attn us/layer-step (append + split-K attention) + achieved HBM GB/s",
+        "value": round(us_layer, 3),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (int4/int8 codes)",
+        "data": "synthetic (seeded; distinct cache per layer)",
+        "config": {
+            "workload": cfg.name,
+            "config_index": cfg.index,
+            "batch": cfg.batch,
+            "q_heads": cfg.q_heads,
+            "kv_heads": cfg.kv_heads,
+            "layers": nl,
+            "context": ctx,
+            "kv_format": f"K {cfg.k_format} / V {cfg.v_format} g32"
+                         + (" + 4 fp16 K channels" if cfg.outlier_channels else ""),
+            "chunk_tokens": layers[0].plan.chunk_tokens,
+            "hip_graph": use_graph,
+        },
+        "attention_us_per_layer_step": round(us_attn, 3),
+        "append_us_per_layer_step": round(us_app, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": nbytes,
+            "kernel": "decode_splitk_kernel + combine_kernel (per layer)",
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,165 @@
+/*
+ * kvq.h -- C ABI of the MI355X (gfx950) quantized-KV decode path.
+ *
+ * libkvq.so exports three groups of entry points: quantize-on-append, split-K
+ * decode attention and error reporting.  Every entry point
+ *   - takes plain device pointers, sizes and strides (no framework types);
+ *   - never allocates, never synchronises, and enqueues its work on the
+ *     hipStream_t it is given;
+ *   - returns KVQ_OK or a KVQ_ERR_* code.  kvq_last_error() then returns a
+ *     message for the calling thread.
+ *
+ * The reference (zilangchen/LLM_KVCache_Quantization) has no C/C++ layer.  Its
+ * path is PyTorch + Triton.  Each entry point below names the reference Python
+ * interface it replaces.  The Python mirror in
+ * llm_kvcache_quantization_amd/ keeps those interfaces' names, arguments and
+ * exceptions, and calls this ABI through ctypes.
+ */
+#ifndef KVQ_H_
+#define KVQ_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* kvq_stream_t; /* == hipStream_t */
+
+/* status codes */
+#define KVQ_OK 0
+#define KVQ_ERR_INVALID 1     /* bad argument: shape, stride, size or null pointer */
+#define KVQ_ERR_UNSUPPORTED 2 /* valid request outside what this build implements */
+#define KVQ_ERR_LAUNCH 3      /* HIP reported an error when the kernel was enqueued */
+
+/* element dtypes for scales */
+#define KVQ_DTYPE_F16 0
+#define KVQ_DTYPE_F32 1
+
+/* KV cache formats (one per K and one per V) */
+#define KVQ_FMT_INT8_SYM 1  /* int8 codes [..., D]; fp16/fp32 scale per (token, group) */
+#define KVQ_FMT_INT4_SYM 2  /* packed nibbles [..., D/2], byte = ((c[2i]+8)<<4)|(c[2i+1]+8),
+                               codes in [-7,7]; fp16/fp32 scale per (token, group) */
+#define KVQ_FMT_INT4_ASYM 3 /* packed nibbles as above, codes in [-8,7]; static fp16 scale
+                               and zero-point per (kv head, group of 32); optional fp16
+                               side-band holding n_outlier channels per K head verbatim */
+
+/* A read-only view of one layer's quantized K or V cache. */
+typedef struct kvq_kv_view {
+  const void* codes;     /* code byte of (b=0, h=0, t=0, d=0) */
+  int64_t stride_b;      /* bytes */
+  int64_t stride_h;      /* bytes */
+  int64_t stride_t;      /* bytes; the D (or D/2) code bytes of a token are contiguous */
+  const void* scale;     /* INT8_SYM/INT4_SYM: [B,H,T,G] (any strides, 0 allowed);
+                            INT4_ASYM: [H,G] (only stride_h / stride_g are read) */
+  int64_t scale_stride_b, scale_stride_h, scale_stride_t, scale_stride_g; /* elements */
+  int32_t scale_dtype;   /* KVQ_DTYPE_F16 or KVQ_DTYPE_F32 (F32 is rounded to fp16 in-kernel) */
+  int32_t n_outlier;     /* INT4_ASYM K only: 0 or 4 */
+  const void* zero_point;         /* INT4_ASYM: fp16 [H,G], same strides as scale */
+  const int32_t* outlier_idx;     /* [H, n_outlier] channel indices, distinct, in [0, D) */
+  const void* outlier_val;        /* fp16 [B,H,T,n_outlier] */
+  int64_t outlier_stride_b, outlier_stride_h, outlier_stride_t; /* elements */
+} kvq_kv_view;
+
+/* Decode attention (q_len == 1), split-K with an in-kernel GQA head group.
+ *
+ * Replaces:
+ *   decode_attn_int8(q, k_cache, v_cache, k_scale, v_scale, context_lens, sm_scale)
+ *     src/kernels/triton_decode_attn_int8.py:306-519   (formats INT8_SYM / INT8_SYM)
+ *   decode_attn_int4(q, k_cache_int4, v_cache_int4, k_scale, v_scale, context_lens, ...)
+ *     src/kernels/triton_decode_attn_int4.py:62-121    (formats INT4_SYM / INT4_SYM,
+ *     read packed in place instead of unpacking the whole cache to int8)
+ *   and the per-head inv_tau query scaling of src/engine/patch_model.py:711-746.
+ * The INT4_ASYM formats (and INT8_SYM K with INT4_ASYM V) have no reference kernel;
+ * they follow the asymmetric formula of src/quant/asymmetric_quant.py:24-196 with
+ * static group parameters.
+ *
+ * out[b, h, :] = softmax_t(sm_scale * q'[b,h] . khat[b, h/n_rep, t]) @ vhat[b, h/n_rep, t]
+ * for t < context_lens[b] (clamped to [0, capacity]); rows with an empty context are 0.
+ * q' = fp16(q * inv_tau[h]) when inv_tau is given.  Requires head_dim == 128 and
+ * q_heads / kv_heads <= 16.  INT4_ASYM requires group_size == 32; the scale formats
+ * require group_size in {8, 16, 32, 64, 128}.
+ */
+typedef struct kvq_decode_params {
+  const void* q;          /* fp16 [B, Hq, D], d contiguous */
+  int64_t q_stride_b, q_stride_h;     /* elements */
+  const void* inv_tau;    /* fp16 [Hq] or NULL */
+  int32_t k_format, v_format;
+  kvq_kv_view k, v;
+  const int32_t* context_lens;        /* device int32 [B] */
+  int32_t batch, q_heads, kv_heads, head_dim, group_size;
+  int64_t capacity;       /* token dimension of the cache views */
+  float sm_scale;
+  int32_t chunk_tokens;   /* tokens per work-group; 0 = choose automatically */
+  void* workspace;        /* device scratch of kvq_decode_workspace_bytes() bytes */
+  int64_t workspace_bytes;
+  void* out;              /* fp16 [B, Hq, D], d contiguous */
+  int64_t out_stride_b, out_stride_h; /* elements */
+} kvq_decode_params;
+
+int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream);
+/* chunk size kvq_decode_attn will use for p (p->chunk_tokens if nonzero) */
+int32_t kvq_decode_chunk_tokens(const kvq_decode_params* p);
+/* bytes of workspace kvq_decode_attn needs for p */
+int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p);
+
+/* Quantize-on-append of new K and V rows into a cache layer.
+ *
+ * Replaces the quantize + pack + slice-write part of:
+ *   INT8KVCache.append   src/cache/int8_cache.py:350-488
+ *     (quantize_symmetric_int8_with_scale src/quant/int8_basic.py:111-164,
+ *      quantize_symmetric_int8 (percentile 100) int8_basic.py:18-108)
+ *   INT4KVCache.append   src/cache/int4_cache.py:392-589
+ *     (quantize_symmetric_int4_with_scale src/quant/int4_basic.py:115-159,
+ *      _apply_outlier_rescue int4_cache.py:360-390, pack_int4 int4_basic.py:230-272)
+ *   the static-parameter asymmetric INT4 K quantizer of
+ *     src/kernels/triton_quantize_pack_int4.py:18-62 (INT4_ASYM; per group instead of
+ *     per channel, plus the fp16 outlier-channel side-band, which has no reference).
+ * Codes are bit-exact with those torch formulas: IEEE fp32 division, round half to
+ * even; INT8 rounds the quotient to fp16 before rounding to an integer.
+ */
+typedef struct kvq_append_params {
+  int32_t format;         /* KVQ_FMT_* */
+  const void* x;          /* fp16 [B, H, S_new, D], d contiguous */
+  int64_t x_stride_b, x_stride_h, x_stride_s;   /* elements */
+  int32_t batch, heads, seq_new, head_dim, group_size;
+  /* static parameters per (head, group); NULL static_scale = dynamic (absmax) scales */
+  const void* static_scale;
+  int32_t static_scale_dtype;                   /* KVQ_DTYPE_* */
+  int64_t static_stride_h, static_stride_g;     /* elements */
+  const void* static_zp;                        /* INT4_ASYM: fp16, same strides */
+  /* scale policy (INT8_SYM and INT4_SYM with a static scale) */
+  int32_t adaptive;        /* scale = max(static * margin, dynamic) */
+  float adaptive_margin;
+  int32_t mixed_rescue;    /* INT4_SYM: scale = max(scale, dynamic) */
+  float rescue_quantile;   /* INT4_SYM: 0 = off; else fp32(1 - outlier_rescue_ratio) */
+  int32_t rescue_all;      /* INT4_SYM: ratio >= 1: scale = max(scale, dynamic) everywhere */
+  /* destination */
+  void* codes;             /* code byte of (b=0, h=0, t=0) */
+  int64_t codes_stride_b, codes_stride_h, codes_stride_t;   /* bytes */
+  void* scale_out;         /* per-token scale [B,H,T,G] or NULL */
+  int32_t scale_out_dtype;
+  int64_t so_stride_b, so_stride_h, so_stride_t, so_stride_g; /* elements */
+  int32_t n_outlier;       /* INT4_ASYM: 0 or 4 */
+  const int32_t* outlier_idx;     /* [H, n_outlier] */
+  void* outlier_out;              /* fp16 [B,H,T,n_outlier] */
+  int64_t oo_stride_b, oo_stride_h, oo_stride_t;            /* elements */
+  int64_t write_pos;       /* first token slot written */
+  int64_t capacity;        /* token slots in the destination */
+  int32_t* status;         /* device int32[2] or NULL: [0] |= 1 if x had NaN/Inf,
+                              [1] += number of clipped elements */
+} kvq_append_params;
+
+/* Appends K and V of one layer with one launch (either pointer may be NULL). */
+int kvq_quant_append(const kvq_append_params* k, const kvq_append_params* v,
+                     kvq_stream_t stream);
+
+/* message for the last non-OK return on this thread ("" if none) */
+const char* kvq_last_error(void);
+/* ABI version (increments on incompatible changes to the structs above) */
+int32_t kvq_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KVQ_H_ */

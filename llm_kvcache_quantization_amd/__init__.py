@@ -1,0 +1,28 @@
+"""MI355X-native quantized KV-cache decode path (HIP/CDNA4).
+
+Drop-in for the decode (q_len == 1) path of zilangchen/LLM_KVCache_Quantization:
+quantize-on-append into the cache and fused quantized decode attention, behind the
+reference's Python API (``decode_attn_int8``, ``decode_attn_int4``, ``INT8KVCache``,
+``INT4KVCache``).  The kernels are in ``csrc/``, the C ABI is ``include/kvq.h`` and the
+library is loaded through ctypes by ``_capi``.  Nothing here computes on a fallback:
+without ``libkvq.so`` every kernel entry point raises.
+"""
+from .kernels import (  # noqa: F401
+    DecodePlan,
+    decode_attn_int4,
+    decode_attn_int4_asym,
+    decode_attn_int8,
+    decode_attn_k8v4,
+)
+from .cache import INT4AsymKVCache, INT4KVCache, INT8KVCache  # noqa: F401
+
+__all__ = [
+    "DecodePlan",
+    "decode_attn_int8",
+    "decode_attn_int4",
+    "decode_attn_int4_asym",
+    "decode_attn_k8v4",
+    "INT8KVCache",
+    "INT4KVCache",
+    "INT4AsymKVCache",
+]

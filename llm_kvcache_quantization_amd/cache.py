@@ -1,0 +1,739 @@
+"""Quantized KV-cache engines whose append runs the HIP quantize-on-append kernel.
+
+:class:`INT8KVCache` and :class:`INT4KVCache` keep the constructor arguments,
+methods, attributes, exceptions and warnings of the reference engines:
+
+* ``src/cache/int8_cache.py:29-682``
+* ``src/cache/int4_cache.py:32-760``
+
+``append`` quantises on the GPU in one launch for K and V, and the kernel writes
+straight into the preallocated buffers.  The codes are bit-exact with the
+reference torch quantizers.
+
+Where the layout differs from the reference:
+
+* With a static scale and no adaptive/rescue policy, every token gets the same
+  scale.  The engines then keep the effective per-(head, group) scale once.
+  ``get_int8_tensors`` / ``get_int4_tensors`` return it as a stride-0 expanded
+  view [B, H, S, G] with the values the reference stores per token.
+* INT8 scales are kept in fp16.  The INT8 quantizer returns its scale in fp16, so
+  the reference's fp32 copy carries the same values.  The kernel boundary's
+  ``.to(torch.float16)`` is therefore free.
+* Host synchronisation is optional.  With ``check_numerics=True`` (the default)
+  ``append`` reads a device status word back, like the reference's
+  NaN/Inf/clip checks, and raises/warns the same way.  With
+  ``check_numerics=False`` nothing synchronises.
+
+:class:`INT4AsymKVCache` (asymmetric INT4, static group-32 parameters, optional fp16
+K outlier channels) and :class:`MixedK8V4KVCache` are build-native formats of the
+BASELINE configurations; they have no reference engine.
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+import warnings
+from typing import Dict, List, Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _capi as C
+
+logger = logging.getLogger(__name__)
+
+_CLIP_WARN_THRESHOLD = 0.05
+
+
+def _new_decode_stats() -> Dict[str, object]:
+    return {
+        "fused_decode_calls": 0,
+        "triton_kernel_calls": 0,
+        "triton_decode_calls": 0,
+        "torch_ref_calls": 0,
+        "layer_hits": {},
+        "triton_layer_hits": {},
+    }
+
+
+def _static_2d(scale: Tensor, heads: int, groups: int, name: str) -> Tensor:
+    """Accept [H, G] (or [1, H, G] / [H, 1, G] / [H, G, 1]) static scales."""
+    s = scale
+    if s.ndim == 3:
+        if s.shape[0] == 1 and s.shape[1] == heads:
+            s = s[0]
+        elif s.shape[1] == 1 and s.shape[0] == heads:
+            s = s[:, 0]
+        elif s.shape[2] == 1 and s.shape[0] == heads:
+            s = s[..., 0]
+    if s.ndim != 2:
+        raise NotImplementedError(
+            f"{name}: static scale layout {tuple(scale.shape)} is not supported by the HIP "
+            "append; use [H, G]")
+    if s.shape[0] != heads:
+        raise ValueError(
+            "_normalize_static_scale: calibration vs model heads mismatch (fail-fast; wrong "
+            f"calibration file was loaded).\n  expected heads: {heads}\n  scale heads: {s.shape[0]}")
+    if s.shape[1] != groups:
+        raise ValueError(f"{name}: static scale has {s.shape[1]} groups, expected {groups}")
+    return s
+
+
+class _EngineBase:
+    """Capacity management, stats and bookkeeping shared by the engines."""
+
+    _min_capacity = 256
+
+    def _init_common(self, num_layers, device, max_seq_len, decode_attn_impl, check_numerics):
+        if num_layers <= 0:
+            raise ValueError(f"num_layers must be > 0, got {num_layers}")
+        self.num_layers = num_layers
+        self.device = device
+        self.max_seq_len = int(max_seq_len) if max_seq_len is not None else None
+        if self.max_seq_len is not None and self.max_seq_len <= 0:
+            raise ValueError(f"max_seq_len must be > 0, got {self.max_seq_len}")
+        self.decode_attn_impl = decode_attn_impl
+        self.check_numerics = bool(check_numerics)
+        self._layer_seq_lens: List[int] = [0] * num_layers
+        self._layer_capacity: List[int] = [0] * num_layers
+        self._seq_len = 0
+        self.decode_stats: Dict[str, object] = _new_decode_stats()
+        self._status: Optional[Tensor] = None
+
+    # -- decode stats (src/cache/int8_cache.py:255-296)
+    def _bump_counter(self, key: str, delta: int = 1) -> None:
+        self.decode_stats[key] = int(self.decode_stats.get(key, 0)) + int(delta)
+
+    def record_fused_decode(self, layer_id: int, decode_impl: str) -> None:
+        self._bump_counter("fused_decode_calls", 1)
+        if decode_impl in ("triton_fused", "hip_fused"):
+            self._bump_counter("triton_decode_calls", 1)
+        elif decode_impl == "torch_ref":
+            self._bump_counter("torch_ref_calls", 1)
+        hits = self.decode_stats.setdefault("layer_hits", {})
+        hits[str(layer_id)] = int(hits.get(str(layer_id), 0)) + 1
+
+    def record_triton_kernel_call(self, layer_id: Optional[int] = None) -> None:
+        self._bump_counter("triton_kernel_calls", 1)
+        if layer_id is None:
+            return
+        hits = self.decode_stats.setdefault("triton_layer_hits", {})
+        hits[str(layer_id)] = int(hits.get(str(layer_id), 0)) + 1
+
+    def reset_decode_stats(self) -> None:
+        self.decode_stats = _new_decode_stats()
+
+    def get_decode_stats(self) -> Dict[str, object]:
+        d = self.decode_stats
+        return {
+            "fused_decode_calls": int(d.get("fused_decode_calls", 0)),
+            "triton_kernel_calls": int(d.get("triton_kernel_calls", 0)),
+            "torch_ref_calls": int(d.get("torch_ref_calls", 0)),
+            "triton_decode_calls": int(d.get("triton_decode_calls", 0)),
+            "layer_hits": dict(d.get("layer_hits", {})),
+            "triton_layer_hits": dict(d.get("triton_layer_hits", {})),
+        }
+
+    def get_seq_len(self) -> int:
+        return self._seq_len
+
+    def _new_capacity(self, layer_id: int, target_len: int, capacity: int) -> int:
+        if self.max_seq_len is not None and target_len > self.max_seq_len:
+            raise ValueError(
+                f"target_len {target_len} exceeds max_seq_len {self.max_seq_len} for layer {layer_id}")
+        new_cap = max(target_len, self._min_capacity) if capacity == 0 else max(target_len, capacity * 2)
+        if self.max_seq_len is not None:
+            new_cap = min(new_cap, self.max_seq_len)
+            if new_cap < target_len:
+                raise ValueError(
+                    f"target_len {target_len} exceeds capped capacity {new_cap} for layer {layer_id}")
+        return new_cap
+
+    def _validate_kv(self, layer_id: int, k: Tensor, v: Tensor) -> None:
+        if layer_id < 0 or layer_id >= self.num_layers:
+            raise ValueError(f"layer_id {layer_id} out of range")
+        if k.ndim != 4:
+            raise ValueError(f"k must be 4D [B,H,S,D], got ndim={k.ndim}")
+        if v.ndim != 4:
+            raise ValueError(f"v must be 4D [B,H,S,D], got ndim={v.ndim}")
+        if tuple(k.shape) != tuple(v.shape):
+            raise ValueError(f"k/v shape mismatch: k={tuple(k.shape)} vs v={tuple(v.shape)}")
+        target = torch.device(self.device)
+        if k.device.type != target.type or v.device.type != target.type:
+            raise ValueError(
+                f"Device mismatch: cache_device={target}, k.device={k.device}, v.device={v.device}")
+        if not k.is_cuda:
+            raise ValueError("the HIP cache engines need GPU (ROCm) tensors")
+        if k.dtype != torch.float16 or v.dtype != torch.float16:
+            raise NotImplementedError(
+                f"the HIP append quantizes fp16 K/V (got {k.dtype}/{v.dtype}); the reference "
+                "divides in the input dtype, so other dtypes would not give the same codes")
+        if k.shape[-1] != 128:
+            raise NotImplementedError(f"head_dim must be 128, got {k.shape[-1]}")
+
+    def _status_buf(self, device) -> Tensor:
+        if self._status is None or self._status.device != device:
+            self._status = torch.zeros(4, dtype=torch.int32, device=device)
+        return self._status
+
+    def _check_status(self, layer_id: int, n_elem: int, kind: str, qrange: str) -> None:
+        st = self._status.cpu().tolist()
+        self._status.zero_()
+        if st[0] & 1:
+            raise ValueError(f"{kind} append: K input contains NaN or Inf — refusing to quantize corrupt data")
+        if st[2] & 1:
+            raise ValueError(f"{kind} append: V input contains NaN or Inf — refusing to quantize corrupt data")
+        for side, cnt in (("K", st[1]), ("V", st[3])):
+            ratio = cnt / max(n_elem, 1)
+            if ratio > _CLIP_WARN_THRESHOLD:
+                warnings.warn(
+                    f"Static {side} scale overflow at layer {layer_id}: {ratio:.1%} of values "
+                    f"clipped to {qrange} (threshold={_CLIP_WARN_THRESHOLD:.0%}). The static scale "
+                    "may be too small for this input. Consider re-calibrating or enabling "
+                    "adaptive_static_scales.", RuntimeWarning)
+
+    def _launch_append(self, pk: C.AppendParams, pv: C.AppendParams, device) -> None:
+        C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
+                                         ctypes.c_void_p(C.stream_handle(device))))
+
+
+def _fill_append(p: C.AppendParams, fmt: int, x: Tensor, gs: int, codes: Tensor, write_pos: int,
+                 status_ptr: Optional[int]) -> None:
+    B, H, S, D = x.shape
+    p.format = fmt
+    p.x = x.data_ptr()
+    p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride(0), x.stride(1), x.stride(2)
+    p.batch, p.heads, p.seq_new, p.head_dim, p.group_size = B, H, S, D, gs
+    p.codes = codes.data_ptr()
+    p.codes_stride_b, p.codes_stride_h, p.codes_stride_t = codes.stride(0), codes.stride(1), codes.stride(2)
+    p.write_pos = write_pos
+    p.capacity = codes.shape[2]
+    p.status = status_ptr
+
+
+class _SymCacheBase(_EngineBase):
+    """Shared logic of the INT8 / INT4 symmetric engines (reference layout)."""
+
+    _fmt = None
+    _qrange = ""
+    _kind = ""
+
+    def _init_sym(self, num_layers, device, clip_percentile, group_size, dtype, max_seq_len,
+                  decode_attn_impl, static_k_scale, static_v_scale, inv_tau, use_attn_temperature,
+                  adaptive_static_scales, adaptive_static_margin, adaptive_static_k,
+                  adaptive_static_v, check_numerics):
+        self._init_common(num_layers, device, max_seq_len, decode_attn_impl, check_numerics)
+        if adaptive_static_margin <= 0:
+            raise ValueError(f"adaptive_static_margin must be > 0, got {adaptive_static_margin}")
+        self.clip_percentile = clip_percentile
+        self.group_size = group_size
+        self.dtype = dtype
+        self.static_k_scale = static_k_scale
+        self.static_v_scale = static_v_scale
+        self.inv_tau = inv_tau
+        self.use_attn_temperature = use_attn_temperature
+        self.adaptive_static_scales = adaptive_static_scales
+        self.adaptive_static_margin = adaptive_static_margin
+        self.adaptive_static_k = adaptive_static_k
+        self.adaptive_static_v = adaptive_static_v
+        self._k_cache: List[Optional[Tensor]] = [None] * num_layers
+        self._v_cache: List[Optional[Tensor]] = [None] * num_layers
+        self._k_scale: List[Optional[Tensor]] = [None] * num_layers
+        self._v_scale: List[Optional[Tensor]] = [None] * num_layers
+        # per layer: True if scales are stored per token, False if one static table
+        self._k_tok: List[bool] = [True] * num_layers
+        self._v_tok: List[bool] = [True] * num_layers
+
+    # -- subclass hooks
+    def _code_dim(self, D: int) -> int:
+        raise NotImplementedError
+
+    def _scale_dtype(self) -> torch.dtype:
+        raise NotImplementedError
+
+    def _side_is_token(self, side: str) -> bool:
+        raise NotImplementedError
+
+    def _effective_static(self, s: Tensor) -> Tensor:
+        raise NotImplementedError
+
+    def _policy(self, p: C.AppendParams, side: str) -> None:
+        pass
+
+    def _ensure_capacity(self, layer_id, batch, heads, head_dim, num_groups, target_len):
+        bufs = [self._k_cache[layer_id], self._v_cache[layer_id],
+                self._k_scale[layer_id], self._v_scale[layer_id]]
+        non_none = sum(b is not None for b in bufs)
+        if non_none not in (0, 4):
+            raise RuntimeError(
+                f"Inconsistent buffer state for layer {layer_id}: {non_none}/4 buffers are not None "
+                "(expected 0 or 4). This may indicate a partial OOM during a prior allocation. "
+                "Call release() and retry.")
+        cd = self._code_dim(head_dim)
+        if non_none == 4:
+            kb = self._k_cache[layer_id]
+            if kb.shape[0] != batch or kb.shape[1] != heads or kb.shape[3] != cd or \
+                    self._k_scale[layer_id].shape[-1] != num_groups:
+                raise ValueError(
+                    f"Inconsistent KV shape for layer {layer_id}: existing K={tuple(kb.shape)}, "
+                    f"incoming=({batch}, {heads}, *, {cd}) with groups={num_groups}")
+        capacity = self._layer_capacity[layer_id]
+        if non_none == 4 and target_len <= capacity:
+            return
+        new_cap = self._new_capacity(layer_id, target_len, capacity if non_none else 0)
+        old_len = self._layer_seq_lens[layer_id]
+        try:
+            nk = torch.empty((batch, heads, new_cap, cd), device=self.device, dtype=torch.int8)
+            nv = torch.empty((batch, heads, new_cap, cd), device=self.device, dtype=torch.int8)
+            nks = self._alloc_scale("k", layer_id, batch, heads, new_cap, num_groups)
+            nvs = self._alloc_scale("v", layer_id, batch, heads, new_cap, num_groups)
+        except torch.cuda.OutOfMemoryError:
+            if non_none == 0:
+                self._k_cache[layer_id] = self._v_cache[layer_id] = None
+                self._k_scale[layer_id] = self._v_scale[layer_id] = None
+                self._layer_capacity[layer_id] = 0
+            raise
+        if non_none == 4 and old_len > 0:
+            nk[:, :, :old_len] = self._k_cache[layer_id][:, :, :old_len]
+            nv[:, :, :old_len] = self._v_cache[layer_id][:, :, :old_len]
+            if self._k_tok[layer_id]:
+                nks[:, :, :old_len] = self._k_scale[layer_id][:, :, :old_len]
+            if self._v_tok[layer_id]:
+                nvs[:, :, :old_len] = self._v_scale[layer_id][:, :, :old_len]
+        self._k_cache[layer_id], self._v_cache[layer_id] = nk, nv
+        self._k_scale[layer_id], self._v_scale[layer_id] = nks, nvs
+        self._layer_capacity[layer_id] = new_cap
+
+    def _alloc_scale(self, side, layer_id, batch, heads, cap, groups):
+        tok = self._side_is_token(side)
+        (self._k_tok if side == "k" else self._v_tok)[layer_id] = tok
+        if tok:
+            return torch.empty((batch, heads, cap, groups), device=self.device, dtype=self._scale_dtype())
+        static = (self.static_k_scale if side == "k" else self.static_v_scale)[layer_id]
+        s = _static_2d(static.to(self.device), heads, groups, f"static_{side}_scale")
+        return self._effective_static(s).contiguous()
+
+    def _static_for(self, side: str, layer_id: int, heads: int, groups: int) -> Optional[Tensor]:
+        st = self.static_k_scale if side == "k" else self.static_v_scale
+        if st is None:
+            return None
+        if layer_id >= len(st):
+            raise IndexError(
+                f"layer_id {layer_id} exceeds calibration layers {len(st)} for static_{side}_scale")
+        s = _static_2d(st[layer_id].to(self.device), heads, groups, f"static_{side}_scale")
+        if s.dtype not in (torch.float16, torch.float32):
+            s = s.float()
+        return s
+
+    def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
+        """Quantize and append KV tensors to the cache (one HIP launch for K and V)."""
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        if D % self.group_size:
+            raise ValueError(f"head_dim {D} must be divisible by group_size {self.group_size}")
+        G = D // self.group_size
+        self._pre_append_checks(layer_id)
+        sk = self._static_for("k", layer_id, H, G)
+        sv = self._static_for("v", layer_id, H, G)
+        if (sk is None or sv is None) and self.clip_percentile < 100.0:
+            raise NotImplementedError(
+                "dynamic (no static scale) quantization with percentile clipping < 100 is not "
+                "implemented in the HIP append; pass clip_percentile=100.0 or static scales")
+        old_len = self._layer_seq_lens[layer_id]
+        target = old_len + S
+        self._ensure_capacity(layer_id, B, H, D, G, target)
+        if S == 0:
+            return
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv = C.AppendParams(), C.AppendParams()
+        for side, p, x, codes, scale_buf, st, tok in (
+                ("k", pk, k, self._k_cache[layer_id], self._k_scale[layer_id], sk, self._k_tok[layer_id]),
+                ("v", pv, v, self._v_cache[layer_id], self._v_scale[layer_id], sv, self._v_tok[layer_id])):
+            xs = x if x.stride(-1) == 1 else x.contiguous()
+            sptr = None
+            if status is not None:
+                sptr = status.data_ptr() + (0 if side == "k" else 8)
+            _fill_append(p, self._fmt, xs, self.group_size, codes, old_len, sptr)
+            if st is not None:
+                p.static_scale = st.data_ptr()
+                p.static_scale_dtype = C.KVQ_DTYPE_F32 if st.dtype == torch.float32 else C.KVQ_DTYPE_F16
+                p.static_stride_h, p.static_stride_g = st.stride()
+                self._policy(p, side)
+            if tok:
+                p.scale_out = scale_buf.data_ptr()
+                p.scale_out_dtype = C.KVQ_DTYPE_F32 if scale_buf.dtype == torch.float32 else C.KVQ_DTYPE_F16
+                p.so_stride_b, p.so_stride_h, p.so_stride_t, p.so_stride_g = scale_buf.stride()
+            # keep the (possibly temporary) tensors alive until the launch returns
+            p._keep = (xs, st)
+        self._launch_append(pk, pv, k.device)
+        if status is not None:
+            self._check_status(layer_id, k.numel(), self._kind, self._qrange)
+        self._layer_seq_lens[layer_id] = target
+        if layer_id == 0:
+            self._seq_len = target
+
+    def _pre_append_checks(self, layer_id: int) -> None:
+        pass
+
+    def _raw_views(self, layer_id: int):
+        if layer_id < 0 or layer_id >= self.num_layers:
+            raise ValueError(f"layer_id {layer_id} out of range [0, {self.num_layers})")
+        if self._k_cache[layer_id] is None:
+            raise ValueError(f"Cache for layer {layer_id} is empty")
+        n = self._layer_seq_lens[layer_id]
+        kc = self._k_cache[layer_id][:, :, :n, :]
+        vc = self._v_cache[layer_id][:, :, :n, :]
+        B, H = kc.shape[0], kc.shape[1]
+
+        def sv(buf, tok):
+            if tok:
+                return buf[:, :, :n, :]
+            return buf[None, :, None, :].expand(B, H, n, buf.shape[-1])
+
+        return kc, vc, sv(self._k_scale[layer_id], self._k_tok[layer_id]), \
+            sv(self._v_scale[layer_id], self._v_tok[layer_id])
+
+    def clear(self) -> None:
+        self._layer_seq_lens = [0] * self.num_layers
+        self._seq_len = 0
+
+    def release(self) -> None:
+        n = self.num_layers
+        self._k_cache, self._v_cache = [None] * n, [None] * n
+        self._k_scale, self._v_scale = [None] * n, [None] * n
+        self._layer_seq_lens = [0] * n
+        self._layer_capacity = [0] * n
+        self._seq_len = 0
+
+    def get_memory_mb(self) -> float:
+        total = 0
+        for i in range(self.num_layers):
+            for buf in (self._k_cache[i], self._v_cache[i], self._k_scale[i], self._v_scale[i]):
+                if buf is not None:
+                    total += buf.numel() * buf.element_size()
+        return total / (1024 * 1024)
+
+    def to_tuple(self) -> Tuple[Tuple[Tensor, Tensor], ...]:
+        out = []
+        for i in range(self.num_layers):
+            if self._k_cache[i] is None:
+                raise ValueError(f"Layer {i} cache is empty")
+            out.append(self.get_kv(i))
+        return tuple(out)
+
+
+class INT8KVCache(_SymCacheBase):
+    """INT8 symmetric KV cache (src/cache/int8_cache.py:29)."""
+
+    _fmt = C.KVQ_FMT_INT8_SYM
+    _qrange = "[-127, 127]"
+    _kind = "INT8"
+
+    def __init__(
+        self,
+        num_layers: int,
+        device: str = "cuda",
+        clip_percentile: float = 99.9,
+        group_size: int = 128,
+        dtype: torch.dtype = torch.float16,
+        max_seq_len: Optional[int] = None,
+        decode_attn_impl: str = "triton_fused",
+        static_k_scale: Optional[Tensor] = None,
+        static_v_scale: Optional[Tensor] = None,
+        inv_tau: Optional[Tensor] = None,
+        use_attn_temperature: bool = True,
+        adaptive_static_scales: bool = False,
+        adaptive_static_margin: float = 1.0,
+        adaptive_static_k: bool = True,
+        adaptive_static_v: bool = True,
+        check_numerics: bool = True,
+    ):
+        self._init_sym(num_layers, device, clip_percentile, group_size, dtype, max_seq_len,
+                       decode_attn_impl, static_k_scale, static_v_scale, inv_tau,
+                       use_attn_temperature, adaptive_static_scales, adaptive_static_margin,
+                       adaptive_static_k, adaptive_static_v, check_numerics)
+
+    def _code_dim(self, D):
+        return D
+
+    def _scale_dtype(self):
+        return torch.float16
+
+    def _side_is_token(self, side):
+        st = self.static_k_scale if side == "k" else self.static_v_scale
+        if st is None:
+            return True
+        return bool(self.adaptive_static_scales and
+                    (self.adaptive_static_k if side == "k" else self.adaptive_static_v))
+
+    def _effective_static(self, s):
+        # quantize_symmetric_int8_with_scale: clamp(min=1e-5) then cast to fp16
+        return s.clamp(min=1e-5).to(torch.float16)
+
+    def _policy(self, p, side):
+        if self._side_is_token(side):
+            p.adaptive = 1
+            p.adaptive_margin = float(self.adaptive_static_margin)
+
+    def get_int8_tensors(self, layer_id: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+        """(k_int8, v_int8, k_scale, v_scale) views [B, H, S, D] / [B, H, S, G] (fp16 scales)."""
+        return self._raw_views(layer_id)
+
+    def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
+        """Dequantize (code * scale in fp32) and return fp16 K/V (int8_cache.py:490-542)."""
+        kc, vc, ks, vs = self._raw_views(layer_id)
+        if kc.shape[2] == 0:
+            logger.warning("get_kv(layer_id=%d) returning zero-length tensors.", layer_id)
+        return _deq_sym(kc, ks).to(self.dtype), _deq_sym(vc, vs).to(self.dtype)
+
+    @classmethod
+    def from_tuple(cls, past_key_values, device: str = "cuda", clip_percentile: float = 99.9,
+                   group_size: int = 128) -> "INT8KVCache":
+        cache = cls(num_layers=len(past_key_values), device=device,
+                    clip_percentile=clip_percentile, group_size=group_size)
+        for i, (k, v) in enumerate(past_key_values):
+            cache.append(i, k.to(device), v.to(device))
+        return cache
+
+    def __repr__(self) -> str:
+        return (f"INT8KVCache(num_layers={self.num_layers}, seq_len={self._seq_len}, "
+                f"memory={self.get_memory_mb():.2f}MB)")
+
+
+class INT4KVCache(_SymCacheBase):
+    """INT4 symmetric, bit-packed KV cache (src/cache/int4_cache.py:32)."""
+
+    _fmt = C.KVQ_FMT_INT4_SYM
+    _qrange = "[-7, 7]"
+    _kind = "INT4"
+
+    def __init__(
+        self,
+        num_layers: int,
+        device: str = "cuda",
+        clip_percentile: float = 99.9,
+        group_size: int = 32,
+        dtype: torch.dtype = torch.float16,
+        max_seq_len: Optional[int] = None,
+        bit_packed: bool = True,
+        decode_attn_impl: str = "triton_fused",
+        static_k_scale: Optional[Tensor] = None,
+        static_v_scale: Optional[Tensor] = None,
+        inv_tau: Optional[Tensor] = None,
+        use_attn_temperature: bool = True,
+        adaptive_static_scales: bool = False,
+        adaptive_static_margin: float = 1.0,
+        adaptive_static_k: bool = True,
+        adaptive_static_v: bool = True,
+        outlier_rescue_ratio: float = 0.0,
+        mixed_rescue: bool = False,
+        check_numerics: bool = True,
+    ):
+        if outlier_rescue_ratio < 0.0 or outlier_rescue_ratio > 1.0:
+            raise ValueError(f"outlier_rescue_ratio must be in [0, 1], got {outlier_rescue_ratio}")
+        if not bit_packed:
+            raise NotImplementedError("the HIP INT4 engine stores bit-packed codes only")
+        self._init_sym(num_layers, device, clip_percentile, group_size, dtype, max_seq_len,
+                       decode_attn_impl, static_k_scale, static_v_scale, inv_tau,
+                       use_attn_temperature, adaptive_static_scales, adaptive_static_margin,
+                       adaptive_static_k, adaptive_static_v, check_numerics)
+        self.bit_packed = True
+        self.outlier_rescue_ratio = float(outlier_rescue_ratio)
+        self.mixed_rescue = bool(mixed_rescue)
+
+    def _code_dim(self, D):
+        return D // 2
+
+    def _scale_dtype(self):
+        return torch.float32
+
+    def _side_is_token(self, side):
+        st = self.static_k_scale if side == "k" else self.static_v_scale
+        if st is None:
+            return True
+        adaptive = self.adaptive_static_scales and (
+            self.adaptive_static_k if side == "k" else self.adaptive_static_v)
+        return bool(adaptive or self.mixed_rescue or self.outlier_rescue_ratio > 0.0)
+
+    def _effective_static(self, s):
+        return s.to(torch.float32).clamp(min=1e-5)
+
+    def _policy(self, p, side):
+        adaptive = self.adaptive_static_scales and (
+            self.adaptive_static_k if side == "k" else self.adaptive_static_v)
+        p.adaptive = int(bool(adaptive))
+        p.adaptive_margin = float(self.adaptive_static_margin)
+        p.mixed_rescue = int(self.mixed_rescue)
+        r = self.outlier_rescue_ratio
+        if r >= 1.0:
+            p.rescue_all = 1
+        elif r > 0.0:
+            p.rescue_quantile = float(max(0.0, min(1.0, 1.0 - r)))
+
+    def _pre_append_checks(self, layer_id):
+        missing = [s for s, t in (("K", self.static_k_scale), ("V", self.static_v_scale)) if t is None]
+        if missing:
+            side = " and ".join(missing)
+            if self.outlier_rescue_ratio > 0:
+                warnings.warn(
+                    f"KVC-031: outlier_rescue_ratio={self.outlier_rescue_ratio} has no effect on "
+                    f"{side} at layer {layer_id} because no static {side} scale is provided.",
+                    RuntimeWarning)
+            if self.mixed_rescue:
+                warnings.warn(
+                    f"KVC-031: mixed_rescue=True has no effect on {side} at layer {layer_id} "
+                    f"because no static {side} scale is provided.", RuntimeWarning)
+
+    def get_int4_tensors(self, layer_id: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+        """(k_packed, v_packed, k_scale, v_scale): packed [B,H,S,D/2], fp32 scales [B,H,S,G]."""
+        return self._raw_views(layer_id)
+
+    def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
+        kc, vc, ks, vs = self._raw_views(layer_id)
+        return (_deq_sym(_unpack(kc), ks).to(self.dtype), _deq_sym(_unpack(vc), vs).to(self.dtype))
+
+    @classmethod
+    def from_tuple(cls, past_key_values, device: str = "cuda", clip_percentile: float = 99.9,
+                   group_size: int = 32, bit_packed: bool = True) -> "INT4KVCache":
+        cache = cls(num_layers=len(past_key_values), device=device, clip_percentile=clip_percentile,
+                    group_size=group_size, bit_packed=bit_packed)
+        for i, (k, v) in enumerate(past_key_values):
+            cache.append(i, k.to(device), v.to(device))
+        return cache
+
+    def __repr__(self) -> str:
+        return (f"INT4KVCache(num_layers={self.num_layers}, seq_len={self._seq_len}, "
+                f"memory={self.get_memory_mb():.2f}MB)")
+
+
+def _unpack(packed: Tensor) -> Tensor:
+    u = packed.view(torch.uint8)
+    out = torch.stack([(u >> 4) & 0x0F, u & 0x0F], dim=-1).view(*packed.shape[:-1], packed.shape[-1] * 2)
+    return (out.to(torch.int16) - 8).to(torch.int8)
+
+
+def _deq_sym(q: Tensor, s: Tensor) -> Tensor:
+    B, H, S, D = q.shape
+    G = s.shape[-1]
+    return (q.view(B, H, S, G, D // G).to(s.dtype) * s.unsqueeze(-1)).view(B, H, S, D)
+
+
+class INT4AsymKVCache(_EngineBase):
+    """Asymmetric INT4 cache with static group-32 parameters (build-native format).
+
+    Per layer: packed codes K/V [B, H, cap, 64] (byte = hi nibble even channel, codes
+    c + 8 with c in [-8, 7]), static fp16 scale/zero-point [L, H, 4] for K and V, and
+    optionally ``k_outlier_idx`` int [L, H, 4]: those 4 K channels per head are also
+    stored verbatim in fp16 [B, H, cap, 4] and replace the dequantised codes.
+    """
+
+    def __init__(self, num_layers: int, k_scale: Tensor, k_zp: Tensor, v_scale: Tensor,
+                 v_zp: Tensor, device: str = "cuda", max_seq_len: Optional[int] = None,
+                 k_outlier_idx: Optional[Tensor] = None, inv_tau: Optional[Tensor] = None,
+                 use_attn_temperature: bool = True, decode_attn_impl: str = "hip_fused",
+                 check_numerics: bool = False):
+        self._init_common(num_layers, device, max_seq_len, decode_attn_impl, check_numerics)
+        self.group_size = 32
+        self.k_scale = k_scale.to(device=device, dtype=torch.float16).contiguous()
+        self.k_zp = k_zp.to(device=device, dtype=torch.float16).contiguous()
+        self.v_scale = v_scale.to(device=device, dtype=torch.float16).contiguous()
+        self.v_zp = v_zp.to(device=device, dtype=torch.float16).contiguous()
+        if k_outlier_idx is not None:
+            oi = k_outlier_idx.detach().cpu()
+            if oi.ndim != 3 or oi.shape[0] != num_layers or oi.shape[-1] != 4:
+                raise ValueError(f"k_outlier_idx must be [L, H, 4], got {tuple(oi.shape)}")
+            if oi.min() < 0 or oi.max() > 127:
+                raise ValueError("k_outlier_idx values must lie in [0, 128)")
+            if any(len(set(r.tolist())) != 4 for r in oi.reshape(-1, 4)):
+                raise ValueError("k_outlier_idx channels must be distinct per head")
+        self.k_outlier_idx = (None if k_outlier_idx is None else
+                              k_outlier_idx.to(device=device, dtype=torch.int32).contiguous())
+        self.inv_tau = inv_tau
+        self.use_attn_temperature = use_attn_temperature
+        n = num_layers
+        self._k: List[Optional[Tensor]] = [None] * n
+        self._v: List[Optional[Tensor]] = [None] * n
+        self._ko: List[Optional[Tensor]] = [None] * n
+
+    def _ensure(self, layer_id, B, H, target):
+        cap = self._layer_capacity[layer_id]
+        if self._k[layer_id] is not None:
+            kb = self._k[layer_id]
+            if kb.shape[0] != B or kb.shape[1] != H:
+                raise ValueError(f"Inconsistent KV shape for layer {layer_id}")
+            if target <= cap:
+                return
+        new_cap = self._new_capacity(layer_id, target, cap if self._k[layer_id] is not None else 0)
+        old = self._layer_seq_lens[layer_id]
+        nk = torch.empty((B, H, new_cap, 64), dtype=torch.uint8, device=self.device)
+        nv = torch.empty_like(nk)
+        no = (torch.empty((B, H, new_cap, 4), dtype=torch.float16, device=self.device)
+              if self.k_outlier_idx is not None else None)
+        if self._k[layer_id] is not None and old:
+            nk[:, :, :old] = self._k[layer_id][:, :, :old]
+            nv[:, :, :old] = self._v[layer_id][:, :, :old]
+            if no is not None:
+                no[:, :, :old] = self._ko[layer_id][:, :, :old]
+        self._k[layer_id], self._v[layer_id], self._ko[layer_id] = nk, nv, no
+        self._layer_capacity[layer_id] = new_cap
+
+    def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        old = self._layer_seq_lens[layer_id]
+        self._ensure(layer_id, B, H, old + S)
+        if S == 0:
+            return
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv = C.AppendParams(), C.AppendParams()
+        keep = []
+        for side, p, x, codes, s, z in (("k", pk, k, self._k[layer_id], self.k_scale, self.k_zp),
+                                        ("v", pv, v, self._v[layer_id], self.v_scale, self.v_zp)):
+            xs = x if x.stride(-1) == 1 else x.contiguous()
+            keep.append(xs)
+            sptr = None if status is None else status.data_ptr() + (0 if side == "k" else 8)
+            _fill_append(p, C.KVQ_FMT_INT4_ASYM, xs, 32, codes, old, sptr)
+            sl, zl = s[layer_id], z[layer_id]
+            p.static_scale, p.static_zp = sl.data_ptr(), zl.data_ptr()
+            p.static_scale_dtype = C.KVQ_DTYPE_F16
+            p.static_stride_h, p.static_stride_g = sl.stride()
+            if side == "k" and self.k_outlier_idx is not None:
+                oi, oo = self.k_outlier_idx[layer_id], self._ko[layer_id]
+                p.n_outlier = oi.shape[-1]
+                p.outlier_idx, p.outlier_out = oi.data_ptr(), oo.data_ptr()
+                p.oo_stride_b, p.oo_stride_h, p.oo_stride_t = oo.stride(0), oo.stride(1), oo.stride(2)
+        self._launch_append(pk, pv, k.device)
+        if status is not None:
+            self._check_status(layer_id, k.numel(), "INT4-asym", "[-8, 7]")
+        self._layer_seq_lens[layer_id] = old + S
+        if layer_id == 0:
+            self._seq_len = old + S
+
+    def get_int4_g32_tensors(self, layer_id: int):
+        """(k_codes, v_codes, k_scale, k_zp, v_scale, v_zp, k_outlier_idx, k_outlier_val)."""
+        if self._k[layer_id] is None:
+            raise ValueError(f"Cache for layer {layer_id} is empty")
+        n = self._layer_seq_lens[layer_id]
+        ko = None if self._ko[layer_id] is None else self._ko[layer_id][:, :, :n]
+        oi = None if self.k_outlier_idx is None else self.k_outlier_idx[layer_id]
+        return (self._k[layer_id][:, :, :n], self._v[layer_id][:, :, :n], self.k_scale[layer_id],
+                self.k_zp[layer_id], self.v_scale[layer_id], self.v_zp[layer_id], oi, ko)
+
+    def clear(self) -> None:
+        self._layer_seq_lens = [0] * self.num_layers
+        self._seq_len = 0
+
+    def release(self) -> None:
+        n = self.num_layers
+        self._k, self._v, self._ko = [None] * n, [None] * n, [None] * n
+        self._layer_seq_lens = [0] * n
+        self._layer_capacity = [0] * n
+        self._seq_len = 0
+
+    def get_memory_mb(self) -> float:
+        total = 0
+        for bufs in (self._k, self._v, self._ko):
+            for b in bufs:
+                if b is not None:
+                    total += b.numel() * b.element_size()
+        return total / (1024 * 1024)

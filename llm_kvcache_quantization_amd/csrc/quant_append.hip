@@ -1,0 +1,332 @@
+// Quantize-on-append for gfx950: new K/V rows (fp16) -> cache codes (+ scales).
+//
+// One wavefront quantises one (b, h, s) row of D = 128 values (2 per lane); the
+// grid's y dimension selects K (0) or V (1) so one launch appends a layer.  The
+// arithmetic restates the reference torch quantizers element for element:
+//   INT8  sym: q = clamp(rne(fp16(x / s16)), -127, 127), s16 = fp16(max(s, 1e-5))
+//              src/quant/int8_basic.py:111-164 (static), :18-108 (dynamic absmax)
+//   INT4  sym: q = clamp(rne(x / s32), -7, 7), s32 = max(s, 1e-5) [+ rescue]
+//              src/quant/int4_basic.py:115-159, src/cache/int4_cache.py:317-390
+//   INT4 asym: q = clamp(rne((x - zp) / s), -8, 7)   (static s, zp per group)
+//              src/kernels/triton_quantize_pack_int4.py:18-62,
+//              tests/test_fused_quantize_pack.py:8-17
+// Packing: byte = ((q[2i] + 8) << 4) | (q[2i+1] + 8)   src/quant/int4_basic.py:263-270
+// Divisions are IEEE fp32 (__fdiv_rn) and rounding is ties-to-even (rintf), which is
+// what torch does for tensor/tensor ops on both CPU and GPU.
+#include "kvq_common.h"
+#include "kvq.h"
+
+#include <string>
+
+namespace kvq {
+
+extern thread_local std::string g_last_error;
+int fail(int code, const std::string& msg);
+
+constexpr int kAppendWaves = 4;
+constexpr int kRescueMax = 4096;  // (rows x groups) handled by the single-work-group rescue path
+
+struct AppendDev {
+  int valid;
+  int fmt;
+  const half_t* x;
+  int64_t xsb, xsh, xss;
+  int B, H, S, gs;
+  const void* st;
+  int st_f32;
+  int64_t st_sh, st_sg;
+  const half_t* st_zp;
+  int adaptive;
+  float margin;
+  int mixed;
+  float rq;
+  int rescue_all;
+  uint8_t* codes;
+  int64_t csb, csh, cst;
+  void* so;
+  int so_f32;
+  int64_t sosb, sosh, sost, sosg;
+  int n_out;
+  const int32_t* oidx;
+  half_t* oo;
+  int64_t oosb, oosh, oost;
+  int64_t wpos;
+  int32_t* status;
+};
+
+__device__ __forceinline__ float ld_static(const AppendDev& a, int h, int g) {
+  const int64_t off = (int64_t)h * a.st_sh + (int64_t)g * a.st_sg;
+  return a.st_f32 ? reinterpret_cast<const float*>(a.st)[off]
+                  : (float)reinterpret_cast<const half_t*>(a.st)[off];
+}
+
+// max over the lanes of one quantisation group (gs/2 consecutive lanes)
+__device__ __forceinline__ float group_max(float v, int gs) {
+  for (int o = 1; o < gs / 2; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Scale of group g for a row, before the per-format final clamp.
+//  dyn_abs: absmax of the group's fp16 values (as float)
+__device__ __forceinline__ float int4_scale(const AppendDev& a, int h, int g, float dyn_abs,
+                                            float thr) {
+  float s = fmaxf(ld_static(a, h, g), 1e-5f);                 // int4_cache.py:342
+  const float dyn = __fdiv_rn(fmaxf(dyn_abs, 1e-5f), 7.0f);   // int4_cache.py:358
+  if (a.adaptive) s = fmaxf(s * a.margin, dyn);                // :451-455
+  if (a.mixed) s = fmaxf(s, dyn);                              // :457-458
+  if (a.rescue_all) s = fmaxf(s, dyn);                         // :381-382
+  else if (a.rq > 0.f && dyn >= thr) s = fmaxf(s, dyn);        // :384-390
+  return fmaxf(s, 1e-5f);                                      // int4_basic.py:154
+}
+
+__device__ __forceinline__ half_t int8_scale16(const AppendDev& a, int h, int g, float dyn_abs) {
+  if (a.st == nullptr) {
+    // dynamic absmax path: fp16 absmax clamped, then absmax / 127 in fp16 arithmetic
+    const float am = fmaxf(dyn_abs, (float)(half_t)1e-5f);   // int8_basic.py:91-92
+    return (half_t)__fdiv_rn(am, 127.0f);                     // :94
+  }
+  float s = ld_static(a, h, g);
+  if (a.adaptive) {
+    s = fmaxf(s, 1e-5f) * a.margin;                            // int8_cache.py:326,398
+    const float dyn = __fdiv_rn(fmaxf(dyn_abs, 1e-5f), 127.0f);  // :348
+    s = fmaxf(s, dyn);
+  }
+  if (!a.st_f32 && !a.adaptive) {
+    // fp16 static: clamp in fp16 (no fp16 value lies strictly between 1e-5 and fp16(1e-5))
+    return (half_t)fmaxf(s, (float)(half_t)1e-5f);
+  }
+  return (half_t)fmaxf(s, 1e-5f);                              // int8_basic.py:159
+}
+
+__device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
+  const int s_idx = row % a.S;
+  const int bh = row / a.S;
+  const int h = bh % a.H, b = bh / a.H;
+  const int64_t t = a.wpos + s_idx;
+  const half_t* xr = a.x + (int64_t)b * a.xsb + (int64_t)h * a.xsh + (int64_t)s_idx * a.xss;
+  const half2v xv = *reinterpret_cast<const half2v*>(xr + 2 * lane);
+  const float x0 = (float)xv.x, x1 = (float)xv.y;
+  const int d0 = 2 * lane;
+  const int g = d0 / a.gs;
+
+  // NaN / Inf detection (src/quant/_common.py:13-20): reported through status[0]
+  const bool bad = !(__builtin_isfinite(x0) && __builtin_isfinite(x1));
+  const unsigned long long badmask = __ballot(bad);
+  if (badmask && lane == 0 && a.status) atomicOr(&a.status[0], 1);
+
+  const float am = group_max(fmaxf(fabsf(x0), fabsf(x1)), a.gs);
+  uint8_t* crow = a.codes + (int64_t)b * a.csb + (int64_t)h * a.csh + t * a.cst;
+  int clipped = 0;
+
+  if (a.fmt == KVQ_FMT_INT8_SYM) {
+    const half_t s16 = int8_scale16(a, h, g, am);
+    const float sf = (float)s16;
+    const float q0 = rintf((float)(half_t)__fdiv_rn(x0, sf));
+    const float q1 = rintf((float)(half_t)__fdiv_rn(x1, sf));
+    const int c0 = (int)fminf(fmaxf(q0, -127.f), 127.f);
+    const int c1 = (int)fminf(fmaxf(q1, -127.f), 127.f);
+    const uint16_t pair = (uint16_t)((uint8_t)(int8_t)c0 | ((uint16_t)(uint8_t)(int8_t)c1 << 8));
+    *reinterpret_cast<uint16_t*>(crow + d0) = pair;
+    clipped = (c0 == 127 || c0 == -127) + (c1 == 127 || c1 == -127);   // int8_cache.py:409
+    if (a.so && (d0 % a.gs) == 0) {
+      const int64_t off = (int64_t)b * a.sosb + (int64_t)h * a.sosh + t * a.sost + (int64_t)g * a.sosg;
+      if (a.so_f32) reinterpret_cast<float*>(a.so)[off] = sf;
+      else reinterpret_cast<half_t*>(a.so)[off] = s16;
+    }
+  } else if (a.fmt == KVQ_FMT_INT4_SYM) {
+    float s;
+    if (a.st == nullptr) {
+      // fp16 absmax clamped in fp16, then divided in fp32 (int4_basic.py:86-99)
+      s = __fdiv_rn(fmaxf(am, (float)(half_t)1e-5f), 7.0f);
+    } else {
+      s = int4_scale(a, h, g, am, thr);
+    }
+    const float q0 = fminf(fmaxf(rintf(__fdiv_rn(x0, s)), -7.f), 7.f);
+    const float q1 = fminf(fmaxf(rintf(__fdiv_rn(x1, s)), -7.f), 7.f);
+    crow[lane] = (uint8_t)((((int)q0 + 8) << 4) | ((int)q1 + 8));
+    if (a.st != nullptr) {
+      const float bound = s * 7.0f;                          // int4_cache.py:473-476
+      clipped = (fabsf(x0) > bound) + (fabsf(x1) > bound);
+    }
+    if (a.so && (d0 % a.gs) == 0) {
+      const int64_t off = (int64_t)b * a.sosb + (int64_t)h * a.sosh + t * a.sost + (int64_t)g * a.sosg;
+      if (a.so_f32) reinterpret_cast<float*>(a.so)[off] = s;
+      else reinterpret_cast<half_t*>(a.so)[off] = (half_t)s;
+    }
+  } else {  // KVQ_FMT_INT4_ASYM, static parameters
+    const int64_t off = (int64_t)h * a.st_sh + (int64_t)g * a.st_sg;
+    const float s = (float)reinterpret_cast<const half_t*>(a.st)[off];
+    const float z = (float)a.st_zp[off];
+    const float r0 = rintf(__fdiv_rn(x0 - z, s));
+    const float r1 = rintf(__fdiv_rn(x1 - z, s));
+    clipped = (r0 < -8.f || r0 > 7.f) + (r1 < -8.f || r1 > 7.f);
+    const int c0 = (int)fminf(fmaxf(r0, -8.f), 7.f);
+    const int c1 = (int)fminf(fmaxf(r1, -8.f), 7.f);
+    crow[lane] = (uint8_t)(((c0 + 8) << 4) | (c1 + 8));
+    if (a.n_out > 0 && lane < a.n_out) {
+      const int ch = min(max(a.oidx[h * a.n_out + lane], 0), 127);
+      half_t* orow = a.oo + (int64_t)b * a.oosb + (int64_t)h * a.oosh + t * a.oost;
+      orow[lane] = xr[ch];
+    }
+  }
+  // clipped-element count (int8_cache.py:407-419, int4_cache.py:468-485)
+  for (int o = 32; o > 0; o >>= 1) clipped += __shfl_xor(clipped, o, 64);
+  if (lane == 0 && a.status && clipped) atomicAdd(&a.status[1], clipped);
+}
+
+// Bitonic sort of n_pad (power of two) floats in LDS, ascending.
+__device__ void lds_bitonic_sort(float* v, int n_pad) {
+  for (int k = 2; k <= n_pad; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n_pad; i += blockDim.x) {
+        const int p = i ^ j;
+        if (p > i) {
+          const bool up = (i & k) == 0;
+          const float x = v[i], y = v[p];
+          if ((x > y) == up) {
+            v[i] = y;
+            v[p] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// torch.quantile(x, q) with linear interpolation, float32 arithmetic:
+// rank = fp32(q) * (n - 1); lo = floor(rank); hi = ceil(rank); w = rank - lo;
+// lerp(a, b, w) = w < 0.5 ? a + w * (b - a) : b - (b - a) * (1 - w)   (no FMA contraction)
+__device__ float sorted_quantile(const float* v, int n, float q) {
+  const float rank = __fmul_rn(q, (float)(n - 1));
+  const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
+  const float w = __fsub_rn(rank, (float)lo);
+  const float a = v[lo], b = v[hi];
+  const float diff = __fsub_rn(b, a);
+  return w < 0.5f ? __fadd_rn(a, __fmul_rn(w, diff))
+                  : __fsub_rn(b, __fmul_rn(diff, __fsub_rn(1.0f, w)));
+}
+
+__global__ __launch_bounds__(kAppendWaves * 64) void append_kernel(AppendDev k, AppendDev v,
+                                                                    int rescue) {
+  const AppendDev& a = blockIdx.y == 0 ? k : v;
+  if (!a.valid) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = a.B * a.H * a.S;
+  float thr = 0.f;
+  if (rescue && a.fmt == KVQ_FMT_INT4_SYM && a.st != nullptr && a.rq > 0.f && !a.rescue_all) {
+    // Global threshold over every (row, group) dynamic scale of this append
+    // (int4_cache.py:384-389).  Single work-group: grid.x == 1 on this path.
+    __shared__ float dyn[kRescueMax];
+    __shared__ float thr_sh;
+    const int G = 128 / a.gs;
+    const int n = rows * G;
+    int n_pad = 1;
+    while (n_pad < n) n_pad <<= 1;
+    for (int i = threadIdx.x; i < n_pad; i += blockDim.x) dyn[i] = __builtin_inff();
+    __syncthreads();
+    for (int row = wave; row < rows; row += kAppendWaves) {
+      const int s_idx = row % a.S, bh = row / a.S, h = bh % a.H, b = bh / a.H;
+      const half_t* xr = a.x + (int64_t)b * a.xsb + (int64_t)h * a.xsh + (int64_t)s_idx * a.xss;
+      const half2v xv = *reinterpret_cast<const half2v*>(xr + 2 * lane);
+      const float am = group_max(fmaxf(fabsf((float)xv.x), fabsf((float)xv.y)), a.gs);
+      if ((2 * lane) % a.gs == 0) dyn[row * G + (2 * lane) / a.gs] = __fdiv_rn(fmaxf(am, 1e-5f), 7.0f);
+    }
+    __syncthreads();
+    lds_bitonic_sort(dyn, n_pad);
+    if (threadIdx.x == 0) thr_sh = sorted_quantile(dyn, n, a.rq);
+    __syncthreads();
+    thr = thr_sh;
+  }
+  for (int row = blockIdx.x * kAppendWaves + wave; row < rows; row += gridDim.x * kAppendWaves)
+    quant_row(a, row, lane, thr);
+}
+
+static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) {
+  d = AppendDev{};
+  if (!p) return KVQ_OK;
+  const std::string n(name);
+  if (p->format != KVQ_FMT_INT8_SYM && p->format != KVQ_FMT_INT4_SYM &&
+      p->format != KVQ_FMT_INT4_ASYM)
+    return fail(KVQ_ERR_INVALID, n + ": unknown format");
+  if (p->head_dim != 128) return fail(KVQ_ERR_UNSUPPORTED, n + ": head_dim must be 128");
+  const int gs = p->group_size;
+  if (gs != 8 && gs != 16 && gs != 32 && gs != 64 && gs != 128)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": group_size must be 8, 16, 32, 64 or 128");
+  if (p->batch < 0 || p->heads < 0 || p->seq_new < 0)
+    return fail(KVQ_ERR_INVALID, n + ": negative size");
+  if (!p->x || !p->codes) return fail(KVQ_ERR_INVALID, n + ": x/codes is NULL");
+  if (((uintptr_t)p->x % 4) || (p->x_stride_b % 2) || (p->x_stride_h % 2) || (p->x_stride_s % 2))
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": x rows must be 4-byte aligned");
+  if (p->format == KVQ_FMT_INT8_SYM &&
+      (((uintptr_t)p->codes % 2) || p->codes_stride_b % 2 || p->codes_stride_h % 2 ||
+       p->codes_stride_t % 2))
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": int8 code rows must be 2-byte aligned");
+  if (p->write_pos < 0 || p->write_pos + p->seq_new > p->capacity)
+    return fail(KVQ_ERR_INVALID, n + ": write_pos + seq_new exceeds capacity");
+  if (p->format == KVQ_FMT_INT4_ASYM) {
+    if (gs != 32) return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_ASYM needs group_size 32");
+    if (!p->static_scale || !p->static_zp || p->static_scale_dtype != KVQ_DTYPE_F16)
+      return fail(KVQ_ERR_INVALID, n + ": INT4_ASYM needs fp16 static scale and zero-point");
+    if (p->n_outlier != 0 && (p->n_outlier != 4 || !p->outlier_idx || !p->outlier_out))
+      return fail(KVQ_ERR_INVALID, n + ": outliers need n_outlier == 4 and both pointers");
+  } else if (p->n_outlier != 0) {
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
+  }
+  if (p->format == KVQ_FMT_INT4_SYM && p->static_scale && p->rescue_quantile > 0.f &&
+      !p->rescue_all && (int64_t)p->batch * p->heads * p->seq_new * (128 / gs) > kRescueMax)
+    return fail(KVQ_ERR_UNSUPPORTED,
+                n + ": outlier rescue supports at most 4096 (row, group) scales per append");
+  d.valid = p->batch * p->heads * p->seq_new > 0;
+  d.fmt = p->format;
+  d.x = reinterpret_cast<const half_t*>(p->x);
+  d.xsb = p->x_stride_b; d.xsh = p->x_stride_h; d.xss = p->x_stride_s;
+  d.B = p->batch; d.H = p->heads; d.S = p->seq_new; d.gs = gs;
+  d.st = p->static_scale;
+  d.st_f32 = p->static_scale_dtype == KVQ_DTYPE_F32;
+  d.st_sh = p->static_stride_h; d.st_sg = p->static_stride_g;
+  d.st_zp = reinterpret_cast<const half_t*>(p->static_zp);
+  d.adaptive = p->adaptive; d.margin = p->adaptive_margin;
+  d.mixed = p->mixed_rescue; d.rq = p->rescue_quantile; d.rescue_all = p->rescue_all;
+  d.codes = reinterpret_cast<uint8_t*>(p->codes);
+  d.csb = p->codes_stride_b; d.csh = p->codes_stride_h; d.cst = p->codes_stride_t;
+  d.so = p->scale_out; d.so_f32 = p->scale_out_dtype == KVQ_DTYPE_F32;
+  d.sosb = p->so_stride_b; d.sosh = p->so_stride_h; d.sost = p->so_stride_t; d.sosg = p->so_stride_g;
+  d.n_out = p->n_outlier; d.oidx = p->outlier_idx;
+  d.oo = reinterpret_cast<half_t*>(p->outlier_out);
+  d.oosb = p->oo_stride_b; d.oosh = p->oo_stride_h; d.oost = p->oo_stride_t;
+  d.wpos = p->write_pos;
+  d.status = p->status;
+  return KVQ_OK;
+}
+
+static bool needs_rescue(const kvq_append_params* p) {
+  return p && p->format == KVQ_FMT_INT4_SYM && p->static_scale && p->rescue_quantile > 0.f &&
+         !p->rescue_all;
+}
+
+}  // namespace kvq
+
+using namespace kvq;
+
+extern "C" int kvq_quant_append(const kvq_append_params* k, const kvq_append_params* v,
+                                kvq_stream_t stream) {
+  AppendDev dk, dv;
+  int rc = fill_dev(k, dk, "k");
+  if (rc) return rc;
+  rc = fill_dev(v, dv, "v");
+  if (rc) return rc;
+  if (!dk.valid && !dv.valid) return KVQ_OK;
+  const int rescue = needs_rescue(k) || needs_rescue(v);
+  int64_t rows = 0;
+  if (dk.valid) rows = (int64_t)dk.B * dk.H * dk.S;
+  if (dv.valid) rows = rows > (int64_t)dv.B * dv.H * dv.S ? rows : (int64_t)dv.B * dv.H * dv.S;
+  int64_t gx = rescue ? 1 : (rows + kAppendWaves - 1) / kAppendWaves;
+  if (gx > 65535) gx = 65535;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(append_kernel, dim3((unsigned)gx, 2), dim3(kAppendWaves * 64), 0, s, dk, dv,
+                     rescue);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
+  return KVQ_OK;
+}

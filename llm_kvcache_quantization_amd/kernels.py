@@ -1,0 +1,439 @@
+"""Decode-attention entry points (q_len == 1) over quantized KV caches.
+
+Drop-in names and signatures of the reference kernels:
+
+* :func:`decode_attn_int8` -- ``src/kernels/triton_decode_attn_int8.py:306-519``
+* :func:`decode_attn_int4` -- ``src/kernels/triton_decode_attn_int4.py:62-121``
+
+Both keep the reference's argument names, defaults, validation order, exception
+types and zero-context rules.  They run the HIP split-K kernel of libkvq.so.
+The INT4 path reads the packed nibbles in place; the reference first unpacks the
+whole cache to int8.
+
+Build-native formats with no reference kernel:
+
+* :func:`decode_attn_int4_asym` -- asymmetric INT4 with static per-(head, group-32)
+  fp16 scale / zero-point, and optionally 4 fp16 K outlier channels per head.
+* :func:`decode_attn_k8v4` -- INT8 K (per-token/group scale) with asymmetric INT4 V.
+
+:class:`DecodePlan` prepares the ctypes parameter block once for fixed buffers.
+Repeated launches then cost one C call each, with no host synchronisation.  The
+engine and the benchmark use it.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Optional
+
+import torch
+
+from . import _capi as C
+
+_BLOCK_SIZES = (32, 64, 128, 256)
+HEAD_DIM = 128
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _scale_dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float16:
+        return C.KVQ_DTYPE_F16
+    if t.dtype == torch.float32:
+        return C.KVQ_DTYPE_F32
+    raise ValueError(f"scale dtype must be float16 or float32, got {t.dtype}")
+
+
+def kv_view_tok(codes: torch.Tensor, scale: torch.Tensor) -> C.KvView:
+    """View of codes [B,H,T,Dc] (int8/uint8) with per-(token, group) scale [B,H,T,G]."""
+    v = C.KvView()
+    v.codes = codes.data_ptr()
+    v.stride_b, v.stride_h, v.stride_t = (codes.stride(0), codes.stride(1), codes.stride(2))
+    v.scale = scale.data_ptr()
+    (v.scale_stride_b, v.scale_stride_h, v.scale_stride_t, v.scale_stride_g) = scale.stride()
+    v.scale_dtype = _scale_dtype_code(scale)
+    return v
+
+
+def kv_view_static(
+    codes: torch.Tensor,
+    scale: torch.Tensor,
+    zero_point: torch.Tensor,
+    outlier_idx: Optional[torch.Tensor] = None,
+    outlier_val: Optional[torch.Tensor] = None,
+) -> C.KvView:
+    """View of packed asymmetric INT4 codes [B,H,T,D/2] with static scale/zp [H,G]."""
+    v = C.KvView()
+    v.codes = codes.data_ptr()
+    v.stride_b, v.stride_h, v.stride_t = (codes.stride(0), codes.stride(1), codes.stride(2))
+    v.scale = scale.data_ptr()
+    v.scale_stride_b, v.scale_stride_t = 0, 0
+    v.scale_stride_h, v.scale_stride_g = scale.stride()
+    v.scale_dtype = C.KVQ_DTYPE_F16
+    v.zero_point = zero_point.data_ptr()
+    if outlier_idx is not None:
+        v.n_outlier = int(outlier_idx.shape[-1])
+        v.outlier_idx = outlier_idx.data_ptr()
+        v.outlier_val = outlier_val.data_ptr()
+        v.outlier_stride_b, v.outlier_stride_h, v.outlier_stride_t = (
+            outlier_val.stride(0), outlier_val.stride(1), outlier_val.stride(2))
+    return v
+
+
+class DecodePlan:
+    """A prepared kvq_decode_attn call over fixed tensors.
+
+    Holds references to every tensor it points at and owns its workspace and
+    output, so ``launch()`` is a single C call on the current stream.
+    """
+
+    def __init__(
+        self,
+        q: torch.Tensor,
+        k_format: int,
+        k_view: C.KvView,
+        v_format: int,
+        v_view: C.KvView,
+        context_lens: torch.Tensor,
+        kv_heads: int,
+        capacity: int,
+        sm_scale: float,
+        group_size: int,
+        inv_tau: Optional[torch.Tensor] = None,
+        out: Optional[torch.Tensor] = None,
+        chunk_tokens: int = 0,
+        keepalive: tuple = (),
+    ):
+        B, Hq, D = q.shape
+        self.q = q
+        self.context_lens = context_lens
+        self.inv_tau = inv_tau
+        self.out = torch.empty_like(q) if out is None else out
+        self._keep = keepalive
+        p = C.DecodeParams()
+        p.q = q.data_ptr()
+        p.q_stride_b, p.q_stride_h = q.stride(0), q.stride(1)
+        p.inv_tau = _ptr(inv_tau)
+        p.k_format, p.v_format = k_format, v_format
+        p.k, p.v = k_view, v_view
+        p.context_lens = context_lens.data_ptr()
+        p.batch, p.q_heads, p.kv_heads = B, Hq, kv_heads
+        p.head_dim, p.group_size = D, group_size
+        p.capacity = capacity
+        p.sm_scale = float(sm_scale)
+        env_chunk = os.environ.get("KVQ_CHUNK_TOKENS")
+        p.chunk_tokens = int(env_chunk) if (env_chunk and not chunk_tokens) else int(chunk_tokens)
+        L = C.lib()
+        nbytes = int(L.kvq_decode_workspace_bytes(ctypes.byref(p)))
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        p.workspace = self.workspace.data_ptr()
+        p.workspace_bytes = nbytes
+        p.out = self.out.data_ptr()
+        p.out_stride_b, p.out_stride_h = self.out.stride(0), self.out.stride(1)
+        self.params = p
+        self.chunk_tokens = int(L.kvq_decode_chunk_tokens(ctypes.byref(p)))
+        self._pp = ctypes.byref(self.params)
+        self.device = q.device
+
+    def launch(self, stream: Optional[int] = None) -> torch.Tensor:
+        s = C.stream_handle(self.device) if stream is None else stream
+        C.check(C.lib().kvq_decode_attn(self._pp, ctypes.c_void_p(s)))
+        return self.out
+
+
+def _bump_debug_stats(debug_stats, layer_idx, block_size):
+    # same keys as the reference wrapper (triton_decode_attn_int8.py:474-480),
+    # which patch_model.py and the reference tests read
+    if isinstance(debug_stats, dict):
+        debug_stats["triton_kernel_calls"] = int(debug_stats.get("triton_kernel_calls", 0)) + 1
+        debug_stats["triton_block_size"] = int(block_size)
+        if layer_idx is not None:
+            hits = debug_stats.setdefault("triton_layer_hits", {})
+            key = str(layer_idx)
+            hits[key] = int(hits.get(key, 0)) + 1
+
+
+def _resolve_block_size(block_size, max_ctx):
+    if block_size is None:
+        env = os.environ.get("KV_TRITON_BLOCK_SIZE")
+        if env:
+            try:
+                block_size = int(env)
+            except ValueError as exc:
+                raise ValueError(f"KV_TRITON_BLOCK_SIZE must be an integer, got {env!r}") from exc
+        else:
+            block_size = 128 if max_ctx >= 8192 else 64
+    if block_size not in _BLOCK_SIZES:
+        raise ValueError(f"Unsupported block_size={block_size}. Choose from [32, 64, 128, 256].")
+    return block_size
+
+
+def decode_attn_int8(
+    q,
+    k_cache,
+    v_cache,
+    k_scale,
+    v_scale,
+    context_lens,
+    sm_scale=None,
+    debug_stats: Optional[dict] = None,
+    layer_idx: Optional[int] = None,
+    block_size: Optional[int] = None,
+):
+    """q_len == 1 attention over INT8 K/V with per-(token, group) fp16 scales.
+
+    Same contract as ``decode_attn_int8`` (src/kernels/triton_decode_attn_int8.py:306-519):
+    q [B, Hq, D]; k_cache/v_cache int8 [B, Hkv, S, D]; k_scale/v_scale fp16
+    [B, Hkv, S, G]; context_lens [B]; returns [B, Hq, D] in q's dtype.  Rows whose
+    context length is 0 are zero.  ``block_size`` is validated like the reference,
+    but the HIP kernel picks its own split size.
+    """
+    return _decode_tok(q, k_cache, v_cache, k_scale, v_scale, context_lens, sm_scale,
+                       debug_stats, layer_idx, block_size, packed=False, head_dim=None)
+
+
+def decode_attn_int4(
+    q: torch.Tensor,
+    k_cache_int4: torch.Tensor,
+    v_cache_int4: torch.Tensor,
+    k_scale: torch.Tensor,
+    v_scale: torch.Tensor,
+    context_lens: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    *,
+    bit_packed: bool = True,
+    head_dim: Optional[int] = None,
+    debug_stats: Optional[dict] = None,
+    layer_idx: Optional[int] = None,
+    block_size: Optional[int] = None,
+) -> torch.Tensor:
+    """q_len == 1 attention over INT4 K/V (src/kernels/triton_decode_attn_int4.py:62-121).
+
+    Packed caches [B, Hkv, S, D/2] (byte = hi nibble even channel, +8 offset) are read
+    in place.  Unpacked caches (int8 codes in [-8, 7], [B, Hkv, S, D]) take the INT8
+    kernel, exactly as in the reference.
+    """
+    if q.ndim != 3:
+        raise ValueError(f"q must have shape [B, Hq, D], got {tuple(q.shape)}")
+    if head_dim is not None:
+        d = int(head_dim)
+        if d <= 0:
+            raise ValueError(f"head_dim must be positive, got {d}")
+    else:
+        d = q.shape[-1]
+    for name, cache in (("k", k_cache_int4), ("v", v_cache_int4)):
+        if not bit_packed:
+            if cache.shape[-1] != d:
+                raise ValueError(
+                    f"Unpacked INT4 cache last dim mismatch: got {cache.shape[-1]}, expected {d}")
+            if cache.stride(-1) != 1:
+                raise ValueError(
+                    "Unpacked INT4 cache inner dim must be contiguous (stride=1), "
+                    f"got stride={cache.stride(-1)}. Use .contiguous().")
+            if cache.dtype != torch.int8:
+                raise ValueError(
+                    f"Unpacked INT4 cache must be int8, got {cache.dtype}. "
+                    "Unpacked INT4 values should be stored as torch.int8.")
+        elif cache.shape[-1] * 2 != d:
+            raise ValueError(
+                f"Packed INT4 cache last dim mismatch: got {cache.shape[-1]}, expected {d // 2}")
+    return _decode_tok(q, k_cache_int4, v_cache_int4, k_scale, v_scale, context_lens, sm_scale,
+                       debug_stats, layer_idx, block_size, packed=bool(bit_packed), head_dim=d)
+
+
+def _decode_tok(q, k_cache, v_cache, k_scale, v_scale, context_lens, sm_scale, debug_stats,
+                layer_idx, block_size, packed, head_dim):
+    if sm_scale is None:
+        sm_scale = 1.0 / (q.shape[-1] ** 0.5)
+    if q.ndim != 3:
+        raise ValueError(f"q must have shape [B, Hq, D], got {tuple(q.shape)}")
+    if k_cache.ndim != 4 or v_cache.ndim != 4:
+        raise ValueError(
+            "k_cache/v_cache must have shape [B, Hkv, S, D], got "
+            f"{tuple(k_cache.shape)} / {tuple(v_cache.shape)}")
+    if k_scale.ndim != 4 or v_scale.ndim != 4:
+        raise ValueError(
+            "k_scale/v_scale must have shape [B, Hkv, S, G], got "
+            f"{tuple(k_scale.shape)} / {tuple(v_scale.shape)}")
+    if context_lens.ndim != 1:
+        raise ValueError(f"context_lens must be 1D, got {tuple(context_lens.shape)}")
+    if not q.is_cuda:
+        raise ValueError("decode_attn_int8 requires GPU (ROCm) tensors.")
+    if k_cache.dtype != torch.int8:
+        raise ValueError(f"k_cache must be torch.int8, got {k_cache.dtype}")
+    if v_cache.dtype != torch.int8:
+        raise ValueError(f"v_cache must be torch.int8, got {v_cache.dtype}")
+    if k_scale.dtype != torch.float16:
+        raise ValueError(
+            f"k_scale must be torch.float16 for the fused kernel, got {k_scale.dtype}. "
+            "Cast with k_scale.to(torch.float16) before calling.")
+    if v_scale.dtype != torch.float16:
+        raise ValueError(
+            f"v_scale must be torch.float16 for the fused kernel, got {v_scale.dtype}. "
+            "Cast with v_scale.to(torch.float16) before calling.")
+    if k_cache.stride(-1) != 1:
+        raise ValueError(
+            f"k_cache inner dim must be contiguous (stride=1), got stride={k_cache.stride(-1)}. "
+            "Use .contiguous() before passing to kernel.")
+    if v_cache.stride(-1) != 1:
+        raise ValueError(
+            f"v_cache inner dim must be contiguous (stride=1), got stride={v_cache.stride(-1)}.")
+    batch, q_heads, hd = q.shape
+    if hd == 0 or (hd & (hd - 1)) != 0:
+        raise ValueError(f"HEAD_DIM must be a power of 2, got {hd}.")
+    code_dim = hd // 2 if packed else hd
+    if k_cache.shape[0] != batch or v_cache.shape[0] != batch:
+        raise ValueError(
+            f"Batch mismatch: q={batch}, k={k_cache.shape[0]}, v={v_cache.shape[0]}")
+    if k_cache.shape[-1] != code_dim or v_cache.shape[-1] != code_dim:
+        raise ValueError(
+            f"Head dim mismatch: q={hd}, k={k_cache.shape[-1]}, v={v_cache.shape[-1]}")
+    if k_cache.shape[:3] != v_cache.shape[:3]:
+        raise ValueError(
+            f"k/v cache shape mismatch: {tuple(k_cache.shape)} vs {tuple(v_cache.shape)}")
+    if k_scale.shape[:3] != k_cache.shape[:3] or v_scale.shape[:3] != v_cache.shape[:3]:
+        raise ValueError(
+            "Scale and cache shapes mismatch: "
+            f"k_scale={tuple(k_scale.shape)}, v_scale={tuple(v_scale.shape)}, "
+            f"k={tuple(k_cache.shape)}, v={tuple(v_cache.shape)}")
+    if k_scale.shape[-1] != v_scale.shape[-1]:
+        raise ValueError(
+            f"k_scale/v_scale num_groups mismatch: k={k_scale.shape[-1]} vs v={v_scale.shape[-1]}.")
+    if context_lens.shape[0] != batch:
+        raise ValueError(
+            f"context_lens batch mismatch: expected {batch}, got {context_lens.shape[0]}")
+    kv_heads = k_cache.shape[1]
+    if q_heads % kv_heads != 0:
+        raise ValueError(
+            f"GQA head mismatch: q_heads={q_heads} must be a multiple of kv_heads={kv_heads}")
+    num_groups = k_scale.shape[-1]
+    if num_groups <= 0:
+        raise ValueError(f"num_groups must be > 0, got {num_groups}")
+    if hd % num_groups != 0:
+        raise ValueError(f"head_dim {hd} must be divisible by num_groups {num_groups}")
+    group_size = hd // num_groups
+    max_seq = int(k_cache.shape[2])
+    # the reference validates context lengths on the host (one sync); so does this wrapper
+    max_ctx = int(context_lens.max().item()) if context_lens.numel() else 0
+    min_ctx = int(context_lens.min().item()) if context_lens.numel() else 0
+    if min_ctx < 0:
+        raise ValueError(f"context_lens must be >= 0, got min={min_ctx}")
+    if max_ctx > max_seq:
+        raise ValueError(f"context_lens max ({max_ctx}) exceeds cache seq dim ({max_seq})")
+    if max_ctx == 0:
+        return torch.zeros_like(q)
+    if hd != HEAD_DIM:
+        raise NotImplementedError(f"the HIP decode kernel supports head_dim=128, got {hd}")
+    block_size = _resolve_block_size(block_size, max_ctx)
+
+    original_dtype = q.dtype
+    qk = q if q.dtype == torch.float16 else q.to(torch.float16)
+    if qk.stride(-1) != 1:
+        qk = qk.contiguous()
+    ctx = context_lens if context_lens.dtype == torch.int32 else context_lens.to(torch.int32)
+    if ctx.device != q.device:
+        ctx = ctx.to(q.device)
+    fmt = C.KVQ_FMT_INT4_SYM if packed else C.KVQ_FMT_INT8_SYM
+    plan = DecodePlan(
+        qk, fmt, kv_view_tok(k_cache, k_scale), fmt, kv_view_tok(v_cache, v_scale),
+        ctx, kv_heads, max_seq, sm_scale, group_size,
+        keepalive=(k_cache, v_cache, k_scale, v_scale))
+    _bump_debug_stats(debug_stats, layer_idx, block_size)
+    out = plan.launch()
+    if original_dtype != torch.float16:
+        out = out.to(original_dtype)
+    return out
+
+
+def decode_attn_int4_asym(
+    q: torch.Tensor,
+    k_codes: torch.Tensor,
+    v_codes: torch.Tensor,
+    k_scale: torch.Tensor,
+    k_zp: torch.Tensor,
+    v_scale: torch.Tensor,
+    v_zp: torch.Tensor,
+    context_lens: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    *,
+    inv_tau: Optional[torch.Tensor] = None,
+    k_outlier_idx: Optional[torch.Tensor] = None,
+    k_outlier_val: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention over the asymmetric INT4 group-32 format (build-native).
+
+    k_codes/v_codes: packed uint8/int8 [B, Hkv, S, 64]; k_scale/k_zp/v_scale/v_zp: fp16
+    [Hkv, 4] static parameters; optional k_outlier_idx int32 [Hkv, 4] and
+    k_outlier_val fp16 [B, Hkv, S, 4] (K channels stored verbatim).  inv_tau: fp16
+    [Hq] per-head query scale, applied as fp16(q * inv_tau) like the reference
+    (src/engine/patch_model.py:711-746).
+    """
+    _check_static_args(q, k_codes, v_codes, (k_scale, k_zp, v_scale, v_zp), context_lens)
+    if (k_outlier_idx is None) != (k_outlier_val is None):
+        raise ValueError("k_outlier_idx and k_outlier_val must be given together")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(q.shape[-1])
+    plan = DecodePlan(
+        q, C.KVQ_FMT_INT4_ASYM,
+        kv_view_static(k_codes, k_scale, k_zp, k_outlier_idx, k_outlier_val),
+        C.KVQ_FMT_INT4_ASYM, kv_view_static(v_codes, v_scale, v_zp),
+        _ctx_i32(context_lens, q.device), k_codes.shape[1], k_codes.shape[2], sm_scale, 32,
+        inv_tau=inv_tau,
+        keepalive=(k_codes, v_codes, k_scale, k_zp, v_scale, v_zp, k_outlier_idx, k_outlier_val))
+    return plan.launch()
+
+
+def decode_attn_k8v4(
+    q: torch.Tensor,
+    k_codes: torch.Tensor,
+    k_scale: torch.Tensor,
+    v_codes: torch.Tensor,
+    v_scale: torch.Tensor,
+    v_zp: torch.Tensor,
+    context_lens: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    *,
+    inv_tau: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """INT8 K (scale [B,Hkv,S,4], may be an expanded static view) + asymmetric INT4 V."""
+    if k_codes.dtype != torch.int8 or k_codes.shape[-1] != 128:
+        raise ValueError("k_codes must be int8 [B, Hkv, S, 128]")
+    if k_scale.ndim != 4 or k_scale.shape[-1] != 4:
+        raise ValueError("k_scale must be [B, Hkv, S, 4] (group 32)")
+    _check_static_args(q, v_codes, v_codes, (v_scale, v_zp), context_lens)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(q.shape[-1])
+    plan = DecodePlan(
+        q, C.KVQ_FMT_INT8_SYM, kv_view_tok(k_codes, k_scale),
+        C.KVQ_FMT_INT4_ASYM, kv_view_static(v_codes, v_scale, v_zp),
+        _ctx_i32(context_lens, q.device), k_codes.shape[1], k_codes.shape[2], sm_scale, 32,
+        inv_tau=inv_tau, keepalive=(k_codes, k_scale, v_codes, v_scale, v_zp))
+    return plan.launch()
+
+
+def _ctx_i32(context_lens: torch.Tensor, device) -> torch.Tensor:
+    c = context_lens if context_lens.dtype == torch.int32 else context_lens.to(torch.int32)
+    return c if c.device == device else c.to(device)
+
+
+def _check_static_args(q, k_codes, v_codes, params, context_lens):
+    if q.ndim != 3 or q.dtype != torch.float16 or q.shape[-1] != HEAD_DIM:
+        raise ValueError(f"q must be fp16 [B, Hq, 128], got {q.dtype} {tuple(q.shape)}")
+    if not q.is_cuda:
+        raise ValueError("requires GPU (ROCm) tensors")
+    for c in (k_codes, v_codes):
+        if c.ndim != 4 or c.shape[-1] != HEAD_DIM // 2 or c.dtype not in (torch.int8, torch.uint8):
+            raise ValueError(f"packed codes must be int8/uint8 [B, Hkv, S, 64], got {tuple(c.shape)}")
+        if c.stride(-1) != 1:
+            raise ValueError("packed codes must be contiguous in the last dim")
+    Hkv = k_codes.shape[1]
+    for t in params:
+        if t.dtype != torch.float16 or tuple(t.shape) != (Hkv, 4):
+            raise ValueError(f"static scale/zero-point must be fp16 [{Hkv}, 4], got {t.dtype} {tuple(t.shape)}")
+    if context_lens.ndim != 1 or context_lens.shape[0] != q.shape[0]:
+        raise ValueError("context_lens must be [B]")
+    if q.shape[1] % Hkv:
+        raise ValueError("q_heads must be a multiple of kv_heads")

@@ -1,0 +1,112 @@
+"""CPU restatement of the reference decode-attention oracles (test infrastructure).
+
+``decode_attn_int8_torch_ref`` follows ``_decode_attn_int8_torch_ref``
+(/root/reference/src/engine/patch_model.py:281-377) op for op.  K and V are
+dequantised in fp16 (code.to(fp16) * fp16 scale), then GQA heads are expanded
+with repeat_interleave, and scores, softmax and the weighted sum run in fp32 with
+the output cast to q's dtype.  It is also the timed CPU baseline of bench.py
+(``cpu_baseline.kind = "port"``).
+
+``decode_attn_asym_ref`` is the dequantise-then-attention oracle of the
+asymmetric group-32 format.  The reference has no kernel for this format.  It
+dequantises with q * s + zp in fp32 (src/quant/asymmetric_quant.py:196), writes
+the fp16 outlier channels back in verbatim, and applies the same fp32 attention.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .quant import dequantize_asymmetric_static, unpack_int4
+
+
+def prescale_q(q: torch.Tensor, inv_tau: Optional[torch.Tensor]) -> torch.Tensor:
+    """q * inv_tau in q's dtype (src/engine/patch_model.py:723,746)."""
+    if inv_tau is None:
+        return q
+    return q * inv_tau.to(dtype=q.dtype).view(1, -1, 1)
+
+
+def decode_attn_int8_torch_ref(q, k_int8, v_int8, k_scale, v_scale, context_lens, sm_scale):
+    """src/engine/patch_model.py:281-377."""
+    if q.ndim != 3:
+        raise ValueError(f"Expected q [B, H, D], got {q.shape}")
+    bsz, q_heads, head_dim = q.shape
+    _, kv_heads, _, _ = k_int8.shape
+    if q_heads % kv_heads:
+        raise ValueError("GQA unsupported: q_heads not divisible by kv_heads")
+    G = int(k_scale.shape[-1])
+    gs = head_dim // G
+    n_rep = q_heads // kv_heads
+    outs = []
+    for b in range(bsz):
+        ctx = int(context_lens[b].item())
+        if ctx <= 0:
+            outs.append(torch.zeros((q_heads, head_dim), dtype=q.dtype))
+            continue
+        kq = k_int8[b, :, :ctx, :]
+        vq = v_int8[b, :, :ctx, :]
+        ks = k_scale[b, :, :ctx, :]
+        vs = v_scale[b, :, :ctx, :]
+        k = (kq.reshape(kv_heads, ctx, G, gs).to(torch.float16) * ks.unsqueeze(-1)).view(kv_heads, ctx, head_dim)
+        v = (vq.reshape(kv_heads, ctx, G, gs).to(torch.float16) * vs.unsqueeze(-1)).view(kv_heads, ctx, head_dim)
+        if n_rep != 1:
+            k = k.repeat_interleave(n_rep, dim=0)
+            v = v.repeat_interleave(n_rep, dim=0)
+        scores = torch.einsum("hd,hsd->hs", q[b].float(), k.float()) * sm_scale
+        probs = torch.softmax(scores, dim=-1)
+        outs.append(torch.einsum("hs,hsd->hd", probs, v.float()).to(dtype=q.dtype))
+    return torch.stack(outs, dim=0)
+
+
+def decode_attn_int4_torch_ref(q, k_packed, v_packed, k_scale, v_scale, context_lens, sm_scale):
+    """Packed INT4 through the INT8 oracle after unpack_int4
+    (src/engine/patch_model.py:823-831,940-953; src/kernels/triton_decode_attn_int4.py:99-121)."""
+    return decode_attn_int8_torch_ref(q, unpack_int4(k_packed), unpack_int4(v_packed),
+                                      k_scale, v_scale, context_lens, sm_scale)
+
+
+def attention_fp32(q16: torch.Tensor, k: torch.Tensor, v: torch.Tensor, context_lens, sm_scale):
+    """fp32 GQA decode attention over dequantised k/v [B, Hkv, S, D] (float)."""
+    bsz, q_heads, head_dim = q16.shape
+    kv_heads = k.shape[1]
+    n_rep = q_heads // kv_heads
+    outs = []
+    for b in range(bsz):
+        ctx = int(context_lens[b].item())
+        if ctx <= 0:
+            outs.append(torch.zeros((q_heads, head_dim), dtype=q16.dtype))
+            continue
+        kb = k[b, :, :ctx].float().repeat_interleave(n_rep, dim=0)
+        vb = v[b, :, :ctx].float().repeat_interleave(n_rep, dim=0)
+        scores = torch.einsum("hd,hsd->hs", q16[b].float(), kb) * sm_scale
+        probs = torch.softmax(scores, dim=-1)
+        outs.append(torch.einsum("hs,hsd->hd", probs, vb).to(q16.dtype))
+    return torch.stack(outs, dim=0)
+
+
+def dequant_asym_k(k_packed, k_scale, k_zp, k_outlier_idx=None, k_outlier_val=None):
+    k = dequantize_asymmetric_static(unpack_int4(k_packed), k_scale, k_zp)
+    if k_outlier_idx is not None:
+        for h in range(k.shape[1]):
+            k[:, h, :, k_outlier_idx[h].long()] = k_outlier_val[:, h, :, :].float()
+    return k
+
+
+def decode_attn_asym_ref(q, k_packed, v_packed, k_scale, k_zp, v_scale, v_zp, context_lens,
+                         sm_scale, inv_tau=None, k_outlier_idx=None, k_outlier_val=None):
+    """Dequantise-then-attention oracle of the asymmetric INT4 group-32 format."""
+    k = dequant_asym_k(k_packed, k_scale, k_zp, k_outlier_idx, k_outlier_val)
+    v = dequantize_asymmetric_static(unpack_int4(v_packed), v_scale, v_zp)
+    return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)
+
+
+def decode_attn_k8v4_ref(q, k_int8, k_scale16, v_packed, v_scale, v_zp, context_lens, sm_scale,
+                         inv_tau=None):
+    """INT8 K dequantised as the reference does (fp16 product) + asymmetric INT4 V (fp32)."""
+    B, H, S, D = k_int8.shape
+    G = k_scale16.shape[-1]
+    k = (k_int8.view(B, H, S, G, D // G).to(torch.float16) * k_scale16.unsqueeze(-1)).view(B, H, S, D)
+    v = dequantize_asymmetric_static(unpack_int4(v_packed), v_scale, v_zp)
+    return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)

@@ -1,0 +1,268 @@
+"""CPU restatement of the reference quantize-on-append arithmetic (test infrastructure).
+
+Every function follows a reference function op for op, using PyTorch-CPU tensor
+ops in the same dtypes.  The reference path is itself PyTorch, so this is the most
+direct restatement.  The citations are to /root/reference/src.
+
+Scalar divisions (``absmax / 127.0`` etc.) are true divisions here, as on torch-CPU.
+On CUDA, torch multiplies by the reciprocal instead; only the dynamic and adaptive
+scale paths contain such divisions.  The static-scale paths of the north star divide
+tensor by tensor and agree on both devices.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+CLAMP_MIN = 1e-5
+
+
+def check_finite(x: torch.Tensor, name: str) -> None:
+    """src/quant/_common.py:13-20 -- NaN/Inf inputs are rejected with ValueError."""
+    if x.numel() == 0:
+        return
+    if torch.isnan(x).any():
+        raise ValueError(f"{name}: input contains NaN — refusing to quantize corrupt data")
+    if torch.isinf(x).any():
+        raise ValueError(f"{name}: input contains Inf — refusing to quantize corrupt data")
+
+
+def normalize_static_scale(scale: torch.Tensor, B: int, H: int, S: int, G: int) -> torch.Tensor:
+    """Broadcast a static scale to [B, H, S, G, 1] (src/quant/_common.py:37-135).
+
+    Accepted layouts: [H, G]; [B, H, G] / [1, H, G]; [B, H, S, G]; [B, H, S, G, 1].
+    """
+    if scale.ndim == 2:
+        if scale.shape[0] != H:
+            raise ValueError(f"calibration vs model heads mismatch: {scale.shape[0]} vs {H}")
+        view = scale[None, :, None, :, None]
+    elif scale.ndim == 3:
+        if scale.shape[1] != H or scale.shape[2] != G or scale.shape[0] not in (1, B):
+            raise ValueError(f"Unsupported 3D scale shape: {tuple(scale.shape)}")
+        view = scale[:, :, None, :, None]
+    elif scale.ndim == 4:
+        if scale.shape[1] != H:
+            raise ValueError(f"calibration vs model heads mismatch: {scale.shape[1]} vs {H}")
+        view = scale[..., None]
+    elif scale.ndim == 5:
+        view = scale
+    else:
+        raise ValueError(f"Unsupported scale ndim={scale.ndim}, shape={tuple(scale.shape)}")
+    return view.expand(B, H, S, G, 1)
+
+
+def quantize_symmetric_int8_with_scale(
+    x: torch.Tensor, scale: torch.Tensor, group_size: int
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """src/quant/int8_basic.py:111-164.
+
+    The scale is clamped to 1e-5 and cast to x's dtype (fp16).  The quotient
+    x / s is computed in fp16, so it is rounded to fp16 before torch.round
+    (ties to even).  The result is clamped to [-127, 127].
+    """
+    if not x.is_floating_point():
+        raise ValueError(f"Input tensor must be float, got {x.dtype}")
+    check_finite(x, "quantize_symmetric_int8_with_scale")
+    D = x.shape[-1]
+    gs = D if group_size == -1 else group_size
+    if D % gs:
+        raise ValueError(f"head_dim {D} must be divisible by group_size {gs}")
+    B, H, S, _ = x.shape
+    G = D // gs
+    xr = x.view(B, H, S, G, gs)
+    s = normalize_static_scale(scale, B, H, S, G).clamp(min=CLAMP_MIN).to(x.dtype)
+    q = torch.round(xr / s).clamp(-127, 127).to(torch.int8)
+    return q.view(B, H, S, D), s.squeeze(-1)
+
+
+def quantize_symmetric_int8(
+    x: torch.Tensor, percentile: float = 100.0, group_size: int = 128
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Dynamic INT8, absmax branch (src/quant/int8_basic.py:18-108, percentile >= 100)."""
+    if percentile < 100.0:
+        raise NotImplementedError("percentile clipping is not restated (absmax branch only)")
+    check_finite(x, "quantize_symmetric_int8")
+    B, H, S, D = x.shape
+    gs = D if group_size == -1 else group_size
+    G = D // gs
+    xr = x.view(B, H, S, G, gs)
+    am = xr.abs().amax(dim=-1, keepdim=True).clamp(min=CLAMP_MIN).to(x.dtype)
+    s = am / 127.0
+    q = torch.round(xr / s).clamp(-127, 127).to(torch.int8)
+    return q.view(B, H, S, D), s.squeeze(-1)
+
+
+def quantize_symmetric_int4_with_scale(
+    x: torch.Tensor, scale: torch.Tensor, group_size: int
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """src/quant/int4_basic.py:115-159: fp32 scale clamped to 1e-5, fp32 quotient,
+    round half to even, clamp to [-7, 7]."""
+    if not x.is_floating_point():
+        raise ValueError(f"Input tensor must be float, got {x.dtype}")
+    check_finite(x, "quantize_symmetric_int4_with_scale")
+    B, H, S, D = x.shape
+    gs = D if group_size == -1 else group_size
+    G = D // gs
+    xr = x.view(B, H, S, G, gs)
+    s = normalize_static_scale(scale, B, H, S, G).to(torch.float32).clamp(min=CLAMP_MIN)
+    q = torch.round(xr / s).clamp(-7, 7).to(torch.int8)
+    return q.view(B, H, S, D), s.squeeze(-1)
+
+
+def quantize_symmetric_int4(
+    x: torch.Tensor, percentile: float = 100.0, group_size: int = 32
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Dynamic INT4, absmax branch (src/quant/int4_basic.py:24-112, percentile >= 100)."""
+    if percentile < 100.0:
+        raise NotImplementedError("percentile clipping is not restated (absmax branch only)")
+    check_finite(x, "quantize_symmetric_int4")
+    B, H, S, D = x.shape
+    gs = D if group_size == -1 else group_size
+    G = D // gs
+    xr = x.view(B, H, S, G, gs)
+    am = xr.abs().amax(dim=-1, keepdim=True).clamp(min=CLAMP_MIN).to(torch.float32)
+    s = am / 7.0
+    q = torch.round(xr / s).clamp(-7, 7).to(torch.int8)
+    return q.view(B, H, S, D), s.to(torch.float32).squeeze(-1)
+
+
+def pack_int4(q: torch.Tensor) -> torch.Tensor:
+    """src/quant/int4_basic.py:230-272: +8 offset, high nibble = element 2i."""
+    if q.dtype != torch.int8:
+        raise ValueError(f"pack_int4 expects int8 input, got {q.dtype}")
+    if q.shape[-1] % 2:
+        raise ValueError("Last dimension must be even for packing")
+    u = (q.to(torch.int16) + 8).to(torch.uint8)
+    u = u.view(*q.shape[:-1], q.shape[-1] // 2, 2)
+    return ((u[..., 0] << 4) | u[..., 1]).to(torch.int8)
+
+
+def unpack_int4(packed: torch.Tensor) -> torch.Tensor:
+    """src/quant/int4_basic.py:275-303."""
+    if packed.dtype not in (torch.int8, torch.uint8):
+        raise ValueError(f"unpack_int4 expects int8 packed input, got {packed.dtype}")
+    u = packed.view(torch.uint8) if packed.dtype == torch.int8 else packed
+    hi = (u >> 4) & 0x0F
+    lo = u & 0x0F
+    out = torch.stack([hi, lo], dim=-1).view(*packed.shape[:-1], packed.shape[-1] * 2)
+    return (out.to(torch.int16) - 8).to(torch.int8)
+
+
+# ---------------------------------------------------------------- cache scale policies
+
+
+def int8_cache_quantize(
+    x: torch.Tensor,
+    static_scale: Optional[torch.Tensor],
+    group_size: int,
+    adaptive: bool = False,
+    margin: float = 1.0,
+    clip_percentile: float = 100.0,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The quantize step of INT8KVCache.append (src/cache/int8_cache.py:389-453).
+
+    Returns (codes int8 [B,H,S,D], scale [B,H,S,G] in the quantizer's dtype).
+    """
+    if static_scale is None:
+        return quantize_symmetric_int8(x, clip_percentile, group_size)
+    scale = static_scale
+    if adaptive:
+        B, H, S, D = x.shape
+        G = D // group_size
+        st = _expand_cache_scale(scale, B, H, S, G).to(torch.float32).clamp(min=CLAMP_MIN)
+        dyn = x.view(B, H, S, G, group_size).abs().amax(dim=-1).float().clamp(min=CLAMP_MIN) / 127.0
+        scale = torch.maximum(st * float(margin), dyn)
+    return quantize_symmetric_int8_with_scale(x, scale, group_size)
+
+
+def _expand_cache_scale(scale, B, H, S, G):
+    """src/cache/int8_cache.py:298-326 / int4_cache.py:317-342."""
+    if scale.ndim == 2:
+        v = scale[None, :, None, :]
+    elif scale.ndim == 4:
+        v = scale
+    elif scale.ndim == 5 and scale.shape[-1] == 1:
+        v = scale.squeeze(-1)
+    else:
+        raise ValueError(f"Unsupported static scale shape: {tuple(scale.shape)}")
+    return v.expand(B, H, S, G)
+
+
+def int4_dynamic_group_scale(x: torch.Tensor, group_size: int) -> torch.Tensor:
+    """src/cache/int4_cache.py:344-358: absmax/7 per (b, h, s, group), fp32."""
+    B, H, S, D = x.shape
+    am = x.view(B, H, S, D // group_size, group_size).abs().amax(dim=-1)
+    return am.float().clamp(min=CLAMP_MIN) / 7.0
+
+
+def outlier_rescue(x: torch.Tensor, scale: torch.Tensor, ratio: float, group_size: int) -> torch.Tensor:
+    """src/cache/int4_cache.py:360-390 (global torch.quantile threshold)."""
+    if ratio <= 0.0:
+        return scale
+    dyn = int4_dynamic_group_scale(x, group_size)
+    if ratio >= 1.0:
+        return torch.maximum(scale, dyn)
+    thr = torch.quantile(dyn.float().reshape(-1), max(0.0, min(1.0, 1.0 - ratio))).to(dyn.dtype)
+    return torch.where(dyn >= thr, torch.maximum(scale, dyn), scale)
+
+
+def int4_cache_quantize(
+    x: torch.Tensor,
+    static_scale: Optional[torch.Tensor],
+    group_size: int,
+    adaptive: bool = False,
+    margin: float = 1.0,
+    mixed_rescue: bool = False,
+    outlier_rescue_ratio: float = 0.0,
+    clip_percentile: float = 100.0,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The quantize step of INT4KVCache.append (src/cache/int4_cache.py:447-529).
+
+    Returns (codes int8 in [-7, 7] [B,H,S,D], fp32 scale [B,H,S,G]).
+    """
+    if static_scale is None:
+        return quantize_symmetric_int4(x, clip_percentile, group_size)
+    B, H, S, D = x.shape
+    G = D // group_size
+    s = _expand_cache_scale(static_scale, B, H, S, G).to(torch.float32).clamp(min=CLAMP_MIN)
+    if adaptive:
+        s = torch.maximum(s * float(margin), int4_dynamic_group_scale(x, group_size))
+    if mixed_rescue:
+        s = torch.maximum(s, int4_dynamic_group_scale(x, group_size))
+    s = outlier_rescue(x, s, outlier_rescue_ratio, group_size)
+    q, s = quantize_symmetric_int4_with_scale(x, s, group_size)
+    return q, s.to(torch.float32)
+
+
+# ---------------------------------------------------------------- asymmetric, static g32
+
+
+def quantize_asymmetric_static(
+    x: torch.Tensor, scale16: torch.Tensor, zp16: torch.Tensor, group_size: int = 32
+) -> torch.Tensor:
+    """Asymmetric INT4 with static per-(head, group) parameters.
+
+    The element formula is the reference's static-parameter K quantizer:
+    q = clamp(round((fp32(x) - zp) / s), -8, 7).  See
+    tests/test_fused_quantize_pack.py:8-17 and src/kernels/triton_quantize_pack_int4.py:51-55.
+    Here it is applied per group of 32 channels with fp16 parameters widened to fp32
+    (the BASELINE g32 format).  Returns int8 codes [B,H,S,D] in [-8, 7].
+    """
+    check_finite(x, "quantize_asymmetric_static")
+    B, H, S, D = x.shape
+    G = D // group_size
+    xr = x.float().view(B, H, S, G, group_size)
+    s = scale16.float()[None, :, None, :, None]
+    z = zp16.float()[None, :, None, :, None]
+    q = torch.round((xr - z) / s).clamp(-8, 7).to(torch.int8)
+    return q.view(B, H, S, D)
+
+
+def dequantize_asymmetric_static(q: torch.Tensor, scale16, zp16, group_size: int = 32) -> torch.Tensor:
+    """q * s + zp in fp32 (src/quant/asymmetric_quant.py:196 with fp32 parameters)."""
+    B, H, S, D = q.shape
+    G = D // group_size
+    s = scale16.float()[None, :, None, :, None]
+    z = zp16.float()[None, :, None, :, None]
+    return (q.view(B, H, S, G, group_size).float() * s + z).view(B, H, S, D)

@@ -1,0 +1,367 @@
+"""GPU parity: the HIP kernels of libkvq.so against the CPU oracle.
+
+Quantized codes and scales must be bit-exact.  Attention outputs must be within
+max-abs 2e-3 of the dequantise-then-attention oracle with cosine >= 0.9999 (the
+tolerance BASELINE.json's north star states for fp16 outputs).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import attn as OA
+from oracle import quant as OQ
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+ATOL = 2e-3
+COS_MIN = 0.9999
+
+
+def _lib():
+    import llm_kvcache_quantization_amd as K  # noqa: F401
+    from llm_kvcache_quantization_amd import _capi
+
+    _capi.lib()
+    return K
+
+
+def assert_close(out: torch.Tensor, ref: torch.Tensor, tag: str):
+    o = out.detach().float().cpu()
+    r = ref.detach().float().cpu()
+    assert o.shape == r.shape, (tag, o.shape, r.shape)
+    assert torch.isfinite(o).all(), tag
+    err = (o - r).abs().max().item()
+    cos = torch.nn.functional.cosine_similarity(o.flatten(), r.flatten(), dim=0).item() \
+        if r.abs().max() > 0 else 1.0
+    print(f"[{tag}] max_abs={err:.3e} cos={cos:.7f}", flush=True)
+    assert err <= ATOL and cos >= COS_MIN, (tag, err, cos)
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------- append: bit-exact
+
+
+@pytest.mark.parametrize("mode", ["static_f16", "static_f32", "adaptive", "dynamic"])
+@pytest.mark.parametrize("S,gs", [(1, 32), (37, 16), (5, 128)])
+def test_append_int8_bitexact(mode, S, gs):
+    K = _lib()
+    g = gen(11 + S + gs)
+    B, H, D = 3, 2, 128
+    G = D // gs
+    k = (torch.randn(B, H, S, D, generator=g) * 2).to(torch.float16)
+    v = torch.randn(B, H, S, D, generator=g).to(torch.float16)
+    k[0, 1, 0, 3] = 40.0  # forces clipping for static scales
+    st = (torch.rand(1, H, G, generator=g) * 0.02 + 0.005)
+    kw = {}
+    if mode == "static_f16":
+        sk, sv = st.to(torch.float16), (st * 0.5).to(torch.float16)
+    elif mode == "static_f32":
+        sk, sv = st, st * 0.5
+    elif mode == "adaptive":
+        sk, sv = st.to(torch.float16), (st * 0.5).to(torch.float16)
+        kw = dict(adaptive_static_scales=True, adaptive_static_margin=1.25)
+    else:
+        sk = sv = None
+        kw = dict(clip_percentile=100.0)
+    cache = K.INT8KVCache(1, device=DEV, group_size=gs, static_k_scale=sk, static_v_scale=sv,
+                          check_numerics=False, **kw)
+    cache.append(0, k.to(DEV), v.to(DEV))
+    cache.append(0, k.to(DEV), v.to(DEV))  # second append lands at write_pos = S
+    kq, vq, ks, vs = cache.get_int8_tensors(0)
+    for x, stt, q_gpu, s_gpu, tag in ((k, sk, kq, ks, "k"), (v, sv, vq, vs, "v")):
+        ref_q, ref_s = OQ.int8_cache_quantize(
+            x, None if stt is None else stt[0], gs, adaptive=(mode == "adaptive"), margin=1.25)
+        for rep in range(2):
+            got_q = q_gpu[:, :, rep * S:(rep + 1) * S].cpu()
+            got_s = s_gpu[:, :, rep * S:(rep + 1) * S].cpu()
+            assert torch.equal(got_q, ref_q), (mode, tag, (got_q != ref_q).sum().item())
+            assert torch.equal(got_s.float(), ref_s.float()), (mode, tag)
+
+
+@pytest.mark.parametrize("mode", ["static", "adaptive", "mixed", "rescue", "rescue_all", "dynamic"])
+@pytest.mark.parametrize("S", [1, 9])
+def test_append_int4_sym_bitexact(mode, S):
+    K = _lib()
+    g = gen(21 + S)
+    B, H, D, gs = 4, 2, 128, 32
+    k = (torch.randn(B, H, S, D, generator=g) * 1.5).to(torch.float16)
+    v = torch.randn(B, H, S, D, generator=g).to(torch.float16)
+    k[1, 0, 0, 70] = 25.0
+    v[2, 1, S - 1, 3] = -30.0
+    st = torch.rand(H, D // gs, generator=g) * 0.3 + 0.1
+    kw = dict(outlier_rescue_ratio=0.0)
+    ref_kw = {}
+    sk, sv = st, st * 0.8
+    if mode == "adaptive":
+        kw.update(adaptive_static_scales=True, adaptive_static_margin=0.9)
+        ref_kw = dict(adaptive=True, margin=0.9)
+    elif mode == "mixed":
+        kw.update(mixed_rescue=True)
+        ref_kw = dict(mixed_rescue=True)
+    elif mode == "rescue":
+        kw.update(outlier_rescue_ratio=0.01)
+        ref_kw = dict(outlier_rescue_ratio=0.01)
+    elif mode == "rescue_all":
+        kw.update(outlier_rescue_ratio=1.0)
+        ref_kw = dict(outlier_rescue_ratio=1.0)
+    elif mode == "dynamic":
+        sk = sv = None
+        kw.update(clip_percentile=100.0)
+    cache = K.INT4KVCache(1, device=DEV, group_size=gs, static_k_scale=None if sk is None else sk[None],
+                          static_v_scale=None if sv is None else sv[None], check_numerics=False, **kw)
+    cache.append(0, k.to(DEV), v.to(DEV))
+    kp, vp, ks, vs = cache.get_int4_tensors(0)
+    for x, stt, p_gpu, s_gpu, tag in ((k, sk, kp, ks, "k"), (v, sv, vp, vs, "v")):
+        ref_q, ref_s = OQ.int4_cache_quantize(x, stt, gs, **ref_kw)
+        assert torch.equal(p_gpu.cpu(), OQ.pack_int4(ref_q)), (mode, tag)
+        assert torch.equal(s_gpu.cpu().float(), ref_s.float()), (mode, tag)
+
+
+@pytest.mark.parametrize("outliers", [False, True])
+def test_append_asym_bitexact(outliers):
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[3]
+    tables = SY.calibrate(cfg, 0)
+    g = gen(31)
+    k, v = SY.draw_kv(cfg, 0, 3, 19, g)
+    oidx = tables.k_outlier_idx if outliers else None
+    L = 1
+    cache = K.INT4AsymKVCache(L, tables.k_scale[None], tables.k_zp[None], tables.v_scale[None],
+                              tables.v_zp[None], device=DEV,
+                              k_outlier_idx=None if oidx is None else oidx[None])
+    cache.append(0, k[:, :, :7].to(DEV), v[:, :, :7].to(DEV))
+    cache.append(0, k[:, :, 7:].to(DEV), v[:, :, 7:].to(DEV))
+    kc, vc, *_rest, ko = cache.get_int4_g32_tensors(0)
+    ref_k = OQ.pack_int4(OQ.quantize_asymmetric_static(k, tables.k_scale, tables.k_zp)).view(torch.uint8)
+    ref_v = OQ.pack_int4(OQ.quantize_asymmetric_static(v, tables.v_scale, tables.v_zp)).view(torch.uint8)
+    assert torch.equal(kc.cpu(), ref_k)
+    assert torch.equal(vc.cpu(), ref_v)
+    if outliers:
+        ref_o = torch.stack([k[:, h, :, oidx[h].long()] for h in range(cfg.kv_heads)], dim=1)
+        assert torch.equal(ko.cpu(), ref_o)
+
+
+def test_append_nan_raises_and_does_not_advance():
+    K = _lib()
+    cache = K.INT8KVCache(1, device=DEV, group_size=32,
+                          static_k_scale=torch.full((1, 2, 4), 0.01, dtype=torch.float16),
+                          static_v_scale=torch.full((1, 2, 4), 0.01, dtype=torch.float16))
+    x = torch.randn(1, 2, 1, 128, dtype=torch.float16, device=DEV)
+    cache.append(0, x, x)
+    bad = x.clone()
+    bad[0, 1, 0, 9] = float("nan")
+    with pytest.raises(ValueError):
+        cache.append(0, bad, x)
+    assert cache.get_seq_len() == 1
+    big = x * 100
+    with pytest.warns(RuntimeWarning):
+        cache.append(0, big, x)
+
+
+# ---------------------------------------------------------------- decode: tolerance parity
+
+
+def _rand_int8_case(B, Hq, Hkv, S, G, g):
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+    k = torch.randint(-128, 128, (B, Hkv, S, 128), generator=g, dtype=torch.int8)
+    v = torch.randint(-128, 128, (B, Hkv, S, 128), generator=g, dtype=torch.int8)
+    ks = (torch.rand(B, Hkv, S, G, generator=g) * 0.01 + 1e-3).to(torch.float16)
+    vs = (torch.rand(B, Hkv, S, G, generator=g) * 0.01 + 1e-3).to(torch.float16)
+    return q, k, v, ks, vs
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,G,ctx", [
+    (1, 12, 2, 4096, 4, [4096]),
+    (3, 12, 2, 700, 4, [700, 37, 0]),
+    (2, 8, 2, 513, 8, [1, 513]),
+    (2, 7, 7, 300, 1, [129, 300]),
+    (4, 16, 1, 2048, 2, [2048, 2047, 1000, 31]),
+])
+def test_decode_int8_parity(B, Hq, Hkv, S, G, ctx):
+    K = _lib()
+    g = gen(B * 1000 + S)
+    q, k, v, ks, vs = _rand_int8_case(B, Hq, Hkv, S, G, g)
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    sm = 1 / math.sqrt(128)
+    ref = OA.decode_attn_int8_torch_ref(q, k, v, ks, vs, cl, sm)
+    stats = {}
+    out = K.decode_attn_int8(q.to(DEV), k.to(DEV), v.to(DEV), ks.to(DEV), vs.to(DEV), cl.to(DEV),
+                             sm_scale=sm, debug_stats=stats, layer_idx=3)
+    assert_close(out, ref, f"int8 B{B} Hq{Hq} Hkv{Hkv} S{S} G{G}")
+    for b, c in enumerate(ctx):
+        if c == 0:
+            assert torch.all(out[b] == 0)
+    assert stats["triton_kernel_calls"] == 1 and stats["triton_layer_hits"] == {"3": 1}
+
+
+def test_decode_int8_static_expanded_scales_and_fp32_q():
+    K = _lib()
+    g = gen(77)
+    B, Hq, Hkv, S = 2, 12, 2, 1000
+    q, k, v, _, _ = _rand_int8_case(B, Hq, Hkv, S, 4, g)
+    st = (torch.rand(Hkv, 4, generator=g) * 0.01 + 1e-3).to(torch.float16)
+    ks = st[None, :, None, :].expand(B, Hkv, S, 4)
+    cl = torch.tensor([S, 999], dtype=torch.int32)
+    ref = OA.decode_attn_int8_torch_ref(q, k, v, ks, ks, cl, 0.1)
+    out = K.decode_attn_int8(q.float().to(DEV), k.to(DEV), v.to(DEV), ks.to(DEV), ks.to(DEV),
+                             cl.to(DEV), sm_scale=0.1)
+    assert out.dtype == torch.float32
+    assert_close(out, ref.float(), "int8 static-expanded")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,ctx", [
+    (2, 12, 2, 2048, [2048, 1500]),
+    (1, 28, 4, 4096, [4096]),
+    (3, 6, 1, 257, [1, 0, 257]),
+])
+def test_decode_int4_packed_parity(B, Hq, Hkv, S, ctx):
+    K = _lib()
+    g = gen(S + B)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+    kc = torch.randint(-8, 8, (B, Hkv, S, 128), generator=g, dtype=torch.int8)
+    vc = torch.randint(-8, 8, (B, Hkv, S, 128), generator=g, dtype=torch.int8)
+    ks = (torch.rand(B, Hkv, S, 4, generator=g) * 0.3 + 0.01).to(torch.float16)
+    vs = (torch.rand(B, Hkv, S, 4, generator=g) * 0.3 + 0.01).to(torch.float16)
+    kp, vp = OQ.pack_int4(kc), OQ.pack_int4(vc)
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    ref = OA.decode_attn_int4_torch_ref(q, kp, vp, ks, vs, cl, 0.0883883)
+    out = K.decode_attn_int4(q.to(DEV), kp.to(DEV), vp.to(DEV), ks.to(DEV), vs.to(DEV), cl.to(DEV),
+                             sm_scale=0.0883883, bit_packed=True, head_dim=128)
+    assert_close(out, ref, f"int4 packed B{B} S{S}")
+    # unpacked int8 codes take the INT8 kernel, as in the reference wrapper
+    out_u = K.decode_attn_int4(q.to(DEV), kc.to(DEV), vc.to(DEV), ks.to(DEV), vs.to(DEV),
+                               cl.to(DEV), sm_scale=0.0883883, bit_packed=False)
+    assert_close(out_u, ref, f"int4 unpacked B{B} S{S}")
+
+
+def _asym_case(cfg_idx, B, S, ctx, seed, outliers=True):
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[cfg_idx]
+    t = SY.calibrate(cfg, 0)
+    g = gen(seed)
+    k, v = SY.draw_kv(cfg, 0, B, S, g)
+    q = SY.draw_q(cfg, B, g)
+    tau = SY.inv_tau(cfg)[0]
+    kq = OQ.pack_int4(OQ.quantize_asymmetric_static(k, t.k_scale, t.k_zp))
+    vq = OQ.pack_int4(OQ.quantize_asymmetric_static(v, t.v_scale, t.v_zp))
+    oidx = t.k_outlier_idx if outliers else None
+    oval = None
+    if outliers:
+        oval = torch.stack([k[:, h, :, oidx[h].long()] for h in range(cfg.kv_heads)], dim=1).contiguous()
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    return cfg, t, q, tau, kq, vq, oidx, oval, cl
+
+
+@pytest.mark.parametrize("cfg_idx,B,S,ctx,outliers", [
+    (3, 2, 4096, [4096, 3001], True),
+    (2, 3, 2048, [2048, 1, 777], True),
+    (3, 1, 1000, [1000], False),
+    (3, 2, 300, [0, 300], True),
+])
+def test_decode_asym_parity(cfg_idx, B, S, ctx, outliers):
+    K = _lib()
+    cfg, t, q, tau, kq, vq, oidx, oval, cl = _asym_case(cfg_idx, B, S, ctx, 40 + S, outliers)
+    sm = 1 / math.sqrt(128)
+    ref = OA.decode_attn_asym_ref(q, kq, vq, t.k_scale, t.k_zp, t.v_scale, t.v_zp, cl, sm,
+                                  inv_tau=tau, k_outlier_idx=oidx, k_outlier_val=oval)
+    d = lambda x: None if x is None else x.to(DEV)
+    out = K.decode_attn_int4_asym(q.to(DEV), kq.to(DEV), vq.to(DEV), d(t.k_scale), d(t.k_zp),
+                                  d(t.v_scale), d(t.v_zp), cl.to(DEV), sm, inv_tau=tau.to(DEV),
+                                  k_outlier_idx=d(oidx), k_outlier_val=d(oval))
+    assert_close(out, ref, f"asym cfg{cfg_idx} B{B} S{S} out={outliers}")
+
+
+def test_decode_k8v4_parity_ragged():
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[4]
+    t = SY.calibrate(cfg, 0)
+    g = gen(4)
+    B, S = 3, 3000
+    k, v = SY.draw_kv(cfg, 0, B, S, g)
+    q = SY.draw_q(cfg, B, g)
+    tau = SY.inv_tau(cfg)[0]
+    k8, ks16 = OQ.quantize_symmetric_int8_with_scale(k, t.k_scale, 32)
+    vq = OQ.pack_int4(OQ.quantize_asymmetric_static(v, t.v_scale, t.v_zp))
+    cl = torch.tensor([3000, 1234, 4097 - 4096], dtype=torch.int32)
+    ref = OA.decode_attn_k8v4_ref(q, k8, ks16, vq, t.v_scale, t.v_zp, cl, 0.0883883, inv_tau=tau)
+    out = K.decode_attn_k8v4(q.to(DEV), k8.to(DEV), ks16.to(DEV), vq.to(DEV), t.v_scale.to(DEV),
+                             t.v_zp.to(DEV), cl.to(DEV), 0.0883883, inv_tau=tau.to(DEV))
+    assert_close(out, ref, "k8v4 ragged")
+
+
+def test_decode_kat_single_token_and_zero_context():
+    K = _lib()
+    B, H, S = 2, 4, 64
+    q = torch.randn(B, H, 128, dtype=torch.float16)
+    k = torch.randint(-5, 5, (B, H, S, 128), dtype=torch.int8)
+    v = torch.randint(-100, 100, (B, H, S, 128), dtype=torch.int8)
+    s = torch.ones(B, H, S, 4, dtype=torch.float16)
+    cl = torch.tensor([1, 0], dtype=torch.int32)
+    out = K.decode_attn_int8(q.to(DEV), k.to(DEV), v.to(DEV), s.to(DEV), s.to(DEV), cl.to(DEV))
+    assert torch.equal(out[0].cpu(), v[0, :, 0].to(torch.float16))  # one token: output = V
+    assert torch.all(out[1] == 0)
+    allzero = K.decode_attn_int8(q.to(DEV), k.to(DEV), v.to(DEV), s.to(DEV), s.to(DEV),
+                                 torch.zeros(2, dtype=torch.int32, device=DEV))
+    assert torch.all(allzero == 0)
+
+
+def test_decode_split_invariance_and_determinism():
+    """Results do not depend on the split size beyond tolerance and repeat bit-exactly."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import _capi as C
+    from llm_kvcache_quantization_amd.kernels import DecodePlan, kv_view_static
+
+    cfg, t, q, tau, kq, vq, oidx, oval, cl = _asym_case(3, 2, 8192, [8192, 5000], 5)
+    d = lambda x: x.to(DEV)
+    outs = []
+    for chunk in (128, 256, 1024, 4096, 8192):
+        plan = DecodePlan(d(q), C.KVQ_FMT_INT4_ASYM,
+                          kv_view_static(d(kq), d(t.k_scale), d(t.k_zp), d(oidx), d(oval)),
+                          C.KVQ_FMT_INT4_ASYM, kv_view_static(d(vq), d(t.v_scale), d(t.v_zp)),
+                          d(cl), cfg.kv_heads, 8192, 1 / math.sqrt(128), 32, inv_tau=d(tau),
+                          chunk_tokens=chunk)
+        a = plan.launch().clone()
+        b = plan.launch().clone()
+        assert torch.equal(a, b), chunk
+        outs.append(a.cpu())
+    for o in outs[1:]:
+        assert (o.float() - outs[0].float()).abs().max() <= ATOL
+
+
+def test_cfg3_full_size_rows():
+    """One layer at the headline shape (B=8, Hq=28, Hkv=4, 32768 tokens) built by the HIP
+    append kernel; rows 0 and 7 are checked against the oracle."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[3]
+    t = SY.calibrate(cfg, 0)
+    g = torch.Generator(device=DEV).manual_seed(SY.seed_for(3, 0))
+    k, v = SY.draw_kv(cfg, 0, cfg.batch, cfg.context, g, device=DEV)
+    q = SY.draw_q(cfg, cfg.batch, g, device=DEV)
+    tau = SY.inv_tau(cfg)[0].to(DEV)
+    cache = K.INT4AsymKVCache(1, t.k_scale[None], t.k_zp[None], t.v_scale[None], t.v_zp[None],
+                              device=DEV, k_outlier_idx=t.k_outlier_idx[None])
+    cache.append(0, k, v)
+    kc, vc, ks, kz, vs, vz, oi, ov = cache.get_int4_g32_tensors(0)
+    cl = torch.full((cfg.batch,), cfg.context, dtype=torch.int32, device=DEV)
+    out = K.decode_attn_int4_asym(q, kc, vc, ks, kz, vs, vz, cl, 1 / math.sqrt(128), inv_tau=tau,
+                                  k_outlier_idx=oi, k_outlier_val=ov)
+    for b in (0, cfg.batch - 1):
+        sl = slice(b, b + 1)
+        kq_ref = OQ.pack_int4(OQ.quantize_asymmetric_static(k[sl].cpu(), t.k_scale, t.k_zp))
+        assert torch.equal(kc[sl].cpu(), kq_ref.view(torch.uint8))
+        ref = OA.decode_attn_asym_ref(q[sl].cpu(), kc[sl].cpu(), vc[sl].cpu(), t.k_scale, t.k_zp,
+                                      t.v_scale, t.v_zp, cl[sl].cpu(), 1 / math.sqrt(128),
+                                      inv_tau=tau.cpu(), k_outlier_idx=t.k_outlier_idx,
+                                      k_outlier_val=ov[sl].cpu())
+        assert_close(out[sl], ref, f"cfg3 full row {b}")

@@ -1,0 +1,340 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+How each oracle function is pinned, chosen so that a plausible mistake (a dropped
+term, a wrong sign or index, a swapped nibble) fails at least one check:
+
+* quantize_symmetric_int8_with_scale: exhaustive over every finite fp16 input and a
+  sweep of scales, against a numpy closed form.  That closed form divides in float64,
+  rounds to fp16, then to an integer with ties-to-even.  Double rounding is exact here
+  because 53 >= 2*11 + 2.  Plus the clamp KATs.
+* quantize_symmetric_int4_with_scale / dynamic INT4: numpy float64 -> float32 closed
+  form, plus the KATs of reference tests/test_int4_cache.py:559-586.
+* pack_int4 / unpack_int4: the KATs of tests/test_int4_cache.py:469-557 and the byte
+  layout (high nibble = even element).
+* quantize_asymmetric_static: numpy float32 closed form, plus the reference K
+  quantize+pack formula of tests/test_fused_quantize_pack.py:8-17.
+* outlier_rescue: torch.quantile (the library routine the reference calls) is restated
+  in float32 (the arithmetic the HIP kernel uses) and compared bitwise.  The rescued
+  set is checked against the closed form "values >= the interpolated threshold".
+* decode_attn_int8_torch_ref: the KATs of tests/test_patch_model.py:280-368 (S=1 -> V,
+  softmax [e/(e+1), 1/(e+1)], ctx=0 -> 0, GQA head h -> kv head h // n_rep), a float64
+  brute force on tiny inputs, and permutation / scaling invariants.
+* decode_attn_asym_ref: float64 brute force with explicit dequantisation.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn as OA
+from oracle import quant as OQ
+
+
+def all_finite_fp16():
+    bits = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    x = bits.view(np.float16)
+    return x[np.isfinite(x)]
+
+
+# ---------------------------------------------------------------- INT8
+
+
+def int8_closed_form(x16: np.ndarray, s16: np.float16) -> np.ndarray:
+    s = max(np.float64(s16), np.float64(np.float16(1e-5)))
+    s = np.float16(s)
+    qf = np.float16(x16.astype(np.float64) / np.float64(s))  # correctly rounded fp16 quotient
+    q = np.rint(qf.astype(np.float64))
+    return np.clip(q, -127, 127).astype(np.int8)
+
+
+@pytest.mark.parametrize("s", [1e-6, 1.5e-5, 3.3e-4, 0.0078125, 0.0123, 0.37, 1.0, 3.7, 157.0])
+def test_int8_exhaustive_fp16(s):
+    x = all_finite_fp16()
+    s16 = np.float16(s)
+    expect = int8_closed_form(x, s16)
+    xt = torch.from_numpy(x.copy()).view(1, 1, -1, 1).expand(1, 1, x.size, 32).contiguous()
+    scale = torch.full((1, 1), float(s16), dtype=torch.float16)
+    q, s_out = OQ.quantize_symmetric_int8_with_scale(xt, scale, 32)
+    assert torch.equal(q[0, 0, :, 0], torch.from_numpy(expect))
+    assert s_out.dtype == torch.float16
+
+
+def test_int8_ties_round_to_even_and_clamp():
+    # quotients exactly at .5 must round to even; |q| > 127 clamps
+    x = torch.tensor([0.5, 1.5, 2.5, -0.5, -2.5, 200.0, -200.0, 126.5], dtype=torch.float16)
+    xt = x.view(1, 1, 1, -1).repeat(1, 1, 1, 4)
+    q, _ = OQ.quantize_symmetric_int8_with_scale(xt, torch.ones(1, 1, dtype=torch.float16), 32)
+    assert q[0, 0, 0, :8].tolist() == [0, 2, 2, 0, -2, 127, -127, 126]
+
+
+def test_int8_fp16_quotient_rounding_matters():
+    # x/s lands just above k+0.5 in fp32 but rounds to exactly k+0.5 in fp16 -> rounds to even.
+    # A plain fp32 quotient would give the next integer: this pins the fp16 step.
+    x16 = np.float16(1.0009765625)  # 1 + 2^-10
+    s16 = np.float16(0.4)
+    q32 = np.rint(np.float32(x16) / np.float32(s16))
+    qf16 = np.rint(np.float32(np.float16(np.float32(x16) / np.float32(s16))))
+    cases = []
+    for xv in all_finite_fp16()[::97]:
+        a = np.rint(np.float64(np.float16(np.float64(xv) / np.float64(s16))))
+        b = np.rint(np.float64(xv) / np.float64(s16))
+        if a != b and abs(float(xv) / float(s16)) < 127:
+            cases.append(xv)
+    assert cases, "expected fp16-vs-fp32 quotient rounding differences"
+    xt = torch.from_numpy(np.array(cases, dtype=np.float16)).view(1, 1, -1, 1).repeat(1, 1, 1, 32)
+    q, _ = OQ.quantize_symmetric_int8_with_scale(xt, torch.full((1, 1), float(s16), dtype=torch.float16), 32)
+    assert torch.equal(q[0, 0, :, 0], torch.from_numpy(int8_closed_form(np.array(cases, dtype=np.float16), s16)))
+    del q32, qf16
+
+
+def test_int8_dynamic_absmax():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 2, 3, 128, generator=g).to(torch.float16)
+    q, s = OQ.quantize_symmetric_int8(x, 100.0, 32)
+    xn = x.numpy().reshape(2, 2, 3, 4, 32)
+    am = np.maximum(np.abs(xn).max(-1), np.float16(1e-5)).astype(np.float16)
+    s_exp = np.float16(am.astype(np.float64) / 127.0)
+    assert np.array_equal(s.numpy(), s_exp)
+    qe = np.clip(np.rint(np.float16(xn.astype(np.float64) / s_exp[..., None].astype(np.float64)).astype(np.float64)), -127, 127)
+    assert np.array_equal(q.numpy().reshape(2, 2, 3, 4, 32), qe.astype(np.int8))
+    assert q.abs().max() == 127  # the absmax element maps to +-127
+
+
+# ---------------------------------------------------------------- INT4 symmetric
+
+
+def int4_closed_form(x16: np.ndarray, s32: np.ndarray) -> np.ndarray:
+    s = np.maximum(s32.astype(np.float32), np.float32(1e-5))
+    qf = (x16.astype(np.float64) / s.astype(np.float64)).astype(np.float32)
+    return np.clip(np.rint(qf), -7, 7).astype(np.int8)
+
+
+def test_int4_static_closed_form():
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(3, 2, 17, 128, generator=g) * 3).to(torch.float16)
+    scale = (torch.rand(2, 4, generator=g) * 0.5 + 1e-6).float()
+    q, s = OQ.quantize_symmetric_int4_with_scale(x, scale, 32)
+    xn = x.numpy().reshape(3, 2, 17, 4, 32)
+    sn = scale.numpy()[None, :, None, :, None]
+    assert np.array_equal(q.numpy().reshape(3, 2, 17, 4, 32), int4_closed_form(xn, sn))
+    assert s.dtype == torch.float32
+    assert torch.equal(s[0, :, 0], scale.clamp(min=1e-5))
+
+
+def test_int4_kat_boundaries():
+    # reference tests/test_int4_cache.py:559-586
+    for val, code in ((7.0, 7), (-7.0, -7), (0.0, 0)):
+        q, _ = OQ.quantize_symmetric_int4(torch.full((1, 1, 1, 128), val), 100.0, 128)
+        assert (q == code).all()
+    q, _ = OQ.quantize_symmetric_int4(torch.randn(1, 1, 1, 128) * 1000, 100.0, 128)
+    assert q.min() >= -7 and q.max() <= 7
+
+
+def test_pack_unpack_kats():
+    # reference tests/test_int4_cache.py:469-557
+    vals = torch.arange(-8, 8, dtype=torch.int8).view(1, 1, 1, 16)
+    assert torch.equal(OQ.unpack_int4(OQ.pack_int4(vals)), vals)
+    for a, b in [(-8, 7), (7, -8), (-8, -8), (7, 7), (0, 0), (-1, 1)]:
+        x = torch.tensor([a, b], dtype=torch.int8).view(1, 1, 1, 2)
+        p = OQ.pack_int4(x)
+        assert int(p.view(torch.uint8)) == ((a + 8) << 4) | (b + 8)  # high nibble = even element
+        assert torch.equal(OQ.unpack_int4(p), x)
+
+
+def test_rescue_quantile_matches_torch_and_closed_form():
+    rng = np.random.default_rng(0)
+    for n in (1, 2, 3, 16, 127, 128, 129, 512, 4096):
+        for ratio in (0.01, 0.05, 0.3, 0.5, 0.999):
+            v = (np.abs(rng.standard_normal(n)) * rng.uniform(0.1, 10)).astype(np.float32)
+            if n > 8:
+                v[rng.integers(0, n, 3)] = v[0]  # ties
+            q = max(0.0, min(1.0, 1.0 - ratio))
+            ref = torch.quantile(torch.from_numpy(v), q).item()
+            # float32 restatement: the arithmetic of the HIP rescue kernel
+            s = np.sort(v)
+            rank = np.float32(q) * np.float32(n - 1)
+            lo, hi = int(np.floor(rank)), int(np.ceil(rank))
+            w = np.float32(rank - np.float32(lo))
+            a, b = s[lo], s[hi]
+            d = np.float32(b - a)
+            thr = np.float32(a + np.float32(w * d)) if w < 0.5 else np.float32(b - np.float32(d * np.float32(1 - w)))
+            assert np.float32(ref) == thr, (n, ratio, ref, thr)
+            # rescued set: everything >= sorted[hi], plus sorted[lo] only if thr == sorted[lo]
+            mask = v >= thr
+            assert mask.sum() >= n - hi
+            assert set(np.flatnonzero(mask)) >= set(np.flatnonzero(v >= b))
+
+
+def test_outlier_rescue_effect():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 2, 1, 128, generator=g).to(torch.float16)
+    x[0, 1, 0, 5] = 60.0
+    st = torch.full((2, 4), 0.3)
+    q0, s0 = OQ.int4_cache_quantize(x, st, 32)
+    # 16 groups, ratio 0.05: rank = 0.95 * 15 = 14.25 -> only the largest group is rescued
+    q1, s1 = OQ.int4_cache_quantize(x, st, 32, outlier_rescue_ratio=0.05)
+    assert s1[0, 1, 0, 0] == pytest.approx(60.0 / 7.0)  # the outlier group is rescued
+    rest = torch.ones_like(s1, dtype=torch.bool)
+    rest[0, 1, 0, 0] = False
+    assert torch.equal(s0[rest], s1[rest])              # every other group keeps the static scale
+    assert q0[0, 1, 0, 5] == 7 and q1[0, 1, 0, 5] == 7
+    _, s_all = OQ.int4_cache_quantize(x, st, 32, outlier_rescue_ratio=1.0)
+    dyn = OQ.int4_dynamic_group_scale(x, 32)
+    assert torch.equal(s_all, torch.maximum(st[None, :, None, :].expand_as(dyn), dyn))
+
+
+# ---------------------------------------------------------------- asymmetric static
+
+
+def test_asym_static_closed_form_and_reference_formula():
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(2, 3, 11, 128, generator=g) * 2).to(torch.float16)
+    s16 = (torch.rand(3, 4, generator=g) * 0.4 + 0.05).to(torch.float16)
+    z16 = (torch.randn(3, 4, generator=g) * 0.2).to(torch.float16)
+    q = OQ.quantize_asymmetric_static(x, s16, z16)
+    xn = x.numpy().astype(np.float32).reshape(2, 3, 11, 4, 32)
+    sn = s16.numpy().astype(np.float32)[None, :, None, :, None]
+    zn = z16.numpy().astype(np.float32)[None, :, None, :, None]
+    expect = np.clip(np.rint((xn - zn) / sn), -8, 7).astype(np.int8)
+    assert np.array_equal(q.numpy().reshape(2, 3, 11, 4, 32), expect)
+    # reference K quantize+pack formula with per-channel params = group params broadcast
+    ks = s16.float().repeat_interleave(32, dim=1)[None].expand(2, 3, 128)
+    kz = z16.float().repeat_interleave(32, dim=1)[None].expand(2, 3, 128)
+    ref_q = torch.round((x.float() - kz.unsqueeze(2)) / ks.unsqueeze(2)).clamp(-8, 7).to(torch.int8)
+    assert torch.equal(ref_q, q)
+    deq = OQ.dequantize_asymmetric_static(q, s16, z16)
+    assert torch.allclose(deq.view(2, 3, 11, 4, 32), torch.from_numpy(expect * sn + zn), atol=0)
+
+
+# ---------------------------------------------------------------- attention oracle
+
+
+def test_attn_kat_single_token_is_v():
+    q = torch.ones(1, 1, 4, dtype=torch.float16)
+    k = torch.ones(1, 1, 1, 4, dtype=torch.int8)
+    v = torch.tensor([[[[2, 3, 4, 5]]]], dtype=torch.int8)
+    one = torch.ones(1, 1, 1, 1, dtype=torch.float16)
+    out = OA.decode_attn_int8_torch_ref(q, k, v, one, one, torch.tensor([1]), 1.0)
+    assert torch.equal(out, torch.tensor([[[2.0, 3.0, 4.0, 5.0]]], dtype=torch.float16))
+
+
+def test_attn_kat_two_tokens_softmax():
+    q = torch.tensor([[[1.0, 0.0]]], dtype=torch.float16)
+    kv = torch.tensor([[[[1, 0], [0, 1]]]], dtype=torch.int8)
+    one = torch.ones(1, 1, 2, 1, dtype=torch.float16)
+    out = OA.decode_attn_int8_torch_ref(q, kv, kv, one, one, torch.tensor([2]), 1.0)
+    e = math.e
+    assert torch.allclose(out.float(), torch.tensor([[[e / (e + 1), 1 / (e + 1)]]]), atol=1e-3)
+
+
+def test_attn_kat_zero_context_and_gqa_mapping():
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(2, 4, 8, generator=g).to(torch.float16)
+    k = torch.randint(-3, 4, (2, 2, 5, 8), generator=g, dtype=torch.int8)
+    v = torch.randint(-3, 4, (2, 2, 5, 8), generator=g, dtype=torch.int8)
+    s = torch.ones(2, 2, 5, 1, dtype=torch.float16)
+    out = OA.decode_attn_int8_torch_ref(q, k, v, s, s, torch.tensor([0, 5]), 0.5)
+    assert torch.all(out[0] == 0)
+    # head h uses kv head h // 2: recompute each head alone with Hq = Hkv = 1
+    for h in range(4):
+        single = OA.decode_attn_int8_torch_ref(q[1:2, h:h + 1], k[1:2, h // 2:h // 2 + 1],
+                                               v[1:2, h // 2:h // 2 + 1], s[1:2, :1], s[1:2, :1],
+                                               torch.tensor([5]), 0.5)
+        assert torch.equal(single[0, 0], out[1, h])
+
+
+def fp16_close(out16, ref64, rel=2e-4):
+    """|out - ref| <= half an fp16 ulp of ref (the output rounding) + rel * |ref| + 1e-5."""
+    ref = np.asarray(ref64, dtype=np.float64)
+    half_ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
+    err = np.abs(np.asarray(out16, dtype=np.float64) - ref)
+    return bool(np.all(err <= half_ulp + rel * np.abs(ref) + 1e-5)), float(err.max())
+
+
+def brute_attention(q, k, v, ctx, sm):
+    """float64 triple loop; q [Hq, D], k/v [Hkv, S, D] as float64 numpy."""
+    Hq, D = q.shape
+    Hkv = k.shape[0]
+    out = np.zeros((Hq, D))
+    for h in range(Hq):
+        kh = h // (Hq // Hkv)
+        sc = np.array([sum(q[h, d] * k[kh, t, d] for d in range(D)) * sm for t in range(ctx)])
+        p = np.exp(sc - sc.max())
+        p /= p.sum()
+        out[h] = (p[:, None] * v[kh, :ctx]).sum(0)
+    return out
+
+
+def test_attn_int8_brute_force():
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(1, 6, 16, generator=g).to(torch.float16)
+    k = torch.randint(-127, 128, (1, 2, 7, 16), generator=g, dtype=torch.int8)
+    v = torch.randint(-127, 128, (1, 2, 7, 16), generator=g, dtype=torch.int8)
+    ks = (torch.rand(1, 2, 7, 2, generator=g) * 0.02).to(torch.float16)
+    vs = (torch.rand(1, 2, 7, 2, generator=g) * 0.02).to(torch.float16)
+    out = OA.decode_attn_int8_torch_ref(q, k, v, ks, vs, torch.tensor([6]), 0.25)
+    kd = (k.view(1, 2, 7, 2, 8).to(torch.float16) * ks.unsqueeze(-1)).view(1, 2, 7, 16).double().numpy()
+    vd = (v.view(1, 2, 7, 2, 8).to(torch.float16) * vs.unsqueeze(-1)).view(1, 2, 7, 16).double().numpy()
+    ref = brute_attention(q[0].double().numpy(), kd[0], vd[0], 6, 0.25)
+    ok, err = fp16_close(out[0].double().numpy(), ref)
+    assert ok, err
+
+
+def test_attn_invariants():
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(2, 6, 32, generator=g).to(torch.float16)
+    k = torch.randint(-50, 50, (2, 1, 40, 32), generator=g, dtype=torch.int8)
+    v = torch.randint(-50, 50, (2, 1, 40, 32), generator=g, dtype=torch.int8)
+    ks = torch.full((2, 1, 40, 4), 0.01, dtype=torch.float16)
+    ctx = torch.tensor([40, 33])
+    out = OA.decode_attn_int8_torch_ref(q, k, v, ks, ks, ctx, 0.2)
+    perm = torch.randperm(33, generator=g)
+    k2, v2 = k.clone(), v.clone()
+    k2[1, :, :33], v2[1, :, :33] = k[1, :, perm], v[1, :, perm]
+    out2 = OA.decode_attn_int8_torch_ref(q, k2, v2, ks, ks, ctx, 0.2)
+    assert torch.allclose(out[1].float(), out2[1].float(), atol=1e-3)
+    # tokens past the context never matter
+    k3 = k.clone()
+    k3[1, :, 33:] = 127
+    assert torch.equal(OA.decode_attn_int8_torch_ref(q, k3, v, ks, ks, ctx, 0.2)[1], out[1])
+
+
+def test_asym_oracle_brute_force_with_outliers():
+    g = torch.Generator().manual_seed(8)
+    B, H, S, D = 1, 1, 5, 128
+    kq = torch.randint(-8, 8, (B, H, S, D), generator=g, dtype=torch.int8)
+    vq = torch.randint(-8, 8, (B, H, S, D), generator=g, dtype=torch.int8)
+    ks = (torch.rand(H, 4, generator=g) + 0.1).to(torch.float16)
+    kz = torch.randn(H, 4, generator=g).to(torch.float16)
+    vs = (torch.rand(H, 4, generator=g) + 0.1).to(torch.float16)
+    vz = torch.randn(H, 4, generator=g).to(torch.float16)
+    oidx = torch.tensor([[3, 40, 77, 127]], dtype=torch.int32)
+    oval = (torch.randn(B, H, S, 4, generator=g) * 20).to(torch.float16)
+    q = torch.randn(B, 3, D, generator=g).to(torch.float16)
+    tau = torch.tensor([0.9, 1.1, 1.0], dtype=torch.float16)
+    out = OA.decode_attn_asym_ref(q, OQ.pack_int4(kq), OQ.pack_int4(vq), ks, kz, vs, vz,
+                                  torch.tensor([S]), 0.1, inv_tau=tau, k_outlier_idx=oidx,
+                                  k_outlier_val=oval)
+    kd = np.zeros((H, S, D))
+    vd = np.zeros((H, S, D))
+    for t in range(S):
+        for d in range(D):
+            gi = d // 32
+            kd[0, t, d] = float(kq[0, 0, t, d]) * float(ks[0, gi]) + float(kz[0, gi])
+            vd[0, t, d] = float(vq[0, 0, t, d]) * float(vs[0, gi]) + float(vz[0, gi])
+        for j, ch in enumerate(oidx[0].tolist()):
+            kd[0, t, ch] = float(oval[0, 0, t, j])
+    qs = (q[0] * tau.view(-1, 1)).double().numpy()  # fp16 product, as the reference
+    ref = brute_attention(qs, kd, vd, S, 0.1)
+    ok, err = fp16_close(out[0].double().numpy(), ref)
+    assert ok, err
+
+
+def test_planted_mistake_is_caught():
+    """A pack with swapped nibbles (a plausible bug) must fail the layout KAT."""
+    x = torch.tensor([[-8, 7]], dtype=torch.int8).view(1, 1, 1, 2)
+    u = (x.to(torch.int16) + 8).to(torch.uint8).view(1, 1, 1, 1, 2)
+    swapped = ((u[..., 1] << 4) | u[..., 0]).to(torch.int8)
+    assert int(swapped.view(torch.uint8)) != ((-8 + 8) << 4) | (7 + 8)
+    assert int(OQ.pack_int4(x).view(torch.uint8)) == ((-8 + 8) << 4) | (7 + 8)
