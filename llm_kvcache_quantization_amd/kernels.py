@@ -55,6 +55,7 @@ def kv_view_tok(codes: torch.Tensor, scale: torch.Tensor) -> C.KvView:
     v.scale = scale.data_ptr()
     (v.scale_stride_b, v.scale_stride_h, v.scale_stride_t, v.scale_stride_g) = scale.stride()
     v.scale_dtype = _scale_dtype_code(scale)
+    v._keep = (codes, scale)  # the struct holds raw pointers: keep the tensors alive with it
     return v
 
 
@@ -80,6 +81,7 @@ def kv_view_static(
         v.outlier_val = outlier_val.data_ptr()
         v.outlier_stride_b, v.outlier_stride_h, v.outlier_stride_t = (
             outlier_val.stride(0), outlier_val.stride(1), outlier_val.stride(2))
+    v._keep = (codes, scale, zero_point, outlier_idx, outlier_val)
     return v
 
 
@@ -112,7 +114,9 @@ class DecodePlan:
         self.context_lens = context_lens
         self.inv_tau = inv_tau
         self.out = torch.empty_like(q) if out is None else out
-        self._keep = keepalive
+        # ctypes copies the view structs into the params block by value; keep the view
+        # objects (and the tensors they point at) alive for the plan's lifetime
+        self._keep = (keepalive, k_view, v_view)
         p = C.DecodeParams()
         p.q = q.data_ptr()
         p.q_stride_b, p.q_stride_h = q.stride(0), q.stride(1)
