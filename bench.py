@@ -184,6 +184,27 @@ def time_region(fn, stream, steps, warmup, use_graph):
     return e0.elapsed_time(e1) / steps, graph
 
 
+def stream_ceiling(device, nbytes=2 << 30, reps=10):
+    """Measured HBM ceilings on this GPU: torch's device copy (read + write bytes) and a
+    full read-reduction (read bytes), each over a buffer far larger than the 256 MB MALL."""
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=device).uniform_()
+    b = torch.empty_like(a)
+    out = {}
+    for name, fn, moved in (("copy", lambda: b.copy_(a), 2 * nbytes),
+                            ("read", lambda: a.sum(), nbytes)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name + "_GBps"] = round(moved * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    del a, b
+    return out
+
+
 def cpu_baseline(cfg, layers_dev):
     """The CPU oracle (reference torch path) on a bounded sample of the workload:
     one layer, `rows` batch rows at the full context, quantize-on-append of one token
@@ -287,6 +308,8 @@ def main():
           f"(attention {us_attn:.2f} us, append {us_app:.2f} us); attention {achieved:.0f} GB/s",
           file=sys.stderr, flush=True)
 
+    ceiling = stream_ceiling(device)
+    print(f"[bench] stream ceiling {ceiling}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
@@ -329,6 +352,7 @@ def main():
             "bytes_per_launch": nbytes,
             "kernel": "decode_splitk_kernel + combine_kernel (per layer)",
         },
+        "stream_ceiling": ceiling,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

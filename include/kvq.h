@@ -53,7 +53,8 @@ typedef struct kvq_kv_view {
   const void* scale;     /* INT8_SYM/INT4_SYM: [B,H,T,G] (any strides, 0 allowed);
                             INT4_ASYM: [H,G] (only stride_h / stride_g are read) */
   int64_t scale_stride_b, scale_stride_h, scale_stride_t, scale_stride_g; /* elements */
-  int32_t scale_dtype;   /* KVQ_DTYPE_F16 or KVQ_DTYPE_F32 (F32 is rounded to fp16 in-kernel) */
+  int32_t scale_dtype;   /* KVQ_DTYPE_F16 or KVQ_DTYPE_F32 (F32 is rounded to fp16 in-kernel);
+                            K and V per-token scales must have the same dtype */
   int32_t n_outlier;     /* INT4_ASYM K only: 0 or 4 */
   const void* zero_point;         /* INT4_ASYM: fp16 [H,G], same strides as scale */
   const int32_t* outlier_idx;     /* [H, n_outlier] channel indices, distinct, in [0, D) */

@@ -5,27 +5,38 @@
 // heads are the N dimension (padded to 16) of v_mfma_f32_16x16x32_f16 and the
 // tokens are M, so every code byte is read from HBM exactly once.
 //
-//   S^T[t, h]   = K[t, :] . q'[h, :]           A = dequantised K tile, B = q'^T
-//   out^T[d, h] = sum_t V^T[d, t] * P^T[t, h]  A = dequantised V^T,    B = P^T
+//   S^T[t, h]   = K[t, :] . q'[h, :]           A = K tile (codes as fp16), B = q'^T
+//   out^T[d, h] = sum_t V^T[d, t] * P^T[t, h]  A = V^T (codes as fp16),    B = P^T
 //
 // The D layout of the first MFMA (lane = (h, 4 tokens)) is exactly the B layout
-// the second one needs, so the softmax probabilities never leave registers.
-// Each wave keeps an online-softmax state (m, l, acc) for its tokens; the four
-// waves merge through LDS and write one partial (m, l, acc[128]) per head and
-// chunk; kvq_combine merges the chunks (flash-decoding) and applies the V
-// epilogue.  Reference semantics: src/kernels/triton_decode_attn_int8.py:126-303
-// (online softmax, masking) and src/engine/patch_model.py:281-377 (fp16 dequant
-// product code * scale, fp32 softmax, fp16 output).
+// the second one needs, so probabilities never leave registers.  Each wave streams
+// 32-token tiles with a ring of DEPTH tiles in registers (DEPTH-1 in flight while
+// one is computed) and keeps an online-softmax state (m, l, acc).  The running max
+// is raised lazily: p = 2^(x - m) may reach 2^kTau before the accumulators are
+// rescaled.  The four waves merge through LDS into one partial (m, l, acc[128])
+// per head and chunk; combine_kernel merges the chunks (flash-decoding) and applies
+// the V epilogue.
+//
+// Reference semantics: src/kernels/triton_decode_attn_int8.py:126-303 (online
+// softmax, masking, zero-context rows) and src/engine/patch_model.py:281-377
+// (dequant product code * scale in fp16, fp32 softmax, fp16 output).
 #include "kvq_common.h"
 #include "kvq.h"
 
+#include <cstdlib>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 namespace kvq {
 
 constexpr int kWaves = 4;
-constexpr int kTile = 32;  // tokens per wave iteration (two 16-token MFMA row blocks)
+constexpr int kTile = 32;   // tokens per wave iteration (two 16-token MFMA row blocks)
 constexpr int kD = 128;
+constexpr float kTau = 8.0f;  // lazy-rescale headroom in log2 units
+constexpr int kMaxChunks = 2048;
+constexpr int kMinChunk = 256;
 
 struct KvDev {
   const uint8_t* codes;
@@ -56,284 +67,390 @@ struct DecodeArgs {
   int64_t o_sb, o_sh;
 };
 
-__device__ __forceinline__ half_t ld_scale(const KvDev& kv, int64_t off) {
-  if (kv.scale_f32) return (half_t)(reinterpret_cast<const float*>(kv.scale)[off]);
-  return reinterpret_cast<const half_t*>(kv.scale)[off];
-}
-__device__ __forceinline__ uint32_t splat_h2(half_t s) {
-  half2v v = {s, s};
-  return as_u32(v);
-}
-__device__ __forceinline__ uint32_t pair_h2(half_t lo, half_t hi) {
-  half2v v = {lo, hi};
-  return as_u32(v);
-}
+__device__ __forceinline__ uint32_t splat_h2(half_t s) { return as_u32(half2v{s, s}); }
+__device__ __forceinline__ uint32_t pair_h2(half_t lo, half_t hi) { return as_u32(half2v{lo, hi}); }
 // q' = fp16(q * inv_tau): fp16 x fp16 product rounded once, as torch's Half mul
 __device__ __forceinline__ half_t qscale(half_t x, half_t tau, bool has_tau) {
   return has_tau ? (half_t)((float)x * (float)tau) : x;
 }
-// exact dequant of a half2 of codes (64 + n form): (n - 8) * s, rounded to fp16
-__device__ __forceinline__ uint32_t deq_sym4(uint32_t u64pn, uint32_t s2) {
-  const half2v off = {(half_t)72.0f, (half_t)72.0f};
-  half2v c = as_h2(u64pn) - off;  // exact small integers
-  return as_u32(c * as_h2(s2));
-}
-// int8 pair (already xor 0x80 and placed in the low byte of each half) -> (c * s)
-__device__ __forceinline__ uint32_t deq_int8_pair(uint32_t perm_bytes, uint32_t s2) {
-  const half2v off = {(half_t)1152.0f, (half_t)1152.0f};
-  half2v c = as_h2(perm_bytes | kMagic1024) - off;
-  return as_u32(c * as_h2(s2));
-}
-
 // two fp32 -> packed fp16, rounding toward zero (v_cvt_pkrtz_f16_f32)
 __device__ __forceinline__ half2v pk_rtz(float a, float b) {
   return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
+// (x - off) * s on a half2: exact code recovery, then one fp16 rounding of the product
+__device__ __forceinline__ uint32_t deq_pair(uint32_t x, half_t off, uint32_t s2) {
+  const half2v o = {off, off};
+  return as_u32((as_h2(x) - o) * as_h2(s2));
+}
+__device__ __forceinline__ const half_t* q_row(const DecodeArgs& a, int b, int hq) {
+  return a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
+}
+// q'[32 lg + i] for i < 32 (the lane group's quantisation group) with four 16-byte
+// loads issued together; q' = fp16(q * inv_tau) when inv_tau is given
+__device__ __forceinline__ void load_q_group(const half_t* qr, int lg, half_t tau, bool has_tau,
+                                             half_t out[32]) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(qr + 32 * lg);
+  u32x4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = p[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const half2v h = as_h2(w[k]);
+      out[8 * i + 2 * k] = qscale(h.x, tau, has_tau);
+      out[8 * i + 2 * k + 1] = qscale(h.y, tau, has_tau);
+    }
+  }
+}
 
 // ---------------------------------------------------------------- K formats
+//
+// A operand of the QK MFMA: lane (row = lane % 16, lg = lane / 16) of row block s
+// (0/1) supplies token tt + 16 s + row.  For INT4 it reads the 16 bytes [16 lg, 16 lg
+// + 16) of that token's 64-byte code row = channels [32 lg, 32 lg + 32) = quantisation
+// group lg; dword j feeds MFMA j with channels 32 lg + 8 j + kNibSlotElem(e).
 
-// INT4 asymmetric, static scale/zero-point per (kv head, group of 32), optional fp16
-// outlier channels.  One MFMA per quantisation group so the group scale is applied
-// to the fp32 MFMA result (no fp16 rounding of q * s):
-//   logit = sum_g s_g * C_g + sum_g Q_g (zp_g - 72 s_g) + sum_j q[o_j] k16[o_j]
-// with C_g = sum_{d in g} q'_d (64 + n_d), Q_g = sum_{d in g} q'_d (outliers excluded).
+// INT4 asymmetric, static scale s / zero-point z per (kv head, group of 32), optional
+// fp16 outlier channels.  With x = 64 + n = c + 72 the logit is
+//   sum_d q_d (s_g c_d + z_g) = sum_d (q_d s_g) x_d + sum_d q_d (z_g - 72 s_g)
+// q_d s_g (exact in fp32) is split into fp16 hi + lo; both go through the MFMA, so the
+// product is not rounded to fp16.  The constant term is the accumulator's initial value;
+// outlier channels (q zeroed in the main MFMAs) are added by one more MFMA whose A and B
+// operands hold the 4 outlier values / q' entries in lane group 0 and zeros elsewhere.
+template <bool OUT>
 struct KAsym4 {
-  half8v qb[4];
-  half4v qo;
-  float sj[4];
+  static constexpr bool has_out = OUT;
+  half8v qh[4], ql[4];
+  half8v qo;  // q' of the outlier channels in k-slots 0..3 of lane group 0, zero elsewhere
   float bias;
-  float sm;
-  bool has_out;
+  const uint8_t* kb;
+  const half_t* ob;
+  int64_t st, ost;
+  uint32_t koff[2], ooff[2];
+  int row, lg;
   struct Raw {
-    uint32_t w[4];
-    u32x2 o;
+    u32x4 w[2];
+    u32x2 o[2];
   };
 
-  __device__ void setup(const DecodeArgs& a, int b, int hkv, int col, int lg) {
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int col, int lg_) {
+    row = col;
+    lg = lg_;
     const bool valid = col < a.n_rep;
     const int hq = hkv * a.n_rep + (valid ? col : 0);
     const bool has_tau = a.inv_tau != nullptr;
     const half_t tau = has_tau ? a.inv_tau[hq] : (half_t)1.0f;
-    const half_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
-    has_out = a.k.n_out > 0;
-    sm = a.sm_log2e;
+    const half_t* qr = q_row(a, b, hq);
+    // all loads are unconditional and issued together (no branch per element)
     int oc[4] = {-1, -1, -1, -1};
-    for (int i = 0; i < a.k.n_out; ++i) oc[i] = min(max(a.k.oidx[hkv * a.k.n_out + i], 0), kD - 1);
-    float Q[4];
+    if constexpr (OUT) {
+      const int4 o = *reinterpret_cast<const int4*>(a.k.oidx + hkv * 4);
+      oc[0] = min(max(o.x, 0), kD - 1);
+      oc[1] = min(max(o.y, 0), kD - 1);
+      oc[2] = min(max(o.z, 0), kD - 1);
+      oc[3] = min(max(o.w, 0), kD - 1);
+    }
+    half_t qv[32];
+    load_q_group(qr, lg, tau, has_tau, qv);
+    half_t qoe[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qoe[i] = qscale(qr[OUT ? oc[i] : 0], tau, has_tau);
+    const half_t* sc = reinterpret_cast<const half_t*>(a.k.scale);
+    const float s = (float)sc[hkv * a.k.ssh + lg * a.k.ssg];
+    const float z = (float)a.k.zp[hkv * a.k.ssh + lg * a.k.ssg];
+    float part = 0.f;
+#pragma unroll
     for (int j = 0; j < 4; ++j) {
-      half_t v8[8];
-      float part = 0.f;
+      half_t vh[8], vl[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = 32 * j + 8 * lg + kNibSlotElem(e);
-        half_t x = valid ? qscale(qrow[d], tau, has_tau) : (half_t)0.0f;
-        if (d == oc[0] || d == oc[1] || d == oc[2] || d == oc[3]) x = (half_t)0.0f;
-        v8[e] = x;
-        part += (float)x;
+        const int dl = 8 * j + kNibSlotElem(e);
+        const int d = 32 * lg + dl;
+        const bool use = valid && d != oc[0] && d != oc[1] && d != oc[2] && d != oc[3];
+        const float qd = use ? (float)qv[dl] : 0.f;
+        const float P = qd * s;  // exact: 11-bit x 11-bit significands
+        const half_t hi = (half_t)P;
+        const half_t lo = (half_t)(P - (float)hi);
+        vh[e] = hi;
+        vl[e] = lo;
+        part += qd * z - 72.0f * ((float)hi + (float)lo);
       }
-      qb[j] = half8v{v8[0], v8[1], v8[2], v8[3], v8[4], v8[5], v8[6], v8[7]};
-      Q[j] = wave_sum_xor_groups(part);
+      qh[j] = half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]};
+      ql[j] = half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]};
     }
-    half_t o4[4] = {(half_t)0.0f, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
-    if (lg == 0 && valid)
-      for (int i = 0; i < a.k.n_out; ++i) o4[i] = qscale(qrow[oc[i]], tau, has_tau);
-    qo = half4v{o4[0], o4[1], o4[2], o4[3]};
-    const half_t* sc = reinterpret_cast<const half_t*>(a.k.scale);
-    float bsum = 0.f;
-    for (int j = 0; j < 4; ++j) {
-      const float s = (float)sc[hkv * a.k.ssh + j * a.k.ssg];
-      const float z = (float)a.k.zp[hkv * a.k.ssh + j * a.k.ssg];
-      sj[j] = s * a.sm_log2e;
-      bsum += Q[j] * (z - 72.0f * s);
-    }
-    bias = valid ? bsum : 0.f;
+    bias = wave_sum_xor_groups(part);
+    const bool own = lg == 0 && valid && OUT;
+    const half_t h0 = (half_t)0.0f;
+    qo = half8v{own ? qoe[0] : h0, own ? qoe[1] : h0, own ? qoe[2] : h0, own ? qoe[3] : h0,
+                h0, h0, h0, h0};
+    kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    st = a.k.st;
+    koff[0] = (uint32_t)(row * st + 16 * lg);
+    koff[1] = (uint32_t)((row + 16) * st + 16 * lg);
+    ob = a.k.oval + (int64_t)b * a.k.osb + (int64_t)hkv * a.k.osh;
+    ost = a.k.ost;
+    ooff[0] = (uint32_t)(row * ost);
+    ooff[1] = (uint32_t)((row + 16) * ost);
   }
 
-  __device__ __forceinline__ void load(const DecodeArgs& a, int b, int hkv, int t, int lg,
-                                       Raw& r) const {
-    const uint8_t* p = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh +
-                       (int64_t)t * a.k.st + 4 * lg;
+  __device__ __forceinline__ void load_full(int tt, Raw& r) const {
+    const uint8_t* p = kb + (int64_t)tt * st;
+    r.w[0] = ld_stream<u32x4>(p + koff[0]);
+    r.w[1] = ld_stream<u32x4>(p + koff[1]);
+    if constexpr (OUT) {
+      r.o[0] = r.o[1] = u32x2{0u, 0u};
+      if (lg == 0) {
+        const half_t* o = ob + (int64_t)tt * ost;
+        r.o[0] = ld_stream<u32x2>(o + ooff[0]);
+        r.o[1] = ld_stream<u32x2>(o + ooff[1]);
+      }
+    }
+  }
+  __device__ __forceinline__ void load_clamped(int tt, int t1, Raw& r) const {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.w[j] = *reinterpret_cast<const uint32_t*>(p + 16 * j);
-    r.o = u32x2{0u, 0u};
-    if (has_out && lg == 0) {
-      const half_t* o = a.k.oval + (int64_t)b * a.k.osb + (int64_t)hkv * a.k.osh +
-                        (int64_t)t * a.k.ost;
-      r.o = *reinterpret_cast<const u32x2*>(o);
+    for (int s = 0; s < 2; ++s) {
+      const int t = min(tt + 16 * s + row, t1 - 1);
+      r.w[s] = ld_stream<u32x4>(kb + (int64_t)t * st + 16 * lg);
+      if constexpr (OUT) {
+        r.o[s] = u32x2{0u, 0u};
+        if (lg == 0) r.o[s] = ld_stream<u32x2>(ob + (int64_t)t * ost);
+      }
     }
   }
 
-  __device__ __forceinline__ float4v logits(const Raw& r) const {
-    float4v co = {bias, bias, bias, bias};
-    if (has_out) co = mfma16x16x16(pack4(r.o.x, r.o.y), qo, co);
-    float4v x = co * sm;
-    const float4v z = {0.f, 0.f, 0.f, 0.f};
+  __device__ __forceinline__ float4v qk(const Raw& r, int s, const NibConsts& nc) const {
+    float4v c = {bias, bias, bias, bias};
+    // Same MFMA shape as the chain below, so the accumulator chain never changes shape.
+    if constexpr (OUT) c = mfma16x16x32(pack8(r.o[s].x, r.o[s].y, 0u, 0u), qo, c);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t u[4];
-      unpack_dword_64pn(r.w[j], u);
-      const float4v c = mfma16x16x32(pack8(u[0], u[1], u[2], u[3]), qb[j], z);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = fmaf(sj[j], c[i], x[i]);
+      unpack_dword_64pn(r.w[s][j], nc, u);
+      const half8v A = pack8(u[0], u[1], u[2], u[3]);
+      c = mfma16x16x32(A, qh[j], c);
+      c = mfma16x16x32(A, ql[j], c);
     }
-    return x;
+    return c;
   }
 };
 
 // INT8 or INT4-symmetric codes with a per-(token, group) scale.  K is dequantised
-// exactly like the reference torch path, khat = fp16(code * fp16(scale)), then one
-// MFMA accumulator covers all 128 channels.
-template <bool I4>
+// like the reference torch path, khat = fp16(code * fp16(scale)), then one MFMA
+// accumulator covers all 128 channels.
+template <bool I4, bool SF32>
 struct KTok {
   half8v qb[4];
-  float sm;
+  const uint8_t* kb;
+  int64_t st;
+  const void* sp;
+  int64_t sst, ssg;
+  uint32_t koff[2];
+  int row, lg, gsh[4];
   struct Raw {
-    uint32_t w[I4 ? 4 : 8];
-    uint32_t s[4];
+    uint32_t w[2][I4 ? 4 : 8];
+    uint32_t s[2][4];
   };
 
-  __device__ void setup(const DecodeArgs& a, int b, int hkv, int col, int lg) {
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int col, int lg_) {
+    row = col;
+    lg = lg_;
     const bool valid = col < a.n_rep;
     const int hq = hkv * a.n_rep + (valid ? col : 0);
     const bool has_tau = a.inv_tau != nullptr;
     const half_t tau = has_tau ? a.inv_tau[hq] : (half_t)1.0f;
-    const half_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
-    sm = a.sm_log2e;
+    const half_t* qr = q_row(a, b, hq);
+    half_t qv[32];
+    load_q_group(qr, lg, tau, has_tau, qv);
+#pragma unroll
     for (int j = 0; j < 4; ++j) {
       half_t v8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = 32 * lg + 8 * j + (I4 ? kNibSlotElem(e) : e);
-        v8[e] = valid ? qscale(qrow[d], tau, has_tau) : (half_t)0.0f;
+        const int dl = 8 * j + (I4 ? kNibSlotElem(e) : e);
+        v8[e] = valid ? qv[dl] : (half_t)0.0f;
       }
       qb[j] = half8v{v8[0], v8[1], v8[2], v8[3], v8[4], v8[5], v8[6], v8[7]};
+      gsh[j] = (32 * lg + 8 * j) / a.gs;
     }
+    kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    st = a.k.st;
+    const int span = I4 ? 16 : 32;
+    koff[0] = (uint32_t)(row * st + span * lg);
+    koff[1] = (uint32_t)((row + 16) * st + span * lg);
+    sp = reinterpret_cast<const char*>(a.k.scale) +
+         ((int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh) * (SF32 ? 4 : 2);
+    sst = a.k.sst;
+    ssg = a.k.ssg;
   }
 
-  __device__ __forceinline__ void load(const DecodeArgs& a, int b, int hkv, int t, int lg,
-                                       Raw& r) const {
-    const uint8_t* p = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh +
-                       (int64_t)t * a.k.st;
-    if constexpr (I4) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(p + 16 * lg);
-      r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
-    } else {
-      const u32x4 v0 = *reinterpret_cast<const u32x4*>(p + 32 * lg);
-      const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 32 * lg + 16);
-      r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
-      r.w[4] = v1.x; r.w[5] = v1.y; r.w[6] = v1.z; r.w[7] = v1.w;
-    }
-    const int64_t sbase = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh + (int64_t)t * a.k.sst;
+  __device__ __forceinline__ half_t scale_at(int t, int gi) const {
+    const int64_t off = (int64_t)t * sst + (int64_t)gi * ssg;
+    if constexpr (SF32) return (half_t)(reinterpret_cast<const float*>(sp)[off]);
+    return reinterpret_cast<const half_t*>(sp)[off];
+  }
+
+  __device__ __forceinline__ void load_full(int tt, Raw& r) const { load_impl<true>(tt, 0, r); }
+  __device__ __forceinline__ void load_clamped(int tt, int t1, Raw& r) const {
+    load_impl<false>(tt, t1, r);
+  }
+  template <bool FULL>
+  __device__ __forceinline__ void load_impl(int tt, int t1, Raw& r) const {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int gi = (32 * lg + 8 * j) / a.gs;
-      r.s[j] = splat_h2(ld_scale(a.k, sbase + (int64_t)gi * a.k.ssg));
+    for (int s = 0; s < 2; ++s) {
+      const int t = FULL ? tt + 16 * s + row : min(tt + 16 * s + row, t1 - 1);
+      const uint8_t* p = FULL ? kb + (int64_t)tt * st + koff[s]
+                              : kb + (int64_t)t * st + (I4 ? 16 : 32) * lg;
+      const u32x4 v0 = ld_stream<u32x4>(p);
+      r.w[s][0] = v0.x; r.w[s][1] = v0.y; r.w[s][2] = v0.z; r.w[s][3] = v0.w;
+      if constexpr (!I4) {
+        const u32x4 v1 = ld_stream<u32x4>(p + 16);
+        r.w[s][4] = v1.x; r.w[s][5] = v1.y; r.w[s][6] = v1.z; r.w[s][7] = v1.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.s[s][j] = splat_h2(scale_at(t, gsh[j]));
     }
   }
 
-  __device__ __forceinline__ float4v logits(const Raw& r) const {
+  __device__ __forceinline__ float4v qk(const Raw& r, int s, const NibConsts& nc) const {
     float4v c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t u[4];
       if constexpr (I4) {
-        unpack_dword_64pn(r.w[j], u);
+        unpack_dword_64pn(r.w[s][j], nc, u);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) u[i] = deq_sym4(u[i], r.s[j]);
+        for (int i = 0; i < 4; ++i) u[i] = deq_pair(u[i], (half_t)72.0f, r.s[s][j]);
       } else {
-        const uint32_t w0 = r.w[2 * j] ^ 0x80808080u;
-        const uint32_t w1 = r.w[2 * j + 1] ^ 0x80808080u;
-        u[0] = deq_int8_pair(perm_b32(0u, w0, 0x0c010c00u), r.s[j]);
-        u[1] = deq_int8_pair(perm_b32(0u, w0, 0x0c030c02u), r.s[j]);
-        u[2] = deq_int8_pair(perm_b32(0u, w1, 0x0c010c00u), r.s[j]);
-        u[3] = deq_int8_pair(perm_b32(0u, w1, 0x0c030c02u), r.s[j]);
+        const uint32_t w0 = r.w[s][2 * j] ^ 0x80808080u;
+        const uint32_t w1 = r.w[s][2 * j + 1] ^ 0x80808080u;
+        u[0] = deq_pair(perm_b32(0u, w0, 0x0c010c00u) | nc.c1024, (half_t)1152.0f, r.s[s][j]);
+        u[1] = deq_pair(perm_b32(0u, w0, 0x0c030c02u) | nc.c1024, (half_t)1152.0f, r.s[s][j]);
+        u[2] = deq_pair(perm_b32(0u, w1, 0x0c010c00u) | nc.c1024, (half_t)1152.0f, r.s[s][j]);
+        u[3] = deq_pair(perm_b32(0u, w1, 0x0c030c02u) | nc.c1024, (half_t)1152.0f, r.s[s][j]);
       }
       c = mfma16x16x32(pack8(u[0], u[1], u[2], u[3]), qb[j], c);
     }
-    return c * sm;
+    return c;
   }
 };
 
 // ---------------------------------------------------------------- V formats
 //
 // V^T operand: lane (c = lane % 16, lg = lane / 16) supplies d-row c and the 8 tokens
-// T(lg) = {4lg..4lg+3, 16+4lg..16+4lg+3} of the tile (the tokens whose
-// probabilities the same lane group holds after the QK MFMA).  It reads 8 channels
-// d = 8c..8c+7 of each token; MFMA mb uses channel 8c + mb, so acc[mb][r] holds
-// out^T[d = 32*lg + 8*r + mb, h = lane % 16].
+// T(lg) = {4lg..4lg+3, 16+4lg..16+4lg+3} of the tile, which are the tokens whose
+// probabilities the same lane group holds after the QK MFMA.  It reads channels
+// 8c..8c+7 of each token, and MFMA mb uses channel 8c + mb, so acc[mb][r] holds
+// out^T[d = 32 lg + 8 r + mb, h = lane % 16].  Byte k of two tokens is gathered into
+// one dword with v_perm_b32; its high nibbles (even channels) become 64 + n and its
+// low nibbles (odd channels) 1024 + n.
 
-__device__ __forceinline__ int tile_token(int lg, int e) {
-  return e < 4 ? 4 * lg + e : 16 + 4 * lg + (e - 4);
-}
+__device__ __forceinline__ int tile_token_uniform(int e) { return e < 4 ? e : e + 12; }
 __device__ __forceinline__ uint32_t sel_byte_pair(int k) {
   // [lo.byte_k, 0, hi.byte_k, 0]
   return (uint32_t)k | 0x0c00u | ((uint32_t)(4 + k) << 16) | 0x0c000000u;
 }
 
-// INT4 asymmetric static: accumulate sum_t p16 * (64 + n); the combine applies
-// out = s_g * (acc / l - 72) + zp_g.
+// INT4 asymmetric static: accumulates sum_t p16 * x with x = 64 + n (even d) or 1024 + n
+// (odd d); combine_kernel applies out_d = s_g * (acc_d / l - off_d) + z_g, off_d = 72 or 1032.
 struct VAsym4 {
+  const uint8_t* vb;
+  int64_t st;
+  uint32_t voff;
+  int col, lg;
   struct Raw {
     uint32_t w[8];
   };
-  __device__ void setup(const DecodeArgs&, int, int, int, int) {}
-  __device__ __forceinline__ void load(const DecodeArgs& a, int b, int hkv, int tt, int t1,
-                                       int col, int lg, Raw& r) const {
-    const uint8_t* base = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh + 4 * col;
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int col_, int lg_) {
+    col = col_;
+    lg = lg_;
+    vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    st = a.v.st;
+    voff = (uint32_t)(4 * lg * st + 4 * col);
+  }
+  __device__ __forceinline__ void load_full(int tt, Raw& r) const {
+    const uint8_t* p = vb + (int64_t)tt * st + voff;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      r.w[e] = ld_stream<uint32_t>(p + (int64_t)tile_token_uniform(e) * st);
+  }
+  __device__ __forceinline__ void load_clamped(int tt, int t1, Raw& r) const {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int t = min(tt + tile_token(lg, e), t1 - 1);
-      r.w[e] = *reinterpret_cast<const uint32_t*>(base + (int64_t)t * a.v.st);
+      const int t = min(tt + 4 * lg + tile_token_uniform(e), t1 - 1);
+      r.w[e] = ld_stream<uint32_t>(vb + (int64_t)t * st + 4 * col);
     }
   }
-  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8]) const {
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8],
+                                      const NibConsts& nc) const {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint32_t sel = sel_byte_pair(k);
       uint32_t R[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) R[p] = perm_b32(r.w[2 * p + 1], r.w[2 * p], sel);
-      acc[2 * k] = mfma16x16x32(
-          pack8(nib_hi_pair(R[0]), nib_hi_pair(R[1]), nib_hi_pair(R[2]), nib_hi_pair(R[3])),
-          pb, acc[2 * k]);
-      acc[2 * k + 1] = mfma16x16x32(pack8(nib_hi_pair(R[0] << 4), nib_hi_pair(R[1] << 4),
-                                          nib_hi_pair(R[2] << 4), nib_hi_pair(R[3] << 4)),
-                                    pb, acc[2 * k + 1]);
+      acc[2 * k] = mfma16x16x32(pack8(and_or(R[0], nc.m_hi, nc.c64), and_or(R[1], nc.m_hi, nc.c64),
+                                      and_or(R[2], nc.m_hi, nc.c64), and_or(R[3], nc.m_hi, nc.c64)),
+                                pb, acc[2 * k]);
+      acc[2 * k + 1] =
+          mfma16x16x32(pack8(and_or(R[0], nc.m_lo, nc.c1024), and_or(R[1], nc.m_lo, nc.c1024),
+                             and_or(R[2], nc.m_lo, nc.c1024), and_or(R[3], nc.m_lo, nc.c1024)),
+                       pb, acc[2 * k + 1]);
     }
   }
 };
 
 // INT8 / INT4-symmetric codes with per-(token, group) scale: vhat = fp16(code * scale).
-template <bool I4>
+template <bool I4, bool SF32>
 struct VTok {
+  const uint8_t* vb;
+  int64_t st;
+  const void* sp;
+  int64_t sst;
+  int col, lg;
   struct Raw {
     uint32_t w[8][I4 ? 1 : 2];
     uint32_t s[4];
   };
-  __device__ void setup(const DecodeArgs&, int, int, int, int) {}
-  __device__ __forceinline__ void load(const DecodeArgs& a, int b, int hkv, int tt, int t1,
-                                       int col, int lg, Raw& r) const {
-    const uint8_t* base = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh +
-                          (I4 ? 4 : 8) * col;
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int col_, int lg_) {
+    col = col_;
+    lg = lg_;
+    vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh + (I4 ? 4 : 8) * col;
+    st = a.v.st;
     const int gi = (8 * col) / a.gs;
-    const int64_t sbase = (int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh + (int64_t)gi * a.v.ssg;
+    sp = reinterpret_cast<const char*>(a.v.scale) +
+         ((int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh + (int64_t)gi * a.v.ssg) * (SF32 ? 4 : 2);
+    sst = a.v.sst;
+  }
+  __device__ __forceinline__ void load_full(int tt, Raw& r) const { load_impl<true>(tt, 0, r); }
+  __device__ __forceinline__ void load_clamped(int tt, int t1, Raw& r) const {
+    load_impl<false>(tt, t1, r);
+  }
+  template <bool FULL>
+  __device__ __forceinline__ void load_impl(int tt, int t1, Raw& r) const {
     half_t sv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int t = min(tt + tile_token(lg, e), t1 - 1);
+      int t = tt + 4 * lg + tile_token_uniform(e);
+      if (!FULL) t = min(t, t1 - 1);
+      const uint8_t* p = vb + (int64_t)t * st;
       if constexpr (I4) {
-        r.w[e][0] = *reinterpret_cast<const uint32_t*>(base + (int64_t)t * a.v.st);
+        r.w[e][0] = ld_stream<uint32_t>(p);
       } else {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(base + (int64_t)t * a.v.st);
+        const u32x2 v = ld_stream<u32x2>(p);
         r.w[e][0] = v.x;
         r.w[e][1] = v.y;
       }
-      sv[e] = ld_scale(a.v, sbase + (int64_t)t * a.v.sst);
+      const int64_t so = (int64_t)t * sst;
+      if constexpr (SF32) sv[e] = (half_t)(reinterpret_cast<const float*>(sp)[so]);
+      else sv[e] = reinterpret_cast<const half_t*>(sp)[so];
     }
 #pragma unroll
     for (int p = 0; p < 4; ++p) r.s[p] = pair_h2(sv[2 * p], sv[2 * p + 1]);
   }
-  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8]) const {
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8],
+                                      const NibConsts& nc) const {
     if constexpr (I4) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -341,30 +458,26 @@ struct VTok {
         uint32_t R[4];
 #pragma unroll
         for (int p = 0; p < 4; ++p) R[p] = perm_b32(r.w[2 * p + 1][0], r.w[2 * p][0], sel);
-        acc[2 * k] = mfma16x16x32(
-            pack8(deq_sym4(nib_hi_pair(R[0]), r.s[0]), deq_sym4(nib_hi_pair(R[1]), r.s[1]),
-                  deq_sym4(nib_hi_pair(R[2]), r.s[2]), deq_sym4(nib_hi_pair(R[3]), r.s[3])),
-            pb, acc[2 * k]);
-        acc[2 * k + 1] = mfma16x16x32(pack8(deq_sym4(nib_hi_pair(R[0] << 4), r.s[0]),
-                                            deq_sym4(nib_hi_pair(R[1] << 4), r.s[1]),
-                                            deq_sym4(nib_hi_pair(R[2] << 4), r.s[2]),
-                                            deq_sym4(nib_hi_pair(R[3] << 4), r.s[3])),
-                                      pb, acc[2 * k + 1]);
+        uint32_t h[4], o[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          h[p] = deq_pair(and_or(R[p], nc.m_hi, nc.c64), (half_t)72.0f, r.s[p]);
+          o[p] = deq_pair(and_or(R[p], nc.m_lo, nc.c1024), (half_t)1032.0f, r.s[p]);
+        }
+        acc[2 * k] = mfma16x16x32(pack8(h[0], h[1], h[2], h[3]), pb, acc[2 * k]);
+        acc[2 * k + 1] = mfma16x16x32(pack8(o[0], o[1], o[2], o[3]), pb, acc[2 * k + 1]);
       }
     } else {
-      uint32_t wx[8][2];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        wx[e][0] = r.w[e][0] ^ 0x80808080u;
-        wx[e][1] = r.w[e][1] ^ 0x80808080u;
-      }
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const uint32_t sel = sel_byte_pair(k & 3);
         uint32_t u[4];
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
-          u[p] = deq_int8_pair(perm_b32(wx[2 * p + 1][k >> 2], wx[2 * p][k >> 2], sel), r.s[p]);
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t hi = r.w[2 * p + 1][k >> 2] ^ 0x80808080u;
+          const uint32_t lo = r.w[2 * p][k >> 2] ^ 0x80808080u;
+          u[p] = deq_pair(perm_b32(hi, lo, sel) | nc.c1024, (half_t)1152.0f, r.s[p]);
+        }
         acc[k] = mfma16x16x32(pack8(u[0], u[1], u[2], u[3]), pb, acc[k]);
       }
     }
@@ -373,10 +486,13 @@ struct VTok {
 
 // ---------------------------------------------------------------- main kernel
 
-template <class KF, class VF>
-__global__ __launch_bounds__(kWaves * 64) void decode_splitk_kernel(DecodeArgs a) {
+template <class KF, class VF, int DEPTH>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_splitk_kernel(DecodeArgs a) {
   const int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // wave index is uniform per wave; say so, so tile addressing stays in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, lg = lane >> 4;
 
   int64_t ctx64 = a.ctx[b];
@@ -386,6 +502,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_splitk_kernel(DecodeArgs a
   if (t0 >= ctx) return;  // uniform over the work-group
   const int t1 = min(t0 + a.chunk, ctx);
 
+  NibConsts nc;
+  nc.init();
   KF kf;
   kf.setup(a, b, hkv, col, lg);
   VF vf;
@@ -395,66 +513,83 @@ __global__ __launch_bounds__(kWaves * 64) void decode_splitk_kernel(DecodeArgs a
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
   float m = kNegInf, l = 0.f;
+  const float sm = a.sm_log2e;
   const half2v ones = {(half_t)1.0f, (half_t)1.0f};
+  constexpr int kStep = kTile * kWaves;
+  const int tw = t0 + kTile * wave;
 
-  int tt = t0 + kTile * wave;
-  typename KF::Raw kr0, kr1;
-  typename VF::Raw vr;
-  if (tt < t1) {
-    kf.load(a, b, hkv, min(tt + col, t1 - 1), lg, kr0);
-    kf.load(a, b, hkv, min(tt + 16 + col, t1 - 1), lg, kr1);
-    vf.load(a, b, hkv, tt, t1, col, lg, vr);
-  }
-  for (; tt < t1; tt += kTile * kWaves) {
-    // prefetch the next tile of this wave
-    const int tn = tt + kTile * kWaves;
-    typename KF::Raw nk0, nk1;
-    typename VF::Raw nv;
-    if (tn < t1) {
-      kf.load(a, b, hkv, min(tn + col, t1 - 1), lg, nk0);
-      kf.load(a, b, hkv, min(tn + 16 + col, t1 - 1), lg, nk1);
-      vf.load(a, b, hkv, tn, t1, col, lg, nv);
-    }
-
-    float4v x0 = kf.logits(kr0);
-    float4v x1 = kf.logits(kr1);
-    if (tt + kTile > t1) {
+  // Softmax + PV of one tile whose QK logits (x0: tokens 4lg+r, x1: 16+4lg+r) are known.
+  auto finish = [&](float4v x0, float4v x1, const typename VF::Raw& vt, int tt, bool masked) {
+    if (masked) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if (tt + 4 * lg + r >= t1) x0[r] = kNegInf;
         if (tt + 16 + 4 * lg + r >= t1) x1[r] = kNegInf;
       }
     }
-    float mx = fmaxf(fmaxf(fmaxf(x0[0], x0[1]), fmaxf(x0[2], x0[3])),
-                     fmaxf(fmaxf(x1[0], x1[1]), fmaxf(x1[2], x1[3])));
-    mx = wave_max_xor_groups(mx);
-    const float mn = fmaxf(m, mx);
-    const float alpha = fast_exp2(m - mn);
-    m = mn;
-    float p[8];
+    const float lmax = max8f(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]) * sm;
+    if (__ballot(lmax > m + kTau)) {
+      // raise the running max of every head to its current wave-wide maximum
+      const float mn = fmaxf(m, wave_max_xor_groups(lmax));
+      const float alpha = fast_exp2(m - mn);
+      m = mn;
+      l *= alpha;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = fast_exp2(x0[r] - m);
-      p[4 + r] = fast_exp2(x1[r] - m);
+      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
     }
-    const half2v pp0 = pk_rtz(p[0], p[1]);
-    const half2v pp1 = pk_rtz(p[2], p[3]);
-    const half2v pp2 = pk_rtz(p[4], p[5]);
-    const half2v pp3 = pk_rtz(p[6], p[7]);
+    const float nm = -m;
+    const half2v pp0 = pk_rtz(fast_exp2(fmaf(x0[0], sm, nm)), fast_exp2(fmaf(x0[1], sm, nm)));
+    const half2v pp1 = pk_rtz(fast_exp2(fmaf(x0[2], sm, nm)), fast_exp2(fmaf(x0[3], sm, nm)));
+    const half2v pp2 = pk_rtz(fast_exp2(fmaf(x1[0], sm, nm)), fast_exp2(fmaf(x1[1], sm, nm)));
+    const half2v pp3 = pk_rtz(fast_exp2(fmaf(x1[2], sm, nm)), fast_exp2(fmaf(x1[3], sm, nm)));
     // l accumulates exactly the fp16 probabilities the PV MFMA consumes
-    float ls = __builtin_amdgcn_fdot2(pp0, ones, 0.f, false);
-    ls = __builtin_amdgcn_fdot2(pp1, ones, ls, false);
-    ls = __builtin_amdgcn_fdot2(pp2, ones, ls, false);
-    ls = __builtin_amdgcn_fdot2(pp3, ones, ls, false);
-    l = fmaf(l, alpha, ls);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-    const half8v pb = pack8(as_u32(pp0), as_u32(pp1), as_u32(pp2), as_u32(pp3));
-    vf.mma(vr, pb, acc);
+    l = __builtin_amdgcn_fdot2(pp0, ones, l, false);
+    l = __builtin_amdgcn_fdot2(pp1, ones, l, false);
+    l = __builtin_amdgcn_fdot2(pp2, ones, l, false);
+    l = __builtin_amdgcn_fdot2(pp3, ones, l, false);
+    vf.mma(vt, pack8(as_u32(pp0), as_u32(pp1), as_u32(pp2), as_u32(pp3)), acc, nc);
+  };
 
-    kr0 = nk0;
-    kr1 = nk1;
-    vr = nv;
+  // Full tiles of this wave are tw + i * kStep for i < nfull; the (at most one) partial
+  // tile after them is peeled off with clamped loads and masking.  QK runs one tile
+  // ahead of softmax/PV, so the next tile's MFMA chain overlaps this tile's VALU work.
+  // K tile i + DEPTH and V tile i + DEPTH - 1 are fetched during iteration i.
+  const int nfull = (t1 - tw >= kTile) ? (t1 - tw - kTile) / kStep + 1 : 0;
+  if (nfull > 0) {
+    typename KF::Raw kr[DEPTH];
+    typename VF::Raw vr[DEPTH];
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s)
+      if (s < nfull) kf.load_full(tw + s * kStep, kr[s]);
+#pragma unroll
+    for (int s = 0; s < DEPTH - 1; ++s)
+      if (s < nfull) vf.load_full(tw + s * kStep, vr[s]);
+    float4v xa0 = kf.qk(kr[0], 0, nc), xa1 = kf.qk(kr[0], 1, nc);
+    for (int i0 = 0; i0 < nfull; i0 += DEPTH) {
+#pragma unroll
+      for (int s = 0; s < DEPTH; ++s) {
+        const int i = i0 + s;
+        if (i >= nfull) break;
+        if (i + DEPTH - 1 < nfull) vf.load_full(tw + (i + DEPTH - 1) * kStep, vr[(s + DEPTH - 1) % DEPTH]);
+        float4v xb0 = xa0, xb1 = xa1;
+        if (i + 1 < nfull) {
+          xb0 = kf.qk(kr[(s + 1) % DEPTH], 0, nc);
+          xb1 = kf.qk(kr[(s + 1) % DEPTH], 1, nc);
+        }
+        if (i + DEPTH < nfull) kf.load_full(tw + (i + DEPTH) * kStep, kr[s]);
+        finish(xa0, xa1, vr[s], tw + i * kStep, false);
+        xa0 = xb0;
+        xa1 = xb1;
+      }
+    }
+  }
+  const int ttail = tw + nfull * kStep;
+  if (ttail < t1) {
+    typename KF::Raw kt;
+    typename VF::Raw vt;
+    kf.load_clamped(ttail, t1, kt);
+    vf.load_clamped(ttail, t1, vt);
+    finish(kf.qk(kt, 0, nc), kf.qk(kt, 1, nc), vt, ttail, true);
   }
 
   l = wave_sum_xor_groups(l);
@@ -503,15 +638,19 @@ __global__ __launch_bounds__(kD) void combine_kernel(DecodeArgs a, int v_affine)
     o[d] = (half_t)0.0f;
     return;
   }
+  __shared__ float2 ml[kMaxChunks];
   const int64_t base = ((int64_t)b * a.Hq + hq) * a.n_chunks;
+  for (int c = d; c < nvalid; c += kD) ml[c] = a.part_ml[base + c];
+  __syncthreads();
   float M = kNegInf;
-  for (int c = 0; c < nvalid; ++c) M = fmaxf(M, a.part_ml[base + c].x);
+  for (int c = 0; c < nvalid; ++c) M = fmaxf(M, ml[c].x);
   float num = 0.f, den = 0.f;
+  const float* pa = a.part_acc + base * kD + d;
+#pragma unroll 8
   for (int c = 0; c < nvalid; ++c) {
-    const float2 ml = a.part_ml[base + c];
-    const float e = fast_exp2(ml.x - M);
-    num = fmaf(e, a.part_acc[(base + c) * kD + d], num);
-    den = fmaf(e, ml.y, den);
+    const float e = fast_exp2(ml[c].x - M);
+    num = fmaf(e, pa[(int64_t)c * kD], num);
+    den = fmaf(e, ml[c].y, den);
   }
   float r = num / den;
   if (v_affine) {
@@ -519,7 +658,7 @@ __global__ __launch_bounds__(kD) void combine_kernel(DecodeArgs a, int v_affine)
     const half_t* sc = reinterpret_cast<const half_t*>(a.v.scale);
     const float s = (float)sc[hkv * a.v.ssh + g * a.v.ssg];
     const float z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
-    r = fmaf(s, r - 72.0f, z);
+    r = fmaf(s, r - ((d & 1) ? 1032.0f : 72.0f), z);
   }
   o[d] = (half_t)r;
 }
@@ -535,14 +674,105 @@ int fail(int code, const std::string& msg) {
 
 static bool aligned(const void* p, int n) { return ((uintptr_t)p % n) == 0; }
 
+// Register-ring depth = tiles per wave in flight + 1.  Default: the deepest ring (4, 3
+// or 2) whose kernel needs no scratch (no register spills); KVQ_RING_DEPTH=2|3|4
+// overrides it.
+template <class KF, class VF>
+static const void* kernel_ptr(int depth) {
+  if (depth == 2) return reinterpret_cast<const void*>(&decode_splitk_kernel<KF, VF, 2>);
+  if (depth == 3) return reinterpret_cast<const void*>(&decode_splitk_kernel<KF, VF, 3>);
+  return reinterpret_cast<const void*>(&decode_splitk_kernel<KF, VF, 4>);
+}
+
+template <class KF, class VF>
+static int ring_depth() {
+  static int d = [] {
+    const char* e = getenv("KVQ_RING_DEPTH");
+    if (e) {
+      const int v = atoi(e);
+      if (v >= 2 && v <= 4) return v;
+    }
+    for (int cand = 4; cand >= 2; --cand) {
+      hipFuncAttributes at;
+      if (hipFuncGetAttributes(&at, kernel_ptr<KF, VF>(cand)) == hipSuccess && at.localSizeBytes == 0)
+        return cand;
+    }
+    (void)hipGetLastError();
+    return 2;
+  }();
+  return d;
+}
+
+template <class KF, class VF>
+static const void* selected_kernel() {
+  return kernel_ptr<KF, VF>(ring_depth<KF, VF>());
+}
+
+// (k_format, v_format, scale dtype) -> kernel family; 0 means unsupported
+enum Family { kNone = 0, kI8I8_16, kI8I8_32, kI4I4_16, kI4I4_32, kA4A4, kA4A4o, kI8A4_16, kI8A4_32 };
+
+static Family family(int kf, int vf, int ksf32, int vsf32, int kout) {
+  if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT8_SYM && ksf32 == vsf32)
+    return ksf32 ? kI8I8_32 : kI8I8_16;
+  if (kf == KVQ_FMT_INT4_SYM && vf == KVQ_FMT_INT4_SYM && ksf32 == vsf32)
+    return ksf32 ? kI4I4_32 : kI4I4_16;
+  if (kf == KVQ_FMT_INT4_ASYM && vf == KVQ_FMT_INT4_ASYM) return kout ? kA4A4o : kA4A4;
+  if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT4_ASYM) return ksf32 ? kI8A4_32 : kI8A4_16;
+  return kNone;
+}
+
+static const void* select_kernel(Family f) {
+  switch (f) {
+    case kI8I8_16: return selected_kernel<KTok<false, false>, VTok<false, false>>();
+    case kI8I8_32: return selected_kernel<KTok<false, true>, VTok<false, true>>();
+    case kI4I4_16: return selected_kernel<KTok<true, false>, VTok<true, false>>();
+    case kI4I4_32: return selected_kernel<KTok<true, true>, VTok<true, true>>();
+    case kA4A4: return selected_kernel<KAsym4<false>, VAsym4>();
+    case kA4A4o: return selected_kernel<KAsym4<true>, VAsym4>();
+    case kI8A4_16: return selected_kernel<KTok<false, false>, VAsym4>();
+    case kI8A4_32: return selected_kernel<KTok<false, true>, VAsym4>();
+    default: return nullptr;
+  }
+}
+
+// work-groups of the selected kernel that fit on the device at once
+static int64_t resident_slots(const void* fn) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int64_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1024;
+  std::lock_guard<std::mutex> g(mu);
+  auto key = std::make_pair(fn, dev);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWaves * 64, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      per_cu <= 0 || cus <= 0) {
+    (void)hipGetLastError();
+    return 1024;
+  }
+  const int64_t slots = (int64_t)per_cu * cus;
+  cache[key] = slots;
+  return slots;
+}
+
+// Tokens per work-group: fill every resident work-group slot exactly once when the
+// context is long enough (one wave of work-groups, no tail), in multiples of the
+// 32-token tile, never below kMinChunk.
 int32_t choose_chunk(const kvq_decode_params* p) {
   if (p->chunk_tokens > 0) return p->chunk_tokens;
   const int64_t units = (int64_t)p->batch * p->kv_heads;
-  const int64_t target_wgs = 1024;  // 4 work-groups per CU on 256 CUs
-  int64_t c = (p->capacity * units + target_wgs - 1) / target_wgs;
-  c = ((c + 127) / 128) * 128;
-  if (c < 256) c = 256;
-  if (c > 8192) c = 8192;
+  const void* fn = select_kernel(family(p->k_format, p->v_format, p->k.scale_dtype == KVQ_DTYPE_F32,
+                                        p->v.scale_dtype == KVQ_DTYPE_F32, p->k.n_outlier > 0));
+  const int64_t slots = fn ? resident_slots(fn) : 1024;
+  int64_t per_unit = slots / (units > 0 ? units : 1);
+  if (per_unit < 1) per_unit = 1;
+  int64_t c = (p->capacity + per_unit - 1) / per_unit;
+  c = ((c + kTile - 1) / kTile) * kTile;
+  if (c < kMinChunk) c = kMinChunk;
+  const int64_t min_for_cap = (p->capacity + kMaxChunks - 1) / kMaxChunks;
+  if (c < min_for_cap) c = ((min_for_cap + kTile - 1) / kTile) * kTile;
   return (int32_t)c;
 }
 
@@ -567,9 +797,12 @@ static int check_view(const kvq_kv_view& v, int fmt, bool is_k, const char* name
   if (!v.codes) return fail(KVQ_ERR_INVALID, n + ": codes is NULL");
   if (!v.scale) return fail(KVQ_ERR_INVALID, n + ": scale is NULL");
   const int row_bytes = fmt == KVQ_FMT_INT8_SYM ? kD : kD / 2;
-  if (v.stride_t < row_bytes && v.stride_t != 0)
+  if (v.stride_t < row_bytes)
     return fail(KVQ_ERR_INVALID, n + ": token stride smaller than a code row");
-  const int need = (fmt == KVQ_FMT_INT4_SYM && is_k) ? 16 : (fmt == KVQ_FMT_INT8_SYM ? (is_k ? 16 : 8) : 4);
+  // lane byte offsets within a 32-token tile are 32-bit
+  if (v.stride_t > ((int64_t)1 << 24) || v.outlier_stride_t > ((int64_t)1 << 22))
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": token stride too large");
+  const int need = is_k ? 16 : (fmt == KVQ_FMT_INT8_SYM ? 8 : 4);
   if (!aligned(v.codes, need) || v.stride_b % need || v.stride_h % need || v.stride_t % need)
     return fail(KVQ_ERR_UNSUPPORTED,
                 n + ": code rows must be " + std::to_string(need) + "-byte aligned");
@@ -598,7 +831,17 @@ static int check_view(const kvq_kv_view& v, int fmt, bool is_k, const char* name
 
 template <class KF, class VF>
 static void launch(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((decode_splitk_kernel<KF, VF>), grid, dim3(kWaves * 64), 0, s, a);
+  const int d = ring_depth<KF, VF>();
+  if (d == 2)
+    hipLaunchKernelGGL((decode_splitk_kernel<KF, VF, 2>), grid, dim3(kWaves * 64), 0, s, a);
+  else if (d == 3)
+    hipLaunchKernelGGL((decode_splitk_kernel<KF, VF, 3>), grid, dim3(kWaves * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_splitk_kernel<KF, VF, 4>), grid, dim3(kWaves * 64), 0, s, a);
+}
+
+static int64_t n_chunks_for(const kvq_decode_params* p, int32_t chunk) {
+  return p->capacity > 0 ? (p->capacity + chunk - 1) / chunk : 1;
 }
 
 }  // namespace kvq
@@ -611,9 +854,8 @@ extern "C" int32_t kvq_decode_chunk_tokens(const kvq_decode_params* p) {
 
 extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   if (!p) return 0;
-  const int64_t chunk = choose_chunk(p);
-  const int64_t nch = (p->capacity + chunk - 1) / chunk;
-  const int64_t rows = (int64_t)p->batch * p->q_heads * (nch > 0 ? nch : 1);
+  const int64_t nch = n_chunks_for(p, choose_chunk(p));
+  const int64_t rows = (int64_t)p->batch * p->q_heads * nch;
   return rows * (kD * 4 + 8) + 256;
 }
 
@@ -622,6 +864,8 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   if (p->head_dim != kD) return fail(KVQ_ERR_UNSUPPORTED, "head_dim must be 128");
   if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0)
     return fail(KVQ_ERR_INVALID, "batch/q_heads/kv_heads must be positive");
+  if (p->batch > 65535 || p->kv_heads > 65535 || p->q_heads > 65535)
+    return fail(KVQ_ERR_UNSUPPORTED, "batch/head counts above 65535");
   if (p->q_heads % p->kv_heads)
     return fail(KVQ_ERR_INVALID, "q_heads must be a multiple of kv_heads");
   const int n_rep = p->q_heads / p->kv_heads;
@@ -636,21 +880,21 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   if (!aligned(p->q, 16) || p->q_stride_b % 8 || p->q_stride_h % 8)
     return fail(KVQ_ERR_UNSUPPORTED, "q rows must be 16-byte aligned");
   const int kf = p->k_format, vf = p->v_format;
-  const bool combo_ok = (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT8_SYM) ||
-                        (kf == KVQ_FMT_INT4_SYM && vf == KVQ_FMT_INT4_SYM) ||
-                        (kf == KVQ_FMT_INT4_ASYM && vf == KVQ_FMT_INT4_ASYM) ||
-                        (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT4_ASYM);
-  if (!combo_ok) return fail(KVQ_ERR_UNSUPPORTED, "unsupported (k_format, v_format) pair");
+  const Family fam = family(kf, vf, p->k.scale_dtype == KVQ_DTYPE_F32, p->v.scale_dtype == KVQ_DTYPE_F32,
+                            p->k.n_outlier > 0);
+  if (fam == kNone)
+    return fail(KVQ_ERR_UNSUPPORTED,
+                "unsupported (k_format, v_format) pair or mixed K/V scale dtypes");
   int rc = check_view(p->k, kf, true, "k", gs);
   if (rc) return rc;
   rc = check_view(p->v, vf, false, "v", gs);
   if (rc) return rc;
 
   const int32_t chunk = choose_chunk(p);
-  if (chunk <= 0 || chunk % (kTile * kWaves))
-    return fail(KVQ_ERR_INVALID, "chunk_tokens must be a positive multiple of 128");
-  const int64_t nch64 = p->capacity > 0 ? (p->capacity + chunk - 1) / chunk : 1;
-  if (nch64 > 65535) return fail(KVQ_ERR_UNSUPPORTED, "too many chunks");
+  if (chunk <= 0 || chunk % kTile)
+    return fail(KVQ_ERR_INVALID, "chunk_tokens must be a positive multiple of 32");
+  const int64_t nch64 = n_chunks_for(p, chunk);
+  if (nch64 > kMaxChunks) return fail(KVQ_ERR_UNSUPPORTED, "too many chunks (raise chunk_tokens)");
   const int64_t need = kvq_decode_workspace_bytes(p);
   if (!p->workspace || p->workspace_bytes < need)
     return fail(KVQ_ERR_INVALID, "workspace too small: need " + std::to_string(need) + " bytes");
@@ -677,14 +921,17 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (p->capacity > 0) {
     const dim3 grid((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch);
-    if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT8_SYM)
-      launch<KTok<false>, VTok<false>>(a, grid, s);
-    else if (kf == KVQ_FMT_INT4_SYM)
-      launch<KTok<true>, VTok<true>>(a, grid, s);
-    else if (kf == KVQ_FMT_INT4_ASYM)
-      launch<KAsym4, VAsym4>(a, grid, s);
-    else
-      launch<KTok<false>, VAsym4>(a, grid, s);
+    switch (fam) {
+      case kI8I8_16: launch<KTok<false, false>, VTok<false, false>>(a, grid, s); break;
+      case kI8I8_32: launch<KTok<false, true>, VTok<false, true>>(a, grid, s); break;
+      case kI4I4_16: launch<KTok<true, false>, VTok<true, false>>(a, grid, s); break;
+      case kI4I4_32: launch<KTok<true, true>, VTok<true, true>>(a, grid, s); break;
+      case kA4A4: launch<KAsym4<false>, VAsym4>(a, grid, s); break;
+      case kA4A4o: launch<KAsym4<true>, VAsym4>(a, grid, s); break;
+      case kI8A4_16: launch<KTok<false, false>, VAsym4>(a, grid, s); break;
+      case kI8A4_32: launch<KTok<false, true>, VAsym4>(a, grid, s); break;
+      default: break;
+    }
   }
   hipLaunchKernelGGL(combine_kernel, dim3(p->q_heads, p->batch), dim3(kD), 0, s, a,
                      vf == KVQ_FMT_INT4_ASYM ? 1 : 0);

@@ -50,22 +50,34 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t 
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// Nibble -> fp16 "64 + n" (exponent 6, mantissa LSB = 1/16 so n<<4 lands on the units):
-// (x & 0x00F000F0) | 0x54005400 turns the nibbles sitting in bits 4..7 and 20..23 into
-// two halves 64+n.  Exact.
-constexpr uint32_t kNibMask = 0x00F000F0u;
-constexpr uint32_t kMagic64 = 0x54005400u;
-__device__ __forceinline__ uint32_t nib_hi_pair(uint32_t x) { return (x & kNibMask) | kMagic64; }
+// Nibble -> fp16 conversion by the exponent trick.  A half with exponent field 0x15
+// (0x5400 = 64.0) has a mantissa LSB worth 1/16, so a nibble placed in bits 4..7 of
+// each 16-bit half gives 64 + n exactly: (x & 0x00F000F0) | 0x54005400.  With exponent
+// 0x19 (0x6400 = 1024.0) the LSB is worth 1, so a nibble in bits 0..3 gives 1024 + n:
+// (x & 0x000F000F) | 0x64006400.  Both are one v_and_or_b32 per two values.
+//
+// The masks and magics live in VGPRs (NibConsts) so the compiler can select the
+// three-operand v_and_or_b32: a VOP3 instruction on gfx9 cannot encode literals.
+struct NibConsts {
+  uint32_t m_hi, m_lo, c64, c1024;
+  __device__ __forceinline__ void init() {
+    m_hi = 0x00F000F0u;
+    m_lo = 0x000F000Fu;
+    c64 = 0x54005400u;
+    c1024 = 0x64006400u;
+    asm volatile("" : "+v"(m_hi), "+v"(m_lo), "+v"(c64), "+v"(c1024));
+  }
+};
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
 
 // Packed INT4 dword w holds bytes b0..b3; byte k = (code[2k] << 4) | code[2k+1]
-// (high nibble = even element).  unpack_dword_64pn returns the 8 elements as
-// fp16 values 64 + n in the k-slot order [0, 4, 1, 5, 2, 6, 3, 7] (element index
-// within the dword).
-__device__ __forceinline__ void unpack_dword_64pn(uint32_t w, uint32_t out[4]) {
-  out[0] = nib_hi_pair(w);        // e0, e4
-  out[1] = nib_hi_pair(w << 4);   // e1, e5
-  out[2] = nib_hi_pair(w >> 8);   // e2, e6
-  out[3] = nib_hi_pair(w >> 4);   // e3, e7
+// (high nibble = even element).  unpack_dword_64pn returns the 8 elements as fp16
+// values 64 + n in the k-slot order [0, 4, 1, 5, 2, 6, 3, 7] (element within dword).
+__device__ __forceinline__ void unpack_dword_64pn(uint32_t w, const NibConsts& nc, uint32_t out[4]) {
+  out[0] = and_or(w, nc.m_hi, nc.c64);        // e0, e4
+  out[1] = and_or(w << 4, nc.m_hi, nc.c64);   // e1, e5
+  out[2] = and_or(w >> 8, nc.m_hi, nc.c64);   // e2, e6
+  out[3] = and_or(w >> 4, nc.m_hi, nc.c64);   // e3, e7
 }
 // k-slot -> element-within-dword map for unpack_dword_64pn
 __host__ __device__ constexpr int kNibSlotElem(int slot) {
@@ -88,5 +100,22 @@ __device__ __forceinline__ float wave_sum_xor_groups(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max of 8 floats with v_max3_f32 (no NaN canonicalisation; inputs are finite or -inf)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max8f(float a, float b, float c, float d, float e, float f,
+                                       float g, float h) {
+  return max3f(max3f(a, b, c), max3f(d, e, f), max3f(g, h, h));
+}
+
+// streaming loads: the code bytes are read once, so do not keep them in the caches
+template <class T>
+__device__ __forceinline__ T ld_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
+}
 
 }  // namespace kvq
