@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--chunk", type=int, default=0)
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (debug only)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a 1 GiB device copy three times (rocprof counter calibration)")
     return ap.parse_args()
 
 
@@ -205,16 +207,42 @@ def stream_ceiling(device, nbytes=2 << 30, reps=10):
     return out
 
 
+def copy_probe(device, nbytes=1 << 30, reps=3):
+    """A plain copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters: each
+    launch reads and writes exactly `nbytes`."""
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=device).uniform_()
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes,
+                      "launches": reps}), flush=True)
+
+
+def measured_traffic(cfg_index):
+    """HBM bytes per attention call measured by rocprofv3 counters for this configuration,
+    from profiles/traffic.json (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the
+    factor a copy of known size gives); None if no measurement is recorded."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(f"config{cfg_index}")
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else int(rec["traffic_bytes_per_call"])
+
+
 def cpu_baseline(cfg, layers_dev):
-    """The CPU oracle (reference torch path) on a bounded sample of the workload:
-    one layer, `rows` batch rows at the full context, quantize-on-append of one token
-    + fp16-dequant fp32 attention; scaled to microseconds per layer-step."""
+    """The CPU oracle (reference torch path) on a bounded sample of the workload: one
+    whole layer-step of layer 0 (every batch row at the full context): quantize-on-append
+    of the new token + fp16-dequant fp32 attention, median of at least 3 runs."""
     from oracle import attn as OA
     from oracle import quant as OQ
 
     torch.set_num_threads(os.cpu_count() or 1)
     L0 = layers_dev[0]
-    rows = 1
+    rows = cfg.batch
     sl = slice(0, rows)
     t = L0.tables
     ctx = L0.ctx[sl].cpu()
@@ -249,7 +277,7 @@ def cpu_baseline(cfg, layers_dev):
     times = []
     budget = 20.0
     t_start = time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - t_start) < budget or len(times) < 2:
+    while len(times) < 10 and (time.perf_counter() - t_start) < budget or len(times) < 3:
         t0 = time.perf_counter()
         one()
         times.append(time.perf_counter() - t0)
@@ -261,10 +289,11 @@ def cpu_baseline(cfg, layers_dev):
         "unit": "us/layer-step",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"oracle (reference torch path restated, fp16 dequant + fp32 softmax) on "
-                   f"{rows} of {cfg.batch} batch rows of layer 0 at full context, median of "
-                   f"{len(times)} runs, scaled x{cfg.batch // rows} to the full layer-step; "
-                   f"os.cpu_count()={os.cpu_count()}"),
+        "sample": (f"oracle (reference torch path restated: quantize-on-append, fp16 dequant, "
+                   f"fp32 softmax attention) over {rows} of {cfg.batch} batch rows of layer 0 at "
+                   f"full context, median of {len(times)} runs"
+                   + (f", scaled x{cfg.batch / rows:g} to the full layer-step" if rows != cfg.batch else "")
+                   + f"; os.cpu_count()={os.cpu_count()}"),
     }
 
 
@@ -275,6 +304,9 @@ def main():
                           "measured on one MI355X (see DESIGN.md for how it would shard)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.copy_probe:
+        copy_probe("cuda:0")
+        return
     from llm_kvcache_quantization_amd import _capi as C
     from llm_kvcache_quantization_amd import synthetic as SY
 
@@ -348,7 +380,7 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(cfg.index),
             "bytes_per_launch": nbytes,
             "kernel": "decode_splitk_kernel + combine_kernel (per layer)",
         },

@@ -14,7 +14,7 @@ from .kernels import (  # noqa: F401
     decode_attn_int8,
     decode_attn_k8v4,
 )
-from .cache import INT4AsymKVCache, INT4KVCache, INT8KVCache  # noqa: F401
+from .cache import INT4AsymKVCache, INT4KVCache, INT8KVCache, K8V4KVCache  # noqa: F401
 
 __all__ = [
     "DecodePlan",
@@ -25,4 +25,5 @@ __all__ = [
     "INT8KVCache",
     "INT4KVCache",
     "INT4AsymKVCache",
+    "K8V4KVCache",
 ]

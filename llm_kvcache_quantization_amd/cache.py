@@ -25,8 +25,9 @@ Where the layout differs from the reference:
   ``check_numerics=False`` nothing synchronises.
 
 :class:`INT4AsymKVCache` (asymmetric INT4, static group-32 parameters, optional fp16
-K outlier channels) and :class:`MixedK8V4KVCache` are build-native formats of the
-BASELINE configurations; they have no reference engine.
+K outlier channels) and :class:`K8V4KVCache` (INT8 K, asymmetric INT4 V) hold the
+static-group formats of the benchmark configurations 2-4; the reference has no engine
+for them.
 """
 from __future__ import annotations
 
@@ -618,27 +619,40 @@ def _deq_sym(q: Tensor, s: Tensor) -> Tensor:
     return (q.view(B, H, S, G, D // G).to(s.dtype) * s.unsqueeze(-1)).view(B, H, S, D)
 
 
-class INT4AsymKVCache(_EngineBase):
-    """Asymmetric INT4 cache with static group-32 parameters (build-native format).
+class _StaticG32Cache(_EngineBase):
+    """Caches whose every scale is static per (layer, head, group of 32).
 
-    Per layer: packed codes K/V [B, H, cap, 64] (byte = hi nibble even channel, codes
-    c + 8 with c in [-8, 7]), static fp16 scale/zero-point [L, H, 4] for K and V, and
-    optionally ``k_outlier_idx`` int [L, H, 4]: those 4 K channels per head are also
-    stored verbatim in fp16 [B, H, cap, 4] and replace the dequantised codes.
+    Per layer: K codes [B, H, cap, 64] packed INT4 (asymmetric, byte = hi nibble even
+    channel, codes c + 8 with c in [-8, 7]) or [B, H, cap, 128] INT8 (symmetric); V codes
+    [B, H, cap, 64] packed asymmetric INT4.  The static tables are [L, H, 4].  With
+    ``k_outlier_idx`` (INT4 K only) those 4 K channels per head are also stored verbatim
+    in fp16 [B, H, cap, 4] and replace the dequantised codes.  No per-token scale is
+    stored: the kernels read the static tables.
     """
 
-    def __init__(self, num_layers: int, k_scale: Tensor, k_zp: Tensor, v_scale: Tensor,
+    _k_int8 = False
+
+    def __init__(self, num_layers: int, k_scale: Tensor, k_zp: Optional[Tensor], v_scale: Tensor,
                  v_zp: Tensor, device: str = "cuda", max_seq_len: Optional[int] = None,
                  k_outlier_idx: Optional[Tensor] = None, inv_tau: Optional[Tensor] = None,
                  use_attn_temperature: bool = True, decode_attn_impl: str = "hip_fused",
                  check_numerics: bool = False):
         self._init_common(num_layers, device, max_seq_len, decode_attn_impl, check_numerics)
         self.group_size = 32
+        for name, t in (("k_scale", k_scale), ("v_scale", v_scale), ("v_zp", v_zp)) + \
+                (() if self._k_int8 else (("k_zp", k_zp),)):
+            if t is None or t.ndim != 3 or t.shape[0] != num_layers or t.shape[-1] != 4:
+                raise ValueError(f"{name} must be [L, H, 4], got "
+                                 f"{None if t is None else tuple(t.shape)}")
+        # INT8 K keeps the reference's fp16 clamp(min=1e-5) of the static scale
+        # (src/quant/int8_basic.py:159); the INT4 tables are fp16 as stored.
         self.k_scale = k_scale.to(device=device, dtype=torch.float16).contiguous()
-        self.k_zp = k_zp.to(device=device, dtype=torch.float16).contiguous()
+        self.k_zp = None if self._k_int8 else k_zp.to(device=device, dtype=torch.float16).contiguous()
         self.v_scale = v_scale.to(device=device, dtype=torch.float16).contiguous()
         self.v_zp = v_zp.to(device=device, dtype=torch.float16).contiguous()
         if k_outlier_idx is not None:
+            if self._k_int8:
+                raise ValueError("k_outlier_idx needs INT4 K")
             oi = k_outlier_idx.detach().cpu()
             if oi.ndim != 3 or oi.shape[0] != num_layers or oi.shape[-1] != 4:
                 raise ValueError(f"k_outlier_idx must be [L, H, 4], got {tuple(oi.shape)}")
@@ -665,8 +679,9 @@ class INT4AsymKVCache(_EngineBase):
                 return
         new_cap = self._new_capacity(layer_id, target, cap if self._k[layer_id] is not None else 0)
         old = self._layer_seq_lens[layer_id]
-        nk = torch.empty((B, H, new_cap, 64), dtype=torch.uint8, device=self.device)
-        nv = torch.empty_like(nk)
+        nk = torch.empty((B, H, new_cap, 128 if self._k_int8 else 64), dtype=torch.uint8,
+                         device=self.device)
+        nv = torch.empty((B, H, new_cap, 64), dtype=torch.uint8, device=self.device)
         no = (torch.empty((B, H, new_cap, 4), dtype=torch.float16, device=self.device)
               if self.k_outlier_idx is not None else None)
         if self._k[layer_id] is not None and old:
@@ -680,6 +695,8 @@ class INT4AsymKVCache(_EngineBase):
     def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
         self._validate_kv(layer_id, k, v)
         B, H, S, D = k.shape
+        if self.k_scale.shape[1] != H:
+            raise ValueError(f"calibration vs model heads mismatch: {self.k_scale.shape[1]} vs {H}")
         old = self._layer_seq_lens[layer_id]
         self._ensure(layer_id, B, H, old + S)
         if S == 0:
@@ -687,14 +704,18 @@ class INT4AsymKVCache(_EngineBase):
         status = self._status_buf(k.device) if self.check_numerics else None
         pk, pv = C.AppendParams(), C.AppendParams()
         keep = []
-        for side, p, x, codes, s, z in (("k", pk, k, self._k[layer_id], self.k_scale, self.k_zp),
-                                        ("v", pv, v, self._v[layer_id], self.v_scale, self.v_zp)):
+        kfmt = C.KVQ_FMT_INT8_SYM if self._k_int8 else C.KVQ_FMT_INT4_ASYM
+        for side, p, x, codes, s, z, fmt in (
+                ("k", pk, k, self._k[layer_id], self.k_scale, self.k_zp, kfmt),
+                ("v", pv, v, self._v[layer_id], self.v_scale, self.v_zp, C.KVQ_FMT_INT4_ASYM)):
             xs = x if x.stride(-1) == 1 else x.contiguous()
             keep.append(xs)
             sptr = None if status is None else status.data_ptr() + (0 if side == "k" else 8)
-            _fill_append(p, C.KVQ_FMT_INT4_ASYM, xs, 32, codes, old, sptr)
-            sl, zl = s[layer_id], z[layer_id]
-            p.static_scale, p.static_zp = sl.data_ptr(), zl.data_ptr()
+            _fill_append(p, fmt, xs, 32, codes, old, sptr)
+            sl = s[layer_id]
+            p.static_scale = sl.data_ptr()
+            if z is not None:
+                p.static_zp = z[layer_id].data_ptr()
             p.static_scale_dtype = C.KVQ_DTYPE_F16
             p.static_stride_h, p.static_stride_g = sl.stride()
             if side == "k" and self.k_outlier_idx is not None:
@@ -704,20 +725,16 @@ class INT4AsymKVCache(_EngineBase):
                 p.oo_stride_b, p.oo_stride_h, p.oo_stride_t = oo.stride(0), oo.stride(1), oo.stride(2)
         self._launch_append(pk, pv, k.device)
         if status is not None:
-            self._check_status(layer_id, k.numel(), "INT4-asym", "[-8, 7]")
+            self._check_status(layer_id, k.numel(), "K8V4" if self._k_int8 else "INT4-asym",
+                               "the code range")
         self._layer_seq_lens[layer_id] = old + S
         if layer_id == 0:
             self._seq_len = old + S
 
-    def get_int4_g32_tensors(self, layer_id: int):
-        """(k_codes, v_codes, k_scale, k_zp, v_scale, v_zp, k_outlier_idx, k_outlier_val)."""
+    def _check_layer(self, layer_id: int) -> int:
         if self._k[layer_id] is None:
             raise ValueError(f"Cache for layer {layer_id} is empty")
-        n = self._layer_seq_lens[layer_id]
-        ko = None if self._ko[layer_id] is None else self._ko[layer_id][:, :, :n]
-        oi = None if self.k_outlier_idx is None else self.k_outlier_idx[layer_id]
-        return (self._k[layer_id][:, :, :n], self._v[layer_id][:, :, :n], self.k_scale[layer_id],
-                self.k_zp[layer_id], self.v_scale[layer_id], self.v_zp[layer_id], oi, ko)
+        return self._layer_seq_lens[layer_id]
 
     def clear(self) -> None:
         self._layer_seq_lens = [0] * self.num_layers
@@ -737,3 +754,43 @@ class INT4AsymKVCache(_EngineBase):
                 if b is not None:
                     total += b.numel() * b.element_size()
         return total / (1024 * 1024)
+
+
+class INT4AsymKVCache(_StaticG32Cache):
+    """Asymmetric INT4 K and V with static group-32 scale / zero-point (configs 2 and 3),
+    optionally with 4 fp16 outlier K channels per head."""
+
+    def get_int4_g32_tensors(self, layer_id: int):
+        """(k_codes, v_codes, k_scale, k_zp, v_scale, v_zp, k_outlier_idx, k_outlier_val)."""
+        n = self._check_layer(layer_id)
+        ko = None if self._ko[layer_id] is None else self._ko[layer_id][:, :, :n]
+        oi = None if self.k_outlier_idx is None else self.k_outlier_idx[layer_id]
+        return (self._k[layer_id][:, :, :n], self._v[layer_id][:, :, :n], self.k_scale[layer_id],
+                self.k_zp[layer_id], self.v_scale[layer_id], self.v_zp[layer_id], oi, ko)
+
+
+class K8V4KVCache(_StaticG32Cache):
+    """K INT8 symmetric with a static group-32 scale, V asymmetric INT4 with static group-32
+    scale / zero-point (config 4).  The reference's closest engine is MixedKVCache
+    (src/cache/mixed_kv_cache.py:150-248), whose quantizers are dynamic per token; this
+    one uses the static tables of the INT8 path (src/quant/int8_basic.py:111-164) for K."""
+
+    _k_int8 = True
+
+    def __init__(self, num_layers: int, k_scale: Tensor, v_scale: Tensor, v_zp: Tensor,
+                 device: str = "cuda", max_seq_len: Optional[int] = None,
+                 inv_tau: Optional[Tensor] = None, use_attn_temperature: bool = True,
+                 decode_attn_impl: str = "hip_fused", check_numerics: bool = False):
+        super().__init__(num_layers, k_scale, None, v_scale, v_zp, device=device,
+                         max_seq_len=max_seq_len, inv_tau=inv_tau,
+                         use_attn_temperature=use_attn_temperature,
+                         decode_attn_impl=decode_attn_impl, check_numerics=check_numerics)
+
+    def get_k8v4_tensors(self, layer_id: int):
+        """(k_codes int8 [B,H,n,128], k_scale fp16 [B,H,n,4] (a stride-0 view of the static
+        table after the fp16 clamp to 1e-5), v_codes, v_scale, v_zp)."""
+        n = self._check_layer(layer_id)
+        k = self._k[layer_id][:, :, :n].view(torch.int8)
+        B, H = k.shape[:2]
+        ks = self.k_scale[layer_id].clamp(min=1e-5)[None, :, None, :].expand(B, H, n, 4)
+        return k, ks, self._v[layer_id][:, :, :n], self.v_scale[layer_id], self.v_zp[layer_id]
