@@ -79,7 +79,13 @@ class Layer:
         kb = 128 if cfg.k_format == "int8" else 64
         vb = 128 if cfg.v_format == "int8" else 64
         self.k = torch.empty(B, Hkv, cap, kb, dtype=torch.uint8, device=device)
-        self.v = torch.empty(B, Hkv, cap, vb, dtype=torch.uint8, device=device)
+        # V of the all-INT4-asymmetric formats in the TILE32 layout, as INT4AsymKVCache keeps it
+        self.v_tiled = cfg.k_format != "int8" and cfg.v_format != "int8"
+        if self.v_tiled:
+            assert cap % 32 == 0
+            self.v = torch.empty(B, Hkv, cap // 32, 2048, dtype=torch.uint8, device=device)
+        else:
+            self.v = torch.empty(B, Hkv, cap, vb, dtype=torch.uint8, device=device)
         self.ko = None
         dev = lambda x: None if x is None else x.to(device)
         self.ks, self.kz = dev(t.k_scale), dev(t.k_zp)
@@ -143,6 +149,10 @@ class Layer:
             p.codes_stride_b, p.codes_stride_h, p.codes_stride_t = codes.stride(0), codes.stride(1), codes.stride(2)
             p.write_pos = pos
             p.capacity = codes.shape[2]
+            if side == "v" and self.v_tiled:
+                p.codes_layout = C.KVQ_LAYOUT_TILE32
+                p.codes_stride_t = 64
+                p.capacity = codes.shape[2] * 32
             if side == "k" and self.ko is not None:
                 p.n_outlier = 4
                 p.outlier_idx = self.oidx.data_ptr()
@@ -255,7 +265,11 @@ def cpu_baseline(cfg, layers_dev):
     else:
         kc = L0.k[sl].cpu()
         ko = L0.ko[sl].cpu() if L0.ko is not None else None
-    vc = L0.v[sl].cpu() if cfg.v_format != "int8" else L0.v[sl].cpu().view(torch.int8)
+    if L0.v_tiled:  # the oracle reads packed rows; converted before timing
+        from llm_kvcache_quantization_amd.kernels import untile_v
+        vc = untile_v(L0.v[sl], L0.k.shape[2]).cpu()
+    else:
+        vc = L0.v[sl].cpu() if cfg.v_format != "int8" else L0.v[sl].cpu().view(torch.int8)
 
     def one():
         if cfg.k_format == "int8":
@@ -382,7 +396,8 @@ def main():
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": measured_traffic(cfg.index),
             "bytes_per_launch": nbytes,
-            "kernel": "decode_splitk_kernel + combine_kernel (per layer)",
+            "kernel": ("decode_tiled_kernel" if layers[0].v_tiled else "decode_splitk_kernel")
+                      + " + combine_kernel (one kvq_decode_attn call per layer)",
         },
         "stream_ceiling": ceiling,
         "cpu_baseline": cpu,

@@ -1,5 +1,5 @@
 /*
- * kvq.h -- C ABI of the MI355X (gfx950) quantized-KV decode path.
+ * kvq.h -- C ABI (version 2) of the MI355X (gfx950) quantized-KV decode path.
  *
  * libkvq.so exports three groups of entry points: quantize-on-append, split-K
  * decode attention and error reporting.  Every entry point
@@ -44,6 +44,15 @@ typedef struct ihipStream_t* kvq_stream_t; /* == hipStream_t */
                                and zero-point per (kv head, group of 32); optional fp16
                                side-band holding n_outlier channels per K head verbatim */
 
+/* code layouts (kvq_kv_view.layout, kvq_append_params.codes_layout) */
+#define KVQ_LAYOUT_ROWS 0   /* token-major: the code bytes of token t start at t * stride_t */
+#define KVQ_LAYOUT_TILE32 1 /* INT4_ASYM V only: 32-token tiles of 2048 bytes, tile i at
+                               i * 32 * stride_t (stride_t must be 64).  Within a tile, byte
+                               ((L * 8 + 2 p + k) * 4 + 2 a + j) holds packed byte 4 c + 2 k + j
+                               of token T(g, p, a), where L = 16 g + c (g < 4, c < 16),
+                               T(g, p, a) = 16 (p / 2) + 4 g + 2 (p % 2) + a (p < 4, a, k, j < 2):
+                               the 32 bytes of L are one lane's PV operand on gfx950 */
+
 /* A read-only view of one layer's quantized K or V cache. */
 typedef struct kvq_kv_view {
   const void* codes;     /* code byte of (b=0, h=0, t=0, d=0) */
@@ -60,6 +69,8 @@ typedef struct kvq_kv_view {
   const int32_t* outlier_idx;     /* [H, n_outlier] channel indices, distinct, in [0, D) */
   const void* outlier_val;        /* fp16 [B,H,T,n_outlier] */
   int64_t outlier_stride_b, outlier_stride_h, outlier_stride_t; /* elements */
+  int32_t layout;                 /* KVQ_LAYOUT_ROWS or KVQ_LAYOUT_TILE32 */
+  int32_t reserved;               /* 0 */
 } kvq_kv_view;
 
 /* Decode attention (q_len == 1), split-K with an in-kernel GQA head group.
@@ -91,15 +102,17 @@ typedef struct kvq_decode_params {
   int32_t batch, q_heads, kv_heads, head_dim, group_size;
   int64_t capacity;       /* token dimension of the cache views */
   float sm_scale;
-  int32_t chunk_tokens;   /* tokens per work-group; 0 = choose automatically */
-  void* workspace;        /* device scratch of kvq_decode_workspace_bytes() bytes */
+  int32_t chunk_tokens;   /* split size in tokens (work-groups per (b, kv head) =
+                             ceil(capacity / chunk_tokens)); 0 = choose automatically */
+  void* workspace;        /* device scratch of kvq_decode_workspace_bytes() bytes; calls
+                             sharing a workspace must be ordered on one stream */
   int64_t workspace_bytes;
   void* out;              /* fp16 [B, Hq, D], d contiguous */
   int64_t out_stride_b, out_stride_h; /* elements */
 } kvq_decode_params;
 
 int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream);
-/* chunk size kvq_decode_attn will use for p (p->chunk_tokens if nonzero) */
+/* split size kvq_decode_attn will use for p (p->chunk_tokens if nonzero) */
 int32_t kvq_decode_chunk_tokens(const kvq_decode_params* p);
 /* bytes of workspace kvq_decode_attn needs for p */
 int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p);
@@ -149,6 +162,9 @@ typedef struct kvq_append_params {
   int64_t capacity;        /* token slots in the destination */
   int32_t* status;         /* device int32[2] or NULL: [0] |= 1 if x had NaN/Inf,
                               [1] += number of clipped elements */
+  int32_t codes_layout;    /* KVQ_LAYOUT_ROWS, or KVQ_LAYOUT_TILE32 for INT4_ASYM
+                              (codes_stride_t must then be 64 and capacity a multiple of 32) */
+  int32_t reserved;        /* 0 */
 } kvq_append_params;
 
 /* Appends K and V of one layer with one launch (either pointer may be NULL). */
@@ -157,7 +173,7 @@ int kvq_quant_append(const kvq_append_params* k, const kvq_append_params* v,
 
 /* message for the last non-OK return on this thread ("" if none) */
 const char* kvq_last_error(void);
-/* ABI version (increments on incompatible changes to the structs above) */
+/* ABI version (increments on incompatible changes to the structs above); this is 2 */
 int32_t kvq_abi_version(void);
 
 #ifdef __cplusplus

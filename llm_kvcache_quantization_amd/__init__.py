@@ -13,6 +13,8 @@ from .kernels import (  # noqa: F401
     decode_attn_int4_asym,
     decode_attn_int8,
     decode_attn_k8v4,
+    tile_v,
+    untile_v,
 )
 from .cache import INT4AsymKVCache, INT4KVCache, INT8KVCache, K8V4KVCache  # noqa: F401
 
@@ -22,6 +24,8 @@ __all__ = [
     "decode_attn_int4",
     "decode_attn_int4_asym",
     "decode_attn_k8v4",
+    "tile_v",
+    "untile_v",
     "INT8KVCache",
     "INT4KVCache",
     "INT4AsymKVCache",

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before libkvq.so, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 KVQ_OK = 0
 KVQ_ERR_INVALID = 1
@@ -29,6 +29,9 @@ KVQ_DTYPE_F32 = 1
 KVQ_FMT_INT8_SYM = 1
 KVQ_FMT_INT4_SYM = 2
 KVQ_FMT_INT4_ASYM = 3
+
+KVQ_LAYOUT_ROWS = 0
+KVQ_LAYOUT_TILE32 = 1
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -49,6 +52,7 @@ class KvView(ctypes.Structure):
         ("outlier_idx", c_vp),
         ("outlier_val", c_vp),
         ("outlier_stride_b", c_i64), ("outlier_stride_h", c_i64), ("outlier_stride_t", c_i64),
+        ("layout", c_i32), ("reserved", c_i32),
     ]
 
 
@@ -101,6 +105,7 @@ class AppendParams(ctypes.Structure):
         ("write_pos", c_i64),
         ("capacity", c_i64),
         ("status", c_vp),
+        ("codes_layout", c_i32), ("reserved", c_i32),
     ]
 
 

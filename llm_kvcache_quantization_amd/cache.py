@@ -40,6 +40,7 @@ import torch
 from torch import Tensor
 
 from . import _capi as C
+from .kernels import TILE_BYTES, TILE_TOKENS
 
 logger = logging.getLogger(__name__)
 
@@ -623,8 +624,10 @@ class _StaticG32Cache(_EngineBase):
     """Caches whose every scale is static per (layer, head, group of 32).
 
     Per layer: K codes [B, H, cap, 64] packed INT4 (asymmetric, byte = hi nibble even
-    channel, codes c + 8 with c in [-8, 7]) or [B, H, cap, 128] INT8 (symmetric); V codes
-    [B, H, cap, 64] packed asymmetric INT4.  The static tables are [L, H, 4].  With
+    channel, codes c + 8 with c in [-8, 7]) or [B, H, cap, 128] INT8 (symmetric).  V codes
+    are packed asymmetric INT4; with INT4 K they are kept in the TILE32 layout
+    [B, H, cap / 32, 2048] the decode kernel streams (:func:`kernels.tile_v`), with INT8 K
+    as rows [B, H, cap, 64].  The static tables are [L, H, 4].  With
     ``k_outlier_idx`` (INT4 K only) those 4 K channels per head are also stored verbatim
     in fp16 [B, H, cap, 4] and replace the dequantised codes.  No per-token scale is
     stored: the kernels read the static tables.
@@ -669,6 +672,11 @@ class _StaticG32Cache(_EngineBase):
         self._v: List[Optional[Tensor]] = [None] * n
         self._ko: List[Optional[Tensor]] = [None] * n
 
+    @property
+    def v_tiled(self) -> bool:
+        """V codes are kept in the TILE32 layout (INT4 K) rather than as rows."""
+        return not self._k_int8
+
     def _ensure(self, layer_id, B, H, target):
         cap = self._layer_capacity[layer_id]
         if self._k[layer_id] is not None:
@@ -678,15 +686,21 @@ class _StaticG32Cache(_EngineBase):
             if target <= cap:
                 return
         new_cap = self._new_capacity(layer_id, target, cap if self._k[layer_id] is not None else 0)
+        new_cap = -(-new_cap // TILE_TOKENS) * TILE_TOKENS
         old = self._layer_seq_lens[layer_id]
         nk = torch.empty((B, H, new_cap, 128 if self._k_int8 else 64), dtype=torch.uint8,
                          device=self.device)
-        nv = torch.empty((B, H, new_cap, 64), dtype=torch.uint8, device=self.device)
+        if self.v_tiled:
+            nv = torch.empty((B, H, new_cap // TILE_TOKENS, TILE_BYTES), dtype=torch.uint8,
+                             device=self.device)
+        else:
+            nv = torch.empty((B, H, new_cap, 64), dtype=torch.uint8, device=self.device)
         no = (torch.empty((B, H, new_cap, 4), dtype=torch.float16, device=self.device)
               if self.k_outlier_idx is not None else None)
         if self._k[layer_id] is not None and old:
             nk[:, :, :old] = self._k[layer_id][:, :, :old]
-            nv[:, :, :old] = self._v[layer_id][:, :, :old]
+            vold = -(-old // TILE_TOKENS) if self.v_tiled else old
+            nv[:, :, :vold] = self._v[layer_id][:, :, :vold]
             if no is not None:
                 no[:, :, :old] = self._ko[layer_id][:, :, :old]
         self._k[layer_id], self._v[layer_id], self._ko[layer_id] = nk, nv, no
@@ -712,6 +726,10 @@ class _StaticG32Cache(_EngineBase):
             keep.append(xs)
             sptr = None if status is None else status.data_ptr() + (0 if side == "k" else 8)
             _fill_append(p, fmt, xs, 32, codes, old, sptr)
+            if side == "v" and self.v_tiled:
+                p.codes_layout = C.KVQ_LAYOUT_TILE32
+                p.codes_stride_t = 64
+                p.capacity = codes.shape[2] * TILE_TOKENS
             sl = s[layer_id]
             p.static_scale = sl.data_ptr()
             if z is not None:
@@ -761,11 +779,14 @@ class INT4AsymKVCache(_StaticG32Cache):
     optionally with 4 fp16 outlier K channels per head."""
 
     def get_int4_g32_tensors(self, layer_id: int):
-        """(k_codes, v_codes, k_scale, k_zp, v_scale, v_zp, k_outlier_idx, k_outlier_val)."""
+        """(k_codes [B,H,n,64], v_tiles [B,H,ceil(n/32),2048] (TILE32 layout), k_scale, k_zp,
+        v_scale, v_zp, k_outlier_idx, k_outlier_val [B,H,n,4]).  ``untile_v(v_tiles, n)``
+        gives V as packed rows."""
         n = self._check_layer(layer_id)
         ko = None if self._ko[layer_id] is None else self._ko[layer_id][:, :, :n]
         oi = None if self.k_outlier_idx is None else self.k_outlier_idx[layer_id]
-        return (self._k[layer_id][:, :, :n], self._v[layer_id][:, :, :n], self.k_scale[layer_id],
+        vt = self._v[layer_id][:, :, :-(-n // TILE_TOKENS)]
+        return (self._k[layer_id][:, :, :n], vt, self.k_scale[layer_id],
                 self.k_zp[layer_id], self.v_scale[layer_id], self.v_zp[layer_id], oi, ko)
 
 

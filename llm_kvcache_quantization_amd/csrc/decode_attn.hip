@@ -20,8 +20,7 @@
 // Reference semantics: src/kernels/triton_decode_attn_int8.py:126-303 (online
 // softmax, masking, zero-context rows) and src/engine/patch_model.py:281-377
 // (dequant product code * scale in fp16, fp32 softmax, fp16 output).
-#include "kvq_common.h"
-#include "kvq.h"
+#include "decode_common.h"
 
 #include <cstdlib>
 #include <map>
@@ -30,80 +29,6 @@
 #include <utility>
 
 namespace kvq {
-
-constexpr int kWaves = 4;
-constexpr int kTile = 32;   // tokens per wave iteration (two 16-token MFMA row blocks)
-constexpr int kD = 128;
-constexpr float kTau = 8.0f;  // lazy-rescale headroom in log2 units
-constexpr int kMaxChunks = 2048;
-constexpr int kMinChunk = 256;
-
-struct KvDev {
-  const uint8_t* codes;
-  int64_t sb, sh, st;
-  const void* scale;
-  int64_t ssb, ssh, sst, ssg;
-  int scale_f32;
-  int n_out;
-  const half_t* zp;
-  const int32_t* oidx;
-  const half_t* oval;
-  int64_t osb, osh, ost;
-};
-
-struct DecodeArgs {
-  const half_t* q;
-  int64_t q_sb, q_sh;
-  const half_t* inv_tau;
-  KvDev k, v;
-  const int32_t* ctx;
-  int B, Hq, Hkv, n_rep, gs;
-  int64_t cap;
-  float sm_log2e;
-  int chunk, n_chunks;
-  float* part_acc;  // [B, Hq, n_chunks, 128]
-  float2* part_ml;  // [B, Hq, n_chunks]
-  half_t* out;
-  int64_t o_sb, o_sh;
-};
-
-__device__ __forceinline__ uint32_t splat_h2(half_t s) { return as_u32(half2v{s, s}); }
-__device__ __forceinline__ uint32_t pair_h2(half_t lo, half_t hi) { return as_u32(half2v{lo, hi}); }
-// q' = fp16(q * inv_tau): fp16 x fp16 product rounded once, as torch's Half mul
-__device__ __forceinline__ half_t qscale(half_t x, half_t tau, bool has_tau) {
-  return has_tau ? (half_t)((float)x * (float)tau) : x;
-}
-// two fp32 -> packed fp16, rounding toward zero (v_cvt_pkrtz_f16_f32)
-__device__ __forceinline__ half2v pk_rtz(float a, float b) {
-  return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
-}
-// (x - off) * s on a half2: exact code recovery, then one fp16 rounding of the product
-__device__ __forceinline__ uint32_t deq_pair(uint32_t x, half_t off, uint32_t s2) {
-  const half2v o = {off, off};
-  return as_u32((as_h2(x) - o) * as_h2(s2));
-}
-__device__ __forceinline__ const half_t* q_row(const DecodeArgs& a, int b, int hq) {
-  return a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
-}
-// q'[32 lg + i] for i < 32 (the lane group's quantisation group) with four 16-byte
-// loads issued together; q' = fp16(q * inv_tau) when inv_tau is given
-__device__ __forceinline__ void load_q_group(const half_t* qr, int lg, half_t tau, bool has_tau,
-                                             half_t out[32]) {
-  const u32x4* p = reinterpret_cast<const u32x4*>(qr + 32 * lg);
-  u32x4 v[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = p[i];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const half2v h = as_h2(w[k]);
-      out[8 * i + 2 * k] = qscale(h.x, tau, has_tau);
-      out[8 * i + 2 * k + 1] = qscale(h.y, tau, has_tau);
-    }
-  }
-}
 
 // ---------------------------------------------------------------- K formats
 //
@@ -514,40 +439,14 @@ void decode_splitk_kernel(DecodeArgs a) {
   for (int i = 0; i < 8; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
   float m = kNegInf, l = 0.f;
   const float sm = a.sm_log2e;
-  const half2v ones = {(half_t)1.0f, (half_t)1.0f};
   constexpr int kStep = kTile * kWaves;
   const int tw = t0 + kTile * wave;
 
   // Softmax + PV of one tile whose QK logits (x0: tokens 4lg+r, x1: 16+4lg+r) are known.
   auto finish = [&](float4v x0, float4v x1, const typename VF::Raw& vt, int tt, bool masked) {
-    if (masked) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (tt + 4 * lg + r >= t1) x0[r] = kNegInf;
-        if (tt + 16 + 4 * lg + r >= t1) x1[r] = kNegInf;
-      }
-    }
-    const float lmax = max8f(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]) * sm;
-    if (__ballot(lmax > m + kTau)) {
-      // raise the running max of every head to its current wave-wide maximum
-      const float mn = fmaxf(m, wave_max_xor_groups(lmax));
-      const float alpha = fast_exp2(m - mn);
-      m = mn;
-      l *= alpha;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-    }
-    const float nm = -m;
-    const half2v pp0 = pk_rtz(fast_exp2(fmaf(x0[0], sm, nm)), fast_exp2(fmaf(x0[1], sm, nm)));
-    const half2v pp1 = pk_rtz(fast_exp2(fmaf(x0[2], sm, nm)), fast_exp2(fmaf(x0[3], sm, nm)));
-    const half2v pp2 = pk_rtz(fast_exp2(fmaf(x1[0], sm, nm)), fast_exp2(fmaf(x1[1], sm, nm)));
-    const half2v pp3 = pk_rtz(fast_exp2(fmaf(x1[2], sm, nm)), fast_exp2(fmaf(x1[3], sm, nm)));
-    // l accumulates exactly the fp16 probabilities the PV MFMA consumes
-    l = __builtin_amdgcn_fdot2(pp0, ones, l, false);
-    l = __builtin_amdgcn_fdot2(pp1, ones, l, false);
-    l = __builtin_amdgcn_fdot2(pp2, ones, l, false);
-    l = __builtin_amdgcn_fdot2(pp3, ones, l, false);
-    vf.mma(vt, pack8(as_u32(pp0), as_u32(pp1), as_u32(pp2), as_u32(pp3)), acc, nc);
+    if (masked) mask_tile(x0, x1, tt, t1, lg);
+    const half8v pb = softmax_tile(x0, x1, sm, m, l, acc);
+    vf.mma(vt, pb, acc, nc);
   };
 
   // Full tiles of this wave are tw + i * kStep for i < nfull; the (at most one) partial
@@ -592,75 +491,17 @@ void decode_splitk_kernel(DecodeArgs a) {
     finish(kf.qk(kt, 0, nc), kf.qk(kt, 1, nc), vt, ttail, true);
   }
 
-  l = wave_sum_xor_groups(l);
-
-  // ---- merge the 4 waves of the work-group through LDS
-  __shared__ float sm_m[kWaves][16];
-  __shared__ float sm_l[kWaves][16];
-  __shared__ float sm_acc[kWaves][16][kD + 1];
-  if (lg == 0) {
-    sm_m[wave][col] = m;
-    sm_l[wave][col] = l;
-  }
-#pragma unroll
-  for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sm_acc[wave][col][32 * lg + 8 * r + mb] = acc[mb][r];
-  __syncthreads();
-
-  for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kWaves * 64) {
-    const int h = idx >> 7, d = idx & (kD - 1);
-    float M = sm_m[0][h];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float e = fast_exp2(sm_m[w][h] - M);
-      num = fmaf(e, sm_acc[w][h][d], num);
-      den = fmaf(e, sm_l[w][h], den);
-    }
-    const int hq = hkv * a.n_rep + h;
-    const int64_t pi = ((int64_t)b * a.Hq + hq) * a.n_chunks + chunk;
-    a.part_acc[pi * kD + d] = num;
-    if (d == 0) a.part_ml[pi] = float2{M, den};
-  }
+  __shared__ MergeLds msh;
+  merge_and_store(a, msh, wave, col, lg, m, l, acc, b, hkv, chunk);
 }
 
-// Combine the chunk partials of one (b, query head) and apply the V epilogue.
+// Combine the chunk partials of one (b, query head) and apply the V epilogue (the
+// row-layout kernels; the tiled kernels combine in their last work-group).
 __global__ __launch_bounds__(kD) void combine_kernel(DecodeArgs a, int v_affine) {
   const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   int64_t ctx64 = a.ctx[b];
   ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);
-  const int nvalid = (int)((ctx64 + a.chunk - 1) / a.chunk);
-  half_t* o = a.out + (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh;
-  if (nvalid == 0) {
-    o[d] = (half_t)0.0f;
-    return;
-  }
-  __shared__ float2 ml[kMaxChunks];
-  const int64_t base = ((int64_t)b * a.Hq + hq) * a.n_chunks;
-  for (int c = d; c < nvalid; c += kD) ml[c] = a.part_ml[base + c];
-  __syncthreads();
-  float M = kNegInf;
-  for (int c = 0; c < nvalid; ++c) M = fmaxf(M, ml[c].x);
-  float num = 0.f, den = 0.f;
-  const float* pa = a.part_acc + base * kD + d;
-#pragma unroll 8
-  for (int c = 0; c < nvalid; ++c) {
-    const float e = fast_exp2(ml[c].x - M);
-    num = fmaf(e, pa[(int64_t)c * kD], num);
-    den = fmaf(e, ml[c].y, den);
-  }
-  float r = num / den;
-  if (v_affine) {
-    const int hkv = hq / a.n_rep, g = d >> 5;
-    const half_t* sc = reinterpret_cast<const half_t*>(a.v.scale);
-    const float s = (float)sc[hkv * a.v.ssh + g * a.v.ssg];
-    const float z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
-    r = fmaf(s, r - ((d & 1) ? 1032.0f : 72.0f), z);
-  }
-  o[d] = (half_t)r;
+  combine_one(a, b, hq, d, valid_chunks(a, ctx64), v_affine);
 }
 
 // ---------------------------------------------------------------- host side
@@ -757,19 +598,25 @@ static int64_t resident_slots(const void* fn) {
   return slots;
 }
 
+// the split-K kernel kvq_decode_attn launches for p (nullptr if unsupported)
+static const void* kernel_for(const kvq_decode_params* p) {
+  if (p->v.layout == KVQ_LAYOUT_TILE32) return tiled_kernel(p->k_format, p->k.n_outlier > 0);
+  return select_kernel(family(p->k_format, p->v_format, p->k.scale_dtype == KVQ_DTYPE_F32,
+                              p->v.scale_dtype == KVQ_DTYPE_F32, p->k.n_outlier > 0));
+}
+
 // Tokens per work-group: fill every resident work-group slot exactly once when the
 // context is long enough (one wave of work-groups, no tail), in multiples of the
-// 32-token tile, never below kMinChunk.
+// kWaves x 32 tokens one pass of the work-group covers, never below kMinChunk.
 int32_t choose_chunk(const kvq_decode_params* p) {
   if (p->chunk_tokens > 0) return p->chunk_tokens;
   const int64_t units = (int64_t)p->batch * p->kv_heads;
-  const void* fn = select_kernel(family(p->k_format, p->v_format, p->k.scale_dtype == KVQ_DTYPE_F32,
-                                        p->v.scale_dtype == KVQ_DTYPE_F32, p->k.n_outlier > 0));
+  const void* fn = kernel_for(p);
   const int64_t slots = fn ? resident_slots(fn) : 1024;
   int64_t per_unit = slots / (units > 0 ? units : 1);
   if (per_unit < 1) per_unit = 1;
   int64_t c = (p->capacity + per_unit - 1) / per_unit;
-  c = ((c + kTile - 1) / kTile) * kTile;
+  c = ((c + kTile * kWaves - 1) / (kTile * kWaves)) * (kTile * kWaves);
   if (c < kMinChunk) c = kMinChunk;
   const int64_t min_for_cap = (p->capacity + kMaxChunks - 1) / kMaxChunks;
   if (c < min_for_cap) c = ((min_for_cap + kTile - 1) / kTile) * kTile;
@@ -789,12 +636,21 @@ static KvDev to_dev(const kvq_kv_view& v) {
   d.oidx = v.outlier_idx;
   d.oval = reinterpret_cast<const half_t*>(v.outlier_val);
   d.osb = v.outlier_stride_b; d.osh = v.outlier_stride_h; d.ost = v.outlier_stride_t;
+  d.layout = v.layout;
   return d;
 }
 
 static int check_view(const kvq_kv_view& v, int fmt, bool is_k, const char* name, int gs) {
   std::string n(name);
   if (!v.codes) return fail(KVQ_ERR_INVALID, n + ": codes is NULL");
+  if (v.layout != KVQ_LAYOUT_ROWS && v.layout != KVQ_LAYOUT_TILE32)
+    return fail(KVQ_ERR_INVALID, n + ": unknown layout");
+  if (v.layout == KVQ_LAYOUT_TILE32) {
+    if (is_k || fmt != KVQ_FMT_INT4_ASYM)
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": the TILE32 layout is for INT4_ASYM V only");
+    if (v.stride_t != kD / 2)
+      return fail(KVQ_ERR_INVALID, n + ": TILE32 needs stride_t == 64");
+  }
   if (!v.scale) return fail(KVQ_ERR_INVALID, n + ": scale is NULL");
   const int row_bytes = fmt == KVQ_FMT_INT8_SYM ? kD : kD / 2;
   if (v.stride_t < row_bytes)
@@ -852,6 +708,7 @@ extern "C" int32_t kvq_decode_chunk_tokens(const kvq_decode_params* p) {
   return p ? choose_chunk(p) : 0;
 }
 
+// workspace: partial acc [B, Hq, n_chunks, 128] f32, then partial (m, l) [B, Hq, n_chunks]
 extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   if (!p) return 0;
   const int64_t nch = n_chunks_for(p, choose_chunk(p));
@@ -885,6 +742,14 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   if (fam == kNone)
     return fail(KVQ_ERR_UNSUPPORTED,
                 "unsupported (k_format, v_format) pair or mixed K/V scale dtypes");
+  const bool tiled = p->v.layout == KVQ_LAYOUT_TILE32;
+  if (tiled && !tiled_kernel(kf, p->k.n_outlier > 0))
+    return fail(KVQ_ERR_UNSUPPORTED, "TILE32 V is supported with INT4_ASYM K only");
+  if (tiled && (p->k.stride_t != kD / 2 || (p->k.n_outlier && p->k.outlier_stride_t != 4)))
+    return fail(KVQ_ERR_UNSUPPORTED, "with TILE32 V, K rows and outlier rows must be dense");
+  // buffer loads address each (b, head) slab with 32-bit byte offsets
+  if (tiled && (p->capacity + kTile) * p->k.stride_t >= ((int64_t)1 << 31))
+    return fail(KVQ_ERR_UNSUPPORTED, "capacity too large for one (b, head) slab");
   int rc = check_view(p->k, kf, true, "k", gs);
   if (rc) return rc;
   rc = check_view(p->v, vf, false, "v", gs);
@@ -912,14 +777,19 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   a.sm_log2e = p->sm_scale * kLog2e;
   a.chunk = chunk;
   a.n_chunks = (int)nch64;
+  a.strided = tiled ? 1 : 0;
   const int64_t rows = (int64_t)p->batch * p->q_heads * nch64;
   a.part_acc = reinterpret_cast<float*>(p->workspace);
   a.part_ml = reinterpret_cast<float2*>(reinterpret_cast<char*>(p->workspace) + rows * kD * 4);
+
   a.out = reinterpret_cast<half_t*>(p->out);
   a.o_sb = p->out_stride_b; a.o_sh = p->out_stride_h;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (p->capacity > 0) {
+  if (p->capacity > 0 && tiled) {
+    launch_tiled(a, kf, p->k.n_outlier > 0,
+                 dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch), s);
+  } else if (p->capacity > 0) {
     const dim3 grid((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch);
     switch (fam) {
       case kI8I8_16: launch<KTok<false, false>, VTok<false, false>>(a, grid, s); break;
@@ -941,4 +811,4 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
 }
 
 extern "C" const char* kvq_last_error(void) { return g_last_error.c_str(); }
-extern "C" int32_t kvq_abi_version(void) { return 1; }
+extern "C" int32_t kvq_abi_version(void) { return 2; }

@@ -1,0 +1,244 @@
+// Definitions shared by the split-K decode kernels (decode_attn.hip, decode_tiled.hip).
+#pragma once
+#include "kvq_common.h"
+#include "kvq.h"
+
+#include <string>
+
+namespace kvq {
+
+constexpr int kWaves = 4;
+constexpr int kTile = 32;   // tokens per wave iteration (two 16-token MFMA row blocks)
+constexpr int kD = 128;
+constexpr float kTau = 8.0f;  // lazy-rescale headroom in log2 units
+constexpr int kMaxChunks = 2048;
+constexpr int kMinChunk = 256;
+
+struct KvDev {
+  const uint8_t* codes;
+  int64_t sb, sh, st;
+  const void* scale;
+  int64_t ssb, ssh, sst, ssg;
+  int scale_f32;
+  int n_out;
+  const half_t* zp;
+  const int32_t* oidx;
+  const half_t* oval;
+  int64_t osb, osh, ost;
+  int layout;  // KVQ_LAYOUT_*
+};
+
+struct DecodeArgs {
+  const half_t* q;
+  int64_t q_sb, q_sh;
+  const half_t* inv_tau;
+  KvDev k, v;
+  const int32_t* ctx;
+  int B, Hq, Hkv, n_rep, gs;
+  int64_t cap;
+  float sm_log2e;
+  int chunk, n_chunks;
+  int strided;      // work-group c takes 32-token tiles c*kWaves + w + i*n_chunks*kWaves
+                    // (wave w) instead of the contiguous tokens [c*chunk, (c+1)*chunk)
+  float* part_acc;  // [B, Hq, n_chunks, 128]
+  float2* part_ml;  // [B, Hq, n_chunks]
+  half_t* out;
+  int64_t o_sb, o_sh;
+};
+
+__device__ __forceinline__ uint32_t splat_h2(half_t s) { return as_u32(half2v{s, s}); }
+__device__ __forceinline__ uint32_t pair_h2(half_t lo, half_t hi) { return as_u32(half2v{lo, hi}); }
+// q' = fp16(q * inv_tau): fp16 x fp16 product rounded once, as torch's Half mul
+__device__ __forceinline__ half_t qscale(half_t x, half_t tau, bool has_tau) {
+  return has_tau ? (half_t)((float)x * (float)tau) : x;
+}
+// two fp32 -> packed fp16, rounding toward zero (v_cvt_pkrtz_f16_f32)
+__device__ __forceinline__ half2v pk_rtz(float a, float b) {
+  return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+// (x - off) * s on a half2: exact code recovery, then one fp16 rounding of the product
+__device__ __forceinline__ uint32_t deq_pair(uint32_t x, half_t off, uint32_t s2) {
+  const half2v o = {off, off};
+  return as_u32((as_h2(x) - o) * as_h2(s2));
+}
+__device__ __forceinline__ const half_t* q_row(const DecodeArgs& a, int b, int hq) {
+  return a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
+}
+// q'[32 lg + i] for i < 32 (the lane group's quantisation group) with four 16-byte
+// loads issued together; q' = fp16(q * inv_tau) when inv_tau is given
+__device__ __forceinline__ void load_q_group(const half_t* qr, int lg, half_t tau, bool has_tau,
+                                             half_t out[32]) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(qr + 32 * lg);
+  u32x4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = p[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const half2v h = as_h2(w[k]);
+      out[8 * i + 2 * k] = qscale(h.x, tau, has_tau);
+      out[8 * i + 2 * k + 1] = qscale(h.y, tau, has_tau);
+    }
+  }
+}
+
+// Online-softmax update of one 32-token tile.  x0 / x1 are the fp32 logits of tokens
+// 4 lg + r and 16 + 4 lg + r (r < 4) for head lane % 16, already masked to -inf where
+// invalid.  The running max m is raised only when a tile's max exceeds it by more than
+// kTau (decided wave-wide with a ballot), in which case l and acc are rescaled.
+// Returns the fp16 probabilities (rounded toward zero) as the PV B operand, in k-slot
+// order [4lg, 4lg+1, 4lg+2, 4lg+3, 16+4lg, .., 16+4lg+3]; l accumulates exactly those
+// fp16 values.
+__device__ __forceinline__ half8v softmax_tile(float4v x0, float4v x1, float sm, float& m,
+                                               float& l, float4v acc[8]) {
+  const float lmax = max8f(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]) * sm;
+  if (__ballot(lmax > m + kTau)) {
+    // raise the running max of every head to its current wave-wide maximum
+    const float mn = fmaxf(m, wave_max_xor_groups(lmax));
+    const float alpha = fast_exp2(m - mn);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+  }
+  const float nm = -m;
+  const half2v pp0 = pk_rtz(fast_exp2(fmaf(x0[0], sm, nm)), fast_exp2(fmaf(x0[1], sm, nm)));
+  const half2v pp1 = pk_rtz(fast_exp2(fmaf(x0[2], sm, nm)), fast_exp2(fmaf(x0[3], sm, nm)));
+  const half2v pp2 = pk_rtz(fast_exp2(fmaf(x1[0], sm, nm)), fast_exp2(fmaf(x1[1], sm, nm)));
+  const half2v pp3 = pk_rtz(fast_exp2(fmaf(x1[2], sm, nm)), fast_exp2(fmaf(x1[3], sm, nm)));
+  const half2v ones = {(half_t)1.0f, (half_t)1.0f};
+  l = __builtin_amdgcn_fdot2(pp0, ones, l, false);
+  l = __builtin_amdgcn_fdot2(pp1, ones, l, false);
+  l = __builtin_amdgcn_fdot2(pp2, ones, l, false);
+  l = __builtin_amdgcn_fdot2(pp3, ones, l, false);
+  return pack8(as_u32(pp0), as_u32(pp1), as_u32(pp2), as_u32(pp3));
+}
+
+// masks logits of tokens >= t1 (tile starts at tt) to -inf
+__device__ __forceinline__ void mask_tile(float4v& x0, float4v& x1, int tt, int t1, int lg) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (tt + 4 * lg + r >= t1) x0[r] = kNegInf;
+    if (tt + 16 + 4 * lg + r >= t1) x1[r] = kNegInf;
+  }
+}
+
+// Merges the (m, l, acc) states of the kWaves waves of a work-group through LDS and
+// writes one partial (M, L, acc[128]) per valid head of this chunk.  acc[mb][r] of lane
+// (head, lg) holds channel d = 32 lg + 8 r + mb.
+struct MergeLds {
+  float m[kWaves][16];
+  float l[kWaves][16];
+  float acc[kWaves][16][kD + 1];
+};
+
+__device__ __forceinline__ void merge_and_store(const DecodeArgs& a, MergeLds& sh, int wave,
+                                                int col, int lg, float m, float l,
+                                                const float4v acc[8], int b, int hkv, int chunk) {
+  l = wave_sum_xor_groups(l);
+  if (lg == 0) {
+    sh.m[wave][col] = m;
+    sh.l[wave][col] = l;
+  }
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sh.acc[wave][col][32 * lg + 8 * r + mb] = acc[mb][r];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kWaves * 64) {
+    const int h = idx >> 7, d = idx & (kD - 1);
+    float M = sh.m[0][h];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sh.m[w][h]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float e = fast_exp2(sh.m[w][h] - M);
+      num = fmaf(e, sh.acc[w][h][d], num);
+      den = fmaf(e, sh.l[w][h], den);
+    }
+    const int hq = hkv * a.n_rep + h;
+    const int64_t pi = ((int64_t)b * a.Hq + hq) * a.n_chunks + chunk;
+    a.part_acc[pi * kD + d] = num;
+    if (d == 0) a.part_ml[pi] = float2{M, den};
+  }
+}
+
+// number of work-groups (partials) with at least one token for a context of ctx tokens
+__host__ __device__ __forceinline__ int valid_chunks(const DecodeArgs& a, int64_t ctx) {
+  if (a.strided) {
+    const int64_t tiles = (ctx + kTile - 1) / kTile;
+    const int64_t n = (tiles + kWaves - 1) / kWaves;
+    return (int)(n < a.n_chunks ? n : a.n_chunks);
+  }
+  return (int)((ctx + a.chunk - 1) / a.chunk);
+}
+
+// Merges the first nvalid chunk partials of (b, query head hq) for output channel d and
+// writes the fp16 output, applying the asymmetric V epilogue
+// out = s (acc / l - off) + z (off = 72 or 1032 by channel parity) when v_affine.
+// Every partial of a batch of kCombineBatch chunks is requested before any is used.
+constexpr int kCombineBatch = 32;
+
+__device__ __forceinline__ void combine_one(const DecodeArgs& a, int b, int hq, int d, int nvalid,
+                                            int v_affine) {
+  half_t* o = a.out + (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh;
+  if (nvalid <= 0) {
+    o[d] = (half_t)0.0f;
+    return;
+  }
+  const int64_t base = ((int64_t)b * a.Hq + hq) * a.n_chunks;
+  const float* pa = a.part_acc + base * kD + d;
+  const float2* pm = a.part_ml + base;
+  float M = kNegInf, num = 0.f, den = 0.f;
+  for (int c0 = 0; c0 < nvalid; c0 += kCombineBatch) {
+    const int n = nvalid - c0 < kCombineBatch ? nvalid - c0 : kCombineBatch;
+    float av[kCombineBatch];
+    float2 mv[kCombineBatch];
+#pragma unroll
+    for (int c = 0; c < kCombineBatch; ++c) {
+      av[c] = 0.f;
+      mv[c] = float2{kNegInf, 0.f};
+      if (c < n) {
+        av[c] = pa[(int64_t)(c0 + c) * kD];
+        mv[c] = pm[c0 + c];
+      }
+    }
+    float Mb = M;
+#pragma unroll
+    for (int c = 0; c < kCombineBatch; ++c)
+      if (c < n) Mb = fmaxf(Mb, mv[c].x);
+    const float r = fast_exp2(M - Mb);  // 0 on the first batch (M = -inf)
+    num *= r;
+    den *= r;
+    M = Mb;
+#pragma unroll
+    for (int c = 0; c < kCombineBatch; ++c) {
+      if (c < n) {
+        const float e = fast_exp2(mv[c].x - M);
+        num = fmaf(e, av[c], num);
+        den = fmaf(e, mv[c].y, den);
+      }
+    }
+  }
+  float r = num / den;
+  if (v_affine) {
+    const int hkv = hq / a.n_rep, g = d >> 5;
+    const float s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
+    const float z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
+    r = fmaf(s, r - ((d & 1) ? 1032.0f : 72.0f), z);
+  }
+  o[d] = (half_t)r;
+}
+
+// ---- host side (decode_attn.hip)
+int fail(int code, const std::string& msg);
+
+// ---- tiled-V kernels (decode_tiled.hip)
+// kernel of the tiled family for K format kf (kout: outlier channels), or nullptr
+const void* tiled_kernel(int kf, int kout);
+void launch_tiled(const DecodeArgs& a, int kf, int kout, dim3 grid, hipStream_t s);
+
+}  // namespace kvq

@@ -52,7 +52,19 @@ struct AppendDev {
   int64_t oosb, oosh, oost;
   int64_t wpos;
   int32_t* status;
+  int tile32;  // codes in KVQ_LAYOUT_TILE32 (INT4_ASYM)
 };
+
+// Byte offset, within the (b, h) slab of a KVQ_LAYOUT_TILE32 cache, of packed byte bi
+// (0..63) of token t: tile t / 32 holds for lane L = 16 g + c the 32 bytes of its PV
+// operand, dword 2 p + k = bytes (4c + 2k, 4c + 2k + 1) of the two tokens a = 0, 1 of
+// pair p, where token r = t % 32 = 16 (p / 2) + 4 g + 2 (p % 2) + a.
+__device__ __forceinline__ int64_t tile32_offset(int64_t t, int bi) {
+  const int r = (int)(t & 31);
+  const int g = (r & 15) >> 2, p = 2 * (r >> 4) + ((r & 3) >> 1), a = r & 1;
+  const int c = bi >> 2, k = (bi >> 1) & 1, j = bi & 1;
+  return (t >> 5) * 2048 + ((16 * g + c) * 8 + 2 * p + k) * 4 + 2 * a + j;
+}
 
 __device__ __forceinline__ float ld_static(const AppendDev& a, int h, int g) {
   const int64_t off = (int64_t)h * a.st_sh + (int64_t)g * a.st_sg;
@@ -162,7 +174,11 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
     clipped = (r0 < -8.f || r0 > 7.f) + (r1 < -8.f || r1 > 7.f);
     const int c0 = (int)fminf(fmaxf(r0, -8.f), 7.f);
     const int c1 = (int)fminf(fmaxf(r1, -8.f), 7.f);
-    crow[lane] = (uint8_t)(((c0 + 8) << 4) | (c1 + 8));
+    const uint8_t byte = (uint8_t)(((c0 + 8) << 4) | (c1 + 8));
+    if (a.tile32)
+      a.codes[(int64_t)b * a.csb + (int64_t)h * a.csh + tile32_offset(t, lane)] = byte;
+    else
+      crow[lane] = byte;
     if (a.n_out > 0 && lane < a.n_out) {
       const int ch = min(max(a.oidx[h * a.n_out + lane], 0), 127);
       half_t* orow = a.oo + (int64_t)b * a.oosb + (int64_t)h * a.oosh + t * a.oost;
@@ -273,6 +289,14 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   } else if (p->n_outlier != 0) {
     return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
   }
+  if (p->codes_layout != KVQ_LAYOUT_ROWS && p->codes_layout != KVQ_LAYOUT_TILE32)
+    return fail(KVQ_ERR_INVALID, n + ": unknown codes_layout");
+  if (p->codes_layout == KVQ_LAYOUT_TILE32) {
+    if (p->format != KVQ_FMT_INT4_ASYM)
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": the TILE32 layout is for INT4_ASYM only");
+    if (p->codes_stride_t != 64 || p->capacity % 32)
+      return fail(KVQ_ERR_INVALID, n + ": TILE32 needs codes_stride_t == 64 and capacity % 32 == 0");
+  }
   if (p->format == KVQ_FMT_INT4_SYM && p->static_scale && p->rescue_quantile > 0.f &&
       !p->rescue_all && (int64_t)p->batch * p->heads * p->seq_new * (128 / gs) > kRescueMax)
     return fail(KVQ_ERR_UNSUPPORTED,
@@ -297,6 +321,7 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   d.oosb = p->oo_stride_b; d.oosh = p->oo_stride_h; d.oost = p->oo_stride_t;
   d.wpos = p->write_pos;
   d.status = p->status;
+  d.tile32 = p->codes_layout == KVQ_LAYOUT_TILE32;
   return KVQ_OK;
 }
 

@@ -59,6 +59,58 @@ def kv_view_tok(codes: torch.Tensor, scale: torch.Tensor) -> C.KvView:
     return v
 
 
+# ---------------------------------------------------------------- TILE32 layout
+#
+# Asymmetric INT4 V can be stored in 32-token tiles of 2048 bytes ([B, H, T/32, 2048])
+# in which lane L = 16 g + c of the decode kernel finds its PV operand at bytes
+# [32 L, 32 L + 32): dword 2 p + k holds packed bytes (4 c + 2 k, 4 c + 2 k + 1) of the
+# two tokens a = 0, 1 of k-slot pair p, token r = 16 (p // 2) + 4 g + 2 (p % 2) + a.
+TILE_TOKENS = 32
+TILE_BYTES = TILE_TOKENS * HEAD_DIM // 2
+_TILE_OFF = {}
+
+
+def _tile32_offsets(device) -> torch.Tensor:
+    """int64 [32 * 64]: byte offset within a tile of packed byte bi of tile token r,
+    indexed by r * 64 + bi."""
+    key = str(device)
+    if key not in _TILE_OFF:
+        r = torch.arange(TILE_TOKENS).view(-1, 1)
+        bi = torch.arange(HEAD_DIM // 2).view(1, -1)
+        g, p, a = (r % 16) // 4, 2 * (r // 16) + (r % 4) // 2, r % 2
+        c, k, j = bi // 4, (bi // 2) % 2, bi % 2
+        off = ((16 * g + c) * 8 + 2 * p + k) * 4 + 2 * a + j
+        _TILE_OFF[key] = off.reshape(-1).to(device)
+    return _TILE_OFF[key]
+
+
+def tile_v(rows: torch.Tensor) -> torch.Tensor:
+    """Packed codes [B, H, T, 64] -> TILE32 layout [B, H, ceil(T/32), 2048] (zero padded)."""
+    B, H, T, Dc = rows.shape
+    if Dc != HEAD_DIM // 2:
+        raise ValueError(f"packed rows must be [B, H, T, 64], got {tuple(rows.shape)}")
+    nt = (T + TILE_TOKENS - 1) // TILE_TOKENS
+    src = torch.zeros(B, H, nt * TILE_TOKENS, Dc, dtype=torch.uint8, device=rows.device)
+    src[:, :, :T] = rows.view(torch.uint8)
+    off = _tile32_offsets(rows.device)
+    out = torch.empty(B, H, nt, TILE_BYTES, dtype=torch.uint8, device=rows.device)
+    out[..., off] = src.view(B, H, nt, TILE_BYTES)
+    return out
+
+
+def untile_v(tiles: torch.Tensor, tokens: int) -> torch.Tensor:
+    """TILE32 layout [B, H, nt, 2048] -> packed codes [B, H, tokens, 64]."""
+    B, H, nt, nb = tiles.shape
+    if nb != TILE_BYTES or tokens > nt * TILE_TOKENS:
+        raise ValueError(f"tiles must be [B, H, nt, {TILE_BYTES}] covering {tokens} tokens")
+    rows = tiles.view(torch.uint8)[..., _tile32_offsets(tiles.device)]
+    return rows.view(B, H, nt * TILE_TOKENS, HEAD_DIM // 2)[:, :, :tokens]
+
+
+def is_tiled(codes: torch.Tensor) -> bool:
+    return codes.ndim == 4 and codes.shape[-1] == TILE_BYTES
+
+
 def kv_view_static(
     codes: torch.Tensor,
     scale: torch.Tensor,
@@ -66,10 +118,16 @@ def kv_view_static(
     outlier_idx: Optional[torch.Tensor] = None,
     outlier_val: Optional[torch.Tensor] = None,
 ) -> C.KvView:
-    """View of packed asymmetric INT4 codes [B,H,T,D/2] with static scale/zp [H,G]."""
+    """View of packed asymmetric INT4 codes with static scale/zp [H,G]: rows [B,H,T,D/2],
+    or V tiles [B,H,T/32,2048] (TILE32 layout)."""
     v = C.KvView()
     v.codes = codes.data_ptr()
-    v.stride_b, v.stride_h, v.stride_t = (codes.stride(0), codes.stride(1), codes.stride(2))
+    if is_tiled(codes):
+        v.layout = C.KVQ_LAYOUT_TILE32
+        v.stride_b, v.stride_h, v.stride_t = codes.stride(0), codes.stride(1), HEAD_DIM // 2
+    else:
+        v.layout = C.KVQ_LAYOUT_ROWS
+        v.stride_b, v.stride_h, v.stride_t = (codes.stride(0), codes.stride(1), codes.stride(2))
     v.scale = scale.data_ptr()
     v.scale_stride_b, v.scale_stride_t = 0, 0
     v.scale_stride_h, v.scale_stride_g = scale.stride()
@@ -369,7 +427,8 @@ def decode_attn_int4_asym(
 ) -> torch.Tensor:
     """Attention over the asymmetric INT4 group-32 format (build-native).
 
-    k_codes/v_codes: packed uint8/int8 [B, Hkv, S, 64]; k_scale/k_zp/v_scale/v_zp: fp16
+    k_codes: packed uint8/int8 [B, Hkv, S, 64]; v_codes: the same, or V in the TILE32
+    layout [B, Hkv, ceil(S/32), 2048] (:func:`tile_v`); k_scale/k_zp/v_scale/v_zp: fp16
     [Hkv, 4] static parameters; optional k_outlier_idx int32 [Hkv, 4] and
     k_outlier_val fp16 [B, Hkv, S, 4] (K channels stored verbatim).  inv_tau: fp16
     [Hq] per-head query scale, applied as fp16(q * inv_tau) like the reference
@@ -429,6 +488,12 @@ def _check_static_args(q, k_codes, v_codes, params, context_lens):
     if not q.is_cuda:
         raise ValueError("requires GPU (ROCm) tensors")
     for c in (k_codes, v_codes):
+        if c is v_codes and is_tiled(c):
+            if c.dtype != torch.uint8 or c.shape[:2] != k_codes.shape[:2] or \
+                    c.shape[2] * TILE_TOKENS < k_codes.shape[2] or c.stride(-1) != 1:
+                raise ValueError(f"TILE32 V must be uint8 [B, Hkv, >= S/32, {TILE_BYTES}] "
+                                 f"contiguous in the last dim, got {tuple(c.shape)}")
+            continue
         if c.ndim != 4 or c.shape[-1] != HEAD_DIM // 2 or c.dtype not in (torch.int8, torch.uint8):
             raise ValueError(f"packed codes must be int8/uint8 [B, Hkv, S, 64], got {tuple(c.shape)}")
         if c.stride(-1) != 1:

@@ -70,9 +70,16 @@ def test_gpu_matches_golden(path):
                                   k_outlier_idx=None if oi is None else oi[None], check_numerics=True)
         append_twice(cache, k, v)
         kc, vc, ks, kz, vs, vz, goi, gov = cache.get_int4_g32_tensors(0)
-        assert torch.equal(kc.cpu(), f["k_codes"]) and torch.equal(vc.cpu(), f["v_codes"])
+        S = k.shape[2]
+        assert torch.equal(kc.cpu(), f["k_codes"])
+        assert torch.equal(K.untile_v(vc, S).cpu(), f["v_codes"])  # V is kept in TILE32
         if oi is not None:
             assert torch.equal(gov.cpu(), f["k_outlier_val"])
+        # V as packed rows takes the row-layout kernel
+        out_rows = K.decode_attn_int4_asym(qd, kc, K.untile_v(vc, S).contiguous(), ks, kz, vs, vz,
+                                           cld, sm, inv_tau=taud, k_outlier_idx=goi,
+                                           k_outlier_val=gov)
+        check_out(out_rows, f["out"], name + " rows")
         out = K.decode_attn_int4_asym(qd, kc, vc, ks, kz, vs, vz, cld, sm, inv_tau=taud,
                                       k_outlier_idx=goi, k_outlier_val=gov)
     elif "v_zp" in f:  # config 4: INT8 K, INT4 asym V

@@ -141,7 +141,8 @@ def test_append_asym_bitexact(outliers):
     ref_k = OQ.pack_int4(OQ.quantize_asymmetric_static(k, tables.k_scale, tables.k_zp)).view(torch.uint8)
     ref_v = OQ.pack_int4(OQ.quantize_asymmetric_static(v, tables.v_scale, tables.v_zp)).view(torch.uint8)
     assert torch.equal(kc.cpu(), ref_k)
-    assert torch.equal(vc.cpu(), ref_v)
+    assert vc.shape[-1] == K.kernels.TILE_BYTES  # the engine keeps V in the TILE32 layout
+    assert torch.equal(K.untile_v(vc, 19).cpu(), ref_v)  # slots past 19 are unwritten
     if outliers:
         ref_o = torch.stack([k[:, h, :, oidx[h].long()] for h in range(cfg.kv_heads)], dim=1)
         assert torch.equal(ko.cpu(), ref_o)
@@ -259,23 +260,26 @@ def _asym_case(cfg_idx, B, S, ctx, seed, outliers=True):
     return cfg, t, q, tau, kq, vq, oidx, oval, cl
 
 
+@pytest.mark.parametrize("layout", ["rows", "tile32"])
 @pytest.mark.parametrize("cfg_idx,B,S,ctx,outliers", [
     (3, 2, 4096, [4096, 3001], True),
     (2, 3, 2048, [2048, 1, 777], True),
     (3, 1, 1000, [1000], False),
     (3, 2, 300, [0, 300], True),
+    (3, 2, 45, [45, 33], True),
 ])
-def test_decode_asym_parity(cfg_idx, B, S, ctx, outliers):
+def test_decode_asym_parity(cfg_idx, B, S, ctx, outliers, layout):
     K = _lib()
     cfg, t, q, tau, kq, vq, oidx, oval, cl = _asym_case(cfg_idx, B, S, ctx, 40 + S, outliers)
     sm = 1 / math.sqrt(128)
     ref = OA.decode_attn_asym_ref(q, kq, vq, t.k_scale, t.k_zp, t.v_scale, t.v_zp, cl, sm,
                                   inv_tau=tau, k_outlier_idx=oidx, k_outlier_val=oval)
     d = lambda x: None if x is None else x.to(DEV)
-    out = K.decode_attn_int4_asym(q.to(DEV), kq.to(DEV), vq.to(DEV), d(t.k_scale), d(t.k_zp),
+    vd = K.tile_v(vq.to(DEV)) if layout == "tile32" else vq.to(DEV)
+    out = K.decode_attn_int4_asym(q.to(DEV), kq.to(DEV), vd, d(t.k_scale), d(t.k_zp),
                                   d(t.v_scale), d(t.v_zp), cl.to(DEV), sm, inv_tau=tau.to(DEV),
                                   k_outlier_idx=d(oidx), k_outlier_val=d(oval))
-    assert_close(out, ref, f"asym cfg{cfg_idx} B{B} S{S} out={outliers}")
+    assert_close(out, ref, f"asym {layout} cfg{cfg_idx} B{B} S{S} out={outliers}")
 
 
 def test_decode_k8v4_parity_ragged():
@@ -314,7 +318,8 @@ def test_decode_kat_single_token_and_zero_context():
     assert torch.all(allzero == 0)
 
 
-def test_decode_split_invariance_and_determinism():
+@pytest.mark.parametrize("layout", ["rows", "tile32"])
+def test_decode_split_invariance_and_determinism(layout):
     """Results do not depend on the split size beyond tolerance and repeat bit-exactly."""
     K = _lib()
     from llm_kvcache_quantization_amd import _capi as C
@@ -322,11 +327,12 @@ def test_decode_split_invariance_and_determinism():
 
     cfg, t, q, tau, kq, vq, oidx, oval, cl = _asym_case(3, 2, 8192, [8192, 5000], 5)
     d = lambda x: x.to(DEV)
+    vd = K.tile_v(d(vq)) if layout == "tile32" else d(vq)
     outs = []
     for chunk in (128, 256, 1024, 4096, 8192):
         plan = DecodePlan(d(q), C.KVQ_FMT_INT4_ASYM,
                           kv_view_static(d(kq), d(t.k_scale), d(t.k_zp), d(oidx), d(oval)),
-                          C.KVQ_FMT_INT4_ASYM, kv_view_static(d(vq), d(t.v_scale), d(t.v_zp)),
+                          C.KVQ_FMT_INT4_ASYM, kv_view_static(vd, d(t.v_scale), d(t.v_zp)),
                           d(cl), cfg.kv_heads, 8192, 1 / math.sqrt(128), 32, inv_tau=d(tau),
                           chunk_tokens=chunk)
         a = plan.launch().clone()
@@ -360,8 +366,9 @@ def test_cfg3_full_size_rows():
         sl = slice(b, b + 1)
         kq_ref = OQ.pack_int4(OQ.quantize_asymmetric_static(k[sl].cpu(), t.k_scale, t.k_zp))
         assert torch.equal(kc[sl].cpu(), kq_ref.view(torch.uint8))
-        ref = OA.decode_attn_asym_ref(q[sl].cpu(), kc[sl].cpu(), vc[sl].cpu(), t.k_scale, t.k_zp,
-                                      t.v_scale, t.v_zp, cl[sl].cpu(), 1 / math.sqrt(128),
+        ref = OA.decode_attn_asym_ref(q[sl].cpu(), kc[sl].cpu(), K.untile_v(vc[sl], cfg.context).cpu(),
+                                      t.k_scale, t.k_zp, t.v_scale, t.v_zp, cl[sl].cpu(),
+                                      1 / math.sqrt(128),
                                       inv_tau=tau.cpu(), k_outlier_idx=t.k_outlier_idx,
                                       k_outlier_val=ov[sl].cpu())
         assert_close(out[sl], ref, f"cfg3 full row {b}")
