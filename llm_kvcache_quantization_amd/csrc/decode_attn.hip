@@ -600,7 +600,8 @@ static int64_t resident_slots(const void* fn) {
 
 // the split-K kernel kvq_decode_attn launches for p (nullptr if unsupported)
 static const void* kernel_for(const kvq_decode_params* p) {
-  if (p->v.layout == KVQ_LAYOUT_TILE32) return tiled_kernel(p->k_format, p->k.n_outlier > 0);
+  if (p->v.layout == KVQ_LAYOUT_TILE32)
+    return tiled_kernel(p->k_format, p->k.n_outlier > 0, p->q_heads / p->kv_heads);
   return select_kernel(family(p->k_format, p->v_format, p->k.scale_dtype == KVQ_DTYPE_F32,
                               p->v.scale_dtype == KVQ_DTYPE_F32, p->k.n_outlier > 0));
 }
@@ -743,7 +744,7 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
     return fail(KVQ_ERR_UNSUPPORTED,
                 "unsupported (k_format, v_format) pair or mixed K/V scale dtypes");
   const bool tiled = p->v.layout == KVQ_LAYOUT_TILE32;
-  if (tiled && !tiled_kernel(kf, p->k.n_outlier > 0))
+  if (tiled && !tiled_kernel(kf, p->k.n_outlier > 0, n_rep))
     return fail(KVQ_ERR_UNSUPPORTED, "TILE32 V is supported with INT4_ASYM K only");
   if (tiled && (p->k.stride_t != kD / 2 || (p->k.n_outlier && p->k.outlier_stride_t != 4)))
     return fail(KVQ_ERR_UNSUPPORTED, "with TILE32 V, K rows and outlier rows must be dense");

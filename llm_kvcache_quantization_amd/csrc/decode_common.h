@@ -116,6 +116,49 @@ __device__ __forceinline__ half8v softmax_tile(float4v x0, float4v x1, float sm,
   return pack8(as_u32(pp0), as_u32(pp1), as_u32(pp2), as_u32(pp3));
 }
 
+// DPP row_ror:8 within each row of 16 lanes (lane c reads lane (c + 8) % 16), written only
+// to the lanes of bank_mask (bank = 4 lanes; 0xC = lanes 8..15, 0x3 = lanes 0..7 of each
+// row); the other lanes keep `old`.
+template <int BANKS>
+__device__ __forceinline__ uint32_t dpp_ror8(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, 0x128, 0xF, BANKS, false);
+}
+template <int BANKS>
+__device__ __forceinline__ float dpp_ror8f(float old, float src) {
+  return __builtin_bit_cast(float, dpp_ror8<BANKS>(__builtin_bit_cast(uint32_t, old),
+                                                   __builtin_bit_cast(uint32_t, src)));
+}
+
+// softmax_tile for at most 8 heads (n_rep <= 8): head h's logits of row block 1 are moved
+// from lane h into the padding lane h + 8, so each lane exponentiates 4 values instead of
+// 8.  m is kept equal in lanes h and h + 8; l holds the block-0 part of head h's sum in
+// lane h and the block-1 part in lane h + 8 (merge_and_store adds them).  The returned PV
+// operand is valid in lanes h < 8; lanes 8..15 carry finite values of padding columns.
+__device__ __forceinline__ half8v softmax_tile8(float4v x0, float4v x1, float sm, float& m,
+                                                float& l, float4v acc[8]) {
+  float y[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[r] = dpp_ror8f<0xC>(x0[r], x1[r]);
+  const float lmax = max3f(max3f(y[0], y[1], y[2]), y[3], y[3]) * sm;
+  if (__ballot(lmax > m + kTau)) {
+    const float hm = fmaxf(lmax, dpp_ror8f<0xF>(lmax, lmax));  // both halves of the head
+    const float mn = fmaxf(m, wave_max_xor_groups(hm));
+    const float alpha = fast_exp2(m - mn);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+  }
+  const float nm = -m;
+  const half2v pa = pk_rtz(fast_exp2(fmaf(y[0], sm, nm)), fast_exp2(fmaf(y[1], sm, nm)));
+  const half2v pb = pk_rtz(fast_exp2(fmaf(y[2], sm, nm)), fast_exp2(fmaf(y[3], sm, nm)));
+  const half2v ones = {(half_t)1.0f, (half_t)1.0f};
+  l = __builtin_amdgcn_fdot2(pa, ones, l, false);
+  l = __builtin_amdgcn_fdot2(pb, ones, l, false);
+  const uint32_t a0 = as_u32(pa), a1 = as_u32(pb);
+  return pack8(a0, a1, dpp_ror8<0x3>(a0, a0), dpp_ror8<0x3>(a1, a1));
+}
+
 // masks logits of tokens >= t1 (tile starts at tt) to -inf
 __device__ __forceinline__ void mask_tile(float4v& x0, float4v& x1, int tt, int t1, int lg) {
 #pragma unroll
@@ -134,9 +177,11 @@ struct MergeLds {
   float acc[kWaves][16][kD + 1];
 };
 
+template <bool PACK8 = false>
 __device__ __forceinline__ void merge_and_store(const DecodeArgs& a, MergeLds& sh, int wave,
                                                 int col, int lg, float m, float l,
                                                 const float4v acc[8], int b, int hkv, int chunk) {
+  if constexpr (PACK8) l += dpp_ror8f<0xF>(l, l);  // add the block-1 part from lane h + 8
   l = wave_sum_xor_groups(l);
   if (lg == 0) {
     sh.m[wave][col] = m;
@@ -238,7 +283,7 @@ int fail(int code, const std::string& msg);
 
 // ---- tiled-V kernels (decode_tiled.hip)
 // kernel of the tiled family for K format kf (kout: outlier channels), or nullptr
-const void* tiled_kernel(int kf, int kout);
+const void* tiled_kernel(int kf, int kout, int n_rep);
 void launch_tiled(const DecodeArgs& a, int kf, int kout, dim3 grid, hipStream_t s);
 
 }  // namespace kvq

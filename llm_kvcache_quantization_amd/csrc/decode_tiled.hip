@@ -245,7 +245,7 @@ struct VAsymT {
   }
 };
 
-template <bool OUT, int LOOK>
+template <bool OUT, int LOOK, bool PACK8>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3)))
 void decode_tiled_kernel(DecodeArgs a) {
   const int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
@@ -320,23 +320,24 @@ void decode_tiled_kernel(DecodeArgs a) {
         }
         float4v x0 = x[u & 1][0], x1 = x[u & 1][1];
         if (partial && i == ntiles - 1) mask_tile(x0, x1, tw + i * kStep, t1, lg);
-        const half8v pb = softmax_tile(x0, x1, sm, m, l, acc);
+        half8v pb;
+        if constexpr (PACK8) pb = softmax_tile8(x0, x1, sm, m, l, acc);
+        else pb = softmax_tile(x0, x1, sm, m, l, acc);
         vf.mma(vr[u % R], pb, acc, nc);
       }
     }
   }
-  merge_and_store(a, msh, wave, col, lg, m, l, acc, b, hkv, chunk);
+  merge_and_store<PACK8>(a, msh, wave, col, lg, m, l, acc, b, hkv, chunk);
 }
 
-template <bool OUT>
+template <bool OUT, bool PACK8>
 const void* tiled_ptr(int look) {
-  if (look == 2) return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 2>);
-  return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 1>);
+  if (look == 2) return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 2, PACK8>);
+  return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 1, PACK8>);
 }
 
 // Tiles of lookahead: 1 (measured fastest at the headline shape: both variants keep 3
 // waves per SIMD, and the deeper ring spills), or KVQ_TILED_LOOK=1|2.
-template <bool OUT>
 int tiled_look() {
   static int d = [] {
     const char* e = getenv("KVQ_TILED_LOOK");
@@ -346,26 +347,34 @@ int tiled_look() {
   return d;
 }
 
+template <bool OUT, bool PACK8>
+void launch_one(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  const dim3 block(kWaves * 64);
+  if (tiled_look() == 2)
+    hipLaunchKernelGGL((decode_tiled_kernel<OUT, 2, PACK8>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_tiled_kernel<OUT, 1, PACK8>), grid, block, 0, s, a);
+}
+
 }  // namespace
 
-const void* tiled_kernel(int kf, int kout) {
+// the kernels for n_rep <= 8 pack the second row block's softmax into the padding lanes
+const void* tiled_kernel(int kf, int kout, int n_rep) {
   if (kf != KVQ_FMT_INT4_ASYM) return nullptr;
-  return kout ? tiled_ptr<true>(tiled_look<true>()) : tiled_ptr<false>(tiled_look<false>());
+  const bool p8 = n_rep <= 8;
+  if (kout) return p8 ? tiled_ptr<true, true>(tiled_look()) : tiled_ptr<true, false>(tiled_look());
+  return p8 ? tiled_ptr<false, true>(tiled_look()) : tiled_ptr<false, false>(tiled_look());
 }
 
 void launch_tiled(const DecodeArgs& a, int kf, int kout, dim3 grid, hipStream_t s) {
   (void)kf;
-  const dim3 block(kWaves * 64);
+  const bool p8 = a.n_rep <= 8;
   if (kout) {
-    if (tiled_look<true>() == 2)
-      hipLaunchKernelGGL((decode_tiled_kernel<true, 2>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((decode_tiled_kernel<true, 1>), grid, block, 0, s, a);
+    if (p8) launch_one<true, true>(a, grid, s);
+    else launch_one<true, false>(a, grid, s);
   } else {
-    if (tiled_look<false>() == 2)
-      hipLaunchKernelGGL((decode_tiled_kernel<false, 2>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((decode_tiled_kernel<false, 1>), grid, block, 0, s, a);
+    if (p8) launch_one<false, true>(a, grid, s);
+    else launch_one<false, false>(a, grid, s);
   }
 }
 

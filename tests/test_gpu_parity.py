@@ -372,3 +372,30 @@ def test_cfg3_full_size_rows():
                                       inv_tau=tau.cpu(), k_outlier_idx=t.k_outlier_idx,
                                       k_outlier_val=ov[sl].cpu())
         assert_close(out[sl], ref, f"cfg3 full row {b}")
+
+
+@pytest.mark.parametrize("layout", ["rows", "tile32"])
+@pytest.mark.parametrize("Hq,Hkv,S,ctx", [(32, 2, 333, [333]), (9, 1, 700, [700, 65]), (8, 1, 96, [96])])
+def test_decode_asym_wide_gqa(Hq, Hkv, S, ctx, layout):
+    """GQA groups of 8, 9 and 16 query heads per kv head (the tiled kernel packs the
+    softmax of groups up to 8 into the MFMA's padding columns; wider groups do not)."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import calib
+
+    B = len(ctx)
+    g = gen(Hq * 1000 + S)
+    k = (torch.randn(B, Hkv, S, 128, generator=g) * 1.5).to(torch.float16)
+    v = torch.randn(B, Hkv, S, 128, generator=g).to(torch.float16)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+    tau = (0.8 + 0.4 * torch.rand(Hq, generator=g)).to(torch.float16)
+    ks, kz = calib.asym_g32_params(k)
+    vs, vz = calib.asym_g32_params(v)
+    kq = OQ.pack_int4(OQ.quantize_asymmetric_static(k, ks, kz))
+    vq = OQ.pack_int4(OQ.quantize_asymmetric_static(v, vs, vz))
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    sm = 1 / math.sqrt(128)
+    ref = OA.decode_attn_asym_ref(q, kq, vq, ks, kz, vs, vz, cl, sm, inv_tau=tau)
+    vd = K.tile_v(vq.to(DEV)) if layout == "tile32" else vq.to(DEV)
+    out = K.decode_attn_int4_asym(q.to(DEV), kq.to(DEV), vd, ks.to(DEV), kz.to(DEV), vs.to(DEV),
+                                  vz.to(DEV), cl.to(DEV), sm, inv_tau=tau.to(DEV))
+    assert_close(out, ref, f"asym {layout} Hq{Hq} Hkv{Hkv} S{S}")
