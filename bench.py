@@ -2,7 +2,9 @@
 
 A step is one decode step over every layer of the configuration.  Per layer it runs:
 - quantize-on-append of the new token's K/V (one HIP launch);
-- split-K quantized decode attention plus combine over the whole context.
+- split-K quantized decode attention over the whole context, whose chunk partials are
+  merged in the same launch (TILE32 V, at most 24 chunks and 8 query heads per KV head)
+  or by a second, combine launch.
 
 Caches are seeded synthetic data of the configured shape, one distinct cache per
 layer, built on the GPU with the same HIP append kernel.  Each step rewrites the
@@ -230,6 +232,17 @@ def copy_probe(device, nbytes=1 << 30, reps=3):
                       "launches": reps}), flush=True)
 
 
+def attention_kernels(cfg, layer):
+    """Kernels one kvq_decode_attn call launches for this configuration: the tiled kernel
+    merges its chunk partials itself when it runs at most 24 chunks per (b, kv head) and
+    at most 8 query heads per kv head; otherwise a combine launch follows."""
+    p = layer.plan.params
+    n_chunks = -(-int(p.capacity) // int(layer.plan.chunk_tokens))
+    if layer.v_tiled and n_chunks <= 24 and cfg.q_heads // cfg.kv_heads <= 8:
+        return "decode_tiled_kernel (single launch, merge in the last work-group)"
+    return ("decode_tiled_kernel" if layer.v_tiled else "decode_splitk_kernel") + " + combine_kernel"
+
+
 def measured_traffic(cfg_index):
     """HBM bytes per attention call measured by rocprofv3 counters for this configuration,
     from profiles/traffic.json (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the
@@ -396,8 +409,7 @@ def main():
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": measured_traffic(cfg.index),
             "bytes_per_launch": nbytes,
-            "kernel": ("decode_tiled_kernel" if layers[0].v_tiled else "decode_splitk_kernel")
-                      + " + combine_kernel (one kvq_decode_attn call per layer)",
+            "kernel": attention_kernels(cfg, layers[0]) + " (one kvq_decode_attn call per layer)",
         },
         "stream_ceiling": ceiling,
         "cpu_baseline": cpu,

@@ -104,8 +104,10 @@ typedef struct kvq_decode_params {
   float sm_scale;
   int32_t chunk_tokens;   /* split size in tokens (work-groups per (b, kv head) =
                              ceil(capacity / chunk_tokens)); 0 = choose automatically */
-  void* workspace;        /* device scratch of kvq_decode_workspace_bytes() bytes; calls
-                             sharing a workspace must be ordered on one stream */
+  void* workspace;        /* device scratch of kvq_decode_workspace_bytes() bytes, zero-filled
+                             before its first use (it holds work-group arrival counters that
+                             every call leaves zero); calls sharing a workspace must be
+                             ordered on one stream */
   int64_t workspace_bytes;
   void* out;              /* fp16 [B, Hq, D], d contiguous */
   int64_t out_stride_b, out_stride_h; /* elements */

@@ -709,12 +709,17 @@ extern "C" int32_t kvq_decode_chunk_tokens(const kvq_decode_params* p) {
   return p ? choose_chunk(p) : 0;
 }
 
-// workspace: partial acc [B, Hq, n_chunks, 128] f32, then partial (m, l) [B, Hq, n_chunks]
+// workspace: partial acc [B, Hq, n_chunks, 128] f32, partial (m, l) [B, Hq, n_chunks]
+// float2, then (256-byte aligned) the arrival counters [B, Hkv] u32 of the fused combine
+static int64_t counters_offset(const kvq_decode_params* p, int64_t nch) {
+  const int64_t rows = (int64_t)p->batch * p->q_heads * nch;
+  return ((rows * (kD * 4 + 8) + 255) / 256) * 256;
+}
+
 extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   if (!p) return 0;
   const int64_t nch = n_chunks_for(p, choose_chunk(p));
-  const int64_t rows = (int64_t)p->batch * p->q_heads * nch;
-  return rows * (kD * 4 + 8) + 256;
+  return counters_offset(p, nch) + (int64_t)p->batch * p->kv_heads * 4 + 256;
 }
 
 extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) {
@@ -782,14 +787,23 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   const int64_t rows = (int64_t)p->batch * p->q_heads * nch64;
   a.part_acc = reinterpret_cast<float*>(p->workspace);
   a.part_ml = reinterpret_cast<float2*>(reinterpret_cast<char*>(p->workspace) + rows * kD * 4);
+  a.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(p->workspace) +
+                                           counters_offset(p, nch64));
 
   a.out = reinterpret_cast<half_t*>(p->out);
   a.o_sb = p->out_stride_b; a.o_sh = p->out_stride_h;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (p->capacity > 0 && tiled) {
+  a.fused = tiled && nch64 <= kUnitChunks && n_rep <= 8;
+  if (tiled) {
     launch_tiled(a, kf, p->k.n_outlier > 0,
                  dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch), s);
+    if (a.fused) {  // one launch: the last work-group of each (b, kv head) merged
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess)
+        return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
+      return KVQ_OK;
+    }
   } else if (p->capacity > 0) {
     const dim3 grid((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch);
     switch (fam) {

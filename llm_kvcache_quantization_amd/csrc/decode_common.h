@@ -42,6 +42,8 @@ struct DecodeArgs {
                     // (wave w) instead of the contiguous tokens [c*chunk, (c+1)*chunk)
   float* part_acc;  // [B, Hq, n_chunks, 128]
   float2* part_ml;  // [B, Hq, n_chunks]
+  uint32_t* counters;  // [B, Hkv] work-group arrival counters (fused combine), zero between calls
+  int fused;           // 1: the split-K kernel merges the partials itself (combine_unit)
   half_t* out;
   int64_t o_sb, o_sh;
 };
@@ -177,7 +179,15 @@ struct MergeLds {
   float acc[kWaves][16][kD + 1];
 };
 
-template <bool PACK8 = false>
+// partial stores; WT = write-through at device scope, so a work-group of the same launch
+// on another XCD can read them once the store has completed (no L2 write-back needed)
+template <bool WT>
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  if constexpr (WT) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+
+template <bool PACK8 = false, bool WT = false>
 __device__ __forceinline__ void merge_and_store(const DecodeArgs& a, MergeLds& sh, int wave,
                                                 int col, int lg, float m, float l,
                                                 const float4v acc[8], int b, int hkv, int chunk) {
@@ -206,8 +216,11 @@ __device__ __forceinline__ void merge_and_store(const DecodeArgs& a, MergeLds& s
     }
     const int hq = hkv * a.n_rep + h;
     const int64_t pi = ((int64_t)b * a.Hq + hq) * a.n_chunks + chunk;
-    a.part_acc[pi * kD + d] = num;
-    if (d == 0) a.part_ml[pi] = float2{M, den};
+    store_partial<WT>(a.part_acc + pi * kD + d, num);
+    if (d == 0) {
+      store_partial<WT>(&a.part_ml[pi].x, M);
+      store_partial<WT>(&a.part_ml[pi].y, den);
+    }
   }
 }
 
@@ -226,6 +239,9 @@ __host__ __device__ __forceinline__ int valid_chunks(const DecodeArgs& a, int64_
 // out = s (acc / l - off) + z (off = 72 or 1032 by channel parity) when v_affine.
 // Every partial of a batch of kCombineBatch chunks is requested before any is used.
 constexpr int kCombineBatch = 32;
+// the split-K kernels with a single-launch merge take at most this many chunks per
+// (b, kv head): its last work-group keeps one 16-byte partial per chunk in flight
+constexpr int kUnitChunks = 24;
 
 __device__ __forceinline__ void combine_one(const DecodeArgs& a, int b, int hq, int d, int nvalid,
                                             int v_affine) {

@@ -31,7 +31,10 @@
 //    LOOK + 1 tiles); QK of tile i + 1 is issued before softmax / PV of tile i.  The
 //    first tiles are requested before the q set-up.
 //  * The n_chunks work-groups of a (b, kv head) interleave tile by tile, so the device
-//    streams each slab front to back; combine_kernel merges their partials.
+//    streams each slab front to back.  With at most kUnitChunks of them and n_rep <= 8
+//    the last of them to finish merges their partials (no second launch; the arrival
+//    counters live in the workspace, which must be zero-filled before its first use and
+//    which every call leaves zero); otherwise combine_kernel does.
 #include "decode_common.h"
 
 #include <cstdlib>
@@ -45,6 +48,9 @@ constexpr int kRsrcWord3 = 0x00020000;  // buffer descriptor word 3 for raw load
 constexpr int kRowK = kD / 2;           // bytes per token of packed K (dense rows)
 constexpr int kRowO = 4 * 2;            // bytes per token of the fp16 outlier side-band
 
+// Raw buffer loads return 0 when voffset + the instruction offset is at or past the
+// descriptor's byte size; soffset is added to the address but not range checked.  Every
+// offset that may run past a buffer's end therefore goes into voffset.
 __device__ __forceinline__ rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            kRsrcWord3);
@@ -55,6 +61,70 @@ __device__ __forceinline__ u32x4 bload4(rsrc_t r, uint32_t voff, uint32_t soff) 
 }
 __device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t voff, uint32_t soff) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kBufNT);
+}
+
+// Fused combine: the last work-group of a (b, kv head) to finish merges the partials of
+// its n_rep heads, which the other work-groups of the launch stored write-through, and
+// writes the output rows with combine_one's arithmetic.  Needs n_rep <= 8 and n_chunks <=
+// kUnitChunks.  Thread t takes head t / 32 and channels 4 (t % 32) .. +3: one 16-byte
+// load per chunk, all issued at once, bypassing the non-coherent cache levels (sc1, as
+// device-scope atomic loads).  The (m, l) pairs go through LDS.  Loads of chunks past
+// nvalid (or heads past n_rep) use an offset past the descriptor's end and read 0.
+constexpr int kBufSC1 = 16;  // cache-policy bits: sc1 (device-coherent load)
+
+struct UnitLds {
+  float2 ml[8][32];
+};
+
+__device__ __forceinline__ void combine_unit(const DecodeArgs& a, UnitLds& sh, int b, int hkv,
+                                             int nvalid) {
+  const int t = threadIdx.x;
+  const int h = t >> 5, dg = t & 31;
+  const bool hv = h < a.n_rep;
+  const int64_t row0 = ((int64_t)b * a.Hq + hkv * a.n_rep) * a.n_chunks;
+  const rsrc_t r = buffer_rsrc(a.part_acc + row0 * kD, (uint32_t)(a.n_rep * a.n_chunks * kD * 4));
+  const uint32_t vbase = (uint32_t)((h * a.n_chunks * kD + 4 * dg) * 4);
+  u32x4 av[kUnitChunks];
+#pragma unroll
+  for (int c = 0; c < kUnitChunks; ++c) {
+    const uint32_t voff = (hv && c < nvalid) ? vbase + (uint32_t)(c * kD * 4) : 0x80000000u;
+    av[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, kBufSC1));
+  }
+  {
+    float m = kNegInf, l = 0.f;
+    if (hv && dg < nvalid) {
+      const float* pm =
+          reinterpret_cast<const float*>(a.part_ml + row0 + (int64_t)h * a.n_chunks + dg);
+      m = __hip_atomic_load(pm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      l = __hip_atomic_load(pm + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    sh.ml[h][dg] = float2{m, l};
+  }
+  __syncthreads();
+  if (!hv) return;
+  float M = kNegInf;
+#pragma unroll
+  for (int c = 0; c < kUnitChunks; ++c) M = fmaxf(M, sh.ml[h][c].x);
+  float num[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.f;
+#pragma unroll
+  for (int c = 0; c < kUnitChunks; ++c) {
+    const float2 ml = sh.ml[h][c];
+    const float e = fast_exp2(ml.x - M);
+    // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of an
+    // ext_vector element lvalue reads element 0 whatever the index
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      num[j] = fmaf(e, __builtin_bit_cast(float, (uint32_t)av[c][j]), num[j]);
+    den = fmaf(e, ml.y, den);
+  }
+  const int g = dg >> 3;  // quantisation group of channels 4 dg .. 4 dg + 3
+  const float s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
+  const float z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
+  half4v o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = (half_t)fmaf(s, num[j] / den - ((j & 1) ? 1032.0f : 72.0f), z);
+  *reinterpret_cast<half4v*>(a.out + (int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + h) * a.o_sh +
+                             4 * dg) = o;
 }
 
 // 8 packed codes -> 8 fp16 operands in k-slot order [e0, e4, e1, e5, e2, e6, e3, e7]
@@ -176,11 +246,12 @@ struct KAsymT {
     bias = (sh.bias[0][col] + sh.bias[1][col]) + (sh.bias[2][col] + sh.bias[3][col]);
   }
 
+  // rows of a partial last tile past the capacity read 0 (tok in voffset, range checked)
   __device__ __forceinline__ void load(int tok, Raw& r) const {
-    const uint32_t soff = (uint32_t)tok * kRowK;
-    r.w[0] = bload4(rk, vk, soff);
-    r.w[1] = bload4(rk, vk + 16 * kRowK, soff);
-    if constexpr (OUT) r.o = bload1(ro, vo, (uint32_t)tok * kRowO);
+    const uint32_t v = vk + (uint32_t)tok * kRowK;
+    r.w[0] = bload4(rk, v, 0);
+    r.w[1] = bload4(rk, v + 16 * kRowK, 0);
+    if constexpr (OUT) r.o = bload1(ro, vo + (uint32_t)tok * kRowO, 0);
   }
 
   __device__ __forceinline__ float4v qk(const Raw& r, int s, const NibConsts& nc) const {
@@ -214,6 +285,7 @@ struct VAsymT {
     rv = buffer_rsrc(vb, (uint32_t)(((a.cap + kTile - 1) / kTile) * kTile * (kD / 2)));
     vv = (uint32_t)lane * 32u;
   }
+  // whole tiles only: the descriptor spans ceil(capacity / 32) tiles
   __device__ __forceinline__ void load(int tok, Raw& r) const {
     const uint32_t soff = (uint32_t)tok * (kD / 2);  // tile index * 2048
     r.w[0] = bload4(rv, vv, soff);
@@ -260,6 +332,13 @@ void decode_tiled_kernel(DecodeArgs a) {
   // them read one contiguous run of n_chunks * kWaves tiles, so the device streams each
   // slab front to back.  Wave w of work-group c takes tiles c*kWaves + w + i*stride.
   const int ntot = (ctx + kTile - 1) / kTile;
+  if (ntot == 0) {  // empty context: the first work-group writes zero rows
+    if (chunk == 0 && a.fused)
+      for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kWaves * 64)
+        a.out[(int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + (idx >> 7)) * a.o_sh +
+              (idx & (kD - 1))] = (half_t)0.0f;
+    return;
+  }
   if (chunk * kWaves >= ntot) return;  // no tile for this work-group (uniform)
 
   __shared__ QShareLds qsh;
@@ -327,7 +406,25 @@ void decode_tiled_kernel(DecodeArgs a) {
       }
     }
   }
-  merge_and_store<PACK8>(a, msh, wave, col, lg, m, l, acc, b, hkv, chunk);
+  merge_and_store<PACK8, true>(a, msh, wave, col, lg, m, l, acc, b, hkv, chunk);
+
+  // Fused combine.  The partials were stored write-through; once every store of the
+  // work-group has completed, one thread counts the work-group in.  The last of the
+  // (b, kv head)'s work-groups merges all partials and resets the counter.
+  if (!a.fused) return;  // combine_kernel merges
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ int is_last;
+  __shared__ UnitLds ush;
+  const int nvalid = valid_chunks(a, ctx);
+  uint32_t* counter = a.counters + (int64_t)b * a.Hkv + hkv;
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (uint32_t)(nvalid - 1);
+  __syncthreads();
+  if (!is_last) return;
+  combine_unit(a, ush, b, hkv, nvalid);
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <bool OUT, bool PACK8>

@@ -190,7 +190,9 @@ class DecodePlan:
         p.chunk_tokens = int(env_chunk) if (env_chunk and not chunk_tokens) else int(chunk_tokens)
         L = C.lib()
         nbytes = int(L.kvq_decode_workspace_bytes(ctypes.byref(p)))
-        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        # zero-filled once: the workspace holds the fused combine's arrival counters, which
+        # every call leaves zero
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=q.device)
         p.workspace = self.workspace.data_ptr()
         p.workspace_bytes = nbytes
         p.out = self.out.data_ptr()

@@ -399,3 +399,28 @@ def test_decode_asym_wide_gqa(Hq, Hkv, S, ctx, layout):
     out = K.decode_attn_int4_asym(q.to(DEV), kq.to(DEV), vd, ks.to(DEV), kz.to(DEV), vs.to(DEV),
                                   vz.to(DEV), cl.to(DEV), sm, inv_tau=tau.to(DEV))
     assert_close(out, ref, f"asym {layout} Hq{Hq} Hkv{Hkv} S{S}")
+
+
+def test_tiled_plan_reuse_changing_context():
+    """One plan (one workspace) launched repeatedly while context_lens changes in place:
+    the number of work-groups that report per (b, kv head) changes between calls, and the
+    arrival counters of the single-launch merge must start from zero every time."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import _capi as C
+    from llm_kvcache_quantization_amd.kernels import DecodePlan, kv_view_static
+
+    S = 8192
+    cfg, t, q, tau, kq, vq, oidx, oval, cl = _asym_case(3, 2, S, [S, S], 9)
+    d = lambda x: x.to(DEV)
+    cl_dev = d(cl)
+    plan = DecodePlan(d(q), C.KVQ_FMT_INT4_ASYM,
+                      kv_view_static(d(kq), d(t.k_scale), d(t.k_zp), d(oidx), d(oval)),
+                      C.KVQ_FMT_INT4_ASYM, kv_view_static(K.tile_v(d(vq)), d(t.v_scale), d(t.v_zp)),
+                      cl_dev, cfg.kv_heads, S, 1 / math.sqrt(128), 32, inv_tau=d(tau))
+    for ctx in ([S, 5000], [100, 7000], [0, 33], [S, S], [4097, 1]):
+        cl_dev.copy_(torch.tensor(ctx, dtype=torch.int32))
+        out = plan.launch().clone()
+        ref = OA.decode_attn_asym_ref(q, kq, vq, t.k_scale, t.k_zp, t.v_scale, t.v_zp,
+                                      torch.tensor(ctx, dtype=torch.int32), 1 / math.sqrt(128),
+                                      inv_tau=tau, k_outlier_idx=oidx, k_outlier_val=oval)
+        assert_close(out, ref, f"plan reuse ctx={ctx}")
