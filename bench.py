@@ -3,7 +3,7 @@
 A step is one decode step over every layer of the configuration.  Per layer it runs:
 - quantize-on-append of the new token's K/V (one HIP launch);
 - split-K quantized decode attention over the whole context, whose chunk partials are
-  merged in the same launch (TILE32 V, at most 24 chunks and 8 query heads per KV head)
+  merged in the same launch (TILE32 V, at most 64 chunks and 8 query heads per KV head)
   or by a second, combine launch.
 
 Caches are seeded synthetic data of the configured shape, one distinct cache per
@@ -234,11 +234,11 @@ def copy_probe(device, nbytes=1 << 30, reps=3):
 
 def attention_kernels(cfg, layer):
     """Kernels one kvq_decode_attn call launches for this configuration: the tiled kernel
-    merges its chunk partials itself when it runs at most 24 chunks per (b, kv head) and
+    merges its chunk partials itself when it runs at most 64 chunks per (b, kv head) and
     at most 8 query heads per kv head; otherwise a combine launch follows."""
     p = layer.plan.params
     n_chunks = -(-int(p.capacity) // int(layer.plan.chunk_tokens))
-    if layer.v_tiled and n_chunks <= 24 and cfg.q_heads // cfg.kv_heads <= 8:
+    if layer.v_tiled and n_chunks <= 64 and cfg.q_heads // cfg.kv_heads <= 8:
         return "decode_tiled_kernel (single launch, merge in the last work-group)"
     return ("decode_tiled_kernel" if layer.v_tiled else "decode_splitk_kernel") + " + combine_kernel"
 

@@ -710,7 +710,8 @@ extern "C" int32_t kvq_decode_chunk_tokens(const kvq_decode_params* p) {
 }
 
 // workspace: partial acc [B, Hq, n_chunks, 128] f32, partial (m, l) [B, Hq, n_chunks]
-// float2, then (256-byte aligned) the arrival counters [B, Hkv] u32 of the fused combine
+// float2, then (256-byte aligned) the counter slots [B, Hkv] x 128 bytes of the tiled
+// kernel's single-launch merge
 static int64_t counters_offset(const kvq_decode_params* p, int64_t nch) {
   const int64_t rows = (int64_t)p->batch * p->q_heads * nch;
   return ((rows * (kD * 4 + 8) + 255) / 256) * 256;
@@ -719,7 +720,7 @@ static int64_t counters_offset(const kvq_decode_params* p, int64_t nch) {
 extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   if (!p) return 0;
   const int64_t nch = n_chunks_for(p, choose_chunk(p));
-  return counters_offset(p, nch) + (int64_t)p->batch * p->kv_heads * 4 + 256;
+  return counters_offset(p, nch) + (int64_t)p->batch * p->kv_heads * kCtrSlotWords * 4 + 256;
 }
 
 extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) {

@@ -12,6 +12,11 @@ constexpr int kTile = 32;   // tokens per wave iteration (two 16-token MFMA row 
 constexpr int kD = 128;
 constexpr float kTau = 8.0f;  // lazy-rescale headroom in log2 units
 constexpr int kMaxChunks = 2048;
+// The workspace's counter area holds one slot of kCtrSlotWords u32 per (b, kv head), one
+// 128-byte line each (no two counters share a line).  Word 0 counts the work-groups that
+// have stored their partial (the tiled kernel's single-launch merge); it is zero between
+// calls.
+constexpr int kCtrSlotWords = 32;
 constexpr int kMinChunk = 256;
 
 struct KvDev {
@@ -42,7 +47,7 @@ struct DecodeArgs {
                     // (wave w) instead of the contiguous tokens [c*chunk, (c+1)*chunk)
   float* part_acc;  // [B, Hq, n_chunks, 128]
   float2* part_ml;  // [B, Hq, n_chunks]
-  uint32_t* counters;  // [B, Hkv] work-group arrival counters (fused combine), zero between calls
+  uint32_t* counters;  // [B, Hkv] slots of kCtrSlotWords u32, zero between calls (below)
   int fused;           // 1: the split-K kernel merges the partials itself (combine_unit)
   half_t* out;
   int64_t o_sb, o_sh;
@@ -239,9 +244,9 @@ __host__ __device__ __forceinline__ int valid_chunks(const DecodeArgs& a, int64_
 // out = s (acc / l - off) + z (off = 72 or 1032 by channel parity) when v_affine.
 // Every partial of a batch of kCombineBatch chunks is requested before any is used.
 constexpr int kCombineBatch = 32;
-// the split-K kernels with a single-launch merge take at most this many chunks per
-// (b, kv head): its last work-group keeps one 16-byte partial per chunk in flight
-constexpr int kUnitChunks = 24;
+// the tiled kernel merges its chunk partials in the same launch (its last work-group per
+// (b, kv head) reads them) when there are at most this many chunks per (b, kv head)
+constexpr int kUnitChunks = 64;
 
 __device__ __forceinline__ void combine_one(const DecodeArgs& a, int b, int hq, int d, int nvalid,
                                             int v_affine) {

@@ -47,6 +47,8 @@ constexpr int kBufNT = 2;               // cache-policy bits of the buffer loads
 constexpr int kRsrcWord3 = 0x00020000;  // buffer descriptor word 3 for raw loads on gfx9 parts
 constexpr int kRowK = kD / 2;           // bytes per token of packed K (dense rows)
 constexpr int kRowO = 4 * 2;            // bytes per token of the fp16 outlier side-band
+// a voffset past every slab (slabs are below 2^31 bytes): such a buffer load returns 0
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
 // Raw buffer loads return 0 when voffset + the instruction offset is at or past the
 // descriptor's byte size; soffset is added to the address but not range checked.  Every
@@ -67,55 +69,65 @@ __device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t voff, uint32_t sof
 // its n_rep heads, which the other work-groups of the launch stored write-through, and
 // writes the output rows with combine_one's arithmetic.  Needs n_rep <= 8 and n_chunks <=
 // kUnitChunks.  Thread t takes head t / 32 and channels 4 (t % 32) .. +3: one 16-byte
-// load per chunk, all issued at once, bypassing the non-coherent cache levels (sc1, as
-// device-scope atomic loads).  The (m, l) pairs go through LDS.  Loads of chunks past
-// nvalid (or heads past n_rep) use an offset past the descriptor's end and read 0.
+// load per chunk, kUnitBatch of them in flight at once, bypassing the non-coherent cache
+// levels (sc1, as device-scope atomic loads).  The (m, l) pairs go through LDS.  Loads of
+// chunks past nvalid (or heads past n_rep) use an offset past the descriptor's end and
+// read 0.
 constexpr int kBufSC1 = 16;  // cache-policy bits: sc1 (device-coherent load)
+constexpr int kUnitBatch = 32;
 
 struct UnitLds {
-  float2 ml[8][32];
+  float2 ml[8][kUnitChunks];
 };
 
 __device__ __forceinline__ void combine_unit(const DecodeArgs& a, UnitLds& sh, int b, int hkv,
                                              int nvalid) {
+  static_assert(kUnitChunks % 32 == 0 && kUnitChunks % kUnitBatch == 0, "chunk tiling");
   const int t = threadIdx.x;
   const int h = t >> 5, dg = t & 31;
   const bool hv = h < a.n_rep;
   const int64_t row0 = ((int64_t)b * a.Hq + hkv * a.n_rep) * a.n_chunks;
   const rsrc_t r = buffer_rsrc(a.part_acc + row0 * kD, (uint32_t)(a.n_rep * a.n_chunks * kD * 4));
+  const rsrc_t rml = buffer_rsrc(a.part_ml + row0, (uint32_t)(a.n_rep * a.n_chunks * 8));
   const uint32_t vbase = (uint32_t)((h * a.n_chunks * kD + 4 * dg) * 4);
-  u32x4 av[kUnitChunks];
+  u32x4 av[kUnitBatch];
+  auto issue = [&](int c0) {
 #pragma unroll
-  for (int c = 0; c < kUnitChunks; ++c) {
-    const uint32_t voff = (hv && c < nvalid) ? vbase + (uint32_t)(c * kD * 4) : 0x80000000u;
-    av[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, kBufSC1));
-  }
-  {
-    float m = kNegInf, l = 0.f;
-    if (hv && dg < nvalid) {
-      const float* pm =
-          reinterpret_cast<const float*>(a.part_ml + row0 + (int64_t)h * a.n_chunks + dg);
-      m = __hip_atomic_load(pm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      l = __hip_atomic_load(pm + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int c = 0; c < kUnitBatch; ++c) {
+      const uint32_t voff =
+          (hv && c0 + c < nvalid) ? vbase + (uint32_t)((c0 + c) * kD * 4) : kOutOfRange;
+      av[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, kBufSC1));
     }
-    sh.ml[h][dg] = float2{m, l};
+  };
+  // (m, l) of chunks dg + 32 k of head h
+#pragma unroll
+  for (int k = 0; k < kUnitChunks / 32; ++k) {
+    const int c = dg + 32 * k;
+    const bool ok = hv && c < nvalid;
+    const uint32_t off = ok ? (uint32_t)((h * a.n_chunks + c) * 8) : kOutOfRange;
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, (int)off, 0, kBufSC1));
+    sh.ml[h][c] = ok ? float2{__builtin_bit_cast(float, (uint32_t)v.x), __builtin_bit_cast(float, (uint32_t)v.y)}
+                     : float2{kNegInf, 0.f};
   }
+  issue(0);
   __syncthreads();
   if (!hv) return;
   float M = kNegInf;
-#pragma unroll
-  for (int c = 0; c < kUnitChunks; ++c) M = fmaxf(M, sh.ml[h][c].x);
+  for (int c = 0; c < nvalid; ++c) M = fmaxf(M, sh.ml[h][c].x);
   float num[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.f;
+  for (int c0 = 0; c0 < nvalid; c0 += kUnitBatch) {
+    if (c0 > 0) issue(c0);
 #pragma unroll
-  for (int c = 0; c < kUnitChunks; ++c) {
-    const float2 ml = sh.ml[h][c];
-    const float e = fast_exp2(ml.x - M);
-    // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of an
-    // ext_vector element lvalue reads element 0 whatever the index
+    for (int c = 0; c < kUnitBatch; ++c) {
+      const float2 ml = sh.ml[h][c0 + c];  // -inf, 0 past nvalid: weight 0
+      const float e = fast_exp2(ml.x - M);
+      // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of
+      // an ext_vector element lvalue reads element 0 whatever the index
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      num[j] = fmaf(e, __builtin_bit_cast(float, (uint32_t)av[c][j]), num[j]);
-    den = fmaf(e, ml.y, den);
+      for (int j = 0; j < 4; ++j)
+        num[j] = fmaf(e, __builtin_bit_cast(float, (uint32_t)av[c][j]), num[j]);
+      den = fmaf(e, ml.y, den);
+    }
   }
   const int g = dg >> 3;  // quantisation group of channels 4 dg .. 4 dg + 3
   const float s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
@@ -140,11 +152,23 @@ __host__ __device__ constexpr float slot_offset(int k) {  // operand offset + co
   return ((k >> 1) & 1) ? 1032.0f : 72.0f;
 }
 
-// LDS through which the 4 waves share the q-dependent K operands
+// LDS through which the 4 waves share the q-dependent K operands, and the scaled q rows
+// from which the outlier operand is gathered
 struct QShareLds {
   u32x4 qh[4][64];
   u32x4 ql[4][64];
   float bias[4][16];
+  half_t qv[16][kD];  // q' of head column c (zero for padding columns)
+};
+
+// The q-side inputs of one lane: q[32 lg + 8 wave .. + 7] of head column lane % 16, its
+// inverse temperature and the K scale / zero-point of group lg.  They are fetched before
+// the first cache loads, so waiting for them does not wait for those (vmcnt counts loads
+// in issue order).
+struct QIn {
+  u32x4 q;
+  half_t tau, s, z;
+  int4 oc;
 };
 
 // INT4 asymmetric K with static scale s / zero-point z per (kv head, group of 32).  With
@@ -156,7 +180,7 @@ struct QShareLds {
 // outlier values and q' of those channels in the first two k-slots of each lane group.
 template <bool OUT>
 struct KAsymT {
-  half8v qh[4], ql[4];
+  half8v qh[4];
   half8v qo;
   float bias;
   rsrc_t rk, ro;
@@ -181,39 +205,45 @@ struct KAsymT {
     }
   }
 
-  // q-dependent operands of this wave's channel slice, shared through LDS
-  __device__ void setup_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QShareLds& sh) {
+  // issues the loads of the q-side inputs (padding columns read head 0's row)
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
     const int col = lane & 15, lg = lane >> 4;
-    const bool valid = col < a.n_rep;
-    const int hq = hkv * a.n_rep + (valid ? col : 0);
-    const bool has_tau = a.inv_tau != nullptr;
-    const half_t tau = has_tau ? a.inv_tau[hq] : (half_t)1.0f;
-    const half_t* qr = q_row(a, b, hq);
-    int oc[4] = {-1, -1, -1, -1};
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * wave);
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.s = reinterpret_cast<const half_t*>(a.k.scale)[hkv * a.k.ssh + lg * a.k.ssg];
+    in.z = a.k.zp[hkv * a.k.ssh + lg * a.k.ssg];
+    in.oc = int4{-1, -1, -1, -1};
     if constexpr (OUT) {
       const int4 o = *reinterpret_cast<const int4*>(a.k.oidx + hkv * 4);
-      oc[0] = min(max(o.x, 0), kD - 1);
-      oc[1] = min(max(o.y, 0), kD - 1);
-      oc[2] = min(max(o.z, 0), kD - 1);
-      oc[3] = min(max(o.w, 0), kD - 1);
+      in.oc = int4{min(max(o.x, 0), kD - 1), min(max(o.y, 0), kD - 1), min(max(o.z, 0), kD - 1),
+                   min(max(o.w, 0), kD - 1)};
     }
+  }
+
+  // q-dependent operands of this wave's channel slice, shared through LDS
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int wave, QShareLds& sh) {
+    const int col = lane & 15, lg = lane >> 4;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
     // this wave builds the operands of channels 32 lg + 8 j + e, j = wave
     const int j = wave;
-    const u32x4 qraw = *reinterpret_cast<const u32x4*>(qr + 32 * lg + 8 * j);
-    const uint32_t qw[4] = {qraw.x, qraw.y, qraw.z, qraw.w};
-    const half_t* sc = reinterpret_cast<const half_t*>(a.k.scale);
-    const float s = (float)sc[hkv * a.k.ssh + lg * a.k.ssg];
-    const float z = (float)a.k.zp[hkv * a.k.ssh + lg * a.k.ssg];
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    const float s = (float)in.s;
+    const float z = (float)in.z;
     float part = 0.f;
-    half_t vh[8], vl[8];
+    half_t vh[8], vl[8], qs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      qs[e] = valid ? qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int e = slot_elem(k);
       const int d = 32 * lg + 8 * j + e;
-      const half2v h2 = as_h2(qw[e >> 1]);
-      const half_t qe = qscale((e & 1) ? h2.y : h2.x, tau, has_tau);
-      const bool use = valid && d != oc[0] && d != oc[1] && d != oc[2] && d != oc[3];
-      const float qd = use ? (float)qe : 0.f;
+      const bool use = d != in.oc.x && d != in.oc.y && d != in.oc.z && d != in.oc.w;
+      const float qd = use ? (float)qs[e] : 0.f;
       const float P = qd * s;  // exact: 11-bit x 11-bit significands
       const half_t hi = (half_t)P;
       const half_t lo = (half_t)(P - (float)hi);
@@ -223,50 +253,61 @@ struct KAsymT {
     }
     sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
     sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
+    *reinterpret_cast<u32x4*>(&sh.qv[col][32 * lg + 8 * j]) =
+        __builtin_bit_cast(u32x4, half8v{qs[0], qs[1], qs[2], qs[3], qs[4], qs[5], qs[6], qs[7]});
     part = wave_sum_xor_groups(part);
     if (lg == 0) sh.bias[j][col] = part;
-    const half_t h0 = (half_t)0.0f;
-    qo = half8v{h0, h0, h0, h0, h0, h0, h0, h0};
-    if constexpr (OUT) {
-      const int i0 = 2 * (lg & 1);
-      const half_t o0 = valid ? qscale(qr[oc[i0]], tau, has_tau) : h0;
-      const half_t o1 = valid ? qscale(qr[oc[i0 + 1]], tau, has_tau) : h0;
-      qo = half8v{o0, o1, h0, h0, h0, h0, h0, h0};
-    }
   }
 
   // after the work-group barrier: pick up the operands all four waves built
-  __device__ void finish_setup(const QShareLds& sh, int lane) {
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
-      ql[j] = __builtin_bit_cast(half8v, sh.ql[j][lane]);
-    }
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
     const int col = lane & 15;
     bias = (sh.bias[0][col] + sh.bias[1][col]) + (sh.bias[2][col] + sh.bias[3][col]);
+    const half_t h0 = (half_t)0.0f;
+    qo = half8v{h0, h0, h0, h0, h0, h0, h0, h0};
+    if constexpr (OUT) {
+      // lane group lg supplies outlier channels 2 (lg & 1) and 2 (lg & 1) + 1
+      const bool odd = ((lane >> 4) & 1) != 0;
+      qo = half8v{sh.qv[col][odd ? in.oc.z : in.oc.x], sh.qv[col][odd ? in.oc.w : in.oc.y],
+                  h0, h0, h0, h0, h0, h0};
+    }
   }
 
-  // rows of a partial last tile past the capacity read 0 (tok in voffset, range checked)
-  __device__ __forceinline__ void load(int tok, Raw& r) const {
-    const uint32_t v = vk + (uint32_t)tok * kRowK;
+  // rows of a partial last tile past the capacity read 0 (tok in voffset, range checked);
+  // with !valid (wave-uniform) every load is out of range: it reads 0 and touches no memory
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kRowK : kOutOfRange);
     r.w[0] = bload4(rk, v, 0);
     r.w[1] = bload4(rk, v + 16 * kRowK, 0);
-    if constexpr (OUT) r.o = bload1(ro, vo + (uint32_t)tok * kRowO, 0);
+    if constexpr (OUT) r.o = bload1(ro, vo + (valid ? (uint32_t)tok * kRowO : kOutOfRange), 0);
   }
 
-  __device__ __forceinline__ float4v qk(const Raw& r, int s, const NibConsts& nc) const {
-    float4v c = {bias, bias, bias, bias};
+  // logits of the tile's two 16-token row blocks (x0: tokens 4 lg + r, x1: 16 + 4 lg + r).
+  // The lo halves of q * s are read from LDS at every tile (16 VGPRs fewer); qlo is the
+  // lane's byte offset into them, made opaque by the caller so the reads stay in the loop.
+  __device__ __forceinline__ void qk(const Raw& r, const QShareLds& sh, uint32_t qlo,
+                                     const NibConsts& nc, float4v& x0, float4v& x1) const {
+    float4v c0 = {bias, bias, bias, bias};
+    float4v c1 = c0;
     if constexpr (OUT) {
-      const uint32_t w = (olo == (s == 0)) ? r.o : 0u;
-      c = mfma16x16x32(pack8(w, 0u, 0u, 0u), qo, c);
+      c0 = mfma16x16x32(pack8(olo ? r.o : 0u, 0u, 0u, 0u), qo, c0);
+      c1 = mfma16x16x32(pack8(olo ? 0u : r.o, 0u, 0u, 0u), qo, c1);
     }
+    const char* qlb = reinterpret_cast<const char*>(&sh.ql[0][0]) + qlo;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const half8v A = unpack5(r.w[s][j], nc);
-      c = mfma16x16x32(A, qh[j], c);
-      c = mfma16x16x32(A, ql[j], c);
+      const half8v lo = __builtin_bit_cast(half8v, *reinterpret_cast<const u32x4*>(qlb + j * 64 * 16));
+      const half8v A0 = unpack5(r.w[0][j], nc);
+      const half8v A1 = unpack5(r.w[1][j], nc);
+      c0 = mfma16x16x32(A0, qh[j], c0);
+      c1 = mfma16x16x32(A1, qh[j], c1);
+      c0 = mfma16x16x32(A0, lo, c0);
+      c1 = mfma16x16x32(A1, lo, c1);
     }
-    return c;
+    x0 = c0;
+    x1 = c1;
   }
 };
 
@@ -285,11 +326,13 @@ struct VAsymT {
     rv = buffer_rsrc(vb, (uint32_t)(((a.cap + kTile - 1) / kTile) * kTile * (kD / 2)));
     vv = (uint32_t)lane * 32u;
   }
-  // whole tiles only: the descriptor spans ceil(capacity / 32) tiles
-  __device__ __forceinline__ void load(int tok, Raw& r) const {
-    const uint32_t soff = (uint32_t)tok * (kD / 2);  // tile index * 2048
-    r.w[0] = bload4(rv, vv, soff);
-    r.w[1] = bload4(rv, vv + 16u, soff);
+  // whole tiles only: the descriptor spans ceil(capacity / 32) tiles; with !valid
+  // (wave-uniform) voffset is out of range, so the loads read 0 and touch no memory
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t soff = valid ? (uint32_t)tok * (kD / 2) : 0u;  // tile index * 2048
+    const uint32_t v = vv + (valid ? 0u : kOutOfRange);
+    r.w[0] = bload4(rv, v, soff);
+    r.w[1] = bload4(rv, v + 16u, soff);
   }
   __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8],
                                       const NibConsts& nc) const {
@@ -317,8 +360,8 @@ struct VAsymT {
   }
 };
 
-template <bool OUT, int LOOK, bool PACK8>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3)))
+template <bool OUT, int LOOK, bool PACK8, int WPE = 3>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
   const int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63;
@@ -344,65 +387,83 @@ void decode_tiled_kernel(DecodeArgs a) {
   __shared__ QShareLds qsh;
   __shared__ MergeLds msh;
   KAsymT<OUT> kf;
+  // the q-side inputs are requested first: the wait for them then does not include the
+  // cache tiles requested next
+  QIn qin;
+  kf.fetch_q(a, b, hkv, lane, wave, qin);
   kf.setup_addr(a, b, hkv, lane);
   VAsymT vf;
   vf.setup(a, b, hkv, lane);
 
-  // This wave's tiles start at tokens tw + i * kStep, i < ntiles; only the context's
-  // last tile may be partial.
+  // Tile schedule: the n_chunks work-groups of a (b, kv head) interleave, so at step i the
+  // waves of all of them read one contiguous run of n_chunks * kWaves tiles and the device
+  // streams each slab front to back.  Wave w of work-group c takes tiles c * kWaves + w +
+  // i * stride (tile = 32 tokens; only the context's last tile, ntot - 1, may be partial).
+  // The schedule is static, so results do not depend on timing.
   const int first = chunk * kWaves + wave;
   const int stride = a.n_chunks * kWaves;
-  const int ntiles = first < ntot ? (ntot - first + stride - 1) / stride : 0;
-  const int tw = kTile * first;
-  const int kStep = kTile * stride;
-  const int t1 = ctx;
-  const bool partial = ntiles > 0 && tw + (ntiles - 1) * kStep + kTile > t1;
+  const bool partial = (ctx & (kTile - 1)) != 0;
+  // tile[j] = tile of step i + j (j <= LOOK + 1)
+  int tile[LOOK + 2];
+#pragma unroll
+  for (int j = 0; j <= LOOK; ++j) tile[j] = first + j * stride;
   constexpr int R = LOOK + 1;                 // ring slots per stream
   constexpr int U = (R % 2 == 0) ? R : 2 * R;  // unroll: ring slot and x buffer are static
   typename KAsymT<OUT>::Raw kr[R];
   VAsymT::Raw vr[R];
-  // K tiles 0..LOOK and V tiles 0..LOOK-1 are requested before the q set-up, so the
-  // memory system is busy from the start of the kernel
+  // K tiles of steps 0..LOOK and V tiles of steps 0..LOOK-1 are requested before the q
+  // set-up, so the memory system is busy from the start of the kernel.  Every ring load is
+  // issued unconditionally (out of range for a tile past the context): conditional loads
+  // would make the compiler's vmcnt waits conservative at the joins, i.e. wait for the
+  // tiles just requested.
+#ifdef KVQ_EXP_QWAIT
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#else
+  asm volatile("" ::: "memory");
+#endif
 #pragma unroll
   for (int s = 0; s <= LOOK; ++s) {
-    if (s < ntiles) kf.load(tw + s * kStep, kr[s]);
-    if (s < LOOK && s < ntiles) vf.load(tw + s * kStep, vr[s]);
+    kf.load(kTile * tile[s], tile[s] < ntot, kr[s]);
+    if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ntot, vr[s]);
   }
-  kf.setup_q(a, b, hkv, lane, wave, qsh);
+  kf.setup_q(a, qin, lane, wave, qsh);
   NibConsts nc;
   nc.init();
   __syncthreads();
-  kf.finish_setup(qsh, lane);
+  kf.finish_setup(qsh, qin, lane);
 
   float4v acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
   float m = kNegInf, l = 0.f;
   const float sm = a.sm_log2e;
-  if (ntiles > 0) {
+  if (tile[0] < ntot) {
     float4v x[2][2];
-    x[0][0] = kf.qk(kr[0], 0, nc);
-    x[0][1] = kf.qk(kr[0], 1, nc);
-    for (int i0 = 0; i0 < ntiles; i0 += U) {
+    kf.qk(kr[0], qsh, (uint32_t)lane * 16u, nc, x[0][0], x[0][1]);
+    while (tile[0] < ntot) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int i = i0 + u;
-        if (i >= ntiles) break;
-        // step i: fetch K of tile i + LOOK + 1 (into the slot K of tile i used) and V of
-        // tile i + LOOK (into the slot V of tile i - 1 used), QK of tile i + 1, then
-        // softmax and PV of tile i
-        if (i + LOOK + 1 < ntiles) kf.load(tw + (i + LOOK + 1) * kStep, kr[u % R]);
-        if (i + LOOK < ntiles) vf.load(tw + (i + LOOK) * kStep, vr[(u + LOOK) % R]);
-        if (i + 1 < ntiles) {
-          x[(u + 1) & 1][0] = kf.qk(kr[(u + 1) % R], 0, nc);
-          x[(u + 1) & 1][1] = kf.qk(kr[(u + 1) % R], 1, nc);
+        // step i (i % U == u): the tiles of this wave form a prefix of its schedule
+        if (tile[0] >= ntot) break;
+        tile[LOOK + 1] = tile[LOOK] + stride;
+        // fetch K of step i + LOOK + 1 (into the slot K of step i used) and V of step
+        // i + LOOK (into the slot V of step i - 1 used), QK of step i + 1, then softmax
+        // and PV of step i
+        kf.load(kTile * tile[LOOK + 1], tile[LOOK + 1] < ntot, kr[u % R]);
+        vf.load(kTile * tile[LOOK], tile[LOOK] < ntot, vr[(u + LOOK) % R]);
+        if (tile[1] < ntot) {
+          uint32_t qlo = (uint32_t)lane * 16u;
+          asm volatile("" : "+v"(qlo));
+          kf.qk(kr[(u + 1) % R], qsh, qlo, nc, x[(u + 1) & 1][0], x[(u + 1) & 1][1]);
         }
         float4v x0 = x[u & 1][0], x1 = x[u & 1][1];
-        if (partial && i == ntiles - 1) mask_tile(x0, x1, tw + i * kStep, t1, lg);
+        if (partial && tile[0] == ntot - 1) mask_tile(x0, x1, kTile * tile[0], ctx, lg);
         half8v pb;
         if constexpr (PACK8) pb = softmax_tile8(x0, x1, sm, m, l, acc);
         else pb = softmax_tile(x0, x1, sm, m, l, acc);
         vf.mma(vr[u % R], pb, acc, nc);
+#pragma unroll
+        for (int j = 0; j <= LOOK; ++j) tile[j] = tile[j + 1];
       }
     }
   }
@@ -417,7 +478,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   __shared__ int is_last;
   __shared__ UnitLds ush;
   const int nvalid = valid_chunks(a, ctx);
-  uint32_t* counter = a.counters + (int64_t)b * a.Hkv + hkv;
+  uint32_t* counter = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
   if (threadIdx.x == 0)
     is_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               (uint32_t)(nvalid - 1);
