@@ -1,10 +1,13 @@
 """Decode-attention layer-step benchmark on one MI355X.
 
-A step is one decode step over every layer of the configuration.  Per layer it runs:
-- quantize-on-append of the new token's K/V (one HIP launch);
-- split-K quantized decode attention over the whole context, whose chunk partials are
-  merged in the same launch (TILE32 V, at most 64 chunks and 8 query heads per KV head)
-  or by a second, combine launch.
+A step is one decode step over every layer of the configuration.  Per layer it runs
+quantize-on-append of the new token's K/V and split-K quantized decode attention over
+the whole context:
+- INT4-asymmetric K with TILE32 V (configs 2, 3): both in one launch
+  (kvq_append_decode_attn), whose chunk partials are merged in the same launch (at most
+  64 chunks and 8 query heads per KV head);
+- otherwise: the append launch, then the attention launch (plus a combine launch for the
+  row-layout kernels).
 
 Caches are seeded synthetic data of the configured shape, one distinct cache per
 layer, built on the GPU with the same HIP append kernel.  Each step rewrites the
@@ -13,7 +16,10 @@ last slot and attends over the full context, so every step does identical work.
 The timed region replays a HIP graph of W warm-up and then K timed steps, bracketed
 by hipEvents on the launch stream.  ``value`` is the mean microseconds per
 layer-step (append + attention).  The line also carries:
-- ``roofline``: algorithmic bytes of the attention kernel / its measured time;
+- ``roofline``: algorithmic bytes of the dominant kernel (the fused step kernel, else
+  the attention kernel) / its measured time per layer;
+- ``attention_us_per_layer_step`` / ``append_us_per_layer_step``: each half timed alone
+  (its own HIP graph), as a breakdown;
 - ``cpu_baseline``: the CPU oracle (the reference's torch path restated) timed on a
   bounded sample on this host's cores.
 
@@ -50,6 +56,13 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device copy three times (rocprof counter calibration)")
     return ap.parse_args()
+
+
+def append_bytes(cfg):
+    """Bytes of one layer's quantize-on-append: fp16 K and V rows in, codes (+ fp16
+    outlier channels) out, for every (b, kv head)."""
+    out = (128 if cfg.k_format == "int8" else 64) + 64 + (8 if cfg.outlier_channels else 0)
+    return cfg.batch * cfg.kv_heads * (2 * 128 * 2 + out)
 
 
 def algorithmic_bytes(cfg, ctx_list):
@@ -130,6 +143,8 @@ class Layer:
         del ks_view
         self.plan = DecodePlan(self.q, kfmt, kview, vfmt, vview, self.ctx, Hkv, cap,
                                1.0 / math.sqrt(128), 32, inv_tau=self.inv_tau, chunk_tokens=chunk)
+        # INT4-asymmetric K and TILE32 V: kvq_append_decode_attn does the step in one launch
+        self.fused = self.v_tiled
 
     def _append_params(self, cfg, kx, vx, pos):
         C = self.C
@@ -169,6 +184,15 @@ class Layer:
 
     def attend(self, stream):
         self.plan.launch(stream)
+
+    def step(self, stream):
+        """One decode layer-step: one fused launch (append + attention) where the format
+        has it, else the append launch then the attention launch."""
+        if self.fused:
+            self.plan.launch_append(self.pk, self.pv, stream)
+        else:
+            self.append(stream)
+            self.attend(stream)
 
 
 def time_region(fn, stream, steps, warmup, use_graph):
@@ -352,7 +376,7 @@ def main():
           file=sys.stderr, flush=True)
 
     use_graph = not args.no_graph
-    step_fn = lambda s: [(L.append(s), L.attend(s)) for L in layers]
+    step_fn = lambda s: [L.step(s) for L in layers]
     attn_fn = lambda s: [L.attend(s) for L in layers]
     app_fn = lambda s: [L.append(s) for L in layers]
     ms_step, g_step = time_region(step_fn, None, args.steps, args.warmup, use_graph)
@@ -362,9 +386,15 @@ def main():
     us_attn = ms_attn * 1000.0 / nl
     us_app = ms_app * 1000.0 / nl
     nbytes = algorithmic_bytes(cfg, ctx)
-    achieved = nbytes / (us_attn * 1e-6) / 1e9
-    print(f"[bench] step {ms_step:.3f} ms = {us_layer:.2f} us/layer-step "
-          f"(attention {us_attn:.2f} us, append {us_app:.2f} us); attention {achieved:.0f} GB/s",
+    fused = layers[0].fused
+    # the dominant kernel: the fused step kernel (append + attention, one launch per layer)
+    # where the format has it, else the attention kernel; its algorithmic bytes include the
+    # append's (the new rows in, their codes out)
+    roof_bytes = nbytes + (append_bytes(cfg) if fused else 0)
+    roof_us = us_layer if fused else us_attn
+    achieved = roof_bytes / (roof_us * 1e-6) / 1e9
+    print(f"[bench] step {ms_step:.3f} ms = {us_layer:.2f} us/layer-step (fused={fused}; "
+          f"attention alone {us_attn:.2f} us, append alone {us_app:.2f} us); {achieved:.0f} GB/s",
           file=sys.stderr, flush=True)
 
     ceiling = stream_ceiling(device)
@@ -398,6 +428,7 @@ def main():
                          + (" + 4 fp16 K channels" if cfg.outlier_channels else ""),
             "chunk_tokens": layers[0].plan.chunk_tokens,
             "hip_graph": use_graph,
+            "fused_step": fused,
         },
         "attention_us_per_layer_step": round(us_attn, 3),
         "append_us_per_layer_step": round(us_app, 3),
@@ -408,8 +439,10 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": measured_traffic(cfg.index),
-            "bytes_per_launch": nbytes,
-            "kernel": attention_kernels(cfg, layers[0]) + " (one kvq_decode_attn call per layer)",
+            "bytes_per_launch": roof_bytes,
+            "kernel": (attention_kernels(cfg, layers[0]) +
+                       (" with the append fused (one kvq_append_decode_attn call per layer)"
+                        if fused else " (one kvq_decode_attn call per layer)")),
         },
         "stream_ceiling": ceiling,
         "cpu_baseline": cpu,

@@ -173,6 +173,21 @@ typedef struct kvq_append_params {
 int kvq_quant_append(const kvq_append_params* k, const kvq_append_params* v,
                      kvq_stream_t stream);
 
+/* Decode step of one layer in one launch: quantize-on-append of one new token per
+ * (b, kv head) followed by the decode attention of p over the cache that now holds it.
+ *
+ * Replaces the append + attention pair of the reference's decode step,
+ *   cache.append(layer, k, v)            src/engine/patch_model.py:755
+ *   decode_attn_*(q, caches..., ctx)     src/engine/patch_model.py:837-957
+ * with the codes and the output bit-identical to kvq_quant_append then kvq_decode_attn.
+ * Supported for INT4_ASYM K and V with V in the TILE32 layout (k_new / v_new: seq_new 1,
+ * static fp16 tables, no scale policy); k_new and v_new must name the very buffers,
+ * tables and strides p reads (codes, outlier side-band), and share write_pos.  Anything
+ * else returns KVQ_ERR_UNSUPPORTED (or KVQ_ERR_INVALID), and the caller makes the two
+ * calls instead.  The status words are updated as kvq_quant_append does. */
+int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
+                           const kvq_append_params* v_new, kvq_stream_t stream);
+
 /* message for the last non-OK return on this thread ("" if none) */
 const char* kvq_last_error(void);
 /* ABI version (increments on incompatible changes to the structs above); this is 2 */

@@ -111,6 +111,7 @@ class AppendParams(ctypes.Structure):
 
 EXPORTED_SYMBOLS = (
     "kvq_decode_attn",
+    "kvq_append_decode_attn",
     "kvq_decode_chunk_tokens",
     "kvq_decode_workspace_bytes",
     "kvq_quant_append",
@@ -152,6 +153,9 @@ def lib() -> ctypes.CDLL:
         L.kvq_decode_workspace_bytes.restype = c_i64
         L.kvq_quant_append.argtypes = [ctypes.POINTER(AppendParams), ctypes.POINTER(AppendParams), c_vp]
         L.kvq_quant_append.restype = c_i32
+        L.kvq_append_decode_attn.argtypes = [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams),
+                                             ctypes.POINTER(AppendParams), c_vp]
+        L.kvq_append_decode_attn.restype = c_i32
         L.kvq_last_error.argtypes = []
         L.kvq_last_error.restype = ctypes.c_char_p
         L.kvq_abi_version.argtypes = []

@@ -32,6 +32,7 @@ for them.
 from __future__ import annotations
 
 import ctypes
+import math
 import logging
 import warnings
 from typing import Dict, List, Optional, Tuple
@@ -706,16 +707,9 @@ class _StaticG32Cache(_EngineBase):
         self._k[layer_id], self._v[layer_id], self._ko[layer_id] = nk, nv, no
         self._layer_capacity[layer_id] = new_cap
 
-    def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
-        self._validate_kv(layer_id, k, v)
-        B, H, S, D = k.shape
-        if self.k_scale.shape[1] != H:
-            raise ValueError(f"calibration vs model heads mismatch: {self.k_scale.shape[1]} vs {H}")
-        old = self._layer_seq_lens[layer_id]
-        self._ensure(layer_id, B, H, old + S)
-        if S == 0:
-            return
-        status = self._status_buf(k.device) if self.check_numerics else None
+    def _append_params(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status):
+        """kvq_append_params for K and V of this layer written at slot pos, and the
+        tensors they point at."""
         pk, pv = C.AppendParams(), C.AppendParams()
         keep = []
         kfmt = C.KVQ_FMT_INT8_SYM if self._k_int8 else C.KVQ_FMT_INT4_ASYM
@@ -725,7 +719,7 @@ class _StaticG32Cache(_EngineBase):
             xs = x if x.stride(-1) == 1 else x.contiguous()
             keep.append(xs)
             sptr = None if status is None else status.data_ptr() + (0 if side == "k" else 8)
-            _fill_append(p, fmt, xs, 32, codes, old, sptr)
+            _fill_append(p, fmt, xs, 32, codes, pos, sptr)
             if side == "v" and self.v_tiled:
                 p.codes_layout = C.KVQ_LAYOUT_TILE32
                 p.codes_stride_t = 64
@@ -741,6 +735,19 @@ class _StaticG32Cache(_EngineBase):
                 p.n_outlier = oi.shape[-1]
                 p.outlier_idx, p.outlier_out = oi.data_ptr(), oo.data_ptr()
                 p.oo_stride_b, p.oo_stride_h, p.oo_stride_t = oo.stride(0), oo.stride(1), oo.stride(2)
+        return pk, pv, keep
+
+    def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        if self.k_scale.shape[1] != H:
+            raise ValueError(f"calibration vs model heads mismatch: {self.k_scale.shape[1]} vs {H}")
+        old = self._layer_seq_lens[layer_id]
+        self._ensure(layer_id, B, H, old + S)
+        if S == 0:
+            return
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv, keep = self._append_params(layer_id, k, v, old, status)
         self._launch_append(pk, pv, k.device)
         if status is not None:
             self._check_status(layer_id, k.numel(), "K8V4" if self._k_int8 else "INT4-asym",
@@ -777,6 +784,51 @@ class _StaticG32Cache(_EngineBase):
 class INT4AsymKVCache(_StaticG32Cache):
     """Asymmetric INT4 K and V with static group-32 scale / zero-point (configs 2 and 3),
     optionally with 4 fp16 outlier K channels per head."""
+
+    def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
+                           sm_scale: Optional[float] = None,
+                           inv_tau: Optional[Tensor] = None) -> Tensor:
+        """Decode step of one layer in one HIP launch: append the new token (k, v: fp16
+        [B, H, 1, 128]) and attend over the layer's whole cache, the new token included.
+        Returns fp16 [B, Hq, 128].  Codes and output are bit-identical to ``append`` then
+        :func:`kernels.decode_attn_int4_asym` over ``get_int4_g32_tensors`` with context
+        lengths ``get_seq_len()`` (the append + attention of the reference's decode step,
+        src/engine/patch_model.py:755-957).  With ``check_numerics``, NaN / Inf in k or v
+        raise ValueError and the cache does not advance."""
+        from .kernels import DecodePlan, _check_static_args, kv_view_static
+
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        if S != 1:
+            raise ValueError(f"append_decode_attn appends one token per step, got S={S}")
+        if self.k_scale.shape[1] != H:
+            raise ValueError(f"calibration vs model heads mismatch: {self.k_scale.shape[1]} vs {H}")
+        old = self._layer_seq_lens[layer_id]
+        self._ensure(layer_id, B, H, old + 1)
+        # the views get_int4_g32_tensors gives once the token is in (same split as the
+        # two-call path, hence the same output bits)
+        n = old + 1
+        kb, vb = self._k[layer_id][:, :, :n], self._v[layer_id][:, :, :-(-n // TILE_TOKENS)]
+        ob = None if self._ko[layer_id] is None else self._ko[layer_id][:, :, :n]
+        ks, kz = self.k_scale[layer_id], self.k_zp[layer_id]
+        vs, vz = self.v_scale[layer_id], self.v_zp[layer_id]
+        oi = None if self.k_outlier_idx is None else self.k_outlier_idx[layer_id]
+        _check_static_args(q, kb, vb, (ks, kz, vs, vz), torch.empty(B))
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv, keep = self._append_params(layer_id, k, v, old, status)
+        ctx = torch.full((B,), n, dtype=torch.int32, device=q.device)
+        plan = DecodePlan(q, C.KVQ_FMT_INT4_ASYM, kv_view_static(kb, ks, kz, oi, ob),
+                          C.KVQ_FMT_INT4_ASYM, kv_view_static(vb, vs, vz), ctx, H, kb.shape[2],
+                          sm_scale, 32, inv_tau=inv_tau, keepalive=(keep, kb, vb, ob))
+        out = plan.launch_append(pk, pv)
+        if status is not None:
+            self._check_status(layer_id, k.numel(), "INT4-asym", "the code range")
+        self._layer_seq_lens[layer_id] = old + 1
+        if layer_id == 0:
+            self._seq_len = old + 1
+        return out
 
     def get_int4_g32_tensors(self, layer_id: int):
         """(k_codes [B,H,n,64], v_tiles [B,H,ceil(n/32),2048] (TILE32 layout), k_scale, k_zp,

@@ -723,7 +723,8 @@ extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   return counters_offset(p, nch) + (int64_t)p->batch * p->kv_heads * kCtrSlotWords * 4 + 256;
 }
 
-extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) {
+// kvq_decode_attn, and with app != nullptr kvq_append_decode_attn (tiled path only)
+static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_stream_t stream) {
   if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
   if (p->head_dim != kD) return fail(KVQ_ERR_UNSUPPORTED, "head_dim must be 128");
   if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0)
@@ -794,6 +795,12 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   a.out = reinterpret_cast<half_t*>(p->out);
   a.o_sb = p->out_stride_b; a.o_sh = p->out_stride_h;
 
+  a.app = FusedAppend{};
+  if (app) {
+    if (!tiled) return fail(KVQ_ERR_UNSUPPORTED, "fused append needs the TILE32 V layout");
+    a.app = *app;
+  }
+
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   a.fused = tiled && nch64 <= kUnitChunks && n_rep <= 8;
   if (tiled) {
@@ -824,6 +831,73 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
   return KVQ_OK;
+}
+
+extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) {
+  return decode_impl(p, nullptr, stream);
+}
+
+// One new token per (b, kv head) appended to the cache p attends over, in the same launch.
+// The append parameters must describe exactly that cache: the same code, outlier and
+// static-table buffers with the same strides (so the kernel writes what it later reads).
+static int check_fused_side(const kvq_append_params* x, const kvq_kv_view& v,
+                            const kvq_decode_params* p, bool is_k) {
+  const std::string n(is_k ? "k_new" : "v_new");
+  if (!x) return fail(KVQ_ERR_INVALID, n + " is NULL");
+  if (x->format != KVQ_FMT_INT4_ASYM)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append supports INT4_ASYM only");
+  if (x->seq_new != 1) return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append takes one token");
+  if (x->batch != p->batch || x->heads != p->kv_heads || x->head_dim != kD || x->group_size != 32)
+    return fail(KVQ_ERR_INVALID, n + ": shape does not match the decode call");
+  if (!x->x || ((uintptr_t)x->x % 4) || (x->x_stride_b % 2) || (x->x_stride_h % 2))
+    return fail(KVQ_ERR_INVALID, n + ": x is NULL or its rows are not 4-byte aligned");
+  if (x->write_pos < 0 || x->write_pos >= p->capacity)
+    return fail(KVQ_ERR_INVALID, n + ": write_pos outside the cache capacity");
+  if (x->codes != v.codes || x->codes_stride_b != v.stride_b || x->codes_stride_h != v.stride_h)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": codes must be the buffer the decode call reads");
+  if (is_k ? (x->codes_layout != KVQ_LAYOUT_ROWS || x->codes_stride_t != v.stride_t)
+           : (x->codes_layout != KVQ_LAYOUT_TILE32))
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": codes layout differs from the decode call's");
+  if (x->static_scale != v.scale || x->static_zp != v.zero_point ||
+      x->static_scale_dtype != KVQ_DTYPE_F16 || x->static_stride_h != v.scale_stride_h ||
+      x->static_stride_g != v.scale_stride_g)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": static tables differ from the decode call's");
+  if (x->adaptive || x->mixed_rescue || x->rescue_quantile > 0.f || x->rescue_all || x->scale_out)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": scale policies do not apply to INT4_ASYM");
+  if (x->n_outlier != v.n_outlier)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels differ from the decode call's");
+  if (x->n_outlier &&
+      (x->outlier_idx != v.outlier_idx || x->outlier_out != v.outlier_val ||
+       x->oo_stride_b != v.outlier_stride_b || x->oo_stride_h != v.outlier_stride_h ||
+       x->oo_stride_t != v.outlier_stride_t))
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier buffers differ from the decode call's");
+  return KVQ_OK;
+}
+
+extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
+                                      const kvq_append_params* v_new, kvq_stream_t stream) {
+  if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
+  if (p->v.layout != KVQ_LAYOUT_TILE32 || p->k_format != KVQ_FMT_INT4_ASYM ||
+      p->v_format != KVQ_FMT_INT4_ASYM)
+    return fail(KVQ_ERR_UNSUPPORTED,
+                "the fused append needs INT4_ASYM K and INT4_ASYM V in the TILE32 layout");
+  int rc = check_fused_side(k_new, p->k, p, true);
+  if (rc) return rc;
+  rc = check_fused_side(v_new, p->v, p, false);
+  if (rc) return rc;
+  if (k_new->write_pos != v_new->write_pos)
+    return fail(KVQ_ERR_INVALID, "k_new and v_new must share write_pos");
+  FusedAppend f;
+  f.kx = reinterpret_cast<const half_t*>(k_new->x);
+  f.ksb = k_new->x_stride_b;
+  f.ksh = k_new->x_stride_h;
+  f.vx = reinterpret_cast<const half_t*>(v_new->x);
+  f.vsb = v_new->x_stride_b;
+  f.vsh = v_new->x_stride_h;
+  f.wpos = k_new->write_pos;
+  f.kstatus = k_new->status;
+  f.vstatus = v_new->status;
+  return decode_impl(p, &f, stream);
 }
 
 extern "C" const char* kvq_last_error(void) { return g_last_error.c_str(); }

@@ -33,6 +33,19 @@ struct KvDev {
   int layout;  // KVQ_LAYOUT_*
 };
 
+// The new token of a fused quantize-on-append (kvq_append_decode_attn): fp16 K / V rows
+// [B, Hkv, 128] (strides in elements), the slot they go to, and the optional status words
+// (int32 [2] each: NaN/Inf flag, clamped-element count).  kx == nullptr: no append.
+struct FusedAppend {
+  const half_t* kx;
+  int64_t ksb, ksh;
+  const half_t* vx;
+  int64_t vsb, vsh;
+  int64_t wpos;
+  int32_t* kstatus;
+  int32_t* vstatus;
+};
+
 struct DecodeArgs {
   const half_t* q;
   int64_t q_sb, q_sh;
@@ -51,6 +64,7 @@ struct DecodeArgs {
   int fused;           // 1: the split-K kernel merges the partials itself (combine_unit)
   half_t* out;
   int64_t o_sb, o_sh;
+  FusedAppend app;
 };
 
 __device__ __forceinline__ uint32_t splat_h2(half_t s) { return as_u32(half2v{s, s}); }

@@ -360,6 +360,55 @@ struct VAsymT {
   }
 };
 
+// Fused quantize-on-append of the new token of (b, kv head): one wave, two values per
+// lane, the arithmetic of the append kernel (asym_pack_pair with the decode's static
+// tables).  K goes to row wpos, V to its TILE32 bytes, the outlier channels verbatim.
+// NaN / Inf set status[0], clamped elements are added to status[1] (per side).
+template <bool OUT>
+__device__ __forceinline__ void append_token(const DecodeArgs& a, int b, int hkv, int lane) {
+  const FusedAppend& f = a.app;
+  const int64_t t = f.wpos;
+  const int g = lane >> 4;  // group of channels 2 lane, 2 lane + 1
+  const half_t* xk = f.kx + (int64_t)b * f.ksb + (int64_t)hkv * f.ksh;
+  const half_t* xv = f.vx + (int64_t)b * f.vsb + (int64_t)hkv * f.vsh;
+  const half2v k2 = *reinterpret_cast<const half2v*>(xk + 2 * lane);
+  const half2v v2 = *reinterpret_cast<const half2v*>(xv + 2 * lane);
+  const half_t* ks = reinterpret_cast<const half_t*>(a.k.scale);
+  const half_t* vs = reinterpret_cast<const half_t*>(a.v.scale);
+  int kclip = 0, vclip = 0;
+  const uint8_t kb = asym_pack_pair((float)k2.x, (float)k2.y, (float)ks[hkv * a.k.ssh + g * a.k.ssg],
+                                    (float)a.k.zp[hkv * a.k.ssh + g * a.k.ssg], kclip);
+  const uint8_t vb = asym_pack_pair((float)v2.x, (float)v2.y, (float)vs[hkv * a.v.ssh + g * a.v.ssg],
+                                    (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg], vclip);
+  uint8_t* kc = const_cast<uint8_t*>(a.k.codes) + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+  uint8_t* vc = const_cast<uint8_t*>(a.v.codes) + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+  kc[t * a.k.st + lane] = kb;
+  vc[tile32_offset(t, lane)] = vb;
+  if constexpr (OUT) {
+    if (lane < 4) {
+      const int ch = min(max(a.k.oidx[hkv * 4 + lane], 0), kD - 1);
+      half_t* orow = const_cast<half_t*>(a.k.oval) + (int64_t)b * a.k.osb + (int64_t)hkv * a.k.osh +
+                     t * a.k.ost;
+      orow[lane] = xk[ch];
+    }
+  }
+  const bool kbad = !(__builtin_isfinite((float)k2.x) && __builtin_isfinite((float)k2.y));
+  const bool vbad = !(__builtin_isfinite((float)v2.x) && __builtin_isfinite((float)v2.y));
+  const bool any_kbad = __ballot(kbad) != 0, any_vbad = __ballot(vbad) != 0;
+  kclip = wave_sum_int(kclip);
+  vclip = wave_sum_int(vclip);
+  if (lane == 0) {
+    if (f.kstatus) {
+      if (any_kbad) atomicOr(&f.kstatus[0], 1);
+      if (kclip) atomicAdd(&f.kstatus[1], kclip);
+    }
+    if (f.vstatus) {
+      if (any_vbad) atomicOr(&f.vstatus[0], 1);
+      if (vclip) atomicAdd(&f.vstatus[1], vclip);
+    }
+  }
+}
+
 template <bool OUT, int LOOK, bool PACK8, int WPE = 3>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
@@ -367,6 +416,14 @@ void decode_tiled_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, lg = lane >> 4;
+
+  // Fused quantize-on-append: the wave whose schedule holds the new token's tile (below)
+  // writes it before it issues any load, so its loads of that tile, later in program
+  // order and to the same addresses, read the new codes.  (The tile may lie past the
+  // context, and that wave's work-group may then have nothing else to do.)
+  if (a.app.kx != nullptr &&
+      chunk * kWaves + wave == (int)((a.app.wpos / kTile) % (a.n_chunks * kWaves)))
+    append_token<OUT>(a, b, hkv, lane);
 
   int64_t ctx64 = a.ctx[b];
   ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);

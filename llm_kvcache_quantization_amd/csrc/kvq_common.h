@@ -99,6 +99,12 @@ __device__ __forceinline__ float wave_sum_xor_groups(float x) {
   return x;
 }
 
+__device__ __forceinline__ int wave_sum_int(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // max of 8 floats with v_max3_f32 (no NaN canonicalisation; inputs are finite or -inf)
@@ -110,6 +116,32 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 __device__ __forceinline__ float max8f(float a, float b, float c, float d, float e, float f,
                                        float g, float h) {
   return max3f(max3f(a, b, c), max3f(d, e, f), max3f(g, h, h));
+}
+
+// Byte offset, within the (b, h) slab of a KVQ_LAYOUT_TILE32 cache, of packed byte bi
+// (0..63) of token t: tile t / 32 holds for lane L = 16 g + c the 32 bytes of its PV
+// operand, dword 2 p + k = bytes (4c + 2k, 4c + 2k + 1) of the two tokens a = 0, 1 of
+// pair p, where token r = t % 32 = 16 (p / 2) + 4 g + 2 (p % 2) + a.
+__host__ __device__ __forceinline__ int64_t tile32_offset(int64_t t, int bi) {
+  const int r = (int)(t & 31);
+  const int g = (r & 15) >> 2, p = 2 * (r >> 4) + ((r & 3) >> 1), a = r & 1;
+  const int c = bi >> 2, k = (bi >> 1) & 1, j = bi & 1;
+  return (t >> 5) * 2048 + ((16 * g + c) * 8 + 2 * p + k) * 4 + 2 * a + j;
+}
+
+// Asymmetric INT4 with a static scale s and zero-point z of the pair's group:
+// c = clamp(rne((x - z) / s), -8, 7), packed as ((c0 + 8) << 4) | (c1 + 8) (even element
+// in the high nibble).  The quotient is an IEEE fp32 division, as torch's.  Adds the
+// number of clamped elements to clipped.  (src/kernels/triton_quantize_pack_int4.py:18-62,
+// tests/test_fused_quantize_pack.py:8-17, src/quant/int4_basic.py:263-270)
+__device__ __forceinline__ uint8_t asym_pack_pair(float x0, float x1, float s, float z,
+                                                  int& clipped) {
+  const float r0 = rintf(__fdiv_rn(x0 - z, s));
+  const float r1 = rintf(__fdiv_rn(x1 - z, s));
+  clipped += (r0 < -8.f || r0 > 7.f) + (r1 < -8.f || r1 > 7.f);
+  const int c0 = (int)fminf(fmaxf(r0, -8.f), 7.f);
+  const int c1 = (int)fminf(fmaxf(r1, -8.f), 7.f);
+  return (uint8_t)(((c0 + 8) << 4) | (c1 + 8));
 }
 
 // streaming loads: the code bytes are read once, so do not keep them in the caches

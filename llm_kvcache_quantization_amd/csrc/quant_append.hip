@@ -55,17 +55,6 @@ struct AppendDev {
   int tile32;  // codes in KVQ_LAYOUT_TILE32 (INT4_ASYM)
 };
 
-// Byte offset, within the (b, h) slab of a KVQ_LAYOUT_TILE32 cache, of packed byte bi
-// (0..63) of token t: tile t / 32 holds for lane L = 16 g + c the 32 bytes of its PV
-// operand, dword 2 p + k = bytes (4c + 2k, 4c + 2k + 1) of the two tokens a = 0, 1 of
-// pair p, where token r = t % 32 = 16 (p / 2) + 4 g + 2 (p % 2) + a.
-__device__ __forceinline__ int64_t tile32_offset(int64_t t, int bi) {
-  const int r = (int)(t & 31);
-  const int g = (r & 15) >> 2, p = 2 * (r >> 4) + ((r & 3) >> 1), a = r & 1;
-  const int c = bi >> 2, k = (bi >> 1) & 1, j = bi & 1;
-  return (t >> 5) * 2048 + ((16 * g + c) * 8 + 2 * p + k) * 4 + 2 * a + j;
-}
-
 __device__ __forceinline__ float ld_static(const AppendDev& a, int h, int g) {
   const int64_t off = (int64_t)h * a.st_sh + (int64_t)g * a.st_sg;
   return a.st_f32 ? reinterpret_cast<const float*>(a.st)[off]
@@ -169,12 +158,7 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
     const int64_t off = (int64_t)h * a.st_sh + (int64_t)g * a.st_sg;
     const float s = (float)reinterpret_cast<const half_t*>(a.st)[off];
     const float z = (float)a.st_zp[off];
-    const float r0 = rintf(__fdiv_rn(x0 - z, s));
-    const float r1 = rintf(__fdiv_rn(x1 - z, s));
-    clipped = (r0 < -8.f || r0 > 7.f) + (r1 < -8.f || r1 > 7.f);
-    const int c0 = (int)fminf(fmaxf(r0, -8.f), 7.f);
-    const int c1 = (int)fminf(fmaxf(r1, -8.f), 7.f);
-    const uint8_t byte = (uint8_t)(((c0 + 8) << 4) | (c1 + 8));
+    const uint8_t byte = asym_pack_pair(x0, x1, s, z, clipped);
     if (a.tile32)
       a.codes[(int64_t)b * a.csb + (int64_t)h * a.csh + tile32_offset(t, lane)] = byte;
     else

@@ -207,6 +207,17 @@ class DecodePlan:
         C.check(C.lib().kvq_decode_attn(self._pp, ctypes.c_void_p(s)))
         return self.out
 
+    def launch_append(self, k_new: C.AppendParams, v_new: C.AppendParams,
+                      stream: Optional[int] = None) -> torch.Tensor:
+        """One launch: quantize-on-append of the new token described by k_new / v_new
+        (which must target this plan's cache buffers) followed by this plan's attention
+        (kvq_append_decode_attn).  The caller keeps the tensors k_new / v_new point at
+        alive until the launch has run."""
+        s = C.stream_handle(self.device) if stream is None else stream
+        C.check(C.lib().kvq_append_decode_attn(self._pp, ctypes.byref(k_new), ctypes.byref(v_new),
+                                               ctypes.c_void_p(s)))
+        return self.out
+
 
 def _bump_debug_stats(debug_stats, layer_idx, block_size):
     # same keys as the reference wrapper (triton_decode_attn_int8.py:474-480),

@@ -18,7 +18,7 @@ def declared_functions():
 
 def test_header_declares_entry_points():
     assert declared_functions() == sorted([
-        "kvq_abi_version", "kvq_decode_attn", "kvq_decode_chunk_tokens",
+        "kvq_abi_version", "kvq_append_decode_attn", "kvq_decode_attn", "kvq_decode_chunk_tokens",
         "kvq_decode_workspace_bytes", "kvq_last_error", "kvq_quant_append"])
 
 

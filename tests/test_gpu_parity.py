@@ -424,3 +424,80 @@ def test_tiled_plan_reuse_changing_context():
                                       torch.tensor(ctx, dtype=torch.int32), 1 / math.sqrt(128),
                                       inv_tau=tau, k_outlier_idx=oidx, k_outlier_val=oval)
         assert_close(out, ref, f"plan reuse ctx={ctx}")
+
+
+# ---------------------------------------------------------------- fused decode step
+
+
+@pytest.mark.parametrize("cfg_idx,B,S0,steps,outliers", [
+    (3, 2, 4095, 3, True),     # the new tokens cross a tile boundary (4095, 4096, 4097)
+    (3, 3, 40, 2, True),       # new token's tile is in each wave's first (burst) tiles
+    (2, 2, 9000, 2, True),     # GQA 6, the tile read late in the wave's schedule
+    (3, 1, 700, 2, False),     # no outlier channels
+    (3, 2, 0, 2, True),        # empty cache: the first token is the whole context
+])
+def test_fused_append_decode_matches_two_calls(cfg_idx, B, S0, steps, outliers):
+    """append_decode_attn (one launch) against append + decode_attn_int4_asym (two
+    launches) on twin caches: codes, outlier side-band and outputs bit-identical, and the
+    output within tolerance of the oracle."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[cfg_idx]
+    t = SY.calibrate(cfg, 0)
+    g = gen(500 + S0)
+    k, v = SY.draw_kv(cfg, 0, B, S0 + steps, g)
+    qs = [SY.draw_q(cfg, B, g) for _ in range(steps)]
+    tau = SY.inv_tau(cfg)[0]
+    oi = t.k_outlier_idx[None] if outliers else None
+    mk = lambda: K.INT4AsymKVCache(1, t.k_scale[None], t.k_zp[None], t.v_scale[None], t.v_zp[None],
+                                   device=DEV, k_outlier_idx=oi)
+    two, one = mk(), mk()
+    if S0:
+        two.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
+        one.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
+    sm = 1 / math.sqrt(128)
+    for i in range(steps):
+        kn, vn = k[:, :, S0 + i:S0 + i + 1].to(DEV), v[:, :, S0 + i:S0 + i + 1].to(DEV)
+        q = qs[i].to(DEV)
+        two.append(0, kn, vn)
+        kc, vc, ks, kz, vs, vz, oidx, ov = two.get_int4_g32_tensors(0)
+        n = two.get_seq_len()
+        cl = torch.full((B,), n, dtype=torch.int32, device=DEV)
+        ref_out = K.decode_attn_int4_asym(q, kc, vc, ks, kz, vs, vz, cl, sm, inv_tau=tau.to(DEV),
+                                          k_outlier_idx=oidx, k_outlier_val=ov)
+        out = one.append_decode_attn(0, q, kn, vn, sm_scale=sm, inv_tau=tau.to(DEV))
+        torch.cuda.synchronize()
+        assert one.get_seq_len() == n
+        kc1, vc1, _, _, _, _, _, ov1 = one.get_int4_g32_tensors(0)
+        assert torch.equal(kc1, kc), f"K codes differ at step {i}"
+        assert torch.equal(K.untile_v(vc1, n), K.untile_v(vc, n)), f"V codes differ at step {i}"
+        if outliers:
+            assert torch.equal(ov1, ov), f"outlier values differ at step {i}"
+        assert torch.equal(out, ref_out), f"fused output differs from the two-call path at step {i}"
+        ref = OA.decode_attn_asym_ref(qs[i], kc.cpu(), K.untile_v(vc, n).cpu(), t.k_scale, t.k_zp,
+                                      t.v_scale, t.v_zp, cl.cpu(), sm, inv_tau=tau,
+                                      k_outlier_idx=t.k_outlier_idx if outliers else None,
+                                      k_outlier_val=None if ov is None else ov.cpu())
+        assert_close(out, ref, f"fused step cfg{cfg_idx} S{n}")
+
+
+def test_fused_append_decode_nan_raises_and_does_not_advance():
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[3]
+    t = SY.calibrate(cfg, 0)
+    g = gen(77)
+    k, v = SY.draw_kv(cfg, 0, 2, 65, g)
+    q = SY.draw_q(cfg, 2, g).to(DEV)
+    cache = K.INT4AsymKVCache(1, t.k_scale[None], t.k_zp[None], t.v_scale[None], t.v_zp[None],
+                              device=DEV, k_outlier_idx=t.k_outlier_idx[None], check_numerics=True)
+    cache.append(0, k[:, :, :64].to(DEV), v[:, :, :64].to(DEV))
+    bad = v[:, :, 64:].clone()
+    bad[1, 2, 0, 17] = float("nan")
+    with pytest.raises(ValueError, match="NaN or Inf"):
+        cache.append_decode_attn(0, q, k[:, :, 64:].to(DEV), bad.to(DEV))
+    assert cache.get_seq_len() == 64
+    out = cache.append_decode_attn(0, q, k[:, :, 64:].to(DEV), v[:, :, 64:].to(DEV))
+    assert cache.get_seq_len() == 65 and torch.isfinite(out.float()).all()
