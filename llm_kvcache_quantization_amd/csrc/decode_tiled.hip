@@ -68,21 +68,35 @@ __device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t voff, uint32_t sof
 // Fused combine: the last work-group of a (b, kv head) to finish merges the partials of
 // its n_rep heads, which the other work-groups of the launch stored write-through, and
 // writes the output rows with combine_one's arithmetic.  Needs n_rep <= 8 and n_chunks <=
-// kUnitChunks.  Thread t takes head t / 32 and channels 4 (t % 32) .. +3: one 16-byte
-// load per chunk, kUnitBatch of them in flight at once, bypassing the non-coherent cache
-// levels (sc1, as device-scope atomic loads).  The (m, l) pairs go through LDS.  Loads of
-// chunks past nvalid (or heads past n_rep) use an offset past the descriptor's end and
-// read 0.
+// kUnitChunks.  Thread t takes head h = t / 32 and channels 4 (t % 32) .. +3; the 32
+// threads of a head are one half of a wave.  Every load is issued first: (m, l) of chunks
+// t % 32 (+ 32) and one 16-byte acc load per chunk (kUnitBatch in flight), bypassing the
+// non-coherent cache levels (sc1, as device-scope atomic loads).  The max and the
+// denominator are reduced across the half-wave; the chunk weights reach the other lanes
+// of the head through LDS.  Loads of chunks past nvalid (or heads past n_rep) use an
+// offset past the descriptor's end and read 0.
 constexpr int kBufSC1 = 16;  // cache-policy bits: sc1 (device-coherent load)
 constexpr int kUnitBatch = 32;
 
 struct UnitLds {
-  float2 ml[8][kUnitChunks];
+  float e[8][kUnitChunks];  // chunk weights exp2(m_c - M) of head h
 };
+
+// max / sum over the 32 lanes of a half-wave (lanes l and l ^ 1, ^ 2, .., ^ 16)
+__device__ __forceinline__ float halfwave_max(float x) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+__device__ __forceinline__ float halfwave_sum(float x) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
 
 __device__ __forceinline__ void combine_unit(const DecodeArgs& a, UnitLds& sh, int b, int hkv,
                                              int nvalid) {
-  static_assert(kUnitChunks % 32 == 0 && kUnitChunks % kUnitBatch == 0, "chunk tiling");
+  static_assert(kUnitChunks == 64 && kUnitChunks % kUnitBatch == 0, "chunk tiling");
   const int t = threadIdx.x;
   const int h = t >> 5, dg = t & 31;
   const bool hv = h < a.n_rep;
@@ -99,36 +113,42 @@ __device__ __forceinline__ void combine_unit(const DecodeArgs& a, UnitLds& sh, i
       av[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, kBufSC1));
     }
   };
-  // (m, l) of chunks dg + 32 k of head h
+  // (m, l) of chunks dg and dg + 32 of head h (m = -inf, l = 0 past nvalid)
+  float m2[2], l2[2];
 #pragma unroll
-  for (int k = 0; k < kUnitChunks / 32; ++k) {
+  for (int k = 0; k < 2; ++k) {
     const int c = dg + 32 * k;
     const bool ok = hv && c < nvalid;
     const uint32_t off = ok ? (uint32_t)((h * a.n_chunks + c) * 8) : kOutOfRange;
     const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, (int)off, 0, kBufSC1));
-    sh.ml[h][c] = ok ? float2{__builtin_bit_cast(float, (uint32_t)v.x), __builtin_bit_cast(float, (uint32_t)v.y)}
-                     : float2{kNegInf, 0.f};
+    m2[k] = ok ? __builtin_bit_cast(float, (uint32_t)v.x) : kNegInf;
+    l2[k] = __builtin_bit_cast(float, (uint32_t)v.y);  // 0 when out of range
   }
   issue(0);
-  __syncthreads();
-  if (!hv) return;
-  float M = kNegInf;
-  for (int c = 0; c < nvalid; ++c) M = fmaxf(M, sh.ml[h][c].x);
-  float num[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.f;
+  const float M = halfwave_max(fmaxf(m2[0], m2[1]));
+  float e2[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) e2[k] = m2[k] == kNegInf ? 0.f : fast_exp2(m2[k] - M);
+  const float den = halfwave_sum(fmaf(e2[0], l2[0], e2[1] * l2[1]));
+  sh.e[h][dg] = e2[0];
+  sh.e[h][dg + 32] = e2[1];
+  // the weights of head h were written by this half-wave: a wave-level LDS wait suffices
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  float num[4] = {0.f, 0.f, 0.f, 0.f};
   for (int c0 = 0; c0 < nvalid; c0 += kUnitBatch) {
     if (c0 > 0) issue(c0);
 #pragma unroll
     for (int c = 0; c < kUnitBatch; ++c) {
-      const float2 ml = sh.ml[h][c0 + c];  // -inf, 0 past nvalid: weight 0
-      const float e = fast_exp2(ml.x - M);
+      const float e = sh.e[h][c0 + c];  // 0 past nvalid
       // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of
       // an ext_vector element lvalue reads element 0 whatever the index
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         num[j] = fmaf(e, __builtin_bit_cast(float, (uint32_t)av[c][j]), num[j]);
-      den = fmaf(e, ml.y, den);
     }
   }
+  if (!hv) return;
   const int g = dg >> 3;  // quantisation group of channels 4 dg .. 4 dg + 3
   const float s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
   const float z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
