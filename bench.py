@@ -41,6 +41,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+MIN_ROTATE = 4  # distinct caches timed in turn for single-layer configurations
 
 
 def parse():
@@ -88,9 +89,9 @@ class Layer:
         self.C = C
         B, Hkv, Hq = cfg.batch, cfg.kv_heads, cfg.q_heads
         cap = int(max(ctx))
-        t = SY.calibrate(cfg, layer)
+        t = SY.calibrate(cfg, layer % cfg.layers)
         self.tables = t
-        ch = SY.outlier_channels(cfg, layer)
+        ch = SY.outlier_channels(cfg, layer % cfg.layers)
         kb = 128 if cfg.k_format == "int8" else 64
         vb = 128 if cfg.v_format == "int8" else 64
         self.k = torch.empty(B, Hkv, cap, kb, dtype=torch.uint8, device=device)
@@ -110,18 +111,18 @@ class Layer:
             self.ko = torch.empty(B, Hkv, cap, 4, dtype=torch.float16, device=device)
         self.ctx = torch.tensor(ctx, dtype=torch.int32, device=device)
         self.q = SY.draw_q(cfg, B, gen, device=device)
-        self.inv_tau = SY.inv_tau(cfg)[layer].to(device)
+        self.inv_tau = SY.inv_tau(cfg)[layer % cfg.layers].to(device)
         # prefill: every slot [0, cap) gets quantized seeded data (chunks bound the temporaries)
         step = 8192
         for s0 in range(0, cap, step):
             n = min(step, cap - s0)
-            kx, vx = SY.draw_kv(cfg, layer, B, n, gen, device=device, ch=ch)
+            kx, vx = SY.draw_kv(cfg, layer % cfg.layers, B, n, gen, device=device, ch=ch)
             pk, pv = self._append_params(cfg, kx, vx, s0)
             C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
                                              ctypes.c_void_p(C.stream_handle(torch.device(device)))))
             del kx, vx
         # the decode-step token: rewrites slot cap-1 of every sequence each step
-        self.k_new, self.v_new = SY.draw_kv(cfg, layer, B, 1, gen, device=device, ch=ch)
+        self.k_new, self.v_new = SY.draw_kv(cfg, layer % cfg.layers, B, 1, gen, device=device, ch=ch)
         self.step_slot = cap - 1
         self.pk, self.pv = self._append_params(cfg, self.k_new, self.v_new, self.step_slot)
         self._pk, self._pv = ctypes.byref(self.pk), ctypes.byref(self.pv)
@@ -364,6 +365,11 @@ def main():
     C.lib()
     cfg = SY.CONFIGS[args.config]
     nl = args.layers or cfg.layers
+    # A single-layer configuration is timed over MIN_ROTATE distinct copies of the layer's
+    # cache (seeded like layers 0, 1, ...), so that no step is served from the 256 MB
+    # Infinity Cache; the result is still per layer-step.
+    if not args.layers and nl < MIN_ROTATE:
+        nl = MIN_ROTATE
     device = "cuda:0"
     torch.cuda.set_device(0)
     ctx = SY.context_lengths(cfg).tolist()
@@ -377,6 +383,14 @@ def main():
 
     use_graph = not args.no_graph
     step_fn = lambda s: [L.step(s) for L in layers]
+    # bring the GPU to its steady state before any timed region (untimed, not counted in
+    # --warmup): the first region timed otherwise runs about 2% slow
+    s0 = torch.cuda.current_stream().cuda_stream
+    t_warm = time.time()
+    while time.time() - t_warm < 0.3:
+        for L in layers:
+            L.attend(s0)
+        torch.cuda.synchronize()
     attn_fn = lambda s: [L.attend(s) for L in layers]
     app_fn = lambda s: [L.append(s) for L in layers]
     ms_step, g_step = time_region(step_fn, None, args.steps, args.warmup, use_graph)
@@ -423,6 +437,7 @@ def main():
             "q_heads": cfg.q_heads,
             "kv_heads": cfg.kv_heads,
             "layers": nl,
+            "model_layers": cfg.layers,
             "context": ctx,
             "kv_format": f"K {cfg.k_format} / V {cfg.v_format} g32"
                          + (" + 4 fp16 K channels" if cfg.outlier_channels else ""),

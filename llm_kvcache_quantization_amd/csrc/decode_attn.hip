@@ -577,17 +577,17 @@ static const void* select_kernel(Family f) {
 }
 
 // work-groups of the selected kernel that fit on the device at once
-static int64_t resident_slots(const void* fn) {
+static int64_t resident_slots(const void* fn, int threads) {
   static std::mutex mu;
   static std::map<std::pair<const void*, int>, int64_t> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 1024;
   std::lock_guard<std::mutex> g(mu);
-  auto key = std::make_pair(fn, dev);
+  auto key = std::make_pair(fn, dev * 4096 + threads);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWaves * 64, 0) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       per_cu <= 0 || cus <= 0) {
     (void)hipGetLastError();
@@ -606,18 +606,24 @@ static const void* kernel_for(const kvq_decode_params* p) {
                               p->v.scale_dtype == KVQ_DTYPE_F32, p->k.n_outlier > 0));
 }
 
+// waves per work-group of the split-K kernel kvq_decode_attn launches for p
+static int waves_for(const kvq_decode_params* p) {
+  return p->v.layout == KVQ_LAYOUT_TILE32 ? kTiledWaves : kWaves;
+}
+
 // Tokens per work-group: fill every resident work-group slot exactly once when the
 // context is long enough (one wave of work-groups, no tail), in multiples of the
-// kWaves x 32 tokens one pass of the work-group covers, never below kMinChunk.
+// waves x 32 tokens one pass of the work-group covers, never below kMinChunk.
 int32_t choose_chunk(const kvq_decode_params* p) {
   if (p->chunk_tokens > 0) return p->chunk_tokens;
   const int64_t units = (int64_t)p->batch * p->kv_heads;
   const void* fn = kernel_for(p);
-  const int64_t slots = fn ? resident_slots(fn) : 1024;
+  const int nw = waves_for(p);
+  const int64_t slots = fn ? resident_slots(fn, nw * 64) : 1024;
   int64_t per_unit = slots / (units > 0 ? units : 1);
   if (per_unit < 1) per_unit = 1;
   int64_t c = (p->capacity + per_unit - 1) / per_unit;
-  c = ((c + kTile * kWaves - 1) / (kTile * kWaves)) * (kTile * kWaves);
+  c = ((c + kTile * nw - 1) / (kTile * nw)) * (kTile * nw);
   if (c < kMinChunk) c = kMinChunk;
   const int64_t min_for_cap = (p->capacity + kMaxChunks - 1) / kMaxChunks;
   if (c < min_for_cap) c = ((min_for_cap + kTile - 1) / kTile) * kTile;
@@ -786,6 +792,7 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   a.chunk = chunk;
   a.n_chunks = (int)nch64;
   a.strided = tiled ? 1 : 0;
+  a.nw = waves_for(p);
   const int64_t rows = (int64_t)p->batch * p->q_heads * nch64;
   a.part_acc = reinterpret_cast<float*>(p->workspace);
   a.part_ml = reinterpret_cast<float2*>(reinterpret_cast<char*>(p->workspace) + rows * kD * 4);
@@ -802,7 +809,7 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   }
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  a.fused = tiled && nch64 <= kUnitChunks && n_rep <= 8;
+  a.fused = tiled && nch64 <= kUnitChunks;
   if (tiled) {
     launch_tiled(a, kf, p->k.n_outlier > 0,
                  dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch), s);

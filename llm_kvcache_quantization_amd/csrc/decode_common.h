@@ -7,7 +7,8 @@
 
 namespace kvq {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;       // waves per work-group of the row-layout split-K kernel
+constexpr int kTiledWaves = 8;  // waves per work-group of the tiled kernel (two per SIMD)
 constexpr int kTile = 32;   // tokens per wave iteration (two 16-token MFMA row blocks)
 constexpr int kD = 128;
 constexpr float kTau = 8.0f;  // lazy-rescale headroom in log2 units
@@ -56,8 +57,9 @@ struct DecodeArgs {
   int64_t cap;
   float sm_log2e;
   int chunk, n_chunks;
-  int strided;      // work-group c takes 32-token tiles c*kWaves + w + i*n_chunks*kWaves
-                    // (wave w) instead of the contiguous tokens [c*chunk, (c+1)*chunk)
+  int strided;      // work-group c takes 32-token tiles c*nw + w + i*n_chunks*nw (wave w)
+                    // instead of the contiguous tokens [c*chunk, (c+1)*chunk)
+  int nw;           // waves per work-group of the split-K kernel
   float* part_acc;  // [B, Hq, n_chunks, 128]
   float2* part_ml;  // [B, Hq, n_chunks]
   uint32_t* counters;  // [B, Hkv] slots of kCtrSlotWords u32, zero between calls (below)
@@ -189,14 +191,16 @@ __device__ __forceinline__ void mask_tile(float4v& x0, float4v& x1, int tt, int 
   }
 }
 
-// Merges the (m, l, acc) states of the kWaves waves of a work-group through LDS and
+// Merges the (m, l, acc) states of the NW waves of a work-group through LDS and
 // writes one partial (M, L, acc[128]) per valid head of this chunk.  acc[mb][r] of lane
 // (head, lg) holds channel d = 32 lg + 8 r + mb.
-struct MergeLds {
-  float m[kWaves][16];
-  float l[kWaves][16];
-  float acc[kWaves][16][kD + 1];
+template <int NW>
+struct MergeLdsT {
+  float m[NW][16];
+  float l[NW][16];
+  float acc[NW][16][kD + 1];
 };
+using MergeLds = MergeLdsT<kWaves>;
 
 // partial stores; WT = write-through at device scope, so a work-group of the same launch
 // on another XCD can read them once the store has completed (no L2 write-back needed)
@@ -206,8 +210,8 @@ __device__ __forceinline__ void store_partial(float* p, float v) {
   else *p = v;
 }
 
-template <bool PACK8 = false, bool WT = false>
-__device__ __forceinline__ void merge_and_store(const DecodeArgs& a, MergeLds& sh, int wave,
+template <bool PACK8 = false, bool WT = false, int NW = kWaves>
+__device__ __forceinline__ void merge_and_store(const DecodeArgs& a, MergeLdsT<NW>& sh, int wave,
                                                 int col, int lg, float m, float l,
                                                 const float4v acc[8], int b, int hkv, int chunk) {
   if constexpr (PACK8) l += dpp_ror8f<0xF>(l, l);  // add the block-1 part from lane h + 8
@@ -221,14 +225,14 @@ __device__ __forceinline__ void merge_and_store(const DecodeArgs& a, MergeLds& s
 #pragma unroll
     for (int r = 0; r < 4; ++r) sh.acc[wave][col][32 * lg + 8 * r + mb] = acc[mb][r];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kWaves * 64) {
+  for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += NW * 64) {
     const int h = idx >> 7, d = idx & (kD - 1);
     float M = sh.m[0][h];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sh.m[w][h]);
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, sh.m[w][h]);
     float num = 0.f, den = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float e = fast_exp2(sh.m[w][h] - M);
       num = fmaf(e, sh.acc[w][h][d], num);
       den = fmaf(e, sh.l[w][h], den);
@@ -247,7 +251,7 @@ __device__ __forceinline__ void merge_and_store(const DecodeArgs& a, MergeLds& s
 __host__ __device__ __forceinline__ int valid_chunks(const DecodeArgs& a, int64_t ctx) {
   if (a.strided) {
     const int64_t tiles = (ctx + kTile - 1) / kTile;
-    const int64_t n = (tiles + kWaves - 1) / kWaves;
+    const int64_t n = (tiles + a.nw - 1) / a.nw;
     return (int)(n < a.n_chunks ? n : a.n_chunks);
   }
   return (int)((ctx + a.chunk - 1) / a.chunk);

@@ -1,20 +1,27 @@
 // Split-K decode attention for gfx950 over INT4_ASYM K (optional fp16 outlier
-// channels) and INT4_ASYM V stored in the TILE32 layout.
+// channels) and INT4_ASYM V stored in the TILE32 layout, optionally with the
+// quantize-on-append of the step's new token in the same launch.
 //
-// The work decomposition is that of decode_attn.hip: one work-group = 4 waves = one
-// (batch b, kv head, chunk of tokens), the GQA heads of the kv head are the N = 16
-// columns of v_mfma_f32_16x16x32_f16 and each wave walks 32-token tiles.  What is
-// different is how the bytes get into registers and how cheaply they become fp16:
+// One work-group = kTW (8) waves = one (batch b, kv head, chunk); the GQA heads of the kv
+// head are the N = 16 columns of v_mfma_f32_16x16x32_f16 and each wave walks 32-token
+// tiles.  At the headline shape one work-group fills one CU (two waves per SIMD).
 //
+//  * Tile schedule: the n_chunks work-groups of a (b, kv head) interleave tile by tile
+//    (wave w of work-group c takes tiles c * kTW + w + i * n_chunks * kTW), so the device
+//    streams each slab front to back and every wave gets the same number of tiles when
+//    the context allows.  The schedule is static: results do not depend on timing.
+//  * The two waves of a SIMD (w and w + 4) publish their step counts in LDS; the one
+//    ahead lowers its priority (s_setprio), which cancels the SIMD's oldest-first issue
+//    order that would otherwise let one of them finish far earlier.
 //  * K rows are dense (64 bytes per token) and so is the outlier side-band (8 bytes).
 //  * Every cache read is a buffer load.  The (b, kv head) slab of each stream is a
 //    wave-uniform buffer resource whose size bounds the reads (bytes past it read as
-//    zero), the per-tile offset is a scalar and the per-lane offset is loop-invariant,
-//    so the loop does no 64-bit address arithmetic on the vector ALU.
+//    zero, with no memory access), the per-tile offset is a scalar and the per-lane
+//    offset is loop-invariant.  Loads past a wave's last tile are issued with an
+//    out-of-range offset rather than skipped, which keeps the compiler's vmcnt waits
+//    exact.
 //  * V in the TILE32 layout stores, for each tile, the 32 bytes lane L needs for its PV
 //    operand contiguously at L * 32: two dwordx4 loads per lane, fully coalesced.
-//    Within a lane's 32 bytes, dword 2 p + k holds bytes (2k, 2k+1) of the lane's 4-byte
-//    column slice for the two tokens of k-slot pair p.
 //  * The 4 fp16 outlier channels of the 32 tokens of a tile (256 bytes) are fetched by
 //    one dword load of the whole wave: lane (row, g) takes the channel pair g & 1 of
 //    token 16 (g >> 1) + row, which is where the outlier MFMA of row block g >> 1
@@ -25,16 +32,14 @@
 //    The two offsets are exact in fp16 and are removed in the bias (K) or the
 //    epilogue (V): channel offsets 72 = 64 + 8 and 1032 = 1024 + 8.
 //  * The q-dependent operands (q * s split into fp16 hi + lo, the bias) are built once
-//    per work-group: wave j builds those of channel slice 8j..8j+7 of each group and
-//    shares them through LDS.
+//    per work-group and shared through LDS; the q loads are issued before the first
+//    cache loads.  The lo halves are read from LDS at every tile (fewer VGPRs).
 //  * K and V tiles are fetched LOOK steps ahead of their use (register rings of
-//    LOOK + 1 tiles); QK of tile i + 1 is issued before softmax / PV of tile i.  The
-//    first tiles are requested before the q set-up.
-//  * The n_chunks work-groups of a (b, kv head) interleave tile by tile, so the device
-//    streams each slab front to back.  With at most kUnitChunks of them and n_rep <= 8
-//    the last of them to finish merges their partials (no second launch; the arrival
-//    counters live in the workspace, which must be zero-filled before its first use and
-//    which every call leaves zero); otherwise combine_kernel does.
+//    LOOK + 1 tiles); QK of tile i + 1 is issued before softmax / PV of tile i.
+//  * With at most kUnitChunks chunks per (b, kv head) the last work-group to finish
+//    merges the partials (no second launch; its arrival counters live in the workspace,
+//    which must be zero-filled before its first use and which every call leaves zero);
+//    otherwise combine_kernel does.
 #include "decode_common.h"
 
 #include <cstdlib>
@@ -67,96 +72,156 @@ __device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t voff, uint32_t sof
 
 // Fused combine: the last work-group of a (b, kv head) to finish merges the partials of
 // its n_rep heads, which the other work-groups of the launch stored write-through, and
-// writes the output rows with combine_one's arithmetic.  Needs n_rep <= 8 and n_chunks <=
-// kUnitChunks.  Thread t takes head h = t / 32 and channels 4 (t % 32) .. +3; the 32
-// threads of a head are one half of a wave.  Every load is issued first: (m, l) of chunks
-// t % 32 (+ 32) and one 16-byte acc load per chunk (kUnitBatch in flight), bypassing the
-// non-coherent cache levels (sc1, as device-scope atomic loads).  The max and the
-// denominator are reduced across the half-wave; the chunk weights reach the other lanes
-// of the head through LDS.  Loads of chunks past nvalid (or heads past n_rep) use an
-// offset past the descriptor's end and read 0.
+// writes the output rows with combine_one's arithmetic.  Needs n_chunks <= kUnitChunks
+// (64).  Wave w merges query heads w, w + kTW, ..; lane l takes channels 2 l and 2 l + 1
+// and the (m, l) pair of chunk l.  Only the nvalid chunks that hold partials are read
+// (8 bytes per lane, kUnitBatch chunks in flight), bypassing the non-coherent cache
+// levels (sc1, as device-scope atomic loads); the max and the denominator are wave
+// reductions and the chunk weights are broadcast with readlane.
+constexpr int kTW = kTiledWaves;
 constexpr int kBufSC1 = 16;  // cache-policy bits: sc1 (device-coherent load)
-constexpr int kUnitBatch = 32;
+constexpr int kUnitBatch = 16;
 
-struct UnitLds {
-  float e[8][kUnitChunks];  // chunk weights exp2(m_c - M) of head h
+// Wave-wide max / sum without the LDS crossbar: DPP within each row of 16 lanes (xor 1,
+// xor 2 in the quad, then rotations by 4 and 8), then the four row results by readlane.
+// Every lane gets the same value; the order of operations is fixed.
+template <int CTRL>
+__device__ __forceinline__ float dppf(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_lane(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+__device__ __forceinline__ float wave_max64(float x) {
+  x = fmaxf(x, dppf<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+  x = fmaxf(x, dppf<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+  x = fmaxf(x, dppf<0x124>(x));  // row_ror:4
+  x = fmaxf(x, dppf<0x128>(x));  // row_ror:8
+  return fmaxf(fmaxf(row_lane(x, 0), row_lane(x, 16)), fmaxf(row_lane(x, 32), row_lane(x, 48)));
+}
+__device__ __forceinline__ float wave_sum64(float x) {
+  x += dppf<0xB1>(x);
+  x += dppf<0x4E>(x);
+  x += dppf<0x124>(x);
+  x += dppf<0x128>(x);
+  return (row_lane(x, 0) + row_lane(x, 16)) + (row_lane(x, 32) + row_lane(x, 48));
+}
+
+// The work-group's merged partial: acc[h][d] = sum over its waves of e_w acc_w, ml[h] =
+// (M, sum_w e_w l_w) with e_w = exp2(m_w - M), for query heads h < n_rep.
+struct OwnPartial {
+  float acc[16][kD];
+  float2 ml[16];
 };
 
-// max / sum over the 32 lanes of a half-wave (lanes l and l ^ 1, ^ 2, .., ^ 16)
-__device__ __forceinline__ float halfwave_max(float x) {
+// Merges the (m, l, acc) states of the kTW waves into `own` (LDS).  acc[mb][r] of lane
+// (head, lg) holds channel d = 32 lg + 8 r + mb.  Ends with a work-group barrier.
+template <bool PACK8>
+__device__ __forceinline__ void merge_waves(const DecodeArgs& a, MergeLdsT<kTW>& sh, OwnPartial& own,
+                                            int wave, int col, int lg, float m, float l,
+                                            const float4v acc[8]) {
+  if constexpr (PACK8) l += dpp_ror8f<0xF>(l, l);  // add the block-1 part from lane h + 8
+  l = wave_sum_xor_groups(l);
+  if (lg == 0) {
+    sh.m[wave][col] = m;
+    sh.l[wave][col] = l;
+  }
+  if (col < a.n_rep) {
 #pragma unroll
-  for (int o = 1; o < 32; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-  return x;
-}
-__device__ __forceinline__ float halfwave_sum(float x) {
+    for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-  for (int o = 1; o < 32; o <<= 1) x += __shfl_xor(x, o, 64);
-  return x;
+      for (int r = 0; r < 4; ++r) sh.acc[wave][col][32 * lg + 8 * r + mb] = acc[mb][r];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64) {
+    const int h = idx >> 7, d = idx & (kD - 1);
+    float M = sh.m[0][h];
+#pragma unroll
+    for (int w = 1; w < kTW; ++w) M = fmaxf(M, sh.m[w][h]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kTW; ++w) {
+      const float e = fast_exp2(sh.m[w][h] - M);
+      num = fmaf(e, sh.acc[w][h][d], num);
+      den = fmaf(e, sh.l[w][h], den);
+    }
+    own.acc[h][d] = num;
+    if (d == 0) own.ml[h] = float2{M, den};
+  }
+  __syncthreads();
 }
 
-__device__ __forceinline__ void combine_unit(const DecodeArgs& a, UnitLds& sh, int b, int hkv,
-                                             int nvalid) {
-  static_assert(kUnitChunks == 64 && kUnitChunks % kUnitBatch == 0, "chunk tiling");
-  const int t = threadIdx.x;
-  const int h = t >> 5, dg = t & 31;
-  const bool hv = h < a.n_rep;
+// Stores the work-group's partial for the merge of another work-group (write-through at
+// device scope: visible to any XCD once the store has completed).
+__device__ __forceinline__ void store_own(const DecodeArgs& a, const OwnPartial& own, int b,
+                                         int hkv, int chunk) {
+  for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64) {
+    const int h = idx >> 7, d = idx & (kD - 1);
+    const int64_t pi = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks + chunk;
+    store_partial<true>(a.part_acc + pi * kD + d, own.acc[h][d]);
+    if (d == 0) {
+      store_partial<true>(&a.part_ml[pi].x, own.ml[h].x);
+      store_partial<true>(&a.part_ml[pi].y, own.ml[h].y);
+    }
+  }
+}
+
+// The last work-group's combine: its own partial (chunk `mine`) comes from LDS, the
+// others' from memory.
+__device__ __forceinline__ void combine_unit(const DecodeArgs& a, const OwnPartial& own, int b,
+                                             int hkv, int nvalid, int mine, int wave, int lane) {
+  static_assert(kUnitChunks <= 64, "one (m, l) pair per lane");
   const int64_t row0 = ((int64_t)b * a.Hq + hkv * a.n_rep) * a.n_chunks;
   const rsrc_t r = buffer_rsrc(a.part_acc + row0 * kD, (uint32_t)(a.n_rep * a.n_chunks * kD * 4));
   const rsrc_t rml = buffer_rsrc(a.part_ml + row0, (uint32_t)(a.n_rep * a.n_chunks * 8));
-  const uint32_t vbase = (uint32_t)((h * a.n_chunks * kD + 4 * dg) * 4);
-  u32x4 av[kUnitBatch];
-  auto issue = [&](int c0) {
-#pragma unroll
-    for (int c = 0; c < kUnitBatch; ++c) {
-      const uint32_t voff =
-          (hv && c0 + c < nvalid) ? vbase + (uint32_t)((c0 + c) * kD * 4) : kOutOfRange;
-      av[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, kBufSC1));
-    }
-  };
-  // (m, l) of chunks dg and dg + 32 of head h (m = -inf, l = 0 past nvalid)
-  float m2[2], l2[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int c = dg + 32 * k;
-    const bool ok = hv && c < nvalid;
-    const uint32_t off = ok ? (uint32_t)((h * a.n_chunks + c) * 8) : kOutOfRange;
-    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, (int)off, 0, kBufSC1));
-    m2[k] = ok ? __builtin_bit_cast(float, (uint32_t)v.x) : kNegInf;
-    l2[k] = __builtin_bit_cast(float, (uint32_t)v.y);  // 0 when out of range
-  }
-  issue(0);
-  const float M = halfwave_max(fmaxf(m2[0], m2[1]));
-  float e2[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) e2[k] = m2[k] == kNegInf ? 0.f : fast_exp2(m2[k] - M);
-  const float den = halfwave_sum(fmaf(e2[0], l2[0], e2[1] * l2[1]));
-  sh.e[h][dg] = e2[0];
-  sh.e[h][dg + 32] = e2[1];
-  // the weights of head h were written by this half-wave: a wave-level LDS wait suffices
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
-  float num[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int c0 = 0; c0 < nvalid; c0 += kUnitBatch) {
-    if (c0 > 0) issue(c0);
-#pragma unroll
-    for (int c = 0; c < kUnitBatch; ++c) {
-      const float e = sh.e[h][c0 + c];  // 0 past nvalid
-      // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of
-      // an ext_vector element lvalue reads element 0 whatever the index
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        num[j] = fmaf(e, __builtin_bit_cast(float, (uint32_t)av[c][j]), num[j]);
-    }
-  }
-  if (!hv) return;
-  const int g = dg >> 3;  // quantisation group of channels 4 dg .. 4 dg + 3
+  const int g = lane >> 4;  // quantisation group of channels 2 lane, 2 lane + 1
   const float s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
   const float z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
-  half4v o;
+  for (int h = wave; h < a.n_rep; h += kTW) {
+    const bool ok = lane < nvalid;
+    const bool ext = ok && lane != mine;
+    const u32x2 mlv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+        rml, (int)(ext ? (uint32_t)((h * a.n_chunks + lane) * 8) : kOutOfRange), 0, kBufSC1));
+    const uint32_t vbase = (uint32_t)((h * a.n_chunks * kD + 2 * lane) * 4);
+    u32x2 av[kUnitBatch];
+    auto issue = [&](int c0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o[j] = (half_t)fmaf(s, num[j] / den - ((j & 1) ? 1032.0f : 72.0f), z);
-  *reinterpret_cast<half4v*>(a.out + (int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + h) * a.o_sh +
-                             4 * dg) = o;
+      for (int c = 0; c < kUnitBatch; ++c) {
+        const int cc = c0 + c;
+        const uint32_t voff =
+            (cc < nvalid && cc != mine) ? vbase + (uint32_t)(cc * kD * 4) : kOutOfRange;
+        av[c] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, 0, kBufSC1));
+      }
+    };
+    issue(0);
+    const float2 mo = own.ml[h];
+    const float mc = !ok ? kNegInf : (ext ? __builtin_bit_cast(float, (uint32_t)mlv.x) : mo.x);
+    const float lc = !ok ? 0.f : (ext ? __builtin_bit_cast(float, (uint32_t)mlv.y) : mo.y);
+    const float M = wave_max64(mc);
+    const float e = ok ? fast_exp2(mc - M) : 0.f;
+    const float den = wave_sum64(e * lc);
+    // the chunks are added in chunk order whichever work-group merges (same bits every call)
+    const float o0 = own.acc[h][2 * lane], o1 = own.acc[h][2 * lane + 1];
+    float n0 = 0.f, n1 = 0.f;
+    for (int c0 = 0; c0 < nvalid; c0 += kUnitBatch) {
+      if (c0 > 0) issue(c0);
+#pragma unroll
+      for (int c = 0; c < kUnitBatch; ++c) {
+        // weight of chunk c0 + c (0 past nvalid), uniform
+        const float ec = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), c0 + c));
+        // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of
+        // an ext_vector element lvalue reads element 0 whatever the index
+        const bool is_own = c0 + c == mine;
+        n0 = fmaf(ec, is_own ? o0 : __builtin_bit_cast(float, (uint32_t)av[c].x), n0);
+        n1 = fmaf(ec, is_own ? o1 : __builtin_bit_cast(float, (uint32_t)av[c].y), n1);
+      }
+    }
+    const half2v o = {(half_t)fmaf(s, n0 / den - 72.0f, z), (half_t)fmaf(s, n1 / den - 1032.0f, z)};
+    *reinterpret_cast<half2v*>(a.out + (int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + h) * a.o_sh +
+                               2 * lane) = o;
+  }
 }
 
 // 8 packed codes -> 8 fp16 operands in k-slot order [e0, e4, e1, e5, e2, e6, e3, e7]
@@ -229,7 +294,7 @@ struct KAsymT {
   __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
     const int col = lane & 15, lg = lane >> 4;
     const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
-    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * wave);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
     in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
     in.s = reinterpret_cast<const half_t*>(a.k.scale)[hkv * a.k.ssh + lg * a.k.ssg];
     in.z = a.k.zp[hkv * a.k.ssh + lg * a.k.ssg];
@@ -246,8 +311,9 @@ struct KAsymT {
     const int col = lane & 15, lg = lane >> 4;
     const bool valid = col < a.n_rep;
     const bool has_tau = a.inv_tau != nullptr;
-    // this wave builds the operands of channels 32 lg + 8 j + e, j = wave
-    const int j = wave;
+    // waves j < 4 build the operands of channels 32 lg + 8 j + e (waves 4..7 compute the
+    // same values as wave j - 4 and do not store them)
+    const int j = wave & 3;
     const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
     const float s = (float)in.s;
     const float z = (float)in.z;
@@ -271,12 +337,14 @@ struct KAsymT {
       vl[k] = lo;
       part += qd * z - slot_offset(k) * ((float)hi + (float)lo);
     }
-    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
-    sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
-    *reinterpret_cast<u32x4*>(&sh.qv[col][32 * lg + 8 * j]) =
-        __builtin_bit_cast(u32x4, half8v{qs[0], qs[1], qs[2], qs[3], qs[4], qs[5], qs[6], qs[7]});
     part = wave_sum_xor_groups(part);
-    if (lg == 0) sh.bias[j][col] = part;
+    if (wave < 4) {
+      sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+      sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
+      *reinterpret_cast<u32x4*>(&sh.qv[col][32 * lg + 8 * j]) =
+          __builtin_bit_cast(u32x4, half8v{qs[0], qs[1], qs[2], qs[3], qs[4], qs[5], qs[6], qs[7]});
+      if (lg == 0) sh.bias[j][col] = part;
+    }
   }
 
   // after the work-group barrier: pick up the operands all four waves built
@@ -380,89 +448,148 @@ struct VAsymT {
   }
 };
 
-// Fused quantize-on-append of the new token of (b, kv head): one wave, two values per
-// lane, the arithmetic of the append kernel (asym_pack_pair with the decode's static
-// tables).  K goes to row wpos, V to its TILE32 bytes, the outlier channels verbatim.
-// NaN / Inf set status[0], clamped elements are added to status[1] (per side).
+// Fused quantize-on-append of the new token of (b, kv head): one wave (the writer), two
+// values per lane, the arithmetic of the append kernel (asym_pack_pair with the decode's
+// static tables).  K goes to row wpos, V to its TILE32 bytes, the outlier channels
+// verbatim.  The other waves issue nothing for it (even out-of-range memory operations
+// would occupy their address unit ahead of their first cache loads).  NaN / Inf set
+// status[0] and clamped elements are added to status[1] (per side).
+struct AppendIn {
+  uint32_t k2, v2;  // fp16 pair of channels 2 lane, 2 lane + 1
+  uint32_t o;       // lanes < 4: fp16 K value of outlier channel lane
+  float vs, vz;     // V scale / zero-point of group lane / 16
+};
+struct AppendFlags {
+  bool kbad = false, vbad = false;
+  int kclip = 0, vclip = 0;
+};
+
+// oc: the kv head's 4 outlier channels (from the q set-up's inputs)
 template <bool OUT>
-__device__ __forceinline__ void append_token(const DecodeArgs& a, int b, int hkv, int lane) {
+__device__ __forceinline__ void append_fetch(const DecodeArgs& a, int b, int hkv, int lane,
+                                             bool writer, int4 oc, AppendIn& in) {
   const FusedAppend& f = a.app;
-  const int64_t t = f.wpos;
-  const int g = lane >> 4;  // group of channels 2 lane, 2 lane + 1
   const half_t* xk = f.kx + (int64_t)b * f.ksb + (int64_t)hkv * f.ksh;
   const half_t* xv = f.vx + (int64_t)b * f.vsb + (int64_t)hkv * f.vsh;
-  const half2v k2 = *reinterpret_cast<const half2v*>(xk + 2 * lane);
-  const half2v v2 = *reinterpret_cast<const half2v*>(xv + 2 * lane);
-  const half_t* ks = reinterpret_cast<const half_t*>(a.k.scale);
-  const half_t* vs = reinterpret_cast<const half_t*>(a.v.scale);
-  int kclip = 0, vclip = 0;
-  const uint8_t kb = asym_pack_pair((float)k2.x, (float)k2.y, (float)ks[hkv * a.k.ssh + g * a.k.ssg],
-                                    (float)a.k.zp[hkv * a.k.ssh + g * a.k.ssg], kclip);
-  const uint8_t vb = asym_pack_pair((float)v2.x, (float)v2.y, (float)vs[hkv * a.v.ssh + g * a.v.ssg],
-                                    (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg], vclip);
-  uint8_t* kc = const_cast<uint8_t*>(a.k.codes) + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
-  uint8_t* vc = const_cast<uint8_t*>(a.v.codes) + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
-  kc[t * a.k.st + lane] = kb;
-  vc[tile32_offset(t, lane)] = vb;
+  const rsrc_t rk = buffer_rsrc(xk, kD * 2), rv = buffer_rsrc(xv, kD * 2);
+  in.k2 = bload1(rk, writer ? 4u * lane : kOutOfRange, 0);
+  in.v2 = bload1(rv, writer ? 4u * lane : kOutOfRange, 0);
+  in.o = 0;
   if constexpr (OUT) {
-    if (lane < 4) {
-      const int ch = min(max(a.k.oidx[hkv * 4 + lane], 0), kD - 1);
-      half_t* orow = const_cast<half_t*>(a.k.oval) + (int64_t)b * a.k.osb + (int64_t)hkv * a.k.osh +
-                     t * a.k.ost;
-      orow[lane] = xk[ch];
-    }
+    const int ch = lane == 0 ? oc.x : lane == 1 ? oc.y : lane == 2 ? oc.z : oc.w;
+    in.o = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+        rk, (int)(writer && lane < 4 ? 2u * (uint32_t)ch : kOutOfRange), 0, kBufNT);
   }
-  const bool kbad = !(__builtin_isfinite((float)k2.x) && __builtin_isfinite((float)k2.y));
-  const bool vbad = !(__builtin_isfinite((float)v2.x) && __builtin_isfinite((float)v2.y));
-  const bool any_kbad = __ballot(kbad) != 0, any_vbad = __ballot(vbad) != 0;
-  kclip = wave_sum_int(kclip);
-  vclip = wave_sum_int(vclip);
-  if (lane == 0) {
-    if (f.kstatus) {
-      if (any_kbad) atomicOr(&f.kstatus[0], 1);
-      if (kclip) atomicAdd(&f.kstatus[1], kclip);
-    }
-    if (f.vstatus) {
-      if (any_vbad) atomicOr(&f.vstatus[0], 1);
-      if (vclip) atomicAdd(&f.vstatus[1], vclip);
-    }
+  // V scale / zero-point of group lane / 16 (fp16, element offsets hkv * ssh + g * ssg)
+  const int g = lane >> 4;
+  const uint32_t so = (uint32_t)(hkv * a.v.ssh + g * a.v.ssg) * 2u;
+  // uniform descriptors spanning this kv head's 4 groups
+  const uint32_t tb = (uint32_t)(hkv * a.v.ssh + 3 * a.v.ssg + 1) * 2u;
+  const rsrc_t rs = buffer_rsrc(a.v.scale, tb), rz = buffer_rsrc(a.v.zp, tb);
+  in.vs = (float)__builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+      rs, (int)(writer ? so : kOutOfRange), 0, 0));
+  in.vz = (float)__builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+      rz, (int)(writer ? so : kOutOfRange), 0, 0));
+}
+
+// ks / kz: the K scale / zero-point of group lane / 16 (the q set-up reads the same ones)
+template <bool OUT>
+__device__ __forceinline__ void append_store(const DecodeArgs& a, rsrc_t rk, rsrc_t rv, rsrc_t ro,
+                                             int lane, bool write, const AppendIn& in, float ks,
+                                             float kz, AppendFlags& fl) {
+  const int64_t t = a.app.wpos;
+  const half2v k2 = as_h2(in.k2), v2 = as_h2(in.v2);
+  int kclip = 0, vclip = 0;
+  uint32_t kb = 0, vb = 0;
+  if (write) {  // wave-uniform: only the writer quantizes
+    kb = asym_pack_pair((float)k2.x, (float)k2.y, ks, kz, kclip);
+    vb = asym_pack_pair((float)v2.x, (float)v2.y, in.vs, in.vz, vclip);
+  }
+  __builtin_amdgcn_raw_buffer_store_b8((uint8_t)kb, rk, (int)(write ? (uint32_t)(t * kRowK + lane) : kOutOfRange), 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b8((uint8_t)vb, rv, (int)(write ? (uint32_t)tile32_offset(t, lane) : kOutOfRange), 0, 0);
+  if constexpr (OUT)
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)in.o, ro,
+                                          (int)(write && lane < 4 ? (uint32_t)(t * kRowO + 2 * lane) : kOutOfRange), 0, 0);
+  if (write) {
+    fl.kbad |= __ballot(!(__builtin_isfinite((float)k2.x) && __builtin_isfinite((float)k2.y))) != 0;
+    fl.vbad |= __ballot(!(__builtin_isfinite((float)v2.x) && __builtin_isfinite((float)v2.y))) != 0;
+    fl.kclip += wave_sum_int(kclip);
+    fl.vclip += wave_sum_int(vclip);
   }
 }
 
-template <bool OUT, int LOOK, bool PACK8, int WPE = 3>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+__device__ __forceinline__ void append_status(const FusedAppend& f, const AppendFlags& fl) {
+  if (f.kstatus) {
+    if (fl.kbad) atomicOr(&f.kstatus[0], 1);
+    if (fl.kclip) atomicAdd(&f.kstatus[1], fl.kclip);
+  }
+  if (f.vstatus) {
+    if (fl.vbad) atomicOr(&f.vstatus[0], 1);
+    if (fl.vclip) atomicAdd(&f.vstatus[1], fl.vclip);
+  }
+}
+
+template <bool OUT, int LOOK, bool PACK8, int WPE = 2>
+__global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
   const int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, lg = lane >> 4;
 
-  // Fused quantize-on-append: the wave whose schedule holds the new token's tile (below)
-  // writes it before it issues any load, so its loads of that tile, later in program
-  // order and to the same addresses, read the new codes.  (The tile may lie past the
-  // context, and that wave's work-group may then have nothing else to do.)
-  if (a.app.kx != nullptr &&
-      chunk * kWaves + wave == (int)((a.app.wpos / kTile) % (a.n_chunks * kWaves)))
-    append_token<OUT>(a, b, hkv, lane);
+  // Fused quantize-on-append.  The writer is the wave whose schedule (below) holds the new
+  // token's tile wt: its stores precede, in program order, its loads of that tile.  They
+  // are issued after the set-up, when the new rows (requested with q) have arrived, or
+  // before the first cache loads when wt is one of the wave's first LOOK + 1 tiles.  A
+  // writer whose work-group has no tile of the context stores before it leaves.
+  const bool app_on = a.app.kx != nullptr;
+  const int stride_all = a.n_chunks * kTW;
+  const int wt = app_on ? (int)(a.app.wpos / kTile) : 0;
+  const bool writer = app_on && chunk * kTW + wave == wt % stride_all;
+  AppendIn ain;
+  AppendFlags afl;
 
   int64_t ctx64 = a.ctx[b];
   ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);
   const int ctx = (int)ctx64;
   // The n_chunks work-groups of a (b, kv head) interleave: at step i the waves of all of
-  // them read one contiguous run of n_chunks * kWaves tiles, so the device streams each
-  // slab front to back.  Wave w of work-group c takes tiles c*kWaves + w + i*stride.
+  // them read one contiguous run of n_chunks * kTW tiles, so the device streams each
+  // slab front to back.  Wave w of work-group c takes tiles c*kTW + w + i*stride.
   const int ntot = (ctx + kTile - 1) / kTile;
+  if (writer && (ntot == 0 || chunk * kTW >= ntot)) {
+    int4 oc = int4{0, 0, 0, 0};
+    if constexpr (OUT) {
+      const int4 o = *reinterpret_cast<const int4*>(a.k.oidx + hkv * 4);
+      oc = int4{min(max(o.x, 0), kD - 1), min(max(o.y, 0), kD - 1), min(max(o.z, 0), kD - 1),
+                min(max(o.w, 0), kD - 1)};
+    }
+    append_fetch<OUT>(a, b, hkv, lane, true, oc, ain);
+    KAsymT<OUT> k0;
+    k0.setup_addr(a, b, hkv, lane);
+    VAsymT v0;
+    v0.setup(a, b, hkv, lane);
+    const int g = lane >> 4;
+    append_store<OUT>(a, k0.rk, v0.rv, k0.ro, lane, true, ain,
+                      (float)reinterpret_cast<const half_t*>(a.k.scale)[hkv * a.k.ssh + g * a.k.ssg],
+                      (float)a.k.zp[hkv * a.k.ssh + g * a.k.ssg], afl);
+    if (lane == 0) append_status(a.app, afl);
+  }
   if (ntot == 0) {  // empty context: the first work-group writes zero rows
     if (chunk == 0 && a.fused)
-      for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kWaves * 64)
+      for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
         a.out[(int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + (idx >> 7)) * a.o_sh +
               (idx & (kD - 1))] = (half_t)0.0f;
     return;
   }
-  if (chunk * kWaves >= ntot) return;  // no tile for this work-group (uniform)
+  if (chunk * kTW >= ntot) return;  // no tile for this work-group (uniform)
 
   __shared__ QShareLds qsh;
-  __shared__ MergeLds msh;
+  __shared__ MergeLdsT<kTW> msh;
+  // Waves w and w + 4 share a SIMD, which issues the older of two ready waves first;
+  // each publishes its step count and, when ahead of its partner, lowers its priority,
+  // so the two stay in step (the tile schedule, and so every result bit, is fixed).
+  __shared__ int progress[kTW];
+  progress[wave] = 0;
   KAsymT<OUT> kf;
   // the q-side inputs are requested first: the wait for them then does not include the
   // cache tiles requested next
@@ -473,12 +600,12 @@ void decode_tiled_kernel(DecodeArgs a) {
   vf.setup(a, b, hkv, lane);
 
   // Tile schedule: the n_chunks work-groups of a (b, kv head) interleave, so at step i the
-  // waves of all of them read one contiguous run of n_chunks * kWaves tiles and the device
-  // streams each slab front to back.  Wave w of work-group c takes tiles c * kWaves + w +
+  // waves of all of them read one contiguous run of n_chunks * kTW tiles and the device
+  // streams each slab front to back.  Wave w of work-group c takes tiles c * kTW + w +
   // i * stride (tile = 32 tokens; only the context's last tile, ntot - 1, may be partial).
   // The schedule is static, so results do not depend on timing.
-  const int first = chunk * kWaves + wave;
-  const int stride = a.n_chunks * kWaves;
+  const int first = chunk * kTW + wave;
+  const int stride = a.n_chunks * kTW;
   const bool partial = (ctx & (kTile - 1)) != 0;
   // tile[j] = tile of step i + j (j <= LOOK + 1)
   int tile[LOOK + 2];
@@ -493,27 +620,40 @@ void decode_tiled_kernel(DecodeArgs a) {
   // issued unconditionally (out of range for a tile past the context): conditional loads
   // would make the compiler's vmcnt waits conservative at the joins, i.e. wait for the
   // tiles just requested.
-#ifdef KVQ_EXP_QWAIT
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#else
   asm volatile("" ::: "memory");
-#endif
+  const bool early_write = writer && wt / stride_all <= LOOK;
+  if (early_write) {
+    append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
+    append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
+  }
 #pragma unroll
   for (int s = 0; s <= LOOK; ++s) {
     kf.load(kTile * tile[s], tile[s] < ntot, kr[s]);
     if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ntot, vr[s]);
   }
+  // The writer fetches the new rows now and stores their codes in the loop, at the last
+  // step that precedes its loads of tile wt (step wt_step - LOOK - 1), or right after the
+  // set-up when wt lies past the wave's tiles.
+  const bool late_write = writer && !early_write;
+  const int wt_step = (wt - (chunk * kTW + wave)) / stride_all;
+  const int store_step = late_write ? wt_step - LOOK - 1 : -1;
+  if (late_write) append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
   kf.setup_q(a, qin, lane, wave, qsh);
   NibConsts nc;
   nc.init();
   __syncthreads();
   kf.finish_setup(qsh, qin, lane);
+  // (wt past the context: the wave may have fewer steps than store_step)
+  const bool store_now = late_write && (wt >= ntot || store_step <= 0);
+  if (store_now)
+    append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
 
   float4v acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
   float m = kNegInf, l = 0.f;
   const float sm = a.sm_log2e;
+  int steps = 0;
   if (tile[0] < ntot) {
     float4v x[2][2];
     kf.qk(kr[0], qsh, (uint32_t)lane * 16u, nc, x[0][0], x[0][1]);
@@ -522,6 +662,8 @@ void decode_tiled_kernel(DecodeArgs a) {
       for (int u = 0; u < U; ++u) {
         // step i (i % U == u): the tiles of this wave form a prefix of its schedule
         if (tile[0] >= ntot) break;
+        if (late_write && !store_now && steps == store_step)
+          append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
         tile[LOOK + 1] = tile[LOOK] + stride;
         // fetch K of step i + LOOK + 1 (into the slot K of step i used) and V of step
         // i + LOOK (into the slot V of step i - 1 used), QK of step i + 1, then softmax
@@ -539,30 +681,40 @@ void decode_tiled_kernel(DecodeArgs a) {
         if constexpr (PACK8) pb = softmax_tile8(x0, x1, sm, m, l, acc);
         else pb = softmax_tile(x0, x1, sm, m, l, acc);
         vf.mma(vr[u % R], pb, acc, nc);
+        ++steps;
+        progress[wave] = steps;
+        if (__builtin_amdgcn_readfirstlane(progress[wave ^ 4]) < steps)
+          __builtin_amdgcn_s_setprio(0);
+        else
+          __builtin_amdgcn_s_setprio(2);
 #pragma unroll
         for (int j = 0; j <= LOOK; ++j) tile[j] = tile[j + 1];
       }
     }
   }
-  merge_and_store<PACK8, true>(a, msh, wave, col, lg, m, l, acc, b, hkv, chunk);
+  __builtin_amdgcn_s_setprio(0);
+  if (writer && lane == 0) append_status(a.app, afl);
 
-  // Fused combine.  The partials were stored write-through; once every store of the
-  // work-group has completed, one thread counts the work-group in.  The last of the
-  // (b, kv head)'s work-groups merges all partials and resets the counter.
-  if (!a.fused) return;  // combine_kernel merges
+  // Merge.  The waves' states are merged in LDS and the work-group's partial is stored
+  // write-through (combine_kernel merges them when a.fused == 0).  Once every store of the
+  // work-group has completed, one thread counts it in (word 0 of the (b, kv head)'s
+  // counter slot); the last of the (b, kv head)'s work-groups merges every partial, its
+  // own from LDS, writes the output and resets the counter.
+  const int nvalid = valid_chunks(a, ctx);
+  uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
+  __shared__ OwnPartial own;
+  __shared__ int is_last;
+  merge_waves<PACK8>(a, msh, own, wave, col, lg, m, l, acc);
+  store_own(a, own, b, hkv, chunk);
+  if (!a.fused) return;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  __shared__ int is_last;
-  __shared__ UnitLds ush;
-  const int nvalid = valid_chunks(a, ctx);
-  uint32_t* counter = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
   if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-              (uint32_t)(nvalid - 1);
+    is_last = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nvalid - 1);
   __syncthreads();
   if (!is_last) return;
-  combine_unit(a, ush, b, hkv, nvalid);
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  combine_unit(a, own, b, hkv, nvalid, chunk, wave, lane);
+  if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <bool OUT, bool PACK8>
@@ -584,7 +736,7 @@ int tiled_look() {
 
 template <bool OUT, bool PACK8>
 void launch_one(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  const dim3 block(kWaves * 64);
+  const dim3 block(kTW * 64);
   if (tiled_look() == 2)
     hipLaunchKernelGGL((decode_tiled_kernel<OUT, 2, PACK8>), grid, block, 0, s, a);
   else
