@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--chunk", type=int, default=0)
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (debug only)")
+    ap.add_argument("--no-breakdown", action="store_true",
+                    help="time only the layer-step (no attention-only / append-only graphs), "
+                         "so a profiler sees only the step's launches")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device copy three times (rocprof counter calibration)")
     return ap.parse_args()
@@ -388,27 +391,28 @@ def main():
     s0 = torch.cuda.current_stream().cuda_stream
     t_warm = time.time()
     while time.time() - t_warm < 0.3:
-        for L in layers:
-            L.attend(s0)
+        step_fn(s0)
         torch.cuda.synchronize()
     attn_fn = lambda s: [L.attend(s) for L in layers]
     app_fn = lambda s: [L.append(s) for L in layers]
     ms_step, g_step = time_region(step_fn, None, args.steps, args.warmup, use_graph)
-    ms_attn, _ = time_region(attn_fn, None, args.steps, args.warmup, use_graph)
-    ms_app, _ = time_region(app_fn, None, args.steps, args.warmup, use_graph)
+    us_attn = us_app = None
+    if not args.no_breakdown:
+        ms_attn, _ = time_region(attn_fn, None, args.steps, args.warmup, use_graph)
+        ms_app, _ = time_region(app_fn, None, args.steps, args.warmup, use_graph)
+        us_attn = ms_attn * 1000.0 / nl
+        us_app = ms_app * 1000.0 / nl
     us_layer = ms_step * 1000.0 / nl
-    us_attn = ms_attn * 1000.0 / nl
-    us_app = ms_app * 1000.0 / nl
     nbytes = algorithmic_bytes(cfg, ctx)
     fused = layers[0].fused
     # the dominant kernel: the fused step kernel (append + attention, one launch per layer)
     # where the format has it, else the attention kernel; its algorithmic bytes include the
     # append's (the new rows in, their codes out)
     roof_bytes = nbytes + (append_bytes(cfg) if fused else 0)
-    roof_us = us_layer if fused else us_attn
+    roof_us = us_layer if (fused or us_attn is None) else us_attn
     achieved = roof_bytes / (roof_us * 1e-6) / 1e9
     print(f"[bench] step {ms_step:.3f} ms = {us_layer:.2f} us/layer-step (fused={fused}; "
-          f"attention alone {us_attn:.2f} us, append alone {us_app:.2f} us); {achieved:.0f} GB/s",
+          f"attention alone {us_attn} us, append alone {us_app} us); {achieved:.0f} GB/s",
           file=sys.stderr, flush=True)
 
     ceiling = stream_ceiling(device)
@@ -445,8 +449,8 @@ def main():
             "hip_graph": use_graph,
             "fused_step": fused,
         },
-        "attention_us_per_layer_step": round(us_attn, 3),
-        "append_us_per_layer_step": round(us_app, 3),
+        "attention_us_per_layer_step": None if us_attn is None else round(us_attn, 3),
+        "append_us_per_layer_step": None if us_app is None else round(us_app, 3),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
