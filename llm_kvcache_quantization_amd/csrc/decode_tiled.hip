@@ -71,16 +71,12 @@ __device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t voff, uint32_t sof
 }
 
 // Fused combine: the last work-group of a (b, kv head) to finish merges the partials of
-// its n_rep heads, which the other work-groups of the launch stored write-through, and
-// writes the output rows with combine_one's arithmetic.  Needs n_chunks <= kUnitChunks
-// (64).  Wave w merges query heads w, w + kTW, ..; lane l takes channels 2 l and 2 l + 1
-// and the (m, l) pair of chunk l.  Only the nvalid chunks that hold partials are read
-// (8 bytes per lane, kUnitBatch chunks in flight), bypassing the non-coherent cache
-// levels (sc1, as device-scope atomic loads); the max and the denominator are wave
-// reductions and the chunk weights are broadcast with readlane.
+// its n_rep heads, which every work-group of the launch stored write-through, and writes
+// the output rows with combine_one's arithmetic.  Needs n_chunks <= kUnitChunks (64);
+// kUnitBatch chunk loads are in flight at a time.
 constexpr int kTW = kTiledWaves;
 constexpr int kBufSC1 = 16;  // cache-policy bits: sc1 (device-coherent load)
-constexpr int kUnitBatch = 16;
+constexpr int kUnitBatch = 8;
 
 // Wave-wide max / sum without the LDS crossbar: DPP within each row of 16 lanes (xor 1,
 // xor 2 in the quad, then rotations by 4 and 8), then the four row results by readlane.
@@ -108,19 +104,18 @@ __device__ __forceinline__ float wave_sum64(float x) {
   return (row_lane(x, 0) + row_lane(x, 16)) + (row_lane(x, 32) + row_lane(x, 48));
 }
 
-// The work-group's merged partial: acc[h][d] = sum over its waves of e_w acc_w, ml[h] =
-// (M, sum_w e_w l_w) with e_w = exp2(m_w - M), for query heads h < n_rep.
-struct OwnPartial {
-  float acc[16][kD];
-  float2 ml[16];
-};
-
-// Merges the (m, l, acc) states of the kTW waves into `own` (LDS).  acc[mb][r] of lane
-// (head, lg) holds channel d = 32 lg + 8 r + mb.  Ends with a work-group barrier.
+// Merges the (m, l, acc) states of the kTW waves (through LDS) into the work-group's
+// partial and stores it write-through at device scope, so another work-group of the launch,
+// on any XCD, can read it once the stores have completed.  acc[mb][r] of lane (head, lg)
+// holds channel d = 32 lg + 8 r + mb.  Wave w merges heads w, w + kTW, ..; lane l
+// channels 2 l and 2 l + 1: partial = sum_w e_w acc_w with e_w = exp2(m_w - M), (M,
+// sum_w e_w l_w) for the head's (m, l) pair.
 template <bool PACK8>
-__device__ __forceinline__ void merge_waves(const DecodeArgs& a, MergeLdsT<kTW>& sh, OwnPartial& own,
-                                            int wave, int col, int lg, float m, float l,
-                                            const float4v acc[8]) {
+__device__ __forceinline__ void merge_store_partial(const DecodeArgs& a, MergeLdsT<kTW>& sh,
+                                                    int wave, int lane, float m, float l,
+                                                    const float4v acc[8], int b, int hkv,
+                                                    int chunk) {
+  const int col = lane & 15, lg = lane >> 4;
   if constexpr (PACK8) l += dpp_ror8f<0xF>(l, l);  // add the block-1 part from lane h + 8
   l = wave_sum_xor_groups(l);
   if (lg == 0) {
@@ -134,88 +129,75 @@ __device__ __forceinline__ void merge_waves(const DecodeArgs& a, MergeLdsT<kTW>&
       for (int r = 0; r < 4; ++r) sh.acc[wave][col][32 * lg + 8 * r + mb] = acc[mb][r];
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64) {
-    const int h = idx >> 7, d = idx & (kD - 1);
-    float M = sh.m[0][h];
+  for (int h = wave; h < a.n_rep; h += kTW) {
+    float mw[kTW];
 #pragma unroll
-    for (int w = 1; w < kTW; ++w) M = fmaxf(M, sh.m[w][h]);
-    float num = 0.f, den = 0.f;
+    for (int w = 0; w < kTW; ++w) mw[w] = sh.m[w][h];
+    float M = mw[0];
+#pragma unroll
+    for (int w = 1; w < kTW; ++w) M = fmaxf(M, mw[w]);
+    float n0 = 0.f, n1 = 0.f, den = 0.f;
 #pragma unroll
     for (int w = 0; w < kTW; ++w) {
-      const float e = fast_exp2(sh.m[w][h] - M);
-      num = fmaf(e, sh.acc[w][h][d], num);
+      const float e = fast_exp2(mw[w] - M);
+      n0 = fmaf(e, sh.acc[w][h][2 * lane], n0);
+      n1 = fmaf(e, sh.acc[w][h][2 * lane + 1], n1);
       den = fmaf(e, sh.l[w][h], den);
     }
-    own.acc[h][d] = num;
-    if (d == 0) own.ml[h] = float2{M, den};
-  }
-  __syncthreads();
-}
-
-// Stores the work-group's partial for the merge of another work-group (write-through at
-// device scope: visible to any XCD once the store has completed).
-__device__ __forceinline__ void store_own(const DecodeArgs& a, const OwnPartial& own, int b,
-                                         int hkv, int chunk) {
-  for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64) {
-    const int h = idx >> 7, d = idx & (kD - 1);
     const int64_t pi = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks + chunk;
-    store_partial<true>(a.part_acc + pi * kD + d, own.acc[h][d]);
-    if (d == 0) {
-      store_partial<true>(&a.part_ml[pi].x, own.ml[h].x);
-      store_partial<true>(&a.part_ml[pi].y, own.ml[h].y);
-    }
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_acc + pi * kD + 2 * lane),
+                       __builtin_bit_cast(uint64_t, float2{n0, n1}), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_ml + pi),
+                         __builtin_bit_cast(uint64_t, float2{M, den}), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-// The last work-group's combine: its own partial (chunk `mine`) comes from LDS, the
-// others' from memory.
-__device__ __forceinline__ void combine_unit(const DecodeArgs& a, const OwnPartial& own, int b,
-                                             int hkv, int nvalid, int mine, int wave, int lane) {
+// The last work-group's merge of the nvalid chunk partials of each query head (its own
+// included, read back like the others), with combine_one's arithmetic.  Wave w takes heads
+// w, w + kTW, ..; lane l the (m, l) pair of chunk l and channels 2 l, 2 l + 1 of every
+// chunk.  The buffer resources end after the nvalid-th chunk, so the loads of chunks past
+// it read 0 without a branch; their weight is exp2(-inf) = 0.  Loads bypass the
+// non-coherent cache levels (sc1); chunks are added in chunk order whichever work-group
+// merges, so every call gives the same bits.  s, z: the V scale / zero-point of group
+// lane / 16.
+__device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv, int nvalid,
+                                             int wave, int lane, float s, float z) {
   static_assert(kUnitChunks <= 64, "one (m, l) pair per lane");
-  const int64_t row0 = ((int64_t)b * a.Hq + hkv * a.n_rep) * a.n_chunks;
-  const rsrc_t r = buffer_rsrc(a.part_acc + row0 * kD, (uint32_t)(a.n_rep * a.n_chunks * kD * 4));
-  const rsrc_t rml = buffer_rsrc(a.part_ml + row0, (uint32_t)(a.n_rep * a.n_chunks * 8));
-  const int g = lane >> 4;  // quantisation group of channels 2 lane, 2 lane + 1
-  const float s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
-  const float z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
   for (int h = wave; h < a.n_rep; h += kTW) {
-    const bool ok = lane < nvalid;
-    const bool ext = ok && lane != mine;
-    const u32x2 mlv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-        rml, (int)(ext ? (uint32_t)((h * a.n_chunks + lane) * 8) : kOutOfRange), 0, kBufSC1));
-    const uint32_t vbase = (uint32_t)((h * a.n_chunks * kD + 2 * lane) * 4);
+    const int64_t row = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks;
+    const rsrc_t rml = buffer_rsrc(a.part_ml + row, (uint32_t)nvalid * 8u);
+    const rsrc_t racc = buffer_rsrc(a.part_acc + row * kD, (uint32_t)nvalid * (kD * 4u));
+    const u32x2 mlv = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, (int)(lane * 8), 0, kBufSC1));
+    const uint32_t vbase = (uint32_t)lane * 8u;
     u32x2 av[kUnitBatch];
-    auto issue = [&](int c0) {
 #pragma unroll
-      for (int c = 0; c < kUnitBatch; ++c) {
-        const int cc = c0 + c;
-        const uint32_t voff =
-            (cc < nvalid && cc != mine) ? vbase + (uint32_t)(cc * kD * 4) : kOutOfRange;
-        av[c] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, 0, kBufSC1));
-      }
-    };
-    issue(0);
-    const float2 mo = own.ml[h];
-    const float mc = !ok ? kNegInf : (ext ? __builtin_bit_cast(float, (uint32_t)mlv.x) : mo.x);
-    const float lc = !ok ? 0.f : (ext ? __builtin_bit_cast(float, (uint32_t)mlv.y) : mo.y);
+    for (int c = 0; c < kUnitBatch; ++c)
+      av[c] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                            racc, (int)(vbase + (uint32_t)c * (kD * 4u)), 0, kBufSC1));
+    const float mc = lane < nvalid ? __builtin_bit_cast(float, (uint32_t)mlv.x) : kNegInf;
     const float M = wave_max64(mc);
-    const float e = ok ? fast_exp2(mc - M) : 0.f;
-    const float den = wave_sum64(e * lc);
-    // the chunks are added in chunk order whichever work-group merges (same bits every call)
-    const float o0 = own.acc[h][2 * lane], o1 = own.acc[h][2 * lane + 1];
+    const float e = fast_exp2(mc - M);
+    const float den = wave_sum64(e * __builtin_bit_cast(float, (uint32_t)mlv.y));
     float n0 = 0.f, n1 = 0.f;
     for (int c0 = 0; c0 < nvalid; c0 += kUnitBatch) {
-      if (c0 > 0) issue(c0);
+      if (c0 > 0) {
+#pragma unroll
+        for (int c = 0; c < kUnitBatch; ++c)
+          av[c] = __builtin_bit_cast(
+              u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                         racc, (int)(vbase + (uint32_t)(c0 + c) * (kD * 4u)), 0, kBufSC1));
+      }
 #pragma unroll
       for (int c = 0; c < kUnitBatch; ++c) {
-        // weight of chunk c0 + c (0 past nvalid), uniform
-        const float ec = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), c0 + c));
         // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of
         // an ext_vector element lvalue reads element 0 whatever the index
-        const bool is_own = c0 + c == mine;
-        n0 = fmaf(ec, is_own ? o0 : __builtin_bit_cast(float, (uint32_t)av[c].x), n0);
-        n1 = fmaf(ec, is_own ? o1 : __builtin_bit_cast(float, (uint32_t)av[c].y), n1);
+        const float ec = row_lane(e, c0 + c);
+        n0 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)av[c].x), n0);
+        n1 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)av[c].y), n1);
       }
     }
     const half2v o = {(half_t)fmaf(s, n0 / den - 72.0f, z), (half_t)fmaf(s, n1 / den - 1032.0f, z)};
@@ -306,14 +288,12 @@ struct KAsymT {
     }
   }
 
-  // q-dependent operands of this wave's channel slice, shared through LDS
-  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int wave, QShareLds& sh) {
+  // q-dependent operands of channel slice j = 0..3 (channels 32 lg + 8 j + e), shared
+  // through LDS; called by waves 0..3 only
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
     const int col = lane & 15, lg = lane >> 4;
     const bool valid = col < a.n_rep;
     const bool has_tau = a.inv_tau != nullptr;
-    // waves j < 4 build the operands of channels 32 lg + 8 j + e (waves 4..7 compute the
-    // same values as wave j - 4 and do not store them)
-    const int j = wave & 3;
     const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
     const float s = (float)in.s;
     const float z = (float)in.z;
@@ -338,13 +318,11 @@ struct KAsymT {
       part += qd * z - slot_offset(k) * ((float)hi + (float)lo);
     }
     part = wave_sum_xor_groups(part);
-    if (wave < 4) {
-      sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
-      sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
-      *reinterpret_cast<u32x4*>(&sh.qv[col][32 * lg + 8 * j]) =
-          __builtin_bit_cast(u32x4, half8v{qs[0], qs[1], qs[2], qs[3], qs[4], qs[5], qs[6], qs[7]});
-      if (lg == 0) sh.bias[j][col] = part;
-    }
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+    sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
+    *reinterpret_cast<u32x4*>(&sh.qv[col][32 * lg + 8 * j]) =
+        __builtin_bit_cast(u32x4, half8v{qs[0], qs[1], qs[2], qs[3], qs[4], qs[5], qs[6], qs[7]});
+    if (lg == 0) sh.bias[j][col] = part;
   }
 
   // after the work-group barrier: pick up the operands all four waves built
@@ -549,40 +527,6 @@ void decode_tiled_kernel(DecodeArgs a) {
   AppendIn ain;
   AppendFlags afl;
 
-  int64_t ctx64 = a.ctx[b];
-  ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);
-  const int ctx = (int)ctx64;
-  // The n_chunks work-groups of a (b, kv head) interleave: at step i the waves of all of
-  // them read one contiguous run of n_chunks * kTW tiles, so the device streams each
-  // slab front to back.  Wave w of work-group c takes tiles c*kTW + w + i*stride.
-  const int ntot = (ctx + kTile - 1) / kTile;
-  if (writer && (ntot == 0 || chunk * kTW >= ntot)) {
-    int4 oc = int4{0, 0, 0, 0};
-    if constexpr (OUT) {
-      const int4 o = *reinterpret_cast<const int4*>(a.k.oidx + hkv * 4);
-      oc = int4{min(max(o.x, 0), kD - 1), min(max(o.y, 0), kD - 1), min(max(o.z, 0), kD - 1),
-                min(max(o.w, 0), kD - 1)};
-    }
-    append_fetch<OUT>(a, b, hkv, lane, true, oc, ain);
-    KAsymT<OUT> k0;
-    k0.setup_addr(a, b, hkv, lane);
-    VAsymT v0;
-    v0.setup(a, b, hkv, lane);
-    const int g = lane >> 4;
-    append_store<OUT>(a, k0.rk, v0.rv, k0.ro, lane, true, ain,
-                      (float)reinterpret_cast<const half_t*>(a.k.scale)[hkv * a.k.ssh + g * a.k.ssg],
-                      (float)a.k.zp[hkv * a.k.ssh + g * a.k.ssg], afl);
-    if (lane == 0) append_status(a.app, afl);
-  }
-  if (ntot == 0) {  // empty context: the first work-group writes zero rows
-    if (chunk == 0 && a.fused)
-      for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
-        a.out[(int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + (idx >> 7)) * a.o_sh +
-              (idx & (kD - 1))] = (half_t)0.0f;
-    return;
-  }
-  if (chunk * kTW >= ntot) return;  // no tile for this work-group (uniform)
-
   __shared__ QShareLds qsh;
   __shared__ MergeLdsT<kTW> msh;
   // Waves w and w + 4 share a SIMD, which issues the older of two ready waves first;
@@ -606,7 +550,6 @@ void decode_tiled_kernel(DecodeArgs a) {
   // The schedule is static, so results do not depend on timing.
   const int first = chunk * kTW + wave;
   const int stride = a.n_chunks * kTW;
-  const bool partial = (ctx & (kTile - 1)) != 0;
   // tile[j] = tile of step i + j (j <= LOOK + 1)
   int tile[LOOK + 2];
 #pragma unroll
@@ -616,20 +559,42 @@ void decode_tiled_kernel(DecodeArgs a) {
   typename KAsymT<OUT>::Raw kr[R];
   VAsymT::Raw vr[R];
   // K tiles of steps 0..LOOK and V tiles of steps 0..LOOK-1 are requested before the q
-  // set-up, so the memory system is busy from the start of the kernel.  Every ring load is
-  // issued unconditionally (out of range for a tile past the context): conditional loads
-  // would make the compiler's vmcnt waits conservative at the joins, i.e. wait for the
-  // tiles just requested.
+  // set-up and before the context length is known (bounded by the capacity; tiles past
+  // the context are never used), so the memory system is busy from the start of the
+  // kernel.  Every ring load is issued unconditionally (out of range for a tile past the
+  // bound): conditional loads would make the compiler's vmcnt waits conservative at the
+  // joins, i.e. wait for the tiles just requested.
   asm volatile("" ::: "memory");
   const bool early_write = writer && wt / stride_all <= LOOK;
   if (early_write) {
     append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
     append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
   }
+  const int ncap = (a.cap + kTile - 1) / kTile;
 #pragma unroll
   for (int s = 0; s <= LOOK; ++s) {
-    kf.load(kTile * tile[s], tile[s] < ntot, kr[s]);
-    if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ntot, vr[s]);
+    kf.load(kTile * tile[s], tile[s] < ncap, kr[s]);
+    if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ncap, vr[s]);
+  }
+
+  int64_t ctx64 = a.ctx[b];
+  ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);
+  const int ctx = (int)ctx64;
+  const int ntot = (ctx + kTile - 1) / kTile;
+  const bool partial = (ctx & (kTile - 1)) != 0;
+  if (ntot == 0 || chunk * kTW >= ntot) {  // no tile for this work-group (uniform)
+    if (writer) {
+      if (!early_write) {
+        append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
+        append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
+      }
+      if (lane == 0) append_status(a.app, afl);
+    }
+    if (ntot == 0 && chunk == 0 && a.fused)  // empty context: zero rows
+      for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
+        a.out[(int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + (idx >> 7)) * a.o_sh +
+              (idx & (kD - 1))] = (half_t)0.0f;
+    return;
   }
   // The writer fetches the new rows now and stores their codes in the loop, at the last
   // step that precedes its loads of tile wt (step wt_step - LOOK - 1), or right after the
@@ -638,7 +603,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   const int wt_step = (wt - (chunk * kTW + wave)) / stride_all;
   const int store_step = late_write ? wt_step - LOOK - 1 : -1;
   if (late_write) append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
-  kf.setup_q(a, qin, lane, wave, qsh);
+  if (wave < 4) kf.setup_q(a, qin, lane, wave, qsh);  // waves 4..7 would build the same
   NibConsts nc;
   nc.init();
   __syncthreads();
@@ -698,14 +663,18 @@ void decode_tiled_kernel(DecodeArgs a) {
   // Merge.  The waves' states are merged in LDS and the work-group's partial is stored
   // write-through (combine_kernel merges them when a.fused == 0).  Once every store of the
   // work-group has completed, one thread counts it in (word 0 of the (b, kv head)'s
-  // counter slot); the last of the (b, kv head)'s work-groups merges every partial, its
-  // own from LDS, writes the output and resets the counter.
+  // counter slot); the last of the (b, kv head)'s work-groups merges every partial, writes
+  // the output and resets the counter.
   const int nvalid = valid_chunks(a, ctx);
   uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
-  __shared__ OwnPartial own;
   __shared__ int is_last;
-  merge_waves<PACK8>(a, msh, own, wave, col, lg, m, l, acc);
-  store_own(a, own, b, hkv, chunk);
+  float vs = 0.f, vz = 0.f;
+  if (a.fused) {  // V scale / zero-point of group lane / 16, for the output (requested early)
+    const int g = lane >> 4;
+    vs = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
+    vz = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
+  }
+  merge_store_partial<PACK8>(a, msh, wave, lane, m, l, acc, b, hkv, chunk);
   if (!a.fused) return;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -713,12 +682,13 @@ void decode_tiled_kernel(DecodeArgs a) {
     is_last = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nvalid - 1);
   __syncthreads();
   if (!is_last) return;
-  combine_unit(a, own, b, hkv, nvalid, chunk, wave, lane);
+  merge_chunks(a, b, hkv, nvalid, wave, lane, vs, vz);
   if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <bool OUT, bool PACK8>
 const void* tiled_ptr(int look) {
+  if (look == 3) return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 3, PACK8>);
   if (look == 2) return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 2, PACK8>);
   return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 1, PACK8>);
 }
@@ -729,7 +699,7 @@ int tiled_look() {
   static int d = [] {
     const char* e = getenv("KVQ_TILED_LOOK");
     const int v = e ? atoi(e) : 1;
-    return (v == 1 || v == 2) ? v : 1;
+    return (v >= 1 && v <= 3) ? v : 1;
   }();
   return d;
 }
@@ -737,7 +707,9 @@ int tiled_look() {
 template <bool OUT, bool PACK8>
 void launch_one(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   const dim3 block(kTW * 64);
-  if (tiled_look() == 2)
+  if (tiled_look() == 3)
+    hipLaunchKernelGGL((decode_tiled_kernel<OUT, 3, PACK8>), grid, block, 0, s, a);
+  else if (tiled_look() == 2)
     hipLaunchKernelGGL((decode_tiled_kernel<OUT, 2, PACK8>), grid, block, 0, s, a);
   else
     hipLaunchKernelGGL((decode_tiled_kernel<OUT, 1, PACK8>), grid, block, 0, s, a);
