@@ -178,19 +178,15 @@ __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv
     for (int c = 0; c < kUnitBatch; ++c)
       av[c] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
                                             racc, (int)(vbase + (uint32_t)c * (kD * 4u)), 0, kBufSC1));
+    // every load of the first batch is issued before the (m, l) pair is used (one memory
+    // latency, not two)
+    asm volatile("" ::: "memory");
     const float mc = lane < nvalid ? __builtin_bit_cast(float, (uint32_t)mlv.x) : kNegInf;
     const float M = wave_max64(mc);
     const float e = fast_exp2(mc - M);
     const float den = wave_sum64(e * __builtin_bit_cast(float, (uint32_t)mlv.y));
     float n0 = 0.f, n1 = 0.f;
-    for (int c0 = 0; c0 < nvalid; c0 += kUnitBatch) {
-      if (c0 > 0) {
-#pragma unroll
-        for (int c = 0; c < kUnitBatch; ++c)
-          av[c] = __builtin_bit_cast(
-              u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                         racc, (int)(vbase + (uint32_t)(c0 + c) * (kD * 4u)), 0, kBufSC1));
-      }
+    for (int c0 = 0;;) {
 #pragma unroll
       for (int c = 0; c < kUnitBatch; ++c) {
         // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of
@@ -199,6 +195,13 @@ __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv
         n0 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)av[c].x), n0);
         n1 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)av[c].y), n1);
       }
+      c0 += kUnitBatch;
+      if (c0 >= nvalid) break;
+#pragma unroll
+      for (int c = 0; c < kUnitBatch; ++c)
+        av[c] = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                       racc, (int)(vbase + (uint32_t)(c0 + c) * (kD * 4u)), 0, kBufSC1));
     }
     const half2v o = {(half_t)fmaf(s, n0 / den - 72.0f, z), (half_t)fmaf(s, n1 / den - 1032.0f, z)};
     *reinterpret_cast<half2v*>(a.out + (int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + h) * a.o_sh +
