@@ -561,12 +561,15 @@ void decode_tiled_kernel(DecodeArgs a) {
   constexpr int U = (R % 2 == 0) ? R : 2 * R;  // unroll: ring slot and x buffer are static
   typename KAsymT<OUT>::Raw kr[R];
   VAsymT::Raw vr[R];
-  // K tiles of steps 0..LOOK and V tiles of steps 0..LOOK-1 are requested before the q
-  // set-up and before the context length is known (bounded by the capacity; tiles past
-  // the context are never used), so the memory system is busy from the start of the
-  // kernel.  Every ring load is issued unconditionally (out of range for a tile past the
-  // bound): conditional loads would make the compiler's vmcnt waits conservative at the
-  // joins, i.e. wait for the tiles just requested.
+  // The K and V tiles of step 0 are requested before the q set-up and before the context
+  // length is known (bounded by the capacity; tiles past the context are never used), so
+  // the memory system is busy from the start of the kernel; the rest of the ring (K of
+  // steps 1..LOOK, V of steps 1..LOOK-1) after the set-up.  A larger first burst delays
+  // the q loads queued with it, and the set-up waits for those (measured: the whole ring
+  // up front costs about 0.4 us per launch at the headline shape).  Every ring load is
+  // issued unconditionally (out of range for a tile past the bound): conditional loads
+  // would make the compiler's vmcnt waits conservative at the joins, i.e. wait for the
+  // tiles just requested.
   asm volatile("" ::: "memory");
   const bool early_write = writer && wt / stride_all <= LOOK;
   if (early_write) {
@@ -574,11 +577,8 @@ void decode_tiled_kernel(DecodeArgs a) {
     append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
   }
   const int ncap = (a.cap + kTile - 1) / kTile;
-#pragma unroll
-  for (int s = 0; s <= LOOK; ++s) {
-    kf.load(kTile * tile[s], tile[s] < ncap, kr[s]);
-    if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ncap, vr[s]);
-  }
+  kf.load(kTile * tile[0], tile[0] < ncap, kr[0]);
+  vf.load(kTile * tile[0], tile[0] < ncap, vr[0]);
 
   int64_t ctx64 = a.ctx[b];
   ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);
@@ -610,6 +610,11 @@ void decode_tiled_kernel(DecodeArgs a) {
   NibConsts nc;
   nc.init();
   __syncthreads();
+#pragma unroll
+  for (int s = 1; s <= LOOK; ++s) {
+    kf.load(kTile * tile[s], tile[s] < ntot, kr[s]);
+    if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ntot, vr[s]);
+  }
   kf.finish_setup(qsh, qin, lane);
   // (wt past the context: the wave may have fewer steps than store_step)
   const bool store_now = late_write && (wt >= ntot || store_step <= 0);
