@@ -26,14 +26,15 @@
 //    one dword load of the whole wave: lane (row, g) takes the channel pair g & 1 of
 //    token 16 (g >> 1) + row, which is where the outlier MFMA of row block g >> 1
 //    needs it.
-//  * A packed dword becomes 8 fp16 operands with 5 ops: v_and_or_b32 with the masks
-//    0x00F000F0 (high nibbles of bytes 0 and 2 -> 64 + n) and 0x000F000F (low nibbles
-//    -> 1024 + n), then the same on the dword shifted right by 8 (bytes 1 and 3).
-//    The two offsets are exact in fp16 and are removed in the bias (K) or the
-//    epilogue (V): channel offsets 72 = 64 + 8 and 1032 = 1024 + 8.
-//  * The q-dependent operands (q * s split into fp16 hi + lo, the bias) are built once
-//    per work-group and shared through LDS; the q loads are issued before the first
-//    cache loads.  The lo halves are read from LDS at every tile (fewer VGPRs).
+//  * A packed dword becomes 8 fp16 operands with 5 ops.  K: v_and_b32 with the masks
+//    0x00F000F0 (high nibbles of bytes 0 and 2 -> the subnormal 16 n * 2^-24) and
+//    0x000F000F (low nibbles -> n * 2^-24), then the same on the dword shifted right by 8
+//    (bytes 1 and 3); the q side is one fp16 operand per channel and the logits come out
+//    scaled by 2^-24.  V: v_and_or_b32 with the same masks and the magics 0x5400 / 0x6400
+//    (64 + n and 1024 + n); those offsets (72 = 64 + 8 and 1032 = 1024 + 8 with the code
+//    offset) are removed in the epilogue, where they cancel exactly against l.
+//  * The q-dependent operands (fp16(q * s), the bias) are built once per work-group and
+//    shared through LDS; the q loads are issued before the first cache loads.
 //  * K and V tiles are fetched LOOK steps ahead of their use (register rings of
 //    LOOK + 1 tiles); QK of tile i + 1 is issued before softmax / PV of tile i.
 //  * With at most kUnitChunks chunks per (b, kv head) the last work-group to finish
@@ -210,23 +211,25 @@ __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv
 }
 
 // 8 packed codes -> 8 fp16 operands in k-slot order [e0, e4, e1, e5, e2, e6, e3, e7]
-// (e = element within the dword; byte k holds e = 2k in its high nibble), valued
-// 64 + n for even e and 1024 + n for odd e.
-__device__ __forceinline__ half8v unpack5(uint32_t w, const NibConsts& nc) {
+// (e = element within the dword; byte k holds e = 2k in its high nibble), read as fp16
+// subnormals: a nibble in bits 4..7 of a 16-bit half is 16 n * 2^-24, one in bits 0..3 is
+// n * 2^-24, both exact.  The MFMA takes subnormal fp16 inputs without flushing them, and
+// with no offset in the operand the q side needs a single fp16 operand (a product q * s
+// rounded to fp16 perturbs each term by at most 2^-11 of itself).  5 ops per 8 codes.
+__device__ __forceinline__ half8v unpack_sub(uint32_t w, const NibConsts& nc) {
   const uint32_t w8 = w >> 8;
-  return pack8(and_or(w, nc.m_hi, nc.c64), and_or(w, nc.m_lo, nc.c1024),
-               and_or(w8, nc.m_hi, nc.c64), and_or(w8, nc.m_lo, nc.c1024));
+  return pack8(w & nc.m_hi, w & nc.m_lo, w8 & nc.m_hi, w8 & nc.m_lo);
 }
 __host__ __device__ constexpr int slot_elem(int k) { return (k & 1) * 4 + (k >> 1); }
-__host__ __device__ constexpr float slot_offset(int k) {  // operand offset + code offset 8
-  return ((k >> 1) & 1) ? 1032.0f : 72.0f;
-}
+// k-slots holding a high nibble (operand value 16 n * 2^-24)
+__host__ __device__ constexpr bool slot_high(int k) { return ((k >> 1) & 1) == 0; }
+constexpr float kTwo24 = 16777216.0f;       // 2^24
+constexpr float kTwoM24 = 5.9604644775390625e-8f;  // 2^-24
 
 // LDS through which the 4 waves share the q-dependent K operands, and the scaled q rows
 // from which the outlier operand is gathered
 struct QShareLds {
   u32x4 qh[4][64];
-  u32x4 ql[4][64];
   float bias[4][16];
   half_t qv[16][kD];  // q' of head column c (zero for padding columns)
 };
@@ -242,12 +245,13 @@ struct QIn {
 };
 
 // INT4 asymmetric K with static scale s / zero-point z per (kv head, group of 32).  With
-// x = off + n and code c = n - 8 the logit is
-//   sum_d q_d (s c_d + z) = sum_d (q_d s) x_d + sum_d q_d (z - (off_d + 8) s),
-// q_d s is split exactly into fp16 hi + lo (both go through the MFMA) and the constant
-// term is the accumulator's initial value.  Outlier channels (q zeroed in the main
-// MFMAs) are added by one MFMA of the same shape whose operands are the 4 fp16
-// outlier values and q' of those channels in the first two k-slots of each lane group.
+// code c = n - 8 the logit is
+//   sum_d q_d (s c_d + z) = sum_d (q_d s) n_d + sum_d q_d (z - 8 s);
+// the codes enter the MFMA as subnormals n * 2^-24 (16 n * 2^-24 for high nibbles, whose
+// q operand is divided by 16), q_d s rounded to fp16 is the other operand, and the
+// constant term starts the accumulator.  Outlier channels (q zeroed in the main MFMAs)
+// are added by one MFMA of the same shape whose operands are the 4 fp16 outlier values
+// and q' of those channels in the first two k-slots of each lane group.
 template <bool OUT>
 struct KAsymT {
   half8v qh[4];
@@ -292,7 +296,10 @@ struct KAsymT {
   }
 
   // q-dependent operands of channel slice j = 0..3 (channels 32 lg + 8 j + e), shared
-  // through LDS; called by waves 0..3 only
+  // through LDS; called by waves 0..3 only.  Operand k = fp16(q'_d s) (fp16(q'_d s / 16) for a
+  // high-nibble slot) multiplies n_d * 2^-24 (16 n_d * 2^-24), so the MFMA sums
+  // e_d n_d * 2^-24 with e_d = the operand's value (x 16 for a high nibble), and
+  //   logit = sum_d q'_d (s c_d + z) = 2^24 * mfma + sum_d (q'_d z - 8 e_d)  (c = n - 8).
   __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
     const int col = lane & 15, lg = lane >> 4;
     const bool valid = col < a.n_rep;
@@ -301,7 +308,7 @@ struct KAsymT {
     const float s = (float)in.s;
     const float z = (float)in.z;
     float part = 0.f;
-    half_t vh[8], vl[8], qs[8];
+    half_t vh[8], qs[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const half2v h2 = as_h2(qw[e >> 1]);
@@ -314,15 +321,12 @@ struct KAsymT {
       const bool use = d != in.oc.x && d != in.oc.y && d != in.oc.z && d != in.oc.w;
       const float qd = use ? (float)qs[e] : 0.f;
       const float P = qd * s;  // exact: 11-bit x 11-bit significands
-      const half_t hi = (half_t)P;
-      const half_t lo = (half_t)(P - (float)hi);
-      vh[k] = hi;
-      vl[k] = lo;
-      part += qd * z - slot_offset(k) * ((float)hi + (float)lo);
+      const half_t h = (half_t)(slot_high(k) ? P * 0.0625f : P);
+      vh[k] = h;
+      part += qd * z - 8.0f * (slot_high(k) ? 16.0f * (float)h : (float)h);
     }
     part = wave_sum_xor_groups(part);
     sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
-    sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
     *reinterpret_cast<u32x4*>(&sh.qv[col][32 * lg + 8 * j]) =
         __builtin_bit_cast(u32x4, half8v{qs[0], qs[1], qs[2], qs[3], qs[4], qs[5], qs[6], qs[7]});
     if (lg == 0) sh.bias[j][col] = part;
@@ -353,27 +357,34 @@ struct KAsymT {
     if constexpr (OUT) r.o = bload1(ro, vo + (valid ? (uint32_t)tok * kRowO : kOutOfRange), 0);
   }
 
-  // logits of the tile's two 16-token row blocks (x0: tokens 4 lg + r, x1: 16 + 4 lg + r).
-  // The lo halves of q * s are read from LDS at every tile (16 VGPRs fewer); qlo is the
-  // lane's byte offset into them, made opaque by the caller so the reads stay in the loop.
-  __device__ __forceinline__ void qk(const Raw& r, const QShareLds& sh, uint32_t qlo,
-                                     const NibConsts& nc, float4v& x0, float4v& x1) const {
-    float4v c0 = {bias, bias, bias, bias};
-    float4v c1 = c0;
+  // logits of the tile's two 16-token row blocks (x0: tokens 4 lg + r, x1: 16 + 4 lg + r),
+  // scaled by 2^-24 (the softmax multiplies by sm * 2^24).  The outlier channels go through
+  // a separate accumulator at unit scale, started at the bias, and are added at the end.
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    float4v c0, c1;
     if constexpr (OUT) {
-      c0 = mfma16x16x32(pack8(olo ? r.o : 0u, 0u, 0u, 0u), qo, c0);
-      c1 = mfma16x16x32(pack8(olo ? 0u : r.o, 0u, 0u, 0u), qo, c1);
+      c0 = float4v{0.f, 0.f, 0.f, 0.f};
+      c1 = c0;
+    } else {
+      const float b24 = bias * kTwoM24;
+      c0 = float4v{b24, b24, b24, b24};
+      c1 = c0;
     }
-    const char* qlb = reinterpret_cast<const char*>(&sh.ql[0][0]) + qlo;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const half8v lo = __builtin_bit_cast(half8v, *reinterpret_cast<const u32x4*>(qlb + j * 64 * 16));
-      const half8v A0 = unpack5(r.w[0][j], nc);
-      const half8v A1 = unpack5(r.w[1][j], nc);
-      c0 = mfma16x16x32(A0, qh[j], c0);
-      c1 = mfma16x16x32(A1, qh[j], c1);
-      c0 = mfma16x16x32(A0, lo, c0);
-      c1 = mfma16x16x32(A1, lo, c1);
+      c0 = mfma16x16x32(unpack_sub(r.w[0][j], nc), qh[j], c0);
+      c1 = mfma16x16x32(unpack_sub(r.w[1][j], nc), qh[j], c1);
+    }
+    if constexpr (OUT) {
+      const float4v b4 = {bias, bias, bias, bias};
+      const float4v o0 = mfma16x16x32(pack8(olo ? r.o : 0u, 0u, 0u, 0u), qo, b4);
+      const float4v o1 = mfma16x16x32(pack8(olo ? 0u : r.o, 0u, 0u, 0u), qo, b4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c0[i] = fmaf(o0[i], kTwoM24, c0[i]);
+        c1[i] = fmaf(o1[i], kTwoM24, c1[i]);
+      }
     }
     x0 = c0;
     x1 = c1;
@@ -625,11 +636,11 @@ void decode_tiled_kernel(DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
   float m = kNegInf, l = 0.f;
-  const float sm = a.sm_log2e;
+  const float sm = a.sm_log2e * kTwo24;  // the logits arrive scaled by 2^-24
   int steps = 0;
   if (tile[0] < ntot) {
     float4v x[2][2];
-    kf.qk(kr[0], qsh, (uint32_t)lane * 16u, nc, x[0][0], x[0][1]);
+    kf.qk(kr[0], nc, x[0][0], x[0][1]);
     while (tile[0] < ntot) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -643,11 +654,7 @@ void decode_tiled_kernel(DecodeArgs a) {
         // and PV of step i
         kf.load(kTile * tile[LOOK + 1], tile[LOOK + 1] < ntot, kr[u % R]);
         vf.load(kTile * tile[LOOK], tile[LOOK] < ntot, vr[(u + LOOK) % R]);
-        if (tile[1] < ntot) {
-          uint32_t qlo = (uint32_t)lane * 16u;
-          asm volatile("" : "+v"(qlo));
-          kf.qk(kr[(u + 1) % R], qsh, qlo, nc, x[(u + 1) & 1][0], x[(u + 1) & 1][1]);
-        }
+        if (tile[1] < ntot) kf.qk(kr[(u + 1) % R], nc, x[(u + 1) & 1][0], x[(u + 1) & 1][1]);
         float4v x0 = x[u & 1][0], x1 = x[u & 1][1];
         if (partial && tile[0] == ntot - 1) mask_tile(x0, x1, kTile * tile[0], ctx, lg);
         half8v pb;
