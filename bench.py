@@ -95,14 +95,17 @@ class Layer:
         self.C = C
         B, Hkv, Hq = cfg.batch, cfg.kv_heads, cfg.q_heads
         cap = int(max(ctx))
+        if cfg.v_format != "int8":
+            cap = -(-cap // 32) * 32  # TILE32 V holds whole 32-token tiles
         t = SY.calibrate(cfg, layer % cfg.layers)
         self.tables = t
         ch = SY.outlier_channels(cfg, layer % cfg.layers)
         kb = 128 if cfg.k_format == "int8" else 64
         vb = 128 if cfg.v_format == "int8" else 64
         self.k = torch.empty(B, Hkv, cap, kb, dtype=torch.uint8, device=device)
-        # V of the all-INT4-asymmetric formats in the TILE32 layout, as INT4AsymKVCache keeps it
-        self.v_tiled = cfg.k_format != "int8" and cfg.v_format != "int8"
+        # asymmetric INT4 V in the TILE32 layout (as INT4AsymKVCache keeps it), which the
+        # tiled kernels read with INT4-asymmetric or static INT8 K
+        self.v_tiled = cfg.v_format != "int8"
         if self.v_tiled:
             assert cap % 32 == 0
             self.v = torch.empty(B, Hkv, cap // 32, 2048, dtype=torch.uint8, device=device)
@@ -151,7 +154,7 @@ class Layer:
         self.plan = DecodePlan(self.q, kfmt, kview, vfmt, vview, self.ctx, Hkv, cap,
                                1.0 / math.sqrt(128), 32, inv_tau=self.inv_tau, chunk_tokens=chunk)
         # INT4-asymmetric K and TILE32 V: kvq_append_decode_attn does the step in one launch
-        self.fused = self.v_tiled
+        self.fused = self.v_tiled and cfg.k_format != "int8"
 
     def _append_params(self, cfg, kx, vx, pos):
         C = self.C
@@ -264,14 +267,15 @@ def copy_probe(device, nbytes=1 << 30, reps=3):
 
 
 def attention_kernels(cfg, layer):
-    """Kernels one kvq_decode_attn call launches for this configuration: the tiled kernel
-    merges its chunk partials itself when it runs at most 64 chunks per (b, kv head) and
-    at most 8 query heads per kv head; otherwise a combine launch follows."""
+    """Kernels one kvq_decode_attn call launches for this configuration: the tiled kernels
+    (TILE32 V, or static-scale INT8 K) merge their chunk partials themselves when they run
+    at most 64 chunks per (b, kv head); otherwise a combine launch follows."""
     p = layer.plan.params
     n_chunks = -(-int(p.capacity) // int(layer.plan.chunk_tokens))
-    if layer.v_tiled and n_chunks <= 64 and cfg.q_heads // cfg.kv_heads <= 8:
+    tiled = layer.v_tiled or cfg.k_format == "int8"  # static-scale INT8 K: tiled family too
+    if tiled and n_chunks <= 64:
         return "decode_tiled_kernel (single launch, merge in the last work-group)"
-    return ("decode_tiled_kernel" if layer.v_tiled else "decode_splitk_kernel") + " + combine_kernel"
+    return ("decode_tiled_kernel" if tiled else "decode_splitk_kernel") + " + combine_kernel"
 
 
 def measured_traffic(cfg_index):

@@ -598,22 +598,46 @@ static int64_t resident_slots(const void* fn, int threads) {
   return slots;
 }
 
+// The tiled kernel family that serves p, or kTiledNone (a row-layout kernel then does):
+// INT4_ASYM K with TILE32 V, or INT8 K with a static scale (a view with stride 0 over b and t)
+// and dense 128-byte rows, with TILE32 INT4_ASYM V or static-scale INT8 V in dense rows.
+static int tiled_family(const kvq_decode_params* p) {
+  const bool vt = p->v.layout == KVQ_LAYOUT_TILE32;
+  if (p->k_format == KVQ_FMT_INT4_ASYM)
+    return (p->v_format == KVQ_FMT_INT4_ASYM && vt) ? (p->k.n_outlier > 0 ? kTiledA4A4o : kTiledA4A4)
+                                                     : kTiledNone;
+  const bool k8 = p->k_format == KVQ_FMT_INT8_SYM && p->group_size == kTile &&
+                  p->k.scale_stride_b == 0 && p->k.scale_stride_t == 0 && p->k.stride_t == kD;
+  if (!k8) return kTiledNone;
+  if (p->v_format == KVQ_FMT_INT4_ASYM && vt) return kTiledI8A4;
+  if (p->v_format == KVQ_FMT_INT8_SYM && !vt && p->v.scale_stride_b == 0 &&
+      p->v.scale_stride_t == 0 && p->v.stride_t == kD)
+    return kTiledI8I8;
+  return kTiledNone;
+}
+
 // the split-K kernel kvq_decode_attn launches for p (nullptr if unsupported)
 static const void* kernel_for(const kvq_decode_params* p) {
-  if (p->v.layout == KVQ_LAYOUT_TILE32)
-    return tiled_kernel(p->k_format, p->k.n_outlier > 0, p->q_heads / p->kv_heads);
+  const int fam = tiled_family(p);
+  if (fam != kTiledNone) return tiled_kernel(fam, p->q_heads / p->kv_heads);
+  if (p->v.layout == KVQ_LAYOUT_TILE32) return nullptr;
   return select_kernel(family(p->k_format, p->v_format, p->k.scale_dtype == KVQ_DTYPE_F32,
                               p->v.scale_dtype == KVQ_DTYPE_F32, p->k.n_outlier > 0));
 }
 
 // waves per work-group of the split-K kernel kvq_decode_attn launches for p
 static int waves_for(const kvq_decode_params* p) {
-  return p->v.layout == KVQ_LAYOUT_TILE32 ? kTiledWaves : kWaves;
+  return tiled_family(p) != kTiledNone ? kTiledWaves : kWaves;
 }
 
 // Tokens per work-group: fill every resident work-group slot exactly once when the
 // context is long enough (one wave of work-groups, no tail), in multiples of the
-// waves x 32 tokens one pass of the work-group covers, never below kMinChunk.
+// waves x 32 tokens one pass of the work-group covers, never below kMinChunk.  The tiled
+// kernels cap it at kTiledMaxTiles tiles per wave: with many (b, kv head) units or ragged
+// contexts that gives more, shorter work-groups, which the dispatcher spreads over the CUs
+// (work-groups past a short context exit at once).  Measured on MI355X: 16 tiles per wave
+// is the best split at configs 2, 3 (uniform 32k contexts) and 4 (ragged 4k-64k).
+constexpr int kTiledMaxTiles = 16;
 int32_t choose_chunk(const kvq_decode_params* p) {
   if (p->chunk_tokens > 0) return p->chunk_tokens;
   const int64_t units = (int64_t)p->batch * p->kv_heads;
@@ -624,6 +648,8 @@ int32_t choose_chunk(const kvq_decode_params* p) {
   if (per_unit < 1) per_unit = 1;
   int64_t c = (p->capacity + per_unit - 1) / per_unit;
   c = ((c + kTile * nw - 1) / (kTile * nw)) * (kTile * nw);
+  if (tiled_family(p) != kTiledNone && c > (int64_t)kTiledMaxTiles * nw * kTile)
+    c = (int64_t)kTiledMaxTiles * nw * kTile;
   if (c < kMinChunk) c = kMinChunk;
   const int64_t min_for_cap = (p->capacity + kMaxChunks - 1) / kMaxChunks;
   if (c < min_for_cap) c = ((min_for_cap + kTile - 1) / kTile) * kTile;
@@ -756,10 +782,13 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   if (fam == kNone)
     return fail(KVQ_ERR_UNSUPPORTED,
                 "unsupported (k_format, v_format) pair or mixed K/V scale dtypes");
-  const bool tiled = p->v.layout == KVQ_LAYOUT_TILE32;
-  if (tiled && !tiled_kernel(kf, p->k.n_outlier > 0, n_rep))
-    return fail(KVQ_ERR_UNSUPPORTED, "TILE32 V is supported with INT4_ASYM K only");
-  if (tiled && (p->k.stride_t != kD / 2 || (p->k.n_outlier && p->k.outlier_stride_t != 4)))
+  const int tfam = tiled_family(p);
+  const bool tiled = tfam != kTiledNone;
+  if (p->v.layout == KVQ_LAYOUT_TILE32 && !tiled)
+    return fail(KVQ_ERR_UNSUPPORTED,
+                "TILE32 V needs INT4_ASYM K or INT8 K with a static group-32 scale in dense rows");
+  if (tiled && p->k_format == KVQ_FMT_INT4_ASYM &&
+      (p->k.stride_t != kD / 2 || (p->k.n_outlier && p->k.outlier_stride_t != 4)))
     return fail(KVQ_ERR_UNSUPPORTED, "with TILE32 V, K rows and outlier rows must be dense");
   // buffer loads address each (b, head) slab with 32-bit byte offsets
   if (tiled && (p->capacity + kTile) * p->k.stride_t >= ((int64_t)1 << 31))
@@ -804,21 +833,18 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
 
   a.app = FusedAppend{};
   if (app) {
-    if (!tiled) return fail(KVQ_ERR_UNSUPPORTED, "fused append needs the TILE32 V layout");
+    if (tfam != kTiledA4A4 && tfam != kTiledA4A4o)
+      return fail(KVQ_ERR_UNSUPPORTED, "fused append needs INT4_ASYM K and TILE32 V");
     a.app = *app;
   }
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   a.fused = tiled && nch64 <= kUnitChunks;
   if (tiled) {
-    launch_tiled(a, kf, p->k.n_outlier > 0,
-                 dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch), s);
-    if (a.fused) {  // one launch: the last work-group of each (b, kv head) merged
-      const hipError_t e = hipGetLastError();
-      if (e != hipSuccess)
-        return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
-      return KVQ_OK;
-    }
+    const hipError_t e =
+        launch_tiled(a, tfam, dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch), s);
+    if (e != hipSuccess) return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
+    if (a.fused) return KVQ_OK;  // one launch: the last work-group of each (b, kv head) merged
   } else if (p->capacity > 0) {
     const dim3 grid((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch);
     switch (fam) {

@@ -320,9 +320,17 @@ __device__ __forceinline__ void combine_one(const DecodeArgs& a, int b, int hq, 
 // ---- host side (decode_attn.hip)
 int fail(int code, const std::string& msg);
 
-// ---- tiled-V kernels (decode_tiled.hip)
-// kernel of the tiled family for K format kf (kout: outlier channels), or nullptr
-const void* tiled_kernel(int kf, int kout, int n_rep);
-void launch_tiled(const DecodeArgs& a, int kf, int kout, dim3 grid, hipStream_t s);
+// ---- tiled kernels (decode_tiled.hip): 8-wave work-groups, interleaved 32-token tiles,
+// single-launch merge.  Format families:
+enum TiledFam {
+  kTiledNone = 0,
+  kTiledA4A4,   // INT4_ASYM K, INT4_ASYM V in the TILE32 layout
+  kTiledA4A4o,  // the same with 4 fp16 outlier K channels
+  kTiledI8A4,   // INT8_SYM K (static scale), INT4_ASYM V in the TILE32 layout
+  kTiledI8I8,   // INT8_SYM K and V (static scales), token rows
+};
+// kernel of family fam for n_rep query heads per kv head, or nullptr
+const void* tiled_kernel(int fam, int n_rep);
+hipError_t launch_tiled(const DecodeArgs& a, int fam, dim3 grid, hipStream_t s);
 
 }  // namespace kvq

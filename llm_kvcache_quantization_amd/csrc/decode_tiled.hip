@@ -164,6 +164,7 @@ __device__ __forceinline__ void merge_store_partial(const DecodeArgs& a, MergeLd
 // non-coherent cache levels (sc1); chunks are added in chunk order whichever work-group
 // merges, so every call gives the same bits.  s, z: the V scale / zero-point of group
 // lane / 16.
+template <class VF>
 __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv, int nvalid,
                                              int wave, int lane, float s, float z) {
   static_assert(kUnitChunks <= 64, "one (m, l) pair per lane");
@@ -204,7 +205,7 @@ __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv
             u32x2, __builtin_amdgcn_raw_buffer_load_b64(
                        racc, (int)(vbase + (uint32_t)(c0 + c) * (kD * 4u)), 0, kBufSC1));
     }
-    const half2v o = {(half_t)fmaf(s, n0 / den - 72.0f, z), (half_t)fmaf(s, n1 / den - 1032.0f, z)};
+    const half2v o = VF::epilogue(n0 / den, n1 / den, s, z);
     *reinterpret_cast<half2v*>(a.out + (int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + h) * a.o_sh +
                                2 * lane) = o;
   }
@@ -254,6 +255,9 @@ struct QIn {
 // and q' of those channels in the first two k-slots of each lane group.
 template <bool OUT>
 struct KAsymT {
+  static constexpr bool kAppend = true;  // the fused quantize-on-append is built for this format
+  static constexpr bool kOut = OUT;
+  static constexpr bool kSub24 = true;  // logits scaled by 2^-24
   half8v qh[4];
   half8v qo;
   float bias;
@@ -400,6 +404,16 @@ struct VAsymT {
   struct Raw {
     u32x4 w[2];
   };
+  // the V scale / zero-point of group lane / 16 for the output epilogue
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    const int g = lane >> 4;
+    s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
+    z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
+  }
+  // channels 2 lane, 2 lane + 1 from the merged acc / l: x = 72 + c (even) or 1032 + c (odd)
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    return half2v{(half_t)fmaf(s, r0 - 72.0f, z), (half_t)fmaf(s, r1 - 1032.0f, z)};
+  }
 
   __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
     const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
@@ -436,6 +450,164 @@ struct VAsymT {
           mfma16x16x32(pack8(and_or(s0, nc.m_lo, nc.c1024), and_or(s1, nc.m_lo, nc.c1024),
                              and_or(s2, nc.m_lo, nc.c1024), and_or(s3, nc.m_lo, nc.c1024)),
                        pb, acc[4 * k + 3]);
+    }
+  }
+};
+
+// fp16 scale of (kv head, group g) from a scale view that is static over b and t
+// (stride-0 view of per-token scales, fp16 or fp32; an fp32 scale is rounded to fp16)
+__device__ __forceinline__ half_t static_scale16(const KvDev& v, int hkv, int g) {
+  const int64_t i = (int64_t)hkv * v.ssh + (int64_t)g * v.ssg;
+  return v.scale_f32 ? (half_t)reinterpret_cast<const float*>(v.scale)[i]
+                     : reinterpret_cast<const half_t*>(v.scale)[i];
+}
+
+// Two INT8 codes (the low bytes of the two halves of x, the high bytes zero) -> the fp16
+// pair fp16(c * s16), rounded once as the reference's dequantisation (int8 -> fp16, times
+// the fp16 scale, src/engine/patch_model.py:355-362): x ^ 0x64806480 gives 1024 + (c + 128)
+// exactly, minus 1152 gives c, and the packed fp16 product with s16 rounds to nearest even.
+__device__ __forceinline__ uint32_t i8pair_deq(uint32_t x, half2v s2) {
+  const half2v off = {(half_t)1152.0f, (half_t)1152.0f};
+  return as_u32((as_h2(x ^ 0x64806480u) - off) * s2);
+}
+
+// INT8 symmetric K with a static fp16 scale s per (kv head, group of 32), i.e. per-token
+// scales given as a view with stride 0 over b and t (the reference's static-scale cache,
+// src/cache/int8_cache.py:298-488).  Lane (row, lg) of row block rb reads bytes
+// [32 lg, 32 lg + 32) of token 16 rb + row: quantisation group lg.  The A operand is the
+// reference's dequantised k = fp16(c * s16) (i8pair_deq), the B operand q', so the logits
+// are the reference's fp32 dot products of fp16 k and q up to the summation order.
+struct KI8T {
+  static constexpr bool kAppend = false;
+  static constexpr bool kOut = false;
+  static constexpr bool kSub24 = false;  // logits at unit scale
+  half8v qh[4];
+  half2v s2;  // the scale of group lg, twice
+  rsrc_t rk;
+  uint32_t vk;
+  struct Raw {
+    u32x4 w[4];  // [2 rb + i]: bytes [32 lg + 16 i, 32 lg + 16 i + 16) of token 16 rb + row
+  };
+
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kD));
+    vk = (uint32_t)(col * kD + 32 * lg);
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.s = static_scale16(a.k, hkv, lg);
+    in.z = (half_t)0.0f;
+    in.oc = int4{-1, -1, -1, -1};
+  }
+  // channel slice j (channels 32 lg + 8 j + e) of the q operand q' = fp16(q * inv_tau),
+  // shared through LDS
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    half_t vh[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      vh[e] = valid ? qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+  }
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+    s2 = half2v{in.s, in.s};
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kD : kOutOfRange);
+    r.w[0] = bload4(rk, v, 0);
+    r.w[1] = bload4(rk, v + 16, 0);
+    r.w[2] = bload4(rk, v + 16 * kD, 0);
+    r.w[3] = bload4(rk, v + 16 * kD + 16, 0);
+  }
+  // 8 codes (dwords lo = channels 0..3, hi = 4..7) -> fp16(c * s16) in channel order
+  __device__ __forceinline__ half8v deq8(uint32_t lo, uint32_t hi) const {
+    return pack8(i8pair_deq(perm_b32(0u, lo, 0x0C010C00u), s2), i8pair_deq(perm_b32(0u, lo, 0x0C030C02u), s2),
+                 i8pair_deq(perm_b32(0u, hi, 0x0C010C00u), s2), i8pair_deq(perm_b32(0u, hi, 0x0C030C02u), s2));
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    (void)nc;
+    float4v c0 = {0.f, 0.f, 0.f, 0.f};
+    float4v c1 = c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 w0 = r.w[j >> 1], w1 = r.w[2 + (j >> 1)];
+      const uint32_t l0 = (j & 1) ? w0.z : w0.x, h0 = (j & 1) ? w0.w : w0.y;
+      const uint32_t l1 = (j & 1) ? w1.z : w1.x, h1 = (j & 1) ? w1.w : w1.y;
+      c0 = mfma16x16x32(deq8(l0, h0), qh[j], c0);
+      c1 = mfma16x16x32(deq8(l1, h1), qh[j], c1);
+    }
+    x0 = c0;
+    x1 = c1;
+  }
+};
+
+// INT8 symmetric V in token rows (the reference layout) with a static scale per (kv head,
+// group of 32).  Lane (col, lg) reads the 8 bytes of channels 8 col .. 8 col + 7 of its 8
+// PV k-slot tokens T(k) = 4 lg + k (k < 4), 16 + 4 lg + k - 4: each load instruction reads
+// four whole 128-byte rows.  The A operand of MFMA c (channel 8 col + c) is the reference's
+// v = fp16(c * s16) of the 8 tokens (one v_perm_b32 per pair of tokens, then i8pair_deq), so
+// acc / l is the output.
+struct VI8RowT {
+  rsrc_t rv;
+  uint32_t vv;
+  half2v s2;  // the scale of group col / 4, twice
+  struct Raw {
+    u32x2 w[8];  // token T(k)
+  };
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * kD));
+    vv = (uint32_t)((4 * lg) * kD + 8 * col);
+    const half_t sv = static_scale16(a.v, hkv, col >> 2);
+    s2 = half2v{sv, sv};
+  }
+  // rows of a partial last tile past the capacity read 0; !valid: every load out of range
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * kD : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      r.w[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(v + t * kD), 0, kBufNT));
+    }
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8],
+                                      const NibConsts& nc) const {
+    (void)nc;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      // byte c % 4 of the tokens T(2p) and T(2p + 1) into the low bytes of the two halves
+      const uint32_t sel = (uint32_t)(c & 3) | 0x0C00u | ((uint32_t)(4 + (c & 3)) << 16) | 0x0C000000u;
+      uint32_t R[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t lo = (c >> 2) ? r.w[2 * p].y : r.w[2 * p].x;
+        const uint32_t hi = (c >> 2) ? r.w[2 * p + 1].y : r.w[2 * p + 1].x;
+        R[p] = i8pair_deq(perm_b32(hi, lo, sel), s2);
+      }
+      acc[c] = mfma16x16x32(pack8(R[0], R[1], R[2], R[3]), pb, acc[c]);
     }
   }
 };
@@ -521,9 +693,11 @@ __device__ __forceinline__ void append_status(const FusedAppend& f, const Append
   }
 }
 
-template <bool OUT, int LOOK, bool PACK8, int WPE = 2>
+template <class KF, class VF, int LOOK, bool PACK8, int WPE = 2>
 __global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
+  constexpr bool APP = KF::kAppend;  // the fused append exists for INT4_ASYM K + TILE32 V
+  constexpr bool OUT = KF::kOut;
   const int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -534,7 +708,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   // are issued after the set-up, when the new rows (requested with q) have arrived, or
   // before the first cache loads when wt is one of the wave's first LOOK + 1 tiles.  A
   // writer whose work-group has no tile of the context stores before it leaves.
-  const bool app_on = a.app.kx != nullptr;
+  const bool app_on = APP && a.app.kx != nullptr;
   const int stride_all = a.n_chunks * kTW;
   const int wt = app_on ? (int)(a.app.wpos / kTile) : 0;
   const bool writer = app_on && chunk * kTW + wave == wt % stride_all;
@@ -548,14 +722,22 @@ void decode_tiled_kernel(DecodeArgs a) {
   // so the two stay in step (the tile schedule, and so every result bit, is fixed).
   __shared__ int progress[kTW];
   progress[wave] = 0;
-  KAsymT<OUT> kf;
+  KF kf;
   // the q-side inputs are requested first: the wait for them then does not include the
   // cache tiles requested next
   QIn qin;
   kf.fetch_q(a, b, hkv, lane, wave, qin);
   kf.setup_addr(a, b, hkv, lane);
-  VAsymT vf;
+  VF vf;
   vf.setup(a, b, hkv, lane);
+  // the fused append's two steps (compiled only for the format that has it)
+  auto app_fetch = [&]() {
+    if constexpr (APP) append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
+  };
+  auto app_store = [&]() {
+    if constexpr (APP)
+      append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
+  };
 
   // Tile schedule: the n_chunks work-groups of a (b, kv head) interleave, so at step i the
   // waves of all of them read one contiguous run of n_chunks * kTW tiles and the device
@@ -570,8 +752,8 @@ void decode_tiled_kernel(DecodeArgs a) {
   for (int j = 0; j <= LOOK; ++j) tile[j] = first + j * stride;
   constexpr int R = LOOK + 1;                 // ring slots per stream
   constexpr int U = (R % 2 == 0) ? R : 2 * R;  // unroll: ring slot and x buffer are static
-  typename KAsymT<OUT>::Raw kr[R];
-  VAsymT::Raw vr[R];
+  typename KF::Raw kr[R];
+  typename VF::Raw vr[R];
   // The K and V tiles of step 0 are requested before the q set-up and before the context
   // length is known (bounded by the capacity; tiles past the context are never used), so
   // the memory system is busy from the start of the kernel; the rest of the ring (K of
@@ -584,8 +766,8 @@ void decode_tiled_kernel(DecodeArgs a) {
   asm volatile("" ::: "memory");
   const bool early_write = writer && wt / stride_all <= LOOK;
   if (early_write) {
-    append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
-    append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
+    app_fetch();
+    app_store();
   }
   const int ncap = (a.cap + kTile - 1) / kTile;
   kf.load(kTile * tile[0], tile[0] < ncap, kr[0]);
@@ -599,8 +781,8 @@ void decode_tiled_kernel(DecodeArgs a) {
   if (ntot == 0 || chunk * kTW >= ntot) {  // no tile for this work-group (uniform)
     if (writer) {
       if (!early_write) {
-        append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
-        append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
+        app_fetch();
+        app_store();
       }
       if (lane == 0) append_status(a.app, afl);
     }
@@ -616,7 +798,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   const bool late_write = writer && !early_write;
   const int wt_step = (wt - (chunk * kTW + wave)) / stride_all;
   const int store_step = late_write ? wt_step - LOOK - 1 : -1;
-  if (late_write) append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
+  if (late_write) app_fetch();
   if (wave < 4) kf.setup_q(a, qin, lane, wave, qsh);  // waves 4..7 would build the same
   NibConsts nc;
   nc.init();
@@ -629,14 +811,13 @@ void decode_tiled_kernel(DecodeArgs a) {
   kf.finish_setup(qsh, qin, lane);
   // (wt past the context: the wave may have fewer steps than store_step)
   const bool store_now = late_write && (wt >= ntot || store_step <= 0);
-  if (store_now)
-    append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
+  if (store_now) app_store();
 
   float4v acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
   float m = kNegInf, l = 0.f;
-  const float sm = a.sm_log2e * kTwo24;  // the logits arrive scaled by 2^-24
+  const float sm = KF::kSub24 ? a.sm_log2e * kTwo24 : a.sm_log2e;  // logits of KAsymT: x 2^-24
   int steps = 0;
   if (tile[0] < ntot) {
     float4v x[2][2];
@@ -646,8 +827,7 @@ void decode_tiled_kernel(DecodeArgs a) {
       for (int u = 0; u < U; ++u) {
         // step i (i % U == u): the tiles of this wave form a prefix of its schedule
         if (tile[0] >= ntot) break;
-        if (late_write && !store_now && steps == store_step)
-          append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
+        if (late_write && !store_now && steps == store_step) app_store();
         tile[LOOK + 1] = tile[LOOK] + stride;
         // fetch K of step i + LOOK + 1 (into the slot K of step i used) and V of step
         // i + LOOK (into the slot V of step i - 1 used), QK of step i + 1, then softmax
@@ -684,11 +864,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
   __shared__ int is_last;
   float vs = 0.f, vz = 0.f;
-  if (a.fused) {  // V scale / zero-point of group lane / 16, for the output (requested early)
-    const int g = lane >> 4;
-    vs = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
-    vz = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
-  }
+  if (a.fused) VF::epi_params(a, hkv, lane, vs, vz);  // for the output (requested early)
   merge_store_partial<PACK8>(a, msh, wave, lane, m, l, acc, b, hkv, chunk);
   if (!a.fused) return;
   __builtin_amdgcn_s_waitcnt(0);
@@ -697,59 +873,40 @@ void decode_tiled_kernel(DecodeArgs a) {
     is_last = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nvalid - 1);
   __syncthreads();
   if (!is_last) return;
-  merge_chunks(a, b, hkv, nvalid, wave, lane, vs, vz);
+  merge_chunks<VF>(a, b, hkv, nvalid, wave, lane, vs, vz);
   if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <bool OUT, bool PACK8>
-const void* tiled_ptr(int look) {
-  if (look == 3) return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 3, PACK8>);
-  if (look == 2) return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 2, PACK8>);
-  return reinterpret_cast<const void*>(&decode_tiled_kernel<OUT, 1, PACK8>);
+template <class KF, class VF, bool PACK8>
+const void* tiled_ptr() {
+  return reinterpret_cast<const void*>(&decode_tiled_kernel<KF, VF, 1, PACK8>);
 }
 
-// Tiles of lookahead: 1 (measured fastest at the headline shape: both variants keep 3
-// waves per SIMD, and the deeper ring spills), or KVQ_TILED_LOOK=1|2.
-int tiled_look() {
-  static int d = [] {
-    const char* e = getenv("KVQ_TILED_LOOK");
-    const int v = e ? atoi(e) : 1;
-    return (v >= 1 && v <= 3) ? v : 1;
-  }();
-  return d;
-}
-
-template <bool OUT, bool PACK8>
-void launch_one(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  const dim3 block(kTW * 64);
-  if (tiled_look() == 3)
-    hipLaunchKernelGGL((decode_tiled_kernel<OUT, 3, PACK8>), grid, block, 0, s, a);
-  else if (tiled_look() == 2)
-    hipLaunchKernelGGL((decode_tiled_kernel<OUT, 2, PACK8>), grid, block, 0, s, a);
-  else
-    hipLaunchKernelGGL((decode_tiled_kernel<OUT, 1, PACK8>), grid, block, 0, s, a);
+// (format family, n_rep <= 8) -> kernel; the kernels for n_rep <= 8 pack the second row
+// block's softmax into the padding lanes
+template <bool PACK8>
+const void* tiled_ptr_fam(int fam) {
+  switch (fam) {
+    case kTiledA4A4: return tiled_ptr<KAsymT<false>, VAsymT, PACK8>();
+    case kTiledA4A4o: return tiled_ptr<KAsymT<true>, VAsymT, PACK8>();
+    case kTiledI8A4: return tiled_ptr<KI8T, VAsymT, PACK8>();
+    case kTiledI8I8: return tiled_ptr<KI8T, VI8RowT, PACK8>();
+    default: return nullptr;
+  }
 }
 
 }  // namespace
 
-// the kernels for n_rep <= 8 pack the second row block's softmax into the padding lanes
-const void* tiled_kernel(int kf, int kout, int n_rep) {
-  if (kf != KVQ_FMT_INT4_ASYM) return nullptr;
-  const bool p8 = n_rep <= 8;
-  if (kout) return p8 ? tiled_ptr<true, true>(tiled_look()) : tiled_ptr<true, false>(tiled_look());
-  return p8 ? tiled_ptr<false, true>(tiled_look()) : tiled_ptr<false, false>(tiled_look());
+const void* tiled_kernel(int fam, int n_rep) {
+  return n_rep <= 8 ? tiled_ptr_fam<true>(fam) : tiled_ptr_fam<false>(fam);
 }
 
-void launch_tiled(const DecodeArgs& a, int kf, int kout, dim3 grid, hipStream_t s) {
-  (void)kf;
-  const bool p8 = a.n_rep <= 8;
-  if (kout) {
-    if (p8) launch_one<true, true>(a, grid, s);
-    else launch_one<true, false>(a, grid, s);
-  } else {
-    if (p8) launch_one<false, true>(a, grid, s);
-    else launch_one<false, false>(a, grid, s);
-  }
+hipError_t launch_tiled(const DecodeArgs& a, int fam, dim3 grid, hipStream_t s) {
+  const void* fn = tiled_kernel(fam, a.n_rep);
+  if (!fn) return hipErrorInvalidValue;
+  DecodeArgs args = a;
+  void* kargs[] = {&args};
+  return hipLaunchKernel(fn, grid, dim3(kTW * 64), kargs, 0, s);
 }
 
 }  // namespace kvq

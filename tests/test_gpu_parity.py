@@ -216,6 +216,100 @@ def test_decode_int8_static_expanded_scales_and_fp32_q():
     assert_close(out, ref.float(), "int8 static-expanded")
 
 
+def _static_int8_case(B, Hq, Hkv, S, g, scale_dtype=torch.float16):
+    """Codes and static group-32 scales as INT8KVCache stores them: per-token scale views
+    with stride 0 over b and t, which the tiled INT8 kernels serve."""
+    q, k, v, _, _ = _rand_int8_case(B, Hq, Hkv, S, 4, g)
+    sk = (torch.rand(Hkv, 4, generator=g) * 0.01 + 1e-3).to(scale_dtype)
+    sv = (torch.rand(Hkv, 4, generator=g) * 0.02 + 1e-3).to(scale_dtype)
+    ks = sk[None, :, None, :].expand(B, Hkv, S, 4)
+    vs = sv[None, :, None, :].expand(B, Hkv, S, 4)
+    return q, k, v, ks, vs
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,ctx", [
+    (4, 12, 2, 8192, [8192, 8191, 4097, 33]),    # config 1 shape, ragged, partial tiles
+    (3, 12, 2, 700, [700, 1, 0]),                 # a single token and an empty row
+    (2, 32, 2, 1000, [1000, 999]),                # 16 query heads per kv head (no packing)
+    (2, 40, 8, 300, [300, 64]),                   # GQA 5
+])
+def test_decode_int8_static_tiled(B, Hq, Hkv, S, ctx):
+    """Static-scale INT8 K and V (the tiled INT8 kernel) against the oracle."""
+    K = _lib()
+    g = gen(31 * S + Hq)
+    q, k, v, ks, vs = _static_int8_case(B, Hq, Hkv, S, g)
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    sm = 1 / math.sqrt(128)
+    ref = OA.decode_attn_int8_torch_ref(q, k, v, ks, vs, cl, sm)
+    out = K.decode_attn_int8(q.to(DEV), k.to(DEV), v.to(DEV), ks.to(DEV), vs.to(DEV), cl.to(DEV),
+                             sm_scale=sm)
+    assert_close(out, ref, f"int8 static tiled B{B} Hq{Hq} Hkv{Hkv} S{S}")
+    for b, c in enumerate(ctx):
+        if c == 0:
+            assert torch.all(out[b] == 0)
+
+
+def test_decode_int8_static_tiled_f32_scales_inv_tau_and_splits():
+    """fp32 static scales (rounded to fp16 in the kernel, as the reference's fp16 cast),
+    per-head inverse temperature, split-size invariance and bit-exact repeats."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import _capi as C
+    from llm_kvcache_quantization_amd.kernels import DecodePlan, kv_view_tok
+
+    g = gen(5150)
+    B, Hq, Hkv, S = 2, 12, 2, 5000
+    q, k, v, ks, vs = _static_int8_case(B, Hq, Hkv, S, g, torch.float32)
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    cl = torch.tensor([5000, 2222], dtype=torch.int32)
+    sm = 1 / math.sqrt(128)
+    ref = OA.decode_attn_int8_torch_ref(OA.prescale_q(q, tau), k, v, ks.to(torch.float16),
+                                        vs.to(torch.float16), cl, sm)
+    d = lambda x: x.to(DEV)
+    outs = []
+    for chunk in (0, 256, 1024):
+        plan = DecodePlan(d(q), C.KVQ_FMT_INT8_SYM, kv_view_tok(d(k), d(ks)), C.KVQ_FMT_INT8_SYM,
+                          kv_view_tok(d(v), d(vs)), d(cl), Hkv, S, sm, 32, inv_tau=d(tau),
+                          chunk_tokens=chunk)
+        a = plan.launch().clone()
+        b = plan.launch().clone()
+        assert torch.equal(a, b), chunk
+        assert_close(a, ref, f"int8 static f32 chunk={chunk}")
+        outs.append(a.cpu())
+
+
+@pytest.mark.parametrize("B,S,ctx", [
+    (3, 3000, [3000, 1234, 1]),
+    (8, 4096, [4096, 4000, 3001, 2048, 1025, 512, 33, 0]),
+])
+def test_decode_k8v4_tiled_ragged(B, S, ctx):
+    """INT8 K (static) with TILE32 asymmetric INT4 V (the tiled K8/V4 kernel), config 4's
+    heads (GQA 5), ragged contexts."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[4]
+    t = SY.calibrate(cfg, 0)
+    g = gen(40 + B)
+    k, v = SY.draw_kv(cfg, 0, B, S, g)
+    q = SY.draw_q(cfg, B, g)
+    tau = SY.inv_tau(cfg)[0]
+    k8, ks16 = OQ.quantize_symmetric_int8_with_scale(k, t.k_scale, 32)
+    vq = OQ.pack_int4(OQ.quantize_asymmetric_static(v, t.v_scale, t.v_zp))
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    ref = OA.decode_attn_k8v4_ref(q, k8, ks16, vq, t.v_scale, t.v_zp, cl, 0.0883883, inv_tau=tau)
+    # the static table as a stride-0 per-token view (what the tiled kernel serves)
+    ks_view = t.k_scale.clamp(min=1e-5).to(torch.float16).to(DEV)[None, :, None, :].expand(
+        B, cfg.kv_heads, S, 4)
+    assert torch.equal(ks_view.cpu(), ks16)
+    out = K.decode_attn_k8v4(q.to(DEV), k8.to(DEV), ks_view, K.tile_v(vq.to(DEV)),
+                             t.v_scale.to(DEV), t.v_zp.to(DEV), cl.to(DEV), 0.0883883,
+                             inv_tau=tau.to(DEV))
+    assert_close(out, ref, f"k8v4 tiled B{B} S{S}")
+    for b, c in enumerate(ctx):
+        if c == 0:
+            assert torch.all(out[b] == 0)
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,S,ctx", [
     (2, 12, 2, 2048, [2048, 1500]),
     (1, 28, 4, 4096, [4096]),
