@@ -3,19 +3,21 @@
 A step is one decode step over every layer of the configuration.  Per layer it runs
 quantize-on-append of the new token's K/V and split-K quantized decode attention over
 the whole context:
-- INT4-asymmetric K with TILE32 V (configs 2, 3): both in one launch
-  (kvq_append_decode_attn), whose chunk partials are merged in the same launch (at most
-  64 chunks and 8 query heads per KV head);
-- otherwise: the append launch, then the attention launch (plus a combine launch for the
-  row-layout kernels).
+both in one launch (kvq_append_decode_attn) of the tiled kernel of the configuration's
+format, whose chunk partials are merged in the same launch (at most 64 chunks per KV
+head):
+- configs 2, 3: INT4-asymmetric K (4 fp16 outlier channels) and TILE32 V;
+- config 1: static-scale INT8 K and V in token rows;
+- config 4: static-scale INT8 K and TILE32 INT4-asymmetric V.
 
 Caches are seeded synthetic data of the configured shape, one distinct cache per
 layer, built on the GPU with the same HIP append kernel.  Each step rewrites the
 last slot and attends over the full context, so every step does identical work.
 
-The timed region replays a HIP graph of W warm-up and then K timed steps, bracketed
-by hipEvents on the launch stream.  ``value`` is the mean microseconds per
-layer-step (append + attention).  The line also carries:
+The timed region runs W warm-up and then K timed steps, bracketed by hipEvents on the
+launch stream, both as direct launches and as replays of a HIP graph of one step; the
+faster is reported.  ``value`` is the mean microseconds per layer-step (append +
+attention).  The line also carries:
 - ``roofline``: algorithmic bytes of the dominant kernel (the fused step kernel, else
   the attention kernel) / its measured time per layer;
 - ``attention_us_per_layer_step`` / ``append_us_per_layer_step``: each half timed alone
@@ -68,7 +70,8 @@ def parse():
 def append_bytes(cfg):
     """Bytes of one layer's quantize-on-append: fp16 K and V rows in, codes (+ fp16
     outlier channels) out, for every (b, kv head)."""
-    out = (128 if cfg.k_format == "int8" else 64) + 64 + (8 if cfg.outlier_channels else 0)
+    out = ((128 if cfg.k_format == "int8" else 64) + (128 if cfg.v_format == "int8" else 64)
+           + (8 if cfg.outlier_channels else 0))
     return cfg.batch * cfg.kv_heads * (2 * 128 * 2 + out)
 
 
@@ -153,8 +156,9 @@ class Layer:
         del ks_view
         self.plan = DecodePlan(self.q, kfmt, kview, vfmt, vview, self.ctx, Hkv, cap,
                                1.0 / math.sqrt(128), 32, inv_tau=self.inv_tau, chunk_tokens=chunk)
-        # INT4-asymmetric K and TILE32 V: kvq_append_decode_attn does the step in one launch
-        self.fused = self.v_tiled and cfg.k_format != "int8"
+        # every configuration's format has a tiled kernel, so kvq_append_decode_attn does
+        # the step (append + attention) in one launch
+        self.fused = True
 
     def _append_params(self, cfg, kx, vx, pos):
         C = self.C

@@ -348,6 +348,17 @@ class _SymCacheBase(_EngineBase):
         if S == 0:
             return
         status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv = self._append_params(layer_id, k, v, old_len, status, sk, sv)
+        self._launch_append(pk, pv, k.device)
+        if status is not None:
+            self._check_status(layer_id, k.numel(), self._kind, self._qrange)
+        self._layer_seq_lens[layer_id] = target
+        if layer_id == 0:
+            self._seq_len = target
+
+    def _append_params(self, layer_id, k, v, old_len, status, sk, sv):
+        """kvq_append_params of K and V written at slot old_len (each keeps the tensors it
+        points at alive)."""
         pk, pv = C.AppendParams(), C.AppendParams()
         for side, p, x, codes, scale_buf, st, tok in (
                 ("k", pk, k, self._k_cache[layer_id], self._k_scale[layer_id], sk, self._k_tok[layer_id]),
@@ -368,22 +379,18 @@ class _SymCacheBase(_EngineBase):
                 p.so_stride_b, p.so_stride_h, p.so_stride_t, p.so_stride_g = scale_buf.stride()
             # keep the (possibly temporary) tensors alive until the launch returns
             p._keep = (xs, st)
-        self._launch_append(pk, pv, k.device)
-        if status is not None:
-            self._check_status(layer_id, k.numel(), self._kind, self._qrange)
-        self._layer_seq_lens[layer_id] = target
-        if layer_id == 0:
-            self._seq_len = target
+        return pk, pv
 
     def _pre_append_checks(self, layer_id: int) -> None:
         pass
 
-    def _raw_views(self, layer_id: int):
+    def _raw_views(self, layer_id: int, n: Optional[int] = None):
         if layer_id < 0 or layer_id >= self.num_layers:
             raise ValueError(f"layer_id {layer_id} out of range [0, {self.num_layers})")
         if self._k_cache[layer_id] is None:
             raise ValueError(f"Cache for layer {layer_id} is empty")
-        n = self._layer_seq_lens[layer_id]
+        if n is None:
+            n = self._layer_seq_lens[layer_id]
         kc = self._k_cache[layer_id][:, :, :n, :]
         vc = self._v_cache[layer_id][:, :, :n, :]
         B, H = kc.shape[0], kc.shape[1]
@@ -481,6 +488,62 @@ class INT8KVCache(_SymCacheBase):
     def get_int8_tensors(self, layer_id: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
         """(k_int8, v_int8, k_scale, v_scale) views [B, H, S, D] / [B, H, S, G] (fp16 scales)."""
         return self._raw_views(layer_id)
+
+    def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
+                           sm_scale: Optional[float] = None,
+                           inv_tau: Optional[Tensor] = None) -> Tensor:
+        """Decode step of one layer: append the new token (k, v: fp16 [B, H, 1, D]) and
+        attend over the whole cache, the new token included (the append + attention of the
+        reference's decode step, src/engine/patch_model.py:755-957).  Returns fp16
+        [B, Hq, D].  With static group-32 scales (no adaptive policy) both run in one HIP
+        launch (kvq_append_decode_attn); otherwise as ``append`` then the decode kernel.
+        Either way codes and output are bit-identical to ``append`` followed by
+        :func:`kernels.decode_attn_int8` over ``get_int8_tensors`` (q scaled by inv_tau).
+        With ``check_numerics``, NaN / Inf in k or v raise ValueError and the cache does
+        not advance."""
+        from .kernels import DecodePlan, kv_view_tok
+
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        if S != 1:
+            raise ValueError(f"append_decode_attn appends one token per step, got S={S}")
+        if q.ndim != 3 or q.dtype != torch.float16 or q.shape[0] != B or q.shape[1] % H:
+            raise ValueError(f"q must be fp16 [B, Hq, D] with Hq a multiple of {H}, got "
+                             f"{q.dtype} {tuple(q.shape)}")
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        fused = (self.group_size == 32 and D == 128 and not self._side_is_token("k")
+                 and not self._side_is_token("v"))
+        if not fused:
+            self.append(layer_id, k, v)
+            kc, vc, ks, vs = self._raw_views(layer_id)
+            n = kc.shape[2]
+            ctx = torch.full((B,), n, dtype=torch.int32, device=q.device)
+            plan = DecodePlan(q, C.KVQ_FMT_INT8_SYM, kv_view_tok(kc, ks), C.KVQ_FMT_INT8_SYM,
+                              kv_view_tok(vc, vs), ctx, H, n, sm_scale, self.group_size,
+                              inv_tau=inv_tau, keepalive=(kc, vc, ks, vs))
+            return plan.launch()
+        G = D // self.group_size
+        self._pre_append_checks(layer_id)
+        sk = self._static_for("k", layer_id, H, G)
+        sv = self._static_for("v", layer_id, H, G)
+        old = self._layer_seq_lens[layer_id]
+        n = old + 1
+        self._ensure_capacity(layer_id, B, H, D, G, n)
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv = self._append_params(layer_id, k, v, old, status, sk, sv)
+        kc, vc, ks, vs = self._raw_views(layer_id, n)
+        ctx = torch.full((B,), n, dtype=torch.int32, device=q.device)
+        plan = DecodePlan(q, C.KVQ_FMT_INT8_SYM, kv_view_tok(kc, ks), C.KVQ_FMT_INT8_SYM,
+                          kv_view_tok(vc, vs), ctx, H, n, sm_scale, self.group_size,
+                          inv_tau=inv_tau, keepalive=(kc, vc, ks, vs))
+        out = plan.launch_append(pk, pv)
+        if status is not None:
+            self._check_status(layer_id, k.numel(), self._kind, self._qrange)
+        self._layer_seq_lens[layer_id] = n
+        if layer_id == 0:
+            self._seq_len = n
+        return out
 
     def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
         """Dequantize (code * scale in fp32) and return fp16 K/V (int8_cache.py:490-542)."""
@@ -626,9 +689,8 @@ class _StaticG32Cache(_EngineBase):
 
     Per layer: K codes [B, H, cap, 64] packed INT4 (asymmetric, byte = hi nibble even
     channel, codes c + 8 with c in [-8, 7]) or [B, H, cap, 128] INT8 (symmetric).  V codes
-    are packed asymmetric INT4; with INT4 K they are kept in the TILE32 layout
-    [B, H, cap / 32, 2048] the decode kernel streams (:func:`kernels.tile_v`), with INT8 K
-    as rows [B, H, cap, 64].  The static tables are [L, H, 4].  With
+    are packed asymmetric INT4 kept in the TILE32 layout [B, H, cap / 32, 2048] the decode
+    kernels stream (:func:`kernels.tile_v`).  The static tables are [L, H, 4].  With
     ``k_outlier_idx`` (INT4 K only) those 4 K channels per head are also stored verbatim
     in fp16 [B, H, cap, 4] and replace the dequantised codes.  No per-token scale is
     stored: the kernels read the static tables.
@@ -675,8 +737,8 @@ class _StaticG32Cache(_EngineBase):
 
     @property
     def v_tiled(self) -> bool:
-        """V codes are kept in the TILE32 layout (INT4 K) rather than as rows."""
-        return not self._k_int8
+        """V codes are kept in the TILE32 layout rather than as rows."""
+        return True
 
     def _ensure(self, layer_id, B, H, target):
         cap = self._layer_capacity[layer_id]
@@ -756,6 +818,62 @@ class _StaticG32Cache(_EngineBase):
         if layer_id == 0:
             self._seq_len = old + S
 
+    def _k_view(self, layer_id: int, n: int):
+        """(format, view) of layer_id's K over its first n tokens for the decode kernels."""
+        from .kernels import kv_view_static, kv_view_tok
+
+        kb = self._k[layer_id][:, :, :n]
+        if self._k_int8:
+            B, H = kb.shape[:2]
+            ks = self.k_scale[layer_id].clamp(min=1e-5)[None, :, None, :].expand(B, H, n, 4)
+            return C.KVQ_FMT_INT8_SYM, kv_view_tok(kb.view(torch.int8), ks)
+        ob = None if self._ko[layer_id] is None else self._ko[layer_id][:, :, :n]
+        oi = None if self.k_outlier_idx is None else self.k_outlier_idx[layer_id]
+        return C.KVQ_FMT_INT4_ASYM, kv_view_static(kb, self.k_scale[layer_id], self.k_zp[layer_id], oi, ob)
+
+    def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
+                           sm_scale: Optional[float] = None,
+                           inv_tau: Optional[Tensor] = None) -> Tensor:
+        """Decode step of one layer in one HIP launch: append the new token (k, v: fp16
+        [B, H, 1, 128]) and attend over the layer's whole cache, the new token included.
+        Returns fp16 [B, Hq, 128].  Codes and output are bit-identical to ``append`` then
+        the decode kernel over the cache's tensors with context lengths ``get_seq_len()``
+        (the append + attention of the reference's decode step,
+        src/engine/patch_model.py:755-957).  With ``check_numerics``, NaN / Inf in k or v
+        raise ValueError and the cache does not advance."""
+        from .kernels import DecodePlan, _check_static_args, kv_view_static
+
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        if S != 1:
+            raise ValueError(f"append_decode_attn appends one token per step, got S={S}")
+        if self.k_scale.shape[1] != H:
+            raise ValueError(f"calibration vs model heads mismatch: {self.k_scale.shape[1]} vs {H}")
+        old = self._layer_seq_lens[layer_id]
+        self._ensure(layer_id, B, H, old + 1)
+        # the views the cache's getters give once the token is in (same split as the
+        # two-call path, hence the same output bits)
+        n = old + 1
+        vb = self._v[layer_id][:, :, :-(-n // TILE_TOKENS)]
+        vs, vz = self.v_scale[layer_id], self.v_zp[layer_id]
+        kfmt, kview = self._k_view(layer_id, n)
+        _check_static_args(q, vb, vb, (vs, vz), torch.empty(B))
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv, keep = self._append_params(layer_id, k, v, old, status)
+        ctx = torch.full((B,), n, dtype=torch.int32, device=q.device)
+        plan = DecodePlan(q, kfmt, kview, C.KVQ_FMT_INT4_ASYM, kv_view_static(vb, vs, vz), ctx, H,
+                          n, sm_scale, 32, inv_tau=inv_tau, keepalive=(keep, vb))
+        out = plan.launch_append(pk, pv)
+        if status is not None:
+            self._check_status(layer_id, k.numel(), "K8V4" if self._k_int8 else "INT4-asym",
+                               "the code range")
+        self._layer_seq_lens[layer_id] = old + 1
+        if layer_id == 0:
+            self._seq_len = old + 1
+        return out
+
     def _check_layer(self, layer_id: int) -> int:
         if self._k[layer_id] is None:
             raise ValueError(f"Cache for layer {layer_id} is empty")
@@ -784,51 +902,6 @@ class _StaticG32Cache(_EngineBase):
 class INT4AsymKVCache(_StaticG32Cache):
     """Asymmetric INT4 K and V with static group-32 scale / zero-point (configs 2 and 3),
     optionally with 4 fp16 outlier K channels per head."""
-
-    def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
-                           sm_scale: Optional[float] = None,
-                           inv_tau: Optional[Tensor] = None) -> Tensor:
-        """Decode step of one layer in one HIP launch: append the new token (k, v: fp16
-        [B, H, 1, 128]) and attend over the layer's whole cache, the new token included.
-        Returns fp16 [B, Hq, 128].  Codes and output are bit-identical to ``append`` then
-        :func:`kernels.decode_attn_int4_asym` over ``get_int4_g32_tensors`` with context
-        lengths ``get_seq_len()`` (the append + attention of the reference's decode step,
-        src/engine/patch_model.py:755-957).  With ``check_numerics``, NaN / Inf in k or v
-        raise ValueError and the cache does not advance."""
-        from .kernels import DecodePlan, _check_static_args, kv_view_static
-
-        self._validate_kv(layer_id, k, v)
-        B, H, S, D = k.shape
-        if S != 1:
-            raise ValueError(f"append_decode_attn appends one token per step, got S={S}")
-        if self.k_scale.shape[1] != H:
-            raise ValueError(f"calibration vs model heads mismatch: {self.k_scale.shape[1]} vs {H}")
-        old = self._layer_seq_lens[layer_id]
-        self._ensure(layer_id, B, H, old + 1)
-        # the views get_int4_g32_tensors gives once the token is in (same split as the
-        # two-call path, hence the same output bits)
-        n = old + 1
-        kb, vb = self._k[layer_id][:, :, :n], self._v[layer_id][:, :, :-(-n // TILE_TOKENS)]
-        ob = None if self._ko[layer_id] is None else self._ko[layer_id][:, :, :n]
-        ks, kz = self.k_scale[layer_id], self.k_zp[layer_id]
-        vs, vz = self.v_scale[layer_id], self.v_zp[layer_id]
-        oi = None if self.k_outlier_idx is None else self.k_outlier_idx[layer_id]
-        _check_static_args(q, kb, vb, (ks, kz, vs, vz), torch.empty(B))
-        if sm_scale is None:
-            sm_scale = 1.0 / math.sqrt(D)
-        status = self._status_buf(k.device) if self.check_numerics else None
-        pk, pv, keep = self._append_params(layer_id, k, v, old, status)
-        ctx = torch.full((B,), n, dtype=torch.int32, device=q.device)
-        plan = DecodePlan(q, C.KVQ_FMT_INT4_ASYM, kv_view_static(kb, ks, kz, oi, ob),
-                          C.KVQ_FMT_INT4_ASYM, kv_view_static(vb, vs, vz), ctx, H, kb.shape[2],
-                          sm_scale, 32, inv_tau=inv_tau, keepalive=(keep, kb, vb, ob))
-        out = plan.launch_append(pk, pv)
-        if status is not None:
-            self._check_status(layer_id, k.numel(), "INT4-asym", "the code range")
-        self._layer_seq_lens[layer_id] = old + 1
-        if layer_id == 0:
-            self._seq_len = old + 1
-        return out
 
     def get_int4_g32_tensors(self, layer_id: int):
         """(k_codes [B,H,n,64], v_tiles [B,H,ceil(n/32),2048] (TILE32 layout), k_scale, k_zp,
@@ -861,9 +934,11 @@ class K8V4KVCache(_StaticG32Cache):
 
     def get_k8v4_tensors(self, layer_id: int):
         """(k_codes int8 [B,H,n,128], k_scale fp16 [B,H,n,4] (a stride-0 view of the static
-        table after the fp16 clamp to 1e-5), v_codes, v_scale, v_zp)."""
+        table after the fp16 clamp to 1e-5), v_tiles [B,H,ceil(n/32),2048] (TILE32 layout;
+        ``untile_v(v_tiles, n)`` gives packed rows), v_scale, v_zp)."""
         n = self._check_layer(layer_id)
         k = self._k[layer_id][:, :, :n].view(torch.int8)
         B, H = k.shape[:2]
         ks = self.k_scale[layer_id].clamp(min=1e-5)[None, :, None, :].expand(B, H, n, 4)
-        return k, ks, self._v[layer_id][:, :, :n], self.v_scale[layer_id], self.v_zp[layer_id]
+        vt = self._v[layer_id][:, :, :-(-n // TILE_TOKENS)]
+        return k, ks, vt, self.v_scale[layer_id], self.v_zp[layer_id]

@@ -601,17 +601,22 @@ static int64_t resident_slots(const void* fn, int threads) {
 // The tiled kernel family that serves p, or kTiledNone (a row-layout kernel then does):
 // INT4_ASYM K with TILE32 V, or INT8 K with a static scale (a view with stride 0 over b and t)
 // and dense 128-byte rows, with TILE32 INT4_ASYM V or static-scale INT8 V in dense rows.
+// A per-token scale view is static when it does not vary over b and t (stride 0, or a
+// dimension of size 1, whose stride is never used).
+static bool static_over_bt(const kvq_kv_view& v, const kvq_decode_params* p) {
+  return (v.scale_stride_b == 0 || p->batch == 1) && (v.scale_stride_t == 0 || p->capacity <= 1);
+}
+
 static int tiled_family(const kvq_decode_params* p) {
   const bool vt = p->v.layout == KVQ_LAYOUT_TILE32;
   if (p->k_format == KVQ_FMT_INT4_ASYM)
     return (p->v_format == KVQ_FMT_INT4_ASYM && vt) ? (p->k.n_outlier > 0 ? kTiledA4A4o : kTiledA4A4)
                                                      : kTiledNone;
   const bool k8 = p->k_format == KVQ_FMT_INT8_SYM && p->group_size == kTile &&
-                  p->k.scale_stride_b == 0 && p->k.scale_stride_t == 0 && p->k.stride_t == kD;
+                  static_over_bt(p->k, p) && p->k.stride_t == kD;
   if (!k8) return kTiledNone;
   if (p->v_format == KVQ_FMT_INT4_ASYM && vt) return kTiledI8A4;
-  if (p->v_format == KVQ_FMT_INT8_SYM && !vt && p->v.scale_stride_b == 0 &&
-      p->v.scale_stride_t == 0 && p->v.stride_t == kD)
+  if (p->v_format == KVQ_FMT_INT8_SYM && !vt && static_over_bt(p->v, p) && p->v.stride_t == kD)
     return kTiledI8I8;
   return kTiledNone;
 }
@@ -833,8 +838,7 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
 
   a.app = FusedAppend{};
   if (app) {
-    if (tfam != kTiledA4A4 && tfam != kTiledA4A4o)
-      return fail(KVQ_ERR_UNSUPPORTED, "fused append needs INT4_ASYM K and TILE32 V");
+    if (!tiled) return fail(KVQ_ERR_UNSUPPORTED, "the fused append needs a tiled-kernel format");
     a.app = *app;
   }
 
@@ -873,12 +877,12 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
 // One new token per (b, kv head) appended to the cache p attends over, in the same launch.
 // The append parameters must describe exactly that cache: the same code, outlier and
 // static-table buffers with the same strides (so the kernel writes what it later reads).
-static int check_fused_side(const kvq_append_params* x, const kvq_kv_view& v,
+static int check_fused_side(const kvq_append_params* x, const kvq_kv_view& v, int fmt,
                             const kvq_decode_params* p, bool is_k) {
   const std::string n(is_k ? "k_new" : "v_new");
   if (!x) return fail(KVQ_ERR_INVALID, n + " is NULL");
-  if (x->format != KVQ_FMT_INT4_ASYM)
-    return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append supports INT4_ASYM only");
+  if (x->format != fmt)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": format differs from the decode call's");
   if (x->seq_new != 1) return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append takes one token");
   if (x->batch != p->batch || x->heads != p->kv_heads || x->head_dim != kD || x->group_size != 32)
     return fail(KVQ_ERR_INVALID, n + ": shape does not match the decode call");
@@ -888,15 +892,22 @@ static int check_fused_side(const kvq_append_params* x, const kvq_kv_view& v,
     return fail(KVQ_ERR_INVALID, n + ": write_pos outside the cache capacity");
   if (x->codes != v.codes || x->codes_stride_b != v.stride_b || x->codes_stride_h != v.stride_h)
     return fail(KVQ_ERR_UNSUPPORTED, n + ": codes must be the buffer the decode call reads");
-  if (is_k ? (x->codes_layout != KVQ_LAYOUT_ROWS || x->codes_stride_t != v.stride_t)
-           : (x->codes_layout != KVQ_LAYOUT_TILE32))
+  if (x->codes_layout != v.layout || (v.layout == KVQ_LAYOUT_ROWS && x->codes_stride_t != v.stride_t))
     return fail(KVQ_ERR_UNSUPPORTED, n + ": codes layout differs from the decode call's");
+  if (x->adaptive || x->mixed_rescue || x->rescue_quantile > 0.f || x->rescue_all || x->scale_out)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append takes static scales only");
+  if (!x->static_scale) return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append needs a static scale");
+  if (fmt == KVQ_FMT_INT8_SYM) {
+    // the append quantizes with its own table (as kvq_quant_append would); no side-band
+    if (x->static_scale_dtype != KVQ_DTYPE_F16 && x->static_scale_dtype != KVQ_DTYPE_F32)
+      return fail(KVQ_ERR_INVALID, n + ": static_scale_dtype must be F16 or F32");
+    if (x->n_outlier) return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
+    return KVQ_OK;
+  }
   if (x->static_scale != v.scale || x->static_zp != v.zero_point ||
       x->static_scale_dtype != KVQ_DTYPE_F16 || x->static_stride_h != v.scale_stride_h ||
       x->static_stride_g != v.scale_stride_g)
     return fail(KVQ_ERR_UNSUPPORTED, n + ": static tables differ from the decode call's");
-  if (x->adaptive || x->mixed_rescue || x->rescue_quantile > 0.f || x->rescue_all || x->scale_out)
-    return fail(KVQ_ERR_UNSUPPORTED, n + ": scale policies do not apply to INT4_ASYM");
   if (x->n_outlier != v.n_outlier)
     return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels differ from the decode call's");
   if (x->n_outlier &&
@@ -910,17 +921,17 @@ static int check_fused_side(const kvq_append_params* x, const kvq_kv_view& v,
 extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
                                       const kvq_append_params* v_new, kvq_stream_t stream) {
   if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
-  if (p->v.layout != KVQ_LAYOUT_TILE32 || p->k_format != KVQ_FMT_INT4_ASYM ||
-      p->v_format != KVQ_FMT_INT4_ASYM)
+  if (tiled_family(p) == kTiledNone)
     return fail(KVQ_ERR_UNSUPPORTED,
-                "the fused append needs INT4_ASYM K and INT4_ASYM V in the TILE32 layout");
-  int rc = check_fused_side(k_new, p->k, p, true);
+                "the fused append needs a tiled-kernel format: INT4_ASYM K with TILE32 V, or "
+                "static-scale INT8 K with TILE32 INT4_ASYM V or static-scale INT8 V rows");
+  int rc = check_fused_side(k_new, p->k, p->k_format, p, true);
   if (rc) return rc;
-  rc = check_fused_side(v_new, p->v, p, false);
+  rc = check_fused_side(v_new, p->v, p->v_format, p, false);
   if (rc) return rc;
   if (k_new->write_pos != v_new->write_pos)
     return fail(KVQ_ERR_INVALID, "k_new and v_new must share write_pos");
-  FusedAppend f;
+  FusedAppend f{};
   f.kx = reinterpret_cast<const half_t*>(k_new->x);
   f.ksb = k_new->x_stride_b;
   f.ksh = k_new->x_stride_h;
@@ -930,6 +941,14 @@ extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_appe
   f.wpos = k_new->write_pos;
   f.kstatus = k_new->status;
   f.vstatus = v_new->status;
+  f.kst = k_new->static_scale;
+  f.kst_f32 = k_new->static_scale_dtype == KVQ_DTYPE_F32;
+  f.kst_sh = k_new->static_stride_h;
+  f.kst_sg = k_new->static_stride_g;
+  f.vst = v_new->static_scale;
+  f.vst_f32 = v_new->static_scale_dtype == KVQ_DTYPE_F32;
+  f.vst_sh = v_new->static_stride_h;
+  f.vst_sg = v_new->static_stride_g;
   return decode_impl(p, &f, stream);
 }
 

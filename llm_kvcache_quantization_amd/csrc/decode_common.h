@@ -45,6 +45,11 @@ struct FusedAppend {
   int64_t wpos;
   int32_t* kstatus;
   int32_t* vstatus;
+  // INT8 sides: the append's static scale tables [H, G] (elements; fp32 when *_f32)
+  const void* kst;
+  const void* vst;
+  int kst_f32, vst_f32;
+  int64_t kst_sh, kst_sg, vst_sh, vst_sg;
 };
 
 struct DecodeArgs {

@@ -256,6 +256,7 @@ struct QIn {
 template <bool OUT>
 struct KAsymT {
   static constexpr bool kAppend = true;  // the fused quantize-on-append is built for this format
+  static constexpr bool kAsym = true;
   static constexpr bool kOut = OUT;
   static constexpr bool kSub24 = true;  // logits scaled by 2^-24
   half8v qh[4];
@@ -399,6 +400,7 @@ struct KAsymT {
 // channel 8 col + c of the lane's d-row col, x = 64 + n (even c) or 1024 + n (odd c);
 // combine_kernel applies out = s (acc / l - off) + z with off = 72 or 1032.
 struct VAsymT {
+  static constexpr bool kTile32 = true;
   rsrc_t rv;
   uint32_t vv;
   struct Raw {
@@ -478,7 +480,8 @@ __device__ __forceinline__ uint32_t i8pair_deq(uint32_t x, half2v s2) {
 // reference's dequantised k = fp16(c * s16) (i8pair_deq), the B operand q', so the logits
 // are the reference's fp32 dot products of fp16 k and q up to the summation order.
 struct KI8T {
-  static constexpr bool kAppend = false;
+  static constexpr bool kAppend = true;
+  static constexpr bool kAsym = false;
   static constexpr bool kOut = false;
   static constexpr bool kSub24 = false;  // logits at unit scale
   half8v qh[4];
@@ -561,6 +564,7 @@ struct KI8T {
 // v = fp16(c * s16) of the 8 tokens (one v_perm_b32 per pair of tokens, then i8pair_deq), so
 // acc / l is the output.
 struct VI8RowT {
+  static constexpr bool kTile32 = false;
   rsrc_t rv;
   uint32_t vv;
   half2v s2;  // the scale of group col / 4, twice
@@ -613,73 +617,89 @@ struct VI8RowT {
 };
 
 // Fused quantize-on-append of the new token of (b, kv head): one wave (the writer), two
-// values per lane, the arithmetic of the append kernel (asym_pack_pair with the decode's
-// static tables).  K goes to row wpos, V to its TILE32 bytes, the outlier channels
-// verbatim.  The other waves issue nothing for it (even out-of-range memory operations
-// would occupy their address unit ahead of their first cache loads).  NaN / Inf set
-// status[0] and clamped elements are added to status[1] (per side).
+// values per lane, the arithmetic of the append kernel: asym_pack_pair with the decode's
+// static tables for INT4_ASYM, int8_pack_pair with the append's static table for INT8.  K
+// goes to row wpos (INT4_ASYM: its outlier channels verbatim to the side-band), V to its
+// TILE32 bytes or its row.  The other waves issue nothing for it (even out-of-range memory
+// operations would occupy their address unit ahead of their first cache loads).  NaN / Inf
+// set status[0] and clamped elements are added to status[1] (per side).
 struct AppendIn {
   uint32_t k2, v2;  // fp16 pair of channels 2 lane, 2 lane + 1
-  uint32_t o;       // lanes < 4: fp16 K value of outlier channel lane
-  float vs, vz;     // V scale / zero-point of group lane / 16
+  uint32_t o;       // lanes < 4: fp16 K value of outlier channel lane (INT4_ASYM K)
+  float ks;         // INT8 K: the fp16 scale of group lane / 16
+  float vs, vz;     // V of group lane / 16: INT8 fp16 scale, or INT4_ASYM scale / zero-point
 };
 struct AppendFlags {
   bool kbad = false, vbad = false;
   int kclip = 0, vclip = 0;
 };
 
-// oc: the kv head's 4 outlier channels (from the q set-up's inputs)
-template <bool OUT>
+// fp16 scale of group g of the append's static INT8 table tab (fp32 when f32)
+__device__ __forceinline__ float app_int8_scale(const void* tab, int f32, int64_t sh, int64_t sg,
+                                                int hkv, int g) {
+  const int64_t i = (int64_t)hkv * sh + (int64_t)g * sg;
+  const float s = f32 ? reinterpret_cast<const float*>(tab)[i] : (float)reinterpret_cast<const half_t*>(tab)[i];
+  return (float)int8_static_scale16(s, f32 != 0);
+}
+
+// oc: the kv head's 4 outlier channels (from the q set-up's inputs); called by the writer
+template <class KF, class VF>
 __device__ __forceinline__ void append_fetch(const DecodeArgs& a, int b, int hkv, int lane,
-                                             bool writer, int4 oc, AppendIn& in) {
+                                             int4 oc, AppendIn& in) {
   const FusedAppend& f = a.app;
   const half_t* xk = f.kx + (int64_t)b * f.ksb + (int64_t)hkv * f.ksh;
   const half_t* xv = f.vx + (int64_t)b * f.vsb + (int64_t)hkv * f.vsh;
   const rsrc_t rk = buffer_rsrc(xk, kD * 2), rv = buffer_rsrc(xv, kD * 2);
-  in.k2 = bload1(rk, writer ? 4u * lane : kOutOfRange, 0);
-  in.v2 = bload1(rv, writer ? 4u * lane : kOutOfRange, 0);
+  in.k2 = bload1(rk, 4u * lane, 0);
+  in.v2 = bload1(rv, 4u * lane, 0);
   in.o = 0;
-  if constexpr (OUT) {
+  if constexpr (KF::kOut) {
     const int ch = lane == 0 ? oc.x : lane == 1 ? oc.y : lane == 2 ? oc.z : oc.w;
     in.o = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
-        rk, (int)(writer && lane < 4 ? 2u * (uint32_t)ch : kOutOfRange), 0, kBufNT);
+        rk, (int)(lane < 4 ? 2u * (uint32_t)ch : kOutOfRange), 0, kBufNT);
   }
-  // V scale / zero-point of group lane / 16 (fp16, element offsets hkv * ssh + g * ssg)
   const int g = lane >> 4;
-  const uint32_t so = (uint32_t)(hkv * a.v.ssh + g * a.v.ssg) * 2u;
-  // uniform descriptors spanning this kv head's 4 groups
-  const uint32_t tb = (uint32_t)(hkv * a.v.ssh + 3 * a.v.ssg + 1) * 2u;
-  const rsrc_t rs = buffer_rsrc(a.v.scale, tb), rz = buffer_rsrc(a.v.zp, tb);
-  in.vs = (float)__builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
-      rs, (int)(writer ? so : kOutOfRange), 0, 0));
-  in.vz = (float)__builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
-      rz, (int)(writer ? so : kOutOfRange), 0, 0));
+  in.ks = 0.f;
+  if constexpr (!KF::kAsym) in.ks = app_int8_scale(f.kst, f.kst_f32, f.kst_sh, f.kst_sg, hkv, g);
+  if constexpr (VF::kTile32) {
+    // V scale / zero-point of group lane / 16 (fp16, element offsets hkv * ssh + g * ssg)
+    in.vs = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
+    in.vz = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
+  } else {
+    in.vs = app_int8_scale(f.vst, f.vst_f32, f.vst_sh, f.vst_sg, hkv, g);
+    in.vz = 0.f;
+  }
 }
 
-// ks / kz: the K scale / zero-point of group lane / 16 (the q set-up reads the same ones)
-template <bool OUT>
-__device__ __forceinline__ void append_store(const DecodeArgs& a, rsrc_t rk, rsrc_t rv, rsrc_t ro,
-                                             int lane, bool write, const AppendIn& in, float ks,
-                                             float kz, AppendFlags& fl) {
+// ks / kz: the INT4_ASYM K scale / zero-point of group lane / 16 (the q set-up reads the same)
+template <class KF, class VF>
+__device__ __forceinline__ void append_store(const DecodeArgs& a, const KF& kf, const VF& vf,
+                                             int lane, const AppendIn& in, float ks, float kz,
+                                             AppendFlags& fl) {
   const int64_t t = a.app.wpos;
   const half2v k2 = as_h2(in.k2), v2 = as_h2(in.v2);
   int kclip = 0, vclip = 0;
-  uint32_t kb = 0, vb = 0;
-  if (write) {  // wave-uniform: only the writer quantizes
-    kb = asym_pack_pair((float)k2.x, (float)k2.y, ks, kz, kclip);
-    vb = asym_pack_pair((float)v2.x, (float)v2.y, in.vs, in.vz, vclip);
+  if constexpr (KF::kAsym) {
+    const uint32_t kb = asym_pack_pair((float)k2.x, (float)k2.y, ks, kz, kclip);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)kb, kf.rk, (int)(uint32_t)(t * kRowK + lane), 0, 0);
+  } else {
+    const uint16_t kp = int8_pack_pair((float)k2.x, (float)k2.y, (half_t)in.ks, kclip);
+    __builtin_amdgcn_raw_buffer_store_b16(kp, kf.rk, (int)(uint32_t)(t * kD + 2 * lane), 0, 0);
   }
-  __builtin_amdgcn_raw_buffer_store_b8((uint8_t)kb, rk, (int)(write ? (uint32_t)(t * kRowK + lane) : kOutOfRange), 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b8((uint8_t)vb, rv, (int)(write ? (uint32_t)tile32_offset(t, lane) : kOutOfRange), 0, 0);
-  if constexpr (OUT)
-    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)in.o, ro,
-                                          (int)(write && lane < 4 ? (uint32_t)(t * kRowO + 2 * lane) : kOutOfRange), 0, 0);
-  if (write) {
-    fl.kbad |= __ballot(!(__builtin_isfinite((float)k2.x) && __builtin_isfinite((float)k2.y))) != 0;
-    fl.vbad |= __ballot(!(__builtin_isfinite((float)v2.x) && __builtin_isfinite((float)v2.y))) != 0;
-    fl.kclip += wave_sum_int(kclip);
-    fl.vclip += wave_sum_int(vclip);
+  if constexpr (VF::kTile32) {
+    const uint32_t vb = asym_pack_pair((float)v2.x, (float)v2.y, in.vs, in.vz, vclip);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)vb, vf.rv, (int)(uint32_t)tile32_offset(t, lane), 0, 0);
+  } else {
+    const uint16_t vp = int8_pack_pair((float)v2.x, (float)v2.y, (half_t)in.vs, vclip);
+    __builtin_amdgcn_raw_buffer_store_b16(vp, vf.rv, (int)(uint32_t)(t * kD + 2 * lane), 0, 0);
   }
+  if constexpr (KF::kOut)
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)in.o, kf.ro,
+                                          (int)(lane < 4 ? (uint32_t)(t * kRowO + 2 * lane) : kOutOfRange), 0, 0);
+  fl.kbad |= __ballot(!(__builtin_isfinite((float)k2.x) && __builtin_isfinite((float)k2.y))) != 0;
+  fl.vbad |= __ballot(!(__builtin_isfinite((float)v2.x) && __builtin_isfinite((float)v2.y))) != 0;
+  fl.kclip += wave_sum_int(kclip);
+  fl.vclip += wave_sum_int(vclip);
 }
 
 __device__ __forceinline__ void append_status(const FusedAppend& f, const AppendFlags& fl) {
@@ -696,7 +716,7 @@ __device__ __forceinline__ void append_status(const FusedAppend& f, const Append
 template <class KF, class VF, int LOOK, bool PACK8, int WPE = 2>
 __global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
-  constexpr bool APP = KF::kAppend;  // the fused append exists for INT4_ASYM K + TILE32 V
+  constexpr bool APP = KF::kAppend;  // the fused append (the writer's code) is built
   constexpr bool OUT = KF::kOut;
   const int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63;
@@ -732,11 +752,10 @@ void decode_tiled_kernel(DecodeArgs a) {
   vf.setup(a, b, hkv, lane);
   // the fused append's two steps (compiled only for the format that has it)
   auto app_fetch = [&]() {
-    if constexpr (APP) append_fetch<OUT>(a, b, hkv, lane, true, qin.oc, ain);
+    if constexpr (APP) append_fetch<KF, VF>(a, b, hkv, lane, qin.oc, ain);
   };
   auto app_store = [&]() {
-    if constexpr (APP)
-      append_store<OUT>(a, kf.rk, vf.rv, kf.ro, lane, true, ain, (float)qin.s, (float)qin.z, afl);
+    if constexpr (APP) append_store(a, kf, vf, lane, ain, (float)qin.s, (float)qin.z, afl);
   };
 
   // Tile schedule: the n_chunks work-groups of a (b, kv head) interleave, so at step i the

@@ -144,6 +144,28 @@ __device__ __forceinline__ uint8_t asym_pack_pair(float x0, float x1, float s, f
   return (uint8_t)(((c0 + 8) << 4) | (c1 + 8));
 }
 
+// fp16 scale of a static INT8 table entry s: max(s, 1e-5) rounded to fp16
+// (src/quant/int8_basic.py:159).  An fp16 table clamps in fp16: no fp16 value lies strictly
+// between 1e-5 and fp16(1e-5), so clamping at fp16(1e-5) gives the same result.
+__device__ __forceinline__ half_t int8_static_scale16(float s, bool f32) {
+  return f32 ? (half_t)fmaxf(s, 1e-5f) : (half_t)fmaxf(s, (float)(half_t)1e-5f);
+}
+
+// INT8 symmetric with the fp16 scale s16 of the pair's group:
+// c = clamp(rne(fp16(x / s16)), -127, 127), the quotient rounded to fp16 before the integer
+// rounding as torch's Half division does (src/quant/int8_basic.py:111-164).  Returns the two
+// codes as little-endian bytes and adds the codes at +-127 to clipped
+// (src/cache/int8_cache.py:407-419).
+__device__ __forceinline__ uint16_t int8_pack_pair(float x0, float x1, half_t s16, int& clipped) {
+  const float sf = (float)s16;
+  const float q0 = rintf((float)(half_t)__fdiv_rn(x0, sf));
+  const float q1 = rintf((float)(half_t)__fdiv_rn(x1, sf));
+  const int c0 = (int)fminf(fmaxf(q0, -127.f), 127.f);
+  const int c1 = (int)fminf(fmaxf(q1, -127.f), 127.f);
+  clipped += (c0 == 127 || c0 == -127) + (c1 == 127 || c1 == -127);
+  return (uint16_t)((uint8_t)(int8_t)c0 | ((uint16_t)(uint8_t)(int8_t)c1 << 8));
+}
+
 // streaming loads: the code bytes are read once, so do not keep them in the caches
 template <class T>
 __device__ __forceinline__ T ld_stream(const void* p) {

@@ -92,10 +92,7 @@ __device__ __forceinline__ half_t int8_scale16(const AppendDev& a, int h, int g,
     const float dyn = __fdiv_rn(fmaxf(dyn_abs, 1e-5f), 127.0f);  // :348
     s = fmaxf(s, dyn);
   }
-  if (!a.st_f32 && !a.adaptive) {
-    // fp16 static: clamp in fp16 (no fp16 value lies strictly between 1e-5 and fp16(1e-5))
-    return (half_t)fmaxf(s, (float)(half_t)1e-5f);
-  }
+  if (!a.adaptive) return int8_static_scale16(s, a.st_f32);
   return (half_t)fmaxf(s, 1e-5f);                              // int8_basic.py:159
 }
 
@@ -122,13 +119,7 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
   if (a.fmt == KVQ_FMT_INT8_SYM) {
     const half_t s16 = int8_scale16(a, h, g, am);
     const float sf = (float)s16;
-    const float q0 = rintf((float)(half_t)__fdiv_rn(x0, sf));
-    const float q1 = rintf((float)(half_t)__fdiv_rn(x1, sf));
-    const int c0 = (int)fminf(fmaxf(q0, -127.f), 127.f);
-    const int c1 = (int)fminf(fmaxf(q1, -127.f), 127.f);
-    const uint16_t pair = (uint16_t)((uint8_t)(int8_t)c0 | ((uint16_t)(uint8_t)(int8_t)c1 << 8));
-    *reinterpret_cast<uint16_t*>(crow + d0) = pair;
-    clipped = (c0 == 127 || c0 == -127) + (c1 == 127 || c1 == -127);   // int8_cache.py:409
+    *reinterpret_cast<uint16_t*>(crow + d0) = int8_pack_pair(x0, x1, s16, clipped);
     if (a.so && (d0 % a.gs) == 0) {
       const int64_t off = (int64_t)b * a.sosb + (int64_t)h * a.sosh + t * a.sost + (int64_t)g * a.sosg;
       if (a.so_f32) reinterpret_cast<float*>(a.so)[off] = sf;

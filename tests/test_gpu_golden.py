@@ -87,8 +87,14 @@ def test_gpu_matches_golden(path):
                               device=DEV, check_numerics=True)
         append_twice(cache, k, v)
         k8, ks, vc, vs, vz = cache.get_k8v4_tensors(0)
-        assert torch.equal(k8.cpu(), f["k_codes"]) and torch.equal(vc.cpu(), f["v_codes"])
+        S = k.shape[2]
+        assert torch.equal(k8.cpu(), f["k_codes"])
+        assert torch.equal(K.untile_v(vc, S).cpu(), f["v_codes"])  # V is kept in TILE32
         assert torch.equal(ks.cpu(), f["k_scale_tok"])
+        # V as packed rows takes the row-layout kernel
+        out_rows = K.decode_attn_k8v4(qd, k8, ks, K.untile_v(vc, S).contiguous(), vs, vz, cld, sm,
+                                      inv_tau=taud)
+        check_out(out_rows, f["out"], name + " rows")
         out = K.decode_attn_k8v4(qd, k8, ks, vc, vs, vz, cld, sm, inv_tau=taud)
     else:  # configs 0 and 1: INT8 K and V
         cache = K.INT8KVCache(1, device=DEV, group_size=32, static_k_scale=f["k_static"][None],

@@ -576,6 +576,64 @@ def test_fused_append_decode_matches_two_calls(cfg_idx, B, S0, steps, outliers):
         assert_close(out, ref, f"fused step cfg{cfg_idx} S{n}")
 
 
+@pytest.mark.parametrize("kind,B,S0,steps", [
+    ("int8", 2, 4095, 3),   # config 1 heads; the new tokens cross a tile boundary
+    ("int8", 3, 0, 2),      # empty cache: the first token is the whole context
+    ("int8", 4, 700, 2),
+    ("k8v4", 2, 4095, 3),   # config 4 heads (GQA 5), TILE32 V
+    ("k8v4", 3, 40, 2),     # the new token's tile is in each wave's first tiles
+])
+def test_fused_append_decode_int8_matches_two_calls(kind, B, S0, steps):
+    """append_decode_attn with INT8 K (one launch) against append + the decode kernel (two
+    launches) on twin caches: codes and outputs bit-identical, output within tolerance of
+    the oracle."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[1 if kind == "int8" else 4]
+    t = SY.calibrate(cfg, 0)
+    g = gen(900 + S0 + B)
+    k, v = SY.draw_kv(cfg, 0, B, S0 + steps, g)
+    qs = [SY.draw_q(cfg, B, g) for _ in range(steps)]
+    tau = SY.inv_tau(cfg)[0]
+    if kind == "int8":
+        mk = lambda: K.INT8KVCache(1, device=DEV, group_size=32, static_k_scale=t.k_scale[None],
+                                   static_v_scale=t.v_scale[None], check_numerics=True)
+    else:
+        mk = lambda: K.K8V4KVCache(1, t.k_scale[None], t.v_scale[None], t.v_zp[None], device=DEV,
+                                   check_numerics=True)
+    two, one = mk(), mk()
+    if S0:
+        for c in (two, one):
+            c.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
+    sm = 1 / math.sqrt(128)
+    for i in range(steps):
+        kn, vn = k[:, :, S0 + i:S0 + i + 1].to(DEV), v[:, :, S0 + i:S0 + i + 1].to(DEV)
+        q = qs[i].to(DEV)
+        two.append(0, kn, vn)
+        n = two.get_seq_len()
+        cl = torch.full((B,), n, dtype=torch.int32, device=DEV)
+        out = one.append_decode_attn(0, q, kn, vn, sm_scale=sm, inv_tau=tau.to(DEV))
+        assert one.get_seq_len() == n
+        if kind == "int8":
+            k8, v8, ks, vs = two.get_int8_tensors(0)
+            ref_out = K.decode_attn_int8(OA.prescale_q(q, tau.to(DEV)), k8, v8, ks, vs, cl, sm_scale=sm)
+            k8b, v8b, _, _ = one.get_int8_tensors(0)
+            assert torch.equal(k8b, k8) and torch.equal(v8b, v8), f"codes differ at step {i}"
+            ref = OA.decode_attn_int8_torch_ref(OA.prescale_q(qs[i], tau), k8.cpu(), v8.cpu(),
+                                                ks.cpu(), vs.cpu(), cl.cpu(), sm)
+        else:
+            k8, ks, vc, vs, vz = two.get_k8v4_tensors(0)
+            ref_out = K.decode_attn_k8v4(q, k8, ks, vc, vs, vz, cl, sm, inv_tau=tau.to(DEV))
+            k8b, _, vcb, _, _ = one.get_k8v4_tensors(0)
+            assert torch.equal(k8b, k8), f"K codes differ at step {i}"
+            assert torch.equal(K.untile_v(vcb, n), K.untile_v(vc, n)), f"V codes differ at step {i}"
+            ref = OA.decode_attn_k8v4_ref(qs[i], k8.cpu(), ks.cpu(), K.untile_v(vc, n).cpu(),
+                                          vs.cpu(), vz.cpu(), cl.cpu(), sm, inv_tau=tau)
+        assert torch.equal(out, ref_out), f"fused output differs from the two-call path at step {i}"
+        assert_close(out, ref, f"fused {kind} step S{n}")
+
+
 def test_fused_append_decode_nan_raises_and_does_not_advance():
     K = _lib()
     from llm_kvcache_quantization_amd import synthetic as SY
