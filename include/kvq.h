@@ -46,7 +46,8 @@ typedef struct ihipStream_t* kvq_stream_t; /* == hipStream_t */
 
 /* code layouts (kvq_kv_view.layout, kvq_append_params.codes_layout) */
 #define KVQ_LAYOUT_ROWS 0   /* token-major: the code bytes of token t start at t * stride_t */
-#define KVQ_LAYOUT_TILE32 1 /* INT4_ASYM V only: 32-token tiles of 2048 bytes, tile i at
+#define KVQ_LAYOUT_TILE32 1 /* INT4_ASYM V only (with INT4_ASYM K, or INT8_SYM K with a
+                               static group-32 scale): 32-token tiles of 2048 bytes, tile i at
                                i * 32 * stride_t (stride_t must be 64).  Within a tile, byte
                                ((L * 8 + 2 p + k) * 4 + 2 a + j) holds packed byte 4 c + 2 k + j
                                of token T(g, p, a), where L = 16 g + c (g < 4, c < 16),
@@ -91,6 +92,12 @@ typedef struct kvq_kv_view {
  * q' = fp16(q * inv_tau[h]) when inv_tau is given.  Requires head_dim == 128 and
  * q_heads / kv_heads <= 16.  INT4_ASYM requires group_size == 32; the scale formats
  * require group_size in {8, 16, 32, 64, 128}.
+ *
+ * Kernel choice (the same results either way, within the stated tolerance): the tiled
+ * kernel (8-wave work-groups, single-launch merge of the split partials) serves INT4_ASYM K
+ * with TILE32 V, and INT8_SYM K whose scale view is static (stride 0, or size 1, over b and
+ * t; group 32; 128-byte dense rows) with TILE32 INT4_ASYM V or a static INT8_SYM V in dense
+ * rows.  Every other combination runs the row-layout split-K kernel and a combine launch.
  */
 typedef struct kvq_decode_params {
   const void* q;          /* fp16 [B, Hq, D], d contiguous */
@@ -180,11 +187,14 @@ int kvq_quant_append(const kvq_append_params* k, const kvq_append_params* v,
  *   cache.append(layer, k, v)            src/engine/patch_model.py:755
  *   decode_attn_*(q, caches..., ctx)     src/engine/patch_model.py:837-957
  * with the codes and the output bit-identical to kvq_quant_append then kvq_decode_attn.
- * Supported for INT4_ASYM K and V with V in the TILE32 layout (k_new / v_new: seq_new 1,
- * static fp16 tables, no scale policy); k_new and v_new must name the very buffers,
- * tables and strides p reads (codes, outlier side-band), and share write_pos.  Anything
- * else returns KVQ_ERR_UNSUPPORTED (or KVQ_ERR_INVALID), and the caller makes the two
- * calls instead.  The status words are updated as kvq_quant_append does. */
+ * Supported for the formats the tiled kernel serves (see kvq_decode_attn), with k_new /
+ * v_new of seq_new 1, group 32, a static scale table and no scale policy (adaptive,
+ * rescue, scale_out).  k_new and v_new must name the very code buffers and strides p
+ * reads and share write_pos; an INT4_ASYM side must also name p's static tables and
+ * outlier side-band, while an INT8_SYM side quantizes with its own table (fp16 or fp32),
+ * as kvq_quant_append would.  Anything else returns KVQ_ERR_UNSUPPORTED (or
+ * KVQ_ERR_INVALID), and the caller makes the two calls instead.  The status words are
+ * updated as kvq_quant_append does. */
 int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
                            const kvq_append_params* v_new, kvq_stream_t stream);
 
