@@ -166,7 +166,11 @@ __device__ __forceinline__ void merge_store_partial(const DecodeArgs& a, MergeLd
 // lane / 16.
 template <class VF>
 __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv, int nvalid,
-                                             int wave, int lane, float s, float z) {
+                                             int wave, int lane) {
+  // the V epilogue's scale / zero-point, requested with the first partial loads (loaded any
+  // earlier, every work-group's merge would wait for them)
+  float s, z;
+  VF::epi_params(a, hkv, lane, s, z);
   static_assert(kUnitChunks <= 64, "one (m, l) pair per lane");
   for (int h = wave; h < a.n_rep; h += kTW) {
     const int64_t row = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks;
@@ -882,8 +886,6 @@ void decode_tiled_kernel(DecodeArgs a) {
   const int nvalid = valid_chunks(a, ctx);
   uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
   __shared__ int is_last;
-  float vs = 0.f, vz = 0.f;
-  if (a.fused) VF::epi_params(a, hkv, lane, vs, vz);  // for the output (requested early)
   merge_store_partial<PACK8>(a, msh, wave, lane, m, l, acc, b, hkv, chunk);
   if (!a.fused) return;
   __builtin_amdgcn_s_waitcnt(0);
@@ -892,7 +894,7 @@ void decode_tiled_kernel(DecodeArgs a) {
     is_last = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nvalid - 1);
   __syncthreads();
   if (!is_last) return;
-  merge_chunks<VF>(a, b, hkv, nvalid, wave, lane, vs, vz);
+  merge_chunks<VF>(a, b, hkv, nvalid, wave, lane);
   if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
