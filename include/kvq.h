@@ -1,5 +1,5 @@
 /*
- * kvq.h -- C ABI (version 2) of the MI355X (gfx950) quantized-KV decode path.
+ * kvq.h -- C ABI (version 3) of the MI355X (gfx950) quantized-KV decode path.
  *
  * libkvq.so exports three groups of entry points: quantize-on-append, split-K
  * decode attention and error reporting.  Every entry point
@@ -174,11 +174,21 @@ typedef struct kvq_append_params {
   int32_t codes_layout;    /* KVQ_LAYOUT_ROWS, or KVQ_LAYOUT_TILE32 for INT4_ASYM
                               (codes_stride_t must then be 64 and capacity a multiple of 32) */
   int32_t reserved;        /* 0 */
+  void* scratch;           /* device scratch of kvq_append_scratch_bytes() bytes (16-byte
+                              aligned; no initial contents needed) when that is nonzero, else
+                              NULL.  Needed by the INT4_SYM group rescue over more than 4096
+                              (row, group) scales; calls sharing it must be ordered */
+  int64_t scratch_bytes;
 } kvq_append_params;
 
-/* Appends K and V of one layer with one launch (either pointer may be NULL). */
+/* Appends K and V of one layer with one launch (either pointer may be NULL).  The INT4_SYM
+ * group rescue takes torch.quantile's threshold over the dynamic group scales of the whole
+ * call (src/cache/int4_cache.py:384-390): up to 4096 (row, group) scales inside the launch,
+ * beyond that by an exact radix select over p->scratch (a few short launches first). */
 int kvq_quant_append(const kvq_append_params* k, const kvq_append_params* v,
                      kvq_stream_t stream);
+/* bytes of scratch kvq_quant_append needs for p (0: none) */
+int64_t kvq_append_scratch_bytes(const kvq_append_params* p);
 
 /* Decode step of one layer in one launch: quantize-on-append of one new token per
  * (b, kv head) followed by the decode attention of p over the cache that now holds it.
@@ -200,7 +210,7 @@ int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* 
 
 /* message for the last non-OK return on this thread ("" if none) */
 const char* kvq_last_error(void);
-/* ABI version (increments on incompatible changes to the structs above); this is 2 */
+/* ABI version (increments on incompatible changes to the structs above); this is 3 */
 int32_t kvq_abi_version(void);
 
 #ifdef __cplusplus

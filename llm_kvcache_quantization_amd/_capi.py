@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before libkvq.so, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 KVQ_OK = 0
 KVQ_ERR_INVALID = 1
@@ -106,6 +106,7 @@ class AppendParams(ctypes.Structure):
         ("capacity", c_i64),
         ("status", c_vp),
         ("codes_layout", c_i32), ("reserved", c_i32),
+        ("scratch", c_vp), ("scratch_bytes", c_i64),
     ]
 
 
@@ -115,6 +116,7 @@ EXPORTED_SYMBOLS = (
     "kvq_decode_chunk_tokens",
     "kvq_decode_workspace_bytes",
     "kvq_quant_append",
+    "kvq_append_scratch_bytes",
     "kvq_last_error",
     "kvq_abi_version",
 )
@@ -153,6 +155,8 @@ def lib() -> ctypes.CDLL:
         L.kvq_decode_workspace_bytes.restype = c_i64
         L.kvq_quant_append.argtypes = [ctypes.POINTER(AppendParams), ctypes.POINTER(AppendParams), c_vp]
         L.kvq_quant_append.restype = c_i32
+        L.kvq_append_scratch_bytes.argtypes = [ctypes.POINTER(AppendParams)]
+        L.kvq_append_scratch_bytes.restype = c_i64
         L.kvq_append_decode_attn.argtypes = [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams),
                                              ctypes.POINTER(AppendParams), c_vp]
         L.kvq_append_decode_attn.restype = c_i32

@@ -377,8 +377,15 @@ class _SymCacheBase(_EngineBase):
                 p.scale_out = scale_buf.data_ptr()
                 p.scale_out_dtype = C.KVQ_DTYPE_F32 if scale_buf.dtype == torch.float32 else C.KVQ_DTYPE_F16
                 p.so_stride_b, p.so_stride_h, p.so_stride_t, p.so_stride_g = scale_buf.stride()
+            # the group rescue over more than 4096 (row, group) scales selects its
+            # threshold in a scratch buffer
+            scratch = None
+            nbytes = int(C.lib().kvq_append_scratch_bytes(ctypes.byref(p)))
+            if nbytes:
+                scratch = torch.empty(nbytes, dtype=torch.uint8, device=codes.device)
+                p.scratch, p.scratch_bytes = scratch.data_ptr(), nbytes
             # keep the (possibly temporary) tensors alive until the launch returns
-            p._keep = (xs, st)
+            p._keep = (xs, st, scratch)
         return pk, pv
 
     def _pre_append_checks(self, layer_id: int) -> None:

@@ -953,4 +953,4 @@ extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_appe
 }
 
 extern "C" const char* kvq_last_error(void) { return g_last_error.c_str(); }
-extern "C" int32_t kvq_abi_version(void) { return 2; }
+extern "C" int32_t kvq_abi_version(void) { return 3; }

@@ -53,6 +53,22 @@ struct AppendDev {
   int64_t wpos;
   int32_t* status;
   int tile32;  // codes in KVQ_LAYOUT_TILE32 (INT4_ASYM)
+  const float* thr_ptr;  // group-rescue threshold computed by the large-n select, or NULL
+};
+
+// Scratch of the group rescue over more than kRescueMax (row, group) scales: an exact radix
+// select, over the fp32 bit patterns of the append's dynamic group scales (all positive,
+// so their bit patterns sort as their values; a NaN sorts last as in torch.sort), of
+// sorted[lo] (4 histogram passes of 8 bits), then sorted[hi] (lo + 1) from the count of
+// values <= sorted[lo] and the least value above it, then torch.quantile's interpolation.
+struct RescueScratch {
+  uint32_t hist[256];
+  uint32_t prefix;  // bits of sorted[lo] fixed so far (all 32 after the last pass)
+  uint32_t rank;    // rank of sorted[lo] among the values that match prefix
+  uint32_t cnt_le;  // number of values <= sorted[lo]
+  uint32_t min_gt;  // least bit pattern above sorted[lo]
+  float thr;
+  uint32_t pad[3];
 };
 
 __device__ __forceinline__ float ld_static(const AppendDev& a, int h, int g) {
@@ -94,6 +110,114 @@ __device__ __forceinline__ half_t int8_scale16(const AppendDev& a, int h, int g,
   }
   if (!a.adaptive) return int8_static_scale16(s, a.st_f32);
   return (half_t)fmaxf(s, 1e-5f);                              // int8_basic.py:159
+}
+
+// Calls f(bits) for the fp32 bit pattern of the dynamic scale fmax(absmax, 1e-5) / 7 of every
+// (row, group) of the append (int4_cache.py:344-358), one wave per row, grid-stride.
+template <class F>
+__device__ __forceinline__ void for_each_dyn(const AppendDev& a, F f) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = a.B * a.H * a.S;
+  for (int row = blockIdx.x * kAppendWaves + wave; row < rows; row += gridDim.x * kAppendWaves) {
+    const int s_idx = row % a.S, bh = row / a.S, h = bh % a.H, b = bh / a.H;
+    const half_t* xr = a.x + (int64_t)b * a.xsb + (int64_t)h * a.xsh + (int64_t)s_idx * a.xss;
+    const half2v xv = *reinterpret_cast<const half2v*>(xr + 2 * lane);
+    const float am = group_max(fmaxf(fabsf((float)xv.x), fabsf((float)xv.y)), a.gs);
+    if ((2 * lane) % a.gs == 0) f(__float_as_uint(__fdiv_rn(fmaxf(am, 1e-5f), 7.0f)));
+  }
+}
+
+// rank of torch.quantile's lower order statistic: lo = floor(fp32(q) * (n - 1)); hi = ceil
+__device__ __forceinline__ void quantile_ranks(float q, int64_t n, int64_t& lo, int64_t& hi, float& w) {
+  const float rank = __fmul_rn(q, (float)(n - 1));
+  lo = (int64_t)floorf(rank);
+  hi = (int64_t)ceilf(rank);
+  w = __fsub_rn(rank, (float)lo);
+}
+
+__global__ void rescue_init_kernel(RescueScratch* s, float q, int64_t n) {
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) s->hist[i] = 0;
+  if (threadIdx.x == 0) {
+    int64_t lo, hi;
+    float w;
+    quantile_ranks(q, n, lo, hi, w);
+    s->prefix = 0;
+    s->rank = (uint32_t)lo;
+    s->cnt_le = 0;
+    s->min_gt = 0xFFFFFFFFu;
+  }
+}
+
+// histogram of digit `pass` (bits [24 - 8 pass, 32 - 8 pass)) over the values whose higher
+// digits equal the prefix found so far
+__global__ __launch_bounds__(kAppendWaves * 64) void rescue_hist_kernel(AppendDev a, RescueScratch* s,
+                                                                         int pass) {
+  __shared__ uint32_t h[256];
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) h[i] = 0;
+  __syncthreads();
+  const uint32_t pre = s->prefix;
+  const int sh = 24 - 8 * pass;
+  for_each_dyn(a, [&](uint32_t bits) {
+    if (pass == 0 || (bits >> (sh + 8)) == (pre >> (sh + 8))) atomicAdd(&h[(bits >> sh) & 255u], 1u);
+  });
+  __syncthreads();
+  for (int i = threadIdx.x; i < 256; i += blockDim.x)
+    if (h[i]) atomicAdd(&s->hist[i], h[i]);
+}
+
+// picks the digit whose bucket holds the remaining rank, and clears the histogram
+__global__ void rescue_select_kernel(RescueScratch* s, int pass) {
+  __shared__ uint32_t digit, before;
+  if (threadIdx.x == 0) {
+    uint32_t cum = 0, d = 255, r = s->rank;
+    for (uint32_t i = 0; i < 256; ++i) {
+      const uint32_t c = s->hist[i];
+      if (r < cum + c) {
+        d = i;
+        break;
+      }
+      cum += c;
+    }
+    digit = d;
+    before = cum;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) s->hist[i] = 0;
+  if (threadIdx.x == 0) {
+    s->prefix |= digit << (24 - 8 * pass);
+    s->rank -= before;
+  }
+}
+
+// number of values <= sorted[lo] and the least value above it
+__global__ __launch_bounds__(kAppendWaves * 64) void rescue_count_kernel(AppendDev a, RescueScratch* s) {
+  __shared__ uint32_t cnt, mn;
+  if (threadIdx.x == 0) {
+    cnt = 0;
+    mn = 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  const uint32_t lo_bits = s->prefix;
+  for_each_dyn(a, [&](uint32_t bits) {
+    if (bits <= lo_bits) atomicAdd(&cnt, 1u);
+    else atomicMin(&mn, bits);
+  });
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (cnt) atomicAdd(&s->cnt_le, cnt);
+    if (mn != 0xFFFFFFFFu) atomicMin(&s->min_gt, mn);
+  }
+}
+
+// torch.quantile's interpolation of sorted[lo] and sorted[hi] (sorted_quantile's arithmetic)
+__global__ void rescue_thr_kernel(RescueScratch* s, float q, int64_t n) {
+  int64_t lo, hi;
+  float w;
+  quantile_ranks(q, n, lo, hi, w);
+  const float va = __uint_as_float(s->prefix);
+  const float vb = (hi < (int64_t)s->cnt_le) ? va : __uint_as_float(s->min_gt);
+  const float diff = __fsub_rn(vb, va);
+  s->thr = w < 0.5f ? __fadd_rn(va, __fmul_rn(w, diff)) : __fsub_rn(vb, __fmul_rn(diff, __fsub_rn(1.0f, w)));
 }
 
 __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
@@ -204,7 +328,7 @@ __global__ __launch_bounds__(kAppendWaves * 64) void append_kernel(AppendDev k, 
   if (!a.valid) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rows = a.B * a.H * a.S;
-  float thr = 0.f;
+  float thr = a.thr_ptr ? *a.thr_ptr : 0.f;
   if (rescue && a.fmt == KVQ_FMT_INT4_SYM && a.st != nullptr && a.rq > 0.f && !a.rescue_all) {
     // Global threshold over every (row, group) dynamic scale of this append
     // (int4_cache.py:384-389).  Single work-group: grid.x == 1 on this path.
@@ -272,10 +396,6 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
     if (p->codes_stride_t != 64 || p->capacity % 32)
       return fail(KVQ_ERR_INVALID, n + ": TILE32 needs codes_stride_t == 64 and capacity % 32 == 0");
   }
-  if (p->format == KVQ_FMT_INT4_SYM && p->static_scale && p->rescue_quantile > 0.f &&
-      !p->rescue_all && (int64_t)p->batch * p->heads * p->seq_new * (128 / gs) > kRescueMax)
-    return fail(KVQ_ERR_UNSUPPORTED,
-                n + ": outlier rescue supports at most 4096 (row, group) scales per append");
   d.valid = p->batch * p->heads * p->seq_new > 0;
   d.fmt = p->format;
   d.x = reinterpret_cast<const half_t*>(p->x);
@@ -302,7 +422,36 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
 
 static bool needs_rescue(const kvq_append_params* p) {
   return p && p->format == KVQ_FMT_INT4_SYM && p->static_scale && p->rescue_quantile > 0.f &&
-         !p->rescue_all;
+         !p->rescue_all && p->batch * p->heads * p->seq_new > 0;
+}
+
+// (row, group) scales the group rescue of p takes its quantile over
+static int64_t rescue_n(const kvq_append_params* p) {
+  return (int64_t)p->batch * p->heads * p->seq_new * (128 / p->group_size);
+}
+
+// the threshold of p's group rescue over more than kRescueMax scales, into its scratch
+static int rescue_large(const kvq_append_params* p, AppendDev& d, const char* name, hipStream_t st) {
+  const std::string n(name);
+  if (!p->scratch || p->scratch_bytes < (int64_t)sizeof(RescueScratch) || ((uintptr_t)p->scratch % 16))
+    return fail(KVQ_ERR_INVALID, n + ": outlier rescue over more than 4096 (row, group) scales needs "
+                                     "a 16-byte aligned scratch of kvq_append_scratch_bytes() bytes");
+  RescueScratch* s = reinterpret_cast<RescueScratch*>(p->scratch);
+  const int64_t cnt = rescue_n(p);
+  if (cnt >= ((int64_t)1 << 31)) return fail(KVQ_ERR_UNSUPPORTED, n + ": too many (row, group) scales");
+  const int64_t rows = (int64_t)p->batch * p->heads * p->seq_new;
+  int64_t gx = (rows + kAppendWaves - 1) / kAppendWaves;
+  if (gx > 2048) gx = 2048;
+  const dim3 grid((unsigned)gx), block(kAppendWaves * 64);
+  hipLaunchKernelGGL(rescue_init_kernel, dim3(1), dim3(256), 0, st, s, p->rescue_quantile, cnt);
+  for (int pass = 0; pass < 4; ++pass) {
+    hipLaunchKernelGGL(rescue_hist_kernel, grid, block, 0, st, d, s, pass);
+    hipLaunchKernelGGL(rescue_select_kernel, dim3(1), dim3(256), 0, st, s, pass);
+  }
+  hipLaunchKernelGGL(rescue_count_kernel, grid, block, 0, st, d, s);
+  hipLaunchKernelGGL(rescue_thr_kernel, dim3(1), dim3(1), 0, st, s, p->rescue_quantile, cnt);
+  d.thr_ptr = &s->thr;
+  return KVQ_OK;
 }
 
 }  // namespace kvq
@@ -317,16 +466,28 @@ extern "C" int kvq_quant_append(const kvq_append_params* k, const kvq_append_par
   rc = fill_dev(v, dv, "v");
   if (rc) return rc;
   if (!dk.valid && !dv.valid) return KVQ_OK;
-  const int rescue = needs_rescue(k) || needs_rescue(v);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // the group rescue takes its threshold from one work-group's LDS sort when every side
+  // that needs one has at most kRescueMax scales, else from the radix select (scratch)
+  const bool large = (needs_rescue(k) && rescue_n(k) > kRescueMax) ||
+                     (needs_rescue(v) && rescue_n(v) > kRescueMax);
+  if (large) {
+    if (needs_rescue(k) && (rc = rescue_large(k, dk, "k", s))) return rc;
+    if (needs_rescue(v) && (rc = rescue_large(v, dv, "v", s))) return rc;
+  }
+  const int rescue = !large && (needs_rescue(k) || needs_rescue(v));
   int64_t rows = 0;
   if (dk.valid) rows = (int64_t)dk.B * dk.H * dk.S;
   if (dv.valid) rows = rows > (int64_t)dv.B * dv.H * dv.S ? rows : (int64_t)dv.B * dv.H * dv.S;
   int64_t gx = rescue ? 1 : (rows + kAppendWaves - 1) / kAppendWaves;
   if (gx > 65535) gx = 65535;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(append_kernel, dim3((unsigned)gx, 2), dim3(kAppendWaves * 64), 0, s, dk, dv,
                      rescue);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
   return KVQ_OK;
+}
+
+extern "C" int64_t kvq_append_scratch_bytes(const kvq_append_params* p) {
+  return (needs_rescue(p) && rescue_n(p) > kRescueMax) ? (int64_t)sizeof(RescueScratch) : 0;
 }

@@ -19,7 +19,8 @@ def declared_functions():
 def test_header_declares_entry_points():
     assert declared_functions() == sorted([
         "kvq_abi_version", "kvq_append_decode_attn", "kvq_decode_attn", "kvq_decode_chunk_tokens",
-        "kvq_decode_workspace_bytes", "kvq_last_error", "kvq_quant_append"])
+        "kvq_append_scratch_bytes", "kvq_decode_workspace_bytes", "kvq_last_error",
+        "kvq_quant_append"])
 
 
 def test_library_loads_and_exports_all_symbols():

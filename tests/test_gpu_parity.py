@@ -4,6 +4,7 @@ Quantized codes and scales must be bit-exact.  Attention outputs must be within
 max-abs 2e-3 of the dequantise-then-attention oracle with cosine >= 0.9999 (the
 tolerance BASELINE.json's north star states for fp16 outputs).
 """
+import ctypes
 import math
 
 import pytest
@@ -119,6 +120,44 @@ def test_append_int4_sym_bitexact(mode, S):
         ref_q, ref_s = OQ.int4_cache_quantize(x, stt, gs, **ref_kw)
         assert torch.equal(p_gpu.cpu(), OQ.pack_int4(ref_q)), (mode, tag)
         assert torch.equal(s_gpu.cpu().float(), ref_s.float()), (mode, tag)
+
+
+@pytest.mark.parametrize("B,H,S,ratio,ties", [
+    (2, 4, 2048, 0.01, False),    # 65,536 scales: the radix-select path
+    (1, 2, 600, 0.3, True),       # 4,800 scales, many equal (ties at the threshold)
+    (4, 2, 4096, 0.001, False),   # 131,072 scales, a threshold in the far tail
+    (2, 2, 256, 0.05, False),     # 4,096 scales: the one-work-group sort path
+])
+def test_append_int4_rescue_large_bitexact(B, H, S, ratio, ties):
+    """INT4 group outlier rescue over the dynamic scales of a prefill-sized append: the
+    torch.quantile threshold (int4_cache.py:384-390) by the radix select in the scratch
+    buffer (more than 4096 scales) or the LDS sort, codes and scales bit-exact."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import _capi as C
+
+    g = gen(3000 + S)
+    D, gs = 128, 32
+    k = (torch.randn(B, H, S, D, generator=g) * 1.5).to(torch.float16)
+    v = torch.randn(B, H, S, D, generator=g).to(torch.float16)
+    if ties:  # few distinct group absmax values
+        k = (k * 4).round().div(4).to(torch.float16)
+        v = (v * 2).round().div(2).to(torch.float16)
+    k[0, 1, 7, 70] = 25.0
+    st = torch.rand(H, D // gs, generator=g) * 0.3 + 0.1
+    cache = K.INT4KVCache(1, device=DEV, group_size=gs, static_k_scale=st[None],
+                          static_v_scale=(st * 0.8)[None], check_numerics=False,
+                          outlier_rescue_ratio=ratio)
+    p = C.AppendParams()
+    p.format, p.batch, p.heads, p.seq_new, p.group_size = C.KVQ_FMT_INT4_SYM, B, H, S, gs
+    p.static_scale, p.rescue_quantile = 1, float(torch.tensor(1.0 - ratio, dtype=torch.float32))
+    n = B * H * S * (D // gs)
+    assert (C.lib().kvq_append_scratch_bytes(ctypes.byref(p)) > 0) == (n > 4096)
+    cache.append(0, k.to(DEV), v.to(DEV))
+    kp, vp, ks, vs = cache.get_int4_tensors(0)
+    for x, stt, p_gpu, s_gpu, tag in ((k, st, kp, ks, "k"), (v, st * 0.8, vp, vs, "v")):
+        ref_q, ref_s = OQ.int4_cache_quantize(x, stt, gs, outlier_rescue_ratio=ratio)
+        assert torch.equal(s_gpu.cpu().float(), ref_s.float()), (tag, n)
+        assert torch.equal(p_gpu.cpu(), OQ.pack_int4(ref_q)), (tag, n)
 
 
 @pytest.mark.parametrize("outliers", [False, True])
