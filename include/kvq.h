@@ -44,6 +44,13 @@ typedef struct ihipStream_t* kvq_stream_t; /* == hipStream_t */
                                and zero-point per (kv head, group of 32); optional fp16
                                side-band holding n_outlier channels per K head verbatim */
 
+#define KVQ_FMT_INT4_KIVI 4  /* packed nibbles as INT4_SYM, codes in [-8,7], value c * s + z
+                               with fp32 s, z (src/quant/asymmetric_quant.py:24-196,
+                               src/cache/kivi_style_cache.py): K per (b, h, channel)
+                               [B,H,D] (scale_stride_b/_h/_g, channels contiguous), V per
+                               (b, h, token) [B,H,T] (scale_stride_b/_h/_t, tokens
+                               contiguous); zero_point has the scale's strides */
+
 /* code layouts (kvq_kv_view.layout, kvq_append_params.codes_layout) */
 #define KVQ_LAYOUT_ROWS 0   /* token-major: the code bytes of token t start at t * stride_t */
 #define KVQ_LAYOUT_TILE32 1 /* INT4_ASYM V only (with INT4_ASYM K, or INT8_SYM K with a

@@ -29,6 +29,7 @@ KVQ_DTYPE_F32 = 1
 KVQ_FMT_INT8_SYM = 1
 KVQ_FMT_INT4_SYM = 2
 KVQ_FMT_INT4_ASYM = 3
+KVQ_FMT_INT4_KIVI = 4
 
 KVQ_LAYOUT_ROWS = 0
 KVQ_LAYOUT_TILE32 = 1

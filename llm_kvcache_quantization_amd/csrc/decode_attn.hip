@@ -550,7 +550,8 @@ static const void* selected_kernel() {
 }
 
 // (k_format, v_format, scale dtype) -> kernel family; 0 means unsupported
-enum Family { kNone = 0, kI8I8_16, kI8I8_32, kI4I4_16, kI4I4_32, kA4A4, kA4A4o, kI8A4_16, kI8A4_32 };
+enum Family { kNone = 0, kI8I8_16, kI8I8_32, kI4I4_16, kI4I4_32, kA4A4, kA4A4o, kI8A4_16, kI8A4_32,
+              kKivi };
 
 static Family family(int kf, int vf, int ksf32, int vsf32, int kout) {
   if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT8_SYM && ksf32 == vsf32)
@@ -559,6 +560,7 @@ static Family family(int kf, int vf, int ksf32, int vsf32, int kout) {
     return ksf32 ? kI4I4_32 : kI4I4_16;
   if (kf == KVQ_FMT_INT4_ASYM && vf == KVQ_FMT_INT4_ASYM) return kout ? kA4A4o : kA4A4;
   if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT4_ASYM) return ksf32 ? kI8A4_32 : kI8A4_16;
+  if (kf == KVQ_FMT_INT4_KIVI && vf == KVQ_FMT_INT4_KIVI) return kKivi;  // tiled kernel only
   return kNone;
 }
 
@@ -609,6 +611,11 @@ static bool static_over_bt(const kvq_kv_view& v, const kvq_decode_params* p) {
 
 static int tiled_family(const kvq_decode_params* p) {
   const bool vt = p->v.layout == KVQ_LAYOUT_TILE32;
+  if (p->k_format == KVQ_FMT_INT4_KIVI)
+    return (p->v_format == KVQ_FMT_INT4_KIVI && !vt && p->k.stride_t == kD / 2 &&
+            p->v.stride_t == kD / 2)
+               ? kTiledKivi
+               : kTiledNone;
   if (p->k_format == KVQ_FMT_INT4_ASYM)
     return (p->v_format == KVQ_FMT_INT4_ASYM && vt) ? (p->k.n_outlier > 0 ? kTiledA4A4o : kTiledA4A4)
                                                      : kTiledNone;
@@ -702,6 +709,29 @@ static int check_view(const kvq_kv_view& v, int fmt, bool is_k, const char* name
                 n + ": code rows must be " + std::to_string(need) + "-byte aligned");
   if (v.scale_dtype != KVQ_DTYPE_F16 && v.scale_dtype != KVQ_DTYPE_F32)
     return fail(KVQ_ERR_INVALID, n + ": scale_dtype must be F16 or F32");
+  if (fmt == KVQ_FMT_INT4_KIVI) {
+    if (v.layout != KVQ_LAYOUT_ROWS)
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI codes are in token rows");
+    if (v.stride_t != kD / 2)
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI needs dense 64-byte token rows");
+    if (v.scale_dtype != KVQ_DTYPE_F32 || !v.zero_point)
+      return fail(KVQ_ERR_INVALID, n + ": INT4_KIVI needs fp32 scale and zero_point");
+    if (v.n_outlier != 0) return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
+    if (is_k) {
+      // the 8 channels of a lane are read as two 16-byte vectors
+      if (v.scale_stride_g != 1)
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI K parameters need contiguous channels");
+      if (!aligned(v.scale, 16) || !aligned(v.zero_point, 16) || v.scale_stride_b % 4 ||
+          v.scale_stride_h % 4)
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI K parameter rows must be 16-byte aligned");
+    } else {
+      if (v.scale_stride_t != 1)
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI V parameters need contiguous tokens");
+      if (!aligned(v.scale, 4) || !aligned(v.zero_point, 4))
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI V parameters must be 4-byte aligned");
+    }
+    return KVQ_OK;
+  }
   if (fmt == KVQ_FMT_INT4_ASYM) {
     if (gs != 32) return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_ASYM needs group_size 32");
     if (v.scale_dtype != KVQ_DTYPE_F16)
@@ -792,6 +822,8 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   if (p->v.layout == KVQ_LAYOUT_TILE32 && !tiled)
     return fail(KVQ_ERR_UNSUPPORTED,
                 "TILE32 V needs INT4_ASYM K or INT8 K with a static group-32 scale in dense rows");
+  if (fam == kKivi && !tiled)
+    return fail(KVQ_ERR_UNSUPPORTED, "INT4_KIVI K and V need dense 64-byte token rows");
   if (tiled && p->k_format == KVQ_FMT_INT4_ASYM &&
       (p->k.stride_t != kD / 2 || (p->k.n_outlier && p->k.outlier_stride_t != 4)))
     return fail(KVQ_ERR_UNSUPPORTED, "with TILE32 V, K rows and outlier rows must be dense");

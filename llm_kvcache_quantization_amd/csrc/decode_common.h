@@ -119,8 +119,9 @@ __device__ __forceinline__ void load_q_group(const half_t* qr, int lg, half_t ta
 // Returns the fp16 probabilities (rounded toward zero) as the PV B operand, in k-slot
 // order [4lg, 4lg+1, 4lg+2, 4lg+3, 16+4lg, .., 16+4lg+3]; l accumulates exactly those
 // fp16 values.
+// ex: optional two more running sums of the format (rescaled with l and acc)
 __device__ __forceinline__ half8v softmax_tile(float4v x0, float4v x1, float sm, float& m,
-                                               float& l, float4v acc[8]) {
+                                               float& l, float4v acc[8], float* ex = nullptr) {
   const float lmax = max8f(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]) * sm;
   if (__ballot(lmax > m + kTau)) {
     // raise the running max of every head to its current wave-wide maximum
@@ -130,6 +131,10 @@ __device__ __forceinline__ half8v softmax_tile(float4v x0, float4v x1, float sm,
     l *= alpha;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+    if (ex) {
+      ex[0] *= alpha;
+      ex[1] *= alpha;
+    }
   }
   const float nm = -m;
   const half2v pp0 = pk_rtz(fast_exp2(fmaf(x0[0], sm, nm)), fast_exp2(fmaf(x0[1], sm, nm)));
@@ -163,7 +168,7 @@ __device__ __forceinline__ float dpp_ror8f(float old, float src) {
 // lane h and the block-1 part in lane h + 8 (merge_and_store adds them).  The returned PV
 // operand is valid in lanes h < 8; lanes 8..15 carry finite values of padding columns.
 __device__ __forceinline__ half8v softmax_tile8(float4v x0, float4v x1, float sm, float& m,
-                                                float& l, float4v acc[8]) {
+                                                float& l, float4v acc[8], float* ex = nullptr) {
   float y[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) y[r] = dpp_ror8f<0xC>(x0[r], x1[r]);
@@ -176,6 +181,10 @@ __device__ __forceinline__ half8v softmax_tile8(float4v x0, float4v x1, float sm
     l *= alpha;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+    if (ex) {
+      ex[0] *= alpha;
+      ex[1] *= alpha;
+    }
   }
   const float nm = -m;
   const half2v pa = pk_rtz(fast_exp2(fmaf(y[0], sm, nm)), fast_exp2(fmaf(y[1], sm, nm)));
@@ -333,6 +342,7 @@ enum TiledFam {
   kTiledA4A4o,  // the same with 4 fp16 outlier K channels
   kTiledI8A4,   // INT8_SYM K (static scale), INT4_ASYM V in the TILE32 layout
   kTiledI8I8,   // INT8_SYM K and V (static scales), token rows
+  kTiledKivi,   // INT4_KIVI K (per-channel) and V (per-token), token rows
 };
 // kernel of family fam for n_rep query heads per kv head, or nullptr
 const void* tiled_kernel(int fam, int n_rep);

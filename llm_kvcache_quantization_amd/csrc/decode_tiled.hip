@@ -259,6 +259,7 @@ struct QIn {
 // and q' of those channels in the first two k-slots of each lane group.
 template <bool OUT>
 struct KAsymT {
+  using QInT = QIn;
   static constexpr bool kAppend = true;  // the fused quantize-on-append is built for this format
   static constexpr bool kAsym = true;
   static constexpr bool kOut = OUT;
@@ -405,6 +406,11 @@ struct KAsymT {
 // combine_kernel applies out = s (acc / l - off) + z with off = 72 or 1032.
 struct VAsymT {
   static constexpr bool kTile32 = true;
+  // hooks of formats with per-token parameters (none here)
+  template <class Raw>
+  __device__ __forceinline__ void mask(Raw&, int, int, int) const {}
+  __device__ __forceinline__ void finalize(float4v*, int) const {}
+  __device__ __forceinline__ float* extra() { return nullptr; }
   rsrc_t rv;
   uint32_t vv;
   struct Raw {
@@ -484,6 +490,7 @@ __device__ __forceinline__ uint32_t i8pair_deq(uint32_t x, half2v s2) {
 // reference's dequantised k = fp16(c * s16) (i8pair_deq), the B operand q', so the logits
 // are the reference's fp32 dot products of fp16 k and q up to the summation order.
 struct KI8T {
+  using QInT = QIn;
   static constexpr bool kAppend = true;
   static constexpr bool kAsym = false;
   static constexpr bool kOut = false;
@@ -569,6 +576,11 @@ struct KI8T {
 // acc / l is the output.
 struct VI8RowT {
   static constexpr bool kTile32 = false;
+  // hooks of formats with per-token parameters (none here)
+  template <class Raw>
+  __device__ __forceinline__ void mask(Raw&, int, int, int) const {}
+  __device__ __forceinline__ void finalize(float4v*, int) const {}
+  __device__ __forceinline__ float* extra() { return nullptr; }
   rsrc_t rv;
   uint32_t vv;
   half2v s2;  // the scale of group col / 4, twice
@@ -616,6 +628,185 @@ struct VI8RowT {
         R[p] = i8pair_deq(perm_b32(hi, lo, sel), s2);
       }
       acc[c] = mfma16x16x32(pack8(R[0], R[1], R[2], R[3]), pb, acc[c]);
+    }
+  }
+};
+
+// ---- KIVI layout (the reference's asymmetric INT4 kernels,
+// src/kernels/triton_decode_attn_int4_asym.py:28-277 and its v2 / GQA variants): packed
+// nibbles in token rows, K value (n - 8) s_d + z_d with fp32 s, z per (b, h, channel), V
+// value (n - 8) s_t + z_t with fp32 s, z per (b, h, token).
+
+// q-side inputs of KKiviT: the lane's 8 channels' K scale and zero-point
+struct KiviQIn {
+  u32x4 q;
+  half_t tau, s, z;  // s, z unused (the fused append is not built for this format)
+  int4 oc;
+  float4v ks[2], kz[2];
+};
+
+// K of the KIVI layout: as KAsymT<false> (subnormal nibbles, one fp16 q operand, logits x
+// 2^-24) with per-channel parameters: operand fp16(q'_d s_d) (/ 16 for a high nibble) and
+// the constant term sum_d q'_d (z_d - 8 s_d) in fp32.
+struct KKiviT : KAsymT<false> {
+  using QInT = KiviQIn;
+  static constexpr bool kAppend = false;
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, KiviQIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.oc = int4{-1, -1, -1, -1};
+    const int64_t o = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh + 32 * lg + 8 * (wave & 3);
+    const float* ps = reinterpret_cast<const float*>(a.k.scale) + o;
+    const float* pz = reinterpret_cast<const float*>(a.k.zp) + o;
+    in.ks[0] = *reinterpret_cast<const float4v*>(ps);
+    in.ks[1] = *reinterpret_cast<const float4v*>(ps + 4);
+    in.kz[0] = *reinterpret_cast<const float4v*>(pz);
+    in.kz[1] = *reinterpret_cast<const float4v*>(pz + 4);
+  }
+  __device__ void setup_q(const DecodeArgs& a, const KiviQIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15, lg = lane >> 4;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    float part = 0.f;
+    half_t vh[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = slot_elem(k);
+      const half2v h2 = as_h2(qw[e >> 1]);
+      const float qd = valid ? (float)qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : 0.f;
+      const float sd = in.ks[e >> 2][e & 3], zd = in.kz[e >> 2][e & 3];
+      const float P = qd * sd;
+      vh[k] = (half_t)(slot_high(k) ? P * 0.0625f : P);
+      part += qd * fmaf(-8.0f, sd, zd);
+    }
+    part = wave_sum_xor_groups(part);
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+    if (lg == 0) sh.bias[j][col] = part;
+  }
+  __device__ void finish_setup(const QShareLds& sh, const KiviQIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+    const int col = lane & 15;
+    bias = (sh.bias[0][col] + sh.bias[1][col]) + (sh.bias[2][col] + sh.bias[3][col]);
+  }
+};
+
+// V of the KIVI layout in token rows (64 bytes).  Lane (col, lg) reads the dword of
+// channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens T(k) (four 64-byte rows
+// per load instruction) and their fp32 scale / zero-point.  With p' = fp16(p s_t) (round
+// to nearest) as the B operand and the codes as x = 64 + n (even channel) or 1024 + n (odd),
+//   sum_t p v ~= sum_t p' x - (off + 8) sum_t p' + sum_t p z_t,   off = 64 or 1024,
+// i.e. the rounding of p' multiplies the centred code c = n - 8 (|c| <= 8), so the error
+// of a term is at most 8 s 2^-11 of its weight.  The wave keeps Lp = sum p' and
+// Cz = sum p z beside l, and finalize() folds them into acc before the merge (out = acc / l).
+struct VKiviRowT {
+  static constexpr bool kTile32 = false;
+  rsrc_t rv, rs, rz;
+  uint32_t vv, vp;
+  float ex[2];  // Lp, Cz (rescaled with l by the softmax)
+  struct Raw {
+    uint32_t w[8];     // token T(k): bytes 4 col .. 4 col + 3
+    float4v s[2], z[2];  // tokens 4 lg + i, 16 + 4 lg + i
+  };
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * (kD / 2)));
+    vv = (uint32_t)((4 * lg) * (kD / 2) + 4 * col);
+    const int64_t po = (int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh;
+    rs = buffer_rsrc(reinterpret_cast<const float*>(a.v.scale) + po, (uint32_t)(a.cap * 4));
+    rz = buffer_rsrc(reinterpret_cast<const float*>(a.v.zp) + po, (uint32_t)(a.cap * 4));
+    vp = (uint32_t)(4 * lg) * 4u;
+    ex[0] = ex[1] = 0.f;
+  }
+  __device__ __forceinline__ float* extra() { return ex; }
+  // rows of a partial last tile past the capacity read 0; !valid: every load out of range
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * (kD / 2) : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      r.w[k] = bload1(rv, v + t * (kD / 2), 0);
+    }
+    const uint32_t p = vp + (valid ? (uint32_t)tok * 4u : kOutOfRange);
+    r.s[0] = __builtin_bit_cast(float4v, bload4(rs, p, 0));
+    r.s[1] = __builtin_bit_cast(float4v, bload4(rs, p + 64u, 0));
+    r.z[0] = __builtin_bit_cast(float4v, bload4(rz, p, 0));
+    r.z[1] = __builtin_bit_cast(float4v, bload4(rz, p + 64u, 0));
+  }
+  // tokens at or past the context in the last, partial tile: parameters 0 (their memory
+  // may hold anything; p is 0 there)
+  __device__ __forceinline__ void mask(Raw& r, int tt, int ctx, int lg) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (tt + 4 * lg + i >= ctx) r.s[0][i] = r.z[0][i] = 0.f;
+      if (tt + 16 + 4 * lg + i >= ctx) r.s[1][i] = r.z[1][i] = 0.f;
+    }
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8], const NibConsts& nc) {
+    float sk[8], wk[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sk[i] = r.s[0][i];
+      sk[4 + i] = r.s[1][i];
+      wk[i] = r.z[0][i];
+      wk[4 + i] = r.z[1][i];
+    }
+    float cz = ex[1];
+    uint32_t pp[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float p0 = (float)pb[2 * q], p1 = (float)pb[2 * q + 1];
+      cz = fmaf(p0, wk[2 * q], cz);
+      cz = fmaf(p1, wk[2 * q + 1], cz);
+      pp[q] = as_u32(half2v{(half_t)(p0 * sk[2 * q]), (half_t)(p1 * sk[2 * q + 1])});
+    }
+    ex[1] = cz;
+    const half2v ones = {(half_t)1.0f, (half_t)1.0f};
+    float lp = ex[0];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lp = __builtin_amdgcn_fdot2(as_h2(pp[q]), ones, lp, false);
+    ex[0] = lp;
+    const half8v ps = pack8(pp[0], pp[1], pp[2], pp[3]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // byte j of the tokens T(2p), T(2p + 1) into the low bytes of the two halves
+      const uint32_t sel = (uint32_t)j | 0x0C00u | ((uint32_t)(4 + j) << 16) | 0x0C000000u;
+      uint32_t R[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) R[p] = perm_b32(r.w[2 * p + 1], r.w[2 * p], sel);
+      acc[2 * j] = mfma16x16x32(pack8(and_or(R[0], nc.m_hi, nc.c64), and_or(R[1], nc.m_hi, nc.c64),
+                                      and_or(R[2], nc.m_hi, nc.c64), and_or(R[3], nc.m_hi, nc.c64)),
+                                ps, acc[2 * j]);
+      acc[2 * j + 1] =
+          mfma16x16x32(pack8(and_or(R[0], nc.m_lo, nc.c1024), and_or(R[1], nc.m_lo, nc.c1024),
+                             and_or(R[2], nc.m_lo, nc.c1024), and_or(R[3], nc.m_lo, nc.c1024)),
+                       ps, acc[2 * j + 1]);
+    }
+  }
+  // acc[mb][r] (channel 32 lg + 8 r + mb) += Cz - (off + 8) Lp, with Lp, Cz summed over
+  // the lane groups (the k-slots of a head); off = 64 (even channel) or 1024 (odd)
+  __device__ __forceinline__ void finalize(float4v acc[8], int lane) {
+    (void)lane;
+    const float lp = wave_sum_xor_groups(ex[0]), cz = wave_sum_xor_groups(ex[1]);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const float d = fmaf(-((mb & 1) ? 1032.0f : 72.0f), lp, cz);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mb][r] += d;
     }
   }
 };
@@ -749,7 +940,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   KF kf;
   // the q-side inputs are requested first: the wait for them then does not include the
   // cache tiles requested next
-  QIn qin;
+  typename KF::QInT qin;
   kf.fetch_q(a, b, hkv, lane, wave, qin);
   kf.setup_addr(a, b, hkv, lane);
   VF vf;
@@ -859,10 +1050,13 @@ void decode_tiled_kernel(DecodeArgs a) {
         vf.load(kTile * tile[LOOK], tile[LOOK] < ntot, vr[(u + LOOK) % R]);
         if (tile[1] < ntot) kf.qk(kr[(u + 1) % R], nc, x[(u + 1) & 1][0], x[(u + 1) & 1][1]);
         float4v x0 = x[u & 1][0], x1 = x[u & 1][1];
-        if (partial && tile[0] == ntot - 1) mask_tile(x0, x1, kTile * tile[0], ctx, lg);
+        if (partial && tile[0] == ntot - 1) {
+          mask_tile(x0, x1, kTile * tile[0], ctx, lg);
+          vf.mask(vr[u % R], kTile * tile[0], ctx, lg);
+        }
         half8v pb;
-        if constexpr (PACK8) pb = softmax_tile8(x0, x1, sm, m, l, acc);
-        else pb = softmax_tile(x0, x1, sm, m, l, acc);
+        if constexpr (PACK8) pb = softmax_tile8(x0, x1, sm, m, l, acc, vf.extra());
+        else pb = softmax_tile(x0, x1, sm, m, l, acc, vf.extra());
         vf.mma(vr[u % R], pb, acc, nc);
         ++steps;
         progress[wave] = steps;
@@ -886,6 +1080,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   const int nvalid = valid_chunks(a, ctx);
   uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
   __shared__ int is_last;
+  vf.finalize(acc, lane);
   merge_store_partial<PACK8>(a, msh, wave, lane, m, l, acc, b, hkv, chunk);
   if (!a.fused) return;
   __builtin_amdgcn_s_waitcnt(0);
@@ -912,6 +1107,7 @@ const void* tiled_ptr_fam(int fam) {
     case kTiledA4A4o: return tiled_ptr<KAsymT<true>, VAsymT, PACK8>();
     case kTiledI8A4: return tiled_ptr<KI8T, VAsymT, PACK8>();
     case kTiledI8I8: return tiled_ptr<KI8T, VI8RowT, PACK8>();
+    case kTiledKivi: return tiled_ptr<KKiviT, VKiviRowT, PACK8>();
     default: return nullptr;
   }
 }

@@ -423,6 +423,99 @@ def _decode_tok(q, k_cache, v_cache, k_scale, v_scale, context_lens, sm_scale, d
     return out
 
 
+def kv_view_kivi(codes: torch.Tensor, scale: torch.Tensor, zero_point: torch.Tensor,
+                 per_channel: bool) -> C.KvView:
+    """View of KIVI-layout packed INT4 rows [B,H,T,64] with fp32 scale / zero-point
+    (same strides): per channel [B,H,D] (K) or per token [B,H,T] (V)."""
+    v = C.KvView()
+    v.codes = codes.data_ptr()
+    v.layout = C.KVQ_LAYOUT_ROWS
+    v.stride_b, v.stride_h, v.stride_t = codes.stride(0), codes.stride(1), codes.stride(2)
+    v.scale = scale.data_ptr()
+    v.scale_stride_b, v.scale_stride_h = scale.stride(0), scale.stride(1)
+    if per_channel:
+        v.scale_stride_t, v.scale_stride_g = 0, scale.stride(2)
+    else:
+        v.scale_stride_t, v.scale_stride_g = scale.stride(2), 0
+    v.scale_dtype = C.KVQ_DTYPE_F32
+    v.zero_point = zero_point.data_ptr()
+    v._keep = (codes, scale, zero_point)
+    return v
+
+
+def _kivi_params(t: torch.Tensor, shape) -> torch.Tensor:
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"KIVI scale/zero-point must be {tuple(shape)}, got {tuple(t.shape)}")
+    t = t if t.dtype == torch.float32 else t.float()
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def decode_attn_int4_kivi(
+    q: torch.Tensor,
+    k_cache_packed: torch.Tensor,
+    v_cache_packed: torch.Tensor,
+    k_scale: torch.Tensor,
+    k_zp: torch.Tensor,
+    v_scale: torch.Tensor,
+    v_zp: torch.Tensor,
+    context_lens: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    block_size: Optional[int] = None,
+    *,
+    inv_tau: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention over the KIVI layout (src/kernels/triton_decode_attn_int4_asym.py:163-277):
+    packed INT4 K/V rows [B, Hkv, S, 64] (byte = ((c[2i]+8) << 4) | (c[2i+1]+8)),
+    per-channel K scale / zero-point [B, Hkv, D], per-token V scale / zero-point
+    [B, Hkv, S]; value c * s + z.  Parameters are used in fp32 (fp16 ones are widened, as
+    the reference does); q is computed in fp16 and the output has q's dtype.  block_size
+    is accepted for signature compatibility: the split over the context is chosen by the
+    library.  inv_tau (fp16 [Hq]) is an optional per-head query scale.
+    """
+    if q.ndim != 3 or q.shape[-1] != HEAD_DIM:
+        raise ValueError(f"q must be [B, Hq, 128], got {tuple(q.shape)}")
+    if k_cache_packed.ndim != 4 or v_cache_packed.ndim != 4:
+        raise ValueError(f"cache must be [B, Hkv, S, D//2], got K={tuple(k_cache_packed.shape)} "
+                         f"V={tuple(v_cache_packed.shape)}")
+    if k_scale.ndim != 3 or k_zp.ndim != 3:
+        raise ValueError(f"k_scale/k_zp must be [B, Hkv, D], got {tuple(k_scale.shape)}/{tuple(k_zp.shape)}")
+    if v_scale.ndim != 3 or v_zp.ndim != 3:
+        raise ValueError(f"v_scale/v_zp must be [B, Hkv, S], got {tuple(v_scale.shape)}/{tuple(v_zp.shape)}")
+    if not q.is_cuda:
+        raise ValueError("requires GPU (ROCm) tensors")
+    B, Hq, D = q.shape
+    Hkv, S = k_cache_packed.shape[1], k_cache_packed.shape[2]
+    for c in (k_cache_packed, v_cache_packed):
+        if tuple(c.shape) != (B, Hkv, S, D // 2) or c.dtype not in (torch.int8, torch.uint8):
+            raise ValueError(f"packed codes must be int8/uint8 [{B}, {Hkv}, {S}, 64], got {tuple(c.shape)}")
+    if Hq % Hkv:
+        raise ValueError(f"q_heads={Hq} not multiple of kv_heads={Hkv}")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    _resolve_block_size(block_size, S)
+    ks, kz = _kivi_params(k_scale, (B, Hkv, D)), _kivi_params(k_zp, (B, Hkv, D))
+    vs, vz = _kivi_params(v_scale, (B, Hkv, S)), _kivi_params(v_zp, (B, Hkv, S))
+    kc = k_cache_packed if k_cache_packed.stride(-1) == 1 and k_cache_packed.stride(2) == D // 2 \
+        else k_cache_packed.contiguous()
+    vc = v_cache_packed if v_cache_packed.stride(-1) == 1 and v_cache_packed.stride(2) == D // 2 \
+        else v_cache_packed.contiguous()
+    original_dtype = q.dtype
+    q16 = q if q.dtype == torch.float16 else q.to(torch.float16)
+    plan = DecodePlan(
+        q16, C.KVQ_FMT_INT4_KIVI, kv_view_kivi(kc, ks, kz, True),
+        C.KVQ_FMT_INT4_KIVI, kv_view_kivi(vc, vs, vz, False),
+        _ctx_i32(context_lens, q.device), Hkv, S, sm_scale, 32, inv_tau=inv_tau,
+        keepalive=(kc, vc, ks, kz, vs, vz))
+    out = plan.launch()
+    return out if original_dtype == torch.float16 else out.to(original_dtype)
+
+
+# the reference's v2 and GQA-tiled kernels compute the same function with other tilings
+# (src/kernels/triton_decode_attn_int4_asym_v2.py:186, triton_decode_attn_int4_asym_gqa.py:204)
+decode_attn_int4_asym_v2 = decode_attn_int4_kivi
+decode_attn_int4_asym_gqa = decode_attn_int4_kivi
+
+
 def decode_attn_int4_asym(
     q: torch.Tensor,
     k_codes: torch.Tensor,
@@ -433,12 +526,15 @@ def decode_attn_int4_asym(
     v_zp: torch.Tensor,
     context_lens: torch.Tensor,
     sm_scale: Optional[float] = None,
+    block_size: Optional[int] = None,
     *,
     inv_tau: Optional[torch.Tensor] = None,
     k_outlier_idx: Optional[torch.Tensor] = None,
     k_outlier_val: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Attention over the asymmetric INT4 group-32 format (build-native).
+    """Attention over the asymmetric INT4 group-32 format (build-native); with
+    k_scale of rank 3 ([B, Hkv, D], the reference's signature) the KIVI layout
+    (:func:`decode_attn_int4_kivi`).
 
     k_codes: packed uint8/int8 [B, Hkv, S, 64]; v_codes: the same, or V in the TILE32
     layout [B, Hkv, ceil(S/32), 2048] (:func:`tile_v`); k_scale/k_zp/v_scale/v_zp: fp16
@@ -447,6 +543,11 @@ def decode_attn_int4_asym(
     [Hq] per-head query scale, applied as fp16(q * inv_tau) like the reference
     (src/engine/patch_model.py:711-746).
     """
+    if k_scale.ndim == 3:
+        if k_outlier_idx is not None:
+            raise ValueError("outlier channels are not part of the KIVI layout")
+        return decode_attn_int4_kivi(q, k_codes, v_codes, k_scale, k_zp, v_scale, v_zp,
+                                     context_lens, sm_scale, block_size, inv_tau=inv_tau)
     _check_static_args(q, k_codes, v_codes, (k_scale, k_zp, v_scale, v_zp), context_lens)
     if (k_outlier_idx is None) != (k_outlier_val is None):
         raise ValueError("k_outlier_idx and k_outlier_val must be given together")

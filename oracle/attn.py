@@ -18,7 +18,7 @@ from typing import Optional
 
 import torch
 
-from .quant import dequantize_asymmetric_static, unpack_int4
+from .quant import dequantize_asymmetric_static, dequantize_kivi, unpack_int4
 
 
 def prescale_q(q: torch.Tensor, inv_tau: Optional[torch.Tensor]) -> torch.Tensor:
@@ -109,4 +109,14 @@ def decode_attn_k8v4_ref(q, k_int8, k_scale16, v_packed, v_scale, v_zp, context_
     G = k_scale16.shape[-1]
     k = (k_int8.view(B, H, S, G, D // G).to(torch.float16) * k_scale16.unsqueeze(-1)).view(B, H, S, D)
     v = dequantize_asymmetric_static(unpack_int4(v_packed), v_scale, v_zp)
+    return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)
+
+
+def decode_attn_kivi_ref(q, k_packed, v_packed, k_scale, k_zp, v_scale, v_zp, context_lens,
+                         sm_scale, inv_tau=None):
+    """KIVI layout (src/kernels/triton_decode_attn_int4_asym.py:28-160): K and V dequantised
+    in fp32 ((n - 8) s + z, K per channel, V per token), fp32 logits of fp16 q, fp32
+    softmax and PV."""
+    k = dequantize_kivi(unpack_int4(k_packed), k_scale, k_zp, per_channel=True)
+    v = dequantize_kivi(unpack_int4(v_packed), v_scale, v_zp, per_channel=False)
     return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)

@@ -266,3 +266,60 @@ def dequantize_asymmetric_static(q: torch.Tensor, scale16, zp16, group_size: int
     s = scale16.float()[None, :, None, :, None]
     z = zp16.float()[None, :, None, :, None]
     return (q.view(B, H, S, G, group_size).float() * s + z).view(B, H, S, D)
+
+
+# ---------------------------------------------------------------- KIVI (asymmetric, fp32)
+
+
+def quantize_asymmetric(x: torch.Tensor, axis: int, quant_bits: int = 4,
+                        percentile: float = 100.0):
+    """Asymmetric quantization along one axis (src/quant/asymmetric_quant.py:24-141):
+    t_min / t_max over the axis in fp32 (torch.quantile of both tails for percentile < 100),
+    s = max(t_max - t_min, max(1e-5, fp16_tiny * (qmax - qmin))) / (qmax - qmin),
+    z = t_min - qmin * s, q = clamp(round((x - z) / s), qmin, qmax).
+    Returns (int8 codes, fp32 s, fp32 z) with the axis removed from s and z."""
+    check_finite(x, "quantize_asymmetric")
+    if quant_bits not in (4, 8):
+        raise ValueError(f"quant_bits must be 4 or 8, got {quant_bits}")
+    if not (50.0 < percentile <= 100.0):
+        raise ValueError(f"percentile must be in (50.0, 100.0], got {percentile}")
+    qmin, qmax = (-128, 127) if quant_bits == 8 else (-8, 7)
+    axis = axis + x.ndim if axis < 0 else axis
+    xf = x.float()
+    if percentile < 100.0:
+        t_min = torch.quantile(xf, (100.0 - percentile) / 100.0, dim=axis, keepdim=True)
+        t_max = torch.quantile(xf, percentile / 100.0, dim=axis, keepdim=True)
+    else:
+        t_min = xf.amin(dim=axis, keepdim=True)
+        t_max = xf.amax(dim=axis, keepdim=True)
+    floor = max(1e-5, float(torch.finfo(torch.float16).tiny) * (qmax - qmin))
+    s = (t_max - t_min).clamp(min=floor) / (qmax - qmin)
+    z = t_min - qmin * s
+    q = torch.round((xf - z) / s).clamp(qmin, qmax).to(torch.int8)
+    return q, s.squeeze(axis), z.squeeze(axis)
+
+
+def quantize_asymmetric_per_channel(k: torch.Tensor, quant_bits: int = 4, percentile: float = 100.0):
+    """K [B,H,S,D] over the tokens: s, z [B,H,D] (src/quant/asymmetric_quant.py:199-224)."""
+    return quantize_asymmetric(k, 2, quant_bits, percentile)
+
+
+def quantize_asymmetric_per_token(v: torch.Tensor, quant_bits: int = 4, percentile: float = 100.0):
+    """V [B,H,S,D] over the channels: s, z [B,H,S] (src/quant/asymmetric_quant.py:246-270)."""
+    return quantize_asymmetric(v, 3, quant_bits, percentile)
+
+
+def kivi_quantize_k_static(k: torch.Tensor, s: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+    """Decode-time K with the frozen per-channel parameters [B,H,D]
+    (src/cache/kivi_style_cache.py:548-566): clamp(round((fp32(k) - z) / s), -8, 7)."""
+    check_finite(k, "kivi_quantize_k_static")
+    return torch.round((k.float() - z.float().unsqueeze(2)) / s.float().unsqueeze(2)) \
+        .clamp(-8, 7).to(torch.int8)
+
+
+def dequantize_kivi(q: torch.Tensor, s: torch.Tensor, z: torch.Tensor, per_channel: bool) -> torch.Tensor:
+    """q * s + z in fp32 (src/quant/asymmetric_quant.py:144-196): s, z [B,H,D] broadcast
+    over tokens (per channel) or [B,H,S] over channels (per token)."""
+    if per_channel:
+        return q.float() * s.float().unsqueeze(2) + z.float().unsqueeze(2)
+    return q.float() * s.float().unsqueeze(-1) + z.float().unsqueeze(-1)

@@ -692,3 +692,76 @@ def test_fused_append_decode_nan_raises_and_does_not_advance():
     assert cache.get_seq_len() == 64
     out = cache.append_decode_attn(0, q, k[:, :, 64:].to(DEV), v[:, :, 64:].to(DEV))
     assert cache.get_seq_len() == 65 and torch.isfinite(out.float()).all()
+
+
+# ---------------------------------------------------------------- KIVI layout
+
+
+def _kivi_case(B, Hq, Hkv, S, ctx, seed, garbage=True):
+    """Prefill-style KIVI cache: per-channel K and per-token V parameters from the oracle's
+    quantizers over the whole capacity; past each context the V parameters are NaN / inf
+    (memory the reference masks) when garbage is set."""
+    g = gen(seed)
+    D = 128
+    q = torch.randn(B, Hq, D, generator=g).to(torch.float16)
+    k = torch.randn(B, Hkv, S, D, generator=g) * (torch.rand(1, Hkv, 1, D, generator=g) * 3 + 0.2)
+    # |v| stays below 4: there fp16 outputs step by 2^-9 < 2e-3, so a single-token context
+    # (out = v) meets the absolute bound; from 4 up one rounding flip alone is 3.9e-3
+    v = (torch.randn(B, Hkv, S, D, generator=g) * 0.6 + torch.randn(1, Hkv, S, 1, generator=g) * 0.4
+         ).clamp(-3.9, 3.9)
+    qk, ks, kz = OQ.quantize_asymmetric_per_channel(k, 4)
+    qv, vs, vz = OQ.quantize_asymmetric_per_token(v, 4)
+    kp, vp = OQ.pack_int4(qk), OQ.pack_int4(qv)
+    ctx_t = torch.tensor(ctx, dtype=torch.int32)
+    vs_d, vz_d = vs.clone(), vz.clone()
+    if garbage:
+        for b, c in enumerate(ctx):
+            vs_d[b, :, c:] = float("nan")
+            vz_d[b, :, c:] = float("inf")
+    return q, kp, vp, ks, kz, vs, vz, vs_d, vz_d, ctx_t
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,ctx", [
+    (2, 8, 2, 300, [300, 77]),
+    (1, 28, 4, 1000, [1000]),
+    (3, 12, 2, 64, [64, 1, 0]),
+    (1, 16, 1, 4500, [4500]),
+    (2, 4, 4, 9000, [9000, 5003]),
+    (1, 9, 1, 33, [33]),
+])
+def test_decode_kivi_parity(B, Hq, Hkv, S, ctx):
+    K = _lib()
+    q, kp, vp, ks, kz, vs, vz, vs_d, vz_d, ctx_t = _kivi_case(B, Hq, Hkv, S, ctx, 31 + S)
+    ref = OA.decode_attn_kivi_ref(q, kp, vp, ks, kz, vs, vz, ctx_t, 1 / math.sqrt(128))
+    d = lambda t: t.to(DEV)  # noqa: E731
+    out = K.kernels.decode_attn_int4_asym(d(q), d(kp), d(vp), d(ks), d(kz), d(vs_d), d(vz_d),
+                                          d(ctx_t))
+    torch.cuda.synchronize()
+    assert_close(out, ref, f"kivi B{B} Hq{Hq} Hkv{Hkv} S{S}")
+
+
+def test_decode_kivi_inv_tau_bf16_q_and_fp16_params():
+    K = _lib()
+    B, Hq, Hkv, S, ctx = 2, 8, 2, 700, [700, 390]
+    q, kp, vp, ks, kz, vs, vz, vs_d, vz_d, ctx_t = _kivi_case(B, Hq, Hkv, S, ctx, 77, garbage=False)
+    g = gen(78)
+    tau = (torch.rand(Hq, generator=g) + 0.5).to(torch.float16)
+    # fp16 parameters are widened to fp32 (the reference converts them the same way)
+    ks16, kz16 = ks.half(), kz.half()
+    ref = OA.decode_attn_kivi_ref(q, kp, vp, ks16.float(), kz16.float(), vs, vz, ctx_t, 0.07,
+                                  inv_tau=tau)
+    d = lambda t: t.to(DEV)  # noqa: E731
+    out = K.kernels.decode_attn_int4_kivi(d(q).to(torch.bfloat16), d(kp), d(vp), d(ks16), d(kz16),
+                                          d(vs), d(vz), d(ctx_t), 0.07, inv_tau=d(tau))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16
+    # bf16 q is rounded to fp16 first
+    ref16 = OA.decode_attn_kivi_ref(q.to(torch.bfloat16).to(torch.float16), kp, vp, ks16.float(),
+                                    kz16.float(), vs, vz, ctx_t, 0.07, inv_tau=tau)
+    o, r = out.float().cpu(), ref16.float()
+    # the fp16 result rounded to bf16: within 2e-3 plus half a bf16 ulp of the fp16 oracle
+    err = (o - r).abs() - r.abs() * 2.0 ** -8
+    print(f"[kivi bf16 q] max_excess={err.max().item():.3e}", flush=True)
+    assert torch.isfinite(o).all() and (err <= ATOL).all()
+    # the bf16 rounding of q moves the result measurably: the fp16-q oracle is a different case
+    assert (ref - ref16).abs().max().item() > 0
