@@ -186,6 +186,13 @@ typedef struct kvq_append_params {
                               NULL.  Needed by the INT4_SYM group rescue over more than 4096
                               (row, group) scales; calls sharing it must be ordered */
   int64_t scratch_bytes;
+  /* INT4_KIVI (src/cache/kivi_style_cache.py:407-605): K with static_scale / static_zp fp32
+     [B,H,D] (static_stride_b / _h, static_stride_g = the channel stride) quantized as
+     clamp(rint((x - z_d) / s_d), -8, 7); V with static_scale NULL: per-token parameters
+     from the token's min / max over its 128 channels, s = max(max - min, 15 * 2^-14) / 15,
+     z = min + 8 s, written as fp32 to scale_out (so_stride_b/_h/_t) and zp_out (same strides) */
+  int64_t static_stride_b;  /* elements */
+  void* zp_out;
 } kvq_append_params;
 
 /* Appends K and V of one layer with one launch (either pointer may be NULL).  The INT4_SYM

@@ -11,12 +11,15 @@ from .kernels import (  # noqa: F401
     DecodePlan,
     decode_attn_int4,
     decode_attn_int4_asym,
+    decode_attn_int4_asym_gqa,
+    decode_attn_int4_asym_v2,
+    decode_attn_int4_kivi,
     decode_attn_int8,
     decode_attn_k8v4,
     tile_v,
     untile_v,
 )
-from .cache import INT4AsymKVCache, INT4KVCache, INT8KVCache, K8V4KVCache  # noqa: F401
+from .cache import INT4AsymKVCache, INT4KVCache, INT8KVCache, K8V4KVCache, KIVIStyleKVCache  # noqa: F401
 
 __all__ = [
     "DecodePlan",
@@ -30,4 +33,8 @@ __all__ = [
     "INT4KVCache",
     "INT4AsymKVCache",
     "K8V4KVCache",
+    "KIVIStyleKVCache",
+    "decode_attn_int4_kivi",
+    "decode_attn_int4_asym_v2",
+    "decode_attn_int4_asym_gqa",
 ]

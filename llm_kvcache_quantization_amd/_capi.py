@@ -108,6 +108,7 @@ class AppendParams(ctypes.Structure):
         ("status", c_vp),
         ("codes_layout", c_i32), ("reserved", c_i32),
         ("scratch", c_vp), ("scratch_bytes", c_i64),
+        ("static_stride_b", c_i64), ("zp_out", c_vp),
     ]
 
 

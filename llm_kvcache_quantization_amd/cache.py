@@ -949,3 +949,184 @@ class K8V4KVCache(_StaticG32Cache):
         ks = self.k_scale[layer_id].clamp(min=1e-5)[None, :, None, :].expand(B, H, n, 4)
         vt = self._v[layer_id][:, :, :-(-n // TILE_TOKENS)]
         return k, ks, vt, self.v_scale[layer_id], self.v_zp[layer_id]
+
+
+class KIVIStyleKVCache(_EngineBase):
+    """KIVI-style INT4 cache (src/cache/kivi_style_cache.py:38-900): K quantized per
+    channel with scale / zero-point frozen at prefill ([B, H, D] fp32), V per token
+    ([B, H, T] fp32), both as packed nibbles [B, H, T, 64] (byte = ((c[2i]+8) << 4) |
+    (c[2i+1]+8)).  Every token is quantized by kvq_quant_append (HIP); the prefill's
+    per-channel K range is reduced with torch.aminmax as the reference does.  Decode
+    attention reads the cache in place (kvq_decode_attn, format INT4_KIVI).
+
+    Built: quant_bits=4, percentiles 100, residual_length 0; the other settings of the
+    reference raise NotImplementedError.
+    """
+
+    _min_capacity = 256
+
+    def __init__(self, num_layers: int, device: str = "cuda", dtype: torch.dtype = torch.float16,
+                 max_seq_len: Optional[int] = None, quant_bits: int = 8,
+                 k_percentile: float = 100.0, v_percentile: float = 100.0,
+                 inv_tau: Optional[Tensor] = None, use_attn_temperature: bool = False,
+                 residual_length: int = 0, decode_attn_impl: str = "hip_fused",
+                 check_numerics: bool = True):
+        if num_layers <= 0:
+            raise ValueError(f"num_layers must be > 0, got {num_layers}")
+        if quant_bits not in (4, 8):
+            raise ValueError(f"quant_bits must be 4 or 8, got {quant_bits}")
+        if quant_bits != 4:
+            raise NotImplementedError("only the bit-packed INT4 KIVI layout is built (quant_bits=4)")
+        if k_percentile != 100.0 or v_percentile != 100.0:
+            raise NotImplementedError("percentile clipping of the KIVI parameters is not built")
+        if residual_length:
+            raise NotImplementedError("the fp16 residual window is not built (residual_length=0)")
+        self._init_common(num_layers, device, max_seq_len, decode_attn_impl, check_numerics)
+        self.dtype = dtype
+        self.quant_bits, self.bit_packed = 4, True
+        self.k_percentile, self.v_percentile = k_percentile, v_percentile
+        self.residual_length = 0
+        self.inv_tau = inv_tau
+        self.use_attn_temperature = bool(use_attn_temperature)
+        self._scale_dtype = torch.float32
+        n = num_layers
+        self._k_cache: List[Optional[Tensor]] = [None] * n
+        self._v_cache: List[Optional[Tensor]] = [None] * n
+        self._k_scale: List[Optional[Tensor]] = [None] * n
+        self._k_zp: List[Optional[Tensor]] = [None] * n
+        self._v_scale: List[Optional[Tensor]] = [None] * n
+        self._v_zp: List[Optional[Tensor]] = [None] * n
+        self._k_scale_initialized = [False] * n
+
+    def _ensure(self, layer_id: int, B: int, H: int, target: int, device) -> None:
+        cap = self._layer_capacity[layer_id]
+        if self._k_cache[layer_id] is not None and target <= cap:
+            return
+        new_cap = self._new_capacity(layer_id, target, cap)
+        new_cap = ((new_cap + TILE_TOKENS - 1) // TILE_TOKENS) * TILE_TOKENS
+        old = self._layer_seq_lens[layer_id]
+        # int8 storage of the packed bytes, as the reference keeps them
+        kc = torch.zeros(B, H, new_cap, 64, dtype=torch.int8, device=device)
+        vc = torch.zeros_like(kc)
+        vs = torch.zeros(B, H, new_cap, dtype=torch.float32, device=device)
+        vz = torch.zeros_like(vs)
+        if self._k_cache[layer_id] is not None and old > 0:
+            kc[:, :, :old] = self._k_cache[layer_id][:, :, :old]
+            vc[:, :, :old] = self._v_cache[layer_id][:, :, :old]
+            vs[:, :, :old] = self._v_scale[layer_id][:, :, :old]
+            vz[:, :, :old] = self._v_zp[layer_id][:, :, :old]
+        self._k_cache[layer_id], self._v_cache[layer_id] = kc, vc
+        self._v_scale[layer_id], self._v_zp[layer_id] = vs, vz
+        self._layer_capacity[layer_id] = new_cap
+
+    def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        if D != 128:
+            raise NotImplementedError("head_dim 128 only")
+        if k.dtype != torch.float16 or v.dtype != torch.float16:
+            raise NotImplementedError("fp16 K/V inputs only")
+        old = self._layer_seq_lens[layer_id]
+        if S == 0:
+            return
+        self._ensure(layer_id, B, H, old + S, k.device)
+        if not self._k_scale_initialized[layer_id]:
+            # prefill: per-channel range over the incoming tokens (asymmetric_quant.py:102-141)
+            if self.check_numerics and not bool(torch.isfinite(k).all()):
+                raise ValueError("quantize_asymmetric: input contains NaN or Inf")
+            t_min, t_max = torch.aminmax(k.float(), dim=2)
+            floor = max(1e-5, float(torch.finfo(torch.float16).tiny) * 15)
+            # IEEE division, as the formula reads and torch computes it on the CPU (a GPU
+            # tensor divided by a Python scalar is multiplied by fp32(1/15) instead)
+            rng = (t_max - t_min).clamp(min=floor)
+            s = rng / torch.full_like(rng, 15.0)
+            self._k_scale[layer_id] = s.contiguous()
+            self._k_zp[layer_id] = (t_min - (-8) * s).contiguous()
+            self._k_scale_initialized[layer_id] = True
+        ks, kz = self._k_scale[layer_id], self._k_zp[layer_id]
+        if tuple(ks.shape) != (B, H, D):
+            raise ValueError(f"Inconsistent decode K scale/zp shape for layer {layer_id}: "
+                             f"expected {(B, H, D)}, got {tuple(ks.shape)}")
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv = C.AppendParams(), C.AppendParams()
+        ksx = k if k.stride(-1) == 1 else k.contiguous()
+        vsx = v if v.stride(-1) == 1 else v.contiguous()
+        sp = None if status is None else status.data_ptr()
+        _fill_append(pk, C.KVQ_FMT_INT4_KIVI, ksx, 32, self._k_cache[layer_id], old, sp)
+        pk.static_scale, pk.static_zp = ks.data_ptr(), kz.data_ptr()
+        pk.static_scale_dtype = C.KVQ_DTYPE_F32
+        pk.static_stride_b, pk.static_stride_h, pk.static_stride_g = ks.stride()
+        _fill_append(pv, C.KVQ_FMT_INT4_KIVI, vsx, 32, self._v_cache[layer_id], old,
+                     None if sp is None else sp + 8)
+        vs, vz = self._v_scale[layer_id], self._v_zp[layer_id]
+        pv.scale_out, pv.zp_out, pv.scale_out_dtype = vs.data_ptr(), vz.data_ptr(), C.KVQ_DTYPE_F32
+        pv.so_stride_b, pv.so_stride_h, pv.so_stride_t = vs.stride()
+        C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
+                                         ctypes.c_void_p(C.stream_handle(k.device))))
+        if status is not None:
+            self._check_status(layer_id, k.numel(), "KIVI", "[-8, 7]")
+        self._layer_seq_lens[layer_id] = old + S
+        if layer_id == 0:
+            self._seq_len = old + S
+
+    def get_int4_asym_tensors(self, layer_id: int):
+        """(k_packed, v_packed, k_scale, k_zp, v_scale, v_zp) over the stored tokens, the
+        reference's kernel arguments (kivi_style_cache.py:668-700)."""
+        n = self._check_layer(layer_id)
+        return (self._k_cache[layer_id][:, :, :n], self._v_cache[layer_id][:, :, :n],
+                self._k_scale[layer_id], self._k_zp[layer_id],
+                self._v_scale[layer_id][:, :, :n], self._v_zp[layer_id][:, :, :n])
+
+    def _check_layer(self, layer_id: int) -> int:
+        if layer_id < 0 or layer_id >= self.num_layers:
+            raise ValueError(f"layer_id {layer_id} out of range [0, {self.num_layers})")
+        if self._k_cache[layer_id] is None:
+            raise ValueError(f"Cache for layer {layer_id} is empty")
+        n = self._layer_seq_lens[layer_id]
+        if n <= 0:
+            raise ValueError(f"Cache for layer {layer_id} has no tokens")
+        return n
+
+    def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
+        """Dequantised K, V in self.dtype (kivi_style_cache.py:619-666)."""
+        kp, vp, ks, kz, vs, vz = self.get_int4_asym_tensors(layer_id)
+
+        def unpack(p):
+            p = p.to(torch.int16)
+            return torch.stack(((p >> 4) & 15, p & 15), dim=-1).flatten(-2) - 8
+
+        k = (unpack(kp).float() * ks.unsqueeze(2) + kz.unsqueeze(2)).to(self.dtype)
+        v = (unpack(vp).float() * vs.unsqueeze(-1) + vz.unsqueeze(-1)).to(self.dtype)
+        return k, v
+
+    def decode_attn(self, layer_id: int, q: Tensor, sm_scale: Optional[float] = None) -> Tensor:
+        """Attention of q [B, Hq, 128] over layer_id's cache (INT4_KIVI decode kernel)."""
+        from .kernels import decode_attn_int4_kivi
+
+        kp, vp, ks, kz, vs, vz = self.get_int4_asym_tensors(layer_id)
+        n = kp.shape[2]
+        ctx = torch.full((kp.shape[0],), n, dtype=torch.int32, device=q.device)
+        tau = self.inv_tau[layer_id] if (self.use_attn_temperature and self.inv_tau is not None) else None
+        out = decode_attn_int4_kivi(q, kp, vp, ks, kz, vs, vz, ctx, sm_scale, inv_tau=tau)
+        self.record_fused_decode(layer_id, "hip_fused")
+        return out
+
+    def clear(self) -> None:
+        self._layer_seq_lens = [0] * self.num_layers
+        self._seq_len = 0
+        self._k_scale_initialized = [False] * self.num_layers
+        self._k_scale = [None] * self.num_layers
+        self._k_zp = [None] * self.num_layers
+
+    def release(self) -> None:
+        n = self.num_layers
+        self._k_cache, self._v_cache = [None] * n, [None] * n
+        self._v_scale, self._v_zp = [None] * n, [None] * n
+        self._layer_capacity = [0] * n
+        self.clear()
+
+    def get_memory_mb(self) -> float:
+        total = 0
+        for lst in (self._k_cache, self._v_cache, self._k_scale, self._k_zp, self._v_scale, self._v_zp):
+            total += sum(t.numel() * t.element_size() for t in lst if t is not None)
+        return total / (1024 * 1024)

@@ -54,6 +54,8 @@ struct AppendDev {
   int32_t* status;
   int tile32;  // codes in KVQ_LAYOUT_TILE32 (INT4_ASYM)
   const float* thr_ptr;  // group-rescue threshold computed by the large-n select, or NULL
+  int64_t st_sb;         // INT4_KIVI K: batch stride of the per-channel parameters
+  float* zo;             // INT4_KIVI V: per-token zero-point out (scale_out's strides)
 };
 
 // Scratch of the group rescue over more than kRescueMax (row, group) scales: an exact radix
@@ -269,6 +271,36 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
       if (a.so_f32) reinterpret_cast<float*>(a.so)[off] = s;
       else reinterpret_cast<half_t*>(a.so)[off] = (half_t)s;
     }
+  } else if (a.fmt == KVQ_FMT_INT4_KIVI) {
+    float s0, s1, z0, z1;
+    if (a.st != nullptr) {
+      // K: frozen per-channel parameters (kivi_style_cache.py:548-566)
+      const int64_t o = (int64_t)b * a.st_sb + (int64_t)h * a.st_sh + (int64_t)d0 * a.st_sg;
+      const float* ps = reinterpret_cast<const float*>(a.st);
+      const float* pz = reinterpret_cast<const float*>(a.st_zp);
+      s0 = ps[o]; s1 = ps[o + a.st_sg];
+      z0 = pz[o]; z1 = pz[o + a.st_sg];
+    } else {
+      // V: per-token min / max over the 128 channels (asymmetric_quant.py:102-141)
+      float mn = fminf(x0, x1), mx = fmaxf(x0, x1);
+      for (int o = 32; o > 0; o >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, o, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      }
+      // range floor max(1e-5, fp16 tiny * 15) = 15 * 2^-14; z = min - (-8) s
+      s0 = s1 = __fdiv_rn(fmaxf(__fsub_rn(mx, mn), 9.1552734375e-4f), 15.0f);
+      z0 = z1 = __fadd_rn(mn, 8.0f * s0);
+      if (lane == 0 && a.so) {
+        const int64_t off = (int64_t)b * a.sosb + (int64_t)h * a.sosh + t * a.sost;
+        reinterpret_cast<float*>(a.so)[off] = s0;
+        a.zo[off] = z0;
+      }
+    }
+    const float r0 = rintf(__fdiv_rn(__fsub_rn(x0, z0), s0));
+    const float r1 = rintf(__fdiv_rn(__fsub_rn(x1, z1), s1));
+    if (a.st != nullptr) clipped = (r0 < -8.f || r0 > 7.f) + (r1 < -8.f || r1 > 7.f);
+    const int q0 = (int)fminf(fmaxf(r0, -8.f), 7.f), q1 = (int)fminf(fmaxf(r1, -8.f), 7.f);
+    crow[lane] = (uint8_t)(((q0 + 8) << 4) | (q1 + 8));
   } else {  // KVQ_FMT_INT4_ASYM, static parameters
     const int64_t off = (int64_t)h * a.st_sh + (int64_t)g * a.st_sg;
     const float s = (float)reinterpret_cast<const half_t*>(a.st)[off];
@@ -362,7 +394,7 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   if (!p) return KVQ_OK;
   const std::string n(name);
   if (p->format != KVQ_FMT_INT8_SYM && p->format != KVQ_FMT_INT4_SYM &&
-      p->format != KVQ_FMT_INT4_ASYM)
+      p->format != KVQ_FMT_INT4_ASYM && p->format != KVQ_FMT_INT4_KIVI)
     return fail(KVQ_ERR_INVALID, n + ": unknown format");
   if (p->head_dim != 128) return fail(KVQ_ERR_UNSUPPORTED, n + ": head_dim must be 128");
   const int gs = p->group_size;
@@ -387,6 +419,16 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
       return fail(KVQ_ERR_INVALID, n + ": outliers need n_outlier == 4 and both pointers");
   } else if (p->n_outlier != 0) {
     return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
+  }
+  if (p->format == KVQ_FMT_INT4_KIVI) {
+    if (p->codes_layout != KVQ_LAYOUT_ROWS)
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI codes are in token rows");
+    if (p->static_scale) {
+      if (!p->static_zp || p->static_scale_dtype != KVQ_DTYPE_F32)
+        return fail(KVQ_ERR_INVALID, n + ": INT4_KIVI K needs fp32 static scale and zero-point");
+    } else if (!p->scale_out || !p->zp_out || p->scale_out_dtype != KVQ_DTYPE_F32) {
+      return fail(KVQ_ERR_INVALID, n + ": INT4_KIVI V needs fp32 scale_out and zp_out");
+    }
   }
   if (p->codes_layout != KVQ_LAYOUT_ROWS && p->codes_layout != KVQ_LAYOUT_TILE32)
     return fail(KVQ_ERR_INVALID, n + ": unknown codes_layout");
@@ -417,6 +459,8 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   d.wpos = p->write_pos;
   d.status = p->status;
   d.tile32 = p->codes_layout == KVQ_LAYOUT_TILE32;
+  d.st_sb = p->static_stride_b;
+  d.zo = reinterpret_cast<float*>(p->zp_out);
   return KVQ_OK;
 }
 

@@ -765,3 +765,44 @@ def test_decode_kivi_inv_tau_bf16_q_and_fp16_params():
     assert torch.isfinite(o).all() and (err <= ATOL).all()
     # the bf16 rounding of q moves the result measurably: the fp16-q oracle is a different case
     assert (ref - ref16).abs().max().item() > 0
+
+
+@pytest.mark.parametrize("B,H,S0,steps", [(2, 2, 37, 3), (1, 4, 300, 1)])
+def test_kivi_cache_append_bitexact_and_decode(B, H, S0, steps):
+    """KIVIStyleKVCache: prefill + decode appends through kvq_quant_append are bit-exact
+    with the oracle's per-channel / per-token quantizers (fp32 parameters included), and the
+    cache's decode attention matches the oracle over the stored codes."""
+    K = _lib()
+    g = gen(500 + S0)
+    D = 128
+    k0 = (torch.randn(B, H, S0, D, generator=g) * 2).to(torch.float16)
+    v0 = torch.randn(B, H, S0, D, generator=g).to(torch.float16)
+    cache = K.KIVIStyleKVCache(num_layers=1, device=DEV, quant_bits=4)
+    cache.append(0, k0.to(DEV), v0.to(DEV))
+    ks_ref_q, ks, kz = OQ.quantize_asymmetric_per_channel(k0, 4)
+    ks_codes = [ks_ref_q]
+    vq, vs, vz = OQ.quantize_asymmetric_per_token(v0, 4)
+    v_codes, v_s, v_z = [vq], [vs], [vz]
+    for i in range(steps):
+        k1 = (torch.randn(B, H, 1, D, generator=g) * 2.5).to(torch.float16)  # some codes clip
+        v1 = torch.randn(B, H, 1, D, generator=g).to(torch.float16)
+        cache.append(0, k1.to(DEV), v1.to(DEV))
+        ks_codes.append(OQ.kivi_quantize_k_static(k1, ks, kz))
+        q1, s1, z1 = OQ.quantize_asymmetric_per_token(v1, 4)
+        v_codes.append(q1); v_s.append(s1); v_z.append(z1)
+    torch.cuda.synchronize()
+    kp, vp, gks, gkz, gvs, gvz = [t.cpu() for t in cache.get_int4_asym_tensors(0)]
+    assert cache.get_seq_len() == S0 + steps
+    assert torch.equal(gks, ks) and torch.equal(gkz, kz)
+    assert torch.equal(gvs, torch.cat(v_s, 2)) and torch.equal(gvz, torch.cat(v_z, 2))
+    assert kp.dtype == torch.int8 and vp.dtype == torch.int8
+    assert torch.equal(kp, OQ.pack_int4(torch.cat(ks_codes, 2)))
+    assert torch.equal(vp, OQ.pack_int4(torch.cat(v_codes, 2)))
+    q = torch.randn(B, 4 * H, D, generator=g).to(torch.float16)
+    out = cache.decode_attn(0, q.to(DEV))
+    torch.cuda.synchronize()
+    ctx = torch.full((B,), S0 + steps, dtype=torch.int32)
+    ref = OA.decode_attn_kivi_ref(q, kp, vp, gks, gkz, gvs, gvz, ctx, 1 / math.sqrt(D))
+    assert_close(out, ref, f"kivi cache B{B} H{H} S{S0}+{steps}")
+    k_deq, v_deq = cache.get_kv(0)
+    assert k_deq.shape == (B, H, S0 + steps, D)
