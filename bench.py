@@ -64,6 +64,9 @@ def parse():
                          "so a profiler sees only the step's launches")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device copy three times (rocprof counter calibration)")
+    ap.add_argument("--kivi-probe", action="store_true",
+                    help="only time kvq_decode_attn over the KIVI layout at config 3's shape "
+                         "(B 8, 28 / 4 heads, 32k tokens; random codes and parameters)")
     return ap.parse_args()
 
 
@@ -270,6 +273,43 @@ def copy_probe(device, nbytes=1 << 30, reps=3):
                       "launches": reps}), flush=True)
 
 
+def kivi_probe(device, steps, warmup):
+    """Decode attention over the KIVI layout (packed rows, per-channel K and per-token V fp32
+    parameters) at config 3's per-layer shape.  Algorithmic bytes per call: 136 per (token,
+    kv head) (64 + 64 code bytes, 8 bytes of V parameters), 1 KiB of K parameters per
+    (b, kv head), q read and output written."""
+    from llm_kvcache_quantization_amd import _capi as C
+    from llm_kvcache_quantization_amd import kernels as KK
+
+    B, Hq, Hkv, S = 8, 28, 4, 32768
+    g = torch.Generator(device=device).manual_seed(0)
+    q = torch.randn(B, Hq, 128, device=device, generator=g).half()
+    kp = torch.randint(-128, 127, (B, Hkv, S, 64), device=device, dtype=torch.int8, generator=g)
+    vp = torch.randint(-128, 127, (B, Hkv, S, 64), device=device, dtype=torch.int8, generator=g)
+    ks = torch.rand(B, Hkv, 128, device=device, generator=g) * 0.2 + 0.01
+    kz = torch.randn(B, Hkv, 128, device=device, generator=g)
+    vs = torch.rand(B, Hkv, S, device=device, generator=g) * 0.2 + 0.01
+    vz = torch.randn(B, Hkv, S, device=device, generator=g)
+    ctx = torch.full((B,), S, dtype=torch.int32, device=device)
+    plan = KK.DecodePlan(q, C.KVQ_FMT_INT4_KIVI, KK.kv_view_kivi(kp, ks, kz, True),
+                         C.KVQ_FMT_INT4_KIVI, KK.kv_view_kivi(vp, vs, vz, False), ctx, Hkv, S,
+                         1 / math.sqrt(128), 32)
+    for _ in range(warmup):
+        plan.launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        plan.launch()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    nbytes = B * Hkv * S * 136 + B * Hkv * 128 * 8 + B * Hq * 128 * 4
+    print(json.dumps({"kivi_probe_us_per_call": round(us, 3), "bytes_per_call": nbytes,
+                      "GBps": round(nbytes / us / 1e3, 1), "frac_of_8TBps": round(nbytes / us / 8e6, 4),
+                      "chunk_tokens": plan.chunk_tokens, "steps": steps}), flush=True)
+
+
 def attention_kernels(cfg, layer):
     """Kernels one kvq_decode_attn call launches for this configuration: the tiled kernels
     (TILE32 V, or static-scale INT8 K) merge their chunk partials themselves when they run
@@ -372,6 +412,9 @@ def main():
         sys.exit(2)
     if args.copy_probe:
         copy_probe("cuda:0")
+        return
+    if args.kivi_probe:
+        kivi_probe("cuda:0", max(args.steps, 200), max(args.warmup, 20))
         return
     from llm_kvcache_quantization_amd import _capi as C
     from llm_kvcache_quantization_amd import synthetic as SY
