@@ -68,12 +68,15 @@ typedef struct kvq_kv_view {
   int64_t stride_h;      /* bytes */
   int64_t stride_t;      /* bytes; the D (or D/2) code bytes of a token are contiguous */
   const void* scale;     /* INT8_SYM/INT4_SYM: [B,H,T,G] (any strides, 0 allowed);
-                            INT4_ASYM: [H,G] (only stride_h / stride_g are read) */
+                            INT4_ASYM: [H,G] (only stride_h / stride_g are read);
+                            INT4_KIVI (fp32): K [B,H,D] (stride_b / _h / _g = 1, 16-byte
+                            aligned rows), V [B,H,T] (stride_b / _h / _t = 1) */
   int64_t scale_stride_b, scale_stride_h, scale_stride_t, scale_stride_g; /* elements */
   int32_t scale_dtype;   /* KVQ_DTYPE_F16 or KVQ_DTYPE_F32 (F32 is rounded to fp16 in-kernel);
                             K and V per-token scales must have the same dtype */
   int32_t n_outlier;     /* INT4_ASYM K only: 0 or 4 */
-  const void* zero_point;         /* INT4_ASYM: fp16 [H,G], same strides as scale */
+  const void* zero_point;         /* INT4_ASYM: fp16 [H,G]; INT4_KIVI: fp32; same strides
+                                     as scale */
   const int32_t* outlier_idx;     /* [H, n_outlier] channel indices, distinct, in [0, D) */
   const void* outlier_val;        /* fp16 [B,H,T,n_outlier] */
   int64_t outlier_stride_b, outlier_stride_h, outlier_stride_t; /* elements */
