@@ -235,9 +235,17 @@ constexpr float kTwoM24 = 5.9604644775390625e-8f;  // 2^-24
 // from which the outlier operand is gathered
 struct QShareLds {
   u32x4 qh[4][64];
+  u32x4 ql[4][64];  // the low halves of a hi + lo split operand (KKiviT)
   float bias[4][16];
   half_t qv[16][kD];  // q' of head column c (zero for padding columns)
 };
+
+// x = hi + lo with hi = fp16(x) and lo = fp16(x - hi) (x - hi is exact in fp32): the pair
+// carries x to about 2^-22 of itself, where fp16(x) alone carries it to 2^-11
+__device__ __forceinline__ void split_h(float x, half_t& hi, half_t& lo) {
+  hi = (half_t)x;
+  lo = (half_t)(x - (float)hi);
+}
 
 // The q-side inputs of one lane: q[32 lg + 8 wave .. + 7] of head column lane % 16, its
 // inverse temperature and the K scale / zero-point of group lg.  They are fetched before
@@ -645,12 +653,17 @@ struct KiviQIn {
   float4v ks[2], kz[2];
 };
 
-// K of the KIVI layout: as KAsymT<false> (subnormal nibbles, one fp16 q operand, logits x
-// 2^-24) with per-channel parameters: operand fp16(q'_d s_d) (/ 16 for a high nibble) and
-// the constant term sum_d q'_d (z_d - 8 s_d) in fp32.
+// K of the KIVI layout: as KAsymT<false> (subnormal nibbles, logits x 2^-24) with
+// per-channel parameters.  The q operand q'_d s_d (/ 16 for a high nibble) is a hi + lo
+// pair of fp16 values (split_h), each multiplied by the codes in its own MFMA, so the
+// product is carried to about 2^-22 of itself: the reference computes k = (n - 8) s_d + z_d
+// and q . k in fp32, and per-channel scales of K outlier channels can be two orders of
+// magnitude above the rest, where one fp16 rounding of q'_d s_d (2^-11 of the term) would
+// show in the logits.  The constant term sum_d q'_d (z_d - 8 s_d) is summed in fp32.
 struct KKiviT : KAsymT<false> {
   using QInT = KiviQIn;
   static constexpr bool kAppend = false;
+  half8v ql[4];
   __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, KiviQIn& in) const {
     const int col = lane & 15, lg = lane >> 4;
     const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
@@ -671,7 +684,7 @@ struct KKiviT : KAsymT<false> {
     const bool has_tau = a.inv_tau != nullptr;
     const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
     float part = 0.f;
-    half_t vh[8];
+    half_t vh[8], vl[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int e = slot_elem(k);
@@ -679,30 +692,54 @@ struct KKiviT : KAsymT<false> {
       const float qd = valid ? (float)qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : 0.f;
       const float sd = in.ks[e >> 2][e & 3], zd = in.kz[e >> 2][e & 3];
       const float P = qd * sd;
-      vh[k] = (half_t)(slot_high(k) ? P * 0.0625f : P);
+      split_h(slot_high(k) ? P * 0.0625f : P, vh[k], vl[k]);
       part += qd * fmaf(-8.0f, sd, zd);
     }
     part = wave_sum_xor_groups(part);
     sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+    sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
     if (lg == 0) sh.bias[j][col] = part;
   }
   __device__ void finish_setup(const QShareLds& sh, const KiviQIn& in, int lane) {
     (void)in;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+    for (int j = 0; j < 4; ++j) {
+      qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+      ql[j] = __builtin_bit_cast(half8v, sh.ql[j][lane]);
+    }
     const int col = lane & 15;
     bias = (sh.bias[0][col] + sh.bias[1][col]) + (sh.bias[2][col] + sh.bias[3][col]);
+  }
+  // logits x 2^-24 of the tile's two row blocks: the codes times the hi and the lo operand
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    const float b24 = bias * kTwoM24;
+    float4v c0 = {b24, b24, b24, b24};
+    float4v c1 = c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const half8v a0 = unpack_sub(r.w[0][j], nc), a1 = unpack_sub(r.w[1][j], nc);
+      c0 = mfma16x16x32(a0, qh[j], c0);
+      c1 = mfma16x16x32(a1, qh[j], c1);
+      c0 = mfma16x16x32(a0, ql[j], c0);
+      c1 = mfma16x16x32(a1, ql[j], c1);
+    }
+    x0 = c0;
+    x1 = c1;
   }
 };
 
 // V of the KIVI layout in token rows (64 bytes).  Lane (col, lg) reads the dword of
 // channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens T(k) (four 64-byte rows
-// per load instruction) and their fp32 scale / zero-point.  With p' = fp16(p s_t) (round
-// to nearest) as the B operand and the codes as x = 64 + n (even channel) or 1024 + n (odd),
-//   sum_t p v ~= sum_t p' x - (off + 8) sum_t p' + sum_t p z_t,   off = 64 or 1024,
-// i.e. the rounding of p' multiplies the centred code c = n - 8 (|c| <= 8), so the error
-// of a term is at most 8 s 2^-11 of its weight.  The wave keeps Lp = sum p' and
-// Cz = sum p z beside l, and finalize() folds them into acc before the merge (out = acc / l).
+// per load instruction) and their fp32 scale / zero-point.  The codes enter the MFMA as
+// the exact fp16 subnormals n 2^-24 (odd channel, low nibble) and 16 n 2^-24 (even
+// channel, high nibble), and the B operand is w = p s_t (fp32) carried as a hi + lo pair of
+// fp16 values (split_h, two MFMAs per operand), so
+//   sum_t p v = sum_t w (n - 8) + sum_t p z_t = 2^24 acc (/ 16 for an even channel)
+//               - 8 Lp + Cz,   Lp = sum_t (hi + lo),  Cz = sum_t p z_t (fp32),
+// with w rounded to about 2^-22 of itself instead of the 2^-11 of one fp16 operand (the
+// reference dequantises V in fp32).  The wave keeps Lp and Cz beside l (the softmax
+// rescales them with l) and finalize() folds them into acc before the merge (out = acc / l).
 struct VKiviRowT {
   static constexpr bool kTile32 = false;
   rsrc_t rv, rs, rz;
@@ -766,21 +803,29 @@ struct VKiviRowT {
       wk[4 + i] = r.z[1][i];
     }
     float cz = ex[1];
-    uint32_t pp[4];
+    uint32_t ph[4], pl[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float p0 = (float)pb[2 * q], p1 = (float)pb[2 * q + 1];
       cz = fmaf(p0, wk[2 * q], cz);
       cz = fmaf(p1, wk[2 * q + 1], cz);
-      pp[q] = as_u32(half2v{(half_t)(p0 * sk[2 * q]), (half_t)(p1 * sk[2 * q + 1])});
+      half_t h0, l0, h1, l1;
+      split_h(p0 * sk[2 * q], h0, l0);
+      split_h(p1 * sk[2 * q + 1], h1, l1);
+      ph[q] = as_u32(half2v{h0, h1});
+      pl[q] = as_u32(half2v{l0, l1});
     }
     ex[1] = cz;
     const half2v ones = {(half_t)1.0f, (half_t)1.0f};
     float lp = ex[0];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) lp = __builtin_amdgcn_fdot2(as_h2(pp[q]), ones, lp, false);
+    for (int q = 0; q < 4; ++q) {
+      lp = __builtin_amdgcn_fdot2(as_h2(ph[q]), ones, lp, false);
+      lp = __builtin_amdgcn_fdot2(as_h2(pl[q]), ones, lp, false);
+    }
     ex[0] = lp;
-    const half8v ps = pack8(pp[0], pp[1], pp[2], pp[3]);
+    const half8v wh = pack8(ph[0], ph[1], ph[2], ph[3]);
+    const half8v wl = pack8(pl[0], pl[1], pl[2], pl[3]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // byte j of the tokens T(2p), T(2p + 1) into the low bytes of the two halves
@@ -788,25 +833,26 @@ struct VKiviRowT {
       uint32_t R[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) R[p] = perm_b32(r.w[2 * p + 1], r.w[2 * p], sel);
-      acc[2 * j] = mfma16x16x32(pack8(and_or(R[0], nc.m_hi, nc.c64), and_or(R[1], nc.m_hi, nc.c64),
-                                      and_or(R[2], nc.m_hi, nc.c64), and_or(R[3], nc.m_hi, nc.c64)),
-                                ps, acc[2 * j]);
-      acc[2 * j + 1] =
-          mfma16x16x32(pack8(and_or(R[0], nc.m_lo, nc.c1024), and_or(R[1], nc.m_lo, nc.c1024),
-                             and_or(R[2], nc.m_lo, nc.c1024), and_or(R[3], nc.m_lo, nc.c1024)),
-                       ps, acc[2 * j + 1]);
+      const half8v ahi = pack8(R[0] & nc.m_hi, R[1] & nc.m_hi, R[2] & nc.m_hi, R[3] & nc.m_hi);
+      const half8v alo = pack8(R[0] & nc.m_lo, R[1] & nc.m_lo, R[2] & nc.m_lo, R[3] & nc.m_lo);
+      acc[2 * j] = mfma16x16x32(ahi, wh, acc[2 * j]);
+      acc[2 * j + 1] = mfma16x16x32(alo, wh, acc[2 * j + 1]);
+      acc[2 * j] = mfma16x16x32(ahi, wl, acc[2 * j]);
+      acc[2 * j + 1] = mfma16x16x32(alo, wl, acc[2 * j + 1]);
     }
   }
-  // acc[mb][r] (channel 32 lg + 8 r + mb) += Cz - (off + 8) Lp, with Lp, Cz summed over
-  // the lane groups (the k-slots of a head); off = 64 (even channel) or 1024 (odd)
+  // acc[mb][r] (channel 32 lg + 8 r + mb) = 2^24 acc (2^20 for an even channel, whose codes
+  // entered as 16 n 2^-24) - 8 Lp + Cz, with Lp, Cz summed over the lane groups (the k-slots
+  // of a head)
   __device__ __forceinline__ void finalize(float4v acc[8], int lane) {
     (void)lane;
     const float lp = wave_sum_xor_groups(ex[0]), cz = wave_sum_xor_groups(ex[1]);
+    const float d = fmaf(-8.0f, lp, cz);
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
-      const float d = fmaf(-((mb & 1) ? 1032.0f : 72.0f), lp, cz);
+      const float f = (mb & 1) ? kTwo24 : kTwo24 * 0.0625f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[mb][r] += d;
+      for (int r = 0; r < 4; ++r) acc[mb][r] = fmaf(acc[mb][r], f, d);
     }
   }
 };

@@ -20,6 +20,18 @@ term, a wrong sign or index, a swapped nibble) fails at least one check:
   softmax [e/(e+1), 1/(e+1)], ctx=0 -> 0, GQA head h -> kv head h // n_rep), a float64
   brute force on tiny inputs, and permutation / scaling invariants.
 * decode_attn_asym_ref: float64 brute force with explicit dequantisation.
+* int8_cache_quantize(adaptive=True) (src/cache/int8_cache.py:389-453): known answers
+  with scalar arithmetic per group -- a group whose absmax/127 lies between the static
+  scale and static * margin takes static * margin, one above takes absmax/127, an all-zero
+  group takes static * margin -- and the codes of the fp16 closed form.  The same data
+  under the plausible mistakes (margin on the dynamic side, margin dropped, min for max)
+  give other scales, so each mistake fails.
+* int4_cache_quantize(adaptive / mixed_rescue / both / with outlier rescue)
+  (src/cache/int4_cache.py:447-529): the same kind of known answers in fp32, and the
+  reference's documented identity that outlier rescue after mixed rescue changes nothing
+  (int4_cache.py:360-378).
+* decode_attn_k8v4_ref: float64 brute force (INT8 K dequantised as the fp16 product the
+  reference forms, asymmetric V in float64, q * inv_tau as an fp16 product).
 """
 import math
 
@@ -338,3 +350,125 @@ def test_planted_mistake_is_caught():
     swapped = ((u[..., 1] << 4) | u[..., 0]).to(torch.int8)
     assert int(swapped.view(torch.uint8)) != ((-8 + 8) << 4) | (7 + 8)
     assert int(OQ.pack_int4(x).view(torch.uint8)) == ((-8 + 8) << 4) | (7 + 8)
+
+
+# ---------------------------------------------------------------- scale policies (KATs)
+
+
+def _groups_row(absmax, gs):
+    """fp16 x [1, 1, 1, G * gs]: group g holds absmax[g] at its first channel, -absmax[g] / 2
+    at its second and zeros elsewhere (so its absmax is absmax[g])."""
+    G = len(absmax)
+    x = torch.zeros(1, 1, 1, G * gs, dtype=torch.float16)
+    for g, a in enumerate(absmax):
+        x[0, 0, 0, g * gs] = a
+        x[0, 0, 0, g * gs + 1] = -a / 2
+    return x
+
+
+def test_int8_adaptive_scale_kat():
+    gs, m = 32, 2.0
+    s16 = np.float16(0.01)
+    absmax = [1.905, 3.81, 0.0, 1.0]
+    x = _groups_row(absmax, gs)
+    st = torch.full((1, 4), float(s16), dtype=torch.float16)
+    q, sc = OQ.int8_cache_quantize(x, st, gs, adaptive=True, margin=m)
+    st32 = np.float32(s16) * np.float32(m)                     # static side, times the margin
+    dyn = [np.float32(max(np.float32(np.float16(a)), np.float32(1e-5))) / np.float32(127) for a in absmax]
+    want = [np.float16(max(st32, d)) for d in dyn]
+    # which side wins in each group: (s, s*m) -> s*m, above -> dyn, zero -> s*m, below s -> s*m
+    assert [w == np.float16(st32) for w in want] == [True, False, True, True]
+    assert sc.view(-1).tolist() == [float(w) for w in want]
+    for g in range(4):
+        xs = x[0, 0, 0, g * gs:(g + 1) * gs].numpy()
+        assert np.array_equal(q[0, 0, 0, g * gs:(g + 1) * gs].numpy(), int8_closed_form(xs, want[g]))
+    # plausible mistakes give other scales
+    on_dyn = [np.float16(max(np.float32(s16), d * np.float32(m))) for d in dyn]
+    no_margin = [np.float16(max(np.float32(s16), d)) for d in dyn]
+    as_min = [np.float16(min(st32, d)) for d in dyn]
+    for wrong in (on_dyn, no_margin, as_min):
+        assert wrong != want
+
+
+def test_int8_adaptive_off_keeps_static_and_dynamic_without_table():
+    gs = 32
+    x = _groups_row([1.905, 3.81, 0.0, 1.0], gs)
+    st = torch.full((1, 4), 0.01, dtype=torch.float16)
+    _, sc = OQ.int8_cache_quantize(x, st, gs, adaptive=False)
+    assert sc.view(-1).tolist() == [float(np.float16(0.01))] * 4
+    _, sd = OQ.int8_cache_quantize(x, None, gs)
+    # dynamic: fp16 absmax clamped to 1e-5 in fp16, divided by 127 in fp16
+    want = [np.float16(np.float16(max(np.float16(a), np.float16(1e-5))) / np.float16(127))
+            for a in (1.905, 3.81, 0.0, 1.0)]
+    assert sd.view(-1).tolist() == [float(w) for w in want]
+
+
+def _int4_want(x, scale32, gs):
+    xs = x.view(-1).numpy().astype(np.float32)
+    out = np.empty_like(xs, dtype=np.int8)
+    for i, v in enumerate(xs):
+        s = np.float32(max(scale32[i // gs], np.float32(1e-5)))
+        out[i] = np.int8(np.clip(np.rint(np.float32(v) / s), -7, 7))
+    return out
+
+
+def test_int4_adaptive_and_mixed_rescue_kat():
+    gs = 32
+    absmax = [0.7, 1.4, 0.91, 0.35]
+    x = _groups_row(absmax, gs)
+    s32, m = np.float32(0.1), np.float32(1.5)
+    st = torch.full((1, 4), float(s32), dtype=torch.float32)
+    dyn = [np.float32(max(np.float32(np.float16(a)), np.float32(1e-5))) / np.float32(7) for a in absmax]
+    cases = {
+        # adaptive: max(s * margin, absmax / 7)
+        "adaptive": (dict(adaptive=True, margin=float(m)), [max(s32 * m, d) for d in dyn]),
+        # mixed rescue: max(s, absmax / 7)
+        "mixed": (dict(mixed_rescue=True), [max(s32, d) for d in dyn]),
+        # both: adaptive first, then mixed (max is order-free, the margin is not)
+        "both": (dict(adaptive=True, margin=float(m), mixed_rescue=True),
+                 [max(max(s32 * m, d), d) for d in dyn]),
+        # outlier rescue of every group after mixed rescue changes nothing (int4_cache.py:367-375)
+        "mixed+rescue": (dict(mixed_rescue=True, outlier_rescue_ratio=0.5), [max(s32, d) for d in dyn]),
+        "static": (dict(), [s32] * 4),
+    }
+    for name, (kw, want) in cases.items():
+        q, sc = OQ.int4_cache_quantize(x, st, gs, **kw)
+        got = sc.view(-1).tolist()
+        assert got == [float(w) for w in want], (name, got, want)
+        assert np.array_equal(q.view(-1).numpy(), _int4_want(x, want, gs)), name
+    # the KAT separates the policies: adaptive differs from mixed in groups 0 and 2 (the
+    # margin), both from static in groups 1 (dynamic wins)
+    a = cases["adaptive"][1]
+    mx = cases["mixed"][1]
+    assert a[0] != mx[0] and a[2] != mx[2] and a[1] == mx[1] == dyn[1]
+    # margin applied to the dynamic side instead would change group 2
+    assert max(s32, dyn[2] * m) != a[2]
+
+
+def test_k8v4_oracle_brute_force():
+    g = torch.Generator().manual_seed(9)
+    B, H, Hq, S, D = 1, 2, 6, 7, 128
+    kq = torch.randint(-127, 128, (B, H, S, D), generator=g, dtype=torch.int8)
+    ks16 = (torch.rand(B, H, S, 4, generator=g) * 0.02 + 0.001).to(torch.float16)
+    vq = torch.randint(-8, 8, (B, H, S, D), generator=g, dtype=torch.int8)
+    vs = (torch.rand(H, 4, generator=g) + 0.1).to(torch.float16)
+    vz = torch.randn(H, 4, generator=g).to(torch.float16)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.float16)
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    ctx = 5
+    out = OA.decode_attn_k8v4_ref(q, kq, ks16, OQ.pack_int4(vq), vs, vz, torch.tensor([ctx]), 0.1,
+                                  inv_tau=tau)
+    kd = np.zeros((H, S, D))
+    vd = np.zeros((H, S, D))
+    for h in range(H):
+        for t in range(S):
+            for d in range(D):
+                gi = d // 32
+                # the reference's fp16 product code * scale (src/engine/patch_model.py:355-362)
+                kd[h, t, d] = float(np.float16(np.float16(int(kq[0, h, t, d])) * np.float16(ks16[0, h, t, gi])))
+                vd[h, t, d] = float(vq[0, h, t, d]) * float(vs[h, gi]) + float(vz[h, gi])
+    qs = np.array([[float(np.float16(np.float16(q[0, i, d]) * np.float16(tau[i]))) for d in range(D)]
+                   for i in range(Hq)])
+    ref = brute_attention(qs, kd, vd, ctx, 0.1)
+    ok, err = fp16_close(out[0].double().numpy(), ref)
+    assert ok, err
