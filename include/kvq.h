@@ -131,6 +131,21 @@ typedef struct kvq_decode_params {
 } kvq_decode_params;
 
 int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream);
+
+/* kvq_decode_attn without a caller workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc).  No counterpart in the reference, whose Triton wrapper allocates per call.
+ *
+ * p->workspace / p->workspace_bytes are ignored: the split-K partials and merge counters
+ * live in a fixed 16 MiB device array (KVQ_NOALLOC_SCRATCH_BYTES) that libkvq.so holds on
+ * every GPU it runs on until the process ends.  Calls whose kvq_decode_workspace_bytes(p)
+ * exceeds it return KVQ_ERR_UNSUPPORTED.  The call enqueues one small fill kernel that
+ * clears the merge counters, then the kernels of kvq_decode_attn, with bit-identical
+ * results.  It calls no hipMalloc / hipFree.  Every call on one GPU shares that GPU's
+ * array: calls that may overlap on one GPU (different streams without ordering) race. */
+#define KVQ_NOALLOC_SCRATCH_BYTES (16LL << 20)
+int kvq_decode_attn_noalloc(const kvq_decode_params* p, kvq_stream_t stream);
+
 /* split size kvq_decode_attn will use for p (p->chunk_tokens if nonzero) */
 int32_t kvq_decode_chunk_tokens(const kvq_decode_params* p);
 /* bytes of workspace kvq_decode_attn needs for p */

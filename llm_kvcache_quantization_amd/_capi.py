@@ -34,6 +34,9 @@ KVQ_FMT_INT4_KIVI = 4
 KVQ_LAYOUT_ROWS = 0
 KVQ_LAYOUT_TILE32 = 1
 
+# size of the device array kvq_decode_attn_noalloc keeps its workspace in
+KVQ_NOALLOC_SCRATCH_BYTES = 16 << 20
+
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
 c_f32 = ctypes.c_float
@@ -114,6 +117,7 @@ class AppendParams(ctypes.Structure):
 
 EXPORTED_SYMBOLS = (
     "kvq_decode_attn",
+    "kvq_decode_attn_noalloc",
     "kvq_append_decode_attn",
     "kvq_decode_chunk_tokens",
     "kvq_decode_workspace_bytes",
@@ -151,6 +155,8 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(str(LIB_PATH))
         L.kvq_decode_attn.argtypes = [ctypes.POINTER(DecodeParams), c_vp]
         L.kvq_decode_attn.restype = c_i32
+        L.kvq_decode_attn_noalloc.argtypes = [ctypes.POINTER(DecodeParams), c_vp]
+        L.kvq_decode_attn_noalloc.restype = c_i32
         L.kvq_decode_chunk_tokens.argtypes = [ctypes.POINTER(DecodeParams)]
         L.kvq_decode_chunk_tokens.restype = c_i32
         L.kvq_decode_workspace_bytes.argtypes = [ctypes.POINTER(DecodeParams)]

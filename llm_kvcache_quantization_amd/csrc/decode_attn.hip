@@ -906,6 +906,93 @@ extern "C" int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream) 
   return decode_impl(p, nullptr, stream);
 }
 
+// ---------------------------------------------------------------- no-allocation variant
+//
+// kvq_decode_attn_noalloc runs kvq_decode_attn with its split-K workspace (the chunk
+// partials and the single-launch merge's arrival counters) in `scratch`, a file-scope
+// device array every GPU holds once for the life of the process, instead of a
+// caller-provided buffer.  In host code `scratch` names a host-side stand-in, not device
+// memory: its device address is looked up with hipGetSymbolAddress, once per device with
+// that device current, and only that address is ever passed to kernels.
+constexpr int64_t kNoallocScratchBytes = (int64_t)16 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, or null
+
+// the counter words of the merge start at zero on every call (the array keeps whatever
+// the previous call, of any shape, left there)
+__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// device address of `scratch` on device dev (looked up on the first call for dev)
+int scratch_ptr(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(KVQ_ERR_UNSUPPORTED, "device ordinal above 63");
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return fail(KVQ_ERR_LAUNCH, "hipGetDevice failed");
+    if (cur != dev && hipSetDevice(dev) != hipSuccess)
+      return fail(KVQ_ERR_LAUNCH, "hipSetDevice failed");
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !ptr)
+      return fail(KVQ_ERR_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return KVQ_OK;
+}
+}  // namespace
+
+extern "C" int kvq_decode_attn_noalloc(const kvq_decode_params* p, kvq_stream_t stream) {
+  if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
+  // shapes kvq_decode_attn would reject are rejected before anything is enqueued
+  if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0 || p->batch > 65535 ||
+      p->q_heads > 65535 || p->kv_heads > 65535 || p->capacity < 0 ||
+      p->capacity > ((int64_t)1 << 30))
+    return decode_impl(p, nullptr, stream);
+  const int64_t need = kvq_decode_workspace_bytes(p);
+  if (need > kNoallocScratchBytes)
+    return fail(KVQ_ERR_UNSUPPORTED,
+                "kvq_decode_attn_noalloc: the split-K workspace of this call needs " +
+                    std::to_string(need) + " bytes, above the fixed " +
+                    std::to_string(kNoallocScratchBytes) +
+                    "-byte scratch; raise chunk_tokens or call kvq_decode_attn with a workspace");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int dev = -1;
+  if (s != nullptr) {
+    if (hipStreamGetDevice(s, &dev) != hipSuccess) return fail(KVQ_ERR_INVALID, "invalid stream");
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return fail(KVQ_ERR_LAUNCH, "hipGetDevice failed");
+  }
+  void* ws = nullptr;
+  int rc = scratch_ptr(dev, &ws);
+  if (rc) return rc;
+  kvq_decode_params q = *p;
+  q.workspace = ws;
+  q.workspace_bytes = kNoallocScratchBytes;
+  // clear the counter slots this call's merge uses (a fill kernel rather than a memset,
+  // so that the call can be captured into a HIP graph)
+  const int64_t nch = n_chunks_for(p, choose_chunk(p));
+  const int64_t words = (int64_t)p->batch * p->kv_heads * kCtrSlotWords;
+  const int64_t off = counters_offset(p, nch);
+  if (off < 0 || off + words * 4 > kNoallocScratchBytes)
+    return fail(KVQ_ERR_INVALID, "kvq_decode_attn_noalloc: counter slots outside the scratch");
+  uint32_t* ctr = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + off);
+  const int64_t blocks = (words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024;
+  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)blocks), dim3(256), 0, s, ctr, words);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
+  return decode_impl(&q, nullptr, stream);
+}
+
 // One new token per (b, kv head) appended to the cache p attends over, in the same launch.
 // The append parameters must describe exactly that cache: the same code, outlier and
 // static-table buffers with the same strides (so the kernel writes what it later reads).

@@ -207,6 +207,14 @@ class DecodePlan:
         C.check(C.lib().kvq_decode_attn(self._pp, ctypes.c_void_p(s)))
         return self.out
 
+    def launch_noalloc(self, stream: Optional[int] = None) -> torch.Tensor:
+        """The same attention through kvq_decode_attn_noalloc: the split-K workspace is the
+        library's fixed per-GPU device array instead of this plan's (bit-identical output;
+        calls that may overlap on one GPU race on that array)."""
+        s = C.stream_handle(self.device) if stream is None else stream
+        C.check(C.lib().kvq_decode_attn_noalloc(self._pp, ctypes.c_void_p(s)))
+        return self.out
+
     def launch_append(self, k_new: C.AppendParams, v_new: C.AppendParams,
                       stream: Optional[int] = None) -> torch.Tensor:
         """One launch: quantize-on-append of the new token described by k_new / v_new

@@ -18,7 +18,8 @@ def declared_functions():
 
 def test_header_declares_entry_points():
     assert declared_functions() == sorted([
-        "kvq_abi_version", "kvq_append_decode_attn", "kvq_decode_attn", "kvq_decode_chunk_tokens",
+        "kvq_abi_version", "kvq_append_decode_attn", "kvq_decode_attn", "kvq_decode_attn_noalloc",
+        "kvq_decode_chunk_tokens",
         "kvq_append_scratch_bytes", "kvq_decode_workspace_bytes", "kvq_last_error",
         "kvq_quant_append"])
 
