@@ -1,5 +1,5 @@
 /*
- * kvq.h -- C ABI (version 3) of the MI355X (gfx950) quantized-KV decode path.
+ * kvq.h -- C ABI (version 4) of the MI355X (gfx950) quantized-KV decode path.
  *
  * libkvq.so exports three groups of entry points: quantize-on-append, split-K
  * decode attention and error reporting.  Every entry point
@@ -115,19 +115,23 @@ typedef struct kvq_decode_params {
   const void* inv_tau;    /* fp16 [Hq] or NULL */
   int32_t k_format, v_format;
   kvq_kv_view k, v;
-  const int32_t* context_lens;        /* device int32 [B] */
+  const int32_t* context_lens;        /* device int32 [B], or NULL: every row has context_len */
   int32_t batch, q_heads, kv_heads, head_dim, group_size;
   int64_t capacity;       /* token dimension of the cache views */
   float sm_scale;
   int32_t chunk_tokens;   /* split size in tokens (work-groups per (b, kv head) =
                              ceil(capacity / chunk_tokens)); 0 = choose automatically */
   void* workspace;        /* device scratch of kvq_decode_workspace_bytes() bytes, zero-filled
-                             before its first use (it holds work-group arrival counters that
-                             every call leaves zero); calls sharing a workspace must be
-                             ordered on one stream */
+                             before its first use: its first B * kv_heads * 128 bytes hold
+                             work-group arrival counters that every call leaves zero, so one
+                             workspace serves any later call with the same batch * kv_heads
+                             that fits in it; calls sharing a workspace must be ordered on
+                             one stream */
   int64_t workspace_bytes;
   void* out;              /* fp16 [B, Hq, D], d contiguous */
   int64_t out_stride_b, out_stride_h; /* elements */
+  int32_t context_len;    /* context of every row when context_lens is NULL (ABI 4) */
+  int32_t pad0;           /* 0 */
 } kvq_decode_params;
 
 int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream);
@@ -211,6 +215,11 @@ typedef struct kvq_append_params {
      z = min + 8 s, written as fp32 to scale_out (so_stride_b/_h/_t) and zp_out (same strides) */
   int64_t static_stride_b;  /* elements */
   void* zp_out;
+  /* INT8_SYM / INT4_SYM without a static scale (ABI 4): 0 = the group's absmax; else
+     fp32(percentile / 100) in (0, 1): the group's torch.quantile of |x| at that level
+     (linear interpolation in fp32, src/quant/int8_basic.py:78-83, int4_basic.py:84-90) */
+  float dyn_quantile;
+  int32_t pad0;             /* 0 */
 } kvq_append_params;
 
 /* Appends K and V of one layer with one launch (either pointer may be NULL).  The INT4_SYM
@@ -242,7 +251,7 @@ int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* 
 
 /* message for the last non-OK return on this thread ("" if none) */
 const char* kvq_last_error(void);
-/* ABI version (increments on incompatible changes to the structs above); this is 3 */
+/* ABI version (increments on incompatible changes to the structs above); this is 4 */
 int32_t kvq_abi_version(void);
 
 #ifdef __cplusplus

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before libkvq.so, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 KVQ_OK = 0
 KVQ_ERR_INVALID = 1
@@ -77,6 +77,7 @@ class DecodeParams(ctypes.Structure):
         ("workspace_bytes", c_i64),
         ("out", c_vp),
         ("out_stride_b", c_i64), ("out_stride_h", c_i64),
+        ("context_len", c_i32), ("pad0", c_i32),
     ]
 
 
@@ -112,6 +113,7 @@ class AppendParams(ctypes.Structure):
         ("codes_layout", c_i32), ("reserved", c_i32),
         ("scratch", c_vp), ("scratch_bytes", c_i64),
         ("static_stride_b", c_i64), ("zp_out", c_vp),
+        ("dyn_quantile", c_f32), ("pad0", c_i32),
     ]
 
 

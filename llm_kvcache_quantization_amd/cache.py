@@ -102,6 +102,10 @@ class _EngineBase:
         self._seq_len = 0
         self.decode_stats: Dict[str, object] = _new_decode_stats()
         self._status: Optional[Tensor] = None
+        # per layer: the LayerStep over the layer's buffers and the fused append's parameter
+        # blocks, rebuilt when the buffers are reallocated
+        self._steps: List[Optional[object]] = [None] * num_layers
+        self._apps: List[Optional[tuple]] = [None] * num_layers
 
     # -- decode stats (src/cache/int8_cache.py:255-296)
     def _bump_counter(self, key: str, delta: int = 1) -> None:
@@ -198,6 +202,18 @@ class _EngineBase:
     def _launch_append(self, pk: C.AppendParams, pv: C.AppendParams, device) -> None:
         C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
                                          ctypes.c_void_p(C.stream_handle(device))))
+
+
+def _dyn_quantile(percentile: float) -> float:
+    """kvq_append_params.dyn_quantile of a dynamic quantizer with this clip percentile:
+    0 (absmax) at 100 and above, else the quantile level percentile / 100 the reference
+    passes to torch.quantile (src/quant/int8_basic.py:78-83, int4_basic.py:84-90)."""
+    p = float(percentile)
+    if p >= 100.0:
+        return 0.0
+    if not p > 0.0:
+        raise NotImplementedError(f"clip_percentile must be in (0, 100], got {percentile}")
+    return p / 100.0
 
 
 def _fill_append(p: C.AppendParams, fmt: int, x: Tensor, gs: int, codes: Tensor, write_pos: int,
@@ -306,6 +322,7 @@ class _SymCacheBase(_EngineBase):
         self._k_cache[layer_id], self._v_cache[layer_id] = nk, nv
         self._k_scale[layer_id], self._v_scale[layer_id] = nks, nvs
         self._layer_capacity[layer_id] = new_cap
+        self._steps[layer_id] = self._apps[layer_id] = None
 
     def _alloc_scale(self, side, layer_id, batch, heads, cap, groups):
         tok = self._side_is_token(side)
@@ -338,10 +355,6 @@ class _SymCacheBase(_EngineBase):
         self._pre_append_checks(layer_id)
         sk = self._static_for("k", layer_id, H, G)
         sv = self._static_for("v", layer_id, H, G)
-        if (sk is None or sv is None) and self.clip_percentile < 100.0:
-            raise NotImplementedError(
-                "dynamic (no static scale) quantization with percentile clipping < 100 is not "
-                "implemented in the HIP append; pass clip_percentile=100.0 or static scales")
         old_len = self._layer_seq_lens[layer_id]
         target = old_len + S
         self._ensure_capacity(layer_id, B, H, D, G, target)
@@ -373,6 +386,8 @@ class _SymCacheBase(_EngineBase):
                 p.static_scale_dtype = C.KVQ_DTYPE_F32 if st.dtype == torch.float32 else C.KVQ_DTYPE_F16
                 p.static_stride_h, p.static_stride_g = st.stride()
                 self._policy(p, side)
+            else:
+                p.dyn_quantile = _dyn_quantile(self.clip_percentile)
             if tok:
                 p.scale_out = scale_buf.data_ptr()
                 p.scale_out_dtype = C.KVQ_DTYPE_F32 if scale_buf.dtype == torch.float32 else C.KVQ_DTYPE_F16
@@ -390,6 +405,96 @@ class _SymCacheBase(_EngineBase):
 
     def _pre_append_checks(self, layer_id: int) -> None:
         pass
+
+    # -- decode step: the append + attention of src/engine/patch_model.py:755-957
+
+    def _fused_step_ok(self, D: int) -> bool:
+        """The format the tiled kernel appends and attends in one launch (static group-32
+        INT8 scales on both sides, no adaptive policy)."""
+        return False
+
+    def _step_for(self, layer_id: int, q_heads: int):
+        """The layer's LayerStep (kernels.LayerStep) over its whole buffers."""
+        from .kernels import LayerStep, kv_view_tok
+
+        kb = self._k_cache[layer_id]
+        st = self._steps[layer_id]
+        if st is not None and st.key == (q_heads, kb.data_ptr()):
+            return st
+        B, H, cap = kb.shape[0], kb.shape[1], kb.shape[2]
+        kc, vc, ks, vs = self._raw_views(layer_id, cap)
+        st = LayerStep(self._fmt, kv_view_tok(kc, ks), self._fmt, kv_view_tok(vc, vs), B, q_heads, H,
+                       self.group_size, kb.device, keepalive=(kc, vc, ks, vs))
+        st.key = (q_heads, kb.data_ptr())
+        self._steps[layer_id] = st
+        return st
+
+    def _fused_apps(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status):
+        """The fused step's kvq_append_params of K and V (built once per layer buffers;
+        per call the rows, the slot and the status words change)."""
+        B, H, S, D = k.shape
+        ent = self._apps[layer_id]
+        if ent is None:
+            G = D // self.group_size
+            sk = self._static_for("k", layer_id, H, G)
+            sv = self._static_for("v", layer_id, H, G)
+            pk, pv = self._append_params(layer_id, k, v, pos, None, sk, sv)
+            ent = (pk, pv, sk, sv)
+            self._apps[layer_id] = ent
+        pk, pv = ent[0], ent[1]
+        for side, p, x in (("k", pk, k), ("v", pv, v)):
+            if x.stride(-1) != 1:
+                x = x.contiguous()
+            p.x = x.data_ptr()
+            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride(0), x.stride(1), x.stride(2)
+            p.write_pos = pos
+            p.status = None if status is None else status.data_ptr() + (0 if side == "k" else 8)
+            p._keep = (x, ent[2], ent[3])
+        return pk, pv
+
+    def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
+                           sm_scale: Optional[float] = None,
+                           inv_tau: Optional[Tensor] = None) -> Tensor:
+        """Decode step of one layer: append the new token (k, v: fp16 [B, H, 1, D]) and attend
+        over the whole cache, the new token included (the append + attention of the
+        reference's decode step, src/engine/patch_model.py:755-957).  q: fp16 [B, Hq, D];
+        inv_tau: optional fp16 [Hq], applied as fp16(q * inv_tau) in the kernel.  Returns
+        fp16 [B, Hq, D].  With static group-32 INT8 scales (no adaptive policy) both run in
+        one HIP launch (kvq_append_decode_attn); otherwise ``append`` then the decode kernel.
+        Either way codes and output are bit-identical to ``append`` followed by
+        :func:`kernels.decode_attn_int8` / ``decode_attn_int4`` over the cache's tensors.
+        The kernel parameters are kept per layer between calls (no device tensor is created
+        besides the output).  With ``check_numerics``, NaN / Inf in k or v raise ValueError
+        and the cache does not advance."""
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        if S != 1:
+            raise ValueError(f"append_decode_attn appends one token per step, got S={S}")
+        if q.ndim != 3 or q.dtype != torch.float16 or q.shape[0] != B or q.shape[1] % H:
+            raise ValueError(f"q must be fp16 [B, Hq, D] with Hq a multiple of {H}, got "
+                             f"{q.dtype} {tuple(q.shape)}")
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        if not self._fused_step_ok(D):
+            self.append(layer_id, k, v)
+            n = self._layer_seq_lens[layer_id]
+            return self._step_for(layer_id, q.shape[1]).attend(q, n, sm_scale, inv_tau)
+        G = D // self.group_size
+        self._pre_append_checks(layer_id)
+        old = self._layer_seq_lens[layer_id]
+        n = old + 1
+        self._ensure_capacity(layer_id, B, H, D, G, n)
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv = self._fused_apps(layer_id, k, v, old, status)
+        out = self._step_for(layer_id, q.shape[1]).append_attend(q, n, sm_scale, inv_tau, pk, pv)
+        if status is not None:
+            self._check_status(layer_id, k.numel(), self._kind, self._qrange)
+        self._layer_seq_lens[layer_id] = n
+        if layer_id == 0:
+            self._seq_len = n
+        return out
 
     def _raw_views(self, layer_id: int, n: Optional[int] = None):
         if layer_id < 0 or layer_id >= self.num_layers:
@@ -418,6 +523,7 @@ class _SymCacheBase(_EngineBase):
         n = self.num_layers
         self._k_cache, self._v_cache = [None] * n, [None] * n
         self._k_scale, self._v_scale = [None] * n, [None] * n
+        self._steps, self._apps = [None] * n, [None] * n
         self._layer_seq_lens = [0] * n
         self._layer_capacity = [0] * n
         self._seq_len = 0
@@ -496,61 +602,9 @@ class INT8KVCache(_SymCacheBase):
         """(k_int8, v_int8, k_scale, v_scale) views [B, H, S, D] / [B, H, S, G] (fp16 scales)."""
         return self._raw_views(layer_id)
 
-    def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
-                           sm_scale: Optional[float] = None,
-                           inv_tau: Optional[Tensor] = None) -> Tensor:
-        """Decode step of one layer: append the new token (k, v: fp16 [B, H, 1, D]) and
-        attend over the whole cache, the new token included (the append + attention of the
-        reference's decode step, src/engine/patch_model.py:755-957).  Returns fp16
-        [B, Hq, D].  With static group-32 scales (no adaptive policy) both run in one HIP
-        launch (kvq_append_decode_attn); otherwise as ``append`` then the decode kernel.
-        Either way codes and output are bit-identical to ``append`` followed by
-        :func:`kernels.decode_attn_int8` over ``get_int8_tensors`` (q scaled by inv_tau).
-        With ``check_numerics``, NaN / Inf in k or v raise ValueError and the cache does
-        not advance."""
-        from .kernels import DecodePlan, kv_view_tok
-
-        self._validate_kv(layer_id, k, v)
-        B, H, S, D = k.shape
-        if S != 1:
-            raise ValueError(f"append_decode_attn appends one token per step, got S={S}")
-        if q.ndim != 3 or q.dtype != torch.float16 or q.shape[0] != B or q.shape[1] % H:
-            raise ValueError(f"q must be fp16 [B, Hq, D] with Hq a multiple of {H}, got "
-                             f"{q.dtype} {tuple(q.shape)}")
-        if sm_scale is None:
-            sm_scale = 1.0 / math.sqrt(D)
-        fused = (self.group_size == 32 and D == 128 and not self._side_is_token("k")
-                 and not self._side_is_token("v"))
-        if not fused:
-            self.append(layer_id, k, v)
-            kc, vc, ks, vs = self._raw_views(layer_id)
-            n = kc.shape[2]
-            ctx = torch.full((B,), n, dtype=torch.int32, device=q.device)
-            plan = DecodePlan(q, C.KVQ_FMT_INT8_SYM, kv_view_tok(kc, ks), C.KVQ_FMT_INT8_SYM,
-                              kv_view_tok(vc, vs), ctx, H, n, sm_scale, self.group_size,
-                              inv_tau=inv_tau, keepalive=(kc, vc, ks, vs))
-            return plan.launch()
-        G = D // self.group_size
-        self._pre_append_checks(layer_id)
-        sk = self._static_for("k", layer_id, H, G)
-        sv = self._static_for("v", layer_id, H, G)
-        old = self._layer_seq_lens[layer_id]
-        n = old + 1
-        self._ensure_capacity(layer_id, B, H, D, G, n)
-        status = self._status_buf(k.device) if self.check_numerics else None
-        pk, pv = self._append_params(layer_id, k, v, old, status, sk, sv)
-        kc, vc, ks, vs = self._raw_views(layer_id, n)
-        ctx = torch.full((B,), n, dtype=torch.int32, device=q.device)
-        plan = DecodePlan(q, C.KVQ_FMT_INT8_SYM, kv_view_tok(kc, ks), C.KVQ_FMT_INT8_SYM,
-                          kv_view_tok(vc, vs), ctx, H, n, sm_scale, self.group_size,
-                          inv_tau=inv_tau, keepalive=(kc, vc, ks, vs))
-        out = plan.launch_append(pk, pv)
-        if status is not None:
-            self._check_status(layer_id, k.numel(), self._kind, self._qrange)
-        self._layer_seq_lens[layer_id] = n
-        if layer_id == 0:
-            self._seq_len = n
-        return out
+    def _fused_step_ok(self, D: int) -> bool:
+        return (self.group_size == 32 and D == 128 and not self._side_is_token("k")
+                and not self._side_is_token("v"))
 
     def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
         """Dequantize (code * scale in fp32) and return fp16 K/V (int8_cache.py:490-542)."""
@@ -775,6 +829,7 @@ class _StaticG32Cache(_EngineBase):
                 no[:, :, :old] = self._ko[layer_id][:, :, :old]
         self._k[layer_id], self._v[layer_id], self._ko[layer_id] = nk, nv, no
         self._layer_capacity[layer_id] = new_cap
+        self._steps[layer_id] = self._apps[layer_id] = None
 
     def _append_params(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status):
         """kvq_append_params for K and V of this layer written at slot pos, and the
@@ -838,6 +893,24 @@ class _StaticG32Cache(_EngineBase):
         oi = None if self.k_outlier_idx is None else self.k_outlier_idx[layer_id]
         return C.KVQ_FMT_INT4_ASYM, kv_view_static(kb, self.k_scale[layer_id], self.k_zp[layer_id], oi, ob)
 
+    def _step_for(self, layer_id: int, q_heads: int):
+        """The layer's LayerStep (kernels.LayerStep) over its whole buffers."""
+        from .kernels import LayerStep, kv_view_static
+
+        kb = self._k[layer_id]
+        st = self._steps[layer_id]
+        if st is not None and st.key == (q_heads, kb.data_ptr()):
+            return st
+        B, H, cap = kb.shape[0], kb.shape[1], kb.shape[2]
+        kfmt, kview = self._k_view(layer_id, cap)
+        vb = self._v[layer_id]
+        st = LayerStep(kfmt, kview, C.KVQ_FMT_INT4_ASYM,
+                       kv_view_static(vb, self.v_scale[layer_id], self.v_zp[layer_id]),
+                       B, q_heads, H, 32, kb.device, keepalive=(vb,))
+        st.key = (q_heads, kb.data_ptr())
+        self._steps[layer_id] = st
+        return st
+
     def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
                            sm_scale: Optional[float] = None,
                            inv_tau: Optional[Tensor] = None) -> Tensor:
@@ -846,39 +919,48 @@ class _StaticG32Cache(_EngineBase):
         Returns fp16 [B, Hq, 128].  Codes and output are bit-identical to ``append`` then
         the decode kernel over the cache's tensors with context lengths ``get_seq_len()``
         (the append + attention of the reference's decode step,
-        src/engine/patch_model.py:755-957).  With ``check_numerics``, NaN / Inf in k or v
-        raise ValueError and the cache does not advance."""
-        from .kernels import DecodePlan, _check_static_args, kv_view_static
-
+        src/engine/patch_model.py:755-957).  The kernel parameters are kept per layer
+        between calls.  With ``check_numerics``, NaN / Inf in k or v raise ValueError and
+        the cache does not advance."""
         self._validate_kv(layer_id, k, v)
         B, H, S, D = k.shape
         if S != 1:
             raise ValueError(f"append_decode_attn appends one token per step, got S={S}")
         if self.k_scale.shape[1] != H:
             raise ValueError(f"calibration vs model heads mismatch: {self.k_scale.shape[1]} vs {H}")
+        if q.ndim != 3 or q.dtype != torch.float16 or q.shape[0] != B or q.shape[1] % H \
+                or q.shape[2] != 128:
+            raise ValueError(f"q must be fp16 [B, Hq, 128] with Hq a multiple of {H}, got "
+                             f"{q.dtype} {tuple(q.shape)}")
+        if q.stride(-1) != 1:
+            q = q.contiguous()
         old = self._layer_seq_lens[layer_id]
         self._ensure(layer_id, B, H, old + 1)
-        # the views the cache's getters give once the token is in (same split as the
-        # two-call path, hence the same output bits)
         n = old + 1
-        vb = self._v[layer_id][:, :, :-(-n // TILE_TOKENS)]
-        vs, vz = self.v_scale[layer_id], self.v_zp[layer_id]
-        kfmt, kview = self._k_view(layer_id, n)
-        _check_static_args(q, vb, vb, (vs, vz), torch.empty(B))
         if sm_scale is None:
             sm_scale = 1.0 / math.sqrt(D)
         status = self._status_buf(k.device) if self.check_numerics else None
-        pk, pv, keep = self._append_params(layer_id, k, v, old, status)
-        ctx = torch.full((B,), n, dtype=torch.int32, device=q.device)
-        plan = DecodePlan(q, kfmt, kview, C.KVQ_FMT_INT4_ASYM, kv_view_static(vb, vs, vz), ctx, H,
-                          n, sm_scale, 32, inv_tau=inv_tau, keepalive=(keep, vb))
-        out = plan.launch_append(pk, pv)
+        ent = self._apps[layer_id]
+        if ent is None:
+            pk, pv, _ = self._append_params(layer_id, k, v, old, None)
+            ent = (pk, pv)
+            self._apps[layer_id] = ent
+        pk, pv = ent
+        for side, p, x in (("k", pk, k), ("v", pv, v)):
+            if x.stride(-1) != 1:
+                x = x.contiguous()
+            p.x = x.data_ptr()
+            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride(0), x.stride(1), x.stride(2)
+            p.write_pos = old
+            p.status = None if status is None else status.data_ptr() + (0 if side == "k" else 8)
+            p._keep = (x,)
+        out = self._step_for(layer_id, q.shape[1]).append_attend(q, n, sm_scale, inv_tau, pk, pv)
         if status is not None:
             self._check_status(layer_id, k.numel(), "K8V4" if self._k_int8 else "INT4-asym",
                                "the code range")
-        self._layer_seq_lens[layer_id] = old + 1
+        self._layer_seq_lens[layer_id] = n
         if layer_id == 0:
-            self._seq_len = old + 1
+            self._seq_len = n
         return out
 
     def _check_layer(self, layer_id: int) -> int:
@@ -893,6 +975,7 @@ class _StaticG32Cache(_EngineBase):
     def release(self) -> None:
         n = self.num_layers
         self._k, self._v, self._ko = [None] * n, [None] * n, [None] * n
+        self._steps, self._apps = [None] * n, [None] * n
         self._layer_seq_lens = [0] * n
         self._layer_capacity = [0] * n
         self._seq_len = 0
@@ -1018,6 +1101,7 @@ class KIVIStyleKVCache(_EngineBase):
         self._k_cache[layer_id], self._v_cache[layer_id] = kc, vc
         self._v_scale[layer_id], self._v_zp[layer_id] = vs, vz
         self._layer_capacity[layer_id] = new_cap
+        self._steps[layer_id] = self._apps[layer_id] = None
 
     def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
         self._validate_kv(layer_id, k, v)
@@ -1099,21 +1183,71 @@ class KIVIStyleKVCache(_EngineBase):
         v = (unpack(vp).float() * vs.unsqueeze(-1) + vz.unsqueeze(-1)).to(self.dtype)
         return k, v
 
-    def decode_attn(self, layer_id: int, q: Tensor, sm_scale: Optional[float] = None) -> Tensor:
-        """Attention of q [B, Hq, 128] over layer_id's cache (INT4_KIVI decode kernel)."""
-        from .kernels import decode_attn_int4_kivi
+    def _step_for(self, layer_id: int, q_heads: int):
+        """The layer's LayerStep over its whole buffers and its frozen K parameters."""
+        from .kernels import LayerStep, kv_view_kivi
 
-        kp, vp, ks, kz, vs, vz = self.get_int4_asym_tensors(layer_id)
-        n = kp.shape[2]
-        ctx = torch.full((kp.shape[0],), n, dtype=torch.int32, device=q.device)
-        tau = self.inv_tau[layer_id] if (self.use_attn_temperature and self.inv_tau is not None) else None
-        out = decode_attn_int4_kivi(q, kp, vp, ks, kz, vs, vz, ctx, sm_scale, inv_tau=tau)
+        kc, ks = self._k_cache[layer_id], self._k_scale[layer_id]
+        key = (q_heads, kc.data_ptr(), ks.data_ptr())
+        st = self._steps[layer_id]
+        if st is not None and st.key == key:
+            return st
+        B, H = kc.shape[0], kc.shape[1]
+        vc, vs, vz, kz = self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id], \
+            self._k_zp[layer_id]
+        st = LayerStep(C.KVQ_FMT_INT4_KIVI, kv_view_kivi(kc, ks, kz, True), C.KVQ_FMT_INT4_KIVI,
+                       kv_view_kivi(vc, vs, vz, False), B, q_heads, H, 32, kc.device,
+                       keepalive=(kc, ks, kz, vc, vs, vz))
+        st.key = key
+        self._steps[layer_id] = st
+        return st
+
+    def _layer_tau(self, layer_id: int, q: Tensor) -> Optional[Tensor]:
+        """The engine's inv_tau[layer] as fp16 on q's device (converted once per layer)."""
+        if not (self.use_attn_temperature and self.inv_tau is not None):
+            return None
+        cache = self.__dict__.setdefault("_tau16", {})
+        t = cache.get(layer_id)
+        if t is None or t.device != q.device:
+            t = self.inv_tau[layer_id].to(device=q.device, dtype=torch.float16).contiguous()
+            cache[layer_id] = t
+        return t
+
+    def decode_attn(self, layer_id: int, q: Tensor, sm_scale: Optional[float] = None) -> Tensor:
+        """Attention of q [B, Hq, 128] over layer_id's cache (INT4_KIVI decode kernel); with
+        use_attn_temperature and inv_tau [L, Hq], q is scaled by inv_tau[layer] in fp16."""
+        n = self._check_layer(layer_id)
+        if q.ndim != 3 or q.shape[-1] != 128:
+            raise ValueError(f"q must be [B, Hq, 128], got {tuple(q.shape)}")
+        dt = q.dtype
+        q16 = q if q.dtype == torch.float16 else q.to(torch.float16)
+        if q16.stride(-1) != 1:
+            q16 = q16.contiguous()
+        sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
+        out = self._step_for(layer_id, q.shape[1]).attend(q16, n, sm, self._layer_tau(layer_id, q))
         self.record_fused_decode(layer_id, "hip_fused")
-        return out
+        return out if dt == torch.float16 else out.to(dt)
+
+    def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
+                           sm_scale: Optional[float] = None,
+                           inv_tau: Optional[Tensor] = None) -> Tensor:
+        """Decode step of one layer: ``append`` of the new token (k, v [B, H, 1, 128]) then
+        the attention of q [B, Hq, 128] over the cache including it.  inv_tau (fp16 [Hq])
+        overrides the engine's own per-layer inv_tau."""
+        if k.shape[2] != 1:
+            raise ValueError(f"append_decode_attn appends one token per step, got S={k.shape[2]}")
+        self.append(layer_id, k, v)
+        n = self._layer_seq_lens[layer_id]
+        if q.dtype != torch.float16 or q.stride(-1) != 1:
+            q = q.to(torch.float16).contiguous()
+        tau = inv_tau if inv_tau is not None else self._layer_tau(layer_id, q)
+        sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
+        return self._step_for(layer_id, q.shape[1]).attend(q, n, sm, tau)
 
     def clear(self) -> None:
         self._layer_seq_lens = [0] * self.num_layers
         self._seq_len = 0
+        self._steps = [None] * self.num_layers
         self._k_scale_initialized = [False] * self.num_layers
         self._k_scale = [None] * self.num_layers
         self._k_zp = [None] * self.num_layers
@@ -1122,6 +1256,7 @@ class KIVIStyleKVCache(_EngineBase):
         n = self.num_layers
         self._k_cache, self._v_cache = [None] * n, [None] * n
         self._v_scale, self._v_zp = [None] * n, [None] * n
+        self._steps, self._apps = [None] * n, [None] * n
         self._layer_capacity = [0] * n
         self.clear()
 

@@ -307,7 +307,10 @@ struct VAsym4 {
       r.w[e] = ld_stream<uint32_t>(vb + (int64_t)t * st + 4 * col);
     }
   }
-  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8],
+  // codes as the exact fp16 subnormals 16 n 2^-24 (even channel, high nibble) and n 2^-24
+  // (odd channel), each multiplied by both probability operands (softmax_tile); the
+  // combine applies out = s (acc / l * 2^20 or 2^24 - 8) + z
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
                                       const NibConsts& nc) const {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -315,13 +318,12 @@ struct VAsym4 {
       uint32_t R[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) R[p] = perm_b32(r.w[2 * p + 1], r.w[2 * p], sel);
-      acc[2 * k] = mfma16x16x32(pack8(and_or(R[0], nc.m_hi, nc.c64), and_or(R[1], nc.m_hi, nc.c64),
-                                      and_or(R[2], nc.m_hi, nc.c64), and_or(R[3], nc.m_hi, nc.c64)),
-                                pb, acc[2 * k]);
-      acc[2 * k + 1] =
-          mfma16x16x32(pack8(and_or(R[0], nc.m_lo, nc.c1024), and_or(R[1], nc.m_lo, nc.c1024),
-                             and_or(R[2], nc.m_lo, nc.c1024), and_or(R[3], nc.m_lo, nc.c1024)),
-                       pb, acc[2 * k + 1]);
+      const half8v ah = pack8(R[0] & nc.m_hi, R[1] & nc.m_hi, R[2] & nc.m_hi, R[3] & nc.m_hi);
+      const half8v al = pack8(R[0] & nc.m_lo, R[1] & nc.m_lo, R[2] & nc.m_lo, R[3] & nc.m_lo);
+      acc[2 * k] = mfma16x16x32(ah, pb, acc[2 * k]);
+      acc[2 * k + 1] = mfma16x16x32(al, pb, acc[2 * k + 1]);
+      acc[2 * k] = mfma16x16x32(ah, pl, acc[2 * k]);
+      acc[2 * k + 1] = mfma16x16x32(al, pl, acc[2 * k + 1]);
     }
   }
 };
@@ -374,7 +376,8 @@ struct VTok {
 #pragma unroll
     for (int p = 0; p < 4; ++p) r.s[p] = pair_h2(sv[2 * p], sv[2 * p + 1]);
   }
-  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8],
+  // vhat = fp16(code * scale) times both probability operands (softmax_tile)
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
                                       const NibConsts& nc) const {
     if constexpr (I4) {
 #pragma unroll
@@ -389,8 +392,11 @@ struct VTok {
           h[p] = deq_pair(and_or(R[p], nc.m_hi, nc.c64), (half_t)72.0f, r.s[p]);
           o[p] = deq_pair(and_or(R[p], nc.m_lo, nc.c1024), (half_t)1032.0f, r.s[p]);
         }
-        acc[2 * k] = mfma16x16x32(pack8(h[0], h[1], h[2], h[3]), pb, acc[2 * k]);
-        acc[2 * k + 1] = mfma16x16x32(pack8(o[0], o[1], o[2], o[3]), pb, acc[2 * k + 1]);
+        const half8v ah = pack8(h[0], h[1], h[2], h[3]), ao = pack8(o[0], o[1], o[2], o[3]);
+        acc[2 * k] = mfma16x16x32(ah, pb, acc[2 * k]);
+        acc[2 * k + 1] = mfma16x16x32(ao, pb, acc[2 * k + 1]);
+        acc[2 * k] = mfma16x16x32(ah, pl, acc[2 * k]);
+        acc[2 * k + 1] = mfma16x16x32(ao, pl, acc[2 * k + 1]);
       }
     } else {
 #pragma unroll
@@ -403,7 +409,9 @@ struct VTok {
           const uint32_t lo = r.w[2 * p][k >> 2] ^ 0x80808080u;
           u[p] = deq_pair(perm_b32(hi, lo, sel) | nc.c1024, (half_t)1152.0f, r.s[p]);
         }
-        acc[k] = mfma16x16x32(pack8(u[0], u[1], u[2], u[3]), pb, acc[k]);
+        const half8v au = pack8(u[0], u[1], u[2], u[3]);
+        acc[k] = mfma16x16x32(au, pb, acc[k]);
+        acc[k] = mfma16x16x32(au, pl, acc[k]);
       }
     }
   }
@@ -420,8 +428,7 @@ void decode_splitk_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, lg = lane >> 4;
 
-  int64_t ctx64 = a.ctx[b];
-  ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);
+  const int64_t ctx64 = row_context(a, b);
   const int ctx = (int)ctx64;
   const int t0 = chunk * a.chunk;
   if (t0 >= ctx) return;  // uniform over the work-group
@@ -445,8 +452,9 @@ void decode_splitk_kernel(DecodeArgs a) {
   // Softmax + PV of one tile whose QK logits (x0: tokens 4lg+r, x1: 16+4lg+r) are known.
   auto finish = [&](float4v x0, float4v x1, const typename VF::Raw& vt, int tt, bool masked) {
     if (masked) mask_tile(x0, x1, tt, t1, lg);
-    const half8v pb = softmax_tile(x0, x1, sm, m, l, acc);
-    vf.mma(vt, pb, acc, nc);
+    half8v pb, pl;
+    softmax_tile(x0, x1, sm, m, l, acc, pb, pl);
+    vf.mma(vt, pb, pl, acc, nc);
   };
 
   // Full tiles of this wave are tw + i * kStep for i < nfull; the (at most one) partial
@@ -499,8 +507,7 @@ void decode_splitk_kernel(DecodeArgs a) {
 // row-layout kernels; the tiled kernels combine in their last work-group).
 __global__ __launch_bounds__(kD) void combine_kernel(DecodeArgs a, int v_affine) {
   const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  int64_t ctx64 = a.ctx[b];
-  ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);
+  const int64_t ctx64 = row_context(a, b);
   combine_one(a, b, hq, d, valid_chunks(a, ctx64), v_affine);
 }
 
@@ -776,18 +783,19 @@ extern "C" int32_t kvq_decode_chunk_tokens(const kvq_decode_params* p) {
   return p ? choose_chunk(p) : 0;
 }
 
-// workspace: partial acc [B, Hq, n_chunks, 128] f32, partial (m, l) [B, Hq, n_chunks]
-// float2, then (256-byte aligned) the counter slots [B, Hkv] x 128 bytes of the tiled
-// kernel's single-launch merge
-static int64_t counters_offset(const kvq_decode_params* p, int64_t nch) {
-  const int64_t rows = (int64_t)p->batch * p->q_heads * nch;
-  return ((rows * (kD * 4 + 8) + 255) / 256) * 256;
+// workspace: the counter slots [B, Hkv] x 128 bytes of the tiled kernel's single-launch
+// merge (256-byte aligned size), then partial acc [B, Hq, n_chunks, 128] f32 and partial
+// (m, l) [B, Hq, n_chunks] float2.  The counters come first so that their place depends
+// only on B x Hkv: a zero-filled workspace can serve calls with other split counts.
+static int64_t counter_bytes(const kvq_decode_params* p) {
+  return (((int64_t)p->batch * p->kv_heads * kCtrSlotWords * 4 + 255) / 256) * 256;
 }
 
 extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   if (!p) return 0;
   const int64_t nch = n_chunks_for(p, choose_chunk(p));
-  return counters_offset(p, nch) + (int64_t)p->batch * p->kv_heads * kCtrSlotWords * 4 + 256;
+  const int64_t rows = (int64_t)p->batch * p->q_heads * nch;
+  return counter_bytes(p) + rows * (kD * 4 + 8) + 256;
 }
 
 // kvq_decode_attn, and with app != nullptr kvq_append_decode_attn (tiled path only)
@@ -807,8 +815,9 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
     return fail(KVQ_ERR_UNSUPPORTED, "group_size must be 8, 16, 32, 64 or 128");
   if (p->capacity < 0 || p->capacity > (int64_t)1 << 30)
     return fail(KVQ_ERR_INVALID, "capacity out of range");
-  if (!p->q || !p->out || !p->context_lens)
-    return fail(KVQ_ERR_INVALID, "q/out/context_lens is NULL");
+  if (!p->q || !p->out) return fail(KVQ_ERR_INVALID, "q/out is NULL");
+  if (!p->context_lens && p->context_len < 0)
+    return fail(KVQ_ERR_INVALID, "context_len must be >= 0 when context_lens is NULL");
   if (!aligned(p->q, 16) || p->q_stride_b % 8 || p->q_stride_h % 8)
     return fail(KVQ_ERR_UNSUPPORTED, "q rows must be 16-byte aligned");
   const int kf = p->k_format, vf = p->v_format;
@@ -852,6 +861,7 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   a.k = to_dev(p->k);
   a.v = to_dev(p->v);
   a.ctx = p->context_lens;
+  a.ctx_uniform = p->context_len;
   a.B = p->batch; a.Hq = p->q_heads; a.Hkv = p->kv_heads; a.n_rep = n_rep; a.gs = gs;
   a.cap = p->capacity;
   a.sm_log2e = p->sm_scale * kLog2e;
@@ -860,10 +870,10 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   a.strided = tiled ? 1 : 0;
   a.nw = waves_for(p);
   const int64_t rows = (int64_t)p->batch * p->q_heads * nch64;
-  a.part_acc = reinterpret_cast<float*>(p->workspace);
-  a.part_ml = reinterpret_cast<float2*>(reinterpret_cast<char*>(p->workspace) + rows * kD * 4);
-  a.counters = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(p->workspace) +
-                                           counters_offset(p, nch64));
+  char* ws = reinterpret_cast<char*>(p->workspace);
+  a.counters = reinterpret_cast<uint32_t*>(ws);
+  a.part_acc = reinterpret_cast<float*>(ws + counter_bytes(p));
+  a.part_ml = reinterpret_cast<float2*>(ws + counter_bytes(p) + rows * kD * 4);
 
   a.out = reinterpret_cast<half_t*>(p->out);
   a.o_sb = p->out_stride_b; a.o_sh = p->out_stride_h;
@@ -980,12 +990,11 @@ extern "C" int kvq_decode_attn_noalloc(const kvq_decode_params* p, kvq_stream_t 
   q.workspace_bytes = kNoallocScratchBytes;
   // clear the counter slots this call's merge uses (a fill kernel rather than a memset,
   // so that the call can be captured into a HIP graph)
-  const int64_t nch = n_chunks_for(p, choose_chunk(p));
+  // the counter slots are the first B x Hkv x 128 bytes of the workspace
   const int64_t words = (int64_t)p->batch * p->kv_heads * kCtrSlotWords;
-  const int64_t off = counters_offset(p, nch);
-  if (off < 0 || off + words * 4 > kNoallocScratchBytes)
+  if (words * 4 > kNoallocScratchBytes)
     return fail(KVQ_ERR_INVALID, "kvq_decode_attn_noalloc: counter slots outside the scratch");
-  uint32_t* ctr = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + off);
+  uint32_t* ctr = static_cast<uint32_t*>(ws);
   const int64_t blocks = (words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024;
   hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)blocks), dim3(256), 0, s, ctr, words);
   const hipError_t e = hipGetLastError();
@@ -1072,4 +1081,4 @@ extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_appe
 }
 
 extern "C" const char* kvq_last_error(void) { return g_last_error.c_str(); }
-extern "C" int32_t kvq_abi_version(void) { return 3; }
+extern "C" int32_t kvq_abi_version(void) { return 4; }

@@ -13,10 +13,11 @@ constexpr int kTile = 32;   // tokens per wave iteration (two 16-token MFMA row 
 constexpr int kD = 128;
 constexpr float kTau = 8.0f;  // lazy-rescale headroom in log2 units
 constexpr int kMaxChunks = 2048;
-// The workspace's counter area holds one slot of kCtrSlotWords u32 per (b, kv head), one
-// 128-byte line each (no two counters share a line).  Word 0 counts the work-groups that
-// have stored their partial (the tiled kernel's single-launch merge); it is zero between
-// calls.
+// The workspace starts with the counter area: one slot of kCtrSlotWords u32 per (b, kv
+// head), one 128-byte line each (no two counters share a line).  Word 0 counts the
+// work-groups that have stored their partial (the tiled kernel's single-launch merge); it
+// is zero between calls.  The chunk partials follow it, so the counters stay in place
+// when a reused workspace serves calls with other split counts.
 constexpr int kCtrSlotWords = 32;
 constexpr int kMinChunk = 256;
 
@@ -57,7 +58,8 @@ struct DecodeArgs {
   int64_t q_sb, q_sh;
   const half_t* inv_tau;
   KvDev k, v;
-  const int32_t* ctx;
+  const int32_t* ctx;  // context length per batch row, or null: every row has ctx_uniform
+  int ctx_uniform;
   int B, Hq, Hkv, n_rep, gs;
   int64_t cap;
   float sm_log2e;
@@ -73,6 +75,12 @@ struct DecodeArgs {
   int64_t o_sb, o_sh;
   FusedAppend app;
 };
+
+// context length of batch row b, clamped to [0, capacity]
+__device__ __forceinline__ int64_t row_context(const DecodeArgs& a, int b) {
+  const int64_t c = a.ctx != nullptr ? (int64_t)a.ctx[b] : (int64_t)a.ctx_uniform;
+  return c < 0 ? 0 : (c > a.cap ? a.cap : c);
+}
 
 __device__ __forceinline__ uint32_t splat_h2(half_t s) { return as_u32(half2v{s, s}); }
 __device__ __forceinline__ uint32_t pair_h2(half_t lo, half_t hi) { return as_u32(half2v{lo, hi}); }
@@ -116,12 +124,22 @@ __device__ __forceinline__ void load_q_group(const half_t* qr, int lg, half_t ta
 // 4 lg + r and 16 + 4 lg + r (r < 4) for head lane % 16, already masked to -inf where
 // invalid.  The running max m is raised only when a tile's max exceeds it by more than
 // kTau (decided wave-wide with a ballot), in which case l and acc are rescaled.
-// Returns the fp16 probabilities (rounded toward zero) as the PV B operand, in k-slot
-// order [4lg, 4lg+1, 4lg+2, 4lg+3, 16+4lg, .., 16+4lg+3]; l accumulates exactly those
-// fp16 values.
+// The fp32 probabilities p are returned as the PV B operands hi = fp16(p) (rounded toward
+// zero) and lo = fp16(p - hi) (p - hi is exact in fp32), in k-slot order [4lg, 4lg+1,
+// 4lg+2, 4lg+3, 16+4lg, .., 16+4lg+3]; l accumulates hi + lo.  The PV MFMAs multiply the
+// V operand by both, so each weight is carried to about 2^-21 of itself: one fp16 weight
+// alone perturbs the softmax weights by up to 2^-10, which for large V entries (|v - out|
+// of 100 and more) moves an output by more than 2e-3.
 // ex: optional two more running sums of the format (rescaled with l and acc)
-__device__ __forceinline__ half8v softmax_tile(float4v x0, float4v x1, float sm, float& m,
-                                               float& l, float4v acc[8], float* ex = nullptr) {
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const half2v h = pk_rtz(a, b);
+  hi = as_u32(h);
+  lo = as_u32(pk_rtz(a - (float)h.x, b - (float)h.y));
+}
+
+__device__ __forceinline__ void softmax_tile(float4v x0, float4v x1, float sm, float& m, float& l,
+                                             float4v acc[8], half8v& ph, half8v& pl,
+                                             float* ex = nullptr) {
   const float lmax = max8f(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]) * sm;
   if (__ballot(lmax > m + kTau)) {
     // raise the running max of every head to its current wave-wide maximum
@@ -137,16 +155,19 @@ __device__ __forceinline__ half8v softmax_tile(float4v x0, float4v x1, float sm,
     }
   }
   const float nm = -m;
-  const half2v pp0 = pk_rtz(fast_exp2(fmaf(x0[0], sm, nm)), fast_exp2(fmaf(x0[1], sm, nm)));
-  const half2v pp1 = pk_rtz(fast_exp2(fmaf(x0[2], sm, nm)), fast_exp2(fmaf(x0[3], sm, nm)));
-  const half2v pp2 = pk_rtz(fast_exp2(fmaf(x1[0], sm, nm)), fast_exp2(fmaf(x1[1], sm, nm)));
-  const half2v pp3 = pk_rtz(fast_exp2(fmaf(x1[2], sm, nm)), fast_exp2(fmaf(x1[3], sm, nm)));
+  uint32_t h[4], o[4];
+  split_pair(fast_exp2(fmaf(x0[0], sm, nm)), fast_exp2(fmaf(x0[1], sm, nm)), h[0], o[0]);
+  split_pair(fast_exp2(fmaf(x0[2], sm, nm)), fast_exp2(fmaf(x0[3], sm, nm)), h[1], o[1]);
+  split_pair(fast_exp2(fmaf(x1[0], sm, nm)), fast_exp2(fmaf(x1[1], sm, nm)), h[2], o[2]);
+  split_pair(fast_exp2(fmaf(x1[2], sm, nm)), fast_exp2(fmaf(x1[3], sm, nm)), h[3], o[3]);
   const half2v ones = {(half_t)1.0f, (half_t)1.0f};
-  l = __builtin_amdgcn_fdot2(pp0, ones, l, false);
-  l = __builtin_amdgcn_fdot2(pp1, ones, l, false);
-  l = __builtin_amdgcn_fdot2(pp2, ones, l, false);
-  l = __builtin_amdgcn_fdot2(pp3, ones, l, false);
-  return pack8(as_u32(pp0), as_u32(pp1), as_u32(pp2), as_u32(pp3));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    l = __builtin_amdgcn_fdot2(as_h2(h[i]), ones, l, false);
+    l = __builtin_amdgcn_fdot2(as_h2(o[i]), ones, l, false);
+  }
+  ph = pack8(h[0], h[1], h[2], h[3]);
+  pl = pack8(o[0], o[1], o[2], o[3]);
 }
 
 // DPP row_ror:8 within each row of 16 lanes (lane c reads lane (c + 8) % 16), written only
@@ -166,9 +187,10 @@ __device__ __forceinline__ float dpp_ror8f(float old, float src) {
 // from lane h into the padding lane h + 8, so each lane exponentiates 4 values instead of
 // 8.  m is kept equal in lanes h and h + 8; l holds the block-0 part of head h's sum in
 // lane h and the block-1 part in lane h + 8 (merge_and_store adds them).  The returned PV
-// operand is valid in lanes h < 8; lanes 8..15 carry finite values of padding columns.
-__device__ __forceinline__ half8v softmax_tile8(float4v x0, float4v x1, float sm, float& m,
-                                                float& l, float4v acc[8], float* ex = nullptr) {
+// operands are valid in lanes h < 8; lanes 8..15 carry finite values of padding columns.
+__device__ __forceinline__ void softmax_tile8(float4v x0, float4v x1, float sm, float& m,
+                                              float& l, float4v acc[8], half8v& ph, half8v& pl,
+                                              float* ex = nullptr) {
   float y[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) y[r] = dpp_ror8f<0xC>(x0[r], x1[r]);
@@ -187,13 +209,16 @@ __device__ __forceinline__ half8v softmax_tile8(float4v x0, float4v x1, float sm
     }
   }
   const float nm = -m;
-  const half2v pa = pk_rtz(fast_exp2(fmaf(y[0], sm, nm)), fast_exp2(fmaf(y[1], sm, nm)));
-  const half2v pb = pk_rtz(fast_exp2(fmaf(y[2], sm, nm)), fast_exp2(fmaf(y[3], sm, nm)));
+  uint32_t a0, a1, b0, b1;
+  split_pair(fast_exp2(fmaf(y[0], sm, nm)), fast_exp2(fmaf(y[1], sm, nm)), a0, b0);
+  split_pair(fast_exp2(fmaf(y[2], sm, nm)), fast_exp2(fmaf(y[3], sm, nm)), a1, b1);
   const half2v ones = {(half_t)1.0f, (half_t)1.0f};
-  l = __builtin_amdgcn_fdot2(pa, ones, l, false);
-  l = __builtin_amdgcn_fdot2(pb, ones, l, false);
-  const uint32_t a0 = as_u32(pa), a1 = as_u32(pb);
-  return pack8(a0, a1, dpp_ror8<0x3>(a0, a0), dpp_ror8<0x3>(a1, a1));
+  l = __builtin_amdgcn_fdot2(as_h2(a0), ones, l, false);
+  l = __builtin_amdgcn_fdot2(as_h2(b0), ones, l, false);
+  l = __builtin_amdgcn_fdot2(as_h2(a1), ones, l, false);
+  l = __builtin_amdgcn_fdot2(as_h2(b1), ones, l, false);
+  ph = pack8(a0, a1, dpp_ror8<0x3>(a0, a0), dpp_ror8<0x3>(a1, a1));
+  pl = pack8(b0, b1, dpp_ror8<0x3>(b0, b0), dpp_ror8<0x3>(b1, b1));
 }
 
 // masks logits of tokens >= t1 (tile starts at tt) to -inf
@@ -272,8 +297,9 @@ __host__ __device__ __forceinline__ int valid_chunks(const DecodeArgs& a, int64_
 }
 
 // Merges the first nvalid chunk partials of (b, query head hq) for output channel d and
-// writes the fp16 output, applying the asymmetric V epilogue
-// out = s (acc / l - off) + z (off = 72 or 1032 by channel parity) when v_affine.
+// writes the fp16 output, applying the asymmetric V epilogue when v_affine: the codes
+// entered the PV MFMA as the fp16 subnormals 16 n 2^-24 (even channel) and n 2^-24 (odd),
+// so out = s (acc / l * 2^20 or 2^24 - 8) + z.
 // Every partial of a batch of kCombineBatch chunks is requested before any is used.
 constexpr int kCombineBatch = 32;
 // the tiled kernel merges its chunk partials in the same launch (its last work-group per
@@ -326,7 +352,7 @@ __device__ __forceinline__ void combine_one(const DecodeArgs& a, int b, int hq, 
     const int hkv = hq / a.n_rep, g = d >> 5;
     const float s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
     const float z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
-    r = fmaf(s, r - ((d & 1) ? 1032.0f : 72.0f), z);
+    r = fmaf(s, fmaf(r, (d & 1) ? 16777216.0f : 1048576.0f, -8.0f), z);
   }
   o[d] = (half_t)r;
 }

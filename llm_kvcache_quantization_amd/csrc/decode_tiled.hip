@@ -30,9 +30,11 @@
 //    0x00F000F0 (high nibbles of bytes 0 and 2 -> the subnormal 16 n * 2^-24) and
 //    0x000F000F (low nibbles -> n * 2^-24), then the same on the dword shifted right by 8
 //    (bytes 1 and 3); the q side is one fp16 operand per channel and the logits come out
-//    scaled by 2^-24.  V: v_and_or_b32 with the same masks and the magics 0x5400 / 0x6400
-//    (64 + n and 1024 + n); those offsets (72 = 64 + 8 and 1032 = 1024 + 8 with the code
-//    offset) are removed in the epilogue, where they cancel exactly against l.
+//    scaled by 2^-24.  V: the same subnormals; the epilogue scales by 2^20 / 2^24 and
+//    removes the code offset 8 against l.
+//  * The probabilities enter the PV MFMAs as hi = fp16(p) and lo = fp16(p - hi), each
+//    multiplied by the V operand (16 MFMAs per tile), so the softmax weights keep about
+//    21 bits instead of fp16's 11 (see softmax_tile).
 //  * The q-dependent operands (fp16(q * s), the bias) are built once per work-group and
 //    shared through LDS; the q loads are issued before the first cache loads.
 //  * K and V tiles are fetched LOOK steps ahead of their use (register rings of
@@ -409,9 +411,10 @@ struct KAsymT {
   }
 };
 
-// INT4 asymmetric V in the TILE32 layout.  acc[c] (c < 8) accumulates sum_t p16 * x for
-// channel 8 col + c of the lane's d-row col, x = 64 + n (even c) or 1024 + n (odd c);
-// combine_kernel applies out = s (acc / l - off) + z with off = 72 or 1032.
+// INT4 asymmetric V in the TILE32 layout.  acc[c] (c < 8) accumulates sum_t p * x for
+// channel 8 col + c of the lane's d-row col, with the codes as the exact fp16 subnormals
+// x = 16 n 2^-24 (even c, high nibble) or n 2^-24 (odd c) and p the hi + lo probability
+// operands (softmax_tile); the epilogue applies out = s (acc / l * 2^20 or 2^24 - 8) + z.
 struct VAsymT {
   static constexpr bool kTile32 = true;
   // hooks of formats with per-token parameters (none here)
@@ -430,9 +433,10 @@ struct VAsymT {
     s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
     z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
   }
-  // channels 2 lane, 2 lane + 1 from the merged acc / l: x = 72 + c (even) or 1032 + c (odd)
+  // channels 2 lane, 2 lane + 1 from the merged acc / l: 2^20 r0 and 2^24 r1 are n = c + 8
   __device__ static half2v epilogue(float r0, float r1, float s, float z) {
-    return half2v{(half_t)fmaf(s, r0 - 72.0f, z), (half_t)fmaf(s, r1 - 1032.0f, z)};
+    return half2v{(half_t)fmaf(s, fmaf(r0, 1048576.0f, -8.0f), z),
+                  (half_t)fmaf(s, fmaf(r1, 16777216.0f, -8.0f), z)};
   }
 
   __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
@@ -448,7 +452,7 @@ struct VAsymT {
     r.w[0] = bload4(rv, v, soff);
     r.w[1] = bload4(rv, v + 16u, soff);
   }
-  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8],
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
                                       const NibConsts& nc) const {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -456,20 +460,18 @@ struct VAsymT {
       const uint32_t a0 = k ? r.w[0].y : r.w[0].x, a1 = k ? r.w[0].w : r.w[0].z;
       const uint32_t a2 = k ? r.w[1].y : r.w[1].x, a3 = k ? r.w[1].w : r.w[1].z;
       const uint32_t s0 = a0 >> 8, s1 = a1 >> 8, s2 = a2 >> 8, s3 = a3 >> 8;
-      acc[4 * k] = mfma16x16x32(pack8(and_or(a0, nc.m_hi, nc.c64), and_or(a1, nc.m_hi, nc.c64),
-                                      and_or(a2, nc.m_hi, nc.c64), and_or(a3, nc.m_hi, nc.c64)),
-                                pb, acc[4 * k]);
-      acc[4 * k + 1] =
-          mfma16x16x32(pack8(and_or(a0, nc.m_lo, nc.c1024), and_or(a1, nc.m_lo, nc.c1024),
-                             and_or(a2, nc.m_lo, nc.c1024), and_or(a3, nc.m_lo, nc.c1024)),
-                       pb, acc[4 * k + 1]);
-      acc[4 * k + 2] = mfma16x16x32(pack8(and_or(s0, nc.m_hi, nc.c64), and_or(s1, nc.m_hi, nc.c64),
-                                          and_or(s2, nc.m_hi, nc.c64), and_or(s3, nc.m_hi, nc.c64)),
-                                    pb, acc[4 * k + 2]);
-      acc[4 * k + 3] =
-          mfma16x16x32(pack8(and_or(s0, nc.m_lo, nc.c1024), and_or(s1, nc.m_lo, nc.c1024),
-                             and_or(s2, nc.m_lo, nc.c1024), and_or(s3, nc.m_lo, nc.c1024)),
-                       pb, acc[4 * k + 3]);
+      const half8v c0 = pack8(a0 & nc.m_hi, a1 & nc.m_hi, a2 & nc.m_hi, a3 & nc.m_hi);
+      const half8v c1 = pack8(a0 & nc.m_lo, a1 & nc.m_lo, a2 & nc.m_lo, a3 & nc.m_lo);
+      const half8v c2 = pack8(s0 & nc.m_hi, s1 & nc.m_hi, s2 & nc.m_hi, s3 & nc.m_hi);
+      const half8v c3 = pack8(s0 & nc.m_lo, s1 & nc.m_lo, s2 & nc.m_lo, s3 & nc.m_lo);
+      acc[4 * k] = mfma16x16x32(c0, pb, acc[4 * k]);
+      acc[4 * k + 1] = mfma16x16x32(c1, pb, acc[4 * k + 1]);
+      acc[4 * k + 2] = mfma16x16x32(c2, pb, acc[4 * k + 2]);
+      acc[4 * k + 3] = mfma16x16x32(c3, pb, acc[4 * k + 3]);
+      acc[4 * k] = mfma16x16x32(c0, pl, acc[4 * k]);
+      acc[4 * k + 1] = mfma16x16x32(c1, pl, acc[4 * k + 1]);
+      acc[4 * k + 2] = mfma16x16x32(c2, pl, acc[4 * k + 2]);
+      acc[4 * k + 3] = mfma16x16x32(c3, pl, acc[4 * k + 3]);
     }
   }
 };
@@ -621,7 +623,7 @@ struct VI8RowT {
       r.w[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(v + t * kD), 0, kBufNT));
     }
   }
-  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8],
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
                                       const NibConsts& nc) const {
     (void)nc;
 #pragma unroll
@@ -635,7 +637,9 @@ struct VI8RowT {
         const uint32_t hi = (c >> 2) ? r.w[2 * p + 1].y : r.w[2 * p + 1].x;
         R[p] = i8pair_deq(perm_b32(hi, lo, sel), s2);
       }
-      acc[c] = mfma16x16x32(pack8(R[0], R[1], R[2], R[3]), pb, acc[c]);
+      const half8v av = pack8(R[0], R[1], R[2], R[3]);
+      acc[c] = mfma16x16x32(av, pb, acc[c]);
+      acc[c] = mfma16x16x32(av, pl, acc[c]);
     }
   }
 };
@@ -793,7 +797,8 @@ struct VKiviRowT {
       if (tt + 16 + 4 * lg + i >= ctx) r.s[1][i] = r.z[1][i] = 0.f;
     }
   }
-  __device__ __forceinline__ void mma(const Raw& r, half8v pb, float4v acc[8], const NibConsts& nc) {
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v plo, float4v acc[8],
+                                      const NibConsts& nc) {
     float sk[8], wk[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -806,7 +811,8 @@ struct VKiviRowT {
     uint32_t ph[4], pl[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float p0 = (float)pb[2 * q], p1 = (float)pb[2 * q + 1];
+      const float p0 = (float)pb[2 * q] + (float)plo[2 * q];
+      const float p1 = (float)pb[2 * q + 1] + (float)plo[2 * q + 1];
       cz = fmaf(p0, wk[2 * q], cz);
       cz = fmaf(p1, wk[2 * q + 1], cz);
       half_t h0, l0, h1, l1;
@@ -1033,8 +1039,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   kf.load(kTile * tile[0], tile[0] < ncap, kr[0]);
   vf.load(kTile * tile[0], tile[0] < ncap, vr[0]);
 
-  int64_t ctx64 = a.ctx[b];
-  ctx64 = ctx64 < 0 ? 0 : (ctx64 > a.cap ? a.cap : ctx64);
+  const int64_t ctx64 = row_context(a, b);
   const int ctx = (int)ctx64;
   const int ntot = (ctx + kTile - 1) / kTile;
   const bool partial = (ctx & (kTile - 1)) != 0;
@@ -1100,10 +1105,10 @@ void decode_tiled_kernel(DecodeArgs a) {
           mask_tile(x0, x1, kTile * tile[0], ctx, lg);
           vf.mask(vr[u % R], kTile * tile[0], ctx, lg);
         }
-        half8v pb;
-        if constexpr (PACK8) pb = softmax_tile8(x0, x1, sm, m, l, acc, vf.extra());
-        else pb = softmax_tile(x0, x1, sm, m, l, acc, vf.extra());
-        vf.mma(vr[u % R], pb, acc, nc);
+        half8v pb, pl;
+        if constexpr (PACK8) softmax_tile8(x0, x1, sm, m, l, acc, pb, pl, vf.extra());
+        else softmax_tile(x0, x1, sm, m, l, acc, pb, pl, vf.extra());
+        vf.mma(vr[u % R], pb, pl, acc, nc);
         ++steps;
         progress[wave] = steps;
         if (__builtin_amdgcn_readfirstlane(progress[wave ^ 4]) < steps)

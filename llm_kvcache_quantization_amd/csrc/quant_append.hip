@@ -18,6 +18,13 @@
 
 #include <string>
 
+// Every product and sum below is rounded on its own, as torch rounds each tensor op: the
+// compiler must not contract a * b + c into one fused multiply-add.  HIP's __fmul_rn /
+// __fsub_rn do not prevent that (they are inline operators compiled outside this pragma),
+// so this file writes plain operators.  The interpolation of torch.quantile, which ATen
+// does compute as a fused multiply-add, calls fmaf explicitly.
+#pragma clang fp contract(off)
+
 namespace kvq {
 
 extern thread_local std::string g_last_error;
@@ -53,6 +60,7 @@ struct AppendDev {
   int64_t wpos;
   int32_t* status;
   int tile32;  // codes in KVQ_LAYOUT_TILE32 (INT4_ASYM)
+  float dq;              // dynamic scales: fp32(percentile / 100), or 0 for the absmax
   const float* thr_ptr;  // group-rescue threshold computed by the large-n select, or NULL
   int64_t st_sb;         // INT4_KIVI K: batch stride of the per-channel parameters
   float* zo;             // INT4_KIVI V: per-token zero-point out (scale_out's strides)
@@ -85,6 +93,43 @@ __device__ __forceinline__ float group_max(float v, int gs) {
   return v;
 }
 
+// torch.quantile's linear interpolation between the order statistics a <= b with weight
+// w = rank - floor(rank), as ATen's CPU lerp computes it: one fused multiply-add,
+// fma(w, b - a, a) for w < 0.5, else fma(w - 1, b - a, b) (w - 1 is exact).  The unfused
+// a + w (b - a) differs from it in the last bit for about 1 in 1000 inputs.
+__device__ __forceinline__ float quantile_lerp(float a, float b, float w) {
+  const float diff = b - a;
+  return w < 0.5f ? fmaf(w, diff, a) : fmaf(w - 1.0f, diff, b);
+}
+
+
+// torch.quantile(|x|, q) over the gs values of the lane's quantisation group (gs / 2
+// consecutive lanes holding 2 values each; a0, a1 = |x| of the lane's values), as the
+// reference's percentile-clipped dynamic quantizers take it (src/quant/int8_basic.py:78-83,
+// src/quant/int4_basic.py:84-90): every value's rank in the group (ties broken by channel
+// index) selects the order statistics at floor / ceil of fp32(q) * (gs - 1), which are
+// interpolated by quantile_lerp.  The group's lanes all return the result.
+__device__ float group_quantile(float a0, float a1, int gs, float q, int lane) {
+  const int nl = gs >> 1;
+  const int base = lane & ~(nl - 1);
+  const int e0 = 2 * (lane - base), e1 = e0 + 1;
+  int r0 = 0, r1 = 0;
+  for (int j = 0; j < nl; ++j) {
+    const float b0 = __shfl(a0, base + j, 64), b1 = __shfl(a1, base + j, 64);
+    const int f0 = 2 * j, f1 = 2 * j + 1;
+    r0 += (b0 < a0 || (b0 == a0 && f0 < e0)) + (b1 < a0 || (b1 == a0 && f1 < e0));
+    r1 += (b0 < a1 || (b0 == a1 && f0 < e1)) + (b1 < a1 || (b1 == a1 && f1 < e1));
+  }
+  const float rank = q * (float)(gs - 1);
+  const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
+  // the values of ranks lo and hi, spread over the group (|x| >= 0 > -1)
+  float vlo = fmaxf(r0 == lo ? a0 : -1.0f, r1 == lo ? a1 : -1.0f);
+  float vhi = fmaxf(r0 == hi ? a0 : -1.0f, r1 == hi ? a1 : -1.0f);
+  vlo = group_max(vlo, gs);
+  vhi = group_max(vhi, gs);
+  return quantile_lerp(vlo, vhi, rank - (float)lo);
+}
+
 // Scale of group g for a row, before the per-format final clamp.
 //  dyn_abs: absmax of the group's fp16 values (as float)
 __device__ __forceinline__ float int4_scale(const AppendDev& a, int h, int g, float dyn_abs,
@@ -98,11 +143,15 @@ __device__ __forceinline__ float int4_scale(const AppendDev& a, int h, int g, fl
   return fmaxf(s, 1e-5f);                                      // int4_basic.py:154
 }
 
+// dyn_abs: the group's absmax, or with a percentile its fp32 quantile of |x|
 __device__ __forceinline__ half_t int8_scale16(const AppendDev& a, int h, int g, float dyn_abs) {
   if (a.st == nullptr) {
-    // dynamic absmax path: fp16 absmax clamped, then absmax / 127 in fp16 arithmetic
-    const float am = fmaxf(dyn_abs, (float)(half_t)1e-5f);   // int8_basic.py:91-92
-    return (half_t)__fdiv_rn(am, 127.0f);                     // :94
+    // dynamic path: the fp16 absmax clamped in fp16 (int8_basic.py:85, :91-92), or the fp32
+    // quantile clamped in fp32 then rounded to fp16 (:78-83, :91-92); then abs_max / 127 in
+    // fp16 arithmetic (:94)
+    const half_t am = a.dq > 0.f ? (half_t)fmaxf(dyn_abs, 1e-5f)
+                                 : (half_t)fmaxf(dyn_abs, (float)(half_t)1e-5f);
+    return (half_t)__fdiv_rn((float)am, 127.0f);
   }
   float s = ld_static(a, h, g);
   if (a.adaptive) {
@@ -131,10 +180,10 @@ __device__ __forceinline__ void for_each_dyn(const AppendDev& a, F f) {
 
 // rank of torch.quantile's lower order statistic: lo = floor(fp32(q) * (n - 1)); hi = ceil
 __device__ __forceinline__ void quantile_ranks(float q, int64_t n, int64_t& lo, int64_t& hi, float& w) {
-  const float rank = __fmul_rn(q, (float)(n - 1));
+  const float rank = q * (float)(n - 1);
   lo = (int64_t)floorf(rank);
   hi = (int64_t)ceilf(rank);
-  w = __fsub_rn(rank, (float)lo);
+  w = rank - (float)lo;
 }
 
 __global__ void rescue_init_kernel(RescueScratch* s, float q, int64_t n) {
@@ -218,8 +267,7 @@ __global__ void rescue_thr_kernel(RescueScratch* s, float q, int64_t n) {
   quantile_ranks(q, n, lo, hi, w);
   const float va = __uint_as_float(s->prefix);
   const float vb = (hi < (int64_t)s->cnt_le) ? va : __uint_as_float(s->min_gt);
-  const float diff = __fsub_rn(vb, va);
-  s->thr = w < 0.5f ? __fadd_rn(va, __fmul_rn(w, diff)) : __fsub_rn(vb, __fmul_rn(diff, __fsub_rn(1.0f, w)));
+  s->thr = quantile_lerp(va, vb, w);
 }
 
 __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
@@ -238,7 +286,11 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
   const unsigned long long badmask = __ballot(bad);
   if (badmask && lane == 0 && a.status) atomicOr(&a.status[0], 1);
 
-  const float am = group_max(fmaxf(fabsf(x0), fabsf(x1)), a.gs);
+  // the group's absmax, or for a percentile-clipped dynamic scale its quantile of |x|
+  const bool pct = a.st == nullptr && a.dq > 0.f &&
+                   (a.fmt == KVQ_FMT_INT8_SYM || a.fmt == KVQ_FMT_INT4_SYM);
+  const float am = pct ? group_quantile(fabsf(x0), fabsf(x1), a.gs, a.dq, lane)
+                       : group_max(fmaxf(fabsf(x0), fabsf(x1)), a.gs);
   uint8_t* crow = a.codes + (int64_t)b * a.csb + (int64_t)h * a.csh + t * a.cst;
   int clipped = 0;
 
@@ -246,6 +298,8 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
     const half_t s16 = int8_scale16(a, h, g, am);
     const float sf = (float)s16;
     *reinterpret_cast<uint16_t*>(crow + d0) = int8_pack_pair(x0, x1, s16, clipped);
+    // the clip statistic is the static-scale path's (int8_cache.py:401-419)
+    if (a.st == nullptr) clipped = 0;
     if (a.so && (d0 % a.gs) == 0) {
       const int64_t off = (int64_t)b * a.sosb + (int64_t)h * a.sosh + t * a.sost + (int64_t)g * a.sosg;
       if (a.so_f32) reinterpret_cast<float*>(a.so)[off] = sf;
@@ -254,8 +308,9 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
   } else if (a.fmt == KVQ_FMT_INT4_SYM) {
     float s;
     if (a.st == nullptr) {
-      // fp16 absmax clamped in fp16, then divided in fp32 (int4_basic.py:86-99)
-      s = __fdiv_rn(fmaxf(am, (float)(half_t)1e-5f), 7.0f);
+      // the fp16 absmax clamped in fp16, or the fp32 quantile clamped in fp32, then divided
+      // in fp32 (int4_basic.py:84-99)
+      s = __fdiv_rn(pct ? fmaxf(am, 1e-5f) : fmaxf(am, (float)(half_t)1e-5f), 7.0f);
     } else {
       s = int4_scale(a, h, g, am, thr);
     }
@@ -288,16 +343,16 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
         mx = fmaxf(mx, __shfl_xor(mx, o, 64));
       }
       // range floor max(1e-5, fp16 tiny * 15) = 15 * 2^-14; z = min - (-8) s
-      s0 = s1 = __fdiv_rn(fmaxf(__fsub_rn(mx, mn), 9.1552734375e-4f), 15.0f);
-      z0 = z1 = __fadd_rn(mn, 8.0f * s0);
+      s0 = s1 = __fdiv_rn(fmaxf(mx - mn, 9.1552734375e-4f), 15.0f);
+      z0 = z1 = mn + 8.0f * s0;
       if (lane == 0 && a.so) {
         const int64_t off = (int64_t)b * a.sosb + (int64_t)h * a.sosh + t * a.sost;
         reinterpret_cast<float*>(a.so)[off] = s0;
         a.zo[off] = z0;
       }
     }
-    const float r0 = rintf(__fdiv_rn(__fsub_rn(x0, z0), s0));
-    const float r1 = rintf(__fdiv_rn(__fsub_rn(x1, z1), s1));
+    const float r0 = rintf(__fdiv_rn(x0 - z0, s0));
+    const float r1 = rintf(__fdiv_rn(x1 - z1, s1));
     if (a.st != nullptr) clipped = (r0 < -8.f || r0 > 7.f) + (r1 < -8.f || r1 > 7.f);
     const int q0 = (int)fminf(fmaxf(r0, -8.f), 7.f), q1 = (int)fminf(fmaxf(r1, -8.f), 7.f);
     crow[lane] = (uint8_t)(((q0 + 8) << 4) | (q1 + 8));
@@ -343,15 +398,11 @@ __device__ void lds_bitonic_sort(float* v, int n_pad) {
 
 // torch.quantile(x, q) with linear interpolation, float32 arithmetic:
 // rank = fp32(q) * (n - 1); lo = floor(rank); hi = ceil(rank); w = rank - lo;
-// lerp(a, b, w) = w < 0.5 ? a + w * (b - a) : b - (b - a) * (1 - w)   (no FMA contraction)
+// quantile_lerp(v[lo], v[hi], w)
 __device__ float sorted_quantile(const float* v, int n, float q) {
-  const float rank = __fmul_rn(q, (float)(n - 1));
+  const float rank = q * (float)(n - 1);
   const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
-  const float w = __fsub_rn(rank, (float)lo);
-  const float a = v[lo], b = v[hi];
-  const float diff = __fsub_rn(b, a);
-  return w < 0.5f ? __fadd_rn(a, __fmul_rn(w, diff))
-                  : __fsub_rn(b, __fmul_rn(diff, __fsub_rn(1.0f, w)));
+  return quantile_lerp(v[lo], v[hi], rank - (float)lo);
 }
 
 __global__ __launch_bounds__(kAppendWaves * 64) void append_kernel(AppendDev k, AppendDev v,
@@ -430,6 +481,8 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
       return fail(KVQ_ERR_INVALID, n + ": INT4_KIVI V needs fp32 scale_out and zp_out");
     }
   }
+  if (!(p->dyn_quantile >= 0.f && p->dyn_quantile < 1.f))
+    return fail(KVQ_ERR_INVALID, n + ": dyn_quantile must lie in [0, 1)");
   if (p->codes_layout != KVQ_LAYOUT_ROWS && p->codes_layout != KVQ_LAYOUT_TILE32)
     return fail(KVQ_ERR_INVALID, n + ": unknown codes_layout");
   if (p->codes_layout == KVQ_LAYOUT_TILE32) {
@@ -461,6 +514,7 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   d.tile32 = p->codes_layout == KVQ_LAYOUT_TILE32;
   d.st_sb = p->static_stride_b;
   d.zo = reinterpret_cast<float*>(p->zp_out);
+  d.dq = p->dyn_quantile;
   return KVQ_OK;
 }
 

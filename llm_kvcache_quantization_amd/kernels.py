@@ -143,6 +143,24 @@ def kv_view_static(
     return v
 
 
+_WORKSPACES = {}
+
+
+def _shared_workspace(device, nbytes: int, units: int) -> torch.Tensor:
+    """A zero-filled workspace of at least nbytes for the calls of the function-style entry
+    points on the current stream of device with ``units`` = batch x kv_heads, kept and
+    grown between calls.  Its first units x 128 bytes are the merge counters, which every
+    call leaves zero, and the partials follow them: calls with the same units ordered on
+    one stream can share it.  Another units count or stream gets its own (a larger count
+    would find its counters where partials were written)."""
+    key = (str(device), torch.cuda.current_stream(device).cuda_stream, int(units))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 class DecodePlan:
     """A prepared kvq_decode_attn call over fixed tensors.
 
@@ -166,6 +184,7 @@ class DecodePlan:
         out: Optional[torch.Tensor] = None,
         chunk_tokens: int = 0,
         keepalive: tuple = (),
+        shared_workspace: bool = False,
     ):
         B, Hq, D = q.shape
         self.q = q
@@ -190,11 +209,14 @@ class DecodePlan:
         p.chunk_tokens = int(env_chunk) if (env_chunk and not chunk_tokens) else int(chunk_tokens)
         L = C.lib()
         nbytes = int(L.kvq_decode_workspace_bytes(ctypes.byref(p)))
-        # zero-filled once: the workspace holds the fused combine's arrival counters, which
-        # every call leaves zero
-        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=q.device)
+        if shared_workspace:
+            self.workspace = _shared_workspace(q.device, nbytes, B * kv_heads)
+        else:
+            # zero-filled once: the workspace holds the merge's arrival counters, which every
+            # call leaves zero
+            self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=q.device)
         p.workspace = self.workspace.data_ptr()
-        p.workspace_bytes = nbytes
+        p.workspace_bytes = self.workspace.numel()
         p.out = self.out.data_ptr()
         p.out_stride_b, p.out_stride_h = self.out.stride(0), self.out.stride(1)
         self.params = p
@@ -225,6 +247,78 @@ class DecodePlan:
         C.check(C.lib().kvq_append_decode_attn(self._pp, ctypes.byref(k_new), ctypes.byref(v_new),
                                                ctypes.c_void_p(s)))
         return self.out
+
+
+class LayerStep:
+    """The kvq_decode_params block of one cache layer, kept from one decode step to the next.
+
+    The K / V views point at the layer's code and scale buffers (whole capacity); per call
+    only q, the output, the context length (passed by value: ``context_lens`` is NULL, every
+    row has the same length, as in the reference's decode step,
+    src/engine/patch_model.py:799-804) and, for the fused step, the new rows change.  The
+    workspace is kept and grows when a call needs more; its merge counters sit at its start,
+    so a zero-filled workspace serves every later call.  A call costs one C call plus the
+    output allocation: no device tensor is created, filled or read back.
+    """
+
+    def __init__(self, k_format: int, k_view: C.KvView, v_format: int, v_view: C.KvView,
+                 batch: int, q_heads: int, kv_heads: int, group_size: int, device,
+                 keepalive: tuple = ()):
+        self._keep = (keepalive, k_view, v_view)
+        p = C.DecodeParams()
+        p.k_format, p.v_format = k_format, v_format
+        p.k, p.v = k_view, v_view
+        p.context_lens = None
+        p.batch, p.q_heads, p.kv_heads = batch, q_heads, kv_heads
+        p.head_dim, p.group_size = HEAD_DIM, group_size
+        env_chunk = os.environ.get("KVQ_CHUNK_TOKENS")
+        p.chunk_tokens = int(env_chunk) if env_chunk else 0
+        self.params = p
+        self._pp = ctypes.byref(p)
+        self.device = torch.device(device)
+        self.workspace: Optional[torch.Tensor] = None
+        self._tau = None
+
+    def _prepare(self, q: torch.Tensor, n: int, sm_scale: float,
+                 inv_tau: Optional[torch.Tensor]) -> torch.Tensor:
+        p = self.params
+        p.q = q.data_ptr()
+        p.q_stride_b, p.q_stride_h = q.stride(0), q.stride(1)
+        p.inv_tau = _ptr(inv_tau)
+        self._tau = inv_tau
+        p.capacity = n
+        p.context_len = n
+        p.sm_scale = float(sm_scale)
+        L = C.lib()
+        need = int(L.kvq_decode_workspace_bytes(self._pp))
+        if self.workspace is None or self.workspace.numel() < need:
+            # zero-filled when (re)allocated: the merge counters at its start must be zero
+            self.workspace = torch.zeros(max(need, int(need * 1.25)), dtype=torch.uint8,
+                                         device=self.device)
+            p.workspace = self.workspace.data_ptr()
+            p.workspace_bytes = self.workspace.numel()
+        out = torch.empty_like(q)
+        p.out = out.data_ptr()
+        p.out_stride_b, p.out_stride_h = out.stride(0), out.stride(1)
+        return out
+
+    def attend(self, q: torch.Tensor, n: int, sm_scale: float,
+               inv_tau: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """kvq_decode_attn of q [B, Hq, 128] fp16 over the first n tokens of every row."""
+        out = self._prepare(q, n, sm_scale, inv_tau)
+        C.check(C.lib().kvq_decode_attn(self._pp, ctypes.c_void_p(C.stream_handle(self.device))))
+        return out
+
+    def append_attend(self, q: torch.Tensor, n: int, sm_scale: float,
+                      inv_tau: Optional[torch.Tensor], k_new: C.AppendParams,
+                      v_new: C.AppendParams) -> torch.Tensor:
+        """kvq_append_decode_attn: the new token described by k_new / v_new (slot n - 1)
+        quantized into the layer's buffers and attention over the first n tokens, one
+        launch."""
+        out = self._prepare(q, n, sm_scale, inv_tau)
+        C.check(C.lib().kvq_append_decode_attn(self._pp, ctypes.byref(k_new), ctypes.byref(v_new),
+                                               ctypes.c_void_p(C.stream_handle(self.device))))
+        return out
 
 
 def _bump_debug_stats(debug_stats, layer_idx, block_size):
@@ -423,7 +517,7 @@ def _decode_tok(q, k_cache, v_cache, k_scale, v_scale, context_lens, sm_scale, d
     plan = DecodePlan(
         qk, fmt, kv_view_tok(k_cache, k_scale), fmt, kv_view_tok(v_cache, v_scale),
         ctx, kv_heads, max_seq, sm_scale, group_size,
-        keepalive=(k_cache, v_cache, k_scale, v_scale))
+        keepalive=(k_cache, v_cache, k_scale, v_scale), shared_workspace=True)
     _bump_debug_stats(debug_stats, layer_idx, block_size)
     out = plan.launch()
     if original_dtype != torch.float16:
@@ -513,7 +607,7 @@ def decode_attn_int4_kivi(
         q16, C.KVQ_FMT_INT4_KIVI, kv_view_kivi(kc, ks, kz, True),
         C.KVQ_FMT_INT4_KIVI, kv_view_kivi(vc, vs, vz, False),
         _ctx_i32(context_lens, q.device), Hkv, S, sm_scale, 32, inv_tau=inv_tau,
-        keepalive=(kc, vc, ks, kz, vs, vz))
+        keepalive=(kc, vc, ks, kz, vs, vz), shared_workspace=True)
     out = plan.launch()
     return out if original_dtype == torch.float16 else out.to(original_dtype)
 
@@ -567,7 +661,8 @@ def decode_attn_int4_asym(
         C.KVQ_FMT_INT4_ASYM, kv_view_static(v_codes, v_scale, v_zp),
         _ctx_i32(context_lens, q.device), k_codes.shape[1], k_codes.shape[2], sm_scale, 32,
         inv_tau=inv_tau,
-        keepalive=(k_codes, v_codes, k_scale, k_zp, v_scale, v_zp, k_outlier_idx, k_outlier_val))
+        keepalive=(k_codes, v_codes, k_scale, k_zp, v_scale, v_zp, k_outlier_idx, k_outlier_val),
+        shared_workspace=True)
     return plan.launch()
 
 
@@ -595,7 +690,7 @@ def decode_attn_k8v4(
         q, C.KVQ_FMT_INT8_SYM, kv_view_tok(k_codes, k_scale),
         C.KVQ_FMT_INT4_ASYM, kv_view_static(v_codes, v_scale, v_zp),
         _ctx_i32(context_lens, q.device), k_codes.shape[1], k_codes.shape[2], sm_scale, 32,
-        inv_tau=inv_tau, keepalive=(k_codes, k_scale, v_codes, v_scale, v_zp))
+        inv_tau=inv_tau, keepalive=(k_codes, k_scale, v_codes, v_scale, v_zp), shared_workspace=True)
     return plan.launch()
 
 

@@ -76,18 +76,28 @@ def quantize_symmetric_int8_with_scale(
     return q.view(B, H, S, D), s.squeeze(-1)
 
 
+def _group_absmax(xr: torch.Tensor, percentile: float) -> torch.Tensor:
+    """|x| per group: its maximum (in x's dtype), or below percentile 100 its torch.quantile
+    at percentile / 100 in fp32 (src/quant/int8_basic.py:76-85, int4_basic.py:80-92)."""
+    a = xr.abs()
+    if percentile < 100.0:
+        q = max(min(percentile / 100.0, 1.0), 0.0)
+        return torch.quantile(a.float(), q, dim=-1, keepdim=True)
+    return torch.amax(a, dim=-1, keepdim=True)
+
+
 def quantize_symmetric_int8(
     x: torch.Tensor, percentile: float = 100.0, group_size: int = 128
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Dynamic INT8, absmax branch (src/quant/int8_basic.py:18-108, percentile >= 100)."""
-    if percentile < 100.0:
-        raise NotImplementedError("percentile clipping is not restated (absmax branch only)")
+    """Dynamic INT8 (src/quant/int8_basic.py:18-108): abs_max per group (absmax, or the
+    percentile's torch.quantile), clamped to 1e-5, cast to x's dtype, divided by 127 in that
+    dtype; codes round(x / s) in x's dtype, clamped to [-127, 127]."""
     check_finite(x, "quantize_symmetric_int8")
     B, H, S, D = x.shape
     gs = D if group_size == -1 else group_size
     G = D // gs
     xr = x.view(B, H, S, G, gs)
-    am = xr.abs().amax(dim=-1, keepdim=True).clamp(min=CLAMP_MIN).to(x.dtype)
+    am = _group_absmax(xr, percentile).clamp(min=CLAMP_MIN).to(x.dtype)
     s = am / 127.0
     q = torch.round(xr / s).clamp(-127, 127).to(torch.int8)
     return q.view(B, H, S, D), s.squeeze(-1)
@@ -113,18 +123,40 @@ def quantize_symmetric_int4_with_scale(
 def quantize_symmetric_int4(
     x: torch.Tensor, percentile: float = 100.0, group_size: int = 32
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Dynamic INT4, absmax branch (src/quant/int4_basic.py:24-112, percentile >= 100)."""
-    if percentile < 100.0:
-        raise NotImplementedError("percentile clipping is not restated (absmax branch only)")
+    """Dynamic INT4 (src/quant/int4_basic.py:24-112): abs_max per group (absmax, or the
+    percentile's torch.quantile), clamped to 1e-5, in fp32, divided by 7; codes
+    round(x / s) in fp32, clamped to [-7, 7]; fp32 scales."""
     check_finite(x, "quantize_symmetric_int4")
     B, H, S, D = x.shape
     gs = D if group_size == -1 else group_size
     G = D // gs
     xr = x.view(B, H, S, G, gs)
-    am = xr.abs().amax(dim=-1, keepdim=True).clamp(min=CLAMP_MIN).to(torch.float32)
+    am = _group_absmax(xr, percentile).clamp(min=CLAMP_MIN).to(torch.float32)
     s = am / 7.0
     q = torch.round(xr / s).clamp(-7, 7).to(torch.int8)
     return q.view(B, H, S, D), s.to(torch.float32).squeeze(-1)
+
+
+def dequantize_symmetric(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """src/quant/int8_basic.py:167-246 and src/quant/int4_basic.py:162-227 with a 4-D scale
+    [B, H, S, G] (paths B / B'): the codes in the scale's dtype times the group's scale,
+    result in the scale's dtype."""
+    if q.dtype != torch.int8:
+        raise ValueError(f"quantized must be torch.int8, got {q.dtype}")
+    B, H, S, D = q.shape
+    G = scale.shape[-1]
+    if G <= 0 or D % G:
+        raise ValueError(f"Invalid scale shape: quantized={tuple(q.shape)}, scale={tuple(scale.shape)}")
+    if G == 1:
+        return q.to(scale.dtype) * scale
+    return (q.view(B, H, S, G, D // G).to(scale.dtype) * scale.unsqueeze(-1)).view(B, H, S, D)
+
+
+def cache_get_kv(codes: torch.Tensor, scale: torch.Tensor, dtype=torch.float16) -> torch.Tensor:
+    """INT8KVCache / INT4KVCache.get_kv of one side (src/cache/int8_cache.py:490-542,
+    src/cache/int4_cache.py:591-649): the stored fp32 scales (INT8 keeps its fp16 scale
+    widened) times the codes in fp32, then cast to the cache dtype."""
+    return dequantize_symmetric(codes, scale.to(torch.float32)).to(dtype)
 
 
 def pack_int4(q: torch.Tensor) -> torch.Tensor:

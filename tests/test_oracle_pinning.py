@@ -13,9 +13,13 @@ term, a wrong sign or index, a swapped nibble) fails at least one check:
   layout (high nibble = even element).
 * quantize_asymmetric_static: numpy float32 closed form, plus the reference K
   quantize+pack formula of tests/test_fused_quantize_pack.py:8-17.
-* outlier_rescue: torch.quantile (the library routine the reference calls) is restated
-  in float32 (the arithmetic the HIP kernel uses) and compared bitwise.  The rescued
-  set is checked against the closed form "values >= the interpolated threshold".
+* outlier_rescue and the percentile-clipped dynamic quantizers: torch.quantile (the
+  library routine the reference calls) against a float32 closed form -- the order
+  statistics at floor / ceil of fp32(q) (n - 1) and ATen's CPU lerp, one fused
+  multiply-add in exact rational arithmetic -- compared bitwise over 1500 random sets and
+  every group of the quantizer tests.  The unfused a + w (b - a), a plausible
+  restatement, misses torch in some of those cases (asserted).  The rescued set is
+  checked against "values >= the interpolated threshold".
 * decode_attn_int8_torch_ref: the KATs of tests/test_patch_model.py:280-368 (S=1 -> V,
   softmax [e/(e+1), 1/(e+1)], ctx=0 -> 0, GQA head h -> kv head h // n_rep), a float64
   brute force on tiny inputs, and permutation / scaling invariants.
@@ -30,10 +34,15 @@ term, a wrong sign or index, a swapped nibble) fails at least one check:
   (src/cache/int4_cache.py:447-529): the same kind of known answers in fp32, and the
   reference's documented identity that outlier rescue after mixed rescue changes nothing
   (int4_cache.py:360-378).
+* dequantize_symmetric / cache_get_kv: known answers (code x scale of its own group, the
+  group index d // gs, per-token scalar scale) and the exactness of the fp32 product
+  (an 8-bit code times an 11-bit fp16 scale is exact, so the cache's fp16 result is one
+  rounding of the exact product, checked against float64).
 * decode_attn_k8v4_ref: float64 brute force (INT8 K dequantised as the fp16 product the
   reference forms, asymmetric V in float64, q * inv_tau as an fp16 product).
 """
 import math
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -154,28 +163,79 @@ def test_pack_unpack_kats():
         assert torch.equal(OQ.unpack_int4(p), x)
 
 
+def fused_lerp32(a, b, w):
+    """torch.quantile's interpolation as ATen's CPU lerp computes it, one rounding per
+    fused multiply-add (exact rational arithmetic, then the nearest float32)."""
+    a, b, w = np.float32(a), np.float32(b), np.float32(w)
+    d = Fraction(float(np.float32(b - a)))
+    if w < 0.5:
+        exact = Fraction(float(w)) * d + Fraction(float(a))
+    else:
+        exact = Fraction(float(np.float32(w - np.float32(1)))) * d + Fraction(float(b))
+    return np.float32(float(exact))
+
+
+def quantile32(v, q):
+    """Closed form of torch.quantile(v, q) (linear) in float32: rank = fp32(q) * (n - 1),
+    the order statistics at floor / ceil of it, fused_lerp32 between them."""
+    s = np.sort(np.asarray(v, dtype=np.float32))
+    n = s.shape[0]
+    rank = np.float32(np.float32(q) * np.float32(n - 1))
+    lo, hi = int(np.floor(rank)), int(np.ceil(rank))
+    return fused_lerp32(s[lo], s[hi], np.float32(rank - np.float32(lo))), s[lo], s[hi]
+
+
 def test_rescue_quantile_matches_torch_and_closed_form():
     rng = np.random.default_rng(0)
-    for n in (1, 2, 3, 16, 127, 128, 129, 512, 4096):
-        for ratio in (0.01, 0.05, 0.3, 0.5, 0.999):
-            v = (np.abs(rng.standard_normal(n)) * rng.uniform(0.1, 10)).astype(np.float32)
-            if n > 8:
-                v[rng.integers(0, n, 3)] = v[0]  # ties
-            q = max(0.0, min(1.0, 1.0 - ratio))
-            ref = torch.quantile(torch.from_numpy(v), q).item()
-            # float32 restatement: the arithmetic of the HIP rescue kernel
-            s = np.sort(v)
-            rank = np.float32(q) * np.float32(n - 1)
-            lo, hi = int(np.floor(rank)), int(np.ceil(rank))
-            w = np.float32(rank - np.float32(lo))
-            a, b = s[lo], s[hi]
-            d = np.float32(b - a)
-            thr = np.float32(a + np.float32(w * d)) if w < 0.5 else np.float32(b - np.float32(d * np.float32(1 - w)))
-            assert np.float32(ref) == thr, (n, ratio, ref, thr)
-            # rescued set: everything >= sorted[hi], plus sorted[lo] only if thr == sorted[lo]
-            mask = v >= thr
-            assert mask.sum() >= n - hi
-            assert set(np.flatnonzero(mask)) >= set(np.flatnonzero(v >= b))
+    unfused_misses = 0
+    for trial in range(1500):
+        n = int(rng.choice([1, 2, 3, 16, 127, 128, 129, 512, 4096, int(rng.integers(5, 6000))]))
+        ratio = float(rng.choice([0.01, 0.05, 0.3, 0.5, 0.999, 0.0025]))
+        v = (np.abs(rng.standard_normal(n)) * rng.uniform(0.1, 10)).astype(np.float32)
+        if n > 8:
+            v[rng.integers(0, n, 3)] = v[0]  # ties
+        q = max(0.0, min(1.0, 1.0 - ratio))
+        ref = np.float32(torch.quantile(torch.from_numpy(v), q).item())
+        thr, a, b = quantile32(v, q)
+        assert ref == thr, (n, ratio, ref, thr)
+        # the unfused a + w (b - a) (a plausible restatement) misses in some of these cases
+        rank = np.float32(np.float32(q) * np.float32(n - 1))
+        w = np.float32(rank - np.float32(np.floor(rank)))
+        d = np.float32(b - a)
+        unf = np.float32(a + np.float32(w * d)) if w < 0.5 else np.float32(b - np.float32(d * np.float32(1 - w)))
+        unfused_misses += int(unf != ref)
+        # rescued set: everything >= sorted[hi], plus sorted[lo] only if thr == sorted[lo]
+        mask = v >= thr
+        hi = int(np.ceil(rank))
+        assert mask.sum() >= n - hi
+        assert set(np.flatnonzero(mask)) >= set(np.flatnonzero(v >= b))
+    assert unfused_misses > 0
+
+
+@pytest.mark.parametrize("percentile,gs", [(99.9, 128), (99.5, 16), (99.0, 16), (99.9, 32), (99.0, 128), (50.5, 8)])
+def test_dynamic_percentile_quantizers_closed_form(percentile, gs):
+    """quantize_symmetric_int8 / int4 below percentile 100 (src/quant/int8_basic.py:76-94,
+    int4_basic.py:80-99): per group, abs_max = torch.quantile(|x| in fp32); the closed form
+    takes the group's order statistics and fused_lerp32, then the INT8 fp16 / INT4 fp32
+    scale chain."""
+    g = torch.Generator().manual_seed(int(percentile * 10) + gs)
+    x = (torch.randn(2, 2, 9, 128, generator=g) * torch.rand(2, 2, 9, 1, generator=g) * 4).to(torch.float16)
+    x[0, 0, 0, :gs] = 0.0  # an all-zero group: the 1e-5 clamp
+    q8, s8 = OQ.quantize_symmetric_int8(x, percentile, gs)
+    q4, s4 = OQ.quantize_symmetric_int4(x, percentile, gs)
+    xs = x.numpy().reshape(-1, gs)
+    for i, row in enumerate(xs):
+        am, _, _ = quantile32(np.abs(row.astype(np.float32)), percentile / 100.0)
+        a16 = np.float16(max(am, np.float32(1e-5)))
+        sc8 = np.float16(np.float32(a16) / np.float32(127))
+        assert s8.reshape(-1)[i].item() == float(sc8)
+        assert np.array_equal(q8.numpy().reshape(-1, gs)[i], int8_closed_form(row, sc8))
+        sc4 = np.float32(max(am, np.float32(1e-5))) / np.float32(7)
+        assert s4.reshape(-1)[i].item() == float(sc4)
+        want4 = np.clip(np.rint(row.astype(np.float32) / sc4), -7, 7).astype(np.int8)
+        assert np.array_equal(q4.numpy().reshape(-1, gs)[i], want4)
+    # clipping: the largest |x| of a group can exceed 127 * scale
+    assert (q8.abs() == 127).any()
 
 
 def test_outlier_rescue_effect():
@@ -472,3 +532,19 @@ def test_k8v4_oracle_brute_force():
     ref = brute_attention(qs, kd, vd, ctx, 0.1)
     ok, err = fp16_close(out[0].double().numpy(), ref)
     assert ok, err
+
+
+def test_dequantize_symmetric_kats():
+    q = torch.tensor([[-127, 0, 5, 7, -3, 2, 1, -1]], dtype=torch.int8).view(1, 1, 1, 8)
+    sc = torch.tensor([0.5, 0.25, 2.0, 8.0], dtype=torch.float32).view(1, 1, 1, 4)  # groups of 2
+    out = OQ.dequantize_symmetric(q, sc).view(-1).tolist()
+    assert out == [-63.5, 0.0, 1.25, 1.75, -6.0, 4.0, 8.0, -8.0]
+    one = torch.tensor([3.0]).view(1, 1, 1, 1)
+    assert OQ.dequantize_symmetric(q, one).view(-1).tolist() == [3.0 * v for v in q.view(-1).tolist()]
+    # the cache's fp16 result is the exact product rounded once
+    g = torch.Generator().manual_seed(12)
+    codes = torch.randint(-127, 128, (2, 2, 9, 128), generator=g, dtype=torch.int8)
+    s16 = (torch.rand(2, 2, 9, 8, generator=g) * 0.05 + 1e-4).to(torch.float16)
+    got = OQ.cache_get_kv(codes, s16).numpy()
+    exact = codes.double().numpy().reshape(2, 2, 9, 8, 16) * s16.double().numpy()[..., None]
+    assert np.array_equal(got, exact.reshape(2, 2, 9, 128).astype(np.float16))
