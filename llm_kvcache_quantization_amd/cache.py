@@ -22,7 +22,11 @@ Where the layout differs from the reference:
 * Host synchronisation is optional.  With ``check_numerics=True`` (the default)
   ``append`` reads a device status word back, like the reference's
   NaN/Inf/clip checks, and raises/warns the same way.  With
-  ``check_numerics=False`` nothing synchronises.
+  ``check_numerics=False`` nothing synchronises.  :class:`KIVIStyleKVCache` reads it
+  at prefill only, and on the decode steps its frozen-K range check selects
+  (``KV_OOR_CHECK_INTERVAL``, off by default as in the reference).
+
+:class:`FP16KVCache` is the reference's unquantized engine (src/cache/fp16_cache.py).
 
 :class:`INT4AsymKVCache` (asymmetric INT4, static group-32 parameters, optional fp16
 K outlier channels) and :class:`K8V4KVCache` (INT8 K, asymmetric INT4 V) hold the
@@ -32,8 +36,9 @@ for them.
 from __future__ import annotations
 
 import ctypes
-import math
 import logging
+import math
+import os
 import warnings
 from typing import Dict, List, Optional, Tuple
 
@@ -183,9 +188,15 @@ class _EngineBase:
             self._status = torch.zeros(4, dtype=torch.int32, device=device)
         return self._status
 
-    def _check_status(self, layer_id: int, n_elem: int, kind: str, qrange: str) -> None:
+    def _read_status(self) -> List[int]:
+        """The append kernel's status words (NaN flags and clip counts of K and V), then
+        cleared for the next append."""
         st = self._status.cpu().tolist()
         self._status.zero_()
+        return st
+
+    def _check_status(self, layer_id: int, n_elem: int, kind: str, qrange: str) -> None:
+        st = self._read_status()
         if st[0] & 1:
             raise ValueError(f"{kind} append: K input contains NaN or Inf — refusing to quantize corrupt data")
         if st[2] & 1:
@@ -1080,6 +1091,8 @@ class KIVIStyleKVCache(_EngineBase):
         self._v_scale: List[Optional[Tensor]] = [None] * n
         self._v_zp: List[Optional[Tensor]] = [None] * n
         self._k_scale_initialized = [False] * n
+        self._oor_check_interval = int(os.environ.get("KV_OOR_CHECK_INTERVAL", "0"))
+        self._oor_step_counter = 0
 
     def _ensure(self, layer_id: int, B: int, H: int, target: int, device) -> None:
         cap = self._layer_capacity[layer_id]
@@ -1114,7 +1127,15 @@ class KIVIStyleKVCache(_EngineBase):
         if S == 0:
             return
         self._ensure(layer_id, B, H, old + S, k.device)
-        if not self._k_scale_initialized[layer_id]:
+        prefill = not self._k_scale_initialized[layer_id]
+        # the frozen-K range check of decode appends runs every KV_OOR_CHECK_INTERVAL steps
+        # (0, the default: never), counted on layer 0 (kivi_style_cache.py:143-144, 549-560)
+        oor_check = False
+        if not prefill and self._oor_check_interval > 0:
+            if layer_id == 0:
+                self._oor_step_counter += 1
+            oor_check = self._oor_step_counter % self._oor_check_interval == 0
+        if prefill:
             # prefill: per-channel range over the incoming tokens (asymmetric_quant.py:102-141)
             if self.check_numerics and not bool(torch.isfinite(k).all()):
                 raise ValueError("quantize_asymmetric: input contains NaN or Inf")
@@ -1131,7 +1152,9 @@ class KIVIStyleKVCache(_EngineBase):
         if tuple(ks.shape) != (B, H, D):
             raise ValueError(f"Inconsistent decode K scale/zp shape for layer {layer_id}: "
                              f"expected {(B, H, D)}, got {tuple(ks.shape)}")
-        status = self._status_buf(k.device) if self.check_numerics else None
+        # the status words (NaN flags, K range count) cost a host sync: read at prefill
+        # with check_numerics, and on the decode steps the range check selects
+        status = self._status_buf(k.device) if (self.check_numerics and prefill) or oor_check else None
         pk, pv = C.AppendParams(), C.AppendParams()
         ksx = k if k.stride(-1) == 1 else k.contiguous()
         vsx = v if v.stride(-1) == 1 else v.contiguous()
@@ -1148,7 +1171,16 @@ class KIVIStyleKVCache(_EngineBase):
         C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
                                          ctypes.c_void_p(C.stream_handle(k.device))))
         if status is not None:
-            self._check_status(layer_id, k.numel(), "KIVI", "[-8, 7]")
+            st = self._read_status()
+            if st[0] & 1 or st[2] & 1:
+                raise ValueError(f"KIVI append: {'K' if st[0] & 1 else 'V'} input contains NaN or Inf "
+                                 "— refusing to quantize corrupt data")
+            ratio = st[1] / max(k.numel(), 1)
+            if oor_check and ratio > _CLIP_WARN_THRESHOLD:
+                warnings.warn(
+                    f"ENG-041: KIVI decode K clipping at layer {layer_id}: {ratio:.1%} of values exceed "
+                    "prefill-computed scale range [-8, 7]. Decode token magnitudes may have drifted "
+                    "beyond prefill calibration. Attention accuracy may degrade.", RuntimeWarning)
         self._layer_seq_lens[layer_id] = old + S
         if layer_id == 0:
             self._seq_len = old + S
@@ -1232,17 +1264,17 @@ class KIVIStyleKVCache(_EngineBase):
                            sm_scale: Optional[float] = None,
                            inv_tau: Optional[Tensor] = None) -> Tensor:
         """Decode step of one layer: ``append`` of the new token (k, v [B, H, 1, 128]) then
-        the attention of q [B, Hq, 128] over the cache including it.  inv_tau (fp16 [Hq])
-        overrides the engine's own per-layer inv_tau."""
+        the attention of q [B, Hq, 128] over the cache including it.  inv_tau (fp16 [Hq]) is
+        applied as given, as in the symmetric engines; None applies none (``decode_attn``
+        applies the engine's own)."""
         if k.shape[2] != 1:
             raise ValueError(f"append_decode_attn appends one token per step, got S={k.shape[2]}")
         self.append(layer_id, k, v)
         n = self._layer_seq_lens[layer_id]
         if q.dtype != torch.float16 or q.stride(-1) != 1:
             q = q.to(torch.float16).contiguous()
-        tau = inv_tau if inv_tau is not None else self._layer_tau(layer_id, q)
         sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
-        return self._step_for(layer_id, q.shape[1]).attend(q, n, sm, tau)
+        return self._step_for(layer_id, q.shape[1]).attend(q, n, sm, inv_tau)
 
     def clear(self) -> None:
         self._layer_seq_lens = [0] * self.num_layers
@@ -1265,3 +1297,130 @@ class KIVIStyleKVCache(_EngineBase):
         for lst in (self._k_cache, self._v_cache, self._k_scale, self._k_zp, self._v_scale, self._v_zp):
             total += sum(t.numel() * t.element_size() for t in lst if t is not None)
         return total / (1024 * 1024)
+
+
+class FP16KVCache:
+    """The fp16 mode's cache (src/cache/fp16_cache.py:26-366): K / V kept as they come,
+    [B, H, capacity, D] per layer, capacity doubling with a copy, ``get_kv`` returning views
+    of the stored tokens.  Plain storage: nothing is quantized, so no kernel runs here."""
+
+    _min_capacity = 256
+
+    def __init__(self, num_layers: int, device: str = "cuda", dtype: torch.dtype = torch.float16,
+                 max_seq_len: Optional[int] = None):
+        if num_layers <= 0:
+            raise ValueError(f"num_layers must be > 0, got {num_layers}")
+        self.num_layers = num_layers
+        self.device = device
+        self.dtype = dtype
+        self.max_seq_len = int(max_seq_len) if max_seq_len is not None else None
+        if self.max_seq_len is not None and self.max_seq_len <= 0:
+            raise ValueError(f"max_seq_len must be > 0, got {self.max_seq_len}")
+        self._k_cache: List[Optional[Tensor]] = [None] * num_layers
+        self._v_cache: List[Optional[Tensor]] = [None] * num_layers
+        self._layer_seq_lens: List[int] = [0] * num_layers
+        self._layer_capacity: List[int] = [0] * num_layers
+        self._seq_len = 0
+
+    def _grow(self, layer_id: int, batch: int, heads: int, head_dim: int, target: int) -> None:
+        if self.max_seq_len is not None and target > self.max_seq_len:
+            raise ValueError(f"target_len {target} exceeds max_seq_len {self.max_seq_len} for layer {layer_id}")
+        kb, cap = self._k_cache[layer_id], self._layer_capacity[layer_id]
+        if kb is not None:
+            if kb.shape[0] != batch or kb.shape[1] != heads or kb.shape[3] != head_dim:
+                raise ValueError(f"Inconsistent KV shape for layer {layer_id}: existing={tuple(kb.shape)}, "
+                                 f"incoming=({batch}, {heads}, *, {head_dim})")
+            if target <= cap:
+                return
+        new_cap = max(target, self._min_capacity) if kb is None else max(target, cap * 2)
+        if self.max_seq_len is not None:
+            new_cap = min(new_cap, self.max_seq_len)
+            if new_cap < target:
+                raise ValueError(f"target_len {target} exceeds capped capacity {new_cap} for layer {layer_id}")
+        nk = torch.empty((batch, heads, new_cap, head_dim), device=self.device, dtype=self.dtype)
+        nv = torch.empty_like(nk)
+        old = self._layer_seq_lens[layer_id]
+        if kb is not None and old:
+            nk[:, :, :old] = kb[:, :, :old]
+            nv[:, :, :old] = self._v_cache[layer_id][:, :, :old]
+        self._k_cache[layer_id], self._v_cache[layer_id] = nk, nv
+        self._layer_capacity[layer_id] = new_cap
+
+    def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
+        if layer_id < 0 or layer_id >= self.num_layers:
+            raise ValueError(f"layer_id {layer_id} out of range [0, {self.num_layers})")
+        if k.shape != v.shape:
+            raise ValueError(f"K and V shapes must match. Got K: {k.shape}, V: {v.shape}")
+        if k.dim() != 4:
+            raise ValueError(f"K/V must be 4D [batch, heads, seq, dim]. Got {k.dim()}D")
+        k = k.to(device=self.device, dtype=self.dtype)
+        v = v.to(device=self.device, dtype=self.dtype)
+        B, H, S, D = k.shape
+        old = self._layer_seq_lens[layer_id]
+        self._grow(layer_id, B, H, D, old + S)
+        self._k_cache[layer_id][:, :, old:old + S] = k
+        self._v_cache[layer_id][:, :, old:old + S] = v
+        self._layer_seq_lens[layer_id] = old + S
+        if layer_id == 0:
+            self._seq_len = old + S
+
+    def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
+        if layer_id < 0 or layer_id >= self.num_layers:
+            raise ValueError(f"layer_id {layer_id} out of range [0, {self.num_layers})")
+        if self._k_cache[layer_id] is None:
+            raise ValueError(f"Cache for layer {layer_id} is empty. Call append() first.")
+        n = self._layer_seq_lens[layer_id]
+        if n == 0:
+            logger.warning("get_kv(layer_id=%d) returning zero-length tensors. The cache was cleared "
+                           "but buffers are still allocated.", layer_id)
+        return self._k_cache[layer_id][:, :, :n], self._v_cache[layer_id][:, :, :n]
+
+    def get_seq_len(self) -> int:
+        return self._seq_len
+
+    def clear(self) -> None:
+        self._layer_seq_lens = [0] * self.num_layers
+        self._seq_len = 0
+
+    def release(self) -> None:
+        n = self.num_layers
+        self._k_cache, self._v_cache = [None] * n, [None] * n
+        self._layer_seq_lens, self._layer_capacity = [0] * n, [0] * n
+        self._seq_len = 0
+
+    def get_memory_mb(self) -> float:
+        total = sum(t.numel() * t.element_size() for t in self._k_cache + self._v_cache if t is not None)
+        return total / (1024 * 1024)
+
+    def to_tuple(self) -> Tuple[Tuple[Tensor, Tensor], ...]:
+        out = []
+        for i in range(self.num_layers):
+            if self._k_cache[i] is None:
+                raise ValueError(f"Layer {i} cache is empty")
+            out.append(self.get_kv(i))
+        return tuple(out)
+
+    @classmethod
+    def from_tuple(cls, past_key_values, device: str = "cuda") -> "FP16KVCache":
+        cache = cls(num_layers=len(past_key_values), device=device)
+        ref = None
+        for i, (k, v) in enumerate(past_key_values):
+            if k.ndim != 4:
+                raise ValueError(f"from_tuple(): layer {i} k must be 4D, got ndim={k.ndim}")
+            if v.ndim != 4:
+                raise ValueError(f"from_tuple(): layer {i} v must be 4D, got ndim={v.ndim}")
+            if tuple(k.shape) != tuple(v.shape):
+                raise ValueError(f"from_tuple(): layer {i} k/v shape mismatch: k={tuple(k.shape)} "
+                                 f"vs v={tuple(v.shape)}")
+            cur = (k.shape[0], k.shape[1], k.shape[3])
+            if ref is None:
+                ref = cur
+            elif cur != ref:
+                raise ValueError(f"from_tuple(): cross-layer shape inconsistency at layer {i}: "
+                                 f"(batch, heads, head_dim)={cur} vs layer 0={ref}")
+            cache.append(i, k, v)
+        return cache
+
+    def __repr__(self) -> str:
+        return (f"FP16KVCache(num_layers={self.num_layers}, seq_len={self._seq_len}, "
+                f"memory={self.get_memory_mb():.2f}MB)")

@@ -351,9 +351,10 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
         a.zo[off] = z0;
       }
     }
-    const float r0 = rintf(__fdiv_rn(x0 - z0, s0));
-    const float r1 = rintf(__fdiv_rn(x1 - z1, s1));
-    if (a.st != nullptr) clipped = (r0 < -8.f || r0 > 7.f) + (r1 < -8.f || r1 > 7.f);
+    const float u0 = __fdiv_rn(x0 - z0, s0), u1 = __fdiv_rn(x1 - z1, s1);
+    // frozen-K out-of-range count, of the unrounded quotient (kivi_style_cache.py:549-560)
+    if (a.st != nullptr) clipped = (u0 < -8.f || u0 > 7.f) + (u1 < -8.f || u1 > 7.f);
+    const float r0 = rintf(u0), r1 = rintf(u1);
     const int q0 = (int)fminf(fmaxf(r0, -8.f), 7.f), q1 = (int)fminf(fmaxf(r1, -8.f), 7.f);
     crow[lane] = (uint8_t)(((q0 + 8) << 4) | (q1 + 8));
   } else {  // KVQ_FMT_INT4_ASYM, static parameters

@@ -12,6 +12,7 @@
 """
 import math
 import os
+import warnings
 
 import pytest
 import torch
@@ -336,3 +337,30 @@ def test_cached_decode_steps_across_growth(kind):
             if i in (0, 5, 6, 7, steps - 1):
                 ref = _reference_out(K, kind, cache, layer, q, tau, n)
                 assert_close(out, ref, f"{kind} layer {layer} S{n}")
+
+
+def test_kivi_decode_range_check(monkeypatch):
+    """KV_OOR_CHECK_INTERVAL selects the decode steps whose K is checked against the
+    prefill's frozen per-channel range (src/cache/kivi_style_cache.py:549-560); the count
+    is of the unrounded quotient (x - z) / s, so a token at 7.3 steps above the zero point
+    (stored as code 7) counts.  With the default interval (0) no check runs."""
+    K = _k()
+    B, H = 1, 2
+    base = torch.tensor([-1.0, 1.0]).repeat(8)[:, None].expand(16, 128)      # min -1, max 1
+    k0 = base.expand(B, H, 16, 128).to(torch.float16).contiguous()
+    v0 = torch.randn(B, H, 16, 128, generator=gen(77)).to(torch.float16)
+    s = 2.0 / 15.0
+    x = -1.0 + 15.3 * s                                                      # (x - z) / s = 7.3
+    k1 = torch.full((B, H, 1, 128), x, dtype=torch.float16)
+    v1 = torch.randn(B, H, 1, 128, generator=gen(78)).to(torch.float16)
+    for interval, expect in (("0", False), ("1", True)):
+        monkeypatch.setenv("KV_OOR_CHECK_INTERVAL", interval)
+        cache = K.KIVIStyleKVCache(num_layers=1, device=DEV, quant_bits=4)
+        cache.append(0, k0.to(DEV), v0.to(DEV))
+        with warnings.catch_warnings(record=True) as rec:
+            warnings.simplefilter("always")
+            cache.append(0, k1.to(DEV), v1.to(DEV))
+        hits = [r for r in rec if "ENG-041" in str(r.message)]
+        assert bool(hits) == expect, (interval, [str(r.message) for r in rec])
+        kp = cache.get_int4_asym_tensors(0)[0][0, 0, 16].view(torch.uint8).cpu()
+        assert torch.all(kp == 0xFF)                                          # codes 7, 7 stored

@@ -1,0 +1,204 @@
+"""GPU tests of the attention hook and the kv_mode switch on a randomly initialised,
+Qwen2.5-1.5B-shaped attention layer (hidden 1536, 12 query heads, 2 KV heads, head_dim 128).
+
+* Patched vs unpatched: a decode step through the patched forward (one HIP append +
+  split-K attention per layer) against the unpatched transformers forward over a second,
+  identical engine, which reaches the engine through ``INT8CacheWrapperContainer.update``
+  (quantize the new token, then attend over the dequantized cache with SDPA).  Both routes
+  leave bit-identical caches; the outputs agree within the fp16-ulp-aware 2e-3 bound and
+  cosine 0.9999, and both agree with a float64 softmax attention over the dequantized
+  cache.  o_proj is set to the identity so the layer output is the attention output.
+* The engines' inv_tau (the shipped INT8 table's) against float64 attention of fp16(q * tau).
+* generate_from_ids on a 2-layer random Qwen2 model in every built kv_mode; the fused INT8
+  decode through the HIP kernel and through the reference's torch decode path produce the
+  same tokens.
+"""
+import os
+import types
+
+import pytest
+import torch
+
+from test_gpu_engines import ATOL, COS_MIN, GOLDEN, assert_close_ulp
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _pkg():
+    import llm_kvcache_quantization_amd as K
+    from llm_kvcache_quantization_amd import _capi
+
+    _capi.lib()
+    return K
+
+
+def _layer(seed):
+    from transformers import Qwen2Config
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention, Qwen2RotaryEmbedding
+
+    cfg = Qwen2Config(hidden_size=1536, num_attention_heads=12, num_key_value_heads=2, intermediate_size=256,
+                      num_hidden_layers=1, max_position_embeddings=8192)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(seed)
+    attn = Qwen2Attention(cfg, 0)
+    with torch.no_grad():
+        attn.o_proj.weight.copy_(torch.eye(1536))
+        attn.k_proj.weight.mul_(3.0)
+    attn = attn.half().to(DEV).eval()
+    model = types.SimpleNamespace(model=types.SimpleNamespace(layers=[types.SimpleNamespace(self_attn=attn)]),
+                                  config=cfg)
+    return attn, Qwen2RotaryEmbedding(cfg).to(DEV), model
+
+
+def _engine(kind, tau=False):
+    K = _pkg()
+    from llm_kvcache_quantization_amd import modes
+
+    if kind == "int8_dynamic":
+        return K.INT8KVCache(num_layers=1, device=DEV)
+    if kind == "int4_dynamic":
+        return K.INT4KVCache(num_layers=1, device=DEV)
+    if kind == "kivi4":
+        return K.KIVIStyleKVCache(num_layers=1, device=DEV, quant_bits=4)
+    path = os.path.join(GOLDEN, "calib_qwen25_1p5b_int8.json" if kind == "int8_table"
+                        else "calib_qwen25_1p5b_int4.json")
+    mode = "int8_ours" if kind == "int8_table" else "int4_ours"
+    with pytest.warns(UserWarning, match="version=1"):
+        cal = modes.load_calibration(mode, path, device=DEV)
+    cal.static_k_scale, cal.static_v_scale = cal.static_k_scale[:1], cal.static_v_scale[:1]
+    cal.inv_tau = cal.inv_tau[:1] if tau else None
+    return modes.create_kv_cache(mode, 1, device=DEV, calib=cal, use_attn_temperature=tau)
+
+
+def _float64_attention(q, kd, vd, scaling):
+    """q fp16 [B, Hq, D]; kd / vd the dequantized cache [B, Hkv, n, D] -> fp64 [B, Hq, D]."""
+    rep = q.shape[1] // kd.shape[1]
+    k = kd.double().repeat_interleave(rep, 1)
+    v = vd.double().repeat_interleave(rep, 1)
+    s = torch.einsum("bhd,bhsd->bhs", q.double(), k) * scaling
+    return torch.einsum("bhs,bhsd->bhd", torch.softmax(s, -1), v)
+
+
+def _q_of(attn, hidden, cos, sin):
+    from llm_kvcache_quantization_amd import patch as P
+
+    B = hidden.shape[0]
+    q = attn.q_proj(hidden).view(B, 1, 12, 128).transpose(1, 2)
+    q, _ = P._apply_rope(q, q, cos, sin)
+    return q[:, :, 0]
+
+
+@pytest.mark.parametrize("kind", ["int8_dynamic", "int8_table", "int4_dynamic", "int4_table", "kivi4"])
+def test_patched_decode_matches_unpatched_sdpa(kind):
+    from llm_kvcache_quantization_amd import patch as P
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention
+
+    print(f"[hook] {kind}", flush=True)
+    attn, rot, model = _layer(11)
+    B, S = 2, 300
+    g = torch.Generator().manual_seed(5)
+    k0 = (torch.randn(B, 2, S, 128, generator=g) * 2).half().to(DEV)
+    v0 = torch.randn(B, 2, S, 128, generator=g).half().to(DEV)
+    fused_eng, plain_eng = _engine(kind), _engine(kind)
+    for e in (fused_eng, plain_eng):
+        e.append(0, k0, v0)
+    P.apply_int8_fused_patch(model)
+    try:
+        for step in range(3):
+            hidden = torch.randn(B, 1, 1536, generator=g).half().to(DEV)
+            pos = torch.full((B, 1), S + step, device=DEV)
+            cos, sin = rot(hidden, pos)
+            with torch.no_grad():
+                out_f, _ = attn(hidden, position_embeddings=(cos, sin), attention_mask=None,
+                                past_key_values=P.INT8CacheWrapperContainer(fused_eng, 1))
+                out_s, _ = Qwen2Attention._original_forward(
+                    attn, hidden, position_embeddings=(cos, sin), attention_mask=None,
+                    past_key_values=P.INT8CacheWrapperContainer(plain_eng, 1))
+                q = _q_of(attn, hidden, cos, sin)
+            kf, vf = fused_eng.get_kv(0)
+            ks, vs = plain_eng.get_kv(0)
+            assert kf.shape[2] == S + step + 1 and torch.equal(kf, ks) and torch.equal(vf, vs), kind
+            ref = _float64_attention(q, kf, vf, attn.scaling).reshape(B, 1, 1536)
+            assert_close_ulp(out_f, ref, f"{kind} step{step} fused vs fp64")
+            assert_close_ulp(out_s, ref, f"{kind} step{step} sdpa vs fp64")
+            assert_close_ulp(out_f, out_s.float(), f"{kind} step{step} fused vs sdpa")
+        st = fused_eng.get_decode_stats()
+        assert st.get("fused_decode_calls", 3) >= 3
+    finally:
+        P.remove_int8_fused_patch(model)
+
+
+def test_patched_decode_applies_shipped_inv_tau():
+    from llm_kvcache_quantization_amd import patch as P
+
+    attn, rot, model = _layer(12)
+    B, S = 2, 200
+    g = torch.Generator().manual_seed(6)
+    eng = _engine("int8_table", tau=True)
+    eng.append(0, (torch.randn(B, 2, S, 128, generator=g) * 2).half().to(DEV),
+               torch.randn(B, 2, S, 128, generator=g).half().to(DEV))
+    tau = eng.inv_tau[0]
+    assert not torch.all(tau == 1)
+    P.apply_int8_fused_patch(model)
+    try:
+        hidden = torch.randn(B, 1, 1536, generator=g).half().to(DEV)
+        cos, sin = rot(hidden, torch.full((B, 1), S, device=DEV))
+        with torch.no_grad():
+            out, _ = attn(hidden, position_embeddings=(cos, sin), attention_mask=None,
+                          past_key_values=P.INT8CacheWrapperContainer(eng, 1))
+            q = (_q_of(attn, hidden, cos, sin).float() * tau.float().view(1, -1, 1)).half()
+        kd, vd = eng.get_kv(0)
+        ref = _float64_attention(q, kd, vd, attn.scaling).reshape(B, 1, 1536)
+        assert_close_ulp(out, ref, "int8_table inv_tau")
+    finally:
+        P.remove_int8_fused_patch(model)
+
+
+def _tiny_lm(seed=3):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    torch.manual_seed(seed)
+    cfg = Qwen2Config(vocab_size=211, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=1024)
+    cfg._attn_implementation = "sdpa"
+    m = Qwen2ForCausalLM(cfg)
+    with torch.no_grad():
+        m.lm_head.weight.mul_(30.0)             # decisive argmax: greedy tokens are stable
+    return m.half().to(DEV).eval()
+
+
+@pytest.mark.parametrize("kv_mode,impl,bits", [
+    ("fp16", "triton_fused", None), ("int8_baseline", "triton_fused", None),
+    ("int8_fused", "triton_fused", None), ("int8_fused", "torch_ref", None),
+    ("int4_baseline", "triton_fused", None), ("kivi_style", "triton_fused", 4),
+    ("kivi_style", "torch_ref", 4)])
+def test_generate_from_ids_modes(kv_mode, impl, bits):
+    _pkg()
+    from llm_kvcache_quantization_amd import modes
+
+    print(f"[generate] {kv_mode} {impl}", flush=True)
+    m = _tiny_lm()
+    ids = torch.randint(0, 211, (2, 40), generator=torch.Generator().manual_seed(9))
+    kw = dict(quant_bits=bits, use_attn_temperature=False, use_static_scales=False) if kv_mode == "kivi_style" \
+        else {}
+    out = modes.generate_from_ids(m, None, ids, max_new_tokens=12, kv_mode=kv_mode, decode_attn_impl=impl, **kw)
+    assert out.generated_ids.shape == (2, 12) and len(out.decode_times_ms) == 11
+    assert out.ttft_ms > 0 and out.tpot_ms > 0
+    assert not hasattr(type(m.model.layers[0].self_attn), "_original_forward")     # patch removed
+    if kv_mode == "int8_fused" or (kv_mode == "kivi_style" and impl != "torch_ref"):
+        assert out.decode_stats["fused_decode_calls"] == 2 * 11, out.decode_stats
+
+
+def test_generate_fused_int8_hip_and_torch_ref_agree():
+    _pkg()
+    from llm_kvcache_quantization_amd import modes
+
+    m = _tiny_lm()
+    ids = torch.randint(0, 211, (2, 64), generator=torch.Generator().manual_seed(10))
+    a = modes.generate_from_ids(m, None, ids, max_new_tokens=16, kv_mode="int8_fused", decode_attn_impl="triton_fused")
+    b = modes.generate_from_ids(m, None, ids, max_new_tokens=16, kv_mode="int8_fused", decode_attn_impl="torch_ref")
+    c = modes.generate_from_ids(m, None, ids, max_new_tokens=16, kv_mode="fp16")
+    print("[generate] hip", a.generated_ids.tolist(), "torch_ref", b.generated_ids.tolist(),
+          "fp16", c.generated_ids.tolist(), flush=True)
+    assert torch.equal(a.generated_ids, b.generated_ids)
