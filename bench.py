@@ -22,6 +22,10 @@ attention).  The line also carries:
   the attention kernel) / its measured time per layer;
 - ``attention_us_per_layer_step`` / ``append_us_per_layer_step``: each half timed alone
   (its own HIP graph), as a breakdown;
+- ``stream_ceiling``: the library's streaming-read probe (kvq_stream_read) over the same
+  bytes per launch, the read rate this GPU sustains for a launch of that size;
+- ``engine_api``: the same step through the cache engine a caller uses
+  (``cache.append_decode_attn`` per layer, Python included);
 - ``cpu_baseline``: the CPU oracle (the reference's torch path restated) timed on a
   bounded sample on this host's cores.
 
@@ -53,6 +57,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-engine", action="store_true", help="skip the engine-API leg")
     ap.add_argument("--launch", choices=["auto", "graph", "stream"], default="auto",
                     help="how the timed steps are launched: a HIP graph of one step replayed, "
                          "direct launches on the stream, or both timed and the faster reported")
@@ -239,25 +244,126 @@ def time_region(fn, stream, steps, warmup, use_graph):
     return e0.elapsed_time(e1) / steps, graph
 
 
-def stream_ceiling(device, nbytes=2 << 30, reps=10):
-    """Measured HBM ceilings on this GPU: torch's device copy (read + write bytes) and a
-    full read-reduction (read bytes), each over a buffer far larger than the 256 MB MALL."""
-    a = torch.empty(nbytes // 4, dtype=torch.float32, device=device).uniform_()
-    b = torch.empty_like(a)
-    out = {}
-    for name, fn, moved in (("copy", lambda: b.copy_(a), 2 * nbytes),
-                            ("read", lambda: a.sum(), nbytes)):
-        fn()
+def stream_ceiling(device, nbytes, reps=28):
+    """HBM read ceilings of this GPU from kvq_stream_read, the library's streaming-read probe
+    (non-temporal 16-byte loads, as the decode kernels read cache codes, XOR-folded):
+    - ``read_GBps_same_bytes``: launches of `nbytes` each (the bytes of one decode launch),
+      each reading the next window of a 4 GiB buffer, so that, as in the decode step, no
+      launch is served from the 256 MB MALL;
+    - ``read_GBps_4GiB``: one launch over the whole buffer.
+    Each is the best over 1 to 64 work-groups (512 threads, one contiguous slab each) per CU."""
+    from llm_kvcache_quantization_amd import _capi as C
+
+    L = C.lib()
+    big = 4 << 30
+    buf = torch.randint(-2 ** 31, 2 ** 31 - 1, (big // 4,), dtype=torch.int32, device=device)
+    nwin = (int(nbytes) // 256) * 256
+    nwins = big // nwin
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    s = torch.cuda.current_stream().cuda_stream
+    out = {"kernel": "kvq_stream_read", "bytes_per_launch": nwin}
+    best_same, best_big = (0.0, 0), (0.0, 0)
+    for per_cu in (1, 4, 16, 32, 64):
+        wgs = per_cu * cus
+        sink = torch.zeros(wgs, dtype=torch.int32, device=device)
+
+        def launch(off, n):
+            C.check(L.kvq_stream_read(ctypes.c_void_p(buf.data_ptr() + off), n,
+                                      ctypes.c_void_p(sink.data_ptr()), wgs, ctypes.c_void_p(s)))
+
+        for w in range(nwins):
+            launch(w * nwin, nwin)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(reps):
-            fn()
+        for r in range(reps):
+            launch((r % nwins) * nwin, nwin)
         e1.record()
         torch.cuda.synchronize()
-        out[name + "_GBps"] = round(moved * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
-    del a, b
+        gbps = nwin * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        best_same = max(best_same, (gbps, wgs))
+        e0.record()
+        for _ in range(3):
+            launch(0, big)
+        e1.record()
+        torch.cuda.synchronize()
+        gbps = big * 3 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        best_big = max(best_big, (gbps, wgs))
+        del sink
+    del buf
+    out["read_GBps_same_bytes"] = round(best_same[0], 1)
+    out["work_groups_same_bytes"] = best_same[1]
+    out["us_per_launch_same_bytes"] = round(nwin / (best_same[0] * 1e3), 3)
+    out["read_GBps_4GiB"] = round(best_big[0], 1)
+    out["work_groups_4GiB"] = best_big[1]
     return out
+
+
+def engine_leg(cfg, device, steps, warmup):
+    """The engine API a caller uses: ``cache.append_decode_attn(layer, q, k, v, sm_scale,
+    inv_tau)`` for every layer of the configuration (a single-layer configuration rotates
+    MIN_ROTATE layers, as the main timing does), on the cache engine of its format
+    (INT4AsymKVCache, or INT8KVCache with the static group-32 tables), prefilled with
+    seeded data through ``append`` to a context a few tokens short of the configuration's,
+    so that the timed steps end at it.  Timed with hipEvents as the main loop, with
+    check_numerics off (no host read-back) and on (one status read-back per call, as the
+    reference's NaN / clip checks synchronise).  None for ragged batches: an engine holds
+    one length for all rows."""
+    if cfg.ragged_min is not None or cfg.k_format != cfg.v_format:
+        return None
+    import llm_kvcache_quantization_amd as K
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    nl = max(cfg.layers, MIN_ROTATE)
+    calls = 2 + 2 * (warmup + steps)
+    s0 = ((cfg.context - calls) // 32) * 32
+    tabs = [SY.calibrate(cfg, l % cfg.layers) for l in range(nl)]
+    stack = lambda name: torch.stack([getattr(t, name) for t in tabs]).to(device)
+    tau = SY.inv_tau(cfg).to(device)
+    if cfg.k_format == "int8":
+        cache = K.INT8KVCache(nl, device=device, group_size=32, max_seq_len=cfg.context,
+                              static_k_scale=stack("k_scale"), static_v_scale=stack("v_scale"),
+                              check_numerics=False)
+    else:
+        cache = K.INT4AsymKVCache(nl, stack("k_scale"), stack("k_zp"), stack("v_scale"), stack("v_zp"),
+                                  device=device, max_seq_len=cfg.context,
+                                  k_outlier_idx=stack("k_outlier_idx") if cfg.outlier_channels else None)
+    gen = torch.Generator(device=device).manual_seed(SY.seed_for(cfg.index, 0) + 5)
+    for l in range(nl):
+        k, v = SY.draw_kv(cfg, l % cfg.layers, cfg.batch, s0, gen, device=device)
+        cache.append(l, k, v)
+        del k, v
+    q = SY.draw_q(cfg, cfg.batch, gen, device=device)
+    k1, v1 = SY.draw_kv(cfg, 0, cfg.batch, 1, gen, device=device)
+    sm = 1.0 / math.sqrt(128)
+    taus = [tau[l % cfg.layers].contiguous() for l in range(nl)]
+
+    def step():
+        for l in range(nl):
+            cache.append_decode_attn(l, q, k1, v1, sm, inv_tau=taus[l])
+
+    step()          # the first call grows each layer's buffer to the full context
+    torch.cuda.synchronize()
+    res = {"engine": type(cache).__name__, "layers": nl}
+    for checked in (False, True):
+        cache.check_numerics = checked
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        host = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        key = "checked" if checked else "unchecked"
+        res[f"us_per_layer_step_{key}"] = round(e0.elapsed_time(e1) * 1e3 / (steps * nl), 3)
+        res[f"host_us_per_call_{key}"] = round(host * 1e6 / (steps * nl), 3)
+    res["context_timed"] = [s0 + 2 + warmup, cache.get_seq_len()]
+    cache.release()
+    return res
 
 
 def copy_probe(device, nbytes=1 << 30, reps=3):
@@ -480,8 +586,13 @@ def main():
           f"attention alone {us_attn} us, append alone {us_app} us); {achieved:.0f} GB/s",
           file=sys.stderr, flush=True)
 
-    ceiling = stream_ceiling(device)
+    ceiling = stream_ceiling(device, roof_bytes)
     print(f"[bench] stream ceiling {ceiling}", file=sys.stderr, flush=True)
+    eng = None
+    if not args.no_engine:
+        print("[bench] timing the engine API", file=sys.stderr, flush=True)
+        eng = engine_leg(cfg, device, args.steps, args.warmup)
+        print(f"[bench] engine API {eng}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
@@ -524,6 +635,7 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "frac_of_stream_read": round(achieved / ceiling["read_GBps_same_bytes"], 4),
             "traffic": measured_traffic(cfg.index),
             "bytes_per_launch": roof_bytes,
             "kernel": (attention_kernels(cfg, layers[0]) +
@@ -531,6 +643,7 @@ def main():
                         if fused else " (one kvq_decode_attn call per layer)")),
         },
         "stream_ceiling": ceiling,
+        "engine_api": eng,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -249,6 +249,14 @@ int64_t kvq_append_scratch_bytes(const kvq_append_params* p);
 int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
                            const kvq_append_params* v_new, kvq_stream_t stream);
 
+/* Measurement aid, with no counterpart in the reference: reads `bytes` (a multiple of 16)
+ * of device memory at buf (16-byte aligned) once, with the non-temporal 16-byte loads the
+ * decode kernels use for cache codes, over `work_groups` work-groups of 512 threads, and
+ * writes nothing to sink (work_groups words) in practice.  Timing it over the bytes of a
+ * decode launch gives the read ceiling that launch is measured against. */
+int kvq_stream_read(const void* buf, int64_t bytes, uint32_t* sink, int32_t work_groups,
+                    kvq_stream_t stream);
+
 /* message for the last non-OK return on this thread ("" if none) */
 const char* kvq_last_error(void);
 /* ABI version (increments on incompatible changes to the structs above); this is 4 */

@@ -125,6 +125,7 @@ EXPORTED_SYMBOLS = (
     "kvq_decode_workspace_bytes",
     "kvq_quant_append",
     "kvq_append_scratch_bytes",
+    "kvq_stream_read",
     "kvq_last_error",
     "kvq_abi_version",
 )
@@ -170,6 +171,8 @@ def lib() -> ctypes.CDLL:
         L.kvq_append_decode_attn.argtypes = [ctypes.POINTER(DecodeParams), ctypes.POINTER(AppendParams),
                                              ctypes.POINTER(AppendParams), c_vp]
         L.kvq_append_decode_attn.restype = c_i32
+        L.kvq_stream_read.argtypes = [c_vp, c_i64, c_vp, c_i32, c_vp]
+        L.kvq_stream_read.restype = c_i32
         L.kvq_last_error.argtypes = []
         L.kvq_last_error.restype = ctypes.c_char_p
         L.kvq_abi_version.argtypes = []

@@ -21,7 +21,7 @@ def test_header_declares_entry_points():
         "kvq_abi_version", "kvq_append_decode_attn", "kvq_decode_attn", "kvq_decode_attn_noalloc",
         "kvq_decode_chunk_tokens",
         "kvq_append_scratch_bytes", "kvq_decode_workspace_bytes", "kvq_last_error",
-        "kvq_quant_append"])
+        "kvq_quant_append", "kvq_stream_read"])
 
 
 def test_library_loads_and_exports_all_symbols():

@@ -532,6 +532,82 @@ def test_cfg3_full_size_rows():
                                       inv_tau=tau.cpu(), k_outlier_idx=t.k_outlier_idx,
                                       k_outlier_val=ov[sl].cpu())
         assert_close(out[sl], ref, f"cfg3 full row {b}")
+        vq_ref = OQ.pack_int4(OQ.quantize_asymmetric_static(v[sl].cpu(), t.v_scale, t.v_zp))
+        assert torch.equal(K.untile_v(vc[sl], cfg.context).cpu(), vq_ref.view(torch.uint8))
+
+
+def test_cfg2_full_size_rows():
+    """Config 2 at full size (B=16, Hq=12, Hkv=2, 32768 tokens, 4 fp16 K channels) through
+    the fused decode step: K, V and outlier-channel codes of rows 0 and 15 bit-exact, their
+    outputs against the oracle."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[2]
+    t = SY.calibrate(cfg, 0)
+    g = torch.Generator(device=DEV).manual_seed(SY.seed_for(2, 0))
+    S = cfg.context
+    k, v = SY.draw_kv(cfg, 0, cfg.batch, S, g, device=DEV)
+    q = SY.draw_q(cfg, cfg.batch, g, device=DEV)
+    tau = SY.inv_tau(cfg)[0].to(DEV)
+    cache = K.INT4AsymKVCache(1, t.k_scale[None], t.k_zp[None], t.v_scale[None], t.v_zp[None],
+                              device=DEV, k_outlier_idx=t.k_outlier_idx[None], inv_tau=tau[None])
+    cache.append(0, k[:, :, :S - 1].contiguous(), v[:, :, :S - 1].contiguous())
+    out = cache.append_decode_attn(0, q, k[:, :, S - 1:], v[:, :, S - 1:], 1 / math.sqrt(128),
+                                   inv_tau=tau)
+    kc, vc, ks, kz, vs, vz, oi, ov = cache.get_int4_g32_tensors(0)
+    cl = torch.full((1,), S, dtype=torch.int32)
+    for b in (0, cfg.batch - 1):
+        sl = slice(b, b + 1)
+        kq_ref = OQ.pack_int4(OQ.quantize_asymmetric_static(k[sl].cpu(), t.k_scale, t.k_zp))
+        vq_ref = OQ.pack_int4(OQ.quantize_asymmetric_static(v[sl].cpu(), t.v_scale, t.v_zp))
+        vr = K.untile_v(vc[sl], S).cpu()
+        assert torch.equal(kc[sl].cpu(), kq_ref.view(torch.uint8)), b
+        assert torch.equal(vr, vq_ref.view(torch.uint8)), b
+        idx = t.k_outlier_idx.long()
+        want_o = torch.stack([k[b, h, :, idx[h]].cpu() for h in range(cfg.kv_heads)])[None]
+        assert torch.equal(ov[sl].cpu(), want_o), b
+        ref = OA.decode_attn_asym_ref(q[sl].cpu(), kc[sl].cpu(), vr, t.k_scale, t.k_zp, t.v_scale, t.v_zp,
+                                      cl, 1 / math.sqrt(128), inv_tau=tau.cpu(),
+                                      k_outlier_idx=t.k_outlier_idx, k_outlier_val=ov[sl].cpu())
+        assert_close(out[sl], ref, f"cfg2 full row {b}")
+
+
+def test_cfg4_full_size_rows():
+    """Config 4 at full size (B=8, Hq=40, Hkv=8, K INT8 / V INT4 g32) with ragged contexts:
+    the seeded draw with rows 0 and 1 set to the distribution's bounds, 65536 and 4096
+    tokens (the 65536-token row merges 16 chunks of 4096).  Rows 0, 1 and the longest
+    seeded row: codes bit-exact, outputs against the oracle."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[4]
+    t = SY.calibrate(cfg, 0)
+    ctx = SY.context_lengths(cfg)
+    ctx[0], ctx[1] = cfg.context, cfg.ragged_min
+    S = cfg.context
+    g = torch.Generator(device=DEV).manual_seed(SY.seed_for(4, 0))
+    k, v = SY.draw_kv(cfg, 0, cfg.batch, S, g, device=DEV)
+    q = SY.draw_q(cfg, cfg.batch, g, device=DEV)
+    tau = SY.inv_tau(cfg)[0].to(DEV)
+    cache = K.K8V4KVCache(1, t.k_scale[None], t.v_scale[None], t.v_zp[None], device=DEV)
+    cache.append(0, k, v)
+    kc, ks, vt, vs, vz = cache.get_k8v4_tensors(0)
+    out = K.decode_attn_k8v4(q, kc, ks, vt, vs, vz, ctx.to(DEV), 1 / math.sqrt(128), inv_tau=tau)
+    longest = 2 + int(torch.argmax(ctx[2:]))
+    for b in (0, 1, longest):
+        n = int(ctx[b])
+        sl = slice(b, b + 1)
+        k8_ref, ks_ref = OQ.quantize_symmetric_int8_with_scale(k[sl, :, :n].cpu(), t.k_scale, 32)
+        vq_ref = OQ.pack_int4(OQ.quantize_asymmetric_static(v[sl, :, :n].cpu(), t.v_scale, t.v_zp))
+        assert torch.equal(kc[sl, :, :n].cpu().view(torch.int8), k8_ref), b
+        assert torch.equal(ks[sl, :, :n].cpu(), ks_ref), b
+        vr = K.untile_v(vt[sl], S)[:, :, :n].cpu()
+        assert torch.equal(vr, vq_ref.view(torch.uint8)), b
+        ref = OA.decode_attn_k8v4_ref(q[sl].cpu(), k8_ref, ks_ref, vr, t.v_scale, t.v_zp,
+                                      torch.tensor([n], dtype=torch.int32), 1 / math.sqrt(128),
+                                      inv_tau=tau.cpu())
+        assert_close(out[sl], ref, f"cfg4 full row {b} ctx {n}")
 
 
 @pytest.mark.parametrize("layout", ["rows", "tile32"])
