@@ -76,10 +76,13 @@ __device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t voff, uint32_t sof
 // Fused combine: the last work-group of a (b, kv head) to finish merges the partials of
 // its n_rep heads, which every work-group of the launch stored write-through, and writes
 // the output rows with combine_one's arithmetic.  Needs n_chunks <= kUnitChunks (64);
-// kUnitBatch chunk loads are in flight at a time.
+// KF::kMergeBatch chunk loads are in flight at a time.
 constexpr int kTW = kTiledWaves;
 constexpr int kBufSC1 = 16;  // cache-policy bits: sc1 (device-coherent load)
-constexpr int kUnitBatch = 8;
+// Chunk partials whose loads the merging work-group issues together: one memory round trip
+// per batch.  Each K format sets its batch (KF::kMergeBatch): 32 where its kernels split a
+// context into many chunks (static INT8 K: 32 chunks per (b, kv head) at config 1), 8
+// otherwise (the 32-load batch raised the INT4 kernels' VGPR count and cost them 0.5 us).
 
 // Wave-wide max / sum without the LDS crossbar: DPP within each row of 16 lanes (xor 1,
 // xor 2 in the quad, then rotations by 4 and 8), then the four row results by readlane.
@@ -166,7 +169,7 @@ __device__ __forceinline__ void merge_store_partial(const DecodeArgs& a, MergeLd
 // non-coherent cache levels (sc1); chunks are added in chunk order whichever work-group
 // merges, so every call gives the same bits.  s, z: the V scale / zero-point of group
 // lane / 16.
-template <class VF>
+template <class VF, int kUnitBatch>
 __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv, int nvalid,
                                              int wave, int lane) {
   // the V epilogue's scale / zero-point, requested with the first partial loads (loaded any
@@ -269,6 +272,7 @@ struct QIn {
 // and q' of those channels in the first two k-slots of each lane group.
 template <bool OUT>
 struct KAsymT {
+  static constexpr int kMergeBatch = 8;
   using QInT = QIn;
   static constexpr bool kAppend = true;  // the fused quantize-on-append is built for this format
   static constexpr bool kAsym = true;
@@ -500,6 +504,7 @@ __device__ __forceinline__ uint32_t i8pair_deq(uint32_t x, half2v s2) {
 // reference's dequantised k = fp16(c * s16) (i8pair_deq), the B operand q', so the logits
 // are the reference's fp32 dot products of fp16 k and q up to the summation order.
 struct KI8T {
+  static constexpr int kMergeBatch = 32;
   using QInT = QIn;
   static constexpr bool kAppend = true;
   static constexpr bool kAsym = false;
@@ -963,6 +968,10 @@ __device__ __forceinline__ void append_status(const FusedAppend& f, const Append
 template <class KF, class VF, int LOOK, bool PACK8, int WPE = 2>
 __global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
+  // One field of each kernel-argument line the prologue reads, so that the first batch of
+  // scalar loads fetches every such line (a line first touched later costs one more
+  // round trip before the first cache load; measured 0.15-0.25 us per launch).
+  asm volatile("" ::"s"(a.v.scale), "s"(a.ctx), "s"(a.app.kx), "s"(a.app.wpos));
   constexpr bool APP = KF::kAppend;  // the fused append (the writer's code) is built
   constexpr bool OUT = KF::kOut;
   const int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
@@ -1020,15 +1029,19 @@ void decode_tiled_kernel(DecodeArgs a) {
   constexpr int U = (R % 2 == 0) ? R : 2 * R;  // unroll: ring slot and x buffer are static
   typename KF::Raw kr[R];
   typename VF::Raw vr[R];
-  // The K and V tiles of step 0 are requested before the q set-up and before the context
-  // length is known (bounded by the capacity; tiles past the context are never used), so
-  // the memory system is busy from the start of the kernel; the rest of the ring (K of
-  // steps 1..LOOK, V of steps 1..LOOK-1) after the set-up.  A larger first burst delays
-  // the q loads queued with it, and the set-up waits for those (measured: the whole ring
-  // up front costs about 0.4 us per launch at the headline shape).  Every ring load is
-  // issued unconditionally (out of range for a tile past the bound): conditional loads
-  // would make the compiler's vmcnt waits conservative at the joins, i.e. wait for the
-  // tiles just requested.
+  // The context length is read here, ahead of every cache load: before the barrier below
+  // the compiler reads it through the scalar cache, whose wait does not include the cache
+  // tiles (after it, a vector load whose vmcnt wait also waited for the first tiles cost
+  // about 0.5 us per launch).  The K and V tiles of step 0 are then requested before the q
+  // set-up (bounded by the capacity; tiles past the context are never used), so the memory
+  // system is busy from the start of the kernel; the rest of the ring (K of steps 1..LOOK,
+  // V of steps 1..LOOK-1) after the set-up.  A larger first burst delays the q loads
+  // queued with it, and the set-up waits for those (measured: the whole ring up front
+  // costs about 0.4 us per launch at the headline shape; warming loads of the next tiles
+  // during the set-up cost 1.4 us).  Every ring load is issued unconditionally (out of
+  // range for a tile past the bound): conditional loads would make the compiler's vmcnt
+  // waits conservative at the joins, i.e. wait for the tiles just requested.
+  const int64_t ctx64 = row_context(a, b);
   asm volatile("" ::: "memory");
   const bool early_write = writer && wt / stride_all <= LOOK;
   if (early_write) {
@@ -1039,7 +1052,6 @@ void decode_tiled_kernel(DecodeArgs a) {
   kf.load(kTile * tile[0], tile[0] < ncap, kr[0]);
   vf.load(kTile * tile[0], tile[0] < ncap, vr[0]);
 
-  const int64_t ctx64 = row_context(a, b);
   const int ctx = (int)ctx64;
   const int ntot = (ctx + kTile - 1) / kTile;
   const bool partial = (ctx & (kTile - 1)) != 0;
@@ -1140,7 +1152,7 @@ void decode_tiled_kernel(DecodeArgs a) {
     is_last = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nvalid - 1);
   __syncthreads();
   if (!is_last) return;
-  merge_chunks<VF>(a, b, hkv, nvalid, wave, lane);
+  merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, nvalid, wave, lane);
   if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
