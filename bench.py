@@ -13,6 +13,9 @@ head):
 Caches are seeded synthetic data of the configured shape, one distinct cache per
 layer, built on the GPU with the same HIP append kernel.  Each step rewrites the
 last slot and attends over the full context, so every step does identical work.
+Uniform contexts are passed by value, as the cache engines pass them; the ragged batch of
+config 4 passes its per-row lengths (a device tensor), so the kernel shares its
+work-groups out over the rows by length.
 
 The timed region runs W warm-up and then K timed steps, bracketed by hipEvents on the
 launch stream, both as direct launches and as replays of a HIP graph of one step; the
@@ -162,7 +165,10 @@ class Layer:
             vview = kv_view_static(self.v, self.vs, self.vz)
             vfmt = C.KVQ_FMT_INT4_ASYM
         del ks_view
-        self.plan = DecodePlan(self.q, kfmt, kview, vfmt, vview, self.ctx, Hkv, cap,
+        # uniform contexts go by value, as the cache engines pass them (every row has the
+        # same length); a ragged batch passes its per-row lengths
+        ctx_arg = int(ctx[0]) if cfg.ragged_min is None else self.ctx
+        self.plan = DecodePlan(self.q, kfmt, kview, vfmt, vview, ctx_arg, Hkv, cap,
                                1.0 / math.sqrt(128), 32, inv_tau=self.inv_tau, chunk_tokens=chunk)
         # every configuration's format has a tiled kernel, so kvq_append_decode_attn does
         # the step (append + attention) in one launch

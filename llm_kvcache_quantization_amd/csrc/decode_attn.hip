@@ -775,6 +775,46 @@ static int64_t n_chunks_for(const kvq_decode_params* p, int32_t chunk) {
   return p->capacity > 0 ? (p->capacity + chunk - 1) / chunk : 1;
 }
 
+// How a call is split.  Uniform split: every row gets u = capacity / chunk work-groups
+// (grid (u, Hkv, B)).  With the tiled kernels, context lengths given per row (2..64 rows),
+// no explicit chunk_tokens and u <= kUnitChunks, the grid is one dimension per kv head
+// instead: rows of equal length still take u work-groups each, in the same chunks (so
+// their bits are those of the uniform split), while a ragged batch shares share_c work-
+// groups of the kv head, about one per resident slot, out by length: row b gets
+// ceil(t_b / T) of them (t_b its tiles, T the smallest step that fits; see share_rows in
+// decode_tiled.hip), so it runs in one round of equally long work-groups instead of
+// rounds of work-groups as long as their row.  pitch: partial slots per (b, query head).
+struct Split {
+  int32_t chunk;
+  int64_t grid_x, pitch, u, share_c;
+  bool share;
+};
+constexpr int kShareMaxRows = 64;
+static Split plan_split(const kvq_decode_params* p) {
+  Split sp;
+  sp.chunk = choose_chunk(p);
+  sp.u = sp.grid_x = sp.pitch = n_chunks_for(p, sp.chunk);
+  sp.share_c = 0;
+  sp.share = false;
+  if (tiled_family(p) != kTiledNone && p->context_lens != nullptr && p->chunk_tokens <= 0 &&
+      p->batch >= 2 && p->batch <= kShareMaxRows && p->capacity > 0 && sp.u <= kUnitChunks) {
+    const void* fn = kernel_for(p);
+    const int64_t slots = fn ? resident_slots(fn, kTiledWaves * 64) : 256;
+    int64_t c = slots / p->kv_heads;
+    if (c < p->batch) c = p->batch;
+    if (c > (int64_t)kUnitChunks * p->batch) c = (int64_t)kUnitChunks * p->batch;
+    // a row has at most one chunk per kTiledWaves tiles (every chunk holds a tile)
+    const int64_t row_max = ((p->capacity + kTile - 1) / kTile + kTiledWaves - 1) / kTiledWaves;
+    int64_t share_pitch = c < kUnitChunks ? c : kUnitChunks;
+    if (share_pitch > row_max) share_pitch = row_max;
+    sp.share_c = c;
+    sp.grid_x = c > sp.u * p->batch ? c : sp.u * p->batch;
+    sp.pitch = share_pitch > sp.u ? share_pitch : sp.u;
+    sp.share = true;
+  }
+  return sp;
+}
+
 }  // namespace kvq
 
 using namespace kvq;
@@ -793,8 +833,7 @@ static int64_t counter_bytes(const kvq_decode_params* p) {
 
 extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   if (!p) return 0;
-  const int64_t nch = n_chunks_for(p, choose_chunk(p));
-  const int64_t rows = (int64_t)p->batch * p->q_heads * nch;
+  const int64_t rows = (int64_t)p->batch * p->q_heads * plan_split(p).pitch;
   return counter_bytes(p) + rows * (kD * 4 + 8) + 256;
 }
 
@@ -844,10 +883,11 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   rc = check_view(p->v, vf, false, "v", gs);
   if (rc) return rc;
 
-  const int32_t chunk = choose_chunk(p);
+  const Split sp = plan_split(p);
+  const int32_t chunk = sp.chunk;
   if (chunk <= 0 || chunk % kTile)
     return fail(KVQ_ERR_INVALID, "chunk_tokens must be a positive multiple of 32");
-  const int64_t nch64 = n_chunks_for(p, chunk);
+  const int64_t nch64 = sp.pitch;
   if (nch64 > kMaxChunks) return fail(KVQ_ERR_UNSUPPORTED, "too many chunks (raise chunk_tokens)");
   const int64_t need = kvq_decode_workspace_bytes(p);
   if (!p->workspace || p->workspace_bytes < need)
@@ -867,6 +907,9 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   a.sm_log2e = p->sm_scale * kLog2e;
   a.chunk = chunk;
   a.n_chunks = (int)nch64;
+  a.share = sp.share ? 1 : 0;
+  a.u_chunks = (int)sp.u;
+  a.share_c = (int)sp.share_c;
   a.strided = tiled ? 1 : 0;
   a.nw = waves_for(p);
   const int64_t rows = (int64_t)p->batch * p->q_heads * nch64;
@@ -887,8 +930,9 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   a.fused = tiled && nch64 <= kUnitChunks;
   if (tiled) {
-    const hipError_t e =
-        launch_tiled(a, tfam, dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch), s);
+    const dim3 grid = sp.share ? dim3((unsigned)sp.grid_x, (unsigned)p->kv_heads, 1u)
+                               : dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch);
+    const hipError_t e = launch_tiled(a, tfam, grid, s);
     if (e != hipSuccess) return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
     if (a.fused) return KVQ_OK;  // one launch: the last work-group of each (b, kv head) merged
   } else if (p->capacity > 0) {

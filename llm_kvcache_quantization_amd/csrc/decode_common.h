@@ -71,6 +71,11 @@ struct DecodeArgs {
   float2* part_ml;  // [B, Hq, n_chunks]
   uint32_t* counters;  // [B, Hkv] slots of kCtrSlotWords u32, zero between calls (below)
   int fused;           // 1: the split-K kernel merges the partials itself (combine_unit)
+  int share;           // tiled kernel, 1-D grid per kv head (x): rows of equal context
+                       // length take u_chunks work-groups each (the uniform split); a ragged
+                       // batch shares share_c work-groups out by context length.  n_chunks
+                       // is then the partial pitch per row
+  int u_chunks, share_c;
   half_t* out;
   int64_t o_sb, o_sh;
   FusedAppend app;
@@ -219,6 +224,50 @@ __device__ __forceinline__ void softmax_tile8(float4v x0, float4v x1, float sm, 
   l = __builtin_amdgcn_fdot2(as_h2(b1), ones, l, false);
   ph = pack8(a0, a1, dpp_ror8<0x3>(a0, a0), dpp_ror8<0x3>(a1, a1));
   pl = pack8(b0, b1, dpp_ror8<0x3>(b0, b0), dpp_ror8<0x3>(b1, b1));
+}
+
+// softmax_tile8 whose probabilities enter the PV MFMA as one operand: column h < 8 (lane h)
+// carries the hi halves of head h's probabilities and the padding column h + 8 (lane h + 8)
+// the lo halves, in the same k-slot order ([row block 0, row block 1] as softmax_tile8's
+// ph), so one MFMA accumulates hi x V in column h and lo x V in column h + 8; fold_lo adds
+// the two columns once after the loop.  Both lanes of a head hold its m, so a rescale
+// applies to both columns.  Each lane passes its partner (lane ^ 8 within the 16-lane row)
+// the half the partner lacks: lane h < 8 its block-0 lo, lane h + 8 its block-1 hi.
+__device__ __forceinline__ void softmax_tile8c(float4v x0, float4v x1, float sm, float& m,
+                                               float& l, float4v acc[8], half8v& pc, bool lo8) {
+  float y[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[r] = dpp_ror8f<0xC>(x0[r], x1[r]);
+  const float lmax = max3f(max3f(y[0], y[1], y[2]), y[3], y[3]) * sm;
+  if (__ballot(lmax > m + kTau)) {
+    const float hm = fmaxf(lmax, dpp_ror8f<0xF>(lmax, lmax));  // both halves of the head
+    const float mn = fmaxf(m, wave_max_xor_groups(hm));
+    const float alpha = fast_exp2(m - mn);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+  }
+  const float nm = -m;
+  uint32_t a0, a1, b0, b1;
+  split_pair(fast_exp2(fmaf(y[0], sm, nm)), fast_exp2(fmaf(y[1], sm, nm)), a0, b0);
+  split_pair(fast_exp2(fmaf(y[2], sm, nm)), fast_exp2(fmaf(y[3], sm, nm)), a1, b1);
+  const half2v ones = {(half_t)1.0f, (half_t)1.0f};
+  l = __builtin_amdgcn_fdot2(as_h2(a0), ones, l, false);
+  l = __builtin_amdgcn_fdot2(as_h2(b0), ones, l, false);
+  l = __builtin_amdgcn_fdot2(as_h2(a1), ones, l, false);
+  l = __builtin_amdgcn_fdot2(as_h2(b1), ones, l, false);
+  const uint32_t s0 = lo8 ? b0 : a0, s1 = lo8 ? b1 : a1;
+  const uint32_t r0 = dpp_ror8<0xF>(s0, s0), r1 = dpp_ror8<0xF>(s1, s1);
+  pc = lo8 ? pack8(a0, a1, r0, r1) : pack8(r0, r1, b0, b1);
+}
+
+// after a loop of softmax_tile8c steps: column h (lanes h < 8) += column h + 8
+__device__ __forceinline__ void fold_lo(float4v acc[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[i][r] += dpp_ror8f<0x3>(0.0f, acc[i][r]);
 }
 
 // masks logits of tokens >= t1 (tile starts at tt) to -inf

@@ -273,6 +273,10 @@ struct QIn {
 template <bool OUT>
 struct KAsymT {
   static constexpr int kMergeBatch = 8;
+  // hi / lo probabilities in one PV MFMA (softmax_tile8c) when the V format allows it:
+  // measured 0.2 us faster at configs 2-3; with static INT8 K (short per-wave runs at
+  // config 1) the post-loop fold costs more than the MFMAs it saves
+  static constexpr bool kPackPV = true;
   using QInT = QIn;
   static constexpr bool kAppend = true;  // the fused quantize-on-append is built for this format
   static constexpr bool kAsym = true;
@@ -421,6 +425,7 @@ struct KAsymT {
 // operands (softmax_tile); the epilogue applies out = s (acc / l * 2^20 or 2^24 - 8) + z.
 struct VAsymT {
   static constexpr bool kTile32 = true;
+  static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
   // hooks of formats with per-token parameters (none here)
   template <class Raw>
   __device__ __forceinline__ void mask(Raw&, int, int, int) const {}
@@ -456,6 +461,7 @@ struct VAsymT {
     r.w[0] = bload4(rv, v, soff);
     r.w[1] = bload4(rv, v + 16u, soff);
   }
+  template <bool ONE = false>
   __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
                                       const NibConsts& nc) const {
 #pragma unroll
@@ -472,11 +478,18 @@ struct VAsymT {
       acc[4 * k + 1] = mfma16x16x32(c1, pb, acc[4 * k + 1]);
       acc[4 * k + 2] = mfma16x16x32(c2, pb, acc[4 * k + 2]);
       acc[4 * k + 3] = mfma16x16x32(c3, pb, acc[4 * k + 3]);
-      acc[4 * k] = mfma16x16x32(c0, pl, acc[4 * k]);
-      acc[4 * k + 1] = mfma16x16x32(c1, pl, acc[4 * k + 1]);
-      acc[4 * k + 2] = mfma16x16x32(c2, pl, acc[4 * k + 2]);
-      acc[4 * k + 3] = mfma16x16x32(c3, pl, acc[4 * k + 3]);
+      if constexpr (!ONE) {
+        acc[4 * k] = mfma16x16x32(c0, pl, acc[4 * k]);
+        acc[4 * k + 1] = mfma16x16x32(c1, pl, acc[4 * k + 1]);
+        acc[4 * k + 2] = mfma16x16x32(c2, pl, acc[4 * k + 2]);
+        acc[4 * k + 3] = mfma16x16x32(c3, pl, acc[4 * k + 3]);
+      }
     }
+  }
+  // one MFMA per block: pb is softmax_tile8c's combined hi / lo operand
+  __device__ __forceinline__ void mma1(const Raw& r, half8v pc, float4v acc[8],
+                                       const NibConsts& nc) const {
+    mma<true>(r, pc, pc, acc, nc);
   }
 };
 
@@ -505,6 +518,7 @@ __device__ __forceinline__ uint32_t i8pair_deq(uint32_t x, half2v s2) {
 // are the reference's fp32 dot products of fp16 k and q up to the summation order.
 struct KI8T {
   static constexpr int kMergeBatch = 32;
+  static constexpr bool kPackPV = false;
   using QInT = QIn;
   static constexpr bool kAppend = true;
   static constexpr bool kAsym = false;
@@ -590,6 +604,7 @@ struct KI8T {
 // v = fp16(c * s16) of the 8 tokens (one v_perm_b32 per pair of tokens, then i8pair_deq), so
 // acc / l is the output.
 struct VI8RowT {
+  static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
   static constexpr bool kTile32 = false;
   // hooks of formats with per-token parameters (none here)
   template <class Raw>
@@ -628,6 +643,7 @@ struct VI8RowT {
       r.w[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(v + t * kD), 0, kBufNT));
     }
   }
+  template <bool ONE = false>
   __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
                                       const NibConsts& nc) const {
     (void)nc;
@@ -644,8 +660,13 @@ struct VI8RowT {
       }
       const half8v av = pack8(R[0], R[1], R[2], R[3]);
       acc[c] = mfma16x16x32(av, pb, acc[c]);
-      acc[c] = mfma16x16x32(av, pl, acc[c]);
+      if constexpr (!ONE) acc[c] = mfma16x16x32(av, pl, acc[c]);
     }
+  }
+  // one MFMA per block: pb is softmax_tile8c's combined hi / lo operand
+  __device__ __forceinline__ void mma1(const Raw& r, half8v pc, float4v acc[8],
+                                       const NibConsts& nc) const {
+    mma<true>(r, pc, pc, acc, nc);
   }
 };
 
@@ -750,6 +771,7 @@ struct KKiviT : KAsymT<false> {
 // reference dequantises V in fp32).  The wave keeps Lp and Cz beside l (the softmax
 // rescales them with l) and finalize() folds them into acc before the merge (out = acc / l).
 struct VKiviRowT {
+  static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
   rsrc_t rv, rs, rz;
   uint32_t vv, vp;
@@ -965,6 +987,70 @@ __device__ __forceinline__ void append_status(const FusedAppend& f, const Append
   }
 }
 
+// One-dimensional split per kv head (a.share).  Rows of equal context length: row b takes
+// work-groups [b u, (b + 1) u) as the chunks of the uniform split (u = a.u_chunks).  A
+// ragged batch: C = a.share_c work-groups are shared out over the rows by context length.
+// Row b (t_b tiles) gets c_b = min(ceil(t_b / T), ceil(t_b / kTW), kUnitChunks) of them, or
+// one if it is empty (that one writes its zero output), with T the first of
+// ceil(total / C), ceil(total / (C - 1)), .. for which the shares fit C (C >= the row
+// count, so T = total always fits).  Work-group g of the kv head takes chunk g - start_b of
+// the row whose range [start_b, start_b + c_b) holds g; n = 0: past every row's share.  Every wave
+// of every work-group computes the same shares (lane b handles row b), so the assignment
+// is fixed by the context lengths alone.
+struct RowShare {
+  int hkv, b, chunk, n;
+};
+__device__ __forceinline__ int ceil_div_pos(int x, int y) {  // x >= 0, y >= 1, x < 2^24
+  int q = (int)((float)x / (float)y);
+  q += q * y < x;
+  q -= q > 0 && (q - 1) * y >= x;
+  return q;
+}
+// lin: the work-group's index over the whole grid (x fastest); the work-groups that do work
+// come first in it, so they are the first dispatched.
+__device__ RowShare share_rows(const DecodeArgs& a, int lin) {
+  const int lane = threadIdx.x & 63;
+  const bool row = lane < a.B;
+  const int t = row ? (int)((row_context(a, lane) + kTile - 1) / kTile) : 0;
+  RowShare rs{0, 0, 0, 0};
+  const int t0 = __builtin_amdgcn_readlane(t, 0);
+  if (__ballot(row && t != t0) == 0) {  // equal lengths: the uniform split
+    const int per_head = a.u_chunks * a.B;
+    if (lin < per_head * a.Hkv) {
+      rs.hkv = lin / per_head;
+      const int g = lin - rs.hkv * per_head;
+      rs.b = g / a.u_chunks;
+      rs.chunk = g - rs.b * a.u_chunks;
+      rs.n = a.u_chunks;
+    }
+    return rs;
+  }
+  const int C = a.share_c;
+  if (lin >= C * a.Hkv) return rs;
+  rs.hkv = lin / C;
+  const int g = lin - rs.hkv * C;
+  const int cap = t == 0 ? (row ? 1 : 0) : min(ceil_div_pos(t, kTW), kUnitChunks);
+  const int total = (int)wave_sum64((float)t);
+  int c = cap;
+  for (int k = 0; k < C; ++k) {
+    const int T = total > 0 ? max(1, (total + (C - k) - 1) / (C - k)) : 1;
+    c = t == 0 ? cap : min(ceil_div_pos(t, T), cap);
+    if ((int)wave_sum64((float)c) <= C) break;
+  }
+  int start = 0;
+  for (int r = 0; r < a.B; ++r) {
+    const int cr = __builtin_amdgcn_readlane(c, r);
+    if (g < start + cr) {
+      rs.b = r;
+      rs.chunk = g - start;
+      rs.n = cr;
+      break;
+    }
+    start += cr;
+  }
+  return rs;
+}
+
 template <class KF, class VF, int LOOK, bool PACK8, int WPE = 2>
 __global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
@@ -974,7 +1060,15 @@ void decode_tiled_kernel(DecodeArgs a) {
   asm volatile("" ::"s"(a.v.scale), "s"(a.ctx), "s"(a.app.kx), "s"(a.app.wpos));
   constexpr bool APP = KF::kAppend;  // the fused append (the writer's code) is built
   constexpr bool OUT = KF::kOut;
-  const int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z, n_ch = a.n_chunks;  // n_ch: the row's chunks
+  if (a.share) {
+    const RowShare rs = share_rows(a, (int)(blockIdx.y * gridDim.x + blockIdx.x));
+    if (rs.n == 0) return;  // past every row's share (uniform over the work-group)
+    hkv = __builtin_amdgcn_readfirstlane(rs.hkv);
+    b = __builtin_amdgcn_readfirstlane(rs.b);
+    chunk = __builtin_amdgcn_readfirstlane(rs.chunk);
+    n_ch = __builtin_amdgcn_readfirstlane(rs.n);
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, lg = lane >> 4;
@@ -985,7 +1079,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   // before the first cache loads when wt is one of the wave's first LOOK + 1 tiles.  A
   // writer whose work-group has no tile of the context stores before it leaves.
   const bool app_on = APP && a.app.kx != nullptr;
-  const int stride_all = a.n_chunks * kTW;
+  const int stride_all = n_ch * kTW;
   const int wt = app_on ? (int)(a.app.wpos / kTile) : 0;
   const bool writer = app_on && chunk * kTW + wave == wt % stride_all;
   AppendIn ain;
@@ -1014,13 +1108,13 @@ void decode_tiled_kernel(DecodeArgs a) {
     if constexpr (APP) append_store(a, kf, vf, lane, ain, (float)qin.s, (float)qin.z, afl);
   };
 
-  // Tile schedule: the n_chunks work-groups of a (b, kv head) interleave, so at step i the
-  // waves of all of them read one contiguous run of n_chunks * kTW tiles and the device
+  // Tile schedule: the n_ch work-groups of a (b, kv head) interleave, so at step i the
+  // waves of all of them read one contiguous run of n_ch * kTW tiles and the device
   // streams each slab front to back.  Wave w of work-group c takes tiles c * kTW + w +
   // i * stride (tile = 32 tokens; only the context's last tile, ntot - 1, may be partial).
   // The schedule is static, so results do not depend on timing.
   const int first = chunk * kTW + wave;
-  const int stride = a.n_chunks * kTW;
+  const int stride = n_ch * kTW;
   // tile[j] = tile of step i + j (j <= LOOK + 1)
   int tile[LOOK + 2];
 #pragma unroll
@@ -1117,10 +1211,16 @@ void decode_tiled_kernel(DecodeArgs a) {
           mask_tile(x0, x1, kTile * tile[0], ctx, lg);
           vf.mask(vr[u % R], kTile * tile[0], ctx, lg);
         }
-        half8v pb, pl;
-        if constexpr (PACK8) softmax_tile8(x0, x1, sm, m, l, acc, pb, pl, vf.extra());
-        else softmax_tile(x0, x1, sm, m, l, acc, pb, pl, vf.extra());
-        vf.mma(vr[u % R], pb, pl, acc, nc);
+        if constexpr (PACK8 && KF::kPackPV && VF::kPackedPV) {
+          half8v pc;
+          softmax_tile8c(x0, x1, sm, m, l, acc, pc, col < 8);
+          vf.mma1(vr[u % R], pc, acc, nc);
+        } else {
+          half8v pb, pl;
+          if constexpr (PACK8) softmax_tile8(x0, x1, sm, m, l, acc, pb, pl, vf.extra());
+          else softmax_tile(x0, x1, sm, m, l, acc, pb, pl, vf.extra());
+          vf.mma(vr[u % R], pb, pl, acc, nc);
+        }
         ++steps;
         progress[wave] = steps;
         if (__builtin_amdgcn_readfirstlane(progress[wave ^ 4]) < steps)
@@ -1133,6 +1233,7 @@ void decode_tiled_kernel(DecodeArgs a) {
     }
   }
   __builtin_amdgcn_s_setprio(0);
+  if constexpr (PACK8 && KF::kPackPV && VF::kPackedPV) fold_lo(acc);
   if (writer && lane == 0) append_status(a.app, afl);
 
   // Merge.  The waves' states are merged in LDS and the work-group's partial is stored
@@ -1140,7 +1241,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   // work-group has completed, one thread counts it in (word 0 of the (b, kv head)'s
   // counter slot); the last of the (b, kv head)'s work-groups merges every partial, writes
   // the output and resets the counter.
-  const int nvalid = valid_chunks(a, ctx);
+  const int nvalid = min(n_ch, (ntot + kTW - 1) / kTW);  // chunks holding a tile
   uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
   __shared__ int is_last;
   vf.finalize(acc, lane);

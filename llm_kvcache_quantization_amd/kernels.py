@@ -175,7 +175,7 @@ class DecodePlan:
         k_view: C.KvView,
         v_format: int,
         v_view: C.KvView,
-        context_lens: torch.Tensor,
+        context_lens,
         kv_heads: int,
         capacity: int,
         sm_scale: float,
@@ -186,6 +186,8 @@ class DecodePlan:
         keepalive: tuple = (),
         shared_workspace: bool = False,
     ):
+        """context_lens: int32 [B] device tensor (per-row lengths), or an int, the length
+        of every row passed by value (no device read of the lengths)."""
         B, Hq, D = q.shape
         self.q = q
         self.context_lens = context_lens
@@ -200,7 +202,11 @@ class DecodePlan:
         p.inv_tau = _ptr(inv_tau)
         p.k_format, p.v_format = k_format, v_format
         p.k, p.v = k_view, v_view
-        p.context_lens = context_lens.data_ptr()
+        if isinstance(context_lens, torch.Tensor):
+            p.context_lens = context_lens.data_ptr()
+        else:
+            p.context_lens = None
+            p.context_len = int(context_lens)
         p.batch, p.q_heads, p.kv_heads = B, Hq, kv_heads
         p.head_dim, p.group_size = D, group_size
         p.capacity = capacity
