@@ -919,3 +919,30 @@ def test_kivi_cache_append_bitexact_and_decode(B, H, S0, steps):
     assert_close(out, ref, f"kivi cache B{B} H{H} S{S0}+{steps}")
     k_deq, v_deq = cache.get_kv(0)
     assert k_deq.shape == (B, H, S0 + steps, D)
+
+
+@pytest.mark.parametrize("B,S,ctx", [
+    (10, 16384, [0, 1, 31, 33, 500, 4097, 12000, 16384, 257, 64]),
+    (3, 20000, [20000, 19999, 7]),
+    (64, 600, [((i * 37) % 600) for i in range(64)]),
+])
+def test_decode_shared_split_ragged(B, S, ctx):
+    """Ragged per-row contexts (a context tensor, 2..64 rows): the tiled kernel shares the
+    kv head's work-groups out over the rows by length, empty and one-tile rows included.
+    Against the oracle, and two launches bit-identical (the shares depend on the lengths
+    only)."""
+    K = _lib()
+    cfg, t, q, tau, kq, vq, oidx, oval, cl = _asym_case(3, B, S, ctx, 70 + B, True)
+    sm = 1 / math.sqrt(128)
+    ref = OA.decode_attn_asym_ref(q, kq, vq, t.k_scale, t.k_zp, t.v_scale, t.v_zp, cl, sm,
+                                  inv_tau=tau, k_outlier_idx=oidx, k_outlier_val=oval)
+    args = (q.to(DEV), kq.to(DEV), K.tile_v(vq.to(DEV)), t.k_scale.to(DEV), t.k_zp.to(DEV),
+            t.v_scale.to(DEV), t.v_zp.to(DEV), cl.to(DEV), sm)
+    kw = dict(inv_tau=tau.to(DEV), k_outlier_idx=oidx.to(DEV), k_outlier_val=oval.to(DEV))
+    out = K.decode_attn_int4_asym(*args, **kw).clone()
+    again = K.decode_attn_int4_asym(*args, **kw)
+    assert torch.equal(out, again)
+    assert_close(out, ref, f"shared split B{B} S{S}")
+    for b, c in enumerate(ctx):
+        if c == 0:
+            assert torch.all(out[b] == 0)
