@@ -999,6 +999,7 @@ __device__ __forceinline__ void append_status(const FusedAppend& f, const Append
 // is fixed by the context lengths alone.
 struct RowShare {
   int hkv, b, chunk, n;
+  int64_t ctx;  // row b's context length (clamped to the capacity)
 };
 __device__ __forceinline__ int ceil_div_pos(int x, int y) {  // x >= 0, y >= 1, x < 2^24
   int q = (int)((float)x / (float)y);
@@ -1011,8 +1012,9 @@ __device__ __forceinline__ int ceil_div_pos(int x, int y) {  // x >= 0, y >= 1, 
 __device__ RowShare share_rows(const DecodeArgs& a, int lin) {
   const int lane = threadIdx.x & 63;
   const bool row = lane < a.B;
-  const int t = row ? (int)((row_context(a, lane) + kTile - 1) / kTile) : 0;
-  RowShare rs{0, 0, 0, 0};
+  const int len = row ? (int)row_context(a, lane) : 0;
+  const int t = (len + kTile - 1) / kTile;
+  RowShare rs{0, 0, 0, 0, 0};
   const int t0 = __builtin_amdgcn_readlane(t, 0);
   if (__ballot(row && t != t0) == 0) {  // equal lengths: the uniform split
     const int per_head = a.u_chunks * a.B;
@@ -1022,6 +1024,7 @@ __device__ RowShare share_rows(const DecodeArgs& a, int lin) {
       rs.b = g / a.u_chunks;
       rs.chunk = g - rs.b * a.u_chunks;
       rs.n = a.u_chunks;
+      rs.ctx = __builtin_amdgcn_readlane(len, rs.b);
     }
     return rs;
   }
@@ -1044,6 +1047,7 @@ __device__ RowShare share_rows(const DecodeArgs& a, int lin) {
       rs.b = r;
       rs.chunk = g - start;
       rs.n = cr;
+      rs.ctx = __builtin_amdgcn_readlane(len, r);
       break;
     }
     start += cr;
@@ -1061,6 +1065,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   constexpr bool APP = KF::kAppend;  // the fused append (the writer's code) is built
   constexpr bool OUT = KF::kOut;
   int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z, n_ch = a.n_chunks;  // n_ch: the row's chunks
+  int64_t share_ctx = 0;
   if (a.share) {
     const RowShare rs = share_rows(a, (int)(blockIdx.y * gridDim.x + blockIdx.x));
     if (rs.n == 0) return;  // past every row's share (uniform over the work-group)
@@ -1068,6 +1073,7 @@ void decode_tiled_kernel(DecodeArgs a) {
     b = __builtin_amdgcn_readfirstlane(rs.b);
     chunk = __builtin_amdgcn_readfirstlane(rs.chunk);
     n_ch = __builtin_amdgcn_readfirstlane(rs.n);
+    share_ctx = __builtin_amdgcn_readfirstlane((int)rs.ctx);
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1135,7 +1141,8 @@ void decode_tiled_kernel(DecodeArgs a) {
   // during the set-up cost 1.4 us).  Every ring load is issued unconditionally (out of
   // range for a tile past the bound): conditional loads would make the compiler's vmcnt
   // waits conservative at the joins, i.e. wait for the tiles just requested.
-  const int64_t ctx64 = row_context(a, b);
+  // (the shared split has every row's length already)
+  const int64_t ctx64 = a.share ? share_ctx : row_context(a, b);
   asm volatile("" ::: "memory");
   const bool early_write = writer && wt / stride_all <= LOOK;
   if (early_write) {
