@@ -74,6 +74,9 @@ def parse():
                          "so a profiler sees only the step's launches")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device copy three times (rocprof counter calibration)")
+    ap.add_argument("--kv-mode", choices=sorted(MODE_SETTINGS), default=None,
+                    help="time one of the reference's kv_modes through its cache engine at the "
+                         "configuration's shape (shipped calibration settings) and exit")
     ap.add_argument("--kivi-probe", action="store_true",
                     help="only time kvq_decode_attn over the KIVI layout at config 3's shape "
                          "(B 8, 28 / 4 heads, 32k tokens; random codes and parameters)")
@@ -374,6 +377,105 @@ def engine_leg(cfg, device, steps, warmup):
     return res
 
 
+# The reference's own kv_modes with the settings its shipped calibration files carry
+# (artifacts/kv_calib_mse_1p5b_int8.json / _int4.json: group 16, int4_outlier_ratio 0.01;
+# loaded by src/engine/generate_loop.py:751-889): static tables for the *_ours / *_fused
+# modes, dynamic per-token scales for the baselines.
+MODE_SETTINGS = {
+    "int8_baseline": dict(static=False, group_size=128),
+    "int8_fused": dict(static=False, group_size=128),
+    "int8_ours": dict(static=True, group_size=16),
+    "int4_baseline": dict(static=False, group_size=32),
+    "int4_fused": dict(static=True, group_size=16, outlier_rescue_ratio=0.01),
+    "int4_ours": dict(static=True, group_size=16, outlier_rescue_ratio=0.01),
+    "int4_ours_mixed": dict(static=True, group_size=16, outlier_rescue_ratio=0.01, mixed_rescue=True),
+}
+
+
+def modes_leg(cfg, mode, device, steps, warmup):
+    """One of the reference's kv_modes at configuration cfg's model shape, batch and
+    context: the engine modes.create_kv_cache builds for it, with static tables (when the
+    mode has them) from the configuration's seeded calibration sample at the shipped
+    settings (MODE_SETTINGS), and per-head inverse temperatures.  Each layer is prefilled
+    through ``append`` a few tokens short of the context; then ``append_decode_attn`` runs
+    for every layer per step (check_numerics off: no host read-back), timed with
+    hipEvents.  Algorithmic bytes per call: each context token's K and V codes and the
+    per-token scales the engine stores (static tables: none), q and out."""
+    import llm_kvcache_quantization_amd as K
+    from llm_kvcache_quantization_amd import calib as CB
+    from llm_kvcache_quantization_amd import modes as M
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    if cfg.ragged_min is not None:
+        raise SystemExit("--kv-mode: an engine holds one context length for all rows; "
+                         "use a configuration with uniform contexts (1, 2 or 3)")
+    st = MODE_SETTINGS[mode]
+    gs = st["group_size"]
+    nl = max(cfg.layers, MIN_ROTATE)
+    cal = M.Calibration(group_size=gs, clip_percentile=99.9,
+                        outlier_rescue_ratio=st.get("outlier_rescue_ratio", 0.0),
+                        mixed_rescue=st.get("mixed_rescue", False))
+    if st["static"]:
+        make = CB.int8_static_scale if mode.startswith("int8") else CB.int4_static_scale
+        ks, vs = [], []
+        for l in range(nl):
+            g = torch.Generator().manual_seed(SY.seed_for(cfg.index, l % cfg.layers) + 500_000)
+            k, v = SY.draw_kv(cfg, l % cfg.layers, 1, SY.CALIB_TOKENS, g)
+            ks.append(make(k, gs))
+            vs.append(make(v, gs))
+        cal.static_k_scale = torch.stack(ks).to(device)
+        cal.static_v_scale = torch.stack(vs).to(device)
+        cal.inv_tau = SY.inv_tau(cfg).float().to(device)
+    calls = 2 + warmup + steps
+    s0 = ((cfg.context - calls) // 32) * 32
+    cache = M.create_kv_cache(mode, nl, device=device, max_seq_len=cfg.context, calib=cal,
+                              check_numerics=False)
+    gen = torch.Generator(device=device).manual_seed(SY.seed_for(cfg.index, 0) + 6)
+    for l in range(nl):
+        k, v = SY.draw_kv(cfg, l % cfg.layers, cfg.batch, s0, gen, device=device)
+        cache.append(l, k, v)
+        del k, v
+    q = SY.draw_q(cfg, cfg.batch, gen, device=device)
+    k1, v1 = SY.draw_kv(cfg, 0, cfg.batch, 1, gen, device=device)
+    sm = 1.0 / math.sqrt(128)
+    taus = [None if cal.inv_tau is None else cal.inv_tau[l].half().contiguous() for l in range(nl)]
+
+    def step():
+        for l in range(nl):
+            cache.append_decode_attn(l, q, k1, v1, sm, inv_tau=taus[l])
+
+    step()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    host = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (steps * nl)
+    n_mid = s0 + 1 + warmup + (steps + 1) // 2
+    kc, vc, kst, vst = cache._raw_views(0)
+    per_tok = kc.shape[-1] + vc.shape[-1]
+    for tok, s in ((cache._k_tok[0], kst), (cache._v_tok[0], vst)):
+        if tok:
+            per_tok += s.shape[-1] * s.element_size()
+    nbytes = cfg.batch * cfg.kv_heads * n_mid * per_tok + 2 * cfg.batch * cfg.q_heads * 128 * 2
+    fused = cache._fused_step_ok(128)
+    res = {"kv_mode": mode, "engine": type(cache).__name__, "group_size": gs,
+           "static_scales": st["static"], "per_token_scales": [bool(cache._k_tok[0]), bool(cache._v_tok[0])],
+           "fused_step": bool(fused), "layers": nl, "batch": cfg.batch, "context_mid": n_mid,
+           "us_per_layer_step": round(us, 3), "host_us_per_call": round(host * 1e6 / (steps * nl), 3),
+           "bytes_per_call": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+           "frac_of_8TBps": round(nbytes / us / 8e6, 4)}
+    cache.release()
+    return res
+
+
 def copy_probe(device, nbytes=1 << 30, reps=3):
     """A plain copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters: each
     launch reads and writes exactly `nbytes`."""
@@ -529,6 +631,15 @@ def main():
         return
     if args.kivi_probe:
         kivi_probe("cuda:0", max(args.steps, 200), max(args.warmup, 20))
+        return
+    if args.kv_mode:
+        from llm_kvcache_quantization_amd import _capi as C
+        from llm_kvcache_quantization_amd import synthetic as SY
+
+        C.lib()
+        torch.cuda.set_device(0)
+        print(json.dumps(modes_leg(SY.CONFIGS[args.config], args.kv_mode, "cuda:0", args.steps,
+                                   args.warmup)), flush=True)
         return
     from llm_kvcache_quantization_amd import _capi as C
     from llm_kvcache_quantization_amd import synthetic as SY

@@ -420,8 +420,8 @@ class _SymCacheBase(_EngineBase):
     # -- decode step: the append + attention of src/engine/patch_model.py:755-957
 
     def _fused_step_ok(self, D: int) -> bool:
-        """The format the tiled kernel appends and attends in one launch (static group-32
-        INT8 scales on both sides, no adaptive policy)."""
+        """The format the tiled kernel appends and attends in one launch (static INT8
+        scales on both sides, any group size, no adaptive policy)."""
         return False
 
     def _step_for(self, layer_id: int, q_heads: int):
@@ -470,8 +470,9 @@ class _SymCacheBase(_EngineBase):
         over the whole cache, the new token included (the append + attention of the
         reference's decode step, src/engine/patch_model.py:755-957).  q: fp16 [B, Hq, D];
         inv_tau: optional fp16 [Hq], applied as fp16(q * inv_tau) in the kernel.  Returns
-        fp16 [B, Hq, D].  With static group-32 INT8 scales (no adaptive policy) both run in
-        one HIP launch (kvq_append_decode_attn); otherwise ``append`` then the decode kernel.
+        fp16 [B, Hq, D].  With static INT8 scales on both sides (no adaptive policy) both run
+        in one HIP launch (kvq_append_decode_attn); otherwise ``append`` then the decode
+        kernel.
         Either way codes and output are bit-identical to ``append`` followed by
         :func:`kernels.decode_attn_int8` / ``decode_attn_int4`` over the cache's tensors.
         The kernel parameters are kept per layer between calls (no device tensor is created
@@ -614,8 +615,8 @@ class INT8KVCache(_SymCacheBase):
         return self._raw_views(layer_id)
 
     def _fused_step_ok(self, D: int) -> bool:
-        return (self.group_size == 32 and D == 128 and not self._side_is_token("k")
-                and not self._side_is_token("v"))
+        return (self.group_size in (8, 16, 32, 64, 128) and D == 128
+                and not self._side_is_token("k") and not self._side_is_token("v"))
 
     def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
         """Dequantize (code * scale in fp32) and return fp16 K/V (int8_cache.py:490-542)."""

@@ -626,12 +626,13 @@ static int tiled_family(const kvq_decode_params* p) {
   if (p->k_format == KVQ_FMT_INT4_ASYM)
     return (p->v_format == KVQ_FMT_INT4_ASYM && vt) ? (p->k.n_outlier > 0 ? kTiledA4A4o : kTiledA4A4)
                                                      : kTiledNone;
-  const bool k8 = p->k_format == KVQ_FMT_INT8_SYM && p->group_size == kTile &&
-                  static_over_bt(p->k, p) && p->k.stride_t == kD;
+  // static INT8 K with any group size (8 .. 128, checked by the caller); INT4_ASYM V
+  // needs groups of 32, and the call has one group size for both sides
+  const bool k8 = p->k_format == KVQ_FMT_INT8_SYM && static_over_bt(p->k, p) && p->k.stride_t == kD;
   if (!k8) return kTiledNone;
-  if (p->v_format == KVQ_FMT_INT4_ASYM && vt) return kTiledI8A4;
+  if (p->v_format == KVQ_FMT_INT4_ASYM && vt) return p->group_size == kTile ? kTiledI8A4 : kTiledNone;
   if (p->v_format == KVQ_FMT_INT8_SYM && !vt && static_over_bt(p->v, p) && p->v.stride_t == kD)
-    return kTiledI8I8;
+    return p->group_size == kTile ? kTiledI8I8 : kTiledI8I8g;
   return kTiledNone;
 }
 
@@ -1056,7 +1057,8 @@ static int check_fused_side(const kvq_append_params* x, const kvq_kv_view& v, in
   if (x->format != fmt)
     return fail(KVQ_ERR_UNSUPPORTED, n + ": format differs from the decode call's");
   if (x->seq_new != 1) return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append takes one token");
-  if (x->batch != p->batch || x->heads != p->kv_heads || x->head_dim != kD || x->group_size != 32)
+  if (x->batch != p->batch || x->heads != p->kv_heads || x->head_dim != kD ||
+      x->group_size != p->group_size)
     return fail(KVQ_ERR_INVALID, n + ": shape does not match the decode call");
   if (!x->x || ((uintptr_t)x->x % 4) || (x->x_stride_b % 2) || (x->x_stride_h % 2))
     return fail(KVQ_ERR_INVALID, n + ": x is NULL or its rows are not 4-byte aligned");

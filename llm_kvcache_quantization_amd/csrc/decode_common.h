@@ -416,7 +416,8 @@ enum TiledFam {
   kTiledA4A4,   // INT4_ASYM K, INT4_ASYM V in the TILE32 layout
   kTiledA4A4o,  // the same with 4 fp16 outlier K channels
   kTiledI8A4,   // INT8_SYM K (static scale), INT4_ASYM V in the TILE32 layout
-  kTiledI8I8,   // INT8_SYM K and V (static scales), token rows
+  kTiledI8I8,   // INT8_SYM K and V (static scales, groups of 32), token rows
+  kTiledI8I8g,  // the same with any other group size (8, 16, 64, 128)
   kTiledKivi,   // INT4_KIVI K (per-channel) and V (per-token), token rows
 };
 // kernel of family fam for n_rep query heads per kv head, or nullptr

@@ -260,6 +260,7 @@ struct QIn {
   u32x4 q;
   half_t tau, s, z;
   int4 oc;
+  half_t sj[4];  // static INT8 K: the scale of channel slice 32 lg + 8 j (any group size)
 };
 
 // INT4 asymmetric K with static scale s / zero-point z per (kv head, group of 32).  With
@@ -280,6 +281,7 @@ struct KAsymT {
   using QInT = QIn;
   static constexpr bool kAppend = true;  // the fused quantize-on-append is built for this format
   static constexpr bool kAsym = true;
+  static constexpr bool kGsAny = false;  // groups of 32
   static constexpr bool kOut = OUT;
   static constexpr bool kSub24 = true;  // logits scaled by 2^-24
   half8v qh[4];
@@ -510,13 +512,19 @@ __device__ __forceinline__ uint32_t i8pair_deq(uint32_t x, half2v s2) {
   return as_u32((as_h2(x ^ 0x64806480u) - off) * s2);
 }
 
-// INT8 symmetric K with a static fp16 scale s per (kv head, group of 32), i.e. per-token
-// scales given as a view with stride 0 over b and t (the reference's static-scale cache,
+// INT8 symmetric K with a static fp16 scale s per (kv head, group), i.e. per-token scales
+// given as a view with stride 0 over b and t (the reference's static-scale cache,
 // src/cache/int8_cache.py:298-488).  Lane (row, lg) of row block rb reads bytes
-// [32 lg, 32 lg + 32) of token 16 rb + row: quantisation group lg.  The A operand is the
-// reference's dequantised k = fp16(c * s16) (i8pair_deq), the B operand q', so the logits
-// are the reference's fp32 dot products of fp16 k and q up to the summation order.
+// [32 lg, 32 lg + 32) of token 16 rb + row.  GS_ANY = false: groups of 32, so those 32
+// channels are group lg and share one scale.  GS_ANY = true: any group size (8 .. 128,
+// a.gs); each 8-channel slice j takes the scale of its own group (3 more VGPRs; the group
+// index comes from a.gs at run time, which costs the groups-of-32 kernel 0.2 us of set-up
+// at config 1, hence two instantiations).  The A operand is the reference's
+// dequantised k = fp16(c * s16) (i8pair_deq), the B operand q', so the logits are the
+// reference's fp32 dot products of fp16 k and q up to the summation order.
+template <bool GS_ANY>
 struct KI8T {
+  static constexpr bool kGsAny = GS_ANY;
   static constexpr int kMergeBatch = 32;
   static constexpr bool kPackPV = false;
   using QInT = QIn;
@@ -524,8 +532,9 @@ struct KI8T {
   static constexpr bool kAsym = false;
   static constexpr bool kOut = false;
   static constexpr bool kSub24 = false;  // logits at unit scale
+  static constexpr int kNS = GS_ANY ? 4 : 1;
   half8v qh[4];
-  half2v s2;  // the scale of group lg, twice
+  half2v s2[kNS];  // the scale of channel slice 32 lg + 8 j .. + 7 (its group), twice
   rsrc_t rk;
   uint32_t vk;
   struct Raw {
@@ -543,7 +552,15 @@ struct KI8T {
     const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
     in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
     in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
-    in.s = static_scale16(a.k, hkv, lg);
+    if constexpr (GS_ANY) {
+      // slice j of the lane's 32 channels lies in group (32 lg + 8 j) / gs (gs = 8 .. 128)
+      const int sh = __builtin_ctz((unsigned)a.gs);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) in.sj[j] = static_scale16(a.k, hkv, (32 * lg + 8 * j) >> sh);
+    } else {
+      in.sj[0] = static_scale16(a.k, hkv, lg);
+    }
+    in.s = in.sj[0];
     in.z = (half_t)0.0f;
     in.oc = int4{-1, -1, -1, -1};
   }
@@ -565,7 +582,8 @@ struct KI8T {
   __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
-    s2 = half2v{in.s, in.s};
+#pragma unroll
+    for (int j = 0; j < kNS; ++j) s2[j] = half2v{in.sj[j], in.sj[j]};
   }
   __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
     const uint32_t v = vk + (valid ? (uint32_t)tok * kD : kOutOfRange);
@@ -574,10 +592,12 @@ struct KI8T {
     r.w[2] = bload4(rk, v + 16 * kD, 0);
     r.w[3] = bload4(rk, v + 16 * kD + 16, 0);
   }
-  // 8 codes (dwords lo = channels 0..3, hi = 4..7) -> fp16(c * s16) in channel order
-  __device__ __forceinline__ half8v deq8(uint32_t lo, uint32_t hi) const {
-    return pack8(i8pair_deq(perm_b32(0u, lo, 0x0C010C00u), s2), i8pair_deq(perm_b32(0u, lo, 0x0C030C02u), s2),
-                 i8pair_deq(perm_b32(0u, hi, 0x0C010C00u), s2), i8pair_deq(perm_b32(0u, hi, 0x0C030C02u), s2));
+  // 8 codes of slice j (dwords lo = channels 0..3, hi = 4..7) -> fp16(c * s16) in channel
+  // order
+  __device__ __forceinline__ half8v deq8(uint32_t lo, uint32_t hi, int j) const {
+    const half2v s = s2[GS_ANY ? j : 0];
+    return pack8(i8pair_deq(perm_b32(0u, lo, 0x0C010C00u), s), i8pair_deq(perm_b32(0u, lo, 0x0C030C02u), s),
+                 i8pair_deq(perm_b32(0u, hi, 0x0C010C00u), s), i8pair_deq(perm_b32(0u, hi, 0x0C030C02u), s));
   }
   __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
                                      float4v& x1) const {
@@ -589,8 +609,8 @@ struct KI8T {
       const u32x4 w0 = r.w[j >> 1], w1 = r.w[2 + (j >> 1)];
       const uint32_t l0 = (j & 1) ? w0.z : w0.x, h0 = (j & 1) ? w0.w : w0.y;
       const uint32_t l1 = (j & 1) ? w1.z : w1.x, h1 = (j & 1) ? w1.w : w1.y;
-      c0 = mfma16x16x32(deq8(l0, h0), qh[j], c0);
-      c1 = mfma16x16x32(deq8(l1, h1), qh[j], c1);
+      c0 = mfma16x16x32(deq8(l0, h0, j), qh[j], c0);
+      c1 = mfma16x16x32(deq8(l1, h1, j), qh[j], c1);
     }
     x0 = c0;
     x1 = c1;
@@ -598,11 +618,12 @@ struct KI8T {
 };
 
 // INT8 symmetric V in token rows (the reference layout) with a static scale per (kv head,
-// group of 32).  Lane (col, lg) reads the 8 bytes of channels 8 col .. 8 col + 7 of its 8
+// group): groups of 32 (GS_ANY = false) or any group size a.gs (8 .. 128).  Lane (col, lg) reads the 8 bytes of channels 8 col .. 8 col + 7 of its 8
 // PV k-slot tokens T(k) = 4 lg + k (k < 4), 16 + 4 lg + k - 4: each load instruction reads
 // four whole 128-byte rows.  The A operand of MFMA c (channel 8 col + c) is the reference's
 // v = fp16(c * s16) of the 8 tokens (one v_perm_b32 per pair of tokens, then i8pair_deq), so
 // acc / l is the output.
+template <bool GS_ANY>
 struct VI8RowT {
   static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
   static constexpr bool kTile32 = false;
@@ -613,7 +634,7 @@ struct VI8RowT {
   __device__ __forceinline__ float* extra() { return nullptr; }
   rsrc_t rv;
   uint32_t vv;
-  half2v s2;  // the scale of group col / 4, twice
+  half2v s2;  // the scale of the group of channels 8 col .. 8 col + 7, twice
   struct Raw {
     u32x2 w[8];  // token T(k)
   };
@@ -631,7 +652,8 @@ struct VI8RowT {
     const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
     rv = buffer_rsrc(vb, (uint32_t)(a.cap * kD));
     vv = (uint32_t)((4 * lg) * kD + 8 * col);
-    const half_t sv = static_scale16(a.v, hkv, col >> 2);
+    const half_t sv =
+        static_scale16(a.v, hkv, GS_ANY ? (8 * col) >> __builtin_ctz((unsigned)a.gs) : col >> 2);
     s2 = half2v{sv, sv};
   }
   // rows of a partial last tile past the capacity read 0; !valid: every load out of range
@@ -900,8 +922,9 @@ struct VKiviRowT {
 struct AppendIn {
   uint32_t k2, v2;  // fp16 pair of channels 2 lane, 2 lane + 1
   uint32_t o;       // lanes < 4: fp16 K value of outlier channel lane (INT4_ASYM K)
-  float ks;         // INT8 K: the fp16 scale of group lane / 16
-  float vs, vz;     // V of group lane / 16: INT8 fp16 scale, or INT4_ASYM scale / zero-point
+  float ks;         // INT8 K: the fp16 scale of the group of channels 2 lane, 2 lane + 1
+  float vs, vz;     // V: INT8 fp16 scale of that group, or INT4_ASYM scale / zero-point of
+                    // group lane / 16
 };
 struct AppendFlags {
   bool kbad = false, vbad = false;
@@ -932,15 +955,17 @@ __device__ __forceinline__ void append_fetch(const DecodeArgs& a, int b, int hkv
     in.o = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
         rk, (int)(lane < 4 ? 2u * (uint32_t)ch : kOutOfRange), 0, kBufNT);
   }
-  const int g = lane >> 4;
+  const int g = lane >> 4;  // group of 32
+  int g8 = g;               // INT8 sides: the group of channels 2 lane, 2 lane + 1
+  if constexpr (KF::kGsAny) g8 = (2 * lane) >> __builtin_ctz((unsigned)a.gs);
   in.ks = 0.f;
-  if constexpr (!KF::kAsym) in.ks = app_int8_scale(f.kst, f.kst_f32, f.kst_sh, f.kst_sg, hkv, g);
+  if constexpr (!KF::kAsym) in.ks = app_int8_scale(f.kst, f.kst_f32, f.kst_sh, f.kst_sg, hkv, g8);
   if constexpr (VF::kTile32) {
     // V scale / zero-point of group lane / 16 (fp16, element offsets hkv * ssh + g * ssg)
     in.vs = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
     in.vz = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
   } else {
-    in.vs = app_int8_scale(f.vst, f.vst_f32, f.vst_sh, f.vst_sg, hkv, g);
+    in.vs = app_int8_scale(f.vst, f.vst_f32, f.vst_sh, f.vst_sg, hkv, g8);
     in.vz = 0.f;
   }
 }
@@ -1276,8 +1301,9 @@ const void* tiled_ptr_fam(int fam) {
   switch (fam) {
     case kTiledA4A4: return tiled_ptr<KAsymT<false>, VAsymT, PACK8>();
     case kTiledA4A4o: return tiled_ptr<KAsymT<true>, VAsymT, PACK8>();
-    case kTiledI8A4: return tiled_ptr<KI8T, VAsymT, PACK8>();
-    case kTiledI8I8: return tiled_ptr<KI8T, VI8RowT, PACK8>();
+    case kTiledI8A4: return tiled_ptr<KI8T<false>, VAsymT, PACK8>();
+    case kTiledI8I8: return tiled_ptr<KI8T<false>, VI8RowT<false>, PACK8>();
+    case kTiledI8I8g: return tiled_ptr<KI8T<true>, VI8RowT<true>, PACK8>();
     case kTiledKivi: return tiled_ptr<KKiviT, VKiviRowT, PACK8>();
     default: return nullptr;
   }

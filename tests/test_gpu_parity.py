@@ -282,14 +282,14 @@ def test_decode_int8_static_expanded_scales_and_fp32_q():
     assert_close(out, ref.float(), "int8 static-expanded")
 
 
-def _static_int8_case(B, Hq, Hkv, S, g, scale_dtype=torch.float16):
-    """Codes and static group-32 scales as INT8KVCache stores them: per-token scale views
-    with stride 0 over b and t, which the tiled INT8 kernels serve."""
-    q, k, v, _, _ = _rand_int8_case(B, Hq, Hkv, S, 4, g)
-    sk = (torch.rand(Hkv, 4, generator=g) * 0.01 + 1e-3).to(scale_dtype)
-    sv = (torch.rand(Hkv, 4, generator=g) * 0.02 + 1e-3).to(scale_dtype)
-    ks = sk[None, :, None, :].expand(B, Hkv, S, 4)
-    vs = sv[None, :, None, :].expand(B, Hkv, S, 4)
+def _static_int8_case(B, Hq, Hkv, S, g, scale_dtype=torch.float16, G=4):
+    """Codes and static scales (G groups per head) as INT8KVCache stores them: per-token
+    scale views with stride 0 over b and t, which the tiled INT8 kernels serve."""
+    q, k, v, _, _ = _rand_int8_case(B, Hq, Hkv, S, G, g)
+    sk = (torch.rand(Hkv, G, generator=g) * 0.01 + 1e-3).to(scale_dtype)
+    sv = (torch.rand(Hkv, G, generator=g) * 0.02 + 1e-3).to(scale_dtype)
+    ks = sk[None, :, None, :].expand(B, Hkv, S, G)
+    vs = sv[None, :, None, :].expand(B, Hkv, S, G)
     return q, k, v, ks, vs
 
 
@@ -310,6 +310,30 @@ def test_decode_int8_static_tiled(B, Hq, Hkv, S, ctx):
     out = K.decode_attn_int8(q.to(DEV), k.to(DEV), v.to(DEV), ks.to(DEV), vs.to(DEV), cl.to(DEV),
                              sm_scale=sm)
     assert_close(out, ref, f"int8 static tiled B{B} Hq{Hq} Hkv{Hkv} S{S}")
+    for b, c in enumerate(ctx):
+        if c == 0:
+            assert torch.all(out[b] == 0)
+
+
+@pytest.mark.parametrize("G,B,Hq,Hkv,S,ctx", [
+    (8, 4, 12, 2, 8192, [8192, 8191, 4097, 33]),   # group 16 (the shipped int8_ours tables)
+    (16, 3, 12, 2, 700, [700, 1, 0]),              # group 8
+    (2, 2, 28, 4, 1000, [1000, 999]),              # group 64
+    (1, 2, 40, 8, 300, [300, 64]),                 # group 128, GQA 5
+])
+def test_decode_int8_static_tiled_group_sizes(G, B, Hq, Hkv, S, ctx):
+    """Static INT8 tables of every group size the engines take (the tiled INT8 kernel reads
+    one scale per 8-channel slice) against the oracle, with per-head inverse temperature."""
+    K = _lib()
+    g = gen(77 * S + G)
+    q, k, v, ks, vs = _static_int8_case(B, Hq, Hkv, S, g, G=G)
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    sm = 1 / math.sqrt(128)
+    ref = OA.decode_attn_int8_torch_ref(OA.prescale_q(q, tau), k, v, ks, vs, cl, sm)
+    out = K.decode_attn_int8(OA.prescale_q(q, tau).to(DEV), k.to(DEV), v.to(DEV), ks.to(DEV),
+                             vs.to(DEV), cl.to(DEV), sm_scale=sm)
+    assert_close(out, ref, f"int8 static tiled G{G} B{B} Hq{Hq} Hkv{Hkv} S{S}")
     for b, c in enumerate(ctx):
         if c == 0:
             assert torch.all(out[b] == 0)
@@ -718,33 +742,42 @@ def test_fused_append_decode_matches_two_calls(cfg_idx, B, S0, steps, outliers):
         assert_close(out, ref, f"fused step cfg{cfg_idx} S{n}")
 
 
-@pytest.mark.parametrize("kind,B,S0,steps", [
-    ("int8", 2, 4095, 3),   # config 1 heads; the new tokens cross a tile boundary
-    ("int8", 3, 0, 2),      # empty cache: the first token is the whole context
-    ("int8", 4, 700, 2),
-    ("k8v4", 2, 4095, 3),   # config 4 heads (GQA 5), TILE32 V
-    ("k8v4", 3, 40, 2),     # the new token's tile is in each wave's first tiles
+@pytest.mark.parametrize("kind,B,S0,steps,gs", [
+    ("int8", 2, 4095, 3, 32),   # config 1 heads; the new tokens cross a tile boundary
+    ("int8", 3, 0, 2, 32),      # empty cache: the first token is the whole context
+    ("int8", 4, 700, 2, 32),
+    ("int8", 2, 4095, 2, 16),   # group 16 (the shipped int8_ours tables)
+    ("int8", 3, 31, 2, 8),
+    ("int8", 2, 100, 2, 128),
+    ("k8v4", 2, 4095, 3, 32),   # config 4 heads (GQA 5), TILE32 V
+    ("k8v4", 3, 40, 2, 32),     # the new token's tile is in each wave's first tiles
 ])
-def test_fused_append_decode_int8_matches_two_calls(kind, B, S0, steps):
+def test_fused_append_decode_int8_matches_two_calls(kind, B, S0, steps, gs):
     """append_decode_attn with INT8 K (one launch) against append + the decode kernel (two
     launches) on twin caches: codes and outputs bit-identical, output within tolerance of
     the oracle."""
     K = _lib()
+    from llm_kvcache_quantization_amd import calib as CB
     from llm_kvcache_quantization_amd import synthetic as SY
 
     cfg = SY.CONFIGS[1 if kind == "int8" else 4]
     t = SY.calibrate(cfg, 0)
-    g = gen(900 + S0 + B)
+    g = gen(900 + S0 + B + gs)
     k, v = SY.draw_kv(cfg, 0, B, S0 + steps, g)
     qs = [SY.draw_q(cfg, B, g) for _ in range(steps)]
     tau = SY.inv_tau(cfg)[0]
     if kind == "int8":
-        mk = lambda: K.INT8KVCache(1, device=DEV, group_size=32, static_k_scale=t.k_scale[None],
+        if gs != 32:  # tables of this group size from the same calibration sample
+            ck, cv = SY.draw_kv(cfg, 0, 1, SY.CALIB_TOKENS, gen(4242))
+            t.k_scale, t.v_scale = CB.int8_static_scale(ck, gs), CB.int8_static_scale(cv, gs)
+        mk = lambda: K.INT8KVCache(1, device=DEV, group_size=gs, static_k_scale=t.k_scale[None],
                                    static_v_scale=t.v_scale[None], check_numerics=True)
     else:
         mk = lambda: K.K8V4KVCache(1, t.k_scale[None], t.v_scale[None], t.v_zp[None], device=DEV,
                                    check_numerics=True)
     two, one = mk(), mk()
+    if kind == "int8":
+        assert one._fused_step_ok(128), "static INT8 tables take the one-launch step"
     if S0:
         for c in (two, one):
             c.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
