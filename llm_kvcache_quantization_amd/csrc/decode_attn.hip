@@ -616,6 +616,31 @@ static bool static_over_bt(const kvq_kv_view& v, const kvq_decode_params* p) {
   return (v.scale_stride_b == 0 || p->batch == 1) && (v.scale_stride_t == 0 || p->capacity <= 1);
 }
 
+// Per-token scales on both sides in dense token rows (static stride-0 views too): INT8 with
+// fp16 scales or INT4_SYM with fp32 scales (the dtypes the engines store), groups of 16 or
+// more, the groups of a token contiguous.  INT8 K with groups of 16 reads two fp16 scales in
+// one 4-byte load, so its scale rows must be 4-byte aligned.
+static int tok_family(const kvq_decode_params* p) {
+  if (p->k_format != p->v_format || p->v.layout != KVQ_LAYOUT_ROWS) return kTiledNone;
+  const bool i4 = p->k_format == KVQ_FMT_INT4_SYM;
+  if (!i4 && p->k_format != KVQ_FMT_INT8_SYM) return kTiledNone;
+  const int gs = p->group_size;
+  if (gs < 16) return kTiledNone;
+  const int64_t row = i4 ? kD / 2 : kD;
+  const int dt = i4 ? KVQ_DTYPE_F32 : KVQ_DTYPE_F16;
+  const int64_t es = i4 ? 4 : 2;
+  const int64_t w = (!i4 && gs == 16) ? 2 : 1;  // elements per aligned load
+  auto ok = [&](const kvq_kv_view& v) {
+    return v.stride_t == row && v.scale_dtype == dt && v.scale != nullptr &&
+           (v.scale_stride_g == 1 || gs == kD) && ((uintptr_t)v.scale % (w * es)) == 0 &&
+           v.scale_stride_b % w == 0 && v.scale_stride_h % w == 0 && v.scale_stride_t % w == 0 &&
+           v.scale_stride_b >= 0 && v.scale_stride_h >= 0 && v.scale_stride_t >= 0;
+  };
+  if (!ok(p->k) || !ok(p->v)) return kTiledNone;
+  if (i4) return gs == 16 ? kTiledT4g16 : kTiledT4;
+  return gs == 16 ? kTiledT8g16 : kTiledT8;
+}
+
 static int tiled_family(const kvq_decode_params* p) {
   const bool vt = p->v.layout == KVQ_LAYOUT_TILE32;
   if (p->k_format == KVQ_FMT_INT4_KIVI)
@@ -629,11 +654,11 @@ static int tiled_family(const kvq_decode_params* p) {
   // static INT8 K with any group size (8 .. 128, checked by the caller); INT4_ASYM V
   // needs groups of 32, and the call has one group size for both sides
   const bool k8 = p->k_format == KVQ_FMT_INT8_SYM && static_over_bt(p->k, p) && p->k.stride_t == kD;
-  if (!k8) return kTiledNone;
-  if (p->v_format == KVQ_FMT_INT4_ASYM && vt) return p->group_size == kTile ? kTiledI8A4 : kTiledNone;
-  if (p->v_format == KVQ_FMT_INT8_SYM && !vt && static_over_bt(p->v, p) && p->v.stride_t == kD)
+  if (k8 && p->v_format == KVQ_FMT_INT4_ASYM && vt)
+    return p->group_size == kTile ? kTiledI8A4 : kTiledNone;
+  if (k8 && p->v_format == KVQ_FMT_INT8_SYM && !vt && static_over_bt(p->v, p) && p->v.stride_t == kD)
     return p->group_size == kTile ? kTiledI8I8 : kTiledI8I8g;
-  return kTiledNone;
+  return tok_family(p);
 }
 
 // the split-K kernel kvq_decode_attn launches for p (nullptr if unsupported)
@@ -1095,7 +1120,9 @@ static int check_fused_side(const kvq_append_params* x, const kvq_kv_view& v, in
 extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
                                       const kvq_append_params* v_new, kvq_stream_t stream) {
   if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
-  if (tiled_family(p) == kTiledNone)
+  const int fam = tiled_family(p);
+  if (fam != kTiledA4A4 && fam != kTiledA4A4o && fam != kTiledI8A4 && fam != kTiledI8I8 &&
+      fam != kTiledI8I8g)
     return fail(KVQ_ERR_UNSUPPORTED,
                 "the fused append needs a tiled-kernel format: INT4_ASYM K with TILE32 V, or "
                 "static-scale INT8 K with TILE32 INT4_ASYM V or static-scale INT8 V rows");

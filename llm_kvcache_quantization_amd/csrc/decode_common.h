@@ -418,6 +418,10 @@ enum TiledFam {
   kTiledI8A4,   // INT8_SYM K (static scale), INT4_ASYM V in the TILE32 layout
   kTiledI8I8,   // INT8_SYM K and V (static scales, groups of 32), token rows
   kTiledI8I8g,  // the same with any other group size (8, 16, 64, 128)
+  kTiledT8,     // INT8_SYM K and V with per-token fp16 scales, groups of 32 .. 128, rows
+  kTiledT8g16,  // the same with groups of 16
+  kTiledT4,     // INT4_SYM K and V with per-token fp32 scales, groups of 32 .. 128, rows
+  kTiledT4g16,  // the same with groups of 16
   kTiledKivi,   // INT4_KIVI K (per-channel) and V (per-token), token rows
 };
 // kernel of family fam for n_rep query heads per kv head, or nullptr

@@ -912,6 +912,270 @@ struct VKiviRowT {
   }
 };
 
+// ---- Per-token scales: INT8 codes with fp16 scales or packed INT4-symmetric codes with fp32
+// scales per (b, kv head, token, group), in token rows (the reference's dynamic, adaptive and
+// group-rescue caches, src/cache/int8_cache.py:298-488, src/cache/int4_cache.py:298-590, read
+// by src/kernels/triton_decode_attn_int8.py:306-519 and triton_decode_attn_int4.py:62-121).
+// Both sides are dequantised as the reference's torch path does, k = fp16(c * fp16(s)), and
+// enter the MFMAs as fp16 values (the arithmetic of the row kernel's KTok / VTok).  A static
+// table given as a stride-0 view reads like per-token scales (every token one line).
+// NS = scales of a K lane's 32 channels: 1 for groups of 32 or more, 2 for groups of 16.
+// bytes of a (b, kv head)'s per-token scale rows: cap rows of stride sst elements, or one
+// row of 128 / gs groups for a stride-0 (static) view
+__device__ __forceinline__ uint32_t scale_bytes(int64_t cap, int64_t sst, int gs, int es) {
+  return (uint32_t)(sst > 0 ? cap * sst * es : (int64_t)(kD / gs) * es);
+}
+
+template <bool I4, int NS>
+struct KTokT {
+  static_assert(NS == 1 || NS == 2, "groups of 16 or more");
+  static constexpr int kMergeBatch = 16;
+  static constexpr bool kPackPV = false;
+  using QInT = QIn;
+  static constexpr bool kAppend = false;  // appended by kvq_quant_append (the group rescue
+                                          // spans every row of the call)
+  static constexpr bool kAsym = false;
+  static constexpr bool kGsAny = true;
+  static constexpr bool kOut = false;
+  static constexpr bool kSub24 = false;  // logits at unit scale
+  static constexpr int kRow = I4 ? kD / 2 : kD;  // code bytes per token
+  static constexpr int kEs = I4 ? 4 : 2;         // scale bytes (fp32 / fp16)
+  half8v qh[4];
+  rsrc_t rk, rs;
+  uint32_t vk, vs, sst;  // lane code offset, lane scale offset, scale bytes per token
+  struct Raw {
+    u32x4 w[I4 ? 2 : 4];  // I4: [rb] = bytes [16 lg, 16 lg + 16) of token 16 rb + row;
+                          // INT8: [2 rb + i] = bytes [32 lg + 16 i, + 16)
+    uint32_t s[2];        // the NS scales of row block rb (fp16 pair, fp16 or fp32 bits)
+    uint32_t s2[I4 && NS == 2 ? 2 : 1];  // the second fp32 scale of row block rb (NS = 2)
+  };
+
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kRow));
+    vk = (uint32_t)(col * kRow + (kRow / 4) * lg);
+    // the lane's first group: 32 lg / gs; with NS = 2 the next one follows (stride_g = 1)
+    const int g0 = (32 * lg) >> __builtin_ctz((unsigned)a.gs);
+    const char* sb = reinterpret_cast<const char*>(a.k.scale) +
+                     ((int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh) * kEs;
+    sst = (uint32_t)(a.k.sst * kEs);
+    rs = buffer_rsrc(sb, scale_bytes(a.cap, a.k.sst, a.gs, kEs));
+    vs = (uint32_t)(col * sst + g0 * a.k.ssg * kEs);
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.s = (half_t)1.0f;
+    in.z = (half_t)0.0f;
+    in.oc = int4{-1, -1, -1, -1};
+  }
+  // channel slice j of the q operand q' = fp16(q * inv_tau), in the k-slot order of the
+  // codes (INT4: unpack_dword_64pn's), shared through LDS
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    half_t vh[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int el = I4 ? kNibSlotElem(e) : e;
+      const half2v h2 = as_h2(qw[el >> 1]);
+      vh[e] = valid ? qscale((el & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+  }
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kRow : kOutOfRange);
+    if constexpr (I4) {
+      r.w[0] = bload4(rk, v, 0);
+      r.w[1] = bload4(rk, v + 16 * kRow, 0);
+    } else {
+      r.w[0] = bload4(rk, v, 0);
+      r.w[1] = bload4(rk, v + 16, 0);
+      r.w[2] = bload4(rk, v + 16 * kRow, 0);
+      r.w[3] = bload4(rk, v + 16 * kRow + 16, 0);
+    }
+    const uint32_t p = vs + (valid ? (uint32_t)tok * sst : kOutOfRange);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const uint32_t o = p + (uint32_t)rb * 16u * sst;
+      if constexpr (I4 && NS == 2) {
+        const u32x2 s = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, (int)o, 0, kBufNT));
+        r.s[rb] = s.x;
+        r.s2[rb] = s.y;
+      } else if constexpr (I4 || NS == 2) {
+        r.s[rb] = bload1(rs, o, 0);  // one fp32, or two fp16
+      } else {
+        r.s[rb] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)o, 0, kBufNT);
+      }
+    }
+  }
+  // the fp16 scale of slice j in row block rb, twice
+  __device__ __forceinline__ uint32_t scale2(const Raw& r, int rb, int j) const {
+    half_t s;
+    if constexpr (I4) {
+      const uint32_t bits = (NS == 2 && j >= 2) ? r.s2[rb] : r.s[rb];
+      s = (half_t)__builtin_bit_cast(float, bits);
+    } else {
+      const half2v h = as_h2(r.s[rb]);
+      s = (NS == 2 && j >= 2) ? h.y : h.x;
+    }
+    return splat_h2(s);
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    float4v c[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t s2 = scale2(r, rb, j);
+        uint32_t u[4];
+        if constexpr (I4) {
+          const u32x4 w = r.w[rb];
+          const uint32_t d = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+          unpack_dword_64pn(d, nc, u);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) u[i] = deq_pair(u[i], (half_t)72.0f, s2);
+        } else {
+          const u32x4 w = r.w[2 * rb + (j >> 1)];
+          const uint32_t lo = (j & 1) ? w.z : w.x, hi = (j & 1) ? w.w : w.y;
+          u[0] = i8pair_deq(perm_b32(0u, lo, 0x0C010C00u), as_h2(s2));
+          u[1] = i8pair_deq(perm_b32(0u, lo, 0x0C030C02u), as_h2(s2));
+          u[2] = i8pair_deq(perm_b32(0u, hi, 0x0C010C00u), as_h2(s2));
+          u[3] = i8pair_deq(perm_b32(0u, hi, 0x0C030C02u), as_h2(s2));
+        }
+        c[rb] = mfma16x16x32(pack8(u[0], u[1], u[2], u[3]), qh[j], c[rb]);
+      }
+    }
+    x0 = c[0];
+    x1 = c[1];
+  }
+};
+
+// V with per-token scales in token rows: lane (col, lg) reads channels 8 col .. 8 col + 7
+// (8 INT8 bytes or 4 packed INT4 bytes) of its 8 PV k-slot tokens T(k) = 4 lg + k (k < 4),
+// 16 + 4 lg + k - 4, and the scale of their group (8 col) / gs.  The A operand of MFMA c
+// (channel 8 col + c) is vhat = fp16(c * fp16(s)) of the 8 tokens, so acc / l is the output.
+template <bool I4>
+struct VTokT {
+  static constexpr bool kPackedPV = false;
+  static constexpr bool kTile32 = false;
+  static constexpr int kRow = I4 ? kD / 2 : kD;
+  static constexpr int kEs = I4 ? 4 : 2;
+  __device__ __forceinline__ void finalize(float4v*, int) const {}
+  __device__ __forceinline__ float* extra() { return nullptr; }
+  rsrc_t rv, rs;
+  uint32_t vv, vs, sst;
+  struct Raw {
+    uint32_t w[8][I4 ? 1 : 2];  // token T(k)
+    uint32_t s[8];              // token T(k)'s scale (fp32 or fp16 bits)
+  };
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * kRow));
+    vv = (uint32_t)((4 * lg) * kRow + (I4 ? 4 : 8) * col);
+    const int gi = (8 * col) >> __builtin_ctz((unsigned)a.gs);
+    const char* sb = reinterpret_cast<const char*>(a.v.scale) +
+                     ((int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh) * kEs;
+    sst = (uint32_t)(a.v.sst * kEs);
+    rs = buffer_rsrc(sb, scale_bytes(a.cap, a.v.sst, a.gs, kEs));
+    vs = (uint32_t)((4 * lg) * sst + gi * a.v.ssg * kEs);
+  }
+  // rows of a partial last tile past the capacity read 0; !valid: every load out of range
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * kRow : kOutOfRange);
+    const uint32_t p = vs + (valid ? (uint32_t)tok * sst : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      if constexpr (I4) {
+        r.w[k][0] = bload1(rv, v + t * kRow, 0);
+        r.s[k] = bload1(rs, p + t * sst, 0);
+      } else {
+        const u32x2 x = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(v + t * kRow), 0, kBufNT));
+        r.w[k][0] = x.x;
+        r.w[k][1] = x.y;
+        r.s[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(p + t * sst), 0, kBufNT);
+      }
+    }
+  }
+  // tokens at or past the context in the last, partial tile: scale 0 (their memory may
+  // hold anything; p is 0 there)
+  __device__ __forceinline__ void mask(Raw& r, int tt, int ctx, int lg) const {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int t = tt + 4 * lg + ((k < 4) ? k : 12 + k);
+      if (t >= ctx) r.s[k] = 0u;
+    }
+  }
+  __device__ __forceinline__ uint32_t spair(const Raw& r, int p) const {
+    if constexpr (I4)
+      return pair_h2((half_t)__builtin_bit_cast(float, r.s[2 * p]),
+                     (half_t)__builtin_bit_cast(float, r.s[2 * p + 1]));
+    else
+      return (r.s[2 * p] & 0xFFFFu) | (r.s[2 * p + 1] << 16);
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
+                                      const NibConsts& nc) const {
+    uint32_t sp[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) sp[p] = spair(r, p);
+    if constexpr (I4) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        // byte k of the tokens T(2p), T(2p + 1) into the low bytes of the two halves
+        const uint32_t sel = (uint32_t)k | 0x0C00u | ((uint32_t)(4 + k) << 16) | 0x0C000000u;
+        uint32_t h[4], o[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t R = perm_b32(r.w[2 * p + 1][0], r.w[2 * p][0], sel);
+          h[p] = deq_pair(and_or(R, nc.m_hi, nc.c64), (half_t)72.0f, sp[p]);
+          o[p] = deq_pair(and_or(R, nc.m_lo, nc.c1024), (half_t)1032.0f, sp[p]);
+        }
+        const half8v ah = pack8(h[0], h[1], h[2], h[3]), ao = pack8(o[0], o[1], o[2], o[3]);
+        acc[2 * k] = mfma16x16x32(ah, pb, acc[2 * k]);
+        acc[2 * k + 1] = mfma16x16x32(ao, pb, acc[2 * k + 1]);
+        acc[2 * k] = mfma16x16x32(ah, pl, acc[2 * k]);
+        acc[2 * k + 1] = mfma16x16x32(ao, pl, acc[2 * k + 1]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t sel = (uint32_t)(c & 3) | 0x0C00u | ((uint32_t)(4 + (c & 3)) << 16) | 0x0C000000u;
+        uint32_t R[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          R[p] = i8pair_deq(perm_b32(r.w[2 * p + 1][c >> 2], r.w[2 * p][c >> 2], sel), as_h2(sp[p]));
+        const half8v av = pack8(R[0], R[1], R[2], R[3]);
+        acc[c] = mfma16x16x32(av, pb, acc[c]);
+        acc[c] = mfma16x16x32(av, pl, acc[c]);
+      }
+    }
+  }
+};
+
 // Fused quantize-on-append of the new token of (b, kv head): one wave (the writer), two
 // values per lane, the arithmetic of the append kernel: asym_pack_pair with the decode's
 // static tables for INT4_ASYM, int8_pack_pair with the append's static table for INT8.  K
@@ -1304,6 +1568,10 @@ const void* tiled_ptr_fam(int fam) {
     case kTiledI8A4: return tiled_ptr<KI8T<false>, VAsymT, PACK8>();
     case kTiledI8I8: return tiled_ptr<KI8T<false>, VI8RowT<false>, PACK8>();
     case kTiledI8I8g: return tiled_ptr<KI8T<true>, VI8RowT<true>, PACK8>();
+    case kTiledT8: return tiled_ptr<KTokT<false, 1>, VTokT<false>, PACK8>();
+    case kTiledT8g16: return tiled_ptr<KTokT<false, 2>, VTokT<false>, PACK8>();
+    case kTiledT4: return tiled_ptr<KTokT<true, 1>, VTokT<true>, PACK8>();
+    case kTiledT4g16: return tiled_ptr<KTokT<true, 2>, VTokT<true>, PACK8>();
     case kTiledKivi: return tiled_ptr<KKiviT, VKiviRowT, PACK8>();
     default: return nullptr;
   }

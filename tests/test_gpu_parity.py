@@ -425,6 +425,72 @@ def test_decode_int4_packed_parity(B, Hq, Hkv, S, ctx):
     assert_close(out_u, ref, f"int4 unpacked B{B} S{S}")
 
 
+@pytest.mark.parametrize("bits,G,B,Hq,Hkv,S,ctx,static", [
+    (8, 8, 3, 12, 2, 700, [700, 37, 0], False),        # groups of 16, an empty row
+    (8, 1, 2, 28, 4, 1000, [1000, 999], False),        # groups of 128 (int8_baseline)
+    (8, 4, 2, 32, 2, 513, [1, 513], False),            # 16 query heads per kv head
+    (4, 8, 4, 12, 2, 8192, [8192, 8191, 4097, 33], False),  # int4_fused: groups of 16, fp32
+    (4, 4, 2, 40, 8, 300, [300, 64], False),           # groups of 32 (int4_baseline), GQA 5
+    (4, 2, 3, 6, 1, 257, [1, 0, 257], False),          # groups of 64
+    (4, 8, 2, 28, 4, 1000, [1000, 555], True),         # a static fp32 table (stride-0 view)
+])
+def test_decode_per_token_scales_tiled(bits, G, B, Hq, Hkv, S, ctx, static):
+    """Per-token scales (INT8 with fp16, packed INT4 with fp32 scales, the engines' dtypes):
+    the tiled kernel against the oracle, with per-head inverse temperature.  Scales of the
+    tokens past each row's context are NaN, as unwritten cache memory may be."""
+    K = _lib()
+    g = gen(1000 * bits + 10 * G + S)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+    lo = -127 if bits == 8 else -7
+    kc = torch.randint(lo, -lo + 1, (B, Hkv, S, 128), generator=g, dtype=torch.int8)
+    vc = torch.randint(lo, -lo + 1, (B, Hkv, S, 128), generator=g, dtype=torch.int8)
+    sdt = torch.float16 if bits == 8 else torch.float32
+    amp = 0.01 if bits == 8 else 0.3
+    if static:
+        kt = (torch.rand(Hkv, G, generator=g) * amp + 1e-3).to(sdt)
+        vt = (torch.rand(Hkv, G, generator=g) * amp + 1e-3).to(sdt)
+        ks = kt[None, :, None, :].expand(B, Hkv, S, G)
+        vs = vt[None, :, None, :].expand(B, Hkv, S, G)
+    else:
+        ks = (torch.rand(B, Hkv, S, G, generator=g) * amp + 1e-3).to(sdt)
+        vs = (torch.rand(B, Hkv, S, G, generator=g) * amp + 1e-3).to(sdt)
+        for b, c in enumerate(ctx):
+            ks[b, :, c:] = float("nan")
+            vs[b, :, c:] = float("nan")
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    sm = 1 / math.sqrt(128)
+    qs = OA.prescale_q(q, tau)
+    d = lambda x: x.to(DEV)
+    from llm_kvcache_quantization_amd import _capi as C
+    from llm_kvcache_quantization_amd.kernels import DecodePlan, kv_view_tok
+
+    if bits == 8:
+        ref = OA.decode_attn_int8_torch_ref(qs, kc, vc, ks, vs, cl, sm)
+        kx, vx, fmt = kc, vc, C.KVQ_FMT_INT8_SYM
+    else:
+        kx, vx, fmt = OQ.pack_int4(kc), OQ.pack_int4(vc), C.KVQ_FMT_INT4_SYM
+        ref = OA.decode_attn_int4_torch_ref(qs, kx, vx, ks, vs, cl, sm)
+    # the engines' call (fp32 INT4 scales are rounded to fp16 in the kernel, as the
+    # reference casts them before its kernel)
+    if static:  # stride 0 over b and t on the device too
+        ksd = kt.to(DEV)[None, :, None, :].expand(B, Hkv, S, G)
+        vsd = vt.to(DEV)[None, :, None, :].expand(B, Hkv, S, G)
+    else:
+        ksd, vsd = d(ks), d(vs)
+    plan = DecodePlan(d(q), fmt, kv_view_tok(d(kx), ksd), fmt, kv_view_tok(d(vx), vsd), d(cl),
+                      Hkv, S, sm, 128 // G, inv_tau=d(tau))
+    out = plan.launch().clone()
+    assert torch.equal(out, plan.launch()), "repeated launches differ"
+    assert_close(out, ref, f"per-token int{bits} G{G} B{B} Hq{Hq} Hkv{Hkv} S{S} static={static}")
+    if bits == 8 and not static:  # the public entry point takes the same kernel
+        pub = K.decode_attn_int8(d(qs), d(kc), d(vc), d(ks), d(vs), d(cl), sm_scale=sm)
+        assert_close(pub, ref, f"decode_attn_int8 per-token G{G}")
+    for b, c in enumerate(ctx):
+        if c == 0:
+            assert torch.all(out[b] == 0)
+
+
 def _asym_case(cfg_idx, B, S, ctx, seed, outliers=True):
     from llm_kvcache_quantization_amd import synthetic as SY
 
