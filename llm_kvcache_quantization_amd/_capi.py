@@ -194,6 +194,14 @@ def check(rc: int) -> None:
         raise KvqError(rc, msg)
 
 
+# torch's raw current-stream getter: a few hundred ns, where torch.cuda.current_stream(...)
+# builds a Stream object (a few microseconds per decode call)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
     """hipStream_t of torch's current stream on ``device`` (as an int)."""
+    idx = device.index
+    if _raw_stream is not None and idx is not None:
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream

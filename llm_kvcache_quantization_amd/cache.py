@@ -97,6 +97,7 @@ class _EngineBase:
             raise ValueError(f"num_layers must be > 0, got {num_layers}")
         self.num_layers = num_layers
         self.device = device
+        self._dev_type = torch.device(device).type
         self.max_seq_len = int(max_seq_len) if max_seq_len is not None else None
         if self.max_seq_len is not None and self.max_seq_len <= 0:
             raise ValueError(f"max_seq_len must be > 0, got {self.max_seq_len}")
@@ -168,12 +169,12 @@ class _EngineBase:
             raise ValueError(f"k must be 4D [B,H,S,D], got ndim={k.ndim}")
         if v.ndim != 4:
             raise ValueError(f"v must be 4D [B,H,S,D], got ndim={v.ndim}")
-        if tuple(k.shape) != tuple(v.shape):
+        if k.shape != v.shape:
             raise ValueError(f"k/v shape mismatch: k={tuple(k.shape)} vs v={tuple(v.shape)}")
-        target = torch.device(self.device)
-        if k.device.type != target.type or v.device.type != target.type:
+        if k.device.type != self._dev_type or v.device.type != self._dev_type:
             raise ValueError(
-                f"Device mismatch: cache_device={target}, k.device={k.device}, v.device={v.device}")
+                f"Device mismatch: cache_device={torch.device(self.device)}, k.device={k.device}, "
+                f"v.device={v.device}")
         if not k.is_cuda:
             raise ValueError("the HIP cache engines need GPU (ROCm) tensors")
         if k.dtype != torch.float16 or v.dtype != torch.float16:
@@ -410,8 +411,10 @@ class _SymCacheBase(_EngineBase):
             if nbytes:
                 scratch = torch.empty(nbytes, dtype=torch.uint8, device=codes.device)
                 p.scratch, p.scratch_bytes = scratch.data_ptr(), nbytes
-            # keep the (possibly temporary) tensors alive until the launch returns
-            p._keep = (xs, st, scratch)
+            # keep the (possibly temporary) tensors alive until the launch returns; _keep_fixed
+            # is what a reused block must keep (the table and the rescue scratch)
+            p._keep_fixed = (st, scratch)
+            p._keep = (xs,) + p._keep_fixed
         return pk, pv
 
     def _pre_append_checks(self, layer_id: int) -> None:
@@ -426,12 +429,12 @@ class _SymCacheBase(_EngineBase):
 
     def _step_for(self, layer_id: int, q_heads: int):
         """The layer's LayerStep (kernels.LayerStep) over its whole buffers."""
-        from .kernels import LayerStep, kv_view_tok
-
         kb = self._k_cache[layer_id]
         st = self._steps[layer_id]
         if st is not None and st.key == (q_heads, kb.data_ptr()):
             return st
+        from .kernels import LayerStep, kv_view_tok
+
         B, H, cap = kb.shape[0], kb.shape[1], kb.shape[2]
         kc, vc, ks, vs = self._raw_views(layer_id, cap)
         st = LayerStep(self._fmt, kv_view_tok(kc, ks), self._fmt, kv_view_tok(vc, vs), B, q_heads, H,
@@ -441,26 +444,27 @@ class _SymCacheBase(_EngineBase):
         return st
 
     def _fused_apps(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status):
-        """The fused step's kvq_append_params of K and V (built once per layer buffers;
-        per call the rows, the slot and the status words change)."""
+        """The decode step's kvq_append_params of K and V for one new token (built once per
+        layer buffers; per call the rows, the slot and the status words change)."""
         B, H, S, D = k.shape
         ent = self._apps[layer_id]
-        if ent is None:
+        if ent is None or ent[2] != (B, H):
             G = D // self.group_size
             sk = self._static_for("k", layer_id, H, G)
             sv = self._static_for("v", layer_id, H, G)
             pk, pv = self._append_params(layer_id, k, v, pos, None, sk, sv)
-            ent = (pk, pv, sk, sv)
+            ent = (pk, pv, (B, H))
             self._apps[layer_id] = ent
         pk, pv = ent[0], ent[1]
-        for side, p, x in (("k", pk, k), ("v", pv, v)):
+        sptr = None if status is None else status.data_ptr()
+        for p, x, off in ((pk, k, 0), (pv, v, 8)):
             if x.stride(-1) != 1:
                 x = x.contiguous()
             p.x = x.data_ptr()
-            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride(0), x.stride(1), x.stride(2)
+            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride()[:3]
             p.write_pos = pos
-            p.status = None if status is None else status.data_ptr() + (0 if side == "k" else 8)
-            p._keep = (x, ent[2], ent[3])
+            p.status = None if sptr is None else sptr + off
+            p._keep = (x,) + p._keep_fixed
         return pk, pv
 
     def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
@@ -489,20 +493,26 @@ class _SymCacheBase(_EngineBase):
             q = q.contiguous()
         if sm_scale is None:
             sm_scale = 1.0 / math.sqrt(D)
-        if not self._fused_step_ok(D):
-            self.append(layer_id, k, v)
-            n = self._layer_seq_lens[layer_id]
-            return self._step_for(layer_id, q.shape[1]).attend(q, n, sm_scale, inv_tau)
+        if D % self.group_size:
+            raise ValueError(f"head_dim {D} must be divisible by group_size {self.group_size}")
         G = D // self.group_size
         self._pre_append_checks(layer_id)
         old = self._layer_seq_lens[layer_id]
         n = old + 1
         self._ensure_capacity(layer_id, B, H, D, G, n)
         status = self._status_buf(k.device) if self.check_numerics else None
+        # the append's parameter blocks are kept per layer (as ``append`` would build them)
         pk, pv = self._fused_apps(layer_id, k, v, old, status)
-        out = self._step_for(layer_id, q.shape[1]).append_attend(q, n, sm_scale, inv_tau, pk, pv)
-        if status is not None:
-            self._check_status(layer_id, k.numel(), self._kind, self._qrange)
+        step = self._step_for(layer_id, q.shape[1])
+        if self._fused_step_ok(D):
+            out = step.append_attend(q, n, sm_scale, inv_tau, pk, pv)
+            if status is not None:
+                self._check_status(layer_id, k.numel(), self._kind, self._qrange)
+        else:
+            self._launch_append(pk, pv, k.device)
+            if status is not None:
+                self._check_status(layer_id, k.numel(), self._kind, self._qrange)
+            out = step.attend(q, n, sm_scale, inv_tau)
         self._layer_seq_lens[layer_id] = n
         if layer_id == 0:
             self._seq_len = n
@@ -907,12 +917,12 @@ class _StaticG32Cache(_EngineBase):
 
     def _step_for(self, layer_id: int, q_heads: int):
         """The layer's LayerStep (kernels.LayerStep) over its whole buffers."""
-        from .kernels import LayerStep, kv_view_static
-
         kb = self._k[layer_id]
         st = self._steps[layer_id]
         if st is not None and st.key == (q_heads, kb.data_ptr()):
             return st
+        from .kernels import LayerStep, kv_view_static
+
         B, H, cap = kb.shape[0], kb.shape[1], kb.shape[2]
         kfmt, kview = self._k_view(layer_id, cap)
         vb = self._v[layer_id]
@@ -958,13 +968,14 @@ class _StaticG32Cache(_EngineBase):
             ent = (pk, pv)
             self._apps[layer_id] = ent
         pk, pv = ent
-        for side, p, x in (("k", pk, k), ("v", pv, v)):
+        sptr = None if status is None else status.data_ptr()
+        for p, x, off in ((pk, k, 0), (pv, v, 8)):
             if x.stride(-1) != 1:
                 x = x.contiguous()
             p.x = x.data_ptr()
-            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride(0), x.stride(1), x.stride(2)
+            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride()[:3]
             p.write_pos = old
-            p.status = None if status is None else status.data_ptr() + (0 if side == "k" else 8)
+            p.status = None if sptr is None else sptr + off
             p._keep = (x,)
         out = self._step_for(layer_id, q.shape[1]).append_attend(q, n, sm_scale, inv_tau, pk, pv)
         if status is not None:
@@ -1218,13 +1229,13 @@ class KIVIStyleKVCache(_EngineBase):
 
     def _step_for(self, layer_id: int, q_heads: int):
         """The layer's LayerStep over its whole buffers and its frozen K parameters."""
-        from .kernels import LayerStep, kv_view_kivi
-
         kc, ks = self._k_cache[layer_id], self._k_scale[layer_id]
         key = (q_heads, kc.data_ptr(), ks.data_ptr())
         st = self._steps[layer_id]
         if st is not None and st.key == key:
             return st
+        from .kernels import LayerStep, kv_view_kivi
+
         B, H = kc.shape[0], kc.shape[1]
         vc, vs, vz, kz = self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id], \
             self._k_zp[layer_id]

@@ -32,6 +32,9 @@ int fail(int code, const std::string& msg);
 
 constexpr int kAppendWaves = 4;
 constexpr int kRescueMax = 4096;  // (rows x groups) handled by the single-work-group rescue path
+constexpr int kRowBatch = 8;      // rows per wave loaded at once on that path
+constexpr int kTopWalk = 32;      // that path walks down from the maximum when the quantile's
+                                  // ranks lie within kTopWalk of the top; else it sorts
 
 struct AppendDev {
   int valid;
@@ -109,7 +112,35 @@ __device__ __forceinline__ float quantile_lerp(float a, float b, float w) {
 // src/quant/int4_basic.py:84-90): every value's rank in the group (ties broken by channel
 // index) selects the order statistics at floor / ceil of fp32(q) * (gs - 1), which are
 // interpolated by quantile_lerp.  The group's lanes all return the result.
+__device__ __forceinline__ int group_sum(int v, int gs) {
+  for (int o = 1; o < gs / 2; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 __device__ float group_quantile(float a0, float a1, int gs, float q, int lane) {
+  {
+    // Near the top (the reference's 99.9 percentile over groups of up to 128 takes the two
+    // largest values) the order statistics come from walking the distinct values down from
+    // the maximum: value m with multiplicity c holds the ranks [gs - above - c, gs - above),
+    // `above` counting the values already passed.  ktop + 1 steps reach rank lo.
+    const float rank = q * (float)(gs - 1);
+    const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
+    const int ktop = gs - 1 - lo;
+    if (ktop < 4) {
+      float t = __builtin_inff(), vlo = 0.f, vhi = 0.f;
+      int above = 0;
+      for (int it = 0; it <= ktop; ++it) {
+        const float m = group_max(fmaxf(a0 < t ? a0 : -1.0f, a1 < t ? a1 : -1.0f), gs);
+        const int c = group_sum((int)(a0 == m) + (int)(a1 == m), gs);
+        const int r0 = gs - above - c, r1 = gs - above;  // ranks [r0, r1) hold m
+        if (lo >= r0 && lo < r1) vlo = m;
+        if (hi >= r0 && hi < r1) vhi = m;
+        above += c;
+        t = m;
+      }
+      return quantile_lerp(vlo, vhi, rank - (float)lo);
+    }
+  }
   const int nl = gs >> 1;
   const int base = lane & ~(nl - 1);
   const int e0 = 2 * (lane - base), e1 = e0 + 1;
@@ -132,9 +163,9 @@ __device__ float group_quantile(float a0, float a1, int gs, float q, int lane) {
 
 // Scale of group g for a row, before the per-format final clamp.
 //  dyn_abs: absmax of the group's fp16 values (as float)
-__device__ __forceinline__ float int4_scale(const AppendDev& a, int h, int g, float dyn_abs,
-                                            float thr) {
-  float s = fmaxf(ld_static(a, h, g), 1e-5f);                 // int4_cache.py:342
+//  stv: the static scale of the group (ld_static)
+__device__ __forceinline__ float int4_scale(const AppendDev& a, float stv, float dyn_abs, float thr) {
+  float s = fmaxf(stv, 1e-5f);                                 // int4_cache.py:342
   const float dyn = __fdiv_rn(fmaxf(dyn_abs, 1e-5f), 7.0f);   // int4_cache.py:358
   if (a.adaptive) s = fmaxf(s * a.margin, dyn);                // :451-455
   if (a.mixed) s = fmaxf(s, dyn);                              // :457-458
@@ -144,7 +175,9 @@ __device__ __forceinline__ float int4_scale(const AppendDev& a, int h, int g, fl
 }
 
 // dyn_abs: the group's absmax, or with a percentile its fp32 quantile of |x|
-__device__ __forceinline__ half_t int8_scale16(const AppendDev& a, int h, int g, float dyn_abs) {
+// dyn_abs: the group's absmax, or with a percentile its fp32 quantile of |x|; stv: the static
+// scale of the group (ld_static; unused without a static table)
+__device__ __forceinline__ half_t int8_scale16(const AppendDev& a, float stv, float dyn_abs) {
   if (a.st == nullptr) {
     // dynamic path: the fp16 absmax clamped in fp16 (int8_basic.py:85, :91-92), or the fp32
     // quantile clamped in fp32 then rounded to fp16 (:78-83, :91-92); then abs_max / 127 in
@@ -153,7 +186,7 @@ __device__ __forceinline__ half_t int8_scale16(const AppendDev& a, int h, int g,
                                  : (half_t)fmaxf(dyn_abs, (float)(half_t)1e-5f);
     return (half_t)__fdiv_rn((float)am, 127.0f);
   }
-  float s = ld_static(a, h, g);
+  float s = stv;
   if (a.adaptive) {
     s = fmaxf(s, 1e-5f) * a.margin;                            // int8_cache.py:326,398
     const float dyn = __fdiv_rn(fmaxf(dyn_abs, 1e-5f), 127.0f);  // :348
@@ -270,13 +303,30 @@ __global__ void rescue_thr_kernel(RescueScratch* s, float q, int64_t n) {
   s->thr = quantile_lerp(va, vb, w);
 }
 
-__device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
+// the lane's two input values of append row `row` (row = (b * H + h) * S + s)
+__device__ __forceinline__ const half_t* row_x(const AppendDev& a, int row) {
+  const int s_idx = row % a.S, bh = row / a.S, h = bh % a.H, b = bh / a.H;
+  return a.x + (int64_t)b * a.xsb + (int64_t)h * a.xsh + (int64_t)s_idx * a.xss;
+}
+__device__ __forceinline__ half2v load_x(const AppendDev& a, int row, int lane) {
+  return *reinterpret_cast<const half2v*>(row_x(a, row) + 2 * lane);
+}
+
+// the static scale of the lane's group in append row `row` (0 without a static table)
+__device__ __forceinline__ float row_static(const AppendDev& a, int row, int lane) {
+  if (a.st == nullptr || a.fmt == KVQ_FMT_INT4_ASYM || a.fmt == KVQ_FMT_INT4_KIVI) return 0.f;
+  return ld_static(a, (row / a.S) % a.H, (2 * lane) / a.gs);
+}
+
+// Quantizes append row `row` whose lane values xv (and static scale stv, row_static) were
+// loaded by the caller.
+__device__ void quant_row_x(const AppendDev& a, int row, int lane, float thr, half2v xv,
+                            float stv) {
   const int s_idx = row % a.S;
   const int bh = row / a.S;
   const int h = bh % a.H, b = bh / a.H;
   const int64_t t = a.wpos + s_idx;
-  const half_t* xr = a.x + (int64_t)b * a.xsb + (int64_t)h * a.xsh + (int64_t)s_idx * a.xss;
-  const half2v xv = *reinterpret_cast<const half2v*>(xr + 2 * lane);
+  const half_t* xr = row_x(a, row);
   const float x0 = (float)xv.x, x1 = (float)xv.y;
   const int d0 = 2 * lane;
   const int g = d0 / a.gs;
@@ -295,7 +345,7 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
   int clipped = 0;
 
   if (a.fmt == KVQ_FMT_INT8_SYM) {
-    const half_t s16 = int8_scale16(a, h, g, am);
+    const half_t s16 = int8_scale16(a, stv, am);
     const float sf = (float)s16;
     *reinterpret_cast<uint16_t*>(crow + d0) = int8_pack_pair(x0, x1, s16, clipped);
     // the clip statistic is the static-scale path's (int8_cache.py:401-419)
@@ -312,7 +362,7 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
       // in fp32 (int4_basic.py:84-99)
       s = __fdiv_rn(pct ? fmaxf(am, 1e-5f) : fmaxf(am, (float)(half_t)1e-5f), 7.0f);
     } else {
-      s = int4_scale(a, h, g, am, thr);
+      s = int4_scale(a, stv, am, thr);
     }
     const float q0 = fminf(fmaxf(rintf(__fdiv_rn(x0, s)), -7.f), 7.f);
     const float q1 = fminf(fmaxf(rintf(__fdiv_rn(x1, s)), -7.f), 7.f);
@@ -377,6 +427,10 @@ __device__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
   if (lane == 0 && a.status && clipped) atomicAdd(&a.status[1], clipped);
 }
 
+__device__ __forceinline__ void quant_row(const AppendDev& a, int row, int lane, float thr) {
+  quant_row_x(a, row, lane, thr, load_x(a, row, lane), row_static(a, row, lane));
+}
+
 // Bitonic sort of n_pad (power of two) floats in LDS, ascending.
 __device__ void lds_bitonic_sort(float* v, int n_pad) {
   for (int k = 2; k <= n_pad; k <<= 1) {
@@ -397,6 +451,42 @@ __device__ void lds_bitonic_sort(float* v, int n_pad) {
   }
 }
 
+// torch.quantile of the n floats v[0, n) (LDS, one work-group) when the ranks lo <= hi lie
+// near the top (n - 1 - lo < kTopWalk): the distinct values are walked down from the maximum
+// (value m with multiplicity c holds the ranks [n - above - c, n - above)); w = rank - lo.
+// Every thread returns the result.
+__device__ float lds_top_quantile(const float* v, int n, int lo, int hi, float w) {
+  __shared__ float red_m[kAppendWaves];
+  __shared__ int red_c[kAppendWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float t = __builtin_inff(), vlo = 0.f, vhi = 0.f;
+  int above = 0;
+  for (int it = 0; it < kTopWalk && above <= n - 1 - lo; ++it) {
+    float m = -1.0f;  // the scales are positive
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+      if (v[i] < t) m = fmaxf(m, v[i]);
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (lane == 0) red_m[wave] = m;
+    __syncthreads();
+    m = red_m[0];
+    for (int i = 1; i < kAppendWaves; ++i) m = fmaxf(m, red_m[i]);
+    int c = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) c += v[i] == m;
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+    if (lane == 0) red_c[wave] = c;
+    __syncthreads();
+    c = 0;
+    for (int i = 0; i < kAppendWaves; ++i) c += red_c[i];
+    const int r0 = n - above - c, r1 = n - above;
+    if (lo >= r0 && lo < r1) vlo = m;
+    if (hi >= r0 && hi < r1) vhi = m;
+    above += c;
+    t = m;
+    __syncthreads();  // red_m / red_c are rewritten by the next step
+  }
+  return quantile_lerp(vlo, vhi, w);
+}
+
 // torch.quantile(x, q) with linear interpolation, float32 arithmetic:
 // rank = fp32(q) * (n - 1); lo = floor(rank); hi = ceil(rank); w = rank - lo;
 // quantile_lerp(v[lo], v[hi], w)
@@ -415,27 +505,69 @@ __global__ __launch_bounds__(kAppendWaves * 64) void append_kernel(AppendDev k, 
   float thr = a.thr_ptr ? *a.thr_ptr : 0.f;
   if (rescue && a.fmt == KVQ_FMT_INT4_SYM && a.st != nullptr && a.rq > 0.f && !a.rescue_all) {
     // Global threshold over every (row, group) dynamic scale of this append
-    // (int4_cache.py:384-389).  Single work-group: grid.x == 1 on this path.
+    // (int4_cache.py:384-389).  Single work-group: grid.x == 1 on this path.  Each wave
+    // handles rows wave, wave + 8, ..: kRowBatch of them loaded at once, so one memory
+    // latency covers the batch; the values stay in registers for the quantization.
     __shared__ float dyn[kRescueMax];
     __shared__ float thr_sh;
     const int G = 128 / a.gs;
     const int n = rows * G;
     int n_pad = 1;
     while (n_pad < n) n_pad <<= 1;
-    for (int i = threadIdx.x; i < n_pad; i += blockDim.x) dyn[i] = __builtin_inff();
+    const float rank = a.rq * (float)(n - 1);
+    const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
+    const bool top = n - 1 - lo < kTopWalk;
+    if (!top)
+      for (int i = threadIdx.x; i < n_pad; i += blockDim.x) dyn[i] = __builtin_inff();
     __syncthreads();
-    for (int row = wave; row < rows; row += kAppendWaves) {
-      const int s_idx = row % a.S, bh = row / a.S, h = bh % a.H, b = bh / a.H;
-      const half_t* xr = a.x + (int64_t)b * a.xsb + (int64_t)h * a.xsh + (int64_t)s_idx * a.xss;
-      const half2v xv = *reinterpret_cast<const half2v*>(xr + 2 * lane);
-      const float am = group_max(fmaxf(fabsf((float)xv.x), fabsf((float)xv.y)), a.gs);
-      if ((2 * lane) % a.gs == 0) dyn[row * G + (2 * lane) / a.gs] = __fdiv_rn(fmaxf(am, 1e-5f), 7.0f);
+    half2v xb[kRowBatch];
+    float sb[kRowBatch];  // the rows' static scales (loaded with them)
+    const bool cached = rows <= kRowBatch * kAppendWaves;  // every row of the wave in xb
+    for (int r0 = wave; r0 < rows; r0 += kRowBatch * kAppendWaves) {
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        const int row = r0 + u * kAppendWaves;
+        if (row < rows) {
+          xb[u] = load_x(a, row, lane);
+          sb[u] = row_static(a, row, lane);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        const int row = r0 + u * kAppendWaves;
+        if (row >= rows) break;
+        const float am = group_max(fmaxf(fabsf((float)xb[u].x), fabsf((float)xb[u].y)), a.gs);
+        if ((2 * lane) % a.gs == 0) dyn[row * G + (2 * lane) / a.gs] = __fdiv_rn(fmaxf(am, 1e-5f), 7.0f);
+      }
     }
     __syncthreads();
-    lds_bitonic_sort(dyn, n_pad);
-    if (threadIdx.x == 0) thr_sh = sorted_quantile(dyn, n, a.rq);
+    if (top) {
+      const float t = lds_top_quantile(dyn, n, lo, hi, rank - (float)lo);
+      if (threadIdx.x == 0) thr_sh = t;
+    } else {
+      lds_bitonic_sort(dyn, n_pad);
+      if (threadIdx.x == 0) thr_sh = sorted_quantile(dyn, n, a.rq);
+    }
     __syncthreads();
     thr = thr_sh;
+    for (int r0 = wave; r0 < rows; r0 += kRowBatch * kAppendWaves) {
+      if (!cached) {
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) {
+          const int row = r0 + u * kAppendWaves;
+          if (row < rows) {
+            xb[u] = load_x(a, row, lane);
+            sb[u] = row_static(a, row, lane);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        const int row = r0 + u * kAppendWaves;
+        if (row < rows) quant_row_x(a, row, lane, thr, xb[u], sb[u]);
+      }
+    }
+    return;
   }
   for (int row = blockIdx.x * kAppendWaves + wave; row < rows; row += gridDim.x * kAppendWaves)
     quant_row(a, row, lane, thr);

@@ -282,8 +282,13 @@ class LayerStep:
         self.params = p
         self._pp = ctypes.byref(p)
         self.device = torch.device(device)
+        if self.device.index is None:
+            self.device = torch.device(self.device.type, torch.cuda.current_device())
         self.workspace: Optional[torch.Tensor] = None
         self._tau = None
+        # the workspace a call needs depends on the context length only through its 32-token
+        # tile count (chunk sizes are multiples of 32 tokens): asked again when that changes
+        self._ws_tiles = -1
 
     def _prepare(self, q: torch.Tensor, n: int, sm_scale: float,
                  inv_tau: Optional[torch.Tensor]) -> torch.Tensor:
@@ -295,14 +300,16 @@ class LayerStep:
         p.capacity = n
         p.context_len = n
         p.sm_scale = float(sm_scale)
-        L = C.lib()
-        need = int(L.kvq_decode_workspace_bytes(self._pp))
-        if self.workspace is None or self.workspace.numel() < need:
-            # zero-filled when (re)allocated: the merge counters at its start must be zero
-            self.workspace = torch.zeros(max(need, int(need * 1.25)), dtype=torch.uint8,
-                                         device=self.device)
-            p.workspace = self.workspace.data_ptr()
-            p.workspace_bytes = self.workspace.numel()
+        tiles = (n + 31) >> 5
+        if tiles != self._ws_tiles:
+            need = int(C.lib().kvq_decode_workspace_bytes(self._pp))
+            if self.workspace is None or self.workspace.numel() < need:
+                # zero-filled when (re)allocated: the merge counters at its start must be zero
+                self.workspace = torch.zeros(max(need, int(need * 1.25)), dtype=torch.uint8,
+                                             device=self.device)
+                p.workspace = self.workspace.data_ptr()
+                p.workspace_bytes = self.workspace.numel()
+            self._ws_tiles = tiles
         out = torch.empty_like(q)
         p.out = out.data_ptr()
         p.out_stride_b, p.out_stride_h = out.stride(0), out.stride(1)

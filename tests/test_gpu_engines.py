@@ -82,14 +82,21 @@ def _kv(B, H, S, g, scale=1.0, outliers=True):
 
 
 @pytest.mark.parametrize("bits", [8, 4])
-@pytest.mark.parametrize("percentile,gs", [(99.9, 128), (99.5, 16), (99.0, 32), (99.9, 64), (100.0, 32)])
-def test_dynamic_percentile_append_bitexact(bits, percentile, gs):
+@pytest.mark.parametrize("percentile,gs,ties", [
+    (99.9, 128, False), (99.5, 16, False), (99.0, 32, False), (99.9, 64, False), (100.0, 32, False),
+    (99.9, 128, True),   # equal values at the top of the groups
+    (90.0, 128, False),  # ranks far from the top (the rank-count path)
+    (97.0, 64, True),
+])
+def test_dynamic_percentile_append_bitexact(bits, percentile, gs, ties):
     K = _k()
-    print(f"[case] bits={bits} p={percentile} gs={gs}", flush=True)
-    g = gen(int(percentile * 10) + gs + bits)
+    print(f"[case] bits={bits} p={percentile} gs={gs} ties={ties}", flush=True)
+    g = gen(int(percentile * 10) + gs + bits + ties)
     B, H = 2, 2
     k0, v0 = _kv(B, H, 37, g)
     k1, v1 = _kv(B, H, 1, g)
+    if ties:  # few distinct magnitudes, so the largest ones repeat within a group
+        k0, v0, k1, v1 = [(x * 2).round().div(2).to(torch.float16) for x in (k0, v0, k1, v1)]
     Cache = K.INT8KVCache if bits == 8 else K.INT4KVCache
     cache = Cache(1, device=DEV, clip_percentile=percentile, group_size=gs)
     cache.append(0, k0.to(DEV), v0.to(DEV))

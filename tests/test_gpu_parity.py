@@ -154,6 +154,10 @@ def test_append_int4_sym_bitexact(mode, S):
     (1, 2, 600, 0.3, True),       # 4,800 scales, many equal (ties at the threshold)
     (4, 2, 4096, 0.001, False),   # 131,072 scales, a threshold in the far tail
     (2, 2, 256, 0.05, False),     # 4,096 scales: the one-work-group sort path
+    (8, 4, 1, 0.01, False),       # a decode step (128 scales): the walk from the top
+    (16, 4, 1, 0.01, True),       # 64 rows (reloaded for the quantization), ties
+    (8, 4, 1, 0.1, False),        # 13 ranks below the top
+    (4, 2, 16, 0.05, True),       # 512 scales, 26 ranks below the top, ties
 ])
 def test_append_int4_rescue_large_bitexact(B, H, S, ratio, ties):
     """INT4 group outlier rescue over the dynamic scales of a prefill-sized append: the
@@ -169,7 +173,7 @@ def test_append_int4_rescue_large_bitexact(B, H, S, ratio, ties):
     if ties:  # few distinct group absmax values
         k = (k * 4).round().div(4).to(torch.float16)
         v = (v * 2).round().div(2).to(torch.float16)
-    k[0, 1, 7, 70] = 25.0
+    k[0, 1, min(7, S - 1), 70] = 25.0
     st = torch.rand(H, D // gs, generator=g) * 0.3 + 0.1
     cache = K.INT4KVCache(1, device=DEV, group_size=gs, static_k_scale=st[None],
                           static_v_scale=(st * 0.8)[None], check_numerics=False,
