@@ -27,6 +27,7 @@ from .cache import (  # noqa: F401
     INT8KVCache,
     K8V4KVCache,
     KIVIStyleKVCache,
+    MixedKVCache,
 )
 from .patch import (  # noqa: F401
     INT8CacheWrapper,
@@ -50,6 +51,7 @@ __all__ = [
     "INT4AsymKVCache",
     "K8V4KVCache",
     "KIVIStyleKVCache",
+    "MixedKVCache",
     "decode_attn_int4_kivi",
     "decode_attn_int4_asym_v2",
     "decode_attn_int4_asym_gqa",

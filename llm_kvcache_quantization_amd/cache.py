@@ -1311,6 +1311,278 @@ class KIVIStyleKVCache(_EngineBase):
         return total / (1024 * 1024)
 
 
+_MIXED_BITS = {4, 8, 16}
+
+
+class MixedKVCache(_EngineBase):
+    """The reference's K/V mixed-precision cache (src/cache/mixed_kv_cache.py:35-330) with
+    its default bit widths: K INT8 symmetric per group with a dynamic percentile-clipped
+    scale (src/quant/int8_basic.py:18-108), V INT4 asymmetric per token
+    (src/quant/asymmetric_quant.py:246-270).  The buffers are preallocated and grow by
+    doubling (the reference concatenates per append).  Per layer:
+
+    * K codes int8 [B, H, cap, 128] and fp16 scales [B, H, cap, G] (the reference keeps the
+      same fp16-valued scales as fp32);
+    * V codes as packed nibbles [B, H, cap, 64] (byte = ((c[2i]+8) << 4) | (c[2i+1]+8); the
+      reference keeps one code per byte) with fp32 scale / zero-point [B, H, cap].
+
+    Both sides of an append are one kvq_quant_append launch (K INT8_SYM dynamic, V INT4_KIVI
+    per token); decode attention reads the cache in place (the tiled kernel for INT8 K with
+    per-token scales and KIVI-layout V).  Built: k_bits 8 and v_bits 4 on every layer,
+    v_percentile 100; the fp16 and other ablation widths of the reference raise
+    NotImplementedError.
+    """
+
+    _min_capacity = 256
+
+    def __init__(self, num_layers: int, device: str = "cuda", dtype: torch.dtype = torch.float16,
+                 max_seq_len: Optional[int] = None, k_group_size: int = 128,
+                 v_group_size: Optional[int] = None, k_clip_percentile: float = 99.9,
+                 v_percentile: float = 100.0, k_bits: int = 8, v_bits: int = 4,
+                 per_layer_bits: Optional[List[Tuple[int, int]]] = None,
+                 decode_attn_impl: str = "torch_ref", check_numerics: bool = True):
+        if num_layers <= 0:
+            raise ValueError(f"num_layers must be > 0, got {num_layers}")
+        if k_bits not in _MIXED_BITS:
+            raise ValueError(f"k_bits must be one of {_MIXED_BITS}, got {k_bits}")
+        if v_bits not in _MIXED_BITS:
+            raise ValueError(f"v_bits must be one of {_MIXED_BITS}, got {v_bits}")
+        if per_layer_bits is not None:
+            if len(per_layer_bits) != num_layers:
+                raise ValueError(f"per_layer_bits length {len(per_layer_bits)} must equal "
+                                 f"num_layers {num_layers}")
+            for i, entry in enumerate(per_layer_bits):
+                if not isinstance(entry, (tuple, list)) or len(entry) != 2:
+                    raise ValueError(f"per_layer_bits[{i}] must be a 2-tuple (k_bits, v_bits), "
+                                     f"got {entry!r}")
+                if entry[0] not in _MIXED_BITS or entry[1] not in _MIXED_BITS:
+                    raise ValueError(f"per_layer_bits[{i}]=({entry[0]},{entry[1]}) contains "
+                                     f"unsupported bits; allowed values: {_MIXED_BITS}")
+            per_layer_bits = [(int(a), int(b)) for a, b in per_layer_bits]
+        bits = per_layer_bits or [(int(k_bits), int(v_bits))] * num_layers
+        if any(b != (8, 4) for b in bits):
+            raise NotImplementedError("MixedKVCache: only K INT8 / V INT4 layers are built "
+                                      "(the fp16 and other ablation widths are not)")
+        if float(v_percentile) != 100.0:
+            raise NotImplementedError("MixedKVCache: percentile clipping of the V parameters "
+                                      "is not built (v_percentile=100)")
+        if k_group_size not in (8, 16, 32, 64, 128):
+            raise NotImplementedError(f"k_group_size must be 8, 16, 32, 64 or 128, got {k_group_size}")
+        _dyn_quantile(k_clip_percentile)  # (0, 100]
+        self._init_common(num_layers, device, max_seq_len, decode_attn_impl, check_numerics)
+        self.dtype = dtype
+        self.k_group_size = int(k_group_size)
+        self.v_group_size = v_group_size if v_group_size is not None else k_group_size
+        self.k_clip_percentile = float(k_clip_percentile)
+        self.v_percentile = float(v_percentile)
+        self.k_bits, self.v_bits = int(k_bits), int(v_bits)
+        self._per_layer_bits = per_layer_bits
+        self.inv_tau = None
+        self.use_attn_temperature = False
+        n = num_layers
+        self._k_cache: List[Optional[Tensor]] = [None] * n
+        self._k_scale: List[Optional[Tensor]] = [None] * n
+        self._v_cache: List[Optional[Tensor]] = [None] * n
+        self._v_scale: List[Optional[Tensor]] = [None] * n
+        self._v_zp: List[Optional[Tensor]] = [None] * n
+
+    def _resolve_bits(self, layer_id: int) -> Tuple[int, int]:
+        """(k_bits, v_bits) of a layer (mixed_kv_cache.py:138-147)."""
+        if self._per_layer_bits is not None:
+            return self._per_layer_bits[layer_id]
+        return self.k_bits, self.v_bits
+
+    def _ensure(self, layer_id: int, B: int, H: int, target: int, device) -> None:
+        kc = self._k_cache[layer_id]
+        if kc is not None and (kc.shape[0] != B or kc.shape[1] != H):
+            raise ValueError(f"Inconsistent KV shape for layer {layer_id}: existing "
+                             f"K={tuple(kc.shape)}, incoming=({B}, {H}, *, 128)")
+        cap = self._layer_capacity[layer_id]
+        if kc is not None and target <= cap:
+            return
+        new_cap = self._new_capacity(layer_id, target, cap if kc is not None else 0)
+        old = self._layer_seq_lens[layer_id]
+        G = 128 // self.k_group_size
+        nk = torch.empty(B, H, new_cap, 128, dtype=torch.int8, device=device)
+        nks = torch.empty(B, H, new_cap, G, dtype=torch.float16, device=device)
+        nv = torch.empty(B, H, new_cap, 64, dtype=torch.int8, device=device)
+        nvs = torch.empty(B, H, new_cap, dtype=torch.float32, device=device)
+        nvz = torch.empty_like(nvs)
+        if kc is not None and old > 0:
+            nk[:, :, :old] = kc[:, :, :old]
+            nks[:, :, :old] = self._k_scale[layer_id][:, :, :old]
+            nv[:, :, :old] = self._v_cache[layer_id][:, :, :old]
+            nvs[:, :, :old] = self._v_scale[layer_id][:, :, :old]
+            nvz[:, :, :old] = self._v_zp[layer_id][:, :, :old]
+        self._k_cache[layer_id], self._k_scale[layer_id] = nk, nks
+        self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id] = nv, nvs, nvz
+        self._layer_capacity[layer_id] = new_cap
+        self._steps[layer_id] = self._apps[layer_id] = None
+
+    def _params(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status) -> Tuple:
+        """kvq_append_params of K (INT8 dynamic) and V (INT4_KIVI per token) writing at slot
+        pos; the one-token blocks of a decode step are kept per layer."""
+        S = k.shape[2]
+        ent = self._apps[layer_id] if S == 1 else None
+        if ent is None:
+            pk, pv = C.AppendParams(), C.AppendParams()
+            kc, ks = self._k_cache[layer_id], self._k_scale[layer_id]
+            vc, vs, vz = self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id]
+            _fill_append(pk, C.KVQ_FMT_INT8_SYM, k, self.k_group_size, kc, pos, None)
+            pk.dyn_quantile = _dyn_quantile(self.k_clip_percentile)
+            pk.scale_out, pk.scale_out_dtype = ks.data_ptr(), C.KVQ_DTYPE_F16
+            pk.so_stride_b, pk.so_stride_h, pk.so_stride_t, pk.so_stride_g = ks.stride()
+            _fill_append(pv, C.KVQ_FMT_INT4_KIVI, v, 32, vc, pos, None)
+            pv.scale_out, pv.zp_out, pv.scale_out_dtype = vs.data_ptr(), vz.data_ptr(), C.KVQ_DTYPE_F32
+            pv.so_stride_b, pv.so_stride_h, pv.so_stride_t = vs.stride()
+            ent = (pk, pv)
+            if S == 1:
+                self._apps[layer_id] = ent
+        pk, pv = ent
+        sptr = None if status is None else status.data_ptr()
+        for p, x, off in ((pk, k, 0), (pv, v, 8)):
+            p.x = x.data_ptr()
+            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride()[:3]
+            p.seq_new = S
+            p.write_pos = pos
+            p.status = None if sptr is None else sptr + off
+            p._keep = (x,)
+        return pk, pv
+
+    def _append(self, layer_id: int, k: Tensor, v: Tensor) -> int:
+        """Quantizes k, v [B, H, S, 128] into the layer at its length; returns the new length."""
+        self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        old = self._layer_seq_lens[layer_id]
+        if S == 0:
+            return old
+        if k.stride(-1) != 1:
+            k = k.contiguous()
+        if v.stride(-1) != 1:
+            v = v.contiguous()
+        self._ensure(layer_id, B, H, old + S, k.device)
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv = self._params(layer_id, k, v, old, status)
+        C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
+                                         ctypes.c_void_p(C.stream_handle(k.device))))
+        if status is not None:
+            st = self._read_status()
+            if st[0] & 1 or st[2] & 1:
+                raise ValueError(f"MixedKVCache append: {'K' if st[0] & 1 else 'V'} input contains "
+                                 "NaN or Inf — refusing to quantize corrupt data")
+        n = old + S
+        self._layer_seq_lens[layer_id] = n
+        self._seq_len = max(self._layer_seq_lens)
+        return n
+
+    def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
+        """Quantize and append k, v fp16 [B, H, S, 128] (mixed_kv_cache.py:191-240)."""
+        self._append(layer_id, k, v)
+
+    def _check_layer(self, layer_id: int) -> int:
+        if layer_id < 0 or layer_id >= self.num_layers:
+            raise ValueError(f"layer_id {layer_id} out of range [0, {self.num_layers})")
+        if self._k_cache[layer_id] is None:
+            raise ValueError(f"Cache for layer {layer_id} is empty")
+        return self._layer_seq_lens[layer_id]
+
+    def get_mixed_tensors(self, layer_id: int):
+        """(k_int8, k_scale16, v_packed, v_scale, v_zp) over the stored tokens."""
+        n = self._check_layer(layer_id)
+        return (self._k_cache[layer_id][:, :, :n], self._k_scale[layer_id][:, :, :n],
+                self._v_cache[layer_id][:, :, :n], self._v_scale[layer_id][:, :, :n],
+                self._v_zp[layer_id][:, :, :n])
+
+    def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
+        """Dequantised K, V in self.dtype (mixed_kv_cache.py:170-190, 242-254): K = code x
+        scale of its group, V = code x s + z of its token, in fp32, then cast."""
+        kc, ks, vp, vs, vz = self.get_mixed_tensors(layer_id)
+        k = _deq_sym(kc, ks.float()).to(self.dtype)
+        v = (_unpack(vp).float() * vs.unsqueeze(-1) + vz.unsqueeze(-1)).to(self.dtype)
+        return k, v
+
+    def _step_for(self, layer_id: int, q_heads: int):
+        kc = self._k_cache[layer_id]
+        st = self._steps[layer_id]
+        if st is not None and st.key == (q_heads, kc.data_ptr()):
+            return st
+        from .kernels import LayerStep, kv_view_kivi, kv_view_tok
+
+        B, H = kc.shape[0], kc.shape[1]
+        ks, vc, vs, vz = self._k_scale[layer_id], self._v_cache[layer_id], self._v_scale[layer_id], \
+            self._v_zp[layer_id]
+        st = LayerStep(C.KVQ_FMT_INT8_SYM, kv_view_tok(kc, ks), C.KVQ_FMT_INT4_KIVI,
+                       kv_view_kivi(vc, vs, vz, False), B, q_heads, H, self.k_group_size,
+                       kc.device, keepalive=(kc, ks, vc, vs, vz))
+        st.key = (q_heads, kc.data_ptr())
+        self._steps[layer_id] = st
+        return st
+
+    def decode_attn(self, layer_id: int, q: Tensor, sm_scale: Optional[float] = None,
+                    inv_tau: Optional[Tensor] = None) -> Tensor:
+        """Attention of q [B, Hq, 128] over the layer's cache, read in place (one HIP launch);
+        inv_tau (fp16 [Hq]) scales q in fp16 first."""
+        n = self._check_layer(layer_id)
+        if q.ndim != 3 or q.shape[-1] != 128:
+            raise ValueError(f"q must be [B, Hq, 128], got {tuple(q.shape)}")
+        dt = q.dtype
+        q16 = q if q.dtype == torch.float16 and q.stride(-1) == 1 else q.to(torch.float16).contiguous()
+        sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
+        out = self._step_for(layer_id, q.shape[1]).attend(q16, n, sm, inv_tau)
+        return out if dt == torch.float16 else out.to(dt)
+
+    def append_decode_attn(self, layer_id: int, q: Tensor, k: Tensor, v: Tensor,
+                           sm_scale: Optional[float] = None,
+                           inv_tau: Optional[Tensor] = None) -> Tensor:
+        """Decode step of one layer: the new token (k, v [B, H, 1, 128]) appended, then the
+        attention of q [B, Hq, 128] over the cache including it (two HIP launches)."""
+        if k.ndim != 4 or k.shape[2] != 1:
+            raise ValueError(f"append_decode_attn appends one token per step, got {tuple(k.shape)}")
+        n = self._append(layer_id, k, v)
+        if q.dtype != torch.float16 or q.stride(-1) != 1:
+            q = q.to(torch.float16).contiguous()
+        sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
+        return self._step_for(layer_id, q.shape[1]).attend(q, n, sm, inv_tau)
+
+    def clear(self) -> None:
+        self._layer_seq_lens = [0] * self.num_layers
+        self._seq_len = 0
+
+    def release(self) -> None:
+        n = self.num_layers
+        self._k_cache, self._k_scale = [None] * n, [None] * n
+        self._v_cache, self._v_scale, self._v_zp = [None] * n, [None] * n, [None] * n
+        self._steps, self._apps = [None] * n, [None] * n
+        self._layer_capacity = [0] * n
+        self.clear()
+
+    def get_memory_mb(self) -> float:
+        total = 0
+        for lst in (self._k_cache, self._k_scale, self._v_cache, self._v_scale, self._v_zp):
+            total += sum(t.numel() * t.element_size() for t in lst if t is not None)
+        return total / (1024 * 1024)
+
+    def to_tuple(self) -> Tuple[Tuple[Tensor, Tensor], ...]:
+        """Every layer's dequantised (k, v) (mixed_kv_cache.py:311-330)."""
+        out = []
+        for i in range(self.num_layers):
+            if self._k_cache[i] is None:
+                raise ValueError(f"Layer {i} cache is empty")
+            out.append(self.get_kv(i))
+        return tuple(out)
+
+    @classmethod
+    def from_tuple(cls, past_key_values, device: str = "cuda", **kwargs) -> "MixedKVCache":
+        cache = cls(num_layers=len(past_key_values), device=device, **kwargs)
+        for i, (k, v) in enumerate(past_key_values):
+            cache.append(i, k.to(device), v.to(device))
+        return cache
+
+    def __repr__(self) -> str:
+        return (f"MixedKVCache(num_layers={self.num_layers}, k_bits={self.k_bits}, "
+                f"v_bits={self.v_bits}, seq_len={self._seq_len}, memory={self.get_memory_mb():.2f}MB)")
+
+
 class FP16KVCache:
     """The fp16 mode's cache (src/cache/fp16_cache.py:26-366): K / V kept as they come,
     [B, H, capacity, D] per layer, capacity doubling with a copy, ``get_kv`` returning views

@@ -558,7 +558,7 @@ static const void* selected_kernel() {
 
 // (k_format, v_format, scale dtype) -> kernel family; 0 means unsupported
 enum Family { kNone = 0, kI8I8_16, kI8I8_32, kI4I4_16, kI4I4_32, kA4A4, kA4A4o, kI8A4_16, kI8A4_32,
-              kKivi };
+              kKivi, kI8Kv };
 
 static Family family(int kf, int vf, int ksf32, int vsf32, int kout) {
   if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT8_SYM && ksf32 == vsf32)
@@ -568,6 +568,7 @@ static Family family(int kf, int vf, int ksf32, int vsf32, int kout) {
   if (kf == KVQ_FMT_INT4_ASYM && vf == KVQ_FMT_INT4_ASYM) return kout ? kA4A4o : kA4A4;
   if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT4_ASYM) return ksf32 ? kI8A4_32 : kI8A4_16;
   if (kf == KVQ_FMT_INT4_KIVI && vf == KVQ_FMT_INT4_KIVI) return kKivi;  // tiled kernel only
+  if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT4_KIVI) return kI8Kv;  // tiled kernel only
   return kNone;
 }
 
@@ -620,8 +621,13 @@ static bool static_over_bt(const kvq_kv_view& v, const kvq_decode_params* p) {
 // fp16 scales or INT4_SYM with fp32 scales (the dtypes the engines store), groups of 16 or
 // more, the groups of a token contiguous.  INT8 K with groups of 16 reads two fp16 scales in
 // one 4-byte load, so its scale rows must be 4-byte aligned.
+// INT8 K with per-token fp16 scales may also pair with per-token asymmetric INT4 V in the
+// KIVI layout (the reference's MixedKVCache: K INT8 symmetric per group, V INT4 asymmetric
+// per token).
 static int tok_family(const kvq_decode_params* p) {
-  if (p->k_format != p->v_format || p->v.layout != KVQ_LAYOUT_ROWS) return kTiledNone;
+  if (p->v.layout != KVQ_LAYOUT_ROWS) return kTiledNone;
+  const bool kivi_v = p->k_format == KVQ_FMT_INT8_SYM && p->v_format == KVQ_FMT_INT4_KIVI;
+  if (p->k_format != p->v_format && !kivi_v) return kTiledNone;
   const bool i4 = p->k_format == KVQ_FMT_INT4_SYM;
   if (!i4 && p->k_format != KVQ_FMT_INT8_SYM) return kTiledNone;
   const int gs = p->group_size;
@@ -636,6 +642,11 @@ static int tok_family(const kvq_decode_params* p) {
            v.scale_stride_b % w == 0 && v.scale_stride_h % w == 0 && v.scale_stride_t % w == 0 &&
            v.scale_stride_b >= 0 && v.scale_stride_h >= 0 && v.scale_stride_t >= 0;
   };
+  if (kivi_v) {
+    // V codes in dense 64-byte rows, fp32 scale / zero-point per token (checked by check_view)
+    if (!ok(p->k) || p->v.stride_t != kD / 2 || p->v.scale_stride_t != 1) return kTiledNone;
+    return gs == 16 ? kTiledT8Kvg16 : kTiledT8Kv;
+  }
   if (!ok(p->k) || !ok(p->v)) return kTiledNone;
   if (i4) return gs == 16 ? kTiledT4g16 : kTiledT4;
   return gs == 16 ? kTiledT8g16 : kTiledT8;
@@ -898,6 +909,10 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
                 "TILE32 V needs INT4_ASYM K or INT8 K with a static group-32 scale in dense rows");
   if (fam == kKivi && !tiled)
     return fail(KVQ_ERR_UNSUPPORTED, "INT4_KIVI K and V need dense 64-byte token rows");
+  if (fam == kI8Kv && !tiled)
+    return fail(KVQ_ERR_UNSUPPORTED,
+                "INT8 K with INT4_KIVI V needs dense K rows with fp16 per-token scales (groups of "
+                "16 or more, contiguous) and dense 64-byte V rows");
   if (tiled && p->k_format == KVQ_FMT_INT4_ASYM &&
       (p->k.stride_t != kD / 2 || (p->k.n_outlier && p->k.outlier_stride_t != 4)))
     return fail(KVQ_ERR_UNSUPPORTED, "with TILE32 V, K rows and outlier rows must be dense");

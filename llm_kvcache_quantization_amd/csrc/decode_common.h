@@ -422,6 +422,8 @@ enum TiledFam {
   kTiledT8g16,  // the same with groups of 16
   kTiledT4,     // INT4_SYM K and V with per-token fp32 scales, groups of 32 .. 128, rows
   kTiledT4g16,  // the same with groups of 16
+  kTiledT8Kv,   // INT8_SYM K with per-token fp16 scales, INT4_KIVI V (per-token fp32), rows
+  kTiledT8Kvg16,  // the same with K groups of 16
   kTiledKivi,   // INT4_KIVI K (per-channel) and V (per-token), token rows
 };
 // kernel of family fam for n_rep query heads per kv head, or nullptr

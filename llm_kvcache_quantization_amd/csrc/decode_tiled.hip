@@ -1572,6 +1572,8 @@ const void* tiled_ptr_fam(int fam) {
     case kTiledT8g16: return tiled_ptr<KTokT<false, 2>, VTokT<false>, PACK8>();
     case kTiledT4: return tiled_ptr<KTokT<true, 1>, VTokT<true>, PACK8>();
     case kTiledT4g16: return tiled_ptr<KTokT<true, 2>, VTokT<true>, PACK8>();
+    case kTiledT8Kv: return tiled_ptr<KTokT<false, 1>, VKiviRowT, PACK8>();
+    case kTiledT8Kvg16: return tiled_ptr<KTokT<false, 2>, VKiviRowT, PACK8>();
     case kTiledKivi: return tiled_ptr<KKiviT, VKiviRowT, PACK8>();
     default: return nullptr;
   }

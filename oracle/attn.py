@@ -18,7 +18,7 @@ from typing import Optional
 
 import torch
 
-from .quant import dequantize_asymmetric_static, dequantize_kivi, unpack_int4
+from .quant import dequantize_asymmetric_static, dequantize_kivi, dequantize_symmetric, unpack_int4
 
 
 def prescale_q(q: torch.Tensor, inv_tau: Optional[torch.Tensor]) -> torch.Tensor:
@@ -109,6 +109,19 @@ def decode_attn_k8v4_ref(q, k_int8, k_scale16, v_packed, v_scale, v_zp, context_
     G = k_scale16.shape[-1]
     k = (k_int8.view(B, H, S, G, D // G).to(torch.float16) * k_scale16.unsqueeze(-1)).view(B, H, S, D)
     v = dequantize_asymmetric_static(unpack_int4(v_packed), v_scale, v_zp)
+    return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)
+
+
+def decode_attn_mixed_ref(q, k_int8, k_scale, v_codes, v_scale, v_zp, context_lens, sm_scale,
+                          inv_tau=None):
+    """MixedKVCache (src/cache/mixed_kv_cache.py:170-190, 242-254) decoded as the reference
+    decodes kv_mode="int4_mixed_kv" (src/engine/generate_loop.py:1357-1364): get_kv's K =
+    code x its group's scale in fp32 (dequantize_symmetric_int8, src/quant/int8_basic.py:
+    167-246) and V = code x s + z of its token in fp32 (dequantize_asymmetric_per_token,
+    src/quant/asymmetric_quant.py:273-290), each cast to fp16, then fp32 attention.
+    v_codes are the unpacked int8 codes [B, H, S, D]."""
+    k = dequantize_symmetric(k_int8, k_scale.float()).to(torch.float16)
+    v = dequantize_kivi(v_codes, v_scale, v_zp, per_channel=False).to(torch.float16)
     return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)
 
 

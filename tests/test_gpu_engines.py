@@ -293,6 +293,8 @@ def _engine(K, kind, L, H, g):
         return K.K8V4KVCache(L, ks, s, z, device=DEV)
     if kind == "kivi":
         return K.KIVIStyleKVCache(L, device=DEV, quant_bits=4)
+    if kind == "mixed":
+        return K.MixedKVCache(L, device=DEV, k_group_size=32)
     raise ValueError(kind)
 
 
@@ -314,11 +316,15 @@ def _reference_out(K, kind, cache, layer, q, tau, n):
         kc, ks, vt, vs, vz = cache.get_k8v4_tensors(layer)
         return OA.decode_attn_k8v4_ref(q, kc.cpu(), ks.cpu(), K.untile_v(vt, n).cpu(), vs.cpu(),
                                        vz.cpu(), ctx, sm, inv_tau=tau)
+    if kind == "mixed":
+        kc, ks, vp, vs, vz = [x.cpu() for x in cache.get_mixed_tensors(layer)]
+        return OA.decode_attn_mixed_ref(q, kc, ks, OQ.unpack_int4(vp), vs, vz, ctx, sm, inv_tau=tau)
     kp, vp, ks, kz, vs, vz = [x.cpu() for x in cache.get_int4_asym_tensors(layer)]
     return OA.decode_attn_kivi_ref(q, kp, vp, ks, kz, vs, vz, ctx, sm, inv_tau=tau)
 
 
-@pytest.mark.parametrize("kind", ["int8_g32", "int8_g16", "int4_rescue", "asym", "k8v4", "kivi"])
+@pytest.mark.parametrize("kind", ["int8_g32", "int8_g16", "int4_rescue", "asym", "k8v4", "kivi",
+                                  "mixed"])
 def test_cached_decode_steps_across_growth(kind):
     """A prefill of 250 tokens, then 12 decode steps through append_decode_attn on two
     layers: the first capacity (256) is outgrown at step 7, so the cached kernel parameters
@@ -371,3 +377,55 @@ def test_kivi_decode_range_check(monkeypatch):
         assert bool(hits) == expect, (interval, [str(r.message) for r in rec])
         kp = cache.get_int4_asym_tensors(0)[0][0, 0, 16].view(torch.uint8).cpu()
         assert torch.all(kp == 0xFF)                                          # codes 7, 7 stored
+
+
+# ---------------------------------------------------------------- MixedKVCache
+
+
+@pytest.mark.parametrize("k_gs,pct,S0,Hq", [(128, 99.9, 37, 12), (32, 99.9, 300, 14), (16, 99.0, 5, 8),
+                                            (64, 100.0, 1, 4)])
+def test_mixed_cache_append_bitexact_and_decode(k_gs, pct, S0, Hq):
+    """MixedKVCache (K INT8 with a dynamic percentile-clipped scale per token and group, V
+    INT4 asymmetric per token): prefill and decode appends bit-exact with the oracle's
+    quantize_symmetric_int8 / quantize_asymmetric_per_token (codes, fp16 K scales, fp32 V
+    scale and zero-point), decode attention within max-abs 2e-3 / cosine 0.9999 of the
+    dequantise-then-attention oracle (including a one-token context), get_kv exactly the
+    reference's dequantisation."""
+    K = _k()
+    print(f"[case] mixed gs={k_gs} p={pct} S0={S0} Hq={Hq}", flush=True)
+    g = gen(600 + k_gs + S0)
+    B, H, steps = 2, 2, 3
+    cache = K.MixedKVCache(1, device=DEV, k_group_size=k_gs, k_clip_percentile=pct)
+    ks_, vs_ = [], []
+    k0, v0 = _kv(B, H, S0, g)
+    v0 = (v0.float() * torch.rand(B, H, S0, 1, generator=g) * 6 + torch.randn(B, H, S0, 1, generator=g) * 3)
+    v0 = v0.to(torch.float16)
+    cache.append(0, k0.to(DEV), v0.to(DEV))
+    ks_.append(k0); vs_.append(v0)
+    for _ in range(steps):
+        k1, v1 = _kv(B, H, 1, g)
+        cache.append(0, k1.to(DEV), v1.to(DEV))
+        ks_.append(k1); vs_.append(v1)
+    torch.cuda.synchronize()
+    n = S0 + steps
+    assert cache.get_seq_len() == n
+    kc, ksc, vp, vsc, vz = [x.cpu() for x in cache.get_mixed_tensors(0)]
+    rk, rks, rv, rvs, rvz = [], [], [], [], []
+    for k, v in zip(ks_, vs_):  # the reference quantizes each append on its own
+        a, b_ = OQ.quantize_symmetric_int8(k, pct, k_gs)
+        c, d, e = OQ.quantize_asymmetric_per_token(v, 4, 100.0)
+        rk.append(a); rks.append(b_); rv.append(c); rvs.append(d); rvz.append(e)
+    assert torch.equal(kc, torch.cat(rk, 2))
+    assert torch.equal(ksc.float(), torch.cat(rks, 2).float())
+    assert torch.equal(vp, OQ.pack_int4(torch.cat(rv, 2)))
+    assert torch.equal(vsc, torch.cat(rvs, 2)) and torch.equal(vz, torch.cat(rvz, 2))
+    k_deq, v_deq = cache.get_kv(0)
+    assert torch.equal(k_deq.cpu(), OQ.dequantize_symmetric(kc, ksc.float()).to(torch.float16))
+    assert torch.equal(v_deq.cpu(), OQ.dequantize_kivi(OQ.unpack_int4(vp), vsc, vz, False).to(torch.float16))
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+    out = cache.decode_attn(0, q.to(DEV), inv_tau=tau.to(DEV))
+    torch.cuda.synchronize()
+    ref = OA.decode_attn_mixed_ref(q, kc, ksc, OQ.unpack_int4(vp), vsc, vz, torch.full((B,), n), 1 / math.sqrt(128),
+                                   inv_tau=tau)
+    assert_close_ulp(out, ref, f"mixed gs{k_gs} S{n}")

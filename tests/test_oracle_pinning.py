@@ -40,6 +40,9 @@ term, a wrong sign or index, a swapped nibble) fails at least one check:
   rounding of the exact product, checked against float64).
 * decode_attn_k8v4_ref: float64 brute force (INT8 K dequantised as the fp16 product the
   reference forms, asymmetric V in float64, q * inv_tau as an fp16 product).
+* decode_attn_mixed_ref: float64 brute force with per-element dequantisation (K code x the
+  scale of its token's group, V code x s_t + z_t of its token), a one-token known answer and
+  a literal one (codes 3, -8, 7, 0 with s = 0.5, z = -1 give 0.5, -5, 2.5, -1).
 """
 import math
 from fractions import Fraction
@@ -548,3 +551,43 @@ def test_dequantize_symmetric_kats():
     got = OQ.cache_get_kv(codes, s16).numpy()
     exact = codes.double().numpy().reshape(2, 2, 9, 8, 16) * s16.double().numpy()[..., None]
     assert np.array_equal(got, exact.reshape(2, 2, 9, 128).astype(np.float16))
+
+
+def test_mixed_oracle_brute_force_and_kat():
+    """decode_attn_mixed_ref against float64 with explicit per-element dequantisation: K =
+    code x the scale of group d // gs of its own token (fp16 result of the exact product),
+    V = code x s_t + z_t of its own token (fp16).  A transposed V broadcast (per channel
+    instead of per token) or swapped s / z fails both checks."""
+    g = torch.Generator().manual_seed(19)
+    B, H, Hq, S, D, gs = 1, 2, 6, 7, 128, 64
+    kq = torch.randint(-127, 128, (B, H, S, D), generator=g, dtype=torch.int8)
+    ks = (torch.rand(B, H, S, D // gs, generator=g) * 0.02 + 0.001).to(torch.float16).float()
+    vq = torch.randint(-8, 8, (B, H, S, D), generator=g, dtype=torch.int8)
+    vs = torch.rand(B, H, S, generator=g) * 0.3 + 0.05
+    vz = torch.randn(B, H, S, generator=g)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.float16)
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    ctx = 6
+    out = OA.decode_attn_mixed_ref(q, kq, ks, vq, vs, vz, torch.tensor([ctx]), 0.1, inv_tau=tau)
+    kd = np.zeros((H, S, D))
+    vd = np.zeros((H, S, D))
+    for h in range(H):
+        for t in range(S):
+            for d in range(D):
+                kd[h, t, d] = float(np.float16(int(kq[0, h, t, d]) * float(ks[0, h, t, d // gs])))
+                vd[h, t, d] = float(np.float16(np.float32(int(vq[0, h, t, d])) * np.float32(vs[0, h, t])
+                                               + np.float32(vz[0, h, t])))
+    qs = np.array([[float(np.float16(np.float16(q[0, i, d]) * np.float16(tau[i]))) for d in range(D)]
+                   for i in range(Hq)])
+    ref = brute_attention(qs, kd, vd, ctx, 0.1)
+    ok, err = fp16_close(out[0].double().numpy(), ref)
+    assert ok, err
+    # known answer: one-token context returns that token's V = code * s + z, per token
+    one = OA.decode_attn_mixed_ref(q, kq, ks, vq, vs, vz, torch.tensor([1]), 0.1)
+    v0 = (vq[0, :, 0].float() * vs[0, :, 0, None] + vz[0, :, 0, None]).to(torch.float16)
+    assert torch.equal(one[0], v0.repeat_interleave(Hq // H, dim=0))
+    vq2 = torch.tensor([3, -8, 7, 0], dtype=torch.int8).repeat(32).view(1, 1, 1, D).expand(1, H, S, D)
+    sv = torch.full((1, H, S), 0.5)
+    zv = torch.full((1, H, S), -1.0)
+    lit = OA.decode_attn_mixed_ref(q, kq, ks, vq2.contiguous(), sv, zv, torch.tensor([1]), 0.1)
+    assert lit[0, 0, :4].tolist() == [0.5, -5.0, 2.5, -1.0]
