@@ -1,5 +1,5 @@
 /*
- * kvq.h -- C ABI (version 4) of the MI355X (gfx950) quantized-KV decode path.
+ * kvq.h -- C ABI (version 5) of the MI355X (gfx950) quantized-KV decode path.
  *
  * libkvq.so exports three groups of entry points: quantize-on-append, split-K
  * decode attention and error reporting.  Every entry point
@@ -50,6 +50,12 @@ typedef struct ihipStream_t* kvq_stream_t; /* == hipStream_t */
                                [B,H,D] (scale_stride_b/_h/_g, channels contiguous), V per
                                (b, h, token) [B,H,T] (scale_stride_b/_h/_t, tokens
                                contiguous); zero_point has the scale's strides */
+#define KVQ_FMT_INT8_KIVI 5  /* int8 codes [..., D] in [-128,127], value c * s + z, the
+                                parameters as INT4_KIVI (the reference's quant_bits=8 KIVI
+                                cache); append: range floor 255 * 2^-14, s = range / 255,
+                                z = min + 128 s */
+#define KVQ_FMT_FP16 6       /* fp16 values [..., D] as stored (a 16-bit side of the
+                                reference's mixed / allocator caches); decode only */
 
 /* code layouts (kvq_kv_view.layout, kvq_append_params.codes_layout) */
 #define KVQ_LAYOUT_ROWS 0   /* token-major: the code bytes of token t start at t * stride_t */
@@ -219,7 +225,10 @@ typedef struct kvq_append_params {
      fp32(percentile / 100) in (0, 1): the group's torch.quantile of |x| at that level
      (linear interpolation in fp32, src/quant/int8_basic.py:78-83, int4_basic.py:84-90) */
   float dyn_quantile;
-  int32_t pad0;             /* 0 */
+  /* KIVI V (ABI 5): 0 = the token's min / max; with dyn_quantile = fp32(p / 100) > 0 this is
+     fp32((100 - p) / 100): the range is torch.quantile at these two levels over the token's
+     128 channels (src/quant/asymmetric_quant.py:97-103).  0 for every other use. */
+  float dyn_quantile_lo;
 } kvq_append_params;
 
 /* Appends K and V of one layer with one launch (either pointer may be NULL).  The INT4_SYM
@@ -259,7 +268,7 @@ int kvq_stream_read(const void* buf, int64_t bytes, uint32_t* sink, int32_t work
 
 /* message for the last non-OK return on this thread ("" if none) */
 const char* kvq_last_error(void);
-/* ABI version (increments on incompatible changes to the structs above); this is 4 */
+/* ABI version (increments on incompatible changes to the structs above); this is 5 */
 int32_t kvq_abi_version(void);
 
 #ifdef __cplusplus

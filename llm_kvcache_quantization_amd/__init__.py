@@ -28,6 +28,9 @@ from .cache import (  # noqa: F401
     K8V4KVCache,
     KIVIStyleKVCache,
     MixedKVCache,
+    RoleAwareAllocatorKVCache,
+    RoleAwareAsymKVCache,
+    load_per_layer_bits_from_policy,
 )
 from .patch import (  # noqa: F401
     INT8CacheWrapper,
@@ -52,6 +55,9 @@ __all__ = [
     "K8V4KVCache",
     "KIVIStyleKVCache",
     "MixedKVCache",
+    "RoleAwareAsymKVCache",
+    "RoleAwareAllocatorKVCache",
+    "load_per_layer_bits_from_policy",
     "decode_attn_int4_kivi",
     "decode_attn_int4_asym_v2",
     "decode_attn_int4_asym_gqa",

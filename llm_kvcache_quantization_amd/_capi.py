@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before libkvq.so, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 KVQ_OK = 0
 KVQ_ERR_INVALID = 1
@@ -30,6 +30,8 @@ KVQ_FMT_INT8_SYM = 1
 KVQ_FMT_INT4_SYM = 2
 KVQ_FMT_INT4_ASYM = 3
 KVQ_FMT_INT4_KIVI = 4
+KVQ_FMT_INT8_KIVI = 5
+KVQ_FMT_FP16 = 6
 
 KVQ_LAYOUT_ROWS = 0
 KVQ_LAYOUT_TILE32 = 1
@@ -113,7 +115,7 @@ class AppendParams(ctypes.Structure):
         ("codes_layout", c_i32), ("reserved", c_i32),
         ("scratch", c_vp), ("scratch_bytes", c_i64),
         ("static_stride_b", c_i64), ("zp_out", c_vp),
-        ("dyn_quantile", c_f32), ("pad0", c_i32),
+        ("dyn_quantile", c_f32), ("dyn_quantile_lo", c_f32),
     ]
 
 

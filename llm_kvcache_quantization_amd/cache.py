@@ -1057,44 +1057,95 @@ class K8V4KVCache(_StaticG32Cache):
         return k, ks, vt, self.v_scale[layer_id], self.v_zp[layer_id]
 
 
-class KIVIStyleKVCache(_EngineBase):
-    """KIVI-style INT4 cache (src/cache/kivi_style_cache.py:38-900): K quantized per
-    channel with scale / zero-point frozen at prefill ([B, H, D] fp32), V per token
-    ([B, H, T] fp32), both as packed nibbles [B, H, T, 64] (byte = ((c[2i]+8) << 4) |
-    (c[2i+1]+8)).  Every token is quantized by kvq_quant_append (HIP); the prefill's
-    per-channel K range is reduced with torch.aminmax as the reference does.  Decode
-    attention reads the cache in place (kvq_decode_attn, format INT4_KIVI).
+_KIVI_BITS = (4, 8, 16)
 
-    Built: quant_bits=4, percentiles 100, residual_length 0; the other settings of the
-    reference raise NotImplementedError.
+
+def _kivi_format(bits: int) -> int:
+    return {4: C.KVQ_FMT_INT4_KIVI, 8: C.KVQ_FMT_INT8_KIVI, 16: C.KVQ_FMT_FP16}[bits]
+
+
+def _kivi_row(bits: int) -> Tuple[int, torch.dtype]:
+    """(elements per token row, dtype) of a side's storage: packed nibbles, int8 codes or
+    fp16 values."""
+    return {4: (64, torch.int8), 8: (128, torch.int8), 16: (128, torch.float16)}[bits]
+
+
+def _kivi_levels(percentile: float) -> Tuple[float, float]:
+    """The two quantile levels of quantize_asymmetric's clipping (src/quant/asymmetric_quant.py:
+    97-103): (100 - p) / 100 and p / 100, or (0, 0) for the min / max at p = 100."""
+    p = float(percentile)
+    if not (50.0 < p <= 100.0):
+        raise ValueError(f"percentile must be in (50.0, 100.0], got {percentile}. Values <= 50 invert "
+                         "min/max and produce silent errors.")
+    if p >= 100.0:
+        return 0.0, 0.0
+    return max(0.0, min((100.0 - p) / 100.0, 1.0)), max(0.0, min(p / 100.0, 1.0))
+
+
+def _sorted_quantile(sorted_x: Tensor, q: float, dim: int) -> Tensor:
+    """torch.quantile(x, q, dim) from x sorted along dim: the order statistics at floor / ceil
+    of fp32(q) * (n - 1) and torch.lerp between them (ATen's quantile, without its input-size
+    limit)."""
+    import numpy as np
+
+    n = sorted_x.shape[dim]
+    rank = np.float32(q) * np.float32(n - 1)
+    lo, hi = int(np.floor(rank)), int(np.ceil(rank))
+    w = float(np.float32(rank - np.float32(lo)))
+    return torch.lerp(sorted_x.select(dim, lo), sorted_x.select(dim, hi), w)
+
+
+def kivi_channel_params(k: Tensor, bits: int, percentile: float) -> Tuple[Tensor, Tensor]:
+    """Per-channel K scale / zero-point over the tokens of a prefill k [B, H, S, D]
+    (quantize_asymmetric_per_channel, src/quant/asymmetric_quant.py:24-141, 199-224): the
+    range (min / max, or the two quantiles) in fp32, floored at max(1e-5, fp16 tiny x
+    (qmax - qmin)), divided by qmax - qmin; z = min - qmin s.  fp32 [B, H, D]."""
+    qmin, qmax = (-8, 7) if bits == 4 else (-128, 127)
+    lo_q, hi_q = _kivi_levels(percentile)
+    kf = k.float()
+    if hi_q > 0.0:
+        srt = torch.sort(kf, dim=2).values
+        t_min, t_max = _sorted_quantile(srt, lo_q, 2), _sorted_quantile(srt, hi_q, 2)
+    else:
+        t_min, t_max = torch.aminmax(kf, dim=2)
+    span = float(qmax - qmin)
+    floor = max(1e-5, float(torch.finfo(torch.float16).tiny) * span)
+    # IEEE division, as the formula reads and torch computes it on the CPU (a GPU tensor
+    # divided by a Python scalar is multiplied by fp32(1 / span) instead)
+    rng = (t_max - t_min).clamp(min=floor)
+    s = rng / torch.full_like(rng, span)
+    return s.contiguous(), (t_min - qmin * s).contiguous()
+
+
+class _KiviFamily(_EngineBase):
+    """Storage and kernels of the KIVI family (src/cache/kivi_style_cache.py:38-900,
+    src/cache/role_aware_allocator_cache.py:73-502): per layer a (k_bits, v_bits) pair from
+    {4, 8, 16}.  A quantized K side has per-channel asymmetric codes with the scale / zero-point
+    frozen at prefill ([B, H, D] fp32); a quantized V side per-token codes ([B, H, T] fp32
+    parameters); a 16-bit side keeps fp16 values.  Codes: 4 bits packed [B, H, T, 64] (byte =
+    ((c[2i]+8) << 4) | (c[2i+1]+8)), 8 bits int8 [B, H, T, 128].  Every quantized token goes
+    through kvq_quant_append (HIP; per-token percentile clipping in the kernel); the prefill's
+    per-channel K range is reduced with torch (aminmax, or a sort and torch.lerp for a
+    percentile, as torch.quantile does).  Decode attention reads the cache in place through the
+    tiled kernel of the layer's pair (kvq_decode_attn).  residual_length 0 only.
     """
 
     _min_capacity = 256
 
-    def __init__(self, num_layers: int, device: str = "cuda", dtype: torch.dtype = torch.float16,
-                 max_seq_len: Optional[int] = None, quant_bits: int = 8,
-                 k_percentile: float = 100.0, v_percentile: float = 100.0,
-                 inv_tau: Optional[Tensor] = None, use_attn_temperature: bool = False,
-                 residual_length: int = 0, decode_attn_impl: str = "hip_fused",
-                 check_numerics: bool = True):
-        if num_layers <= 0:
-            raise ValueError(f"num_layers must be > 0, got {num_layers}")
-        if quant_bits not in (4, 8):
-            raise ValueError(f"quant_bits must be 4 or 8, got {quant_bits}")
-        if quant_bits != 4:
-            raise NotImplementedError("only the bit-packed INT4 KIVI layout is built (quant_bits=4)")
-        if k_percentile != 100.0 or v_percentile != 100.0:
-            raise NotImplementedError("percentile clipping of the KIVI parameters is not built")
-        if residual_length:
+    def _init_kivi(self, num_layers, device, dtype, max_seq_len, bits, k_percentile, v_percentile,
+                   inv_tau, use_attn_temperature, residual_length, decode_attn_impl, check_numerics):
+        if int(residual_length) != 0:
             raise NotImplementedError("the fp16 residual window is not built (residual_length=0)")
+        _kivi_levels(k_percentile)
+        _kivi_levels(v_percentile)
         self._init_common(num_layers, device, max_seq_len, decode_attn_impl, check_numerics)
         self.dtype = dtype
-        self.quant_bits, self.bit_packed = 4, True
-        self.k_percentile, self.v_percentile = k_percentile, v_percentile
+        self.k_percentile, self.v_percentile = float(k_percentile), float(v_percentile)
         self.residual_length = 0
         self.inv_tau = inv_tau
         self.use_attn_temperature = bool(use_attn_temperature)
         self._scale_dtype = torch.float32
+        self._bits = [tuple(b) for b in bits]
         n = num_layers
         self._k_cache: List[Optional[Tensor]] = [None] * n
         self._v_cache: List[Optional[Tensor]] = [None] * n
@@ -1106,82 +1157,97 @@ class KIVIStyleKVCache(_EngineBase):
         self._oor_check_interval = int(os.environ.get("KV_OOR_CHECK_INTERVAL", "0"))
         self._oor_step_counter = 0
 
+    def _resolve_bits(self, layer_id: int) -> Tuple[int, int]:
+        return self._bits[layer_id]
+
     def _ensure(self, layer_id: int, B: int, H: int, target: int, device) -> None:
+        kb, vb = self._bits[layer_id]
+        kc0 = self._k_cache[layer_id]
+        if kc0 is not None and (kc0.shape[0] != B or kc0.shape[1] != H):
+            raise ValueError(f"Inconsistent KV shape for layer {layer_id}: existing K={tuple(kc0.shape)}, "
+                             f"incoming=({B}, {H}, *, 128)")
         cap = self._layer_capacity[layer_id]
-        if self._k_cache[layer_id] is not None and target <= cap:
+        if kc0 is not None and target <= cap:
             return
-        new_cap = self._new_capacity(layer_id, target, cap)
+        new_cap = self._new_capacity(layer_id, target, cap if kc0 is not None else 0)
         new_cap = ((new_cap + TILE_TOKENS - 1) // TILE_TOKENS) * TILE_TOKENS
         old = self._layer_seq_lens[layer_id]
-        # int8 storage of the packed bytes, as the reference keeps them
-        kc = torch.zeros(B, H, new_cap, 64, dtype=torch.int8, device=device)
-        vc = torch.zeros_like(kc)
-        vs = torch.zeros(B, H, new_cap, dtype=torch.float32, device=device)
-        vz = torch.zeros_like(vs)
-        if self._k_cache[layer_id] is not None and old > 0:
-            kc[:, :, :old] = self._k_cache[layer_id][:, :, :old]
+        (kw, kdt), (vw, vdt) = _kivi_row(kb), _kivi_row(vb)
+        kc = torch.zeros(B, H, new_cap, kw, dtype=kdt, device=device)
+        vc = torch.zeros(B, H, new_cap, vw, dtype=vdt, device=device)
+        vs = vz = None
+        if vb != 16:
+            vs = torch.zeros(B, H, new_cap, dtype=torch.float32, device=device)
+            vz = torch.zeros_like(vs)
+        if kc0 is not None and old > 0:
+            kc[:, :, :old] = kc0[:, :, :old]
             vc[:, :, :old] = self._v_cache[layer_id][:, :, :old]
-            vs[:, :, :old] = self._v_scale[layer_id][:, :, :old]
-            vz[:, :, :old] = self._v_zp[layer_id][:, :, :old]
+            if vs is not None:
+                vs[:, :, :old] = self._v_scale[layer_id][:, :, :old]
+                vz[:, :, :old] = self._v_zp[layer_id][:, :, :old]
         self._k_cache[layer_id], self._v_cache[layer_id] = kc, vc
         self._v_scale[layer_id], self._v_zp[layer_id] = vs, vz
         self._layer_capacity[layer_id] = new_cap
         self._steps[layer_id] = self._apps[layer_id] = None
 
     def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
+        """Quantize (or store) and append k, v fp16 [B, H, S, 128] (kivi_style_cache.py:296-617,
+        role_aware_allocator_cache.py:311-400)."""
         self._validate_kv(layer_id, k, v)
         B, H, S, D = k.shape
-        if D != 128:
-            raise NotImplementedError("head_dim 128 only")
-        if k.dtype != torch.float16 or v.dtype != torch.float16:
-            raise NotImplementedError("fp16 K/V inputs only")
         old = self._layer_seq_lens[layer_id]
         if S == 0:
             return
+        kb, vb = self._bits[layer_id]
         self._ensure(layer_id, B, H, old + S, k.device)
-        prefill = not self._k_scale_initialized[layer_id]
+        prefill = kb != 16 and not self._k_scale_initialized[layer_id]
         # the frozen-K range check of decode appends runs every KV_OOR_CHECK_INTERVAL steps
         # (0, the default: never), counted on layer 0 (kivi_style_cache.py:143-144, 549-560)
         oor_check = False
-        if not prefill and self._oor_check_interval > 0:
+        if kb != 16 and not prefill and self._oor_check_interval > 0:
             if layer_id == 0:
                 self._oor_step_counter += 1
             oor_check = self._oor_step_counter % self._oor_check_interval == 0
         if prefill:
-            # prefill: per-channel range over the incoming tokens (asymmetric_quant.py:102-141)
             if self.check_numerics and not bool(torch.isfinite(k).all()):
                 raise ValueError("quantize_asymmetric: input contains NaN or Inf")
-            t_min, t_max = torch.aminmax(k.float(), dim=2)
-            floor = max(1e-5, float(torch.finfo(torch.float16).tiny) * 15)
-            # IEEE division, as the formula reads and torch computes it on the CPU (a GPU
-            # tensor divided by a Python scalar is multiplied by fp32(1/15) instead)
-            rng = (t_max - t_min).clamp(min=floor)
-            s = rng / torch.full_like(rng, 15.0)
-            self._k_scale[layer_id] = s.contiguous()
-            self._k_zp[layer_id] = (t_min - (-8) * s).contiguous()
+            self._k_scale[layer_id], self._k_zp[layer_id] = kivi_channel_params(k, kb, self.k_percentile)
             self._k_scale_initialized[layer_id] = True
-        ks, kz = self._k_scale[layer_id], self._k_zp[layer_id]
-        if tuple(ks.shape) != (B, H, D):
-            raise ValueError(f"Inconsistent decode K scale/zp shape for layer {layer_id}: "
-                             f"expected {(B, H, D)}, got {tuple(ks.shape)}")
-        # the status words (NaN flags, K range count) cost a host sync: read at prefill
-        # with check_numerics, and on the decode steps the range check selects
+        if kb != 16:
+            ks = self._k_scale[layer_id]
+            if tuple(ks.shape) != (B, H, D):
+                raise ValueError(f"Inconsistent decode K scale/zp shape for layer {layer_id}: "
+                                 f"expected {(B, H, D)}, got {tuple(ks.shape)}")
+        # the status words (NaN flags, K range count) cost a host sync: read at prefill with
+        # check_numerics, and on the decode steps the range check selects
         status = self._status_buf(k.device) if (self.check_numerics and prefill) or oor_check else None
-        pk, pv = C.AppendParams(), C.AppendParams()
+        sp = None if status is None else status.data_ptr()
         ksx = k if k.stride(-1) == 1 else k.contiguous()
         vsx = v if v.stride(-1) == 1 else v.contiguous()
-        sp = None if status is None else status.data_ptr()
-        _fill_append(pk, C.KVQ_FMT_INT4_KIVI, ksx, 32, self._k_cache[layer_id], old, sp)
-        pk.static_scale, pk.static_zp = ks.data_ptr(), kz.data_ptr()
-        pk.static_scale_dtype = C.KVQ_DTYPE_F32
-        pk.static_stride_b, pk.static_stride_h, pk.static_stride_g = ks.stride()
-        _fill_append(pv, C.KVQ_FMT_INT4_KIVI, vsx, 32, self._v_cache[layer_id], old,
-                     None if sp is None else sp + 8)
-        vs, vz = self._v_scale[layer_id], self._v_zp[layer_id]
-        pv.scale_out, pv.zp_out, pv.scale_out_dtype = vs.data_ptr(), vz.data_ptr(), C.KVQ_DTYPE_F32
-        pv.so_stride_b, pv.so_stride_h, pv.so_stride_t = vs.stride()
-        C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
-                                         ctypes.c_void_p(C.stream_handle(k.device))))
+        pk = pv = None
+        if kb == 16:
+            self._k_cache[layer_id][:, :, old:old + S] = ksx
+        else:
+            pk = C.AppendParams()
+            _fill_append(pk, _kivi_format(kb), ksx, 32, self._k_cache[layer_id], old, sp)
+            ks, kz = self._k_scale[layer_id], self._k_zp[layer_id]
+            pk.static_scale, pk.static_zp = ks.data_ptr(), kz.data_ptr()
+            pk.static_scale_dtype = C.KVQ_DTYPE_F32
+            pk.static_stride_b, pk.static_stride_h, pk.static_stride_g = ks.stride()
+        if vb == 16:
+            self._v_cache[layer_id][:, :, old:old + S] = vsx
+        else:
+            pv = C.AppendParams()
+            _fill_append(pv, _kivi_format(vb), vsx, 32, self._v_cache[layer_id], old,
+                         None if sp is None else sp + 8)
+            vs, vz = self._v_scale[layer_id], self._v_zp[layer_id]
+            pv.scale_out, pv.zp_out, pv.scale_out_dtype = vs.data_ptr(), vz.data_ptr(), C.KVQ_DTYPE_F32
+            pv.so_stride_b, pv.so_stride_h, pv.so_stride_t = vs.stride()
+            pv.dyn_quantile_lo, pv.dyn_quantile = _kivi_levels(self.v_percentile)
+        if pk is not None or pv is not None:
+            C.check(C.lib().kvq_quant_append(None if pk is None else ctypes.byref(pk),
+                                             None if pv is None else ctypes.byref(pv),
+                                             ctypes.c_void_p(C.stream_handle(k.device))))
         if status is not None:
             st = self._read_status()
             if st[0] & 1 or st[2] & 1:
@@ -1189,21 +1255,13 @@ class KIVIStyleKVCache(_EngineBase):
                                  "— refusing to quantize corrupt data")
             ratio = st[1] / max(k.numel(), 1)
             if oor_check and ratio > _CLIP_WARN_THRESHOLD:
+                lo, hi = (-8, 7) if kb == 4 else (-128, 127)
                 warnings.warn(
                     f"ENG-041: KIVI decode K clipping at layer {layer_id}: {ratio:.1%} of values exceed "
-                    "prefill-computed scale range [-8, 7]. Decode token magnitudes may have drifted "
+                    f"prefill-computed scale range [{lo}, {hi}]. Decode token magnitudes may have drifted "
                     "beyond prefill calibration. Attention accuracy may degrade.", RuntimeWarning)
         self._layer_seq_lens[layer_id] = old + S
-        if layer_id == 0:
-            self._seq_len = old + S
-
-    def get_int4_asym_tensors(self, layer_id: int):
-        """(k_packed, v_packed, k_scale, k_zp, v_scale, v_zp) over the stored tokens, the
-        reference's kernel arguments (kivi_style_cache.py:668-700)."""
-        n = self._check_layer(layer_id)
-        return (self._k_cache[layer_id][:, :, :n], self._v_cache[layer_id][:, :, :n],
-                self._k_scale[layer_id], self._k_zp[layer_id],
-                self._v_scale[layer_id][:, :, :n], self._v_zp[layer_id][:, :, :n])
+        self._seq_len = max(self._layer_seq_lens)
 
     def _check_layer(self, layer_id: int) -> int:
         if layer_id < 0 or layer_id >= self.num_layers:
@@ -1215,32 +1273,49 @@ class KIVIStyleKVCache(_EngineBase):
             raise ValueError(f"Cache for layer {layer_id} has no tokens")
         return n
 
+    def get_kivi_tensors(self, layer_id: int):
+        """(k_store, v_store, k_scale, k_zp, v_scale, v_zp) over the stored tokens: packed /
+        int8 codes or fp16 values, the per-channel K and per-token V parameters (None for a
+        16-bit side)."""
+        n = self._check_layer(layer_id)
+        vs, vz = self._v_scale[layer_id], self._v_zp[layer_id]
+        return (self._k_cache[layer_id][:, :, :n], self._v_cache[layer_id][:, :, :n],
+                self._k_scale[layer_id], self._k_zp[layer_id],
+                None if vs is None else vs[:, :, :n], None if vz is None else vz[:, :, :n])
+
     def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
-        """Dequantised K, V in self.dtype (kivi_style_cache.py:619-666)."""
-        kp, vp, ks, kz, vs, vz = self.get_int4_asym_tensors(layer_id)
-
-        def unpack(p):
-            p = p.to(torch.int16)
-            return torch.stack(((p >> 4) & 15, p & 15), dim=-1).flatten(-2) - 8
-
-        k = (unpack(kp).float() * ks.unsqueeze(2) + kz.unsqueeze(2)).to(self.dtype)
-        v = (unpack(vp).float() * vs.unsqueeze(-1) + vz.unsqueeze(-1)).to(self.dtype)
+        """Dequantised K, V in self.dtype (kivi_style_cache.py:619-666,
+        role_aware_allocator_cache.py:402-440): code x s + z in fp32, then cast."""
+        kc, vc, ks, kz, vs, vz = self.get_kivi_tensors(layer_id)
+        kb, vb = self._bits[layer_id]
+        if kb == 16:
+            k = kc.to(self.dtype)
+        else:
+            kq = _unpack(kc) if kb == 4 else kc
+            k = (kq.float() * ks.unsqueeze(2) + kz.unsqueeze(2)).to(self.dtype)
+        if vb == 16:
+            v = vc.to(self.dtype)
+        else:
+            vq = _unpack(vc) if vb == 4 else vc
+            v = (vq.float() * vs.unsqueeze(-1) + vz.unsqueeze(-1)).to(self.dtype)
         return k, v
 
     def _step_for(self, layer_id: int, q_heads: int):
         """The layer's LayerStep over its whole buffers and its frozen K parameters."""
         kc, ks = self._k_cache[layer_id], self._k_scale[layer_id]
-        key = (q_heads, kc.data_ptr(), ks.data_ptr())
+        key = (q_heads, kc.data_ptr(), None if ks is None else ks.data_ptr())
         st = self._steps[layer_id]
         if st is not None and st.key == key:
             return st
-        from .kernels import LayerStep, kv_view_kivi
+        from .kernels import LayerStep, kv_view_fp16, kv_view_kivi
 
+        kb, vb = self._bits[layer_id]
         B, H = kc.shape[0], kc.shape[1]
         vc, vs, vz, kz = self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id], \
             self._k_zp[layer_id]
-        st = LayerStep(C.KVQ_FMT_INT4_KIVI, kv_view_kivi(kc, ks, kz, True), C.KVQ_FMT_INT4_KIVI,
-                       kv_view_kivi(vc, vs, vz, False), B, q_heads, H, 32, kc.device,
+        kview = kv_view_fp16(kc) if kb == 16 else kv_view_kivi(kc, ks, kz, True)
+        vview = kv_view_fp16(vc) if vb == 16 else kv_view_kivi(vc, vs, vz, False)
+        st = LayerStep(_kivi_format(kb), kview, _kivi_format(vb), vview, B, q_heads, H, 32, kc.device,
                        keepalive=(kc, ks, kz, vc, vs, vz))
         st.key = key
         self._steps[layer_id] = st
@@ -1258,8 +1333,9 @@ class KIVIStyleKVCache(_EngineBase):
         return t
 
     def decode_attn(self, layer_id: int, q: Tensor, sm_scale: Optional[float] = None) -> Tensor:
-        """Attention of q [B, Hq, 128] over layer_id's cache (INT4_KIVI decode kernel); with
-        use_attn_temperature and inv_tau [L, Hq], q is scaled by inv_tau[layer] in fp16."""
+        """Attention of q [B, Hq, 128] over layer_id's cache (the tiled kernel of the layer's
+        (k_bits, v_bits) pair); with use_attn_temperature and inv_tau [L, Hq], q is scaled by
+        inv_tau[layer] in fp16."""
         n = self._check_layer(layer_id)
         if q.ndim != 3 or q.shape[-1] != 128:
             raise ValueError(f"q must be [B, Hq, 128], got {tuple(q.shape)}")
@@ -1310,30 +1386,152 @@ class KIVIStyleKVCache(_EngineBase):
             total += sum(t.numel() * t.element_size() for t in lst if t is not None)
         return total / (1024 * 1024)
 
+    def to_tuple(self) -> Tuple[Tuple[Tensor, Tensor], ...]:
+        """Every layer's dequantised (k, v) (role_aware_allocator_cache.py:477-483)."""
+        out = []
+        for i in range(self.num_layers):
+            if self._layer_seq_lens[i] <= 0:
+                raise ValueError(f"Layer {i} cache is empty")
+            out.append(self.get_kv(i))
+        return tuple(out)
+
+
+class KIVIStyleKVCache(_KiviFamily):
+    """KIVI-style cache (src/cache/kivi_style_cache.py:38-900): every layer quantized with
+    quant_bits (4: packed nibbles, 8: int8 codes), K per channel with parameters frozen at
+    prefill, V per token, both with optional percentile clipping (k_percentile,
+    v_percentile).  See _KiviFamily for the storage and kernels."""
+
+    def __init__(self, num_layers: int, device: str = "cuda", dtype: torch.dtype = torch.float16,
+                 max_seq_len: Optional[int] = None, quant_bits: int = 8,
+                 k_percentile: float = 100.0, v_percentile: float = 100.0,
+                 inv_tau: Optional[Tensor] = None, use_attn_temperature: bool = False,
+                 residual_length: int = 0, decode_attn_impl: str = "hip_fused",
+                 check_numerics: bool = True):
+        if num_layers <= 0:
+            raise ValueError(f"num_layers must be > 0, got {num_layers}")
+        if quant_bits not in (4, 8):
+            raise ValueError(f"quant_bits must be 4 or 8, got {quant_bits}")
+        self._init_kivi(num_layers, device, dtype, max_seq_len, [(quant_bits, quant_bits)] * num_layers,
+                        k_percentile, v_percentile, inv_tau, use_attn_temperature, residual_length,
+                        decode_attn_impl, check_numerics)
+        self.quant_bits = int(quant_bits)
+        self.bit_packed = self.quant_bits == 4
+
+    def get_int4_asym_tensors(self, layer_id: int):
+        """(k_packed, v_packed, k_scale, k_zp, v_scale, v_zp) over the stored tokens, the
+        reference's kernel arguments (kivi_style_cache.py:668-700); quant_bits=4 only."""
+        if not self.bit_packed:
+            raise RuntimeError("get_int4_asym_tensors requires bit_packed=True (quant_bits=4)")
+        return self.get_kivi_tensors(layer_id)
+
+
+class RoleAwareAsymKVCache(KIVIStyleKVCache):
+    """RoleAlign's cache (src/cache/role_aware_asym_cache.py:27-76): the KIVI layout with
+    calibrated k / v percentiles and inv_tau, tagged with its framework."""
+
+    def __init__(self, num_layers: int, device: str = "cuda", dtype: torch.dtype = torch.float16,
+                 max_seq_len: Optional[int] = None, quant_bits: int = 4,
+                 k_percentile: float = 100.0, v_percentile: float = 100.0,
+                 inv_tau: Optional[Tensor] = None, use_attn_temperature: bool = False,
+                 framework: str = "ours_asym", residual_length: int = 0,
+                 decode_attn_impl: str = "hip_fused", check_numerics: bool = True):
+        super().__init__(num_layers=num_layers, device=device, dtype=dtype, max_seq_len=max_seq_len,
+                         quant_bits=quant_bits, k_percentile=k_percentile, v_percentile=v_percentile,
+                         inv_tau=inv_tau, use_attn_temperature=use_attn_temperature,
+                         residual_length=residual_length, decode_attn_impl=decode_attn_impl,
+                         check_numerics=check_numerics)
+        self.framework = framework
+        self.ba_calibrated = (k_percentile != 100.0) or (v_percentile != 100.0)
+
+
+def load_per_layer_bits_from_policy(policy_json, *, project_root) -> List[Tuple[int, int]]:
+    """Per-layer (k_bits, v_bits) pairs of an allocator policy JSON
+    (src/cache/role_aware_allocator_cache.py:36-70): a relative path resolves against
+    project_root; the file must hold ``per_layer_bits``, each a pair from {4, 8, 16}."""
+    import json
+    from pathlib import Path
+
+    path = Path(policy_json)
+    if not path.is_absolute():
+        path = Path(project_root) / path
+    if not path.exists():
+        raise FileNotFoundError(f"policy_json={str(policy_json)!r} not found (resolved to {str(path)!r}).")
+    with path.open("r", encoding="utf-8") as fh:
+        payload = json.load(fh)
+    raw = payload.get("per_layer_bits")
+    if raw is None:
+        raise ValueError(f"policy_json {str(path)!r} missing required key 'per_layer_bits'")
+    pairs = []
+    for idx, entry in enumerate(raw):
+        if not isinstance(entry, (list, tuple)) or len(entry) != 2:
+            raise ValueError(f"per_layer_bits[{idx}] must be a 2-tuple/list (k_bits, v_bits), got {entry!r}")
+        kb, vb = int(entry[0]), int(entry[1])
+        if kb not in _KIVI_BITS or vb not in _KIVI_BITS:
+            raise ValueError(f"per_layer_bits[{idx}]=({kb},{vb}) contains unsupported bits; allowed "
+                             f"values: {sorted(_KIVI_BITS)}")
+        pairs.append((kb, vb))
+    return pairs
+
+
+class RoleAwareAllocatorKVCache(_KiviFamily):
+    """The allocator's RoleAlign cache (src/cache/role_aware_allocator_cache.py:73-502): the
+    KIVI family with a (k_bits, v_bits) pair from {4, 8, 16} per layer.  See _KiviFamily."""
+
+    def __init__(self, num_layers: int, *, per_layer_bits: List[Tuple[int, int]],
+                 device: str = "cuda", dtype: torch.dtype = torch.float16,
+                 max_seq_len: Optional[int] = None, k_percentile: float = 100.0,
+                 v_percentile: float = 100.0, inv_tau: Optional[Tensor] = None,
+                 use_attn_temperature: bool = False, framework: str = "ours_asym_allocator",
+                 residual_length: int = 0, decode_attn_impl: str = "torch_ref",
+                 check_numerics: bool = True):
+        if num_layers <= 0:
+            raise ValueError(f"num_layers must be > 0, got {num_layers}")
+        if len(per_layer_bits) != num_layers:
+            raise ValueError(f"per_layer_bits length {len(per_layer_bits)} must equal num_layers {num_layers}")
+        norm = []
+        for idx, entry in enumerate(per_layer_bits):
+            if not isinstance(entry, (tuple, list)) or len(entry) != 2:
+                raise ValueError(f"per_layer_bits[{idx}] must be a 2-tuple/list (k_bits, v_bits), got {entry!r}")
+            kb, vb = int(entry[0]), int(entry[1])
+            if kb not in _KIVI_BITS or vb not in _KIVI_BITS:
+                raise ValueError(f"per_layer_bits[{idx}]=({kb},{vb}) contains unsupported bits; allowed "
+                                 f"values: {sorted(_KIVI_BITS)}")
+            norm.append((kb, vb))
+        if int(residual_length) != 0:
+            raise ValueError("RoleAwareAllocatorKVCache currently requires residual_length=0")
+        self._init_kivi(num_layers, device, dtype, max_seq_len, norm, k_percentile, v_percentile,
+                        inv_tau, use_attn_temperature, 0, decode_attn_impl, check_numerics)
+        self.framework = framework
+        self.ba_calibrated = (self.k_percentile != 100.0) or (self.v_percentile != 100.0)
+        self._per_layer_bits = norm
+
 
 _MIXED_BITS = {4, 8, 16}
 
 
 class MixedKVCache(_EngineBase):
-    """The reference's K/V mixed-precision cache (src/cache/mixed_kv_cache.py:35-330) with
-    its default bit widths: K INT8 symmetric per group with a dynamic percentile-clipped
-    scale (src/quant/int8_basic.py:18-108), V INT4 asymmetric per token
-    (src/quant/asymmetric_quant.py:246-270).  The buffers are preallocated and grow by
-    doubling (the reference concatenates per append).  Per layer:
+    """The reference's K/V mixed-precision cache (src/cache/mixed_kv_cache.py:35-330).  Per
+    layer a (k_bits, v_bits) pair (per_layer_bits, or k_bits / v_bits for every layer):
 
-    * K codes int8 [B, H, cap, 128] and fp16 scales [B, H, cap, G] (the reference keeps the
-      same fp16-valued scales as fp32);
-    * V codes as packed nibbles [B, H, cap, 64] (byte = ((c[2i]+8) << 4) | (c[2i+1]+8); the
-      reference keeps one code per byte) with fp32 scale / zero-point [B, H, cap].
+    * K 8: INT8 symmetric per (token, group of k_group_size) with a dynamic percentile-clipped
+      scale (src/quant/int8_basic.py:18-108): codes int8 [B, H, cap, 128], fp16 scales
+      [B, H, cap, Gk] (the reference keeps the same fp16-valued scales as fp32);
+    * V 4: INT4 asymmetric per token (src/quant/asymmetric_quant.py:246-270, v_percentile
+      clipping): packed nibbles [B, H, cap, 64] (byte = ((c[2i]+8) << 4) | (c[2i+1]+8); the
+      reference keeps one code per byte), fp32 scale / zero-point [B, H, cap];
+    * V 8: as K 8 with v_group_size and v_percentile;
+    * 16 (either side): fp16 values as they come.
 
-    Both sides of an append are one kvq_quant_append launch (K INT8_SYM dynamic, V INT4_KIVI
-    per token); decode attention reads the cache in place (the tiled kernel for INT8 K with
-    per-token scales and KIVI-layout V).  Built: k_bits 8 and v_bits 4 on every layer,
-    v_percentile 100; the fp16 and other ablation widths of the reference raise
-    NotImplementedError.
+    The buffers are preallocated and grow by doubling (the reference concatenates per
+    append).  The quantized sides of an append are one kvq_quant_append launch; decode
+    attention reads the cache in place through the tiled kernel of the layer's pair.  Built
+    pairs: (8, 4) (the default), (8, 8) with k_group_size == v_group_size, (8, 16), (16, 4),
+    (16, 16); K 4 (asymmetric per token) and (16, 8) raise NotImplementedError.
     """
 
     _min_capacity = 256
+    _BUILT = {(8, 4), (8, 8), (8, 16), (16, 4), (16, 16)}
 
     def __init__(self, num_layers: int, device: str = "cuda", dtype: torch.dtype = torch.float16,
                  max_seq_len: Optional[int] = None, k_group_size: int = 128,
@@ -1359,24 +1557,31 @@ class MixedKVCache(_EngineBase):
                     raise ValueError(f"per_layer_bits[{i}]=({entry[0]},{entry[1]}) contains "
                                      f"unsupported bits; allowed values: {_MIXED_BITS}")
             per_layer_bits = [(int(a), int(b)) for a, b in per_layer_bits]
+        v_group_size = v_group_size if v_group_size is not None else k_group_size
         bits = per_layer_bits or [(int(k_bits), int(v_bits))] * num_layers
-        if any(b != (8, 4) for b in bits):
-            raise NotImplementedError("MixedKVCache: only K INT8 / V INT4 layers are built "
-                                      "(the fp16 and other ablation widths are not)")
-        if float(v_percentile) != 100.0:
-            raise NotImplementedError("MixedKVCache: percentile clipping of the V parameters "
-                                      "is not built (v_percentile=100)")
-        if k_group_size not in (8, 16, 32, 64, 128):
-            raise NotImplementedError(f"k_group_size must be 8, 16, 32, 64 or 128, got {k_group_size}")
+        for kb, vb in bits:
+            if (kb, vb) not in self._BUILT:
+                raise NotImplementedError(f"MixedKVCache: the ({kb}, {vb}) layer is not built (built: "
+                                          f"{sorted(self._BUILT)})")
+            if (kb, vb) == (8, 8) and k_group_size != v_group_size:
+                raise NotImplementedError("MixedKVCache (8, 8) needs k_group_size == v_group_size")
+        for gs in (k_group_size, v_group_size):
+            if gs not in (16, 32, 64, 128):
+                raise NotImplementedError(f"group sizes must be 16, 32, 64 or 128, got {gs}")
         _dyn_quantile(k_clip_percentile)  # (0, 100]
+        if any(vb == 4 for _, vb in bits):
+            _kivi_levels(v_percentile)
+        elif any(vb == 8 for _, vb in bits):
+            _dyn_quantile(v_percentile)
         self._init_common(num_layers, device, max_seq_len, decode_attn_impl, check_numerics)
         self.dtype = dtype
         self.k_group_size = int(k_group_size)
-        self.v_group_size = v_group_size if v_group_size is not None else k_group_size
+        self.v_group_size = int(v_group_size)
         self.k_clip_percentile = float(k_clip_percentile)
         self.v_percentile = float(v_percentile)
         self.k_bits, self.v_bits = int(k_bits), int(v_bits)
         self._per_layer_bits = per_layer_bits
+        self._bits = bits
         self.inv_tau = None
         self.use_attn_temperature = False
         n = num_layers
@@ -1400,47 +1605,69 @@ class MixedKVCache(_EngineBase):
         cap = self._layer_capacity[layer_id]
         if kc is not None and target <= cap:
             return
+        kb, vb = self._bits[layer_id]
         new_cap = self._new_capacity(layer_id, target, cap if kc is not None else 0)
         old = self._layer_seq_lens[layer_id]
-        G = 128 // self.k_group_size
-        nk = torch.empty(B, H, new_cap, 128, dtype=torch.int8, device=device)
-        nks = torch.empty(B, H, new_cap, G, dtype=torch.float16, device=device)
-        nv = torch.empty(B, H, new_cap, 64, dtype=torch.int8, device=device)
-        nvs = torch.empty(B, H, new_cap, dtype=torch.float32, device=device)
-        nvz = torch.empty_like(nvs)
+        new = {
+            "k": torch.empty(B, H, new_cap, 128, dtype=torch.int8 if kb == 8 else torch.float16, device=device),
+            "ks": (torch.empty(B, H, new_cap, 128 // self.k_group_size, dtype=torch.float16, device=device)
+                   if kb == 8 else None),
+            "v": torch.empty(B, H, new_cap, 64 if vb == 4 else 128,
+                             dtype=torch.float16 if vb == 16 else torch.int8, device=device),
+            "vs": (torch.empty(B, H, new_cap, dtype=torch.float32, device=device) if vb == 4 else
+                   torch.empty(B, H, new_cap, 128 // self.v_group_size, dtype=torch.float16, device=device)
+                   if vb == 8 else None),
+            "vz": torch.empty(B, H, new_cap, dtype=torch.float32, device=device) if vb == 4 else None,
+        }
+        olds = {"k": kc, "ks": self._k_scale[layer_id], "v": self._v_cache[layer_id],
+                "vs": self._v_scale[layer_id], "vz": self._v_zp[layer_id]}
         if kc is not None and old > 0:
-            nk[:, :, :old] = kc[:, :, :old]
-            nks[:, :, :old] = self._k_scale[layer_id][:, :, :old]
-            nv[:, :, :old] = self._v_cache[layer_id][:, :, :old]
-            nvs[:, :, :old] = self._v_scale[layer_id][:, :, :old]
-            nvz[:, :, :old] = self._v_zp[layer_id][:, :, :old]
-        self._k_cache[layer_id], self._k_scale[layer_id] = nk, nks
-        self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id] = nv, nvs, nvz
+            for key, t in new.items():
+                if t is not None:
+                    t[:, :, :old] = olds[key][:, :, :old]
+        self._k_cache[layer_id], self._k_scale[layer_id] = new["k"], new["ks"]
+        self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id] = new["v"], new["vs"], new["vz"]
         self._layer_capacity[layer_id] = new_cap
         self._steps[layer_id] = self._apps[layer_id] = None
 
     def _params(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status) -> Tuple:
-        """kvq_append_params of K (INT8 dynamic) and V (INT4_KIVI per token) writing at slot
-        pos; the one-token blocks of a decode step are kept per layer."""
+        """kvq_append_params of the quantized sides (K INT8 dynamic, V INT4_KIVI per token or
+        INT8 dynamic) writing at slot pos, None for a 16-bit side; the one-token blocks of a
+        decode step are kept per layer."""
         S = k.shape[2]
+        kb, vb = self._bits[layer_id]
         ent = self._apps[layer_id] if S == 1 else None
         if ent is None:
-            pk, pv = C.AppendParams(), C.AppendParams()
-            kc, ks = self._k_cache[layer_id], self._k_scale[layer_id]
-            vc, vs, vz = self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id]
-            _fill_append(pk, C.KVQ_FMT_INT8_SYM, k, self.k_group_size, kc, pos, None)
-            pk.dyn_quantile = _dyn_quantile(self.k_clip_percentile)
-            pk.scale_out, pk.scale_out_dtype = ks.data_ptr(), C.KVQ_DTYPE_F16
-            pk.so_stride_b, pk.so_stride_h, pk.so_stride_t, pk.so_stride_g = ks.stride()
-            _fill_append(pv, C.KVQ_FMT_INT4_KIVI, v, 32, vc, pos, None)
-            pv.scale_out, pv.zp_out, pv.scale_out_dtype = vs.data_ptr(), vz.data_ptr(), C.KVQ_DTYPE_F32
-            pv.so_stride_b, pv.so_stride_h, pv.so_stride_t = vs.stride()
+            pk = pv = None
+            if kb == 8:
+                pk = C.AppendParams()
+                ks = self._k_scale[layer_id]
+                _fill_append(pk, C.KVQ_FMT_INT8_SYM, k, self.k_group_size, self._k_cache[layer_id], pos, None)
+                pk.dyn_quantile = _dyn_quantile(self.k_clip_percentile)
+                pk.scale_out, pk.scale_out_dtype = ks.data_ptr(), C.KVQ_DTYPE_F16
+                pk.so_stride_b, pk.so_stride_h, pk.so_stride_t, pk.so_stride_g = ks.stride()
+            if vb == 4:
+                pv = C.AppendParams()
+                vc, vs, vz = self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id]
+                _fill_append(pv, C.KVQ_FMT_INT4_KIVI, v, 32, vc, pos, None)
+                pv.scale_out, pv.zp_out, pv.scale_out_dtype = vs.data_ptr(), vz.data_ptr(), C.KVQ_DTYPE_F32
+                pv.so_stride_b, pv.so_stride_h, pv.so_stride_t = vs.stride()
+                pv.dyn_quantile_lo, pv.dyn_quantile = _kivi_levels(self.v_percentile)
+            elif vb == 8:
+                pv = C.AppendParams()
+                vs = self._v_scale[layer_id]
+                _fill_append(pv, C.KVQ_FMT_INT8_SYM, v, self.v_group_size, self._v_cache[layer_id], pos, None)
+                pv.dyn_quantile = _dyn_quantile(self.v_percentile)
+                pv.scale_out, pv.scale_out_dtype = vs.data_ptr(), C.KVQ_DTYPE_F16
+                pv.so_stride_b, pv.so_stride_h, pv.so_stride_t, pv.so_stride_g = vs.stride()
             ent = (pk, pv)
             if S == 1:
                 self._apps[layer_id] = ent
         pk, pv = ent
         sptr = None if status is None else status.data_ptr()
         for p, x, off in ((pk, k, 0), (pv, v, 8)):
+            if p is None:
+                continue
             p.x = x.data_ptr()
             p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride()[:3]
             p.seq_new = S
@@ -1460,16 +1687,23 @@ class MixedKVCache(_EngineBase):
             k = k.contiguous()
         if v.stride(-1) != 1:
             v = v.contiguous()
+        kb, vb = self._bits[layer_id]
         self._ensure(layer_id, B, H, old + S, k.device)
-        status = self._status_buf(k.device) if self.check_numerics else None
-        pk, pv = self._params(layer_id, k, v, old, status)
-        C.check(C.lib().kvq_quant_append(ctypes.byref(pk), ctypes.byref(pv),
-                                         ctypes.c_void_p(C.stream_handle(k.device))))
-        if status is not None:
-            st = self._read_status()
-            if st[0] & 1 or st[2] & 1:
-                raise ValueError(f"MixedKVCache append: {'K' if st[0] & 1 else 'V'} input contains "
-                                 "NaN or Inf — refusing to quantize corrupt data")
+        if kb == 16:
+            self._k_cache[layer_id][:, :, old:old + S] = k
+        if vb == 16:
+            self._v_cache[layer_id][:, :, old:old + S] = v
+        if kb != 16 or vb != 16:
+            status = self._status_buf(k.device) if self.check_numerics else None
+            pk, pv = self._params(layer_id, k, v, old, status)
+            C.check(C.lib().kvq_quant_append(None if pk is None else ctypes.byref(pk),
+                                             None if pv is None else ctypes.byref(pv),
+                                             ctypes.c_void_p(C.stream_handle(k.device))))
+            if status is not None:
+                st = self._read_status()
+                if st[0] & 1 or st[2] & 1:
+                    raise ValueError(f"MixedKVCache append: {'K' if st[0] & 1 else 'V'} input contains "
+                                     "NaN or Inf — refusing to quantize corrupt data")
         n = old + S
         self._layer_seq_lens[layer_id] = n
         self._seq_len = max(self._layer_seq_lens)
@@ -1487,18 +1721,30 @@ class MixedKVCache(_EngineBase):
         return self._layer_seq_lens[layer_id]
 
     def get_mixed_tensors(self, layer_id: int):
-        """(k_int8, k_scale16, v_packed, v_scale, v_zp) over the stored tokens."""
+        """(k_store, k_scale16, v_store, v_scale, v_zp) over the stored tokens: K int8 codes or
+        fp16 values, V packed / int8 codes or fp16 values; None where a side has no such
+        parameter."""
         n = self._check_layer(layer_id)
-        return (self._k_cache[layer_id][:, :, :n], self._k_scale[layer_id][:, :, :n],
-                self._v_cache[layer_id][:, :, :n], self._v_scale[layer_id][:, :, :n],
-                self._v_zp[layer_id][:, :, :n])
+
+        def sl(t):
+            return None if t is None else t[:, :, :n]
+
+        return (sl(self._k_cache[layer_id]), sl(self._k_scale[layer_id]), sl(self._v_cache[layer_id]),
+                sl(self._v_scale[layer_id]), sl(self._v_zp[layer_id]))
 
     def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
-        """Dequantised K, V in self.dtype (mixed_kv_cache.py:170-190, 242-254): K = code x
-        scale of its group, V = code x s + z of its token, in fp32, then cast."""
-        kc, ks, vp, vs, vz = self.get_mixed_tensors(layer_id)
-        k = _deq_sym(kc, ks.float()).to(self.dtype)
-        v = (_unpack(vp).float() * vs.unsqueeze(-1) + vz.unsqueeze(-1)).to(self.dtype)
+        """Dequantised K, V in self.dtype (mixed_kv_cache.py:170-190, 242-254): a symmetric
+        side is code x the scale of its group, the asymmetric V code x s + z of its token, in
+        fp32, then cast."""
+        kc, ks, vc, vs, vz = self.get_mixed_tensors(layer_id)
+        kb, vb = self._bits[layer_id]
+        k = kc.to(self.dtype) if kb == 16 else _deq_sym(kc, ks.float()).to(self.dtype)
+        if vb == 16:
+            v = vc.to(self.dtype)
+        elif vb == 8:
+            v = _deq_sym(vc, vs.float()).to(self.dtype)
+        else:
+            v = (_unpack(vc).float() * vs.unsqueeze(-1) + vz.unsqueeze(-1)).to(self.dtype)
         return k, v
 
     def _step_for(self, layer_id: int, q_heads: int):
@@ -1506,13 +1752,23 @@ class MixedKVCache(_EngineBase):
         st = self._steps[layer_id]
         if st is not None and st.key == (q_heads, kc.data_ptr()):
             return st
-        from .kernels import LayerStep, kv_view_kivi, kv_view_tok
+        from .kernels import LayerStep, kv_view_fp16, kv_view_kivi, kv_view_tok
 
+        kb, vb = self._bits[layer_id]
         B, H = kc.shape[0], kc.shape[1]
         ks, vc, vs, vz = self._k_scale[layer_id], self._v_cache[layer_id], self._v_scale[layer_id], \
             self._v_zp[layer_id]
-        st = LayerStep(C.KVQ_FMT_INT8_SYM, kv_view_tok(kc, ks), C.KVQ_FMT_INT4_KIVI,
-                       kv_view_kivi(vc, vs, vz, False), B, q_heads, H, self.k_group_size,
+        if kb == 8:
+            kf, kview = C.KVQ_FMT_INT8_SYM, kv_view_tok(kc, ks)
+        else:
+            kf, kview = C.KVQ_FMT_FP16, kv_view_fp16(kc)
+        if vb == 4:
+            vf, vview = C.KVQ_FMT_INT4_KIVI, kv_view_kivi(vc, vs, vz, False)
+        elif vb == 8:
+            vf, vview = C.KVQ_FMT_INT8_SYM, kv_view_tok(vc, vs)
+        else:
+            vf, vview = C.KVQ_FMT_FP16, kv_view_fp16(vc)
+        st = LayerStep(kf, kview, vf, vview, B, q_heads, H, self.k_group_size if kb == 8 else 32,
                        kc.device, keepalive=(kc, ks, vc, vs, vz))
         st.key = (q_heads, kc.data_ptr())
         self._steps[layer_id] = st

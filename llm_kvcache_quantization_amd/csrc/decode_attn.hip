@@ -560,6 +560,15 @@ static const void* selected_kernel() {
 enum Family { kNone = 0, kI8I8_16, kI8I8_32, kI4I4_16, kI4I4_32, kA4A4, kA4A4o, kI8A4_16, kI8A4_32,
               kKivi, kI8Kv };
 
+// the KIVI family's formats: per-channel K / per-token V asymmetric codes, or fp16 values
+static bool kivi_fmt(int f) {
+  return f == KVQ_FMT_INT4_KIVI || f == KVQ_FMT_INT8_KIVI || f == KVQ_FMT_FP16;
+}
+// bytes of one token's row of a format
+static int row_bytes_of(int f) {
+  return f == KVQ_FMT_FP16 ? 2 * kD : (f == KVQ_FMT_INT8_SYM || f == KVQ_FMT_INT8_KIVI) ? kD : kD / 2;
+}
+
 static Family family(int kf, int vf, int ksf32, int vsf32, int kout) {
   if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT8_SYM && ksf32 == vsf32)
     return ksf32 ? kI8I8_32 : kI8I8_16;
@@ -567,8 +576,9 @@ static Family family(int kf, int vf, int ksf32, int vsf32, int kout) {
     return ksf32 ? kI4I4_32 : kI4I4_16;
   if (kf == KVQ_FMT_INT4_ASYM && vf == KVQ_FMT_INT4_ASYM) return kout ? kA4A4o : kA4A4;
   if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT4_ASYM) return ksf32 ? kI8A4_32 : kI8A4_16;
-  if (kf == KVQ_FMT_INT4_KIVI && vf == KVQ_FMT_INT4_KIVI) return kKivi;  // tiled kernel only
-  if (kf == KVQ_FMT_INT8_SYM && vf == KVQ_FMT_INT4_KIVI) return kI8Kv;  // tiled kernel only
+  if (kivi_fmt(kf) && kivi_fmt(vf)) return kKivi;  // tiled kernel only
+  if (kf == KVQ_FMT_INT8_SYM && (vf == KVQ_FMT_INT4_KIVI || vf == KVQ_FMT_FP16))
+    return kI8Kv;  // tiled kernel only
   return kNone;
 }
 
@@ -626,7 +636,8 @@ static bool static_over_bt(const kvq_kv_view& v, const kvq_decode_params* p) {
 // per token).
 static int tok_family(const kvq_decode_params* p) {
   if (p->v.layout != KVQ_LAYOUT_ROWS) return kTiledNone;
-  const bool kivi_v = p->k_format == KVQ_FMT_INT8_SYM && p->v_format == KVQ_FMT_INT4_KIVI;
+  const bool kivi_v = p->k_format == KVQ_FMT_INT8_SYM &&
+                      (p->v_format == KVQ_FMT_INT4_KIVI || p->v_format == KVQ_FMT_FP16);
   if (p->k_format != p->v_format && !kivi_v) return kTiledNone;
   const bool i4 = p->k_format == KVQ_FMT_INT4_SYM;
   if (!i4 && p->k_format != KVQ_FMT_INT8_SYM) return kTiledNone;
@@ -643,8 +654,11 @@ static int tok_family(const kvq_decode_params* p) {
            v.scale_stride_b >= 0 && v.scale_stride_h >= 0 && v.scale_stride_t >= 0;
   };
   if (kivi_v) {
+    if (!ok(p->k)) return kTiledNone;
+    if (p->v_format == KVQ_FMT_FP16)  // fp16 V in dense 256-byte rows
+      return p->v.stride_t == 2 * kD ? (gs == 16 ? kTiledT8Fg16 : kTiledT8F) : kTiledNone;
     // V codes in dense 64-byte rows, fp32 scale / zero-point per token (checked by check_view)
-    if (!ok(p->k) || p->v.stride_t != kD / 2 || p->v.scale_stride_t != 1) return kTiledNone;
+    if (p->v.stride_t != kD / 2 || p->v.scale_stride_t != 1) return kTiledNone;
     return gs == 16 ? kTiledT8Kvg16 : kTiledT8Kv;
   }
   if (!ok(p->k) || !ok(p->v)) return kTiledNone;
@@ -654,11 +668,16 @@ static int tok_family(const kvq_decode_params* p) {
 
 static int tiled_family(const kvq_decode_params* p) {
   const bool vt = p->v.layout == KVQ_LAYOUT_TILE32;
-  if (p->k_format == KVQ_FMT_INT4_KIVI)
-    return (p->v_format == KVQ_FMT_INT4_KIVI && !vt && p->k.stride_t == kD / 2 &&
-            p->v.stride_t == kD / 2)
-               ? kTiledKivi
-               : kTiledNone;
+  if (kivi_fmt(p->k_format)) {
+    if (!kivi_fmt(p->v_format) || vt || p->k.stride_t != row_bytes_of(p->k_format) ||
+        p->v.stride_t != row_bytes_of(p->v_format))
+      return kTiledNone;
+    const auto idx = [](int f) { return f == KVQ_FMT_INT4_KIVI ? 0 : f == KVQ_FMT_INT8_KIVI ? 1 : 2; };
+    static const int fams[3][3] = {{kTiledKivi, kTiledKv48, kTiledKv4F},
+                                   {kTiledKv84, kTiledKv88, kTiledKv8F},
+                                   {kTiledKvF4, kTiledKvF8, kTiledKvFF}};
+    return fams[idx(p->k_format)][idx(p->v_format)];
+  }
   if (p->k_format == KVQ_FMT_INT4_ASYM)
     return (p->v_format == KVQ_FMT_INT4_ASYM && vt) ? (p->k.n_outlier > 0 ? kTiledA4A4o : kTiledA4A4)
                                                      : kTiledNone;
@@ -740,39 +759,45 @@ static int check_view(const kvq_kv_view& v, int fmt, bool is_k, const char* name
     if (v.stride_t != kD / 2)
       return fail(KVQ_ERR_INVALID, n + ": TILE32 needs stride_t == 64");
   }
-  if (!v.scale) return fail(KVQ_ERR_INVALID, n + ": scale is NULL");
-  const int row_bytes = fmt == KVQ_FMT_INT8_SYM ? kD : kD / 2;
+  if (!v.scale && fmt != KVQ_FMT_FP16) return fail(KVQ_ERR_INVALID, n + ": scale is NULL");
+  const int row_bytes = row_bytes_of(fmt);
   if (v.stride_t < row_bytes)
     return fail(KVQ_ERR_INVALID, n + ": token stride smaller than a code row");
   // lane byte offsets within a 32-token tile are 32-bit
   if (v.stride_t > ((int64_t)1 << 24) || v.outlier_stride_t > ((int64_t)1 << 22))
     return fail(KVQ_ERR_UNSUPPORTED, n + ": token stride too large");
-  const int need = is_k ? 16 : (fmt == KVQ_FMT_INT8_SYM ? 8 : 4);
+  const int need = (is_k || fmt == KVQ_FMT_FP16) ? 16 : (row_bytes == kD ? 8 : 4);
   if (!aligned(v.codes, need) || v.stride_b % need || v.stride_h % need || v.stride_t % need)
     return fail(KVQ_ERR_UNSUPPORTED,
                 n + ": code rows must be " + std::to_string(need) + "-byte aligned");
+  if (fmt == KVQ_FMT_FP16) {
+    if (v.layout != KVQ_LAYOUT_ROWS || v.stride_t != 2 * kD)
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": FP16 needs dense 256-byte token rows");
+    if (v.n_outlier != 0) return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
+    return KVQ_OK;
+  }
   if (v.scale_dtype != KVQ_DTYPE_F16 && v.scale_dtype != KVQ_DTYPE_F32)
     return fail(KVQ_ERR_INVALID, n + ": scale_dtype must be F16 or F32");
-  if (fmt == KVQ_FMT_INT4_KIVI) {
+  if (fmt == KVQ_FMT_INT4_KIVI || fmt == KVQ_FMT_INT8_KIVI) {
     if (v.layout != KVQ_LAYOUT_ROWS)
-      return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI codes are in token rows");
-    if (v.stride_t != kD / 2)
-      return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI needs dense 64-byte token rows");
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI codes are in token rows");
+    if (v.stride_t != row_bytes)
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI needs dense token rows (64 bytes INT4, 128 INT8)");
     if (v.scale_dtype != KVQ_DTYPE_F32 || !v.zero_point)
-      return fail(KVQ_ERR_INVALID, n + ": INT4_KIVI needs fp32 scale and zero_point");
+      return fail(KVQ_ERR_INVALID, n + ": KIVI needs fp32 scale and zero_point");
     if (v.n_outlier != 0) return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
     if (is_k) {
       // the 8 channels of a lane are read as two 16-byte vectors
       if (v.scale_stride_g != 1)
-        return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI K parameters need contiguous channels");
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI K parameters need contiguous channels");
       if (!aligned(v.scale, 16) || !aligned(v.zero_point, 16) || v.scale_stride_b % 4 ||
           v.scale_stride_h % 4)
-        return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI K parameter rows must be 16-byte aligned");
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI K parameter rows must be 16-byte aligned");
     } else {
       if (v.scale_stride_t != 1)
-        return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI V parameters need contiguous tokens");
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI V parameters need contiguous tokens");
       if (!aligned(v.scale, 4) || !aligned(v.zero_point, 4))
-        return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI V parameters must be 4-byte aligned");
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI V parameters must be 4-byte aligned");
     }
     return KVQ_OK;
   }
@@ -908,16 +933,18 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
     return fail(KVQ_ERR_UNSUPPORTED,
                 "TILE32 V needs INT4_ASYM K or INT8 K with a static group-32 scale in dense rows");
   if (fam == kKivi && !tiled)
-    return fail(KVQ_ERR_UNSUPPORTED, "INT4_KIVI K and V need dense 64-byte token rows");
+    return fail(KVQ_ERR_UNSUPPORTED,
+                "KIVI-family K and V (INT4_KIVI, INT8_KIVI, FP16) need dense token rows");
   if (fam == kI8Kv && !tiled)
     return fail(KVQ_ERR_UNSUPPORTED,
-                "INT8 K with INT4_KIVI V needs dense K rows with fp16 per-token scales (groups of "
-                "16 or more, contiguous) and dense 64-byte V rows");
+                "INT8 K with INT4_KIVI or FP16 V needs dense K rows with fp16 per-token scales "
+                "(groups of 16 or more, contiguous) and dense V rows");
   if (tiled && p->k_format == KVQ_FMT_INT4_ASYM &&
       (p->k.stride_t != kD / 2 || (p->k.n_outlier && p->k.outlier_stride_t != 4)))
     return fail(KVQ_ERR_UNSUPPORTED, "with TILE32 V, K rows and outlier rows must be dense");
   // buffer loads address each (b, head) slab with 32-bit byte offsets
-  if (tiled && (p->capacity + kTile) * p->k.stride_t >= ((int64_t)1 << 31))
+  if (tiled && (p->capacity + kTile) * (p->k.stride_t > p->v.stride_t ? p->k.stride_t : p->v.stride_t) >=
+                   ((int64_t)1 << 31))
     return fail(KVQ_ERR_UNSUPPORTED, "capacity too large for one (b, head) slab");
   int rc = check_view(p->k, kf, true, "k", gs);
   if (rc) return rc;
@@ -1169,4 +1196,4 @@ extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_appe
 }
 
 extern "C" const char* kvq_last_error(void) { return g_last_error.c_str(); }
-extern "C" int32_t kvq_abi_version(void) { return 4; }
+extern "C" int32_t kvq_abi_version(void) { return 5; }

@@ -425,6 +425,10 @@ enum TiledFam {
   kTiledT8Kv,   // INT8_SYM K with per-token fp16 scales, INT4_KIVI V (per-token fp32), rows
   kTiledT8Kvg16,  // the same with K groups of 16
   kTiledKivi,   // INT4_KIVI K (per-channel) and V (per-token), token rows
+  // the KIVI family's other (K, V) pairs: 4 = INT4_KIVI, 8 = INT8_KIVI, F = FP16
+  kTiledKv48, kTiledKv4F, kTiledKv84, kTiledKv88, kTiledKv8F, kTiledKvF4, kTiledKvF8, kTiledKvFF,
+  kTiledT8F,    // INT8_SYM K with per-token fp16 scales, FP16 V
+  kTiledT8Fg16,  // the same with K groups of 16
 };
 // kernel of family fam for n_rep query heads per kv head, or nullptr
 const void* tiled_kernel(int fam, int n_rep);

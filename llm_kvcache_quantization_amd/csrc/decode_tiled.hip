@@ -925,6 +925,372 @@ struct VKiviRowT {
   }
 };
 
+// ---- The KIVI family with 8-bit codes and 16-bit sides: the reference's quant_bits=8 KIVI
+// cache (src/cache/kivi_style_cache.py) and the per-layer (k_bits, v_bits) pairs of its
+// allocator and mixed caches (src/cache/role_aware_allocator_cache.py,
+// src/cache/mixed_kv_cache.py), where a 16-bit side stores fp16 values as they come.
+
+// Two int8 codes (the low bytes of the two halves of x, the high bytes zero) -> the exact
+// fp16 pair: x ^ 0x64806480 gives 1024 + (c + 128), minus 1152 gives c.
+__device__ __forceinline__ uint32_t i8pair_exact(uint32_t x) {
+  const half2v off = {(half_t)1152.0f, (half_t)1152.0f};
+  return as_u32(as_h2(x ^ 0x64806480u) - off);
+}
+
+// K of the 8-bit KIVI layout: int8 codes in 128-byte token rows with per-channel fp32 scale
+// s_d and zero-point z_d per (b, kv head).  logit = sum_d q'_d (c_d s_d + z_d): the codes
+// enter the MFMA exactly (i8pair_exact), q'_d s_d as a hi + lo pair of fp16 operands (two
+// MFMAs per slice, as KKiviT), and the constant sum_d q'_d z_d starts the accumulator.
+// Lane (row, lg) of row block rb reads bytes [32 lg, 32 lg + 32) of token 16 rb + row.
+struct KKivi8T {
+  static constexpr int kMergeBatch = 8;
+  static constexpr bool kPackPV = false;
+  using QInT = KiviQIn;
+  static constexpr bool kAppend = false;
+  static constexpr bool kAsym = false;
+  static constexpr bool kGsAny = false;
+  static constexpr bool kOut = false;
+  static constexpr bool kSub24 = false;  // logits at unit scale
+  half8v qh[4], ql[4];
+  float bias;
+  rsrc_t rk;
+  uint32_t vk;
+  struct Raw {
+    u32x4 w[4];  // [2 rb + i]: bytes [32 lg + 16 i, + 16) of token 16 rb + row
+  };
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kD));
+    vk = (uint32_t)(col * kD + 32 * lg);
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, KiviQIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.oc = int4{-1, -1, -1, -1};
+    const int64_t o = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh + 32 * lg + 8 * (wave & 3);
+    const float* ps = reinterpret_cast<const float*>(a.k.scale) + o;
+    const float* pz = reinterpret_cast<const float*>(a.k.zp) + o;
+    in.ks[0] = *reinterpret_cast<const float4v*>(ps);
+    in.ks[1] = *reinterpret_cast<const float4v*>(ps + 4);
+    in.kz[0] = *reinterpret_cast<const float4v*>(pz);
+    in.kz[1] = *reinterpret_cast<const float4v*>(pz + 4);
+  }
+  // channel slice j (channels 32 lg + 8 j + e, in channel order)
+  __device__ void setup_q(const DecodeArgs& a, const KiviQIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15, lg = lane >> 4;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    float part = 0.f;
+    half_t vh[8], vl[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      const float qd = valid ? (float)qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : 0.f;
+      split_h(qd * in.ks[e >> 2][e & 3], vh[e], vl[e]);
+      part = fmaf(qd, in.kz[e >> 2][e & 3], part);
+    }
+    part = wave_sum_xor_groups(part);
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+    sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
+    if (lg == 0) sh.bias[j][col] = part;
+  }
+  __device__ void finish_setup(const QShareLds& sh, const KiviQIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+      ql[j] = __builtin_bit_cast(half8v, sh.ql[j][lane]);
+    }
+    const int col = lane & 15;
+    bias = (sh.bias[0][col] + sh.bias[1][col]) + (sh.bias[2][col] + sh.bias[3][col]);
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kD : kOutOfRange);
+    r.w[0] = bload4(rk, v, 0);
+    r.w[1] = bload4(rk, v + 16, 0);
+    r.w[2] = bload4(rk, v + 16 * kD, 0);
+    r.w[3] = bload4(rk, v + 16 * kD + 16, 0);
+  }
+  __device__ __forceinline__ static half8v codes8(uint32_t lo, uint32_t hi) {
+    return pack8(i8pair_exact(perm_b32(0u, lo, 0x0C010C00u)), i8pair_exact(perm_b32(0u, lo, 0x0C030C02u)),
+                 i8pair_exact(perm_b32(0u, hi, 0x0C010C00u)), i8pair_exact(perm_b32(0u, hi, 0x0C030C02u)));
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    (void)nc;
+    float4v c0 = {bias, bias, bias, bias};
+    float4v c1 = c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 w0 = r.w[j >> 1], w1 = r.w[2 + (j >> 1)];
+      const half8v a0 = codes8((j & 1) ? w0.z : w0.x, (j & 1) ? w0.w : w0.y);
+      const half8v a1 = codes8((j & 1) ? w1.z : w1.x, (j & 1) ? w1.w : w1.y);
+      c0 = mfma16x16x32(a0, qh[j], c0);
+      c1 = mfma16x16x32(a1, qh[j], c1);
+      c0 = mfma16x16x32(a0, ql[j], c0);
+      c1 = mfma16x16x32(a1, ql[j], c1);
+    }
+    x0 = c0;
+    x1 = c1;
+  }
+};
+
+// fp16 K in 256-byte token rows (a 16-bit K side): the logits are the fp32 dot products of
+// the stored fp16 k with q' = fp16(q * inv_tau).  Lane (row, lg) of row block rb reads bytes
+// [64 lg, 64 lg + 64) of token 16 rb + row: channels 32 lg + 8 j .. + 7 are slice j.
+struct KF16T {
+  static constexpr int kMergeBatch = 8;
+  static constexpr bool kPackPV = false;
+  using QInT = QIn;
+  static constexpr bool kAppend = false;
+  static constexpr bool kAsym = false;
+  static constexpr bool kGsAny = false;
+  static constexpr bool kOut = false;
+  static constexpr bool kSub24 = false;
+  static constexpr int kRow = 2 * kD;
+  half8v qh[4];
+  rsrc_t rk;
+  uint32_t vk;
+  struct Raw {
+    u32x4 w[8];  // [4 rb + j]: slice j of token 16 rb + row
+  };
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kRow));
+    vk = (uint32_t)(col * kRow + 64 * lg);
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.s = (half_t)1.0f;
+    in.z = (half_t)0.0f;
+    in.oc = int4{-1, -1, -1, -1};
+  }
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    half_t vh[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      vh[e] = valid ? qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+  }
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kRow : kOutOfRange);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      r.w[j] = bload4(rk, v + 16 * j, 0);
+      r.w[4 + j] = bload4(rk, v + 16 * kRow + 16 * j, 0);
+    }
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    (void)nc;
+    float4v c0 = {0.f, 0.f, 0.f, 0.f};
+    float4v c1 = c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c0 = mfma16x16x32(__builtin_bit_cast(half8v, r.w[j]), qh[j], c0);
+      c1 = mfma16x16x32(__builtin_bit_cast(half8v, r.w[4 + j]), qh[j], c1);
+    }
+    x0 = c0;
+    x1 = c1;
+  }
+};
+
+// V of the 8-bit KIVI layout in 128-byte token rows, per-token fp32 s_t, z_t: lane (col, lg)
+// reads the 8 bytes of channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens T(k)
+// (as VI8RowT) and the tokens' s, z (as VKiviRowT).  The codes enter the MFMA exactly
+// (i8pair_exact), the B operand is w = p s_t as a hi + lo pair (two MFMAs per channel), and
+//   sum_t p v = sum_t w c + Cz,   Cz = sum_t p z_t (fp32, rescaled with l by the softmax).
+struct VKivi8RowT {
+  static constexpr bool kPackedPV = false;
+  static constexpr bool kTile32 = false;
+  rsrc_t rv, rs, rz;
+  uint32_t vv, vp;
+  float ex[2];  // unused, Cz
+  struct Raw {
+    u32x2 w[8];          // token T(k): bytes 8 col .. 8 col + 7
+    float4v s[2], z[2];  // tokens 4 lg + i, 16 + 4 lg + i
+  };
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * kD));
+    vv = (uint32_t)((4 * lg) * kD + 8 * col);
+    const int64_t po = (int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh;
+    rs = buffer_rsrc(reinterpret_cast<const float*>(a.v.scale) + po, (uint32_t)(a.cap * 4));
+    rz = buffer_rsrc(reinterpret_cast<const float*>(a.v.zp) + po, (uint32_t)(a.cap * 4));
+    vp = (uint32_t)(4 * lg) * 4u;
+    ex[0] = ex[1] = 0.f;
+  }
+  __device__ __forceinline__ float* extra() { return ex; }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * kD : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      r.w[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(v + t * kD), 0, kBufNT));
+    }
+    const uint32_t p = vp + (valid ? (uint32_t)tok * 4u : kOutOfRange);
+    r.s[0] = __builtin_bit_cast(float4v, bload4(rs, p, 0));
+    r.s[1] = __builtin_bit_cast(float4v, bload4(rs, p + 64u, 0));
+    r.z[0] = __builtin_bit_cast(float4v, bload4(rz, p, 0));
+    r.z[1] = __builtin_bit_cast(float4v, bload4(rz, p + 64u, 0));
+  }
+  // tokens at or past the context in the last, partial tile: parameters 0
+  __device__ __forceinline__ void mask(Raw& r, int tt, int ctx, int lg) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (tt + 4 * lg + i >= ctx) r.s[0][i] = r.z[0][i] = 0.f;
+      if (tt + 16 + 4 * lg + i >= ctx) r.s[1][i] = r.z[1][i] = 0.f;
+    }
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v plo, float4v acc[8],
+                                      const NibConsts& nc) {
+    (void)nc;
+    float sk[8], wk[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sk[i] = r.s[0][i];
+      sk[4 + i] = r.s[1][i];
+      wk[i] = r.z[0][i];
+      wk[4 + i] = r.z[1][i];
+    }
+    float cz = ex[1];
+    uint32_t ph[4], pl[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float p0 = (float)pb[2 * q] + (float)plo[2 * q];
+      const float p1 = (float)pb[2 * q + 1] + (float)plo[2 * q + 1];
+      cz = fmaf(p0, wk[2 * q], cz);
+      cz = fmaf(p1, wk[2 * q + 1], cz);
+      half_t h0, l0, h1, l1;
+      split_h(p0 * sk[2 * q], h0, l0);
+      split_h(p1 * sk[2 * q + 1], h1, l1);
+      ph[q] = as_u32(half2v{h0, h1});
+      pl[q] = as_u32(half2v{l0, l1});
+    }
+    ex[1] = cz;
+    const half8v wh = pack8(ph[0], ph[1], ph[2], ph[3]);
+    const half8v wl = pack8(pl[0], pl[1], pl[2], pl[3]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      // byte c % 4 of the tokens T(2p) and T(2p + 1) into the low bytes of the two halves
+      const uint32_t sel = (uint32_t)(c & 3) | 0x0C00u | ((uint32_t)(4 + (c & 3)) << 16) | 0x0C000000u;
+      uint32_t R[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t lo = (c >> 2) ? r.w[2 * p].y : r.w[2 * p].x;
+        const uint32_t hi = (c >> 2) ? r.w[2 * p + 1].y : r.w[2 * p + 1].x;
+        R[p] = i8pair_exact(perm_b32(hi, lo, sel));
+      }
+      const half8v av = pack8(R[0], R[1], R[2], R[3]);
+      acc[c] = mfma16x16x32(av, wh, acc[c]);
+      acc[c] = mfma16x16x32(av, wl, acc[c]);
+    }
+  }
+  // acc[mb][r] += Cz, summed over the lane groups (the k-slots of a head)
+  __device__ __forceinline__ void finalize(float4v acc[8], int lane) {
+    (void)lane;
+    const float cz = wave_sum_xor_groups(ex[1]);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mb][r] += cz;
+  }
+};
+
+// fp16 V in 256-byte token rows (a 16-bit V side): lane (col, lg) reads the 16 bytes of
+// channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens; the A operand of channel
+// 8 col + c is the stored v of the 8 tokens (one v_perm_b32 per token pair), so acc / l is
+// the output.
+struct VF16RowT {
+  static constexpr bool kPackedPV = false;
+  static constexpr bool kTile32 = false;
+  static constexpr int kRow = 2 * kD;
+  __device__ __forceinline__ void finalize(float4v*, int) const {}
+  __device__ __forceinline__ float* extra() { return nullptr; }
+  rsrc_t rv;
+  uint32_t vv;
+  struct Raw {
+    u32x4 w[8];  // token T(k): channels 8 col .. 8 col + 7
+  };
+  // tokens at or past the context in the last, partial tile read as 0: their probability is
+  // 0, but the memory may hold any fp16 bits, and 0 x inf or 0 x NaN would reach acc
+  __device__ __forceinline__ void mask(Raw& r, int tt, int ctx, int lg) const {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int t = tt + (k < 4 ? 4 * lg + k : 12 + 4 * lg + k);
+      if (t >= ctx) r.w[k] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * kRow));
+    vv = (uint32_t)((4 * lg) * kRow + 16 * col);
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * kRow : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      r.w[k] = bload4(rv, v + t * kRow, 0);
+    }
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
+                                      const NibConsts& nc) const {
+    (void)nc;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      // half c % 2 of dword c / 2 of the tokens T(2p), T(2p + 1) -> the two halves
+      const uint32_t b0 = 2u * (uint32_t)(c & 1);
+      const uint32_t sel = b0 | ((b0 + 1) << 8) | ((b0 + 4) << 16) | ((b0 + 5) << 24);
+      uint32_t R[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) R[p] = perm_b32(r.w[2 * p + 1][c >> 1], r.w[2 * p][c >> 1], sel);
+      const half8v av = pack8(R[0], R[1], R[2], R[3]);
+      acc[c] = mfma16x16x32(av, pb, acc[c]);
+      acc[c] = mfma16x16x32(av, pl, acc[c]);
+    }
+  }
+};
+
 // ---- Per-token scales: INT8 codes with fp16 scales or packed INT4-symmetric codes with fp32
 // scales per (b, kv head, token, group), in token rows (the reference's dynamic, adaptive and
 // group-rescue caches, src/cache/int8_cache.py:298-488, src/cache/int4_cache.py:298-590, read
@@ -1588,6 +1954,16 @@ const void* tiled_ptr_fam(int fam) {
     case kTiledT8Kv: return tiled_ptr<KTokT<false, 1>, VKiviRowT, PACK8>();
     case kTiledT8Kvg16: return tiled_ptr<KTokT<false, 2>, VKiviRowT, PACK8>();
     case kTiledKivi: return tiled_ptr<KKiviT, VKiviRowT, PACK8>();
+    case kTiledKv48: return tiled_ptr<KKiviT, VKivi8RowT, PACK8>();
+    case kTiledKv4F: return tiled_ptr<KKiviT, VF16RowT, PACK8>();
+    case kTiledKv84: return tiled_ptr<KKivi8T, VKiviRowT, PACK8>();
+    case kTiledKv88: return tiled_ptr<KKivi8T, VKivi8RowT, PACK8>();
+    case kTiledKv8F: return tiled_ptr<KKivi8T, VF16RowT, PACK8>();
+    case kTiledKvF4: return tiled_ptr<KF16T, VKiviRowT, PACK8>();
+    case kTiledKvF8: return tiled_ptr<KF16T, VKivi8RowT, PACK8>();
+    case kTiledKvFF: return tiled_ptr<KF16T, VF16RowT, PACK8>();
+    case kTiledT8F: return tiled_ptr<KTokT<false, 1>, VF16RowT, PACK8>();
+    case kTiledT8Fg16: return tiled_ptr<KTokT<false, 2>, VF16RowT, PACK8>();
     default: return nullptr;
   }
 }

@@ -64,6 +64,7 @@ struct AppendDev {
   int32_t* status;
   int tile32;  // codes in KVQ_LAYOUT_TILE32 (INT4_ASYM)
   float dq;              // dynamic scales: fp32(percentile / 100), or 0 for the absmax
+  float dq_lo;           // KIVI V: fp32((100 - percentile) / 100), the low quantile
   const float* thr_ptr;  // group-rescue threshold computed by the large-n select, or NULL
   int64_t st_sb;         // INT4_KIVI K: batch stride of the per-channel parameters
   float* zo;             // INT4_KIVI V: per-token zero-point out (scale_out's strides)
@@ -117,29 +118,36 @@ __device__ __forceinline__ int group_sum(int v, int gs) {
   return v;
 }
 
-__device__ float group_quantile(float a0, float a1, int gs, float q, int lane) {
-  {
-    // Near the top (the reference's 99.9 percentile over groups of up to 128 takes the two
-    // largest values) the order statistics come from walking the distinct values down from
-    // the maximum: value m with multiplicity c holds the ranks [gs - above - c, gs - above),
-    // `above` counting the values already passed.  ktop + 1 steps reach rank lo.
-    const float rank = q * (float)(gs - 1);
-    const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
-    const int ktop = gs - 1 - lo;
-    if (ktop < 4) {
-      float t = __builtin_inff(), vlo = 0.f, vhi = 0.f;
-      int above = 0;
-      for (int it = 0; it <= ktop; ++it) {
-        const float m = group_max(fmaxf(a0 < t ? a0 : -1.0f, a1 < t ? a1 : -1.0f), gs);
-        const int c = group_sum((int)(a0 == m) + (int)(a1 == m), gs);
-        const int r0 = gs - above - c, r1 = gs - above;  // ranks [r0, r1) hold m
-        if (lo >= r0 && lo < r1) vlo = m;
-        if (hi >= r0 && hi < r1) vhi = m;
-        above += c;
-        t = m;
-      }
-      return quantile_lerp(vlo, vhi, rank - (float)lo);
+// The order statistics v[lo] <= v[hi] (ascending ranks, ties broken by channel index) of
+// the gs finite values of the lane's group (a0, a1 = the lane's two values, any sign).  Near
+// the top (the reference's 99.9 percentile over groups of up to 128 takes the two largest
+// values) they come from walking the distinct values down from the maximum: value m with
+// multiplicity c holds the ranks [gs - above - c, gs - above), `above` counting the values
+// already passed, and gs - lo steps reach rank lo.  Near the bottom the same walk runs on
+// the negated values (v[r] = -(-v)[gs - 1 - r]).  Elsewhere every value's rank is counted.
+// The group's lanes all return the results.
+__device__ void group_order_stats(float a0, float a1, int gs, int lo, int hi, int lane,
+                                  float& vlo, float& vhi) {
+  const bool top = gs - 1 - lo < 4, bottom = !top && hi < 4;
+  if (top || bottom) {
+    const float sg = top ? 1.0f : -1.0f;  // bottom: walk -v from its top
+    const float b0 = sg * a0, b1 = sg * a1;
+    const int rlo = top ? lo : gs - 1 - hi, rhi = top ? hi : gs - 1 - lo;  // ranks in -v
+    const int steps = gs - rlo;
+    float t = __builtin_inff(), wlo = 0.f, whi = 0.f;
+    int above = 0;
+    for (int it = 0; it < steps; ++it) {
+      const float m = group_max(fmaxf(b0 < t ? b0 : -__builtin_inff(), b1 < t ? b1 : -__builtin_inff()), gs);
+      const int c = group_sum((int)(b0 == m) + (int)(b1 == m), gs);
+      const int r0 = gs - above - c, r1 = gs - above;  // ranks [r0, r1) hold m
+      if (rlo >= r0 && rlo < r1) wlo = m;
+      if (rhi >= r0 && rhi < r1) whi = m;
+      above += c;
+      t = m;
     }
+    vlo = top ? wlo : -whi;
+    vhi = top ? whi : -wlo;
+    return;
   }
   const int nl = gs >> 1;
   const int base = lane & ~(nl - 1);
@@ -151,13 +159,18 @@ __device__ float group_quantile(float a0, float a1, int gs, float q, int lane) {
     r0 += (b0 < a0 || (b0 == a0 && f0 < e0)) + (b1 < a0 || (b1 == a0 && f1 < e0));
     r1 += (b0 < a1 || (b0 == a1 && f0 < e1)) + (b1 < a1 || (b1 == a1 && f1 < e1));
   }
+  // the values of ranks lo and hi, spread over the group
+  vlo = group_max(fmaxf(r0 == lo ? a0 : -__builtin_inff(), r1 == lo ? a1 : -__builtin_inff()), gs);
+  vhi = group_max(fmaxf(r0 == hi ? a0 : -__builtin_inff(), r1 == hi ? a1 : -__builtin_inff()), gs);
+}
+
+// torch.quantile(v, q) over the gs values of the lane's group (linear interpolation in fp32:
+// rank = fp32(q) * (gs - 1), w = rank - floor(rank))
+__device__ float group_quantile(float a0, float a1, int gs, float q, int lane) {
   const float rank = q * (float)(gs - 1);
   const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
-  // the values of ranks lo and hi, spread over the group (|x| >= 0 > -1)
-  float vlo = fmaxf(r0 == lo ? a0 : -1.0f, r1 == lo ? a1 : -1.0f);
-  float vhi = fmaxf(r0 == hi ? a0 : -1.0f, r1 == hi ? a1 : -1.0f);
-  vlo = group_max(vlo, gs);
-  vhi = group_max(vhi, gs);
+  float vlo, vhi;
+  group_order_stats(a0, a1, gs, lo, hi, lane, vlo, vhi);
   return quantile_lerp(vlo, vhi, rank - (float)lo);
 }
 
@@ -314,7 +327,9 @@ __device__ __forceinline__ half2v load_x(const AppendDev& a, int row, int lane) 
 
 // the static scale of the lane's group in append row `row` (0 without a static table)
 __device__ __forceinline__ float row_static(const AppendDev& a, int row, int lane) {
-  if (a.st == nullptr || a.fmt == KVQ_FMT_INT4_ASYM || a.fmt == KVQ_FMT_INT4_KIVI) return 0.f;
+  if (a.st == nullptr || a.fmt == KVQ_FMT_INT4_ASYM || a.fmt == KVQ_FMT_INT4_KIVI ||
+      a.fmt == KVQ_FMT_INT8_KIVI)
+    return 0.f;
   return ld_static(a, (row / a.S) % a.H, (2 * lane) / a.gs);
 }
 
@@ -376,7 +391,10 @@ __device__ void quant_row_x(const AppendDev& a, int row, int lane, float thr, ha
       if (a.so_f32) reinterpret_cast<float*>(a.so)[off] = s;
       else reinterpret_cast<half_t*>(a.so)[off] = (half_t)s;
     }
-  } else if (a.fmt == KVQ_FMT_INT4_KIVI) {
+  } else if (a.fmt == KVQ_FMT_INT4_KIVI || a.fmt == KVQ_FMT_INT8_KIVI) {
+    // asymmetric_quant.py:24-141 with qmin, qmax = -8, 7 (4 bits) or -128, 127 (8 bits)
+    const bool b8 = a.fmt == KVQ_FMT_INT8_KIVI;
+    const float qmin = b8 ? -128.f : -8.f, qmax = b8 ? 127.f : 7.f;
     float s0, s1, z0, z1;
     if (a.st != nullptr) {
       // K: frozen per-channel parameters (kivi_style_cache.py:548-566)
@@ -386,15 +404,25 @@ __device__ void quant_row_x(const AppendDev& a, int row, int lane, float thr, ha
       s0 = ps[o]; s1 = ps[o + a.st_sg];
       z0 = pz[o]; z1 = pz[o + a.st_sg];
     } else {
-      // V: per-token min / max over the 128 channels (asymmetric_quant.py:102-141)
-      float mn = fminf(x0, x1), mx = fmaxf(x0, x1);
-      for (int o = 32; o > 0; o >>= 1) {
-        mn = fminf(mn, __shfl_xor(mn, o, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      // V: per-token range over the 128 channels (asymmetric_quant.py:97-141): min / max, or
+      // with a percentile below 100 torch.quantile at (100 - p) / 100 and p / 100
+      float mn, mx;
+      if (a.dq > 0.f) {
+        mn = group_quantile(x0, x1, 128, a.dq_lo, lane);
+        mx = group_quantile(x0, x1, 128, a.dq, lane);
+      } else {
+        mn = fminf(x0, x1);
+        mx = fmaxf(x0, x1);
+        for (int o = 32; o > 0; o >>= 1) {
+          mn = fminf(mn, __shfl_xor(mn, o, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        }
       }
-      // range floor max(1e-5, fp16 tiny * 15) = 15 * 2^-14; z = min - (-8) s
-      s0 = s1 = __fdiv_rn(fmaxf(mx - mn, 9.1552734375e-4f), 15.0f);
-      z0 = z1 = mn + 8.0f * s0;
+      // range floor max(1e-5, fp16 tiny * (qmax - qmin)) = (qmax - qmin) * 2^-14;
+      // z = min - qmin s (qmin s is exact)
+      const float span = qmax - qmin;
+      s0 = s1 = __fdiv_rn(fmaxf(mx - mn, span * 6.103515625e-05f), span);
+      z0 = z1 = mn - qmin * s0;
       if (lane == 0 && a.so) {
         const int64_t off = (int64_t)b * a.sosb + (int64_t)h * a.sosh + t * a.sost;
         reinterpret_cast<float*>(a.so)[off] = s0;
@@ -403,10 +431,13 @@ __device__ void quant_row_x(const AppendDev& a, int row, int lane, float thr, ha
     }
     const float u0 = __fdiv_rn(x0 - z0, s0), u1 = __fdiv_rn(x1 - z1, s1);
     // frozen-K out-of-range count, of the unrounded quotient (kivi_style_cache.py:549-560)
-    if (a.st != nullptr) clipped = (u0 < -8.f || u0 > 7.f) + (u1 < -8.f || u1 > 7.f);
+    if (a.st != nullptr) clipped = (u0 < qmin || u0 > qmax) + (u1 < qmin || u1 > qmax);
     const float r0 = rintf(u0), r1 = rintf(u1);
-    const int q0 = (int)fminf(fmaxf(r0, -8.f), 7.f), q1 = (int)fminf(fmaxf(r1, -8.f), 7.f);
-    crow[lane] = (uint8_t)(((q0 + 8) << 4) | (q1 + 8));
+    const int q0 = (int)fminf(fmaxf(r0, qmin), qmax), q1 = (int)fminf(fmaxf(r1, qmin), qmax);
+    if (b8)
+      *reinterpret_cast<uint16_t*>(crow + d0) = (uint16_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8));
+    else
+      crow[lane] = (uint8_t)(((q0 + 8) << 4) | (q1 + 8));
   } else {  // KVQ_FMT_INT4_ASYM, static parameters
     const int64_t off = (int64_t)h * a.st_sh + (int64_t)g * a.st_sg;
     const float s = (float)reinterpret_cast<const half_t*>(a.st)[off];
@@ -578,8 +609,10 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   if (!p) return KVQ_OK;
   const std::string n(name);
   if (p->format != KVQ_FMT_INT8_SYM && p->format != KVQ_FMT_INT4_SYM &&
-      p->format != KVQ_FMT_INT4_ASYM && p->format != KVQ_FMT_INT4_KIVI)
+      p->format != KVQ_FMT_INT4_ASYM && p->format != KVQ_FMT_INT4_KIVI &&
+      p->format != KVQ_FMT_INT8_KIVI)
     return fail(KVQ_ERR_INVALID, n + ": unknown format");
+  const bool kivi = p->format == KVQ_FMT_INT4_KIVI || p->format == KVQ_FMT_INT8_KIVI;
   if (p->head_dim != 128) return fail(KVQ_ERR_UNSUPPORTED, n + ": head_dim must be 128");
   const int gs = p->group_size;
   if (gs != 8 && gs != 16 && gs != 32 && gs != 64 && gs != 128)
@@ -589,7 +622,7 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   if (!p->x || !p->codes) return fail(KVQ_ERR_INVALID, n + ": x/codes is NULL");
   if (((uintptr_t)p->x % 4) || (p->x_stride_b % 2) || (p->x_stride_h % 2) || (p->x_stride_s % 2))
     return fail(KVQ_ERR_UNSUPPORTED, n + ": x rows must be 4-byte aligned");
-  if (p->format == KVQ_FMT_INT8_SYM &&
+  if ((p->format == KVQ_FMT_INT8_SYM || p->format == KVQ_FMT_INT8_KIVI) &&
       (((uintptr_t)p->codes % 2) || p->codes_stride_b % 2 || p->codes_stride_h % 2 ||
        p->codes_stride_t % 2))
     return fail(KVQ_ERR_UNSUPPORTED, n + ": int8 code rows must be 2-byte aligned");
@@ -604,18 +637,24 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   } else if (p->n_outlier != 0) {
     return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
   }
-  if (p->format == KVQ_FMT_INT4_KIVI) {
+  if (kivi) {
     if (p->codes_layout != KVQ_LAYOUT_ROWS)
-      return fail(KVQ_ERR_UNSUPPORTED, n + ": INT4_KIVI codes are in token rows");
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI codes are in token rows");
     if (p->static_scale) {
       if (!p->static_zp || p->static_scale_dtype != KVQ_DTYPE_F32)
-        return fail(KVQ_ERR_INVALID, n + ": INT4_KIVI K needs fp32 static scale and zero-point");
+        return fail(KVQ_ERR_INVALID, n + ": KIVI K needs fp32 static scale and zero-point");
     } else if (!p->scale_out || !p->zp_out || p->scale_out_dtype != KVQ_DTYPE_F32) {
-      return fail(KVQ_ERR_INVALID, n + ": INT4_KIVI V needs fp32 scale_out and zp_out");
+      return fail(KVQ_ERR_INVALID, n + ": KIVI V needs fp32 scale_out and zp_out");
     }
   }
   if (!(p->dyn_quantile >= 0.f && p->dyn_quantile < 1.f))
     return fail(KVQ_ERR_INVALID, n + ": dyn_quantile must lie in [0, 1)");
+  if (p->dyn_quantile_lo != 0.f &&
+      !(kivi && !p->static_scale && p->dyn_quantile > 0.f && p->dyn_quantile_lo > 0.f &&
+        p->dyn_quantile_lo < p->dyn_quantile))
+    return fail(KVQ_ERR_INVALID, n + ": dyn_quantile_lo is for KIVI V, in (0, dyn_quantile)");
+  if (kivi && !p->static_scale && p->dyn_quantile > 0.f && p->dyn_quantile_lo == 0.f)
+    return fail(KVQ_ERR_INVALID, n + ": KIVI V with a percentile needs dyn_quantile_lo");
   if (p->codes_layout != KVQ_LAYOUT_ROWS && p->codes_layout != KVQ_LAYOUT_TILE32)
     return fail(KVQ_ERR_INVALID, n + ": unknown codes_layout");
   if (p->codes_layout == KVQ_LAYOUT_TILE32) {
@@ -648,6 +687,7 @@ static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) 
   d.st_sb = p->static_stride_b;
   d.zo = reinterpret_cast<float*>(p->zp_out);
   d.dq = p->dyn_quantile;
+  d.dq_lo = p->dyn_quantile_lo;
   return KVQ_OK;
 }
 

@@ -558,6 +558,21 @@ def kv_view_kivi(codes: torch.Tensor, scale: torch.Tensor, zero_point: torch.Ten
     return v
 
 
+def kv_view_fp16(x: torch.Tensor) -> C.KvView:
+    """View of fp16 values [B,H,T,128] (a 16-bit side, format KVQ_FMT_FP16): strides in bytes,
+    no scale."""
+    if x.dtype != torch.float16 or x.stride(-1) != 1:
+        raise ValueError(f"fp16 K/V rows must be fp16 with contiguous channels, got {x.dtype}")
+    v = C.KvView()
+    v.codes = x.data_ptr()
+    v.layout = C.KVQ_LAYOUT_ROWS
+    v.stride_b, v.stride_h, v.stride_t = 2 * x.stride(0), 2 * x.stride(1), 2 * x.stride(2)
+    v.scale = None
+    v.scale_dtype = C.KVQ_DTYPE_F16
+    v._keep = (x,)
+    return v
+
+
 def _kivi_params(t: torch.Tensor, shape) -> torch.Tensor:
     if tuple(t.shape) != tuple(shape):
         raise ValueError(f"KIVI scale/zero-point must be {tuple(shape)}, got {tuple(t.shape)}")

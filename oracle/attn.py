@@ -125,6 +125,41 @@ def decode_attn_mixed_ref(q, k_int8, k_scale, v_codes, v_scale, v_zp, context_le
     return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)
 
 
+def decode_attn_mixed_bits_ref(q, k_store, k_bits, k_scale, v_store, v_bits, v_scale, v_zp,
+                               context_lens, sm_scale, inv_tau=None):
+    """MixedKVCache of any built (k_bits, v_bits) pair (src/cache/mixed_kv_cache.py:150-254),
+    decoded as get_kv then attention: an 8-bit side is code x its group's scale in fp32, the
+    4-bit V code x s + z of its token in fp32 (v_store packed), a 16-bit side the stored fp16
+    values; each side cast to fp16, then fp32 attention."""
+    k = k_store if k_bits == 16 else dequantize_symmetric(k_store, k_scale.float()).to(torch.float16)
+    if v_bits == 16:
+        v = v_store
+    elif v_bits == 8:
+        v = dequantize_symmetric(v_store, v_scale.float()).to(torch.float16)
+    else:
+        v = dequantize_kivi(unpack_int4(v_store), v_scale, v_zp, per_channel=False).to(torch.float16)
+    return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)
+
+
+def dequant_kivi_side(store, bits: int, s, z, per_channel: bool) -> torch.Tensor:
+    """One side of a KIVI-family layer as float (src/cache/role_aware_allocator_cache.py:
+    402-440): 4 bits packed, 8 bits int8 codes, both code x s + z in fp32 (per channel for K,
+    per token for V); 16 bits the stored fp16 values."""
+    if bits == 16:
+        return store.float()
+    codes = unpack_int4(store) if bits == 4 else store
+    return dequantize_kivi(codes, s, z, per_channel=per_channel)
+
+
+def decode_attn_kivi_family_ref(q, k_store, k_bits, k_scale, k_zp, v_store, v_bits, v_scale, v_zp,
+                                context_lens, sm_scale, inv_tau=None):
+    """A KIVI-family layer of any (k_bits, v_bits) pair from {4, 8, 16}: K and V dequantised
+    in fp32 (dequant_kivi_side), fp32 logits of q' = fp16(q * inv_tau), fp32 softmax and PV."""
+    k = dequant_kivi_side(k_store, k_bits, k_scale, k_zp, True)
+    v = dequant_kivi_side(v_store, v_bits, v_scale, v_zp, False)
+    return attention_fp32(prescale_q(q, inv_tau), k, v, context_lens, sm_scale)
+
+
 def decode_attn_kivi_ref(q, k_packed, v_packed, k_scale, k_zp, v_scale, v_zp, context_lens,
                          sm_scale, inv_tau=None):
     """KIVI layout (src/kernels/triton_decode_attn_int4_asym.py:28-160): K and V dequantised

@@ -341,12 +341,14 @@ def quantize_asymmetric_per_token(v: torch.Tensor, quant_bits: int = 4, percenti
     return quantize_asymmetric(v, 3, quant_bits, percentile)
 
 
-def kivi_quantize_k_static(k: torch.Tensor, s: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+def kivi_quantize_k_static(k: torch.Tensor, s: torch.Tensor, z: torch.Tensor, bits: int = 4) -> torch.Tensor:
     """Decode-time K with the frozen per-channel parameters [B,H,D]
-    (src/cache/kivi_style_cache.py:548-566): clamp(round((fp32(k) - z) / s), -8, 7)."""
+    (src/cache/kivi_style_cache.py:548-566, src/cache/role_aware_allocator_cache.py:292-309):
+    clamp(round((fp32(k) - z) / s), qmin, qmax), [-8, 7] for 4 bits, [-128, 127] for 8."""
     check_finite(k, "kivi_quantize_k_static")
+    qmin, qmax = (-8, 7) if bits == 4 else (-128, 127)
     return torch.round((k.float() - z.float().unsqueeze(2)) / s.float().unsqueeze(2)) \
-        .clamp(-8, 7).to(torch.int8)
+        .clamp(qmin, qmax).to(torch.int8)
 
 
 def dequantize_kivi(q: torch.Tensor, s: torch.Tensor, z: torch.Tensor, per_channel: bool) -> torch.Tensor:

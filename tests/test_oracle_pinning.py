@@ -43,6 +43,10 @@ term, a wrong sign or index, a swapped nibble) fails at least one check:
 * decode_attn_mixed_ref: float64 brute force with per-element dequantisation (K code x the
   scale of its token's group, V code x s_t + z_t of its token), a one-token known answer and
   a literal one (codes 3, -8, 7, 0 with s = 0.5, z = -1 give 0.5, -5, 2.5, -1).
+* decode_attn_mixed_bits_ref: the (8, 4) pair equals decode_attn_mixed_ref bit for bit, and
+  one-token contexts return the token's V for the 16- and 8-bit sides.
+* The KIVI family (quantize_asymmetric with 8 bits and two-tailed percentiles,
+  decode_attn_kivi_family_ref): tests/test_oracle_kivi.py.
 """
 import math
 from fractions import Fraction
@@ -591,3 +595,29 @@ def test_mixed_oracle_brute_force_and_kat():
     zv = torch.full((1, H, S), -1.0)
     lit = OA.decode_attn_mixed_ref(q, kq, ks, vq2.contiguous(), sv, zv, torch.tensor([1]), 0.1)
     assert lit[0, 0, :4].tolist() == [0.5, -5.0, 2.5, -1.0]
+
+
+def test_mixed_bits_oracle_kats():
+    """decode_attn_mixed_bits_ref: the (8, 4) pair is decode_attn_mixed_ref (same bits); a
+    one-token context returns that token's V (fp16 values for a 16-bit side, code x scale of
+    its group for an 8-bit side, code x s + z for 4 bits), for every head of its group."""
+    g = torch.Generator().manual_seed(23)
+    B, H, Hq, S, D = 1, 2, 6, 5, 128
+    q = torch.randn(B, Hq, D, generator=g).to(torch.float16)
+    k8 = torch.randint(-127, 128, (B, H, S, D), generator=g, dtype=torch.int8)
+    ks = (torch.rand(B, H, S, 4, generator=g) * 0.02 + 0.001).to(torch.float16)
+    v4 = torch.randint(-8, 8, (B, H, S, D), generator=g, dtype=torch.int8)
+    vs, vz = torch.rand(B, H, S, generator=g) * 0.3 + 0.05, torch.randn(B, H, S, generator=g)
+    ctx = torch.tensor([S])
+    a = OA.decode_attn_mixed_bits_ref(q, k8, 8, ks, OQ.pack_int4(v4), 4, vs, vz, ctx, 0.1)
+    b = OA.decode_attn_mixed_ref(q, k8, ks, v4, vs, vz, ctx, 0.1)
+    assert torch.equal(a, b)
+    k16 = torch.randn(B, H, S, D, generator=g).to(torch.float16)
+    v16 = torch.randn(B, H, S, D, generator=g).to(torch.float16)
+    one = torch.tensor([1])
+    o = OA.decode_attn_mixed_bits_ref(q, k16, 16, None, v16, 16, None, None, one, 0.1)
+    assert torch.equal(o[0], v16[0, :, 0].repeat_interleave(Hq // H, dim=0))
+    v8 = torch.randint(-127, 128, (B, H, S, D), generator=g, dtype=torch.int8)
+    o = OA.decode_attn_mixed_bits_ref(q, k8, 8, ks, v8, 8, ks, None, one, 0.1)
+    exp = (v8[0, :, 0].view(H, 4, 32).float() * ks[0, :, 0].float().unsqueeze(-1)).view(H, D).to(torch.float16)
+    assert torch.equal(o[0], exp.repeat_interleave(Hq // H, dim=0))
