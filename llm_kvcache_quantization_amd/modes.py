@@ -3,24 +3,24 @@
 * :func:`load_calibration` -- the calibration-JSON rules of generate_loop.py:751-889 (the
   tables' dtypes, group-size / percentile precedence, the warnings, the missing-file and
   load-failure policy).
-* :func:`create_kv_cache` -- the engine of each mode (generate_loop.py:891-938):
+* :func:`create_kv_cache` -- the engine of each mode (generate_loop.py:891-1176):
   ``fp16`` -> :class:`FP16KVCache`; ``int8_baseline`` / ``int8_fused`` / ``int8_ours`` ->
   :class:`INT8KVCache`; ``int4_baseline`` / ``int4_fused`` / ``int4_ours`` /
-  ``int4_ours_mixed`` -> :class:`INT4KVCache`; ``kivi_style`` -> :class:`KIVIStyleKVCache`.
+  ``int4_ours_mixed`` -> :class:`INT4KVCache`; ``kivi_style`` / ``int4_kivi_aligned`` ->
+  :class:`KIVIStyleKVCache`; ``int4_ours_asym`` / ``int4_ours_asym_ba`` ->
+  :class:`RoleAwareAsymKVCache`; ``int4_ours_asym_alloc`` -> :class:`RoleAwareAllocatorKVCache`
+  (per-layer bits from a policy JSON); ``int4_mixed_kv`` -> :class:`MixedKVCache`.
 * :func:`generate_from_ids` -- greedy generation with an explicit prefill (the model's own
   attention; the quantized cache is filled from its past_key_values) and token-by-token
   decode, timed per step with a device synchronisation as the reference's CUDATimer does.
   The fused modes decode through the attention hook (:mod:`patch`); fp16 decodes through
   the model's own cache; the baseline modes hand the dequantized cache to the model.
 
-``kivi_style``: the reference always decodes it by dequantizing before attention (it forces
-decode_attn_impl="torch_ref"); here "torch_ref" keeps that, and the kernel names
-("triton_fused", "hip_fused", "triton_int4_asym*") decode through the hook with the
-INT4_KIVI HIP kernel.
-
-The reference's other modes (``int4_kivi_aligned``, ``int4_mixed_kv``,
-``int4_ours_asym*``: RoleAlign and the mixed / allocated layouts) raise
-NotImplementedError.
+The KIVI-family and mixed modes (``kivi_style``, ``int4_kivi_aligned``, ``int4_ours_asym*``,
+``int4_mixed_kv``): the reference decodes them by dequantizing before attention (it forces
+decode_attn_impl="torch_ref" for all but ``int4_ours_asym*``); here "torch_ref" keeps that,
+and the kernel names ("triton_fused", "hip_fused", "triton_int4_asym*") decode through the
+hook with the HIP kernel of each layer's format.
 """
 from __future__ import annotations
 
@@ -33,15 +33,19 @@ from typing import List, Optional
 
 import torch
 
-from .cache import FP16KVCache, INT4KVCache, INT8KVCache, KIVIStyleKVCache
+from .cache import (FP16KVCache, INT4KVCache, INT8KVCache, KIVIStyleKVCache, MixedKVCache,
+                    RoleAwareAllocatorKVCache, RoleAwareAsymKVCache, load_per_layer_bits_from_policy)
 
 # src/engine/generate_loop.py:44-46
 _FUSED_KV_MODES = frozenset({"int8_fused", "int8_ours", "int4_fused", "int4_ours", "int4_ours_mixed"})
-_INT4_ASYM_FUSABLE = frozenset({"kivi_style"})
+# modes whose engines the reference decodes by dequantizing (torch_ref) and the HIP kernels
+# can decode in place
+_KERNEL_FUSABLE = frozenset({"kivi_style", "int4_kivi_aligned", "int4_ours_asym", "int4_ours_asym_ba",
+                             "int4_ours_asym_alloc", "int4_mixed_kv"})
 KV_MODES = ("fp16", "int8_baseline", "int8_fused", "int8_ours", "int4_baseline", "int4_fused",
-            "int4_ours", "int4_ours_mixed", "kivi_style")
-_NOT_BUILT_MODES = ("int4_kivi_aligned", "int4_mixed_kv", "int4_ours_asym", "int4_ours_asym_ba",
-                    "int4_ours_asym_alloc")
+            "int4_ours", "int4_ours_mixed", "kivi_style", "int4_kivi_aligned", "int4_mixed_kv",
+            "int4_ours_asym", "int4_ours_asym_ba", "int4_ours_asym_alloc")
+_NOT_BUILT_MODES: tuple = ()
 # the reference's kernel names map to the HIP kernels; torch_ref is its torch decode path
 DECODE_ATTN_IMPLS = ("triton_fused", "hip_fused", "torch_ref", "triton_int4_asym",
                      "triton_int4_asym_v2", "triton_int4_asym_gqa")
@@ -62,8 +66,6 @@ class Calibration:
 
 
 def check_kv_mode(kv_mode: str) -> None:
-    if kv_mode in _NOT_BUILT_MODES:
-        raise NotImplementedError(f"kv_mode={kv_mode!r} (RoleAlign / mixed / allocated layouts) is not built")
     if kv_mode not in KV_MODES:
         raise ValueError(f"kv_mode='{kv_mode}' not supported. Choose from {list(KV_MODES)}.")
 
@@ -146,15 +148,116 @@ def load_calibration(kv_mode: str, calib_file: Optional[str], group_size: int = 
     return cal
 
 
+@dataclass
+class RoleCalibration:
+    """What the KIVI-family modes read from a calibration file (None / 100: not present)."""
+    k_percentile: float = 100.0
+    v_percentile: float = 100.0
+    inv_tau: Optional[torch.Tensor] = None
+
+
+def _resolve_calib_path(kv_mode: str, calib_file: str, project_root: Optional[str]) -> str:
+    path = calib_file if os.path.isabs(calib_file) or project_root is None \
+        else os.path.join(project_root, calib_file)
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{kv_mode}: calib_file={calib_file!r} not found (resolved to {path!r}). "
+                                "Use an absolute path or run from the project root.")
+    return path
+
+
+def load_role_calibration(kv_mode: str, calib_file: Optional[str], project_root: Optional[str] = None,
+                          device=None) -> RoleCalibration:
+    """The calibration of the KIVI-family modes (src/engine/generate_loop.py:955-1131).
+
+    * int4_kivi_aligned: inv_tau from ``k_calibration.inv_tau`` (v3 schema), else top-level
+      ``inv_tau``; v_percentile from ``v_calibration.v_percentile``.
+    * int4_ours_asym / _ba / _alloc: k_percentile and v_percentile from the ``role_aware``
+      section, else (warning) from ``k_calibration.k_percentile`` / the top level and
+      ``v_calibration.v_percentile``; int4_ours_asym_ba also takes inv_tau (``role_aware``,
+      then ``k_calibration``, then top level).
+    A relative path resolves against project_root (the reference's repository root); a
+    missing file raises FileNotFoundError."""
+    rc = RoleCalibration()
+    if calib_file is None or kv_mode not in ("int4_kivi_aligned", "int4_ours_asym", "int4_ours_asym_ba",
+                                             "int4_ours_asym_alloc"):
+        return rc
+    with open(_resolve_calib_path(kv_mode, calib_file, project_root), "r") as fh:
+        data = json.load(fh)
+    raw_tau = None
+    if kv_mode == "int4_kivi_aligned":
+        if "k_calibration" in data and "inv_tau" in data["k_calibration"]:
+            raw_tau = data["k_calibration"]["inv_tau"]
+        elif "inv_tau" in data:
+            raw_tau = data["inv_tau"]
+        if "v_calibration" in data and "v_percentile" in data["v_calibration"]:
+            rc.v_percentile = float(data["v_calibration"]["v_percentile"])
+    else:
+        if "role_aware" in data:
+            ra = data["role_aware"]
+            rc.k_percentile = float(ra.get("k_percentile", 100.0))
+            rc.v_percentile = float(ra.get("v_percentile", 100.0))
+        elif "k_calibration" in data:
+            if kv_mode == "int4_ours_asym_alloc":
+                warnings.warn("Allocator RoleAlign mode using k_calibration fallback schema; consider "
+                              "re-generating calibration with role_aware schema.", UserWarning)
+            else:
+                warnings.warn(f"RoleAlign mode '{kv_mode}' using k_calibration fallback schema; consider "
+                              "re-generating calibration with role_aware schema.", UserWarning)
+            kc = data["k_calibration"]
+            rc.k_percentile = float(kc.get("k_percentile", data.get("k_percentile", 100.0)))
+            if "v_calibration" in data:
+                rc.v_percentile = float(data["v_calibration"].get("v_percentile", 100.0))
+        if kv_mode == "int4_ours_asym_ba":
+            if "role_aware" in data and "inv_tau" in data["role_aware"]:
+                raw_tau = data["role_aware"]["inv_tau"]
+            elif "k_calibration" in data and "inv_tau" in data["k_calibration"]:
+                raw_tau = data["k_calibration"]["inv_tau"]
+            elif "inv_tau" in data:
+                raw_tau = data["inv_tau"]
+    if raw_tau is not None:
+        rc.inv_tau = torch.tensor(raw_tau, dtype=torch.float32, device=device)
+    return rc
+
+
 def create_kv_cache(kv_mode: str, num_layers: int, device="cuda", max_seq_len: Optional[int] = None,
                     calib: Optional[Calibration] = None, group_size: int = 128,
                     clip_percentile: float = 99.9, decode_attn_impl: str = "triton_fused",
                     use_attn_temperature: bool = True, adaptive_static_scales: bool = False,
                     adaptive_static_margin: float = 1.0, adaptive_static_k: bool = True,
                     adaptive_static_v: bool = True, quant_bits: Optional[int] = None, residual_length: int = 0,
-                    check_numerics: bool = True):
-    """The cache engine of kv_mode (src/engine/generate_loop.py:891-938)."""
+                    check_numerics: bool = True, role: Optional[RoleCalibration] = None,
+                    k_bits: Optional[int] = None, v_bits: Optional[int] = None,
+                    per_layer_bits=None):
+    """The cache engine of kv_mode (src/engine/generate_loop.py:891-1176)."""
     check_kv_mode(kv_mode)
+    role = role or RoleCalibration()
+    if kv_mode == "int4_kivi_aligned":
+        return KIVIStyleKVCache(num_layers=num_layers, device=device, max_seq_len=max_seq_len, quant_bits=4,
+                                v_percentile=role.v_percentile, inv_tau=role.inv_tau,
+                                use_attn_temperature=use_attn_temperature, residual_length=residual_length,
+                                decode_attn_impl=decode_attn_impl, check_numerics=check_numerics)
+    if kv_mode in ("int4_ours_asym", "int4_ours_asym_ba"):
+        ba = kv_mode == "int4_ours_asym_ba"
+        return RoleAwareAsymKVCache(num_layers=num_layers, device=device, max_seq_len=max_seq_len, quant_bits=4,
+                                    k_percentile=role.k_percentile, v_percentile=role.v_percentile,
+                                    inv_tau=role.inv_tau if ba else None,
+                                    use_attn_temperature=use_attn_temperature and ba,
+                                    framework="ours_asym_ba" if ba else "ours_asym",
+                                    decode_attn_impl=decode_attn_impl, check_numerics=check_numerics)
+    if kv_mode == "int4_ours_asym_alloc":
+        if per_layer_bits is None:
+            raise ValueError("kv_mode='int4_ours_asym_alloc' requires a non-empty policy_json")
+        return RoleAwareAllocatorKVCache(num_layers, per_layer_bits=per_layer_bits, device=device,
+                                         max_seq_len=max_seq_len, k_percentile=role.k_percentile,
+                                         v_percentile=role.v_percentile, framework="ours_asym_allocator",
+                                         residual_length=residual_length, decode_attn_impl=decode_attn_impl,
+                                         check_numerics=check_numerics)
+    if kv_mode == "int4_mixed_kv":
+        return MixedKVCache(num_layers=num_layers, device=device, max_seq_len=max_seq_len,
+                            k_group_size=group_size, v_group_size=group_size, k_clip_percentile=clip_percentile,
+                            v_percentile=clip_percentile, k_bits=8 if k_bits is None else int(k_bits),
+                            v_bits=4 if v_bits is None else int(v_bits), per_layer_bits=per_layer_bits,
+                            decode_attn_impl=decode_attn_impl, check_numerics=check_numerics)
     cal = calib or Calibration(group_size=group_size, clip_percentile=clip_percentile)
     gs = cal.group_size if cal.group_size is not None else group_size
     cp = cal.clip_percentile if cal.clip_percentile is not None else clip_percentile
@@ -207,10 +310,13 @@ def _to_model_cache(pairs):
     return DynamicCache(ddp_cache_data=[(k, v) for k, v in pairs])
 
 
-def _temperature_hooks(model, inv_tau: torch.Tensor):
+def _temperature_hooks(model, inv_tau: torch.Tensor, all_steps: bool = False):
     """Per-head inv_tau on the prefill's queries: q_proj's output (or q_norm's) is scaled
     when the step has more than one token; decode steps are scaled by the fused forward
-    (src/engine/generate_loop.py:276-390)."""
+    (src/engine/generate_loop.py:276-390).  all_steps: decode steps too, for the modes whose
+    decode runs the model's own attention over the dequantized cache
+    (_register_all_temperature_hooks, generate_loop.py:184-274)."""
+    lo = 0 if all_steps else 1
     handles = []
     layers = getattr(getattr(model, "model", None), "layers", None)
     if layers is None:
@@ -238,15 +344,15 @@ def _temperature_hooks(model, inv_tau: torch.Tensor):
             def hook(module, inputs, out, _t=tau, _h=int(nh)):
                 if not isinstance(out, torch.Tensor) or out.ndim != 4:
                     return out
-                if out.shape[1] == _h and out.shape[2] > 1:
+                if out.shape[1] == _h and out.shape[2] > lo:
                     return out * _t.to(out.device, out.dtype).view(1, -1, 1, 1)
-                if out.shape[2] == _h and out.shape[1] > 1:
+                if out.shape[2] == _h and out.shape[1] > lo:
                     return out * _t.to(out.device, out.dtype).view(1, 1, -1, 1)
                 return out
             handles.append(attn.q_norm.register_forward_hook(hook))
         elif getattr(attn, "q_proj", None) is not None:
             def hook(module, inputs, out, _t=tau, _h=int(nh), _d=int(hd)):
-                if not isinstance(out, torch.Tensor) or out.ndim != 3 or out.shape[1] <= 1 \
+                if not isinstance(out, torch.Tensor) or out.ndim != 3 or out.shape[1] <= lo \
                         or out.shape[2] != _h * _d:
                     return out
                 b, s, _ = out.shape
@@ -292,7 +398,9 @@ def generate_from_ids(model, tokenizer, input_ids: torch.Tensor, attention_mask=
                       adaptive_static_k: bool = True, adaptive_static_v: bool = True,
                       decode_attn_impl: str = "triton_fused", allow_missing_calib: bool = False,
                       stop_on_eos: bool = True, quant_bits: Optional[int] = None, residual_length: int = 0,
-                      check_numerics: bool = True) -> GenerationBatchOutput:
+                      check_numerics: bool = True, k_bits: Optional[int] = None, v_bits: Optional[int] = None,
+                      policy_json: Optional[str] = None,
+                      project_root: Optional[str] = None) -> GenerationBatchOutput:
     """Greedy generation with explicit prefill + token-by-token decode
     (src/engine/generate_loop.py:393-1581, the modes of ``KV_MODES``).  Batches need
     uniform lengths (an all-ones attention mask), as in the reference."""
@@ -302,6 +410,8 @@ def generate_from_ids(model, tokenizer, input_ids: torch.Tensor, attention_mask=
     if decode_attn_impl not in DECODE_ATTN_IMPLS:
         raise ValueError(f"decode_attn_impl={decode_attn_impl!r} not supported. Choose from "
                          f"{sorted(DECODE_ATTN_IMPLS)}.")
+    if kv_mode == "int4_ours_asym_alloc" and policy_json is None:
+        raise ValueError("kv_mode='int4_ours_asym_alloc' requires a non-empty policy_json")
     if not torch.cuda.is_available():
         raise RuntimeError("CUDA is required for generation. Please run on a GPU-enabled server.")
     if not isinstance(input_ids, torch.Tensor):
@@ -323,9 +433,21 @@ def generate_from_ids(model, tokenizer, input_ids: torch.Tensor, attention_mask=
     if B > 1 and not bool(torch.all(attention_mask == 1).item()):
         raise ValueError(f"Batched generation requires attention_mask to be all ones (no padding). "
                          f"Got batch={B} kv_mode={kv_mode}.")
-    if decode_attn_impl.startswith("triton_int4_asym") and kv_mode != "kivi_style":
-        raise ValueError(f"decode_attn_impl={decode_attn_impl!r} serves the asymmetric INT4 layout "
-                         "(kv_mode='kivi_style')")
+    if decode_attn_impl.startswith("triton_int4_asym") and kv_mode not in _KERNEL_FUSABLE:
+        raise ValueError(f"decode_attn_impl={decode_attn_impl!r} serves the asymmetric layouts "
+                         f"(kv_mode in {sorted(_KERNEL_FUSABLE)})")
+    if kv_mode == "int4_kivi_aligned":
+        quant_bits = 4
+        if calib_file is None and use_attn_temperature:
+            warnings.warn("kv_mode='int4_kivi_aligned' with use_attn_temperature=True but no calib_file "
+                          "— inv_tau will not be applied.", UserWarning)
+        if use_static_scales:
+            warnings.warn("kv_mode='int4_kivi_aligned' ignores use_static_scales (KIVI skeleton).", UserWarning)
+    per_layer_bits = None
+    if kv_mode in ("int4_mixed_kv", "int4_ours_asym_alloc") and policy_json is not None:
+        per_layer_bits = load_per_layer_bits_from_policy(policy_json, project_root=project_root or os.getcwd())
+    if kv_mode == "int4_ours_asym_alloc" and per_layer_bits is None:
+        raise ValueError("kv_mode='int4_ours_asym_alloc' requires a non-empty policy_json")
     if kv_mode == "kivi_style":
         quant_bits = 8 if quant_bits is None else int(quant_bits)
         if quant_bits not in (4, 8):
@@ -343,7 +465,7 @@ def generate_from_ids(model, tokenizer, input_ids: torch.Tensor, attention_mask=
     torch.manual_seed(seed)
     # kivi_style: the reference always dequantizes before attention (its torch_ref); here
     # decode_attn_impl="torch_ref" keeps that, the kernel names run the INT4_KIVI HIP kernel
-    fused = kv_mode in _FUSED_KV_MODES or (kv_mode in _INT4_ASYM_FUSABLE and decode_attn_impl != "torch_ref")
+    fused = kv_mode in _FUSED_KV_MODES or (kv_mode in _KERNEL_FUSABLE and decode_attn_impl != "torch_ref")
     num_layers = int(getattr(model.config, "num_hidden_layers", 28))
     max_len = getattr(model.config, "max_position_embeddings", None)
     if max_len is not None and S + max_new_tokens > int(max_len):
@@ -351,6 +473,7 @@ def generate_from_ids(model, tokenizer, input_ids: torch.Tensor, attention_mask=
                          f"max_position_embeddings={max_len}")
     cal = load_calibration(kv_mode, calib_file, group_size, clip_percentile, use_static_scales,
                            use_attn_temperature, allow_missing_calib, device=dev)
+    role = load_role_calibration(kv_mode, calib_file, project_root, device=dev)
     kv_cache = create_kv_cache(kv_mode, num_layers, device=dev, max_seq_len=S + max_new_tokens, calib=cal,
                                group_size=group_size, clip_percentile=clip_percentile,
                                decode_attn_impl=decode_attn_impl, use_attn_temperature=use_attn_temperature,
@@ -358,7 +481,8 @@ def generate_from_ids(model, tokenizer, input_ids: torch.Tensor, attention_mask=
                                adaptive_static_margin=adaptive_static_margin,
                                adaptive_static_k=adaptive_static_k, adaptive_static_v=adaptive_static_v,
                                quant_bits=quant_bits, residual_length=residual_length,
-                               check_numerics=check_numerics)
+                               check_numerics=check_numerics, role=role, k_bits=k_bits, v_bits=v_bits,
+                               per_layer_bits=per_layer_bits)
     patched = False
     hooks = []
     try:
@@ -367,6 +491,16 @@ def generate_from_ids(model, tokenizer, input_ids: torch.Tensor, attention_mask=
             patched = True
             if use_attn_temperature and cal.inv_tau is not None and kv_mode in _FUSED_KV_MODES:
                 hooks = _temperature_hooks(model, cal.inv_tau)
+            elif use_attn_temperature and role.inv_tau is not None and \
+                    kv_mode in ("int4_kivi_aligned", "int4_ours_asym_ba"):
+                # prefill only; decode steps apply the engine's inv_tau.  (The reference
+                # registers none for a fused int4_ours_asym_ba decode, so its prefill runs
+                # unscaled there while its torch_ref path scales it: here both scale it.)
+                hooks = _temperature_hooks(model, role.inv_tau)
+        elif use_attn_temperature and role.inv_tau is not None and \
+                kv_mode in ("int4_kivi_aligned", "int4_ours_asym_ba"):
+            # dequantized decode through the model's attention: every step's queries
+            hooks = _temperature_hooks(model, role.inv_tau, all_steps=True)
         # ---- prefill (the model's own attention; q_len > 1 never takes the fused path)
         _sync()
         t0 = time.perf_counter()
@@ -385,9 +519,10 @@ def generate_from_ids(model, tokenizer, input_ids: torch.Tensor, attention_mask=
             nxt = torch.argmax(out.logits[:, -1, :], dim=-1)
         _sync()
         ttft_ms = (time.perf_counter() - t0) * 1e3
-        for h in hooks:
-            h.remove()
-        hooks = []
+        if fused:  # prefill-only hooks; the all-step ones stay for the decode
+            for h in hooks:
+                h.remove()
+            hooks = []
         steps = [nxt]
         times: List[float] = []
         eos = getattr(tokenizer, "eos_token_id", None) if tokenizer is not None else None

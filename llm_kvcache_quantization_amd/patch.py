@@ -82,7 +82,7 @@ class INT8CacheWrapper:
 def _is_quantized_engine(engine) -> bool:
     return any(hasattr(engine, n) for n in (
         "get_int8_tensors", "get_int4_tensors", "get_int4_asym_tensors", "get_int4_g32_tensors",
-        "get_k8v4_tensors"))
+        "get_k8v4_tensors", "get_kivi_tensors", "get_mixed_tensors"))
 
 
 class INT8CacheWrapperContainer:
@@ -274,6 +274,16 @@ def _materialize_int4_cache_as_int8(k_int4, v_int4, *, head_dim: int, bit_packed
     return unpack(k_int4), unpack(v_int4)
 
 
+def _attention_fp32(q, k, v, sm_scale):
+    """q [B, Hq, D] over dequantized k / v [B, Hkv, S, D] (every row S tokens): GQA heads
+    expanded, scores / softmax / weighted sum in fp32, output in q's dtype."""
+    rep = q.shape[1] // k.shape[1]
+    kf = k.float().repeat_interleave(rep, dim=1)
+    vf = v.float().repeat_interleave(rep, dim=1)
+    scores = torch.einsum("bhd,bhsd->bhs", q.float(), kf) * sm_scale
+    return torch.einsum("bhs,bhsd->bhd", torch.softmax(scores, dim=-1), vf).to(q.dtype)
+
+
 def _decode_attn_int8_torch_ref(q, k_int8, v_int8, k_scale, v_scale, context_lens, sm_scale):
     """The reference's torch decode attention over INT8 codes with per-(token, group)
     fp16 scales (src/engine/patch_model.py:281-377): codes dequantised as fp16 products,
@@ -389,11 +399,19 @@ def _fused_forward_impl(self, hidden_states, cache_wrapper, attention_mask=None,
                                                 sm_scale=sm_scale).to(q_kernel.dtype)
             if hasattr(engine, "record_triton_kernel_call"):
                 engine.record_triton_kernel_call(layer_idx)
+        elif decode_impl == "torch_ref" and not (hasattr(engine, "get_int8_tensors") or
+                                                 hasattr(engine, "get_int4_tensors")):
+            # the KIVI family and the mixed cache: the reference decodes them by handing the
+            # dequantized cache to the model's attention (src/engine/generate_loop.py:1357-
+            # 1364); here get_kv's fp16 K / V with the same fp32 attention as the INT8 path
+            if not hasattr(engine, "get_kv"):
+                raise RuntimeError(f"decode_attn_impl='torch_ref' needs a cache with get_kv, got "
+                                   f"{type(engine).__name__}")
+            qs = q_kernel * tau.view(1, -1, 1) if tau is not None else q_kernel
+            engine.append(layer_idx, k, v)
+            kd, vd = engine.get_kv(layer_idx)
+            out = _attention_fp32(qs, kd, vd, sm_scale)
         elif decode_impl == "torch_ref":
-            # the reference's torch path serves the symmetric INT8 / INT4 layouts only
-            if not (hasattr(engine, "get_int8_tensors") or hasattr(engine, "get_int4_tensors")):
-                raise RuntimeError(f"decode_attn_impl='torch_ref' needs an INT8 or symmetric INT4 "
-                                   f"engine, got {type(engine).__name__}")
             qs = q_kernel * tau.view(1, -1, 1) if tau is not None else q_kernel
             engine.append(layer_idx, k, v)
             if hasattr(engine, "get_int8_tensors"):

@@ -61,6 +61,17 @@ def _engine(kind, tau=False):
         return K.INT4KVCache(num_layers=1, device=DEV)
     if kind == "kivi4":
         return K.KIVIStyleKVCache(num_layers=1, device=DEV, quant_bits=4)
+    if kind == "kivi8_pct":
+        return K.RoleAwareAsymKVCache(num_layers=1, device=DEV, quant_bits=8, k_percentile=99.5,
+                                      v_percentile=99.9)
+    if kind.startswith("alloc"):
+        pair = {"alloc_48": (4, 8), "alloc_164": (16, 4), "alloc_816": (8, 16)}[kind]
+        return K.RoleAwareAllocatorKVCache(1, per_layer_bits=[pair], device=DEV, v_percentile=99.9,
+                                           decode_attn_impl="hip_fused")
+    if kind.startswith("mixed"):
+        kb, vb = {"mixed_84": (8, 4), "mixed_164": (16, 4), "mixed_88": (8, 8)}[kind]
+        return K.MixedKVCache(1, device=DEV, k_bits=kb, v_bits=vb, k_group_size=32, v_percentile=99.9,
+                              decode_attn_impl="hip_fused")
     path = os.path.join(GOLDEN, "calib_qwen25_1p5b_int8.json" if kind == "int8_table"
                         else "calib_qwen25_1p5b_int4.json")
     mode = "int8_ours" if kind == "int8_table" else "int4_ours"
@@ -89,7 +100,9 @@ def _q_of(attn, hidden, cos, sin):
     return q[:, :, 0]
 
 
-@pytest.mark.parametrize("kind", ["int8_dynamic", "int8_table", "int4_dynamic", "int4_table", "kivi4"])
+@pytest.mark.parametrize("kind", ["int8_dynamic", "int8_table", "int4_dynamic", "int4_table", "kivi4",
+                                  "kivi8_pct", "alloc_48", "alloc_164", "alloc_816", "mixed_84",
+                                  "mixed_164", "mixed_88"])
 def test_patched_decode_matches_unpatched_sdpa(kind):
     from llm_kvcache_quantization_amd import patch as P
     from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention
@@ -202,3 +215,44 @@ def test_generate_fused_int8_hip_and_torch_ref_agree():
     print("[generate] hip", a.generated_ids.tolist(), "torch_ref", b.generated_ids.tolist(),
           "fp16", c.generated_ids.tolist(), flush=True)
     assert torch.equal(a.generated_ids, b.generated_ids)
+
+
+@pytest.mark.parametrize("kv_mode", ["kivi_style", "int4_kivi_aligned", "int4_ours_asym", "int4_ours_asym_ba",
+                                     "int4_ours_asym_alloc", "int4_mixed_kv"])
+def test_generate_kivi_family_modes_hip_matches_torch_ref(kv_mode, tmp_path):
+    """The KIVI-family and mixed modes with their calibration / policy files: the HIP decode
+    (the hook over the engine's kernels) and the reference's dequantize-then-attention decode
+    (torch_ref) generate the same tokens on a random 2-layer Qwen2."""
+    import json
+
+    _pkg()
+    from llm_kvcache_quantization_amd import modes
+
+    print(f"[generate] {kv_mode}", flush=True)
+    # powers of two: q * inv_tau is then exact in fp16, so scaling before RoPE (the reference's
+    # hooks on the dequantized path) and after it (the fused forward) give the same q
+    tau = [[0.5, 1.0, 2.0, 1.0], [1.0, 2.0, 0.5, 0.5]]
+    calib = {"role_aware": {"k_percentile": 99.5, "v_percentile": 99.9, "inv_tau": tau},
+             "k_calibration": {"inv_tau": tau}, "v_calibration": {"v_percentile": 99.9}}
+    (tmp_path / "calib.json").write_text(json.dumps(calib))
+    pol = [[4, 8], [16, 4]] if kv_mode == "int4_ours_asym_alloc" else [[8, 4], [16, 4]]
+    (tmp_path / "policy.json").write_text(json.dumps({"per_layer_bits": pol}))
+    kw = dict(calib_file=str(tmp_path / "calib.json"), use_static_scales=False)
+    if kv_mode == "kivi_style":
+        kw = dict(quant_bits=8, use_attn_temperature=False, use_static_scales=False)
+    if kv_mode in ("int4_ours_asym_alloc", "int4_mixed_kv"):
+        kw["policy_json"] = str(tmp_path / "policy.json")
+    m = _tiny_lm()
+    ids = torch.randint(0, 211, (2, 48), generator=torch.Generator().manual_seed(12))
+    a = modes.generate_from_ids(m, None, ids, max_new_tokens=12, kv_mode=kv_mode, decode_attn_impl="triton_fused",
+                                **kw)
+    b = modes.generate_from_ids(m, None, ids, max_new_tokens=12, kv_mode=kv_mode, decode_attn_impl="torch_ref",
+                                **kw)
+    print("[generate] hip", a.generated_ids.tolist(), "torch_ref", b.generated_ids.tolist(), flush=True)
+    assert a.decode_stats["fused_decode_calls"] == 2 * 11, a.decode_stats
+    # The two decodes attend over the same codes with different rounding (fp32 dequantization
+    # in the kernel, fp16 values through SDPA); a random 2-layer model has near-ties between
+    # candidate tokens, where that can pick the other one late in a run, so the first eight
+    # tokens are compared.  The layer-level numerics of these engines are compared against
+    # float64 in test_patched_decode_matches_unpatched_sdpa.
+    assert torch.equal(a.generated_ids[:, :8], b.generated_ids[:, :8])

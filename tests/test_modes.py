@@ -110,9 +110,7 @@ def test_create_kv_cache_engine_per_mode():
     assert type(M.create_kv_cache("kivi_style", 2, device="cpu", quant_bits=4)) is KIVIStyleKVCache
 
 
-def test_modes_not_built_or_unknown_raise():
-    with pytest.raises(NotImplementedError):
-        M.check_kv_mode("int4_ours_asym")
+def test_unknown_mode_raises():
     with pytest.raises(ValueError):
         M.check_kv_mode("int3_magic")
 
@@ -144,8 +142,70 @@ def test_generate_argument_checks():
 
     with pytest.raises(ValueError, match="decode_attn_impl"):
         M.generate_from_ids(Stub(), None, torch.zeros(1, 3, dtype=torch.long), decode_attn_impl="nope")
-    with pytest.raises(NotImplementedError):
-        M.generate_from_ids(Stub(), None, torch.zeros(1, 3, dtype=torch.long), kv_mode="int4_mixed_kv")
+    with pytest.raises(ValueError, match="kv_mode"):
+        M.generate_from_ids(Stub(), None, torch.zeros(1, 3, dtype=torch.long), kv_mode="int4_kivi")
+    with pytest.raises(ValueError, match="policy_json"):
+        M.generate_from_ids(Stub(), None, torch.zeros(1, 3, dtype=torch.long), kv_mode="int4_ours_asym_alloc")
+
+
+def test_every_reference_kv_mode_is_accepted():
+    """src/engine/generate_loop.py:438-460: the fourteen kv_modes."""
+    ref = ["fp16", "int8_baseline", "int8_fused", "int8_ours", "int4_baseline", "int4_fused", "int4_ours",
+           "int4_ours_mixed", "kivi_style", "int4_kivi_aligned", "int4_mixed_kv", "int4_ours_asym",
+           "int4_ours_asym_ba", "int4_ours_asym_alloc"]
+    assert sorted(M.KV_MODES) == sorted(ref)
+    for m in ref:
+        M.check_kv_mode(m)
+
+
+def test_role_calibration_rules(tmp_path):
+    """generate_loop.py:955-1131: the role_aware section, the k_calibration fallback (with its
+    warning), v3 inv_tau for int4_kivi_aligned, inv_tau only for int4_ours_asym_ba, relative
+    paths against the project root, a missing file."""
+    import json
+
+    ra = {"role_aware": {"k_percentile": 99.5, "v_percentile": 99.0, "inv_tau": [[1.0, 0.5]]},
+          "k_calibration": {"inv_tau": [[2.0, 2.0]], "k_percentile": 98.0},
+          "v_calibration": {"v_percentile": 97.0}}
+    fb = {"k_calibration": {"k_percentile": 98.0, "inv_tau": [[2.0, 3.0]]}, "v_calibration": {"v_percentile": 97.0},
+          "inv_tau": [[4.0, 4.0]]}
+    (tmp_path / "ra.json").write_text(json.dumps(ra))
+    (tmp_path / "fb.json").write_text(json.dumps(fb))
+    r = M.load_role_calibration("int4_ours_asym", "ra.json", project_root=str(tmp_path))
+    assert (r.k_percentile, r.v_percentile, r.inv_tau) == (99.5, 99.0, None)
+    r = M.load_role_calibration("int4_ours_asym_ba", str(tmp_path / "ra.json"))
+    assert r.inv_tau.tolist() == [[1.0, 0.5]]
+    with pytest.warns(UserWarning, match="k_calibration fallback"):
+        r = M.load_role_calibration("int4_ours_asym_ba", str(tmp_path / "fb.json"))
+    assert (r.k_percentile, r.v_percentile) == (98.0, 97.0) and r.inv_tau.tolist() == [[2.0, 3.0]]
+    with pytest.warns(UserWarning, match="Allocator RoleAlign"):
+        r = M.load_role_calibration("int4_ours_asym_alloc", str(tmp_path / "fb.json"))
+    assert r.inv_tau is None
+    r = M.load_role_calibration("int4_kivi_aligned", str(tmp_path / "ra.json"))
+    assert r.inv_tau.tolist() == [[2.0, 2.0]] and r.v_percentile == 97.0 and r.k_percentile == 100.0
+    r = M.load_role_calibration("int4_kivi_aligned", str(tmp_path / "fb.json"))
+    assert r.inv_tau.tolist() == [[2.0, 3.0]]
+    assert M.load_role_calibration("kivi_style", str(tmp_path / "nope.json")).inv_tau is None
+    with pytest.raises(FileNotFoundError):
+        M.load_role_calibration("int4_ours_asym", "nope.json", project_root=str(tmp_path))
+
+
+def test_policy_json_loader(tmp_path):
+    """src/cache/role_aware_allocator_cache.py:36-70."""
+    import json
+
+    from llm_kvcache_quantization_amd import load_per_layer_bits_from_policy as load
+
+    (tmp_path / "p.json").write_text(json.dumps({"per_layer_bits": [[4, 8], [16, 4]]}))
+    assert load("p.json", project_root=str(tmp_path)) == [(4, 8), (16, 4)]
+    (tmp_path / "bad.json").write_text(json.dumps({"per_layer_bits": [[4, 3]]}))
+    with pytest.raises(ValueError, match="unsupported bits"):
+        load(str(tmp_path / "bad.json"), project_root="/")
+    (tmp_path / "nokey.json").write_text(json.dumps({}))
+    with pytest.raises(ValueError, match="per_layer_bits"):
+        load(str(tmp_path / "nokey.json"), project_root="/")
+    with pytest.raises(FileNotFoundError):
+        load("missing.json", project_root=str(tmp_path))
 
 
 def test_past_layers_reads_dynamic_cache_and_tuples():
