@@ -138,6 +138,17 @@ typedef struct kvq_decode_params {
   int64_t out_stride_b, out_stride_h; /* elements */
   int32_t context_len;    /* context of every row when context_lens is NULL (ABI 4) */
   int32_t pad0;           /* 0 */
+  /* fp16 residual window (ABI 5; src/cache/kivi_style_cache.py:102-113, 354-404): the
+     res_tokens most recent tokens of every row kept unquantized, fp16 [B, kv_heads, >=
+     res_tokens, D] with dense 256-byte token rows, attended together with the row's
+     quantized context (any order within the window).  0 = none.  KIVI-family formats
+     (INT4_KIVI, INT8_KIVI, FP16) on the tiled kernel with at most 64 work-groups per
+     (b, kv head); at most 4096 tokens. */
+  const void* res_k;
+  const void* res_v;
+  int64_t res_stride_b, res_stride_h;   /* elements */
+  int32_t res_tokens;
+  int32_t pad1;           /* 0 */
 } kvq_decode_params;
 
 int kvq_decode_attn(const kvq_decode_params* p, kvq_stream_t stream);

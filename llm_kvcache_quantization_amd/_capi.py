@@ -80,6 +80,9 @@ class DecodeParams(ctypes.Structure):
         ("out", c_vp),
         ("out_stride_b", c_i64), ("out_stride_h", c_i64),
         ("context_len", c_i32), ("pad0", c_i32),
+        ("res_k", c_vp), ("res_v", c_vp),
+        ("res_stride_b", c_i64), ("res_stride_h", c_i64),
+        ("res_tokens", c_i32), ("pad1", c_i32),
     ]
 
 

@@ -1127,21 +1127,29 @@ class _KiviFamily(_EngineBase):
     through kvq_quant_append (HIP; per-token percentile clipping in the kernel); the prefill's
     per-channel K range is reduced with torch (aminmax, or a sort and torch.lerp for a
     percentile, as torch.quantile does).  Decode attention reads the cache in place through the
-    tiled kernel of the layer's pair (kvq_decode_attn).  residual_length 0 only.
+    tiled kernel of the layer's pair (kvq_decode_attn), the fp16 residual window (residual_length
+    > 0) with it, merged by the kernel's merging work-group.
     """
 
     _min_capacity = 256
 
     def _init_kivi(self, num_layers, device, dtype, max_seq_len, bits, k_percentile, v_percentile,
                    inv_tau, use_attn_temperature, residual_length, decode_attn_impl, check_numerics):
-        if int(residual_length) != 0:
-            raise NotImplementedError("the fp16 residual window is not built (residual_length=0)")
         _kivi_levels(k_percentile)
         _kivi_levels(v_percentile)
         self._init_common(num_layers, device, max_seq_len, decode_attn_impl, check_numerics)
         self.dtype = dtype
         self.k_percentile, self.v_percentile = float(k_percentile), float(v_percentile)
-        self.residual_length = 0
+        self.residual_length = max(0, int(residual_length))
+        if self.residual_length > 4096:
+            raise NotImplementedError("residual_length above 4096 is not built")
+        # fp16 residual window (kivi_style_cache.py:102-113): per layer a ring of the
+        # residual_length most recent decode tokens, _res_len of them valid, the oldest at
+        # _res_start once the ring is full
+        self._res_k: List[Optional[Tensor]] = [None] * num_layers
+        self._res_v: List[Optional[Tensor]] = [None] * num_layers
+        self._res_len = [0] * num_layers
+        self._res_start = [0] * num_layers
         self.inv_tau = inv_tau
         self.use_attn_temperature = bool(use_attn_temperature)
         self._scale_dtype = torch.float32
@@ -1190,10 +1198,46 @@ class _KiviFamily(_EngineBase):
         self._layer_capacity[layer_id] = new_cap
         self._steps[layer_id] = self._apps[layer_id] = None
 
+    def _residual_seq(self) -> int:
+        return max(q + r for q, r in zip(self._layer_seq_lens, self._res_len))
+
     def append(self, layer_id: int, k: Tensor, v: Tensor) -> None:
         """Quantize (or store) and append k, v fp16 [B, H, S, 128] (kivi_style_cache.py:296-617,
-        role_aware_allocator_cache.py:311-400)."""
+        role_aware_allocator_cache.py:311-400).  With residual_length R, a decode token (S = 1
+        after the prefill) goes to the fp16 window; once R are held, the oldest is quantized
+        into the cache and the new token takes its slot (kivi_style_cache.py:354-404)."""
         self._validate_kv(layer_id, k, v)
+        B, H, S, D = k.shape
+        R = self.residual_length
+        if R > 0 and S == 1 and self._k_scale_initialized[layer_id]:
+            if self._res_k[layer_id] is None:
+                self._res_k[layer_id] = torch.zeros(B, H, R, D, dtype=torch.float16, device=k.device)
+                self._res_v[layer_id] = torch.zeros_like(self._res_k[layer_id])
+            rk, rv = self._res_k[layer_id], self._res_v[layer_id]
+            if tuple(rk.shape[:2]) != (B, H):
+                raise ValueError(f"Inconsistent KV shape for layer {layer_id}: residual window "
+                                 f"{tuple(rk.shape)}, incoming {tuple(k.shape)}")
+            rlen = self._res_len[layer_id]
+            if rlen < R:
+                rk[:, :, rlen] = k[:, :, 0]
+                rv[:, :, rlen] = v[:, :, 0]
+                self._res_len[layer_id] = rlen + 1
+                self._seq_len = self._residual_seq()
+                return
+            slot = self._res_start[layer_id]
+            # the oldest token is quantized from its slot (the kernel reads it before the
+            # copy of the new token, which follows on the same stream)
+            self._append_quantized(layer_id, rk[:, :, slot:slot + 1], rv[:, :, slot:slot + 1])
+            rk[:, :, slot] = k[:, :, 0]
+            rv[:, :, slot] = v[:, :, 0]
+            self._res_start[layer_id] = (slot + 1) % R
+            self._seq_len = self._residual_seq()
+            return
+        self._append_quantized(layer_id, k, v)
+        if R > 0:
+            self._seq_len = self._residual_seq()
+
+    def _append_quantized(self, layer_id: int, k: Tensor, v: Tensor) -> None:
         B, H, S, D = k.shape
         old = self._layer_seq_lens[layer_id]
         if S == 0:
@@ -1298,7 +1342,20 @@ class _KiviFamily(_EngineBase):
         else:
             vq = _unpack(vc) if vb == 4 else vc
             v = (vq.float() * vs.unsqueeze(-1) + vz.unsqueeze(-1)).to(self.dtype)
+        rlen = self._res_len[layer_id]
+        if rlen > 0:  # the fp16 window after the quantized tokens, oldest first
+            rk, rv = self._residual(layer_id)
+            k = torch.cat([k, rk.to(self.dtype)], dim=2)
+            v = torch.cat([v, rv.to(self.dtype)], dim=2)
         return k, v
+
+    def _residual(self, layer_id: int) -> Tuple[Tensor, Tensor]:
+        """The fp16 window's valid tokens in arrival order [B, H, rlen, 128]."""
+        rlen, st = self._res_len[layer_id], self._res_start[layer_id]
+        rk, rv = self._res_k[layer_id], self._res_v[layer_id]
+        if st:
+            rk, rv = torch.roll(rk, -st, dims=2), torch.roll(rv, -st, dims=2)
+        return rk[:, :, :rlen], rv[:, :, :rlen]
 
     def _step_for(self, layer_id: int, q_heads: int):
         """The layer's LayerStep over its whole buffers and its frozen K parameters."""
@@ -1320,6 +1377,12 @@ class _KiviFamily(_EngineBase):
         st.key = key
         self._steps[layer_id] = st
         return st
+
+    def _attend(self, layer_id: int, q16: Tensor, sm: float, tau: Optional[Tensor]) -> Tensor:
+        st = self._step_for(layer_id, q16.shape[1])
+        # the window's slots in ring order: attention does not depend on the token order
+        st.set_residual(self._res_k[layer_id], self._res_v[layer_id], self._res_len[layer_id])
+        return st.attend(q16, self._layer_seq_lens[layer_id], sm, tau)
 
     def _layer_tau(self, layer_id: int, q: Tensor) -> Optional[Tensor]:
         """The engine's inv_tau[layer] as fp16 on q's device (converted once per layer)."""
@@ -1344,7 +1407,7 @@ class _KiviFamily(_EngineBase):
         if q16.stride(-1) != 1:
             q16 = q16.contiguous()
         sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
-        out = self._step_for(layer_id, q.shape[1]).attend(q16, n, sm, self._layer_tau(layer_id, q))
+        out = self._attend(layer_id, q16, sm, self._layer_tau(layer_id, q))
         self.record_fused_decode(layer_id, "hip_fused")
         return out if dt == torch.float16 else out.to(dt)
 
@@ -1358,11 +1421,10 @@ class _KiviFamily(_EngineBase):
         if k.shape[2] != 1:
             raise ValueError(f"append_decode_attn appends one token per step, got S={k.shape[2]}")
         self.append(layer_id, k, v)
-        n = self._layer_seq_lens[layer_id]
         if q.dtype != torch.float16 or q.stride(-1) != 1:
             q = q.to(torch.float16).contiguous()
         sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
-        return self._step_for(layer_id, q.shape[1]).attend(q, n, sm, inv_tau)
+        return self._attend(layer_id, q, sm, inv_tau)
 
     def clear(self) -> None:
         self._layer_seq_lens = [0] * self.num_layers
@@ -1371,12 +1433,18 @@ class _KiviFamily(_EngineBase):
         self._k_scale_initialized = [False] * self.num_layers
         self._k_scale = [None] * self.num_layers
         self._k_zp = [None] * self.num_layers
+        self._res_len = [0] * self.num_layers
+        self._res_start = [0] * self.num_layers
+        for t in self._res_k + self._res_v:
+            if t is not None:
+                t.zero_()
 
     def release(self) -> None:
         n = self.num_layers
         self._k_cache, self._v_cache = [None] * n, [None] * n
         self._v_scale, self._v_zp = [None] * n, [None] * n
         self._steps, self._apps = [None] * n, [None] * n
+        self._res_k, self._res_v = [None] * n, [None] * n
         self._layer_capacity = [0] * n
         self.clear()
 

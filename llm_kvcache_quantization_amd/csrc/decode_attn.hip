@@ -989,6 +989,29 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   a.out = reinterpret_cast<half_t*>(p->out);
   a.o_sb = p->out_stride_b; a.o_sh = p->out_stride_h;
 
+  a.res_k = a.res_v = nullptr;
+  a.rsb = a.rsh = 0;
+  a.res_n = 0;
+  if (p->res_tokens != 0) {
+    if (p->res_tokens < 0 || p->res_tokens > 4096)
+      return fail(KVQ_ERR_INVALID, "res_tokens must lie in [0, 4096]");
+    if (!tiled || !kivi_fmt(kf) || !kivi_fmt(vf))
+      return fail(KVQ_ERR_UNSUPPORTED,
+                  "the fp16 residual window needs KIVI-family formats (INT4_KIVI, INT8_KIVI, FP16)");
+    if (nch64 > kUnitChunks)
+      return fail(KVQ_ERR_UNSUPPORTED, "the fp16 residual window needs at most 64 work-groups per "
+                                       "(b, kv head) (raise chunk_tokens)");
+    if (!p->res_k || !p->res_v) return fail(KVQ_ERR_INVALID, "res_k / res_v is NULL");
+    if (!aligned(p->res_k, 4) || !aligned(p->res_v, 4) || p->res_stride_b % 2 || p->res_stride_h % 2 ||
+        p->res_stride_b < 0 || p->res_stride_h < 0)
+      return fail(KVQ_ERR_UNSUPPORTED, "residual rows must be 4-byte aligned");
+    a.res_k = reinterpret_cast<const half_t*>(p->res_k);
+    a.res_v = reinterpret_cast<const half_t*>(p->res_v);
+    a.rsb = p->res_stride_b;
+    a.rsh = p->res_stride_h;
+    a.res_n = p->res_tokens;
+  }
+
   a.app = FusedAppend{};
   if (app) {
     if (!tiled) return fail(KVQ_ERR_UNSUPPORTED, "the fused append needs a tiled-kernel format");

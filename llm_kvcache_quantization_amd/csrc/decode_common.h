@@ -79,6 +79,12 @@ struct DecodeArgs {
   half_t* out;
   int64_t o_sb, o_sh;
   FusedAppend app;
+  // fp16 residual window: res_n tokens per (b, kv head) at res_k / res_v + b * rsb + h * rsh
+  // (elements, dense 128-element token rows), merged by the merging work-group
+  const half_t* res_k;
+  const half_t* res_v;
+  int64_t rsb, rsh;
+  int res_n;
 };
 
 // context length of batch row b, clamped to [0, capacity]

@@ -174,6 +174,54 @@ __device__ __forceinline__ void merge_store_partial(const DecodeArgs& a, TiledMe
   }
 }
 
+// The attention partial (m, l, acc of channels 2 lane, 2 lane + 1) of query head hq over the
+// fp16 residual window of (b, kv head) (a.res_n tokens), in the units of the chunk partials:
+// logits q' . k * sm * log2(e) with q' = fp16(q * inv_tau) in fp32, base-2 softmax.  The
+// window's rows are read 16 tokens per batch, K and V of a batch in flight together; one wave
+// reduction per token.
+__device__ __forceinline__ void residual_partial(const DecodeArgs& a, int b, int hkv, int hq, int lane,
+                                                 float& mr, float& lr, float& r0, float& r1) {
+  const bool has_tau = a.inv_tau != nullptr;
+  const half_t tau = has_tau ? a.inv_tau[hq] : (half_t)1.0f;
+  const half2v q2 = *reinterpret_cast<const half2v*>(q_row(a, b, hq) + 2 * lane);
+  const float q0 = (float)qscale(q2.x, tau, has_tau), q1 = (float)qscale(q2.y, tau, has_tau);
+  const int64_t off = (int64_t)b * a.rsb + (int64_t)hkv * a.rsh + 2 * lane;
+  const half_t* kr = a.res_k + off;
+  const half_t* vr = a.res_v + off;
+  constexpr int kRB = 16;
+  mr = kNegInf;
+  lr = r0 = r1 = 0.f;
+  for (int t0 = 0; t0 < a.res_n; t0 += kRB) {
+    half2v kb[kRB], vb[kRB];
+#pragma unroll
+    for (int u = 0; u < kRB; ++u) {
+      const int t = t0 + u < a.res_n ? t0 + u : a.res_n - 1;  // in bounds; masked below
+      kb[u] = *reinterpret_cast<const half2v*>(kr + (int64_t)t * kD);
+      vb[u] = *reinterpret_cast<const half2v*>(vr + (int64_t)t * kD);
+    }
+    float sc[kRB];
+    float mx = mr;
+#pragma unroll
+    for (int u = 0; u < kRB; ++u) {
+      const float d = wave_sum64(fmaf(q0, (float)kb[u].x, q1 * (float)kb[u].y));
+      sc[u] = t0 + u < a.res_n ? d * a.sm_log2e : kNegInf;
+      mx = fmaxf(mx, sc[u]);
+    }
+    const float al = fast_exp2(mr - mx);
+    lr *= al;
+    r0 *= al;
+    r1 *= al;
+    mr = mx;
+#pragma unroll
+    for (int u = 0; u < kRB; ++u) {
+      const float p = fast_exp2(sc[u] - mr);
+      lr += p;
+      r0 = fmaf(p, (float)vb[u].x, r0);
+      r1 = fmaf(p, (float)vb[u].y, r1);
+    }
+  }
+}
+
 // The last work-group's merge of the nvalid chunk partials of each query head (its own
 // included, read back like the others), with combine_one's arithmetic.  Wave w takes heads
 // w, w + kTW, ..; lane l the (m, l) pair of chunk l and channels 2 l, 2 l + 1 of every
@@ -205,10 +253,21 @@ __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv
     // every load of the first batch is issued before the (m, l) pair is used (one memory
     // latency, not two)
     asm volatile("" ::: "memory");
+    // the fp16 residual window's partial (KIVI-family V formats), while the chunk partials
+    // are in flight
+    float mr = kNegInf, lr = 0.f, rr0 = 0.f, rr1 = 0.f;
+    if constexpr (VF::kResidual)
+      if (a.res_n > 0) residual_partial(a, b, hkv, hkv * a.n_rep + h, lane, mr, lr, rr0, rr1);
     const float mc = lane < nvalid ? __builtin_bit_cast(float, (uint32_t)mlv.x) : kNegInf;
-    const float M = wave_max64(mc);
+    float M = wave_max64(mc);
+    if constexpr (VF::kResidual) M = fmaxf(M, mr);
     const float e = fast_exp2(mc - M);
-    const float den = wave_sum64(e * __builtin_bit_cast(float, (uint32_t)mlv.y));
+    float den = wave_sum64(e * __builtin_bit_cast(float, (uint32_t)mlv.y));
+    float er = 0.f;  // the window's weight (none without one)
+    if constexpr (VF::kResidual) {
+      er = fast_exp2(mr - M);
+      den = fmaf(er, lr, den);
+    }
     float n0 = 0.f, n1 = 0.f;
     for (int c0 = 0;;) {
 #pragma unroll
@@ -220,7 +279,13 @@ __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv
         n1 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)av[c].y), n1);
       }
       c0 += kUnitBatch;
-      if (c0 >= nvalid) break;
+      if (c0 >= nvalid) {
+        if constexpr (VF::kResidual) {
+          n0 = fmaf(er, rr0, n0);
+          n1 = fmaf(er, rr1, n1);
+        }
+        break;
+      }
 #pragma unroll
       for (int c = 0; c < kUnitBatch; ++c)
         av[c] = __builtin_bit_cast(
@@ -439,6 +504,7 @@ struct KAsymT {
 // x = 16 n 2^-24 (even c, high nibble) or n 2^-24 (odd c) and p the hi + lo probability
 // operands (softmax_tile); the epilogue applies out = s (acc / l * 2^20 or 2^24 - 8) + z.
 struct VAsymT {
+  static constexpr bool kResidual = false;  // merges an fp16 residual window
   static constexpr bool kTile32 = true;
   static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
   // hooks of formats with per-token parameters (none here)
@@ -638,6 +704,7 @@ struct KI8T {
 // acc / l is the output.
 template <bool GS_ANY>
 struct VI8RowT {
+  static constexpr bool kResidual = false;  // merges an fp16 residual window
   static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
   static constexpr bool kTile32 = false;
   // hooks of formats with per-token parameters (none here)
@@ -806,6 +873,7 @@ struct KKiviT : KAsymT<false> {
 // reference dequantises V in fp32).  The wave keeps Lp and Cz beside l (the softmax
 // rescales them with l) and finalize() folds them into acc before the merge (out = acc / l).
 struct VKiviRowT {
+  static constexpr bool kResidual = true;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
   rsrc_t rv, rs, rz;
@@ -1120,6 +1188,7 @@ struct KF16T {
 // (i8pair_exact), the B operand is w = p s_t as a hi + lo pair (two MFMAs per channel), and
 //   sum_t p v = sum_t w c + Cz,   Cz = sum_t p z_t (fp32, rescaled with l by the softmax).
 struct VKivi8RowT {
+  static constexpr bool kResidual = true;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
   rsrc_t rv, rs, rz;
@@ -1231,6 +1300,7 @@ struct VKivi8RowT {
 // 8 col + c is the stored v of the 8 tokens (one v_perm_b32 per token pair), so acc / l is
 // the output.
 struct VF16RowT {
+  static constexpr bool kResidual = true;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
   static constexpr int kRow = 2 * kD;
@@ -1448,6 +1518,7 @@ struct KTokT {
 // (channel 8 col + c) is vhat = fp16(c * fp16(s)) of the 8 tokens, so acc / l is the output.
 template <bool I4>
 struct VTokT {
+  static constexpr bool kResidual = false;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
   static constexpr int kRow = I4 ? kD / 2 : kD;
@@ -1832,10 +1903,15 @@ void decode_tiled_kernel(DecodeArgs a) {
       }
       if (lane == 0) append_status(a.app, afl);
     }
-    if (ntot == 0 && chunk == 0 && a.fused)  // empty context: zero rows
-      for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
-        a.out[(int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + (idx >> 7)) * a.o_sh +
-              (idx & (kD - 1))] = (half_t)0.0f;
+    if (ntot == 0 && chunk == 0 && a.fused) {
+      if (VF::kResidual && a.res_n > 0) {  // empty quantized context: the residual window alone
+        merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, 0, wave, lane);
+      } else {  // empty context: zero rows
+        for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
+          a.out[(int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + (idx >> 7)) * a.o_sh +
+                (idx & (kD - 1))] = (half_t)0.0f;
+      }
+    }
     return;
   }
   // The writer fetches the new rows now and stores their codes in the loop, at the last

@@ -315,6 +315,20 @@ class LayerStep:
         p.out_stride_b, p.out_stride_h = out.stride(0), out.stride(1)
         return out
 
+    def set_residual(self, res_k: Optional[torch.Tensor], res_v: Optional[torch.Tensor], n: int) -> None:
+        """The fp16 residual window attended with the quantized tokens: the first n tokens of
+        res_k / res_v [B, Hkv, R, 128] (fp16, dense rows); n = 0 or None buffers: none."""
+        p = self.params
+        if res_k is None or n <= 0:
+            p.res_k = p.res_v = None
+            p.res_stride_b = p.res_stride_h = 0
+            p.res_tokens = 0
+            return
+        p.res_k, p.res_v = res_k.data_ptr(), res_v.data_ptr()
+        p.res_stride_b, p.res_stride_h = res_k.stride(0), res_k.stride(1)
+        p.res_tokens = int(n)
+        self._res = (res_k, res_v)
+
     def attend(self, q: torch.Tensor, n: int, sm_scale: float,
                inv_tau: Optional[torch.Tensor] = None) -> torch.Tensor:
         """kvq_decode_attn of q [B, Hq, 128] fp16 over the first n tokens of every row."""

@@ -87,7 +87,7 @@ def _ref_layer(kb, vb, k_list, v_list, kp, vp):
     return k_store, ks_, kz_, v_store, vs_, vz_
 
 
-def _check_layer(K, cache, layer, kb, vb, k_list, v_list, kp, vp, g, Hq, tag):
+def _check_codes(cache, layer, kb, vb, k_list, v_list, kp, vp, tag):
     kc, vc, ks, kz, vs, vz = [None if t is None else t.cpu() for t in cache.get_kivi_tensors(layer)]
     rk, rks, rkz, rv, rvs, rvz = _ref_layer(kb, vb, k_list, v_list, kp, vp)
     assert torch.equal(kc, rk), f"{tag} K codes"
@@ -96,6 +96,11 @@ def _check_layer(K, cache, layer, kb, vb, k_list, v_list, kp, vp, g, Hq, tag):
         assert torch.equal(ks, rks) and torch.equal(kz, rkz), f"{tag} K params"
     if vb != 16:
         assert torch.equal(vs, rvs) and torch.equal(vz, rvz), f"{tag} V params"
+    return kc, vc, ks, kz, vs, vz
+
+
+def _check_layer(K, cache, layer, kb, vb, k_list, v_list, kp, vp, g, Hq, tag):
+    kc, vc, ks, kz, vs, vz = _check_codes(cache, layer, kb, vb, k_list, v_list, kp, vp, tag)
     B = kc.shape[0]
     n = kc.shape[2]
     q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
@@ -234,3 +239,48 @@ def test_fp16_pair_partial_tile_ignores_stale_rows():
     ref = OA.decode_attn_kivi_family_ref(q, k0, 16, None, None, v0, 16, None, None, torch.tensor([40]),
                                          1 / math.sqrt(128))
     assert_close_ulp(out, ref, "fp16 stale tail")
+
+
+@pytest.mark.parametrize("bits,R,extra", [(4, 32, 5), (8, 16, 40), (4, 128, 0)])
+def test_kivi_residual_window(bits, R, extra):
+    """residual_length R (src/cache/kivi_style_cache.py:102-113, 354-404): after the prefill,
+    decode tokens fill an fp16 window of R; each later token evicts the oldest into the
+    quantized cache.  Codes bit-exact with the oracle over the evicted tokens, get_kv the
+    dequantized cache followed by the window in arrival order, decode attention over both
+    within the bound; the window alone (an empty quantized context) through the C ABI."""
+    K = _k()
+    print(f"[case] residual bits={bits} R={R} extra={extra}", flush=True)
+    g = gen(1200 + bits + R + extra)
+    B, H, Hq, S0 = 2, 2, 12, 70
+    cache = K.KIVIStyleKVCache(1, device=DEV, quant_bits=bits, residual_length=R, v_percentile=99.9)
+    k0, v0 = _kv(B, H, S0, g)
+    cache.append(0, k0.to(DEV), v0.to(DEV))
+    dec_k, dec_v = [], []
+    for _ in range(R + extra):
+        k1, v1 = _kv(B, H, 1, g)
+        cache.append(0, k1.to(DEV), v1.to(DEV))
+        dec_k.append(k1)
+        dec_v.append(v1)
+    torch.cuda.synchronize()
+    assert cache.get_seq_len() == S0 + R + extra
+    assert cache._layer_seq_lens[0] == S0 + extra and cache._res_len[0] == R
+    kc, vc, ks, kz, vs, vz = _check_codes(cache, 0, bits, bits, [k0] + dec_k[:extra], [v0] + dec_v[:extra],
+                                          100.0, 99.9, f"residual{bits} quantized part")
+    k_all, v_all = cache.get_kv(0)
+    win_k, win_v = torch.cat(dec_k[extra:], 2), torch.cat(dec_v[extra:], 2)
+    assert torch.equal(k_all[:, :, S0 + extra:].cpu(), win_k) and torch.equal(v_all[:, :, S0 + extra:].cpu(), win_v)
+    kd = torch.cat([OA.dequant_kivi_side(kc, bits, ks, kz, True), win_k.float()], 2)
+    vd = torch.cat([OA.dequant_kivi_side(vc, bits, vs, vz, False), win_v.float()], 2)
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+    out = cache.decode_attn(0, q.to(DEV))
+    torch.cuda.synchronize()
+    ref = OA.attention_fp32(q, kd, vd, torch.full((B,), kd.shape[2]), 1 / math.sqrt(128))
+    assert_close_ulp(out, ref, f"residual{bits} R{R} decode")
+    # the window alone: a quantized context of 0 tokens
+    st = cache._step_for(0, Hq)
+    st.set_residual(cache._res_k[0], cache._res_v[0], R)
+    out0 = st.attend(q.to(DEV), 0, 1 / math.sqrt(128))
+    torch.cuda.synchronize()
+    rk, rv = cache._res_k[0].cpu(), cache._res_v[0].cpu()
+    ref0 = OA.attention_fp32(q, rk.float(), rv.float(), torch.full((B,), R), 1 / math.sqrt(128))
+    assert_close_ulp(out0, ref0, f"residual{bits} R{R} window only")
