@@ -105,6 +105,32 @@ __device__ __forceinline__ int wave_sum_int(int x) {
   return x;
 }
 
+// Wave-wide max / sum without the LDS crossbar: DPP within each row of 16 lanes (xor 1,
+// xor 2 in the quad, then rotations by 4 and 8), then the four row results by readlane.
+// Every lane gets the same value; the order of operations is fixed.
+template <int CTRL>
+__device__ __forceinline__ float dppf(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_lane(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+__device__ __forceinline__ float wave_max64(float x) {
+  x = fmaxf(x, dppf<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+  x = fmaxf(x, dppf<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+  x = fmaxf(x, dppf<0x124>(x));  // row_ror:4
+  x = fmaxf(x, dppf<0x128>(x));  // row_ror:8
+  return fmaxf(fmaxf(row_lane(x, 0), row_lane(x, 16)), fmaxf(row_lane(x, 32), row_lane(x, 48)));
+}
+__device__ __forceinline__ float wave_sum64(float x) {
+  x += dppf<0xB1>(x);
+  x += dppf<0x4E>(x);
+  x += dppf<0x124>(x);
+  x += dppf<0x128>(x);
+  return (row_lane(x, 0) + row_lane(x, 16)) + (row_lane(x, 32) + row_lane(x, 48));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // max of 8 floats with v_max3_f32 (no NaN canonicalisation; inputs are finite or -inf)

@@ -32,6 +32,8 @@ int fail(int code, const std::string& msg);
 
 constexpr int kAppendWaves = 4;
 constexpr int kRescueMax = 4096;  // (rows x groups) handled by the single-work-group rescue path
+constexpr int kRescueRank = 1024;  // (rows x groups) up to which every work-group finds the
+                                   // threshold itself by rank counting (decode-sized appends)
 constexpr int kRowBatch = 8;      // rows per wave loaded at once on that path
 constexpr int kTopWalk = 32;      // that path walks down from the maximum when the quantile's
                                   // ranks lie within kTopWalk of the top; else it sorts
@@ -94,6 +96,19 @@ __device__ __forceinline__ float ld_static(const AppendDev& a, int h, int g) {
 // max over the lanes of one quantisation group (gs/2 consecutive lanes)
 __device__ __forceinline__ float group_max(float v, int gs) {
   for (int o = 1; o < gs / 2; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// group_max for values >= +0 (absolute values: the order of the maxima cannot change a bit)
+// with DPP instead of the LDS crossbar: xor 1 and 2 within the quad, then the half-row and
+// row mirrors (lane i with 7 - i, 15 - i), which pair lanes of the two already reduced halves
+__device__ __forceinline__ float group_absmax(float v, int gs) {
+  v = fmaxf(v, dppf<0xB1>(v));                       // quad_perm [1, 0, 3, 2]
+  if (gs >= 8) v = fmaxf(v, dppf<0x4E>(v));          // quad_perm [2, 3, 0, 1]
+  if (gs >= 16) v = fmaxf(v, dppf<0x141>(v));        // row_half_mirror
+  if (gs >= 32) v = fmaxf(v, dppf<0x140>(v));        // row_mirror
+  if (gs >= 64) v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if (gs >= 128) v = fmaxf(v, __shfl_xor(v, 32, 64));
   return v;
 }
 
@@ -335,8 +350,8 @@ __device__ __forceinline__ float row_static(const AppendDev& a, int row, int lan
 
 // Quantizes append row `row` whose lane values xv (and static scale stv, row_static) were
 // loaded by the caller.
-__device__ void quant_row_x(const AppendDev& a, int row, int lane, float thr, half2v xv,
-                            float stv) {
+__device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lane, float thr,
+                                            half2v xv, float stv) {
   const int s_idx = row % a.S;
   const int bh = row / a.S;
   const int h = bh % a.H, b = bh / a.H;
@@ -518,6 +533,36 @@ __device__ float lds_top_quantile(const float* v, int n, int lo, int hi, float w
   return quantile_lerp(vlo, vhi, w);
 }
 
+// lds_top_quantile by one wave alone, without barriers: lane l holds the scales v[l + 64 r]
+// (r < R, n <= 64 R) in registers, and the maximum and multiplicity of each step are DPP
+// wave reductions (the count summed as an exact small float).  Every lane returns the
+// result.
+template <int R>
+__device__ float wave_top_quantile(const float* v, int n, int lo, int hi, float w, int lane) {
+  float x[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) x[r] = lane + 64 * r < n ? v[lane + 64 * r] : -1.0f;  // below every scale
+  float t = __builtin_inff(), vlo = 0.f, vhi = 0.f;
+  int above = 0;
+  for (int it = 0; it < kTopWalk && above <= n - 1 - lo; ++it) {
+    float m = -1.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (x[r] < t) m = fmaxf(m, x[r]);
+    m = wave_max64(m);
+    float cf = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) cf += x[r] == m ? 1.f : 0.f;
+    const int c = (int)wave_sum64(cf);
+    const int r0 = n - above - c, r1 = n - above;
+    if (lo >= r0 && lo < r1) vlo = m;
+    if (hi >= r0 && hi < r1) vhi = m;
+    above += c;
+    t = m;
+  }
+  return quantile_lerp(vlo, vhi, w);
+}
+
 // torch.quantile(x, q) with linear interpolation, float32 arithmetic:
 // rank = fp32(q) * (n - 1); lo = floor(rank); hi = ceil(rank); w = rank - lo;
 // quantile_lerp(v[lo], v[hi], w)
@@ -527,19 +572,86 @@ __device__ float sorted_quantile(const float* v, int n, float q) {
   return quantile_lerp(v[lo], v[hi], rank - (float)lo);
 }
 
-__global__ __launch_bounds__(kAppendWaves * 64) void append_kernel(AppendDev k, AppendDev v,
-                                                                    int rescue) {
-  const AppendDev& a = blockIdx.y == 0 ? k : v;
+// rescue: 0 none (or the threshold in a.thr_ptr), 1 one work-group finds the threshold and
+// quantizes every row, 2 every work-group finds it (rank counting) and quantizes its own rows
+__device__ __forceinline__ void append_side(const AppendDev& a, int rescue) {
   if (!a.valid) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rows = a.B * a.H * a.S;
   float thr = a.thr_ptr ? *a.thr_ptr : 0.f;
-  if (rescue && a.fmt == KVQ_FMT_INT4_SYM && a.st != nullptr && a.rq > 0.f && !a.rescue_all) {
+  __shared__ float dyn[kRescueMax];
+  const bool resc_side = a.fmt == KVQ_FMT_INT4_SYM && a.st != nullptr && a.rq > 0.f && !a.rescue_all;
+  if (rescue == 2 && resc_side) {
+    // Global threshold over every (row, group) dynamic scale of this append
+    // (int4_cache.py:384-389), found by each work-group over all rows (n <= kRescueRank):
+    // near the top (the reference's ratio 0.01) every wave walks down from the maximum on
+    // its own (wave_top_quantile); elsewhere the scale at ascending position p of the
+    // stable order is the one with p smaller values or equal values at lower indices, which
+    // gives sorted[lo] and sorted[hi] without sorting.  Wave w then quantizes row
+    // 4 blockIdx.x + w, which it loads first (the rows are visited rotated by 4 blockIdx.x).
+    __shared__ float ord[2];
+    const int G = 128 / a.gs;
+    const int n = rows * G;
+    const int n4 = (n + 3) & ~3;
+    const int own = blockIdx.x * kAppendWaves + wave;
+    const int rot = (int)(((int64_t)blockIdx.x * kAppendWaves) % rows);
+    for (int i = n + threadIdx.x; i < n4; i += blockDim.x) dyn[i] = __builtin_inff();
+    if (threadIdx.x < 2) ord[threadIdx.x] = 0.f;
+    const float own_st = own < rows ? row_static(a, own, lane) : 0.f;
+    half2v own_x = half2v{(half_t)0.f, (half_t)0.f};
+    for (int r0 = wave; r0 < rows; r0 += kRowBatch * kAppendWaves) {
+      half2v xb[kRowBatch];
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        const int r = r0 + u * kAppendWaves;
+        if (r < rows) xb[u] = load_x(a, (r + rot) % rows, lane);
+      }
+      if (r0 == wave) own_x = xb[0];  // row (wave + rot) % rows == own when own < rows
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        const int r = r0 + u * kAppendWaves;
+        if (r >= rows) break;
+        const int row = (r + rot) % rows;
+        const float am = group_absmax(fmaxf(fabsf((float)xb[u].x), fabsf((float)xb[u].y)), a.gs);
+        if ((2 * lane) % a.gs == 0) dyn[row * G + (2 * lane) / a.gs] = __fdiv_rn(fmaxf(am, 1e-5f), 7.0f);
+      }
+    }
+    __syncthreads();
+    const float rank = a.rq * (float)(n - 1);
+    const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
+    const float wgt = rank - (float)lo;
+    if (n - 1 - lo < kTopWalk) {  // uniform over the work-group
+      thr = n <= 64    ? wave_top_quantile<1>(dyn, n, lo, hi, wgt, lane)
+            : n <= 128 ? wave_top_quantile<2>(dyn, n, lo, hi, wgt, lane)
+            : n <= 256 ? wave_top_quantile<4>(dyn, n, lo, hi, wgt, lane)
+            : n <= 512 ? wave_top_quantile<8>(dyn, n, lo, hi, wgt, lane)
+                       : wave_top_quantile<kRescueRank / 64>(dyn, n, lo, hi, wgt, lane);
+    } else {
+      const float4* d4 = reinterpret_cast<const float4*>(dyn);
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float vi = dyn[i];
+        int c = 0;
+        for (int j = 0; j < n4; j += 4) {
+          const float4 w = d4[j >> 2];  // padding (+inf) is neither smaller nor equal at a lower index
+          c += (w.x < vi) | ((w.x == vi) & (j < i));
+          c += (w.y < vi) | ((w.y == vi) & (j + 1 < i));
+          c += (w.z < vi) | ((w.z == vi) & (j + 2 < i));
+          c += (w.w < vi) | ((w.w == vi) & (j + 3 < i));
+        }
+        if (c == lo) ord[0] = vi;
+        if (c == hi) ord[1] = vi;
+      }
+      __syncthreads();
+      thr = quantile_lerp(ord[0], ord[1], wgt);
+    }
+    if (own < rows) quant_row_x(a, own, lane, thr, own_x, own_st);
+    return;
+  }
+  if (rescue == 1 && resc_side) {
     // Global threshold over every (row, group) dynamic scale of this append
     // (int4_cache.py:384-389).  Single work-group: grid.x == 1 on this path.  Each wave
     // handles rows wave, wave + 8, ..: kRowBatch of them loaded at once, so one memory
     // latency covers the batch; the values stay in registers for the quantization.
-    __shared__ float dyn[kRescueMax];
     __shared__ float thr_sh;
     const int G = 128 / a.gs;
     const int n = rows * G;
@@ -602,6 +714,16 @@ __global__ __launch_bounds__(kAppendWaves * 64) void append_kernel(AppendDev k, 
   }
   for (int row = blockIdx.x * kAppendWaves + wave; row < rows; row += gridDim.x * kAppendWaves)
     quant_row(a, row, lane, thr);
+}
+
+// grid.y selects the side; each branch reads its own kernel arguments directly (selecting
+// between the two structs field by field costs scalar registers)
+__global__ __launch_bounds__(kAppendWaves * 64) void append_kernel(AppendDev k, AppendDev v,
+                                                                    int rescue) {
+  if (blockIdx.y == 0)
+    append_side(k, rescue);
+  else
+    append_side(v, rescue);
 }
 
 static int fill_dev(const kvq_append_params* p, AppendDev& d, const char* name) {
@@ -746,11 +868,17 @@ extern "C" int kvq_quant_append(const kvq_append_params* k, const kvq_append_par
     if (needs_rescue(k) && (rc = rescue_large(k, dk, "k", s))) return rc;
     if (needs_rescue(v) && (rc = rescue_large(v, dv, "v", s))) return rc;
   }
-  const int rescue = !large && (needs_rescue(k) || needs_rescue(v));
+  // decode-sized rescues (at most kRescueRank scales per side): every work-group finds the
+  // threshold; else one work-group does
+  int rescue = 0;
+  if (!large && (needs_rescue(k) || needs_rescue(v))) {
+    const int64_t nk = needs_rescue(k) ? rescue_n(k) : 0, nv = needs_rescue(v) ? rescue_n(v) : 0;
+    rescue = (nk > nv ? nk : nv) <= kRescueRank ? 2 : 1;
+  }
   int64_t rows = 0;
   if (dk.valid) rows = (int64_t)dk.B * dk.H * dk.S;
   if (dv.valid) rows = rows > (int64_t)dv.B * dv.H * dv.S ? rows : (int64_t)dv.B * dv.H * dv.S;
-  int64_t gx = rescue ? 1 : (rows + kAppendWaves - 1) / kAppendWaves;
+  int64_t gx = rescue == 1 ? 1 : (rows + kAppendWaves - 1) / kAppendWaves;
   if (gx > 65535) gx = 65535;
   hipLaunchKernelGGL(append_kernel, dim3((unsigned)gx, 2), dim3(kAppendWaves * 64), 0, s, dk, dv,
                      rescue);

@@ -149,25 +149,32 @@ def test_append_int4_sym_bitexact(mode, S):
         assert torch.equal(s_gpu.cpu().float(), ref_s.float()), (mode, tag)
 
 
-@pytest.mark.parametrize("B,H,S,ratio,ties", [
-    (2, 4, 2048, 0.01, False),    # 65,536 scales: the radix-select path
-    (1, 2, 600, 0.3, True),       # 4,800 scales, many equal (ties at the threshold)
-    (4, 2, 4096, 0.001, False),   # 131,072 scales, a threshold in the far tail
-    (2, 2, 256, 0.05, False),     # 4,096 scales: the one-work-group sort path
-    (8, 4, 1, 0.01, False),       # a decode step (128 scales): the walk from the top
-    (16, 4, 1, 0.01, True),       # 64 rows (reloaded for the quantization), ties
-    (8, 4, 1, 0.1, False),        # 13 ranks below the top
-    (4, 2, 16, 0.05, True),       # 512 scales, 26 ranks below the top, ties
+@pytest.mark.parametrize("B,H,S,ratio,ties,gs", [
+    (2, 4, 2048, 0.01, False, 32),    # 65,536 scales: the radix-select path
+    (1, 2, 600, 0.3, True, 32),       # 4,800 scales, many equal (ties at the threshold)
+    (4, 2, 4096, 0.001, False, 32),   # 131,072 scales, a threshold in the far tail
+    (2, 2, 256, 0.05, False, 32),     # 4,096 scales: the one-work-group sort path
+    (40, 8, 1, 0.01, True, 32),       # 1,280 scales: the one-work-group walk from the top
+    (8, 4, 1, 0.01, False, 32),       # a decode step (128 scales): rank counting
+    (16, 4, 1, 0.01, True, 32),       # 64 rows, ties
+    (8, 4, 1, 0.1, False, 32),        # 13 ranks below the top
+    (4, 2, 16, 0.05, True, 32),       # 512 scales, 26 ranks below the top, ties
+    (8, 4, 1, 0.01, False, 16),       # config 3's decode step at group 16 (256 scales)
+    (3, 3, 1, 0.2, False, 128),       # 9 rows and 9 scales (not a multiple of 4)
+    (32, 8, 1, 0.01, True, 32),       # 1,024 scales: the most that are rank-counted
+    (2, 2, 7, 0.5, True, 16),         # the median, ties: counted ranks
+    (16, 8, 1, 0.3, True, 32),        # 512 scales, 154 ranks below the top: counted ranks
 ])
-def test_append_int4_rescue_large_bitexact(B, H, S, ratio, ties):
-    """INT4 group outlier rescue over the dynamic scales of a prefill-sized append: the
-    torch.quantile threshold (int4_cache.py:384-390) by the radix select in the scratch
-    buffer (more than 4096 scales) or the LDS sort, codes and scales bit-exact."""
+def test_append_int4_rescue_large_bitexact(B, H, S, ratio, ties, gs):
+    """INT4 group outlier rescue over the dynamic scales of an append: the torch.quantile
+    threshold (int4_cache.py:384-390) by the radix select in the scratch buffer (more than
+    4096 scales), one work-group's LDS sort or walk from the top (1025-4096), or rank
+    counting in every work-group (at most 1024), codes and scales bit-exact."""
     K = _lib()
     from llm_kvcache_quantization_amd import _capi as C
 
     g = gen(3000 + S)
-    D, gs = 128, 32
+    D = 128
     k = (torch.randn(B, H, S, D, generator=g) * 1.5).to(torch.float16)
     v = torch.randn(B, H, S, D, generator=g).to(torch.float16)
     if ties:  # few distinct group absmax values
