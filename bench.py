@@ -389,6 +389,11 @@ MODE_SETTINGS = {
     "int4_fused": dict(static=True, group_size=16, outlier_rescue_ratio=0.01),
     "int4_ours": dict(static=True, group_size=16, outlier_rescue_ratio=0.01),
     "int4_ours_mixed": dict(static=True, group_size=16, outlier_rescue_ratio=0.01, mixed_rescue=True),
+    # KIVI family and the mixed cache (per-channel K frozen at prefill, per-token V; the
+    # mixed cache's dynamic INT8 K in groups of 128 with per-token asymmetric INT4 V)
+    "kivi_style": dict(family=True, group_size=128),
+    "int4_kivi_aligned": dict(family=True, group_size=128),
+    "int4_mixed_kv": dict(family=True, group_size=128),
 }
 
 
@@ -400,7 +405,8 @@ def modes_leg(cfg, mode, device, steps, warmup):
     through ``append`` a few tokens short of the context; then ``append_decode_attn`` runs
     for every layer per step (check_numerics off: no host read-back), timed with
     hipEvents.  Algorithmic bytes per call: each context token's K and V codes and the
-    per-token scales the engine stores (static tables: none), q and out."""
+    per-token scales (and zero-points) the engine stores (static tables: none), the KIVI
+    family's per-channel K parameters once per (b, kv head), q and out."""
     import llm_kvcache_quantization_amd as K
     from llm_kvcache_quantization_amd import calib as CB
     from llm_kvcache_quantization_amd import modes as M
@@ -415,7 +421,7 @@ def modes_leg(cfg, mode, device, steps, warmup):
     cal = M.Calibration(group_size=gs, clip_percentile=99.9,
                         outlier_rescue_ratio=st.get("outlier_rescue_ratio", 0.0),
                         mixed_rescue=st.get("mixed_rescue", False))
-    if st["static"]:
+    if st.get("static"):
         make = CB.int8_static_scale if mode.startswith("int8") else CB.int4_static_scale
         ks, vs = [], []
         for l in range(nl):
@@ -428,8 +434,13 @@ def modes_leg(cfg, mode, device, steps, warmup):
         cal.inv_tau = SY.inv_tau(cfg).float().to(device)
     calls = 2 + warmup + steps
     s0 = ((cfg.context - calls) // 32) * 32
-    cache = M.create_kv_cache(mode, nl, device=device, max_seq_len=cfg.context, calib=cal,
-                              check_numerics=False)
+    family = st.get("family", False)
+    if family:
+        cache = M.create_kv_cache(mode, nl, device=device, max_seq_len=cfg.context, group_size=gs,
+                                  check_numerics=False)
+    else:
+        cache = M.create_kv_cache(mode, nl, device=device, max_seq_len=cfg.context, calib=cal,
+                                  check_numerics=False)
     gen = torch.Generator(device=device).manual_seed(SY.seed_for(cfg.index, 0) + 6)
     for l in range(nl):
         k, v = SY.draw_kv(cfg, l % cfg.layers, cfg.batch, s0, gen, device=device)
@@ -459,15 +470,33 @@ def modes_leg(cfg, mode, device, steps, warmup):
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (steps * nl)
     n_mid = s0 + 1 + warmup + (steps + 1) // 2
-    kc, vc, kst, vst = cache._raw_views(0)
-    per_tok = kc.shape[-1] + vc.shape[-1]
-    for tok, s in ((cache._k_tok[0], kst), (cache._v_tok[0], vst)):
-        if tok:
-            per_tok += s.shape[-1] * s.element_size()
-    nbytes = cfg.batch * cfg.kv_heads * n_mid * per_tok + 2 * cfg.batch * cfg.q_heads * 128 * 2
-    fused = cache._fused_step_ok(128)
+    per_bh = 0  # bytes read once per (b, kv head): the KIVI family's per-channel K parameters
+    if family:
+        # every stored tensor: per token ([B, H, n, ...] or [B, H, n]) or per (b, kv head)
+        ts = cache.get_kivi_tensors(0) if hasattr(cache, "get_kivi_tensors") else cache.get_mixed_tensors(0)
+        n_now = ts[0].shape[2]
+        per_tok = 0
+        for t in ts:
+            if t is None:
+                continue
+            if t.shape[2] == n_now:
+                per_tok += (t.shape[3] if t.ndim == 4 else 1) * t.element_size()
+            else:
+                per_bh += t[0, 0].numel() * t.element_size()
+        fused = getattr(cache, "residual_length", 0) == 0
+        tok_scales = None
+    else:
+        kc, vc, kst, vst = cache._raw_views(0)
+        per_tok = kc.shape[-1] + vc.shape[-1]
+        for tok, s in ((cache._k_tok[0], kst), (cache._v_tok[0], vst)):
+            if tok:
+                per_tok += s.shape[-1] * s.element_size()
+        fused = cache._fused_step_ok(128)
+        tok_scales = [bool(cache._k_tok[0]), bool(cache._v_tok[0])]
+    nbytes = (cfg.batch * cfg.kv_heads * (n_mid * per_tok + per_bh) +
+              2 * cfg.batch * cfg.q_heads * 128 * 2)
     res = {"kv_mode": mode, "engine": type(cache).__name__, "group_size": gs,
-           "static_scales": st["static"], "per_token_scales": [bool(cache._k_tok[0]), bool(cache._v_tok[0])],
+           "static_scales": bool(st.get("static")), "per_token_scales": tok_scales,
            "fused_step": bool(fused), "layers": nl, "batch": cfg.batch, "context_mid": n_mid,
            "us_per_layer_step": round(us, 3), "host_us_per_call": round(host * 1e6 / (steps * nl), 3),
            "bytes_per_call": nbytes, "GBps": round(nbytes / us / 1e3, 1),

@@ -55,7 +55,8 @@ typedef struct ihipStream_t* kvq_stream_t; /* == hipStream_t */
                                 cache); append: range floor 255 * 2^-14, s = range / 255,
                                 z = min + 128 s */
 #define KVQ_FMT_FP16 6       /* fp16 values [..., D] as stored (a 16-bit side of the
-                                reference's mixed / allocator caches); decode only */
+                                reference's mixed / allocator caches); an append copies the
+                                row (codes = the fp16 rows, byte strides, no scales) */
 
 /* code layouts (kvq_kv_view.layout, kvq_append_params.codes_layout) */
 #define KVQ_LAYOUT_ROWS 0   /* token-major: the code bytes of token t start at t * stride_t */
@@ -259,13 +260,20 @@ int64_t kvq_append_scratch_bytes(const kvq_append_params* p);
  *   decode_attn_*(q, caches..., ctx)     src/engine/patch_model.py:837-957
  * with the codes and the output bit-identical to kvq_quant_append then kvq_decode_attn.
  * Supported for the formats the tiled kernel serves (see kvq_decode_attn), with k_new /
- * v_new of seq_new 1, group 32, a static scale table and no scale policy (adaptive,
- * rescue, scale_out).  k_new and v_new must name the very code buffers and strides p
- * reads and share write_pos; an INT4_ASYM side must also name p's static tables and
- * outlier side-band, while an INT8_SYM side quantizes with its own table (fp16 or fp32),
- * as kvq_quant_append would.  Anything else returns KVQ_ERR_UNSUPPORTED (or
- * KVQ_ERR_INVALID), and the caller makes the two calls instead.  The status words are
- * updated as kvq_quant_append does. */
+ * v_new of seq_new 1 sharing write_pos and naming the very code buffers and strides p
+ * reads:
+ *  - INT4_ASYM K with TILE32 V, static INT8 K with TILE32 INT4_ASYM V or static INT8 V
+ *    rows: a static scale table and no scale policy (adaptive, rescue, scale_out); an
+ *    INT4_ASYM side must name p's static tables and outlier side-band, an INT8_SYM side
+ *    quantizes with its own table (fp16 or fp32), as kvq_quant_append would;
+ *  - the row formats (per-token INT8_SYM / INT4_SYM scales in dense rows with groups of 16
+ *    or more, INT4_KIVI / INT8_KIVI, FP16 sides): any policy kvq_quant_append takes except
+ *    the INT4_SYM group rescue with a threshold (rescue_quantile > 0 without rescue_all),
+ *    which spans every row of the append; scale_out / zp_out and KIVI K's static
+ *    parameters must be the buffers p reads.  The decode kernel's writer wave runs the
+ *    append kernel's row arithmetic.
+ * Anything else returns KVQ_ERR_UNSUPPORTED (or KVQ_ERR_INVALID), and the caller makes the
+ * two calls instead.  The status words are updated as kvq_quant_append does. */
 int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
                            const kvq_append_params* v_new, kvq_stream_t stream);
 

@@ -474,9 +474,10 @@ class _SymCacheBase(_EngineBase):
         over the whole cache, the new token included (the append + attention of the
         reference's decode step, src/engine/patch_model.py:755-957).  q: fp16 [B, Hq, D];
         inv_tau: optional fp16 [Hq], applied as fp16(q * inv_tau) in the kernel.  Returns
-        fp16 [B, Hq, D].  With static INT8 scales on both sides (no adaptive policy) both run
-        in one HIP launch (kvq_append_decode_attn); otherwise ``append`` then the decode
-        kernel.
+        fp16 [B, Hq, D].  Both run in one HIP launch (kvq_append_decode_attn) with static
+        INT8 scales on both sides, or with the tiled kernel's per-token formats (groups of 16
+        or more; not the INT4 group rescue, whose threshold spans every row of the append);
+        otherwise ``append`` then the decode kernel.
         Either way codes and output are bit-identical to ``append`` followed by
         :func:`kernels.decode_attn_int8` / ``decode_attn_int4`` over the cache's tensors.
         The kernel parameters are kept per layer between calls (no device tensor is created
@@ -625,8 +626,11 @@ class INT8KVCache(_SymCacheBase):
         return self._raw_views(layer_id)
 
     def _fused_step_ok(self, D: int) -> bool:
-        return (self.group_size in (8, 16, 32, 64, 128) and D == 128
-                and not self._side_is_token("k") and not self._side_is_token("v"))
+        # static tables on both sides (any group size), or per-token scales in groups of 16 or
+        # more (the tiled kernel's row formats; its writer runs the append's arithmetic)
+        if D != 128 or self.group_size not in (8, 16, 32, 64, 128):
+            return False
+        return self.group_size >= 16 or not (self._side_is_token("k") or self._side_is_token("v"))
 
     def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
         """Dequantize (code * scale in fp32) and return fp16 K/V (int8_cache.py:490-542)."""
@@ -706,6 +710,14 @@ class INT4KVCache(_SymCacheBase):
 
     def _effective_static(self, s):
         return s.to(torch.float32).clamp(min=1e-5)
+
+    def _fused_step_ok(self, D: int) -> bool:
+        # the tiled kernel's row format (groups of 16 or more) appends in the same launch
+        # unless the group rescue needs its threshold over every row of the append
+        # (int4_cache.py:384-390), which a launch computes before quantizing any row
+        rescue = 0.0 < self.outlier_rescue_ratio < 1.0 and (
+            self.static_k_scale is not None or self.static_v_scale is not None)
+        return D == 128 and self.group_size >= 16 and not rescue
 
     def _policy(self, p, side):
         adaptive = self.adaptive_static_scales and (
@@ -1417,14 +1429,73 @@ class _KiviFamily(_EngineBase):
         """Decode step of one layer: ``append`` of the new token (k, v [B, H, 1, 128]) then
         the attention of q [B, Hq, 128] over the cache including it.  inv_tau (fp16 [Hq]) is
         applied as given, as in the symmetric engines; None applies none (``decode_attn``
-        applies the engine's own)."""
-        if k.shape[2] != 1:
+        applies the engine's own).  After the prefill, without a residual window and without
+        a K range check due at this step, both run in one HIP launch
+        (kvq_append_decode_attn, the append's arithmetic in the decode kernel's writer wave);
+        codes, parameters and output are the same bits as the two-launch path."""
+        if k.ndim != 4 or k.shape[2] != 1:
             raise ValueError(f"append_decode_attn appends one token per step, got S={k.shape[2]}")
-        self.append(layer_id, k, v)
         if q.dtype != torch.float16 or q.stride(-1) != 1:
             q = q.to(torch.float16).contiguous()
         sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
-        return self._attend(layer_id, q, sm, inv_tau)
+        kb, _ = self._bits[layer_id] if 0 <= layer_id < self.num_layers else (16, 16)
+        fused = (self.residual_length == 0 and self._k_cache[layer_id] is not None
+                 and (kb == 16 or self._k_scale_initialized[layer_id])
+                 and (kb == 16 or self._oor_check_interval <= 0))
+        if not fused:
+            self.append(layer_id, k, v)
+            return self._attend(layer_id, q, sm, inv_tau)
+        self._validate_kv(layer_id, k, v)
+        B, H = k.shape[0], k.shape[1]
+        old = self._layer_seq_lens[layer_id]
+        self._ensure(layer_id, B, H, old + 1, k.device)
+        ks = self._k_scale[layer_id]
+        if kb != 16 and tuple(ks.shape) != (B, H, 128):
+            raise ValueError(f"Inconsistent decode K scale/zp shape for layer {layer_id}: "
+                             f"expected {(B, H, 128)}, got {tuple(ks.shape)}")
+        pk, pv = self._fused_apps(layer_id, k, v, old)
+        st = self._step_for(layer_id, q.shape[1])
+        st.set_residual(None, None, 0)
+        out = st.append_attend(q, old + 1, sm, inv_tau, pk, pv)
+        self._layer_seq_lens[layer_id] = old + 1
+        self._seq_len = max(self._layer_seq_lens)
+        return out
+
+    def _fused_apps(self, layer_id: int, k: Tensor, v: Tensor, pos: int):
+        """The fused decode step's kvq_append_params of K and V (one token), kept per layer
+        buffers; per call the rows and the slot change.  A quantized side is set up as
+        ``append`` sets it up; a 16-bit side is an FP16 append (the row stored as it comes)."""
+        kb, vb = self._bits[layer_id]
+        kc, vc = self._k_cache[layer_id], self._v_cache[layer_id]
+        ks, kz = self._k_scale[layer_id], self._k_zp[layer_id]
+        key = (kc.data_ptr(), None if ks is None else ks.data_ptr(), tuple(k.shape[:2]))
+        ent = self._apps[layer_id]
+        if ent is None or ent[2] != key:
+            pk, pv = C.AppendParams(), C.AppendParams()
+            for p, x, bits, buf in ((pk, k, kb, kc), (pv, v, vb, vc)):
+                _fill_append(p, _kivi_format(bits), x, 32, buf, pos, None)
+                if bits == 16:  # byte strides of the fp16 rows
+                    p.codes_stride_b, p.codes_stride_h, p.codes_stride_t = (2 * t for t in buf.stride()[:3])
+            if kb != 16:
+                pk.static_scale, pk.static_zp = ks.data_ptr(), kz.data_ptr()
+                pk.static_scale_dtype = C.KVQ_DTYPE_F32
+                pk.static_stride_b, pk.static_stride_h, pk.static_stride_g = ks.stride()
+            if vb != 16:
+                vs, vz = self._v_scale[layer_id], self._v_zp[layer_id]
+                pv.scale_out, pv.zp_out, pv.scale_out_dtype = vs.data_ptr(), vz.data_ptr(), C.KVQ_DTYPE_F32
+                pv.so_stride_b, pv.so_stride_h, pv.so_stride_t = vs.stride()
+                pv.dyn_quantile_lo, pv.dyn_quantile = _kivi_levels(self.v_percentile)
+            ent = (pk, pv, key)
+            self._apps[layer_id] = ent
+        pk, pv = ent[0], ent[1]
+        for p, x in ((pk, k), (pv, v)):
+            if x.stride(-1) != 1:
+                x = x.contiguous()
+            p.x = x.data_ptr()
+            p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride()[:3]
+            p.write_pos = pos
+            p._keep = (x,)
+        return pk, pv
 
     def clear(self) -> None:
         self._layer_seq_lens = [0] * self.num_layers
@@ -1698,15 +1769,29 @@ class MixedKVCache(_EngineBase):
         self._layer_capacity[layer_id] = new_cap
         self._steps[layer_id] = self._apps[layer_id] = None
 
-    def _params(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status) -> Tuple:
+    def _params(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status,
+                fp16: bool = False) -> Tuple:
         """kvq_append_params of the quantized sides (K INT8 dynamic, V INT4_KIVI per token or
-        INT8 dynamic) writing at slot pos, None for a 16-bit side; the one-token blocks of a
-        decode step are kept per layer."""
+        INT8 dynamic) writing at slot pos; a 16-bit side gets None, or with fp16 an FP16
+        append (the row stored as it comes, for the fused decode step).  The one-token blocks
+        of a decode step are kept per layer."""
         S = k.shape[2]
         kb, vb = self._bits[layer_id]
-        ent = self._apps[layer_id] if S == 1 else None
+        ents = self._apps[layer_id] if S == 1 else None
+        ent = None if ents is None else ents.get(fp16)
         if ent is None:
             pk = pv = None
+            if fp16:
+                for side, bits, buf in (("k", kb, self._k_cache[layer_id]), ("v", vb, self._v_cache[layer_id])):
+                    if bits == 16:
+                        pf = C.AppendParams()
+                        _fill_append(pf, C.KVQ_FMT_FP16, k if side == "k" else v, 32, buf, pos, None)
+                        pf.codes_stride_b, pf.codes_stride_h, pf.codes_stride_t = (2 * t for t in buf.stride()[:3])
+                        pf._fp16 = True
+                        if side == "k":
+                            pk = pf
+                        else:
+                            pv = pf
             if kb == 8:
                 pk = C.AppendParams()
                 ks = self._k_scale[layer_id]
@@ -1730,7 +1815,7 @@ class MixedKVCache(_EngineBase):
                 pv.so_stride_b, pv.so_stride_h, pv.so_stride_t, pv.so_stride_g = vs.stride()
             ent = (pk, pv)
             if S == 1:
-                self._apps[layer_id] = ent
+                self._apps[layer_id] = {**(ents or {}), fp16: ent}
         pk, pv = ent
         sptr = None if status is None else status.data_ptr()
         for p, x, off in ((pk, k, 0), (pv, v, 8)):
@@ -1740,7 +1825,8 @@ class MixedKVCache(_EngineBase):
             p.x_stride_b, p.x_stride_h, p.x_stride_s = x.stride()[:3]
             p.seq_new = S
             p.write_pos = pos
-            p.status = None if sptr is None else sptr + off
+            # a 16-bit side is stored as it comes, unchecked (as the two-launch path's copy)
+            p.status = None if sptr is None or getattr(p, "_fp16", False) else sptr + off
             p._keep = (x,)
         return pk, pv
 
@@ -1859,14 +1945,38 @@ class MixedKVCache(_EngineBase):
                            sm_scale: Optional[float] = None,
                            inv_tau: Optional[Tensor] = None) -> Tensor:
         """Decode step of one layer: the new token (k, v [B, H, 1, 128]) appended, then the
-        attention of q [B, Hq, 128] over the cache including it (two HIP launches)."""
+        attention of q [B, Hq, 128] over the cache including it, in one HIP launch
+        (kvq_append_decode_attn: the append's arithmetic in the decode kernel's writer wave,
+        the same bits as ``append`` then ``decode_attn``).  With check_numerics, NaN / Inf in
+        a quantized side raise ValueError afterwards and the cache does not advance."""
         if k.ndim != 4 or k.shape[2] != 1:
             raise ValueError(f"append_decode_attn appends one token per step, got {tuple(k.shape)}")
-        n = self._append(layer_id, k, v)
         if q.dtype != torch.float16 or q.stride(-1) != 1:
             q = q.to(torch.float16).contiguous()
         sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
-        return self._step_for(layer_id, q.shape[1]).attend(q, n, sm, inv_tau)
+        self._validate_kv(layer_id, k, v)
+        kb, vb = self._bits[layer_id]
+        if kb == 8 and vb == 8 and self.v_group_size != self.k_group_size:
+            n = self._append(layer_id, k, v)  # the decode call has one group size
+            return self._step_for(layer_id, q.shape[1]).attend(q, n, sm, inv_tau)
+        B, H = k.shape[0], k.shape[1]
+        if k.stride(-1) != 1:
+            k = k.contiguous()
+        if v.stride(-1) != 1:
+            v = v.contiguous()
+        old = self._layer_seq_lens[layer_id]
+        self._ensure(layer_id, B, H, old + 1, k.device)
+        status = self._status_buf(k.device) if self.check_numerics else None
+        pk, pv = self._params(layer_id, k, v, old, status, fp16=True)
+        out = self._step_for(layer_id, q.shape[1]).append_attend(q, old + 1, sm, inv_tau, pk, pv)
+        if status is not None:
+            st = self._read_status()
+            if st[0] & 1 or st[2] & 1:
+                raise ValueError(f"MixedKVCache append: {'K' if st[0] & 1 else 'V'} input contains "
+                                 "NaN or Inf — refusing to quantize corrupt data")
+        self._layer_seq_lens[layer_id] = old + 1
+        self._seq_len = max(self._layer_seq_lens)
+        return out
 
     def clear(self) -> None:
         self._layer_seq_lens = [0] * self.num_layers

@@ -899,8 +899,10 @@ extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   return counter_bytes(p) + rows * (kD * 4 + 8) + 256;
 }
 
-// kvq_decode_attn, and with app != nullptr kvq_append_decode_attn (tiled path only)
-static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_stream_t stream) {
+// kvq_decode_attn, and with app != nullptr kvq_append_decode_attn (tiled path only; the
+// row formats pass their two append sides in rk / rv)
+static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_stream_t stream,
+                       const AppendDev* rk = nullptr, const AppendDev* rv = nullptr) {
   if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
   if (p->head_dim != kD) return fail(KVQ_ERR_UNSUPPORTED, "head_dim must be 128");
   if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0)
@@ -1013,6 +1015,8 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   }
 
   a.app = FusedAppend{};
+  a.ark = rk ? *rk : AppendDev{};
+  a.arv = rv ? *rv : AppendDev{};
   if (app) {
     if (!tiled) return fail(KVQ_ERR_UNSUPPORTED, "the fused append needs a tiled-kernel format");
     a.app = *app;
@@ -1182,15 +1186,69 @@ static int check_fused_side(const kvq_append_params* x, const kvq_kv_view& v, in
   return KVQ_OK;
 }
 
+// One side of the row formats' fused append (per-token INT8 / INT4 scales, the KIVI family,
+// fp16 sides): the writer quantises it with the append kernel's arithmetic, into the
+// buffers the decode call reads.
+static int check_row_side(const kvq_append_params* x, const kvq_kv_view& v, int fmt,
+                          const kvq_decode_params* p, bool is_k) {
+  const std::string n(is_k ? "k_new" : "v_new");
+  if (!x) return fail(KVQ_ERR_INVALID, n + " is NULL");
+  if (x->format != fmt)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": format differs from the decode call's");
+  if (x->seq_new != 1) return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append takes one token");
+  if (x->batch != p->batch || x->heads != p->kv_heads || x->head_dim != kD ||
+      ((fmt == KVQ_FMT_INT8_SYM || fmt == KVQ_FMT_INT4_SYM) && x->group_size != p->group_size))
+    return fail(KVQ_ERR_INVALID, n + ": shape does not match the decode call");
+  if (x->write_pos < 0 || x->write_pos >= p->capacity)
+    return fail(KVQ_ERR_INVALID, n + ": write_pos outside the cache capacity");
+  if (x->codes != v.codes || x->codes_stride_b != v.stride_b || x->codes_stride_h != v.stride_h ||
+      x->codes_stride_t != v.stride_t || x->codes_layout != v.layout)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": codes must be the buffer the decode call reads");
+  if (x->rescue_quantile > 0.f && !x->rescue_all)
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": the group rescue's threshold spans every row of the "
+                                         "append (use kvq_quant_append, then kvq_decode_attn)");
+  if (x->scale_out &&
+      (x->scale_out != v.scale || x->scale_out_dtype != v.scale_dtype ||
+       x->so_stride_b != v.scale_stride_b || x->so_stride_h != v.scale_stride_h ||
+       x->so_stride_t != v.scale_stride_t ||
+       ((fmt == KVQ_FMT_INT8_SYM || fmt == KVQ_FMT_INT4_SYM) && x->so_stride_g != v.scale_stride_g)))
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": scale_out must be the scales the decode call reads");
+  if (kivi_fmt(fmt) && fmt != KVQ_FMT_FP16) {
+    const bool ok = x->static_scale ? (x->static_scale == v.scale && x->static_zp == v.zero_point)
+                                    : x->zp_out == v.zero_point;
+    if (!ok)
+      return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI parameters must be the ones the decode call reads");
+  }
+  return KVQ_OK;
+}
+
 extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
                                       const kvq_append_params* v_new, kvq_stream_t stream) {
   if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
   const int fam = tiled_family(p);
-  if (fam != kTiledA4A4 && fam != kTiledA4A4o && fam != kTiledI8A4 && fam != kTiledI8I8 &&
-      fam != kTiledI8I8g)
+  const bool spec = fam == kTiledA4A4 || fam == kTiledA4A4o || fam == kTiledI8A4 ||
+                    fam == kTiledI8I8 || fam == kTiledI8I8g;
+  if (fam == kTiledNone)
     return fail(KVQ_ERR_UNSUPPORTED,
-                "the fused append needs a tiled-kernel format: INT4_ASYM K with TILE32 V, or "
-                "static-scale INT8 K with TILE32 INT4_ASYM V or static-scale INT8 V rows");
+                "the fused append needs a tiled-kernel format: INT4_ASYM K with TILE32 V, "
+                "static-scale INT8 K with TILE32 INT4_ASYM V or static-scale INT8 V rows, "
+                "per-token INT8 / INT4 scales in dense rows (groups of 16 or more), or the "
+                "KIVI family");
+  if (!spec) {  // the row formats: the writer runs the append kernel's row quantizer
+    int rc = check_row_side(k_new, p->k, p->k_format, p, true);
+    if (rc) return rc;
+    rc = check_row_side(v_new, p->v, p->v_format, p, false);
+    if (rc) return rc;
+    if (k_new->write_pos != v_new->write_pos)
+      return fail(KVQ_ERR_INVALID, "k_new and v_new must share write_pos");
+    AppendDev dk, dv;
+    if ((rc = fill_dev(k_new, dk, "k_new"))) return rc;
+    if ((rc = fill_dev(v_new, dv, "v_new"))) return rc;
+    FusedAppend f{};
+    f.kx = reinterpret_cast<const half_t*>(k_new->x);  // marks the fused call
+    f.wpos = k_new->write_pos;
+    return decode_impl(p, &f, stream, &dk, &dv);
+  }
   int rc = check_fused_side(k_new, p->k, p->k_format, p, true);
   if (rc) return rc;
   rc = check_fused_side(v_new, p->v, p->v_format, p, false);

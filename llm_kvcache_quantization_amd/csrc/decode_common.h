@@ -1,5 +1,6 @@
 // Definitions shared by the split-K decode kernels (decode_attn.hip, decode_tiled.hip).
 #pragma once
+#include "append_row.h"
 #include "kvq_common.h"
 #include "kvq.h"
 
@@ -85,6 +86,10 @@ struct DecodeArgs {
   const half_t* res_v;
   int64_t rsb, rsh;
   int res_n;
+  // The fused append of the row formats (per-token INT8 / INT4 scales, the KIVI family, fp16
+  // sides): the writer wave quantises its (b, kv head) row of each side with the append
+  // kernel's quant_row_x (app.kx != nullptr marks the call; app.wpos is the slot)
+  AppendDev ark, arv;
 };
 
 // context length of batch row b, clamped to [0, capacity]

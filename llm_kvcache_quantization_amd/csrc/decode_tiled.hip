@@ -332,6 +332,7 @@ struct KAsymT {
   static constexpr bool kPackPV = true;
   using QInT = QIn;
   static constexpr bool kAppend = true;  // the fused quantize-on-append is built for this format
+  static constexpr bool kAppendRow = false;  // (its own specialised writer code)
   static constexpr bool kAsym = true;
   static constexpr bool kGsAny = false;  // groups of 32
   static constexpr bool kOut = OUT;
@@ -582,6 +583,7 @@ struct KI8T {
   static constexpr bool kPackPV = false;
   using QInT = QIn;
   static constexpr bool kAppend = true;
+  static constexpr bool kAppendRow = false;
   static constexpr bool kAsym = false;
   static constexpr bool kOut = false;
   static constexpr bool kSub24 = false;  // logits at unit scale
@@ -769,6 +771,7 @@ struct KiviQIn {
 struct KKiviT : KAsymT<false> {
   using QInT = KiviQIn;
   static constexpr bool kAppend = false;
+  static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
   half8v ql[4];
   __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, KiviQIn& in) const {
     const int col = lane & 15, lg = lane >> 4;
@@ -989,6 +992,7 @@ struct KKivi8T {
   static constexpr bool kPackPV = false;
   using QInT = KiviQIn;
   static constexpr bool kAppend = false;
+  static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
   static constexpr bool kAsym = false;
   static constexpr bool kGsAny = false;
   static constexpr bool kOut = false;
@@ -1089,6 +1093,7 @@ struct KF16T {
   static constexpr bool kPackPV = false;
   using QInT = QIn;
   static constexpr bool kAppend = false;
+  static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
   static constexpr bool kAsym = false;
   static constexpr bool kGsAny = false;
   static constexpr bool kOut = false;
@@ -1355,8 +1360,10 @@ struct KTokT {
   static constexpr int kMergeBatch = 16;
   static constexpr bool kPackPV = false;
   using QInT = QIn;
-  static constexpr bool kAppend = false;  // appended by kvq_quant_append (the group rescue
-                                          // spans every row of the call)
+  static constexpr bool kAppend = false;
+  // the writer runs quant_row_x (fused step) when the call has no group rescue threshold,
+  // which spans every row of the append (kvq_quant_append then appends)
+  static constexpr bool kAppendRow = true;
   static constexpr bool kAsym = false;
   static constexpr bool kGsAny = true;
   static constexpr bool kOut = false;
@@ -1689,6 +1696,15 @@ __device__ __forceinline__ void append_store(const DecodeArgs& a, const KF& kf, 
   fl.vclip += wave_sum_int(vclip);
 }
 
+// The fused append of the row formats: the writer quantises the (b, kv head) row of each
+// side of the one-token append exactly as kvq_quant_append's kernel does (quant_row_x on
+// row b * H + h), codes, per-token scales and status words included.
+__device__ __forceinline__ void append_row_pair(const DecodeArgs& a, int b, int hkv, int lane) {
+  const int row = b * a.ark.H + hkv;
+  quant_row_x(a.ark, row, lane, 0.f, load_x(a.ark, row, lane), row_static(a.ark, row, lane));
+  quant_row_x(a.arv, row, lane, 0.f, load_x(a.arv, row, lane), row_static(a.arv, row, lane));
+}
+
 __device__ __forceinline__ void append_status(const FusedAppend& f, const AppendFlags& fl) {
   if (f.kstatus) {
     if (fl.kbad) atomicOr(&f.kstatus[0], 1);
@@ -1775,7 +1791,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   // scalar loads fetches every such line (a line first touched later costs one more
   // round trip before the first cache load; measured 0.15-0.25 us per launch).
   asm volatile("" ::"s"(a.v.scale), "s"(a.ctx), "s"(a.app.kx), "s"(a.app.wpos));
-  constexpr bool APP = KF::kAppend;  // the fused append (the writer's code) is built
+  constexpr bool APP = KF::kAppend || KF::kAppendRow;  // a fused append (the writer's code) is built
   constexpr bool OUT = KF::kOut;
   int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z, n_ch = a.n_chunks;  // n_ch: the row's chunks
   int64_t share_ctx = 0;
@@ -1821,10 +1837,11 @@ void decode_tiled_kernel(DecodeArgs a) {
   vf.setup(a, b, hkv, lane);
   // the fused append's two steps (compiled only for the format that has it)
   auto app_fetch = [&]() {
-    if constexpr (APP) append_fetch<KF, VF>(a, b, hkv, lane, qin.oc, ain);
+    if constexpr (KF::kAppend) append_fetch<KF, VF>(a, b, hkv, lane, qin.oc, ain);
   };
   auto app_store = [&]() {
-    if constexpr (APP) append_store(a, kf, vf, lane, ain, (float)qin.s, (float)qin.z, afl);
+    if constexpr (KF::kAppend) append_store(a, kf, vf, lane, ain, (float)qin.s, (float)qin.z, afl);
+    else if constexpr (KF::kAppendRow) append_row_pair(a, b, hkv, lane);
   };
 
   // Tile schedule: the n_ch work-groups of a (b, kv head) interleave, so at step i the
@@ -1905,8 +1922,9 @@ void decode_tiled_kernel(DecodeArgs a) {
     if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ntot, vr[s]);
   }
   kf.finish_setup(qsh, qin, lane);
-  // (wt past the context: the wave may have fewer steps than store_step)
-  const bool store_now = late_write && (wt >= ntot || store_step <= 0);
+  // (wt past the context: the wave may have fewer steps than store_step; the row formats'
+  // writer always stores here, outside the loop)
+  const bool store_now = late_write && (KF::kAppendRow || wt >= ntot || store_step <= 0);
   if (store_now) app_store();
 
   float4v acc[8];
@@ -1923,7 +1941,8 @@ void decode_tiled_kernel(DecodeArgs a) {
       for (int u = 0; u < U; ++u) {
         // step i (i % U == u): the tiles of this wave form a prefix of its schedule
         if (tile[0] >= ntot) break;
-        if (late_write && !store_now && steps == store_step) app_store();
+        if constexpr (!KF::kAppendRow)
+          if (late_write && !store_now && steps == store_step) app_store();
         tile[LOOK + 1] = tile[LOOK] + stride;
         // fetch K of step i + LOOK + 1 (into the slot K of step i used) and V of step
         // i + LOOK (into the slot V of step i - 1 used), QK of step i + 1, then softmax

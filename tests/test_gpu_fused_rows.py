@@ -1,0 +1,217 @@
+"""GPU tests of the fused decode step of the row formats: kvq_append_decode_attn with the
+append kernel's row quantizer run by the decode kernel's writer wave.  Formats: per-token
+INT8 / INT4 scales (dynamic, adaptive, static tables, mixed rescue, rescue-all), the KIVI
+family with quantized and 16-bit sides, and the mixed cache.
+
+Twin caches take the same tokens: one through append_decode_attn (one launch), the other
+through append and then the decode kernel (two launches).  At every step, codes, scales,
+zero-points and outputs must be bit-identical.  The fused output must also be within
+max-abs 2e-3 (one fp16 ulp where |out| >= 4) and cosine 0.9999 of the oracle's attention
+over the stored cache.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import attn as OA
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+ATOL = 2e-3
+COS_MIN = 0.9999
+
+
+def _k():
+    import llm_kvcache_quantization_amd as K
+    from llm_kvcache_quantization_amd import _capi
+
+    _capi.lib()
+    return K
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def assert_close_ulp(out, ref, tag):
+    o, r = out.detach().float().cpu(), ref.detach().float().cpu()
+    assert o.shape == r.shape and torch.isfinite(o).all(), tag
+    ulp = torch.exp2(torch.floor(torch.log2(r.abs().clamp(min=2.0 ** -14))) - 10)
+    err = (o - r).abs()
+    worst = (err - torch.maximum(torch.full_like(r, ATOL), ulp)).max().item()
+    cos = torch.nn.functional.cosine_similarity(o.flatten(), r.flatten(), dim=0).item()
+    print(f"[{tag}] max_abs={err.max().item():.3e} excess={worst:.3e} cos={cos:.7f}", flush=True)
+    assert worst <= 0 and cos >= COS_MIN, (tag, worst, cos)
+
+
+def _kv(B, H, S, g):
+    k = torch.randn(B, H, S, 128, generator=g) * 1.5
+    k[..., 3] *= 15.0
+    k[..., 90] = k[..., 90] * 8.0 + 4.0
+    v = torch.randn(B, H, S, 128, generator=g) * (torch.rand(B, H, S, 1, generator=g) * 3 + 0.2)
+    v = v + torch.randn(B, H, S, 1, generator=g)
+    return k.to(torch.float16), v.to(torch.float16)
+
+
+def _equal(a, b, tag):
+    for i, (x, y) in enumerate(zip(a, b)):
+        if x is None or y is None:
+            assert x is None and y is None, (tag, i)
+            continue
+        assert torch.equal(x, y), f"{tag}: tensor {i} differs"
+
+
+SYM = [
+    # kind, engine arguments, B, H, Hq, S0, steps
+    ("int8", dict(group_size=16), 2, 2, 12, 4095, 3),          # dynamic per-token, group 16
+    ("int8", dict(group_size=128), 3, 2, 12, 0, 2),            # empty start: the token is the context
+    ("int8", dict(group_size=32, clip_percentile=100.0), 2, 4, 28, 40, 2),
+    ("int8", dict(group_size=32, static=True, adaptive_static_scales=True,
+                  adaptive_static_margin=0.9), 2, 2, 12, 300, 2),
+    ("int8", dict(group_size=16, static="k"), 2, 2, 12, 100, 2),  # static K table, per-token V
+    ("int4", dict(group_size=32), 2, 4, 28, 700, 2),           # int4_baseline
+    ("int4", dict(group_size=16, static=True), 2, 2, 12, 33, 2),
+    ("int4", dict(group_size=32, static=True, outlier_rescue_ratio=1.0), 2, 2, 12, 64, 2),
+    ("int4", dict(group_size=32, static=True, mixed_rescue=True), 2, 2, 12, 64, 2),
+]
+
+
+@pytest.mark.parametrize("kind,kw,B,H,Hq,S0,steps", SYM)
+def test_fused_rows_symmetric(kind, kw, B, H, Hq, S0, steps):
+    K = _k()
+    print(f"[case] {kind} {kw} B{B} H{H} S0={S0}", flush=True)
+    kw = dict(kw)
+    g = gen(40 + S0 + B + len(kw))
+    G = 128 // kw["group_size"]
+    static = kw.pop("static", False)
+    if static:
+        st = torch.rand(1, H, G, generator=g) * 0.3 + 0.1
+        kw["static_k_scale"] = st
+        if static is True:
+            kw["static_v_scale"] = st * 0.8
+    cls = K.INT8KVCache if kind == "int8" else K.INT4KVCache
+    mk = lambda: cls(1, device=DEV, check_numerics=False, **kw)
+    one, two = mk(), mk()
+    assert one._fused_step_ok(128), "the case must take the fused step"
+    two._fused_step_ok = lambda D: False  # append, then the decode kernel
+    k, v = _kv(B, H, S0 + steps, g)
+    if S0:
+        for c in (one, two):
+            c.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
+    sm = 1 / math.sqrt(128)
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    get = (lambda c: c.get_int8_tensors(0)) if kind == "int8" else (lambda c: c.get_int4_tensors(0))
+    for i in range(steps):
+        kn, vn = k[:, :, S0 + i:S0 + i + 1].to(DEV), v[:, :, S0 + i:S0 + i + 1].to(DEV)
+        q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+        out1 = one.append_decode_attn(0, q.to(DEV), kn, vn, sm_scale=sm, inv_tau=tau.to(DEV))
+        out2 = two.append_decode_attn(0, q.to(DEV), kn, vn, sm_scale=sm, inv_tau=tau.to(DEV))
+        torch.cuda.synchronize()
+        t1, t2 = get(one), get(two)
+        _equal(t1, t2, f"{kind} step {i}")
+        assert torch.equal(out1, out2), f"{kind} step {i}: fused output differs from two launches"
+        kc, vc, ks, vs = [t.cpu() for t in t1]
+        n = S0 + i + 1
+        cl = torch.full((B,), n, dtype=torch.int32)
+        qq = OA.prescale_q(q, tau)
+        # the reference's decode step casts the engines' scales to fp16 before either kernel
+        # (src/engine/patch_model.py:910-917, 926-933, 944-948)
+        if kind == "int8":
+            ref = OA.decode_attn_int8_torch_ref(qq, kc, vc, ks.half(), vs.half(), cl, sm)
+        else:
+            ref = OA.decode_attn_int4_torch_ref(qq, kc, vc, ks.half(), vs.half(), cl, sm)
+        assert_close_ulp(out1, ref, f"{kind} {n}")
+
+
+KIVI = [
+    # engine, arguments, B, H, Hq, S0, steps
+    ("kivi", dict(quant_bits=4), 2, 2, 12, 300, 3),
+    ("kivi", dict(quant_bits=8, k_percentile=99.0, v_percentile=99.0), 2, 4, 28, 4095, 2),
+    ("kivi", dict(quant_bits=4, v_percentile=99.9), 3, 2, 10, 31, 2),
+    ("alloc", dict(per_layer_bits=[(4, 16)]), 2, 2, 12, 100, 2),
+    ("alloc", dict(per_layer_bits=[(16, 8)]), 2, 2, 12, 100, 2),
+    ("alloc", dict(per_layer_bits=[(16, 16)]), 2, 2, 12, 64, 2),
+    ("alloc", dict(per_layer_bits=[(8, 4)], v_percentile=99.5), 2, 2, 12, 64, 2),
+]
+
+
+@pytest.mark.parametrize("eng,kw,B,H,Hq,S0,steps", KIVI)
+def test_fused_rows_kivi_family(eng, kw, B, H, Hq, S0, steps):
+    K = _k()
+    print(f"[case] {eng} {kw} B{B} H{H} S0={S0}", flush=True)
+    g = gen(70 + S0 + B)
+    if eng == "kivi":
+        mk = lambda: K.KIVIStyleKVCache(1, device=DEV, **kw)
+        kb = vb = kw["quant_bits"]
+    else:
+        mk = lambda: K.RoleAwareAllocatorKVCache(1, device=DEV, **kw)
+        kb, vb = kw["per_layer_bits"][0]
+    one, two = mk(), mk()
+    k, v = _kv(B, H, S0 + steps, g)
+    for c in (one, two):
+        c.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
+    sm = 1 / math.sqrt(128)
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    for i in range(steps):
+        kn, vn = k[:, :, S0 + i:S0 + i + 1].to(DEV), v[:, :, S0 + i:S0 + i + 1].to(DEV)
+        q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+        out1 = one.append_decode_attn(0, q.to(DEV), kn, vn, sm_scale=sm, inv_tau=tau.to(DEV))
+        two.append(0, kn, vn)
+        out2 = two._attend(0, q.to(DEV), sm, tau.to(DEV))
+        torch.cuda.synchronize()
+        t1 = one.get_kivi_tensors(0)
+        _equal(t1, two.get_kivi_tensors(0), f"{eng} step {i}")
+        assert torch.equal(out1, out2), f"{eng} step {i}: fused output differs from two launches"
+        kc, vc, ks, kz, vs, vz = [None if t is None else t.cpu() for t in t1]
+        n = S0 + i + 1
+        ref = OA.decode_attn_kivi_family_ref(q, kc, kb, ks, kz, vc, vb, vs, vz, torch.full((B,), n), sm,
+                                             inv_tau=tau)
+        assert_close_ulp(out1, ref, f"{eng} ({kb},{vb}) {n}")
+
+
+@pytest.mark.parametrize("kb,vb,gs", [(8, 4, 128), (8, 4, 16), (8, 8, 32), (8, 16, 64), (16, 4, 128),
+                                      (16, 16, 128)])
+def test_fused_rows_mixed(kb, vb, gs):
+    K = _k()
+    print(f"[case] mixed ({kb},{vb}) gs={gs}", flush=True)
+    g = gen(90 + kb + vb + gs)
+    B, H, Hq, S0, steps = 2, 2, 10, 95, 3
+    mk = lambda: K.MixedKVCache(1, device=DEV, k_group_size=gs, k_bits=kb, v_bits=vb, v_percentile=99.9)
+    one, two = mk(), mk()
+    k, v = _kv(B, H, S0 + steps, g)
+    for c in (one, two):
+        c.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
+    sm = 1 / math.sqrt(128)
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    for i in range(steps):
+        kn, vn = k[:, :, S0 + i:S0 + i + 1].to(DEV), v[:, :, S0 + i:S0 + i + 1].to(DEV)
+        q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+        out1 = one.append_decode_attn(0, q.to(DEV), kn, vn, sm_scale=sm, inv_tau=tau.to(DEV))
+        n = two._append(0, kn, vn)
+        out2 = two._step_for(0, Hq).attend(q.to(DEV), n, sm, tau.to(DEV))
+        torch.cuda.synchronize()
+        t1 = one.get_mixed_tensors(0)
+        _equal(t1, two.get_mixed_tensors(0), f"mixed step {i}")
+        assert torch.equal(out1, out2), f"mixed step {i}: fused output differs from two launches"
+        kc, ksc, vc, vsc, vz = [None if t is None else t.cpu() for t in t1]
+        ref = OA.decode_attn_mixed_bits_ref(q, kc, kb, ksc, vc, vb, vsc, vz, torch.full((B,), n), sm,
+                                            inv_tau=tau)
+        assert_close_ulp(out1, ref, f"mixed ({kb},{vb}) {n}")
+
+
+def test_fused_rows_rejects_group_rescue():
+    """The group rescue's threshold spans every row of the append, so its decode step keeps
+    two launches (the engine does not take the fused step, and the entry point refuses)."""
+    K = _k()
+    st = torch.rand(1, 2, 4) * 0.3 + 0.1
+    c = K.INT4KVCache(1, device=DEV, group_size=32, static_k_scale=st, static_v_scale=st,
+                      outlier_rescue_ratio=0.01, check_numerics=False)
+    assert not c._fused_step_ok(128)
+    g = gen(5)
+    k, v = _kv(2, 2, 9, g)
+    c.append(0, k[:, :, :8].to(DEV), v[:, :, :8].to(DEV))
+    q = torch.randn(2, 12, 128, generator=g).to(torch.float16).to(DEV)
+    c._fused_step_ok = lambda D: True
+    with pytest.raises(NotImplementedError, match="group rescue"):
+        c.append_decode_attn(0, q, k[:, :, 8:].to(DEV), v[:, :, 8:].to(DEV))
