@@ -66,7 +66,7 @@ __device__ __forceinline__ float group_absmax(float v, int gs) {
 // (row, group) of the append (int4_cache.py:344-358), one wave per row, grid-stride.
 template <class F>
 __device__ __forceinline__ void for_each_dyn(const AppendDev& a, F f) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rows = a.B * a.H * a.S;
   for (int row = blockIdx.x * kAppendWaves + wave; row < rows; row += gridDim.x * kAppendWaves) {
     const int s_idx = row % a.S, bh = row / a.S, h = bh % a.H, b = bh / a.H;
@@ -230,9 +230,8 @@ __device__ float lds_top_quantile(const float* v, int n, int lo, int hi, float w
 }
 
 // lds_top_quantile by one wave alone, without barriers: lane l holds the scales v[l + 64 r]
-// (r < R, n <= 64 R) in registers, and the maximum and multiplicity of each step are DPP
-// wave reductions (the count summed as an exact small float).  Every lane returns the
-// result.
+// (r < R, n <= 64 R) in registers; the maximum of each step is a DPP wave reduction and its
+// multiplicity the population count of one ballot per slot.  Every lane returns the result.
 template <int R>
 __device__ float wave_top_quantile(const float* v, int n, int lo, int hi, float w, int lane) {
   float x[R];
@@ -246,10 +245,9 @@ __device__ float wave_top_quantile(const float* v, int n, int lo, int hi, float 
     for (int r = 0; r < R; ++r)
       if (x[r] < t) m = fmaxf(m, x[r]);
     m = wave_max64(m);
-    float cf = 0.f;
+    int c = 0;  // the multiplicity: a ballot per slot, counted on the scalar unit
 #pragma unroll
-    for (int r = 0; r < R; ++r) cf += x[r] == m ? 1.f : 0.f;
-    const int c = (int)wave_sum64(cf);
+    for (int r = 0; r < R; ++r) c += __builtin_popcountll(__ballot(x[r] == m));
     const int r0 = n - above - c, r1 = n - above;
     if (lo >= r0 && lo < r1) vlo = m;
     if (hi >= r0 && hi < r1) vhi = m;
@@ -272,7 +270,9 @@ __device__ float sorted_quantile(const float* v, int n, float q) {
 // quantizes every row, 2 every work-group finds it (rank counting) and quantizes its own rows
 __device__ __forceinline__ void append_side(const AppendDev& a, int rescue) {
   if (!a.valid) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index is uniform: the row index arithmetic (divisions by H and S) runs on the
+  // scalar unit, not as vector integer division in every lane
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rows = a.B * a.H * a.S;
   float thr = a.thr_ptr ? *a.thr_ptr : 0.f;
   __shared__ float dyn[kRescueMax];
