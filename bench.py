@@ -491,7 +491,7 @@ def modes_leg(cfg, mode, device, steps, warmup):
         for tok, s in ((cache._k_tok[0], kst), (cache._v_tok[0], vst)):
             if tok:
                 per_tok += s.shape[-1] * s.element_size()
-        fused = cache._fused_step_ok(128)
+        fused = cache._fused_step_ok(128, cfg.batch, cfg.kv_heads)
         tok_scales = [bool(cache._k_tok[0]), bool(cache._v_tok[0])]
     nbytes = (cfg.batch * cfg.kv_heads * (n_mid * per_tok + per_bh) +
               2 * cfg.batch * cfg.q_heads * 128 * 2)

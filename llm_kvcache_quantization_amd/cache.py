@@ -422,9 +422,9 @@ class _SymCacheBase(_EngineBase):
 
     # -- decode step: the append + attention of src/engine/patch_model.py:755-957
 
-    def _fused_step_ok(self, D: int) -> bool:
-        """The format the tiled kernel appends and attends in one launch (static INT8
-        scales on both sides, any group size, no adaptive policy)."""
+    def _fused_step_ok(self, D: int, B: Optional[int] = None, H: Optional[int] = None) -> bool:
+        """Whether the tiled kernel appends and attends in one launch for this engine's
+        format (B, H: the step's batch and KV heads, where the answer depends on them)."""
         return False
 
     def _step_for(self, layer_id: int, q_heads: int):
@@ -505,7 +505,7 @@ class _SymCacheBase(_EngineBase):
         # the append's parameter blocks are kept per layer (as ``append`` would build them)
         pk, pv = self._fused_apps(layer_id, k, v, old, status)
         step = self._step_for(layer_id, q.shape[1])
-        if self._fused_step_ok(D):
+        if self._fused_step_ok(D, B, H):
             out = step.append_attend(q, n, sm_scale, inv_tau, pk, pv)
             if status is not None:
                 self._check_status(layer_id, k.numel(), self._kind, self._qrange)
@@ -625,7 +625,7 @@ class INT8KVCache(_SymCacheBase):
         """(k_int8, v_int8, k_scale, v_scale) views [B, H, S, D] / [B, H, S, G] (fp16 scales)."""
         return self._raw_views(layer_id)
 
-    def _fused_step_ok(self, D: int) -> bool:
+    def _fused_step_ok(self, D: int, B: Optional[int] = None, H: Optional[int] = None) -> bool:
         # static tables on both sides (any group size), or per-token scales in groups of 16 or
         # more (the tiled kernel's row formats; its writer runs the append's arithmetic)
         if D != 128 or self.group_size not in (8, 16, 32, 64, 128):
@@ -711,13 +711,25 @@ class INT4KVCache(_SymCacheBase):
     def _effective_static(self, s):
         return s.to(torch.float32).clamp(min=1e-5)
 
-    def _fused_step_ok(self, D: int) -> bool:
-        # the tiled kernel's row format (groups of 16 or more) appends in the same launch
-        # unless the group rescue needs its threshold over every row of the append
-        # (int4_cache.py:384-390), which a launch computes before quantizing any row
+    def _fused_step_ok(self, D: int, B: Optional[int] = None, H: Optional[int] = None) -> bool:
+        # the tiled kernel's row format (groups of 16 or more) appends in the same launch; the
+        # group rescue's threshold (torch.quantile over every (row, group) scale of the append,
+        # int4_cache.py:384-390) is found by the decode kernel's writer wave when it lies within
+        # its walk from the top: at most 32 rows (B * H), lower rank within 32 of the top
+        if D != 128 or self.group_size < 16:
+            return False
         rescue = 0.0 < self.outlier_rescue_ratio < 1.0 and (
             self.static_k_scale is not None or self.static_v_scale is not None)
-        return D == 128 and self.group_size >= 16 and not rescue
+        if not rescue:
+            return True
+        if B is None or H is None:
+            return False
+        import numpy as np
+
+        n = B * H * (D // self.group_size)
+        q = np.float32(max(0.0, min(1.0, 1.0 - self.outlier_rescue_ratio)))
+        lo = int(np.floor(q * np.float32(n - 1)))
+        return B * H <= 32 and n - 1 - lo < 32
 
     def _policy(self, p, side):
         adaptive = self.adaptive_static_scales and (

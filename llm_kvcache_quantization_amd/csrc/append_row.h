@@ -16,6 +16,14 @@ namespace kvq {
 
 int fail(int code, const std::string& msg);
 
+// The INT4 group rescue's threshold (torch.quantile over every (row, group) dynamic scale of
+// the append): up to kRescueRank scales it is found inside the launch that quantizes (the
+// append kernel's work-groups, or the fused decode step's writer wave), walking down from the
+// maximum when its ranks lie within kTopWalk of the top; rows are loaded kRowBatch at a time.
+constexpr int kRescueRank = 1024;
+constexpr int kRowBatch = 8;
+constexpr int kTopWalk = 32;
+
 struct AppendDev {
   int valid;
   int fmt;
@@ -334,6 +342,118 @@ __device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lan
   // clipped-element count (int8_cache.py:407-419, int4_cache.py:468-485)
   for (int o = 32; o > 0; o >>= 1) clipped += __shfl_xor(clipped, o, 64);
   if (lane == 0 && a.status && clipped) atomicAdd(&a.status[1], clipped);
+}
+
+// group_max for values >= +0 (absolute values: the order of the maxima cannot change a bit)
+// with DPP instead of the LDS crossbar: xor 1 and 2 within the quad, then the half-row and
+// row mirrors (lane i with 7 - i, 15 - i), which pair lanes of the two already reduced halves
+__device__ __forceinline__ float group_absmax(float v, int gs) {
+#pragma clang fp contract(off)
+  v = fmaxf(v, dppf<0xB1>(v));                       // quad_perm [1, 0, 3, 2]
+  if (gs >= 8) v = fmaxf(v, dppf<0x4E>(v));          // quad_perm [2, 3, 0, 1]
+  if (gs >= 16) v = fmaxf(v, dppf<0x141>(v));        // row_half_mirror
+  if (gs >= 32) v = fmaxf(v, dppf<0x140>(v));        // row_mirror
+  if (gs >= 64) v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if (gs >= 128) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+// lds_top_quantile by one wave alone, without barriers: lane l holds the scales v[l + 64 r]
+// (r < R, n <= 64 R) in registers; the maximum of each step is a DPP wave reduction and its
+// multiplicity the population count of one ballot per slot.  Every lane returns the result.
+template <int R>
+__device__ __forceinline__ float wave_top_quantile(const float* v, int n, int lo, int hi, float w, int lane) {
+#pragma clang fp contract(off)
+  float x[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) x[r] = lane + 64 * r < n ? v[lane + 64 * r] : -1.0f;  // below every scale
+  float t = __builtin_inff(), vlo = 0.f, vhi = 0.f;
+  int above = 0;
+  for (int it = 0; it < kTopWalk && above <= n - 1 - lo; ++it) {
+    float m = -1.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (x[r] < t) m = fmaxf(m, x[r]);
+    m = wave_max64(m);
+    int c = 0;  // the multiplicity: a ballot per slot, counted on the scalar unit
+#pragma unroll
+    for (int r = 0; r < R; ++r) c += __builtin_popcountll(__ballot(x[r] == m));
+    const int r0 = n - above - c, r1 = n - above;
+    if (lo >= r0 && lo < r1) vlo = m;
+    if (hi >= r0 && hi < r1) vhi = m;
+    above += c;
+    t = m;
+  }
+  return quantile_lerp(vlo, vhi, w);
+}
+
+// The rank of torch.quantile's lower order statistic for level q over n values, and whether
+// the walk from the top reaches it (host and device compute the same fp32 rank).
+__host__ __device__ inline bool rescue_walk_ok(float q, int n) {
+#pragma clang fp contract(off)
+  if (n <= 0 || n > kRescueRank) return false;
+  const float rank = q * (float)(n - 1);
+  const int lo = (int)floorf(rank);
+  return n - 1 - lo < kTopWalk;
+}
+
+// The group-rescue threshold of a one-token append side found by one wave alone (the fused
+// decode step's writer), over at most kRescueRows rows (rows = B * H) in groups of 16 or more.
+// rescue_fetch issues the rows' loads early (lane l: the 32 dwords of channels
+// 64 (l % 2) .. + 63 of row l / 2); rescue_thr_rows then takes each lane's group maxima (a
+// group of 128 with its partner lane), writes the scales fmax(absmax, 1e-5) / 7 to dyn (LDS;
+// one wave, whose own writes its reads see in order) and walks from the top.  Needs
+// rescue_walk_ok(a.rq, rows * 128 / gs).
+constexpr int kRescueRows = 32;
+struct RescueRows {
+  uint32_t w[32];
+};
+__device__ __forceinline__ void rescue_fetch(const AppendDev& a, int lane, RescueRows& x) {
+  const int rows = a.B * a.H * a.S, r = lane >> 1;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(row_x(a, r < rows ? r : 0)) + 32 * (lane & 1);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) x.w[i] = p[i];
+}
+__device__ __forceinline__ float rescue_thr_rows(const AppendDev& a, int lane, const RescueRows& x,
+                                                 float* dyn) {
+#pragma clang fp contract(off)
+  const int rows = a.B * a.H * a.S, gs = a.gs, G = 128 / gs, n = rows * G;
+  const int r = lane >> 1, hh = lane & 1;
+  float m16[4];  // the maxima of |x| over the lane's four runs of 16 channels
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const half2v h = as_h2(x.w[8 * k + i]);
+      m = fmaxf(m, fmaxf(fabsf((float)h.x), fabsf((float)h.y)));
+    }
+    m16[k] = m;
+  }
+  float mm[4] = {m16[0], m16[1], m16[2], m16[3]};
+  int ng = 4;  // the lane's groups
+  if (gs == 32) {
+    mm[0] = fmaxf(m16[0], m16[1]);
+    mm[1] = fmaxf(m16[2], m16[3]);
+    ng = 2;
+  } else if (gs >= 64) {
+    mm[0] = fmaxf(fmaxf(m16[0], m16[1]), fmaxf(m16[2], m16[3]));
+    ng = 1;
+    if (gs == 128) {
+      mm[0] = fmaxf(mm[0], dppf<0xB1>(mm[0]));  // with the partner lane's half
+      ng = hh == 0 ? 1 : 0;
+    }
+  }
+  if (r < rows)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < ng) dyn[r * G + hh * ng + k] = __fdiv_rn(fmaxf(mm[k], 1e-5f), 7.0f);
+  const float rank = a.rq * (float)(n - 1);
+  const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
+  const float w = rank - (float)lo;
+  return n <= 64    ? wave_top_quantile<1>(dyn, n, lo, hi, w, lane)
+         : n <= 128 ? wave_top_quantile<2>(dyn, n, lo, hi, w, lane)
+                    : wave_top_quantile<4>(dyn, n, lo, hi, w, lane);
 }
 
 // The device description of one side of an append call (validated)

@@ -1204,9 +1204,16 @@ static int check_row_side(const kvq_append_params* x, const kvq_kv_view& v, int 
   if (x->codes != v.codes || x->codes_stride_b != v.stride_b || x->codes_stride_h != v.stride_h ||
       x->codes_stride_t != v.stride_t || x->codes_layout != v.layout)
     return fail(KVQ_ERR_UNSUPPORTED, n + ": codes must be the buffer the decode call reads");
-  if (x->rescue_quantile > 0.f && !x->rescue_all)
-    return fail(KVQ_ERR_UNSUPPORTED, n + ": the group rescue's threshold spans every row of the "
-                                         "append (use kvq_quant_append, then kvq_decode_attn)");
+  // the group rescue's threshold spans every row of the append: the writer wave finds it
+  // itself from at most kRescueRows new rows when the walk from the top reaches it
+  if (x->rescue_quantile > 0.f && !x->rescue_all && x->static_scale && fmt == KVQ_FMT_INT4_SYM &&
+      (x->batch * x->heads > kRescueRows ||
+       !rescue_walk_ok(x->rescue_quantile,
+                       x->group_size > 0 ? x->batch * x->heads * (kD / x->group_size) : 0)))
+    return fail(KVQ_ERR_UNSUPPORTED, n + ": the group rescue's threshold is beyond the writer "
+                                         "wave (more than 32 rows, or ranks far from the top of "
+                                         "the append's scales): use kvq_quant_append, then "
+                                         "kvq_decode_attn");
   if (x->scale_out &&
       (x->scale_out != v.scale || x->scale_out_dtype != v.scale_dtype ||
        x->so_stride_b != v.scale_stride_b || x->so_stride_h != v.scale_stride_h ||

@@ -772,6 +772,7 @@ struct KKiviT : KAsymT<false> {
   using QInT = KiviQIn;
   static constexpr bool kAppend = false;
   static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
+  static constexpr bool kRescue = false;     // (no INT4_SYM side)
   half8v ql[4];
   __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, KiviQIn& in) const {
     const int col = lane & 15, lg = lane >> 4;
@@ -993,6 +994,7 @@ struct KKivi8T {
   using QInT = KiviQIn;
   static constexpr bool kAppend = false;
   static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
+  static constexpr bool kRescue = false;     // (no INT4_SYM side)
   static constexpr bool kAsym = false;
   static constexpr bool kGsAny = false;
   static constexpr bool kOut = false;
@@ -1094,6 +1096,7 @@ struct KF16T {
   using QInT = QIn;
   static constexpr bool kAppend = false;
   static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
+  static constexpr bool kRescue = false;     // (no INT4_SYM side)
   static constexpr bool kAsym = false;
   static constexpr bool kGsAny = false;
   static constexpr bool kOut = false;
@@ -1361,9 +1364,10 @@ struct KTokT {
   static constexpr bool kPackPV = false;
   using QInT = QIn;
   static constexpr bool kAppend = false;
-  // the writer runs quant_row_x (fused step) when the call has no group rescue threshold,
-  // which spans every row of the append (kvq_quant_append then appends)
+  // the writer runs quant_row_x (fused step); with INT4_SYM sides it also finds the group
+  // rescue's threshold over every row of the append (rescue_thr_wave)
   static constexpr bool kAppendRow = true;
+  static constexpr bool kRescue = I4;
   static constexpr bool kAsym = false;
   static constexpr bool kGsAny = true;
   static constexpr bool kOut = false;
@@ -1698,11 +1702,43 @@ __device__ __forceinline__ void append_store(const DecodeArgs& a, const KF& kf, 
 
 // The fused append of the row formats: the writer quantises the (b, kv head) row of each
 // side of the one-token append exactly as kvq_quant_append's kernel does (quant_row_x on
-// row b * H + h), codes, per-token scales and status words included.
-__device__ __forceinline__ void append_row_pair(const DecodeArgs& a, int b, int hkv, int lane) {
+// row b * H + h), codes, per-token scales and status words included.  An INT4 side with the
+// group rescue first finds its threshold over every row of the append on its own
+// (rescue_thr_wave: the host admits only thresholds within the walk's reach of the top).
+__device__ __forceinline__ bool rescue_side(const AppendDev& d) {
+  return d.fmt == KVQ_FMT_INT4_SYM && d.st != nullptr && d.rq > 0.f && !d.rescue_all;
+}
+// The writer's inputs, requested at the start of the kernel (under the streaming that
+// follows, a load issued at the store would wait a loaded round trip): its own new rows and
+// their static scales, and with the group rescue every new row of the append.
+struct RowPre {
+  half2v k, v;
+  float sk, sv;
+};
+__device__ __forceinline__ void append_row_fetch(const DecodeArgs& a, int b, int hkv, int lane,
+                                                 RowPre& p) {
   const int row = b * a.ark.H + hkv;
-  quant_row_x(a.ark, row, lane, 0.f, load_x(a.ark, row, lane), row_static(a.ark, row, lane));
-  quant_row_x(a.arv, row, lane, 0.f, load_x(a.arv, row, lane), row_static(a.arv, row, lane));
+  p.k = load_x(a.ark, row, lane);
+  p.sk = row_static(a.ark, row, lane);
+  p.v = load_x(a.arv, row, lane);
+  p.sv = row_static(a.arv, row, lane);
+}
+// (the rescue is compiled only where it can occur: INT4_SYM K and V, RESCUE)
+template <bool RESCUE>
+__device__ __forceinline__ void append_row_pair(const DecodeArgs& a, int b, int hkv, int lane,
+                                                const RowPre& p, const RescueRows& rk,
+                                                const RescueRows& rv) {
+  const int row = b * a.ark.H + hkv;
+  float tk = 0.f, tv = 0.f;
+  if constexpr (RESCUE) {
+    __shared__ float rdyn[kRescueRows * 8];  // the writer's scales (one writer per work-group)
+    if (rescue_side(a.ark)) tk = rescue_thr_rows(a.ark, lane, rk, rdyn);
+    quant_row_x(a.ark, row, lane, tk, p.k, p.sk);
+    if (rescue_side(a.arv)) tv = rescue_thr_rows(a.arv, lane, rv, rdyn);
+  } else {
+    quant_row_x(a.ark, row, lane, tk, p.k, p.sk);
+  }
+  quant_row_x(a.arv, row, lane, tv, p.v, p.sv);
 }
 
 __device__ __forceinline__ void append_status(const FusedAppend& f, const AppendFlags& fl) {
@@ -1819,6 +1855,8 @@ void decode_tiled_kernel(DecodeArgs a) {
   const bool writer = app_on && chunk * kTW + wave == wt % stride_all;
   AppendIn ain;
   AppendFlags afl;
+  [[maybe_unused]] RowPre rpre;
+  [[maybe_unused]] RescueRows rxk, rxv;
 
   __shared__ QShareLds qsh;
   __shared__ TiledMergeLds msh;
@@ -1832,6 +1870,16 @@ void decode_tiled_kernel(DecodeArgs a) {
   // cache tiles requested next
   typename KF::QInT qin;
   kf.fetch_q(a, b, hkv, lane, wave, qin);
+  if constexpr (KF::kAppendRow) {
+    if (writer) {
+      append_row_fetch(a, b, hkv, lane, rpre);
+      if constexpr (KF::kRescue)
+        if (rescue_side(a.ark) || rescue_side(a.arv)) {
+          rescue_fetch(a.ark, lane, rxk);
+          rescue_fetch(a.arv, lane, rxv);
+        }
+    }
+  }
   kf.setup_addr(a, b, hkv, lane);
   VF vf;
   vf.setup(a, b, hkv, lane);
@@ -1841,7 +1889,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   };
   auto app_store = [&]() {
     if constexpr (KF::kAppend) append_store(a, kf, vf, lane, ain, (float)qin.s, (float)qin.z, afl);
-    else if constexpr (KF::kAppendRow) append_row_pair(a, b, hkv, lane);
+    else if constexpr (KF::kAppendRow) append_row_pair<KF::kRescue>(a, b, hkv, lane, rpre, rxk, rxv);
   };
 
   // Tile schedule: the n_ch work-groups of a (b, kv head) interleave, so at step i the

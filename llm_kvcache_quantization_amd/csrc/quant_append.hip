@@ -33,11 +33,6 @@ int fail(int code, const std::string& msg);
 
 constexpr int kAppendWaves = 4;
 constexpr int kRescueMax = 4096;  // (rows x groups) handled by the single-work-group rescue path
-constexpr int kRescueRank = 1024;  // (rows x groups) up to which every work-group finds the
-                                   // threshold itself by rank counting (decode-sized appends)
-constexpr int kRowBatch = 8;      // rows per wave loaded at once on that path
-constexpr int kTopWalk = 32;      // that path walks down from the maximum when the quantile's
-                                  // ranks lie within kTopWalk of the top; else it sorts
 
 struct RescueScratch {
   uint32_t hist[256];
@@ -48,19 +43,6 @@ struct RescueScratch {
   float thr;
   uint32_t pad[3];
 };
-
-// group_max for values >= +0 (absolute values: the order of the maxima cannot change a bit)
-// with DPP instead of the LDS crossbar: xor 1 and 2 within the quad, then the half-row and
-// row mirrors (lane i with 7 - i, 15 - i), which pair lanes of the two already reduced halves
-__device__ __forceinline__ float group_absmax(float v, int gs) {
-  v = fmaxf(v, dppf<0xB1>(v));                       // quad_perm [1, 0, 3, 2]
-  if (gs >= 8) v = fmaxf(v, dppf<0x4E>(v));          // quad_perm [2, 3, 0, 1]
-  if (gs >= 16) v = fmaxf(v, dppf<0x141>(v));        // row_half_mirror
-  if (gs >= 32) v = fmaxf(v, dppf<0x140>(v));        // row_mirror
-  if (gs >= 64) v = fmaxf(v, __shfl_xor(v, 16, 64));
-  if (gs >= 128) v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
-}
 
 // Calls f(bits) for the fp32 bit pattern of the dynamic scale fmax(absmax, 1e-5) / 7 of every
 // (row, group) of the append (int4_cache.py:344-358), one wave per row, grid-stride.
@@ -225,34 +207,6 @@ __device__ float lds_top_quantile(const float* v, int n, int lo, int hi, float w
     above += c;
     t = m;
     __syncthreads();  // red_m / red_c are rewritten by the next step
-  }
-  return quantile_lerp(vlo, vhi, w);
-}
-
-// lds_top_quantile by one wave alone, without barriers: lane l holds the scales v[l + 64 r]
-// (r < R, n <= 64 R) in registers; the maximum of each step is a DPP wave reduction and its
-// multiplicity the population count of one ballot per slot.  Every lane returns the result.
-template <int R>
-__device__ float wave_top_quantile(const float* v, int n, int lo, int hi, float w, int lane) {
-  float x[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) x[r] = lane + 64 * r < n ? v[lane + 64 * r] : -1.0f;  // below every scale
-  float t = __builtin_inff(), vlo = 0.f, vhi = 0.f;
-  int above = 0;
-  for (int it = 0; it < kTopWalk && above <= n - 1 - lo; ++it) {
-    float m = -1.0f;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (x[r] < t) m = fmaxf(m, x[r]);
-    m = wave_max64(m);
-    int c = 0;  // the multiplicity: a ballot per slot, counted on the scalar unit
-#pragma unroll
-    for (int r = 0; r < R; ++r) c += __builtin_popcountll(__ballot(x[r] == m));
-    const int r0 = n - above - c, r1 = n - above;
-    if (lo >= r0 && lo < r1) vlo = m;
-    if (hi >= r0 && hi < r1) vhi = m;
-    above += c;
-    t = m;
   }
   return quantile_lerp(vlo, vhi, w);
 }

@@ -74,6 +74,13 @@ SYM = [
     ("int4", dict(group_size=16, static=True), 2, 2, 12, 33, 2),
     ("int4", dict(group_size=32, static=True, outlier_rescue_ratio=1.0), 2, 2, 12, 64, 2),
     ("int4", dict(group_size=32, static=True, mixed_rescue=True), 2, 2, 12, 64, 2),
+    # the group rescue (int4_fused / int4_ours): the writer finds the threshold over every row
+    ("int4", dict(group_size=16, static=True, outlier_rescue_ratio=0.01), 8, 4, 28, 300, 2),  # 256 scales
+    ("int4", dict(group_size=32, static=True, outlier_rescue_ratio=0.01), 4, 2, 12, 40, 2),   # 32 scales
+    ("int4", dict(group_size=16, static=True, outlier_rescue_ratio=0.02), 8, 4, 28, 33, 2),  # 5 below the top
+    ("int4", dict(group_size=64, static=True, outlier_rescue_ratio=0.05), 4, 8, 32, 50, 2),   # 64 scales
+    ("int4", dict(group_size=128, static=True, outlier_rescue_ratio=0.1), 3, 5, 15, 20, 2),   # 15 rows
+    ("int4", dict(group_size=16, static=True, outlier_rescue_ratio=0.1, ties=True), 4, 4, 16, 70, 2),
 ]
 
 
@@ -85,6 +92,7 @@ def test_fused_rows_symmetric(kind, kw, B, H, Hq, S0, steps):
     g = gen(40 + S0 + B + len(kw))
     G = 128 // kw["group_size"]
     static = kw.pop("static", False)
+    ties = kw.pop("ties", False)
     if static:
         st = torch.rand(1, H, G, generator=g) * 0.3 + 0.1
         kw["static_k_scale"] = st
@@ -93,9 +101,11 @@ def test_fused_rows_symmetric(kind, kw, B, H, Hq, S0, steps):
     cls = K.INT8KVCache if kind == "int8" else K.INT4KVCache
     mk = lambda: cls(1, device=DEV, check_numerics=False, **kw)
     one, two = mk(), mk()
-    assert one._fused_step_ok(128), "the case must take the fused step"
-    two._fused_step_ok = lambda D: False  # append, then the decode kernel
+    assert one._fused_step_ok(128, B, H), "the case must take the fused step"
+    two._fused_step_ok = lambda *args: False  # append, then the decode kernel
     k, v = _kv(B, H, S0 + steps, g)
+    if ties:  # few distinct group maxima: equal scales at the threshold
+        k, v = (k * 2).round().div(2).half(), v.round().half()
     if S0:
         for c in (one, two):
             c.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
@@ -200,18 +210,24 @@ def test_fused_rows_mixed(kb, vb, gs):
         assert_close_ulp(out1, ref, f"mixed ({kb},{vb}) {n}")
 
 
-def test_fused_rows_rejects_group_rescue():
-    """The group rescue's threshold spans every row of the append, so its decode step keeps
-    two launches (the engine does not take the fused step, and the entry point refuses)."""
+def test_fused_rows_group_rescue_far_from_top_keeps_two_launches():
+    """A group rescue threshold far from the top of the append's scales (here the median)
+    is beyond the writer's walk: the engine keeps two launches, and the entry point refuses
+    the fused call."""
     K = _k()
     st = torch.rand(1, 2, 4) * 0.3 + 0.1
     c = K.INT4KVCache(1, device=DEV, group_size=32, static_k_scale=st, static_v_scale=st,
-                      outlier_rescue_ratio=0.01, check_numerics=False)
-    assert not c._fused_step_ok(128)
+                      outlier_rescue_ratio=0.5, check_numerics=False)
+    assert not c._fused_step_ok(128, 16, 2)  # 128 scales, lower rank 63: 64 below the top
+    c01 = K.INT4KVCache(1, device=DEV, group_size=32, static_k_scale=st, static_v_scale=st,
+                        outlier_rescue_ratio=0.01, check_numerics=False)
+    assert c01._fused_step_ok(128, 16, 2) and not c01._fused_step_ok(128, 16, 4)  # 32 rows at most
     g = gen(5)
-    k, v = _kv(2, 2, 9, g)
+    k, v = _kv(16, 2, 9, g)
     c.append(0, k[:, :, :8].to(DEV), v[:, :, :8].to(DEV))
-    q = torch.randn(2, 12, 128, generator=g).to(torch.float16).to(DEV)
-    c._fused_step_ok = lambda D: True
+    q = torch.randn(16, 12, 128, generator=g).to(torch.float16).to(DEV)
+    out = c.append_decode_attn(0, q, k[:, :, 8:].to(DEV), v[:, :, 8:].to(DEV))  # two launches
+    assert out.shape == q.shape and c.get_seq_len() == 9
+    c._fused_step_ok = lambda *args: True
     with pytest.raises(NotImplementedError, match="group rescue"):
         c.append_decode_attn(0, q, k[:, :, 8:].to(DEV), v[:, :, 8:].to(DEV))
