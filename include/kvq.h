@@ -267,11 +267,12 @@ int64_t kvq_append_scratch_bytes(const kvq_append_params* p);
  *    INT4_ASYM side must name p's static tables and outlier side-band, an INT8_SYM side
  *    quantizes with its own table (fp16 or fp32), as kvq_quant_append would;
  *  - the row formats (per-token INT8_SYM / INT4_SYM scales in dense rows with groups of 16
- *    or more, INT4_KIVI / INT8_KIVI, FP16 sides): any policy kvq_quant_append takes except
- *    the INT4_SYM group rescue with a threshold (rescue_quantile > 0 without rescue_all),
- *    which spans every row of the append; scale_out / zp_out and KIVI K's static
- *    parameters must be the buffers p reads.  The decode kernel's writer wave runs the
- *    append kernel's row arithmetic.
+ *    or more, INT4_KIVI / INT8_KIVI, FP16 sides): any policy kvq_quant_append takes; the
+ *    INT4_SYM group rescue with a threshold (rescue_quantile > 0 without rescue_all), which
+ *    spans every row of the append, only with at most 32 rows (batch * heads) and its lower
+ *    rank within 32 of the top of the (row, group) scales; scale_out / zp_out and KIVI K's
+ *    static parameters must be the buffers p reads.  The decode kernel's writer wave runs
+ *    the append kernel's row arithmetic (and finds the rescue threshold itself).
  * Anything else returns KVQ_ERR_UNSUPPORTED (or KVQ_ERR_INVALID), and the caller makes the
  * two calls instead.  The status words are updated as kvq_quant_append does. */
 int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
