@@ -902,7 +902,8 @@ extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
 // kvq_decode_attn, and with app != nullptr kvq_append_decode_attn (tiled path only; the
 // row formats pass their two append sides in rk / rv)
 static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_stream_t stream,
-                       const AppendDev* rk = nullptr, const AppendDev* rv = nullptr) {
+                       const AppendDev* rk = nullptr, const AppendDev* rv = nullptr,
+                       int fam_override = -1) {
   if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
   if (p->head_dim != kD) return fail(KVQ_ERR_UNSUPPORTED, "head_dim must be 128");
   if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0)
@@ -929,7 +930,7 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   if (fam == kNone)
     return fail(KVQ_ERR_UNSUPPORTED,
                 "unsupported (k_format, v_format) pair or mixed K/V scale dtypes");
-  const int tfam = tiled_family(p);
+  const int tfam = fam_override >= 0 ? fam_override : tiled_family(p);
   const bool tiled = tfam != kTiledNone;
   if (p->v.layout == KVQ_LAYOUT_TILE32 && !tiled)
     return fail(KVQ_ERR_UNSUPPORTED,
@@ -1232,9 +1233,23 @@ static int check_row_side(const kvq_append_params* x, const kvq_kv_view& v, int 
 extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_append_params* k_new,
                                       const kvq_append_params* v_new, kvq_stream_t stream) {
   if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
-  const int fam = tiled_family(p);
-  const bool spec = fam == kTiledA4A4 || fam == kTiledA4A4o || fam == kTiledI8A4 ||
-                    fam == kTiledI8I8 || fam == kTiledI8I8g;
+  int fam = tiled_family(p);
+  bool spec = fam == kTiledA4A4 || fam == kTiledA4A4o || fam == kTiledI8A4 ||
+              fam == kTiledI8I8 || fam == kTiledI8I8g;
+  // per-token scale views of one row and one token look static to tiled_family; an append
+  // that computes its scales (no static table, a scale policy or scale_out) takes the
+  // per-token family's writer instead
+  const auto table_append = [](const kvq_append_params* x) {
+    return x && x->static_scale && !x->adaptive && !x->mixed_rescue && x->rescue_quantile <= 0.f &&
+           !x->rescue_all && !x->scale_out;
+  };
+  if ((fam == kTiledI8I8 || fam == kTiledI8I8g) && !(table_append(k_new) && table_append(v_new))) {
+    const int tf = tok_family(p);
+    if (tf != kTiledNone) {
+      fam = tf;
+      spec = false;
+    }
+  }
   if (fam == kTiledNone)
     return fail(KVQ_ERR_UNSUPPORTED,
                 "the fused append needs a tiled-kernel format: INT4_ASYM K with TILE32 V, "
@@ -1254,7 +1269,7 @@ extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_appe
     FusedAppend f{};
     f.kx = reinterpret_cast<const half_t*>(k_new->x);  // marks the fused call
     f.wpos = k_new->write_pos;
-    return decode_impl(p, &f, stream, &dk, &dv);
+    return decode_impl(p, &f, stream, &dk, &dv, fam);
   }
   int rc = check_fused_side(k_new, p->k, p->k_format, p, true);
   if (rc) return rc;

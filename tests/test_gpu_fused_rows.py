@@ -231,3 +231,38 @@ def test_fused_rows_group_rescue_far_from_top_keeps_two_launches():
     c._fused_step_ok = lambda *args: True
     with pytest.raises(NotImplementedError, match="group rescue"):
         c.append_decode_attn(0, q, k[:, :, 8:].to(DEV), v[:, :, 8:].to(DEV))
+
+
+@pytest.mark.parametrize("eng", ["int8", "mixed88", "int4"])
+def test_fused_rows_one_row_first_token(eng):
+    """Batch 1 and an empty cache: the first decode token is the whole context, so its
+    per-token scale views have one row and one token (which look like a static table);
+    the fused step still appends with the per-token arithmetic, bit-identical to two
+    launches."""
+    K = _k()
+    g = gen(77)
+    if eng == "int8":
+        mk = lambda: K.INT8KVCache(1, device=DEV, group_size=128, check_numerics=False)
+    elif eng == "int4":
+        mk = lambda: K.INT4KVCache(1, device=DEV, group_size=32, check_numerics=False)
+    else:
+        mk = lambda: K.MixedKVCache(1, device=DEV, k_group_size=64, k_bits=8, v_bits=8, v_percentile=99.9)
+    one, two = mk(), mk()
+    k, v = _kv(1, 2, 3, g)
+    sm = 1 / math.sqrt(128)
+    for i in range(3):
+        kn, vn = k[:, :, i:i + 1].to(DEV), v[:, :, i:i + 1].to(DEV)
+        q = torch.randn(1, 10, 128, generator=g).to(torch.float16).to(DEV)
+        out1 = one.append_decode_attn(0, q, kn, vn, sm_scale=sm)
+        if eng == "mixed88":
+            n = two._append(0, kn, vn)
+            out2 = two._step_for(0, 10).attend(q, n, sm, None)
+            t1, t2 = one.get_mixed_tensors(0), two.get_mixed_tensors(0)
+        else:
+            two._fused_step_ok = lambda *args: False
+            out2 = two.append_decode_attn(0, q, kn, vn, sm_scale=sm)
+            get = (lambda c: c.get_int8_tensors(0)) if eng == "int8" else (lambda c: c.get_int4_tensors(0))
+            t1, t2 = get(one), get(two)
+        torch.cuda.synchronize()
+        _equal(t1, t2, f"{eng} step {i}")
+        assert torch.equal(out1, out2), f"{eng} step {i}"
