@@ -43,6 +43,12 @@
 //    merges the partials (no second launch; its arrival counters live in the workspace,
 //    which must be zero-filled before its first use and which every call leaves zero);
 //    otherwise combine_kernel does.
+//  * The other operand types (K: KI8T, KTokT, KKiviT, KKivi8T, KF16T; V: VI8RowT, VTokT,
+//    VKiviRowT, VKivi8RowT, VF16RowT) read the reference's token-row layouts with the same
+//    schedule, loads and merge.  Their fused append (kAppendRow) runs the append kernel's
+//    row quantizer (append_row.h) in the writer wave, whose inputs are requested with the
+//    q loads; with INT4_SYM sides (kRescue) the writer also finds the group rescue's
+//    threshold over every new row of the step.
 #include "decode_common.h"
 
 #include <cstdlib>
