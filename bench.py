@@ -652,7 +652,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the decode path is "
-                          "measured on one MI355X (see DESIGN.md for how it would shard)",
+                          "measured on one MI355X (across GPUs it would shard by KV heads "
+                          "and batch rows, each GPU running this kernel on its share)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.copy_probe:
