@@ -1,5 +1,5 @@
 // The append's row quantizer, shared by the append kernel (quant_append.hip) and the tiled
-// decode kernel's fused append (decode_tiled.hip), so that both write the same bits: one
+// decode kernel's fused append (decode_tiled.h), so that both write the same bits: one
 // wavefront quantises one (b, h, s) row of D = 128 values (2 per lane).
 //
 // Every product and sum here is rounded on its own, as torch rounds each tensor op: each

@@ -844,7 +844,7 @@ static int64_t n_chunks_for(const kvq_decode_params* p, int32_t chunk) {
 // their bits are those of the uniform split), while a ragged batch shares share_c work-
 // groups of the kv head, about one per resident slot, out by length: row b gets
 // ceil(t_b / T) of them (t_b its tiles, T the smallest step that fits; see share_rows in
-// decode_tiled.hip), so it runs in one round of equally long work-groups instead of
+// decode_tiled.h), so it runs in one round of equally long work-groups instead of
 // rounds of work-groups as long as their row.  pitch: partial slots per (b, query head).
 struct Split {
   int32_t chunk;

@@ -1,4 +1,4 @@
-// Definitions shared by the split-K decode kernels (decode_attn.hip, decode_tiled.hip).
+// Definitions shared by the split-K decode kernels (decode_attn.hip, decode_tiled.h).
 #pragma once
 #include "append_row.h"
 #include "kvq_common.h"
@@ -420,8 +420,8 @@ __device__ __forceinline__ void combine_one(const DecodeArgs& a, int b, int hq, 
 // ---- host side (decode_attn.hip)
 int fail(int code, const std::string& msg);
 
-// ---- tiled kernels (decode_tiled.hip): 8-wave work-groups, interleaved 32-token tiles,
-// single-launch merge.  Format families:
+// ---- tiled kernels (decode_tiled.h; dispatch in decode_tiled.hip): 8-wave work-groups,
+// interleaved 32-token tiles, single-launch merge.  Format families:
 enum TiledFam {
   kTiledNone = 0,
   kTiledA4A4,   // INT4_ASYM K, INT4_ASYM V in the TILE32 layout
@@ -443,6 +443,11 @@ enum TiledFam {
 };
 // kernel of family fam for n_rep query heads per kv head, or nullptr
 const void* tiled_kernel(int fam, int n_rep);
+// the instantiations, one lookup per translation unit (nullptr: not one of its families)
+const void* tiled_kernel_a4(int fam, bool pack8);
+const void* tiled_kernel_tok(int fam, bool pack8);
+const void* tiled_kernel_kv4(int fam, bool pack8);
+const void* tiled_kernel_kv16(int fam, bool pack8);
 hipError_t launch_tiled(const DecodeArgs& a, int fam, dim3 grid, hipStream_t s);
 
 }  // namespace kvq

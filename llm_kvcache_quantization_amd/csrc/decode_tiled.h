@@ -1,0 +1,2072 @@
+// Split-K decode attention for gfx950 over INT4_ASYM K (optional fp16 outlier
+// channels) and INT4_ASYM V stored in the TILE32 layout, optionally with the
+// quantize-on-append of the step's new token in the same launch.
+//
+// One work-group = kTW (8) waves = one (batch b, kv head, chunk); the GQA heads of the kv
+// head are the N = 16 columns of v_mfma_f32_16x16x32_f16 and each wave walks 32-token
+// tiles.  At the headline shape one work-group fills one CU (two waves per SIMD).
+//
+//  * Tile schedule: the n_chunks work-groups of a (b, kv head) interleave tile by tile
+//    (wave w of work-group c takes tiles c * kTW + w + i * n_chunks * kTW), so the device
+//    streams each slab front to back and every wave gets the same number of tiles when
+//    the context allows.  The schedule is static: results do not depend on timing.
+//  * The two waves of a SIMD (w and w + 4) publish their step counts in LDS; the one
+//    ahead lowers its priority (s_setprio), which cancels the SIMD's oldest-first issue
+//    order that would otherwise let one of them finish far earlier.
+//  * K rows are dense (64 bytes per token) and so is the outlier side-band (8 bytes).
+//  * Every cache read is a buffer load.  The (b, kv head) slab of each stream is a
+//    wave-uniform buffer resource whose size bounds the reads (bytes past it read as
+//    zero, with no memory access), the per-tile offset is a scalar and the per-lane
+//    offset is loop-invariant.  Loads past a wave's last tile are issued with an
+//    out-of-range offset rather than skipped, which keeps the compiler's vmcnt waits
+//    exact.
+//  * V in the TILE32 layout stores, for each tile, the 32 bytes lane L needs for its PV
+//    operand contiguously at L * 32: two dwordx4 loads per lane, fully coalesced.
+//  * The 4 fp16 outlier channels of the 32 tokens of a tile (256 bytes) are fetched by
+//    one dword load of the whole wave: lane (row, g) takes the channel pair g & 1 of
+//    token 16 (g >> 1) + row, which is where the outlier MFMA of row block g >> 1
+//    needs it.
+//  * A packed dword becomes 8 fp16 operands with 5 ops.  K: v_and_b32 with the masks
+//    0x00F000F0 (high nibbles of bytes 0 and 2 -> the subnormal 16 n * 2^-24) and
+//    0x000F000F (low nibbles -> n * 2^-24), then the same on the dword shifted right by 8
+//    (bytes 1 and 3); the q side is one fp16 operand per channel and the logits come out
+//    scaled by 2^-24.  V: the same subnormals; the epilogue scales by 2^20 / 2^24 and
+//    removes the code offset 8 against l.
+//  * The probabilities enter the PV MFMAs as hi = fp16(p) and lo = fp16(p - hi), each
+//    multiplied by the V operand (16 MFMAs per tile), so the softmax weights keep about
+//    21 bits instead of fp16's 11 (see softmax_tile).
+//  * The q-dependent operands (fp16(q * s), the bias) are built once per work-group and
+//    shared through LDS; the q loads are issued before the first cache loads.
+//  * K and V tiles are fetched LOOK steps ahead of their use (register rings of
+//    LOOK + 1 tiles); QK of tile i + 1 is issued before softmax / PV of tile i.
+//  * With at most kUnitChunks chunks per (b, kv head) the last work-group to finish
+//    merges the partials (no second launch; its arrival counters live in the workspace,
+//    which must be zero-filled before its first use and which every call leaves zero);
+//    otherwise combine_kernel does.
+//  * The other operand types (K: KI8T, KTokT, KKiviT, KKivi8T, KF16T; V: VI8RowT, VTokT,
+//    VKiviRowT, VKivi8RowT, VF16RowT) read the reference's token-row layouts with the same
+//    schedule, loads and merge.  Their fused append (kAppendRow) runs the append kernel's
+//    row quantizer (append_row.h) in the writer wave, whose inputs are requested with the
+//    q loads; with INT4_SYM sides (kRescue) the writer also finds the group rescue's
+//    threshold over every new row of the step.
+#pragma once
+
+#include "decode_common.h"
+
+#include <cstdlib>
+
+namespace kvq {
+namespace {
+
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int kBufNT = 2;               // cache-policy bits of the buffer loads: nt (streaming)
+constexpr int kRsrcWord3 = 0x00020000;  // buffer descriptor word 3 for raw loads on gfx9 parts
+constexpr int kRowK = kD / 2;           // bytes per token of packed K (dense rows)
+constexpr int kRowO = 4 * 2;            // bytes per token of the fp16 outlier side-band
+// a voffset past every slab (slabs are below 2^31 bytes): such a buffer load returns 0
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+// Raw buffer loads return 0 when voffset + the instruction offset is at or past the
+// descriptor's byte size; soffset is added to the address but not range checked.  Every
+// offset that may run past a buffer's end therefore goes into voffset.
+__device__ __forceinline__ rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRsrcWord3);
+}
+__device__ __forceinline__ u32x4 bload4(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(
+      u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kBufNT));
+}
+__device__ __forceinline__ uint32_t bload1(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kBufNT);
+}
+
+// Fused combine: the last work-group of a (b, kv head) to finish merges the partials of
+// its n_rep heads, which every work-group of the launch stored write-through, and writes
+// the output rows with combine_one's arithmetic.  Needs n_chunks <= kUnitChunks (64);
+// KF::kMergeBatch chunk loads are in flight at a time.
+constexpr int kTW = kTiledWaves;
+constexpr int kBufSC1 = 16;  // cache-policy bits: sc1 (device-coherent load)
+// Chunk partials whose loads the merging work-group issues together: one memory round trip
+// per batch.  Each K format sets its batch (KF::kMergeBatch): 32 where its kernels split a
+// context into many chunks (static INT8 K: 32 chunks per (b, kv head) at config 1), 8
+// otherwise (the 32-load batch raised the INT4 kernels' VGPR count and cost them 0.5 us).
+
+// LDS of the work-group merge.  A head's row holds its 128 channels contiguous, 16-byte
+// aligned, plus one float4 of padding (rows 132 floats apart): a lane writes its 32 channels
+// with 8 ds_write_b128 (channels 32 lg + 8 r .. + 7 are acc[0..7][r]) and the combine reads
+// channel pairs with ds_read_b64.  (One float of padding and scalar writes, 32 per lane, cost
+// about 0.2 us per launch at the headline shape.)
+struct TiledMergeLds {
+  float m[kTW][16];
+  float l[kTW][16];
+  float4v acc[kTW][16][kD / 4 + 1];
+};
+
+// Merges the (m, l, acc) states of the kTW waves (through LDS) into the work-group's
+// partial and stores it write-through at device scope, so another work-group of the launch,
+// on any XCD, can read it once the stores have completed.  acc[mb][r] of lane (head, lg)
+// holds channel d = 32 lg + 8 r + mb.  Wave w merges heads w, w + kTW, ..; lane l
+// channels 2 l and 2 l + 1: partial = sum_w e_w acc_w with e_w = exp2(m_w - M), (M,
+// sum_w e_w l_w) for the head's (m, l) pair.
+template <bool PACK8>
+__device__ __forceinline__ void merge_store_partial(const DecodeArgs& a, TiledMergeLds& sh,
+                                                    int wave, int lane, float m, float l,
+                                                    const float4v acc[8], int b, int hkv,
+                                                    int chunk) {
+  const int col = lane & 15, lg = lane >> 4;
+  if constexpr (PACK8) l += dpp_ror8f<0xF>(l, l);  // add the block-1 part from lane h + 8
+  l = wave_sum_xor_groups(l);
+  if (lg == 0) {
+    sh.m[wave][col] = m;
+    sh.l[wave][col] = l;
+  }
+  if (col < a.n_rep) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sh.acc[wave][col][8 * lg + 2 * r] = float4v{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+      sh.acc[wave][col][8 * lg + 2 * r + 1] = float4v{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+    }
+  }
+  __syncthreads();
+  for (int h = wave; h < a.n_rep; h += kTW) {
+    float mw[kTW];
+#pragma unroll
+    for (int w = 0; w < kTW; ++w) mw[w] = sh.m[w][h];
+    float M = mw[0];
+#pragma unroll
+    for (int w = 1; w < kTW; ++w) M = fmaxf(M, mw[w]);
+    float n0 = 0.f, n1 = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kTW; ++w) {
+      const float e = fast_exp2(mw[w] - M);
+      const float2 v2 = reinterpret_cast<const float2*>(&sh.acc[w][h][0])[lane];
+      n0 = fmaf(e, v2.x, n0);
+      n1 = fmaf(e, v2.y, n1);
+      den = fmaf(e, sh.l[w][h], den);
+    }
+    const int64_t pi = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks + chunk;
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_acc + pi * kD + 2 * lane),
+                       __builtin_bit_cast(uint64_t, float2{n0, n1}), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_ml + pi),
+                         __builtin_bit_cast(uint64_t, float2{M, den}), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The attention partial (m, l, acc of channels 2 lane, 2 lane + 1) of query head hq over the
+// fp16 residual window of (b, kv head) (a.res_n tokens), in the units of the chunk partials:
+// logits q' . k * sm * log2(e) with q' = fp16(q * inv_tau) in fp32, base-2 softmax.  The
+// window's rows are read 16 tokens per batch, K and V of a batch in flight together; one wave
+// reduction per token.
+__device__ __forceinline__ void residual_partial(const DecodeArgs& a, int b, int hkv, int hq, int lane,
+                                                 float& mr, float& lr, float& r0, float& r1) {
+  const bool has_tau = a.inv_tau != nullptr;
+  const half_t tau = has_tau ? a.inv_tau[hq] : (half_t)1.0f;
+  const half2v q2 = *reinterpret_cast<const half2v*>(q_row(a, b, hq) + 2 * lane);
+  const float q0 = (float)qscale(q2.x, tau, has_tau), q1 = (float)qscale(q2.y, tau, has_tau);
+  const int64_t off = (int64_t)b * a.rsb + (int64_t)hkv * a.rsh + 2 * lane;
+  const half_t* kr = a.res_k + off;
+  const half_t* vr = a.res_v + off;
+  constexpr int kRB = 16;
+  mr = kNegInf;
+  lr = r0 = r1 = 0.f;
+  for (int t0 = 0; t0 < a.res_n; t0 += kRB) {
+    half2v kb[kRB], vb[kRB];
+#pragma unroll
+    for (int u = 0; u < kRB; ++u) {
+      const int t = t0 + u < a.res_n ? t0 + u : a.res_n - 1;  // in bounds; masked below
+      kb[u] = *reinterpret_cast<const half2v*>(kr + (int64_t)t * kD);
+      vb[u] = *reinterpret_cast<const half2v*>(vr + (int64_t)t * kD);
+    }
+    float sc[kRB];
+    float mx = mr;
+#pragma unroll
+    for (int u = 0; u < kRB; ++u) {
+      const float d = wave_sum64(fmaf(q0, (float)kb[u].x, q1 * (float)kb[u].y));
+      sc[u] = t0 + u < a.res_n ? d * a.sm_log2e : kNegInf;
+      mx = fmaxf(mx, sc[u]);
+    }
+    const float al = fast_exp2(mr - mx);
+    lr *= al;
+    r0 *= al;
+    r1 *= al;
+    mr = mx;
+#pragma unroll
+    for (int u = 0; u < kRB; ++u) {
+      const float p = fast_exp2(sc[u] - mr);
+      lr += p;
+      r0 = fmaf(p, (float)vb[u].x, r0);
+      r1 = fmaf(p, (float)vb[u].y, r1);
+    }
+  }
+}
+
+// The last work-group's merge of the nvalid chunk partials of each query head (its own
+// included, read back like the others), with combine_one's arithmetic.  Wave w takes heads
+// w, w + kTW, ..; lane l the (m, l) pair of chunk l and channels 2 l, 2 l + 1 of every
+// chunk.  The buffer resources end after the nvalid-th chunk, so the loads of chunks past
+// it read 0 without a branch; their weight is exp2(-inf) = 0.  Loads bypass the
+// non-coherent cache levels (sc1); chunks are added in chunk order whichever work-group
+// merges, so every call gives the same bits.  s, z: the V scale / zero-point of group
+// lane / 16.
+template <class VF, int kUnitBatch>
+__device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv, int nvalid,
+                                             int wave, int lane) {
+  // the V epilogue's scale / zero-point, requested with the first partial loads (loaded any
+  // earlier, every work-group's merge would wait for them)
+  float s, z;
+  VF::epi_params(a, hkv, lane, s, z);
+  static_assert(kUnitChunks <= 64, "one (m, l) pair per lane");
+  for (int h = wave; h < a.n_rep; h += kTW) {
+    const int64_t row = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks;
+    const rsrc_t rml = buffer_rsrc(a.part_ml + row, (uint32_t)nvalid * 8u);
+    const rsrc_t racc = buffer_rsrc(a.part_acc + row * kD, (uint32_t)nvalid * (kD * 4u));
+    const u32x2 mlv = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, (int)(lane * 8), 0, kBufSC1));
+    const uint32_t vbase = (uint32_t)lane * 8u;
+    u32x2 av[kUnitBatch];
+#pragma unroll
+    for (int c = 0; c < kUnitBatch; ++c)
+      av[c] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                            racc, (int)(vbase + (uint32_t)c * (kD * 4u)), 0, kBufSC1));
+    // every load of the first batch is issued before the (m, l) pair is used (one memory
+    // latency, not two)
+    asm volatile("" ::: "memory");
+    // the fp16 residual window's partial (KIVI-family V formats), while the chunk partials
+    // are in flight
+    float mr = kNegInf, lr = 0.f, rr0 = 0.f, rr1 = 0.f;
+    if constexpr (VF::kResidual)
+      if (a.res_n > 0) residual_partial(a, b, hkv, hkv * a.n_rep + h, lane, mr, lr, rr0, rr1);
+    const float mc = lane < nvalid ? __builtin_bit_cast(float, (uint32_t)mlv.x) : kNegInf;
+    float M = wave_max64(mc);
+    if constexpr (VF::kResidual) M = fmaxf(M, mr);
+    const float e = fast_exp2(mc - M);
+    float den = wave_sum64(e * __builtin_bit_cast(float, (uint32_t)mlv.y));
+    float er = 0.f;  // the window's weight (none without one)
+    if constexpr (VF::kResidual) {
+      er = fast_exp2(mr - M);
+      den = fmaf(er, lr, den);
+    }
+    float n0 = 0.f, n1 = 0.f;
+    for (int c0 = 0;;) {
+#pragma unroll
+      for (int c = 0; c < kUnitBatch; ++c) {
+        // (uint32_t) makes the vector element an rvalue: this clang's __builtin_bit_cast of
+        // an ext_vector element lvalue reads element 0 whatever the index
+        const float ec = row_lane(e, c0 + c);
+        n0 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)av[c].x), n0);
+        n1 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)av[c].y), n1);
+      }
+      c0 += kUnitBatch;
+      if (c0 >= nvalid) {
+        if constexpr (VF::kResidual) {
+          n0 = fmaf(er, rr0, n0);
+          n1 = fmaf(er, rr1, n1);
+        }
+        break;
+      }
+#pragma unroll
+      for (int c = 0; c < kUnitBatch; ++c)
+        av[c] = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                       racc, (int)(vbase + (uint32_t)(c0 + c) * (kD * 4u)), 0, kBufSC1));
+    }
+    const half2v o = VF::epilogue(n0 / den, n1 / den, s, z);
+    *reinterpret_cast<half2v*>(a.out + (int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + h) * a.o_sh +
+                               2 * lane) = o;
+  }
+}
+
+// 8 packed codes -> 8 fp16 operands in k-slot order [e0, e4, e1, e5, e2, e6, e3, e7]
+// (e = element within the dword; byte k holds e = 2k in its high nibble), read as fp16
+// subnormals: a nibble in bits 4..7 of a 16-bit half is 16 n * 2^-24, one in bits 0..3 is
+// n * 2^-24, both exact.  The MFMA takes subnormal fp16 inputs without flushing them, and
+// with no offset in the operand the q side needs a single fp16 operand (a product q * s
+// rounded to fp16 perturbs each term by at most 2^-11 of itself).  5 ops per 8 codes.
+__device__ __forceinline__ half8v unpack_sub(uint32_t w, const NibConsts& nc) {
+  const uint32_t w8 = w >> 8;
+  return pack8(w & nc.m_hi, w & nc.m_lo, w8 & nc.m_hi, w8 & nc.m_lo);
+}
+__host__ __device__ constexpr int slot_elem(int k) { return (k & 1) * 4 + (k >> 1); }
+// k-slots holding a high nibble (operand value 16 n * 2^-24)
+__host__ __device__ constexpr bool slot_high(int k) { return ((k >> 1) & 1) == 0; }
+constexpr float kTwo24 = 16777216.0f;       // 2^24
+constexpr float kTwoM24 = 5.9604644775390625e-8f;  // 2^-24
+
+// LDS through which the 4 waves share the q-dependent K operands, and the scaled q rows
+// from which the outlier operand is gathered
+struct QShareLds {
+  u32x4 qh[4][64];
+  u32x4 ql[4][64];  // the low halves of a hi + lo split operand (KKiviT)
+  float bias[4][16];
+  half_t qv[16][kD];  // q' of head column c (zero for padding columns)
+};
+
+// x = hi + lo with hi = fp16(x) and lo = fp16(x - hi) (x - hi is exact in fp32): the pair
+// carries x to about 2^-22 of itself, where fp16(x) alone carries it to 2^-11
+__device__ __forceinline__ void split_h(float x, half_t& hi, half_t& lo) {
+  hi = (half_t)x;
+  lo = (half_t)(x - (float)hi);
+}
+
+// The q-side inputs of one lane: q[32 lg + 8 wave .. + 7] of head column lane % 16, its
+// inverse temperature and the K scale / zero-point of group lg.  They are fetched before
+// the first cache loads, so waiting for them does not wait for those (vmcnt counts loads
+// in issue order).
+struct QIn {
+  u32x4 q;
+  half_t tau, s, z;
+  int4 oc;
+  half_t sj[4];  // static INT8 K: the scale of channel slice 32 lg + 8 j (any group size)
+};
+
+// INT4 asymmetric K with static scale s / zero-point z per (kv head, group of 32).  With
+// code c = n - 8 the logit is
+//   sum_d q_d (s c_d + z) = sum_d (q_d s) n_d + sum_d q_d (z - 8 s);
+// the codes enter the MFMA as subnormals n * 2^-24 (16 n * 2^-24 for high nibbles, whose
+// q operand is divided by 16), q_d s rounded to fp16 is the other operand, and the
+// constant term starts the accumulator.  Outlier channels (q zeroed in the main MFMAs)
+// are added by one MFMA of the same shape whose operands are the 4 fp16 outlier values
+// and q' of those channels in the first two k-slots of each lane group.
+template <bool OUT>
+struct KAsymT {
+  static constexpr int kMergeBatch = 8;
+  // hi / lo probabilities in one PV MFMA (softmax_tile8c) when the V format allows it:
+  // measured 0.2 us faster at configs 2-3; with static INT8 K (short per-wave runs at
+  // config 1) the post-loop fold costs more than the MFMAs it saves
+  static constexpr bool kPackPV = true;
+  using QInT = QIn;
+  static constexpr bool kAppend = true;  // the fused quantize-on-append is built for this format
+  static constexpr bool kAppendRow = false;  // (its own specialised writer code)
+  static constexpr bool kAsym = true;
+  static constexpr bool kGsAny = false;  // groups of 32
+  static constexpr bool kOut = OUT;
+  static constexpr bool kSub24 = true;  // logits scaled by 2^-24
+  half8v qh[4];
+  half8v qo;
+  float bias;
+  rsrc_t rk, ro;
+  uint32_t vk, vo;
+  bool olo;  // lane group 0 or 1 (row block 0 of the outlier operand)
+  struct Raw {
+    u32x4 w[2];
+    uint32_t o;
+  };
+
+  // buffer resources and lane offsets (no dependence on q: runs before the first loads)
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    olo = lg < 2;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kRowK));
+    vk = (uint32_t)(col * kRowK + 16 * lg);
+    if constexpr (OUT) {
+      const half_t* ob = a.k.oval + (int64_t)b * a.k.osb + (int64_t)hkv * a.k.osh;
+      ro = buffer_rsrc(ob, (uint32_t)(a.cap * kRowO));
+      vo = (uint32_t)((16 * (lg >> 1) + col) * kRowO + (lg & 1) * 4);
+    }
+  }
+
+  // issues the loads of the q-side inputs (padding columns read head 0's row)
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.s = reinterpret_cast<const half_t*>(a.k.scale)[hkv * a.k.ssh + lg * a.k.ssg];
+    in.z = a.k.zp[hkv * a.k.ssh + lg * a.k.ssg];
+    in.oc = int4{-1, -1, -1, -1};
+    if constexpr (OUT) {
+      const int4 o = *reinterpret_cast<const int4*>(a.k.oidx + hkv * 4);
+      in.oc = int4{min(max(o.x, 0), kD - 1), min(max(o.y, 0), kD - 1), min(max(o.z, 0), kD - 1),
+                   min(max(o.w, 0), kD - 1)};
+    }
+  }
+
+  // q-dependent operands of channel slice j = 0..3 (channels 32 lg + 8 j + e), shared
+  // through LDS; called by waves 0..3 only.  Operand k = fp16(q'_d s) (fp16(q'_d s / 16) for a
+  // high-nibble slot) multiplies n_d * 2^-24 (16 n_d * 2^-24), so the MFMA sums
+  // e_d n_d * 2^-24 with e_d = the operand's value (x 16 for a high nibble), and
+  //   logit = sum_d q'_d (s c_d + z) = 2^24 * mfma + sum_d (q'_d z - 8 e_d)  (c = n - 8).
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15, lg = lane >> 4;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    const float s = (float)in.s;
+    const float z = (float)in.z;
+    float part = 0.f;
+    half_t vh[8], qs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      qs[e] = valid ? qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = slot_elem(k);
+      const int d = 32 * lg + 8 * j + e;
+      const bool use = d != in.oc.x && d != in.oc.y && d != in.oc.z && d != in.oc.w;
+      const float qd = use ? (float)qs[e] : 0.f;
+      const float P = qd * s;  // exact: 11-bit x 11-bit significands
+      const half_t h = (half_t)(slot_high(k) ? P * 0.0625f : P);
+      vh[k] = h;
+      part += qd * z - 8.0f * (slot_high(k) ? 16.0f * (float)h : (float)h);
+    }
+    part = wave_sum_xor_groups(part);
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+    *reinterpret_cast<u32x4*>(&sh.qv[col][32 * lg + 8 * j]) =
+        __builtin_bit_cast(u32x4, half8v{qs[0], qs[1], qs[2], qs[3], qs[4], qs[5], qs[6], qs[7]});
+    if (lg == 0) sh.bias[j][col] = part;
+  }
+
+  // after the work-group barrier: pick up the operands all four waves built
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+    const int col = lane & 15;
+    bias = (sh.bias[0][col] + sh.bias[1][col]) + (sh.bias[2][col] + sh.bias[3][col]);
+    const half_t h0 = (half_t)0.0f;
+    qo = half8v{h0, h0, h0, h0, h0, h0, h0, h0};
+    if constexpr (OUT) {
+      // lane group lg supplies outlier channels 2 (lg & 1) and 2 (lg & 1) + 1
+      const bool odd = ((lane >> 4) & 1) != 0;
+      qo = half8v{sh.qv[col][odd ? in.oc.z : in.oc.x], sh.qv[col][odd ? in.oc.w : in.oc.y],
+                  h0, h0, h0, h0, h0, h0};
+    }
+  }
+
+  // rows of a partial last tile past the capacity read 0 (tok in voffset, range checked);
+  // with !valid (wave-uniform) every load is out of range: it reads 0 and touches no memory
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kRowK : kOutOfRange);
+    r.w[0] = bload4(rk, v, 0);
+    r.w[1] = bload4(rk, v + 16 * kRowK, 0);
+    if constexpr (OUT) r.o = bload1(ro, vo + (valid ? (uint32_t)tok * kRowO : kOutOfRange), 0);
+  }
+
+  // logits of the tile's two 16-token row blocks (x0: tokens 4 lg + r, x1: 16 + 4 lg + r),
+  // scaled by 2^-24 (the softmax multiplies by sm * 2^24).  The outlier channels go through
+  // a separate accumulator at unit scale, started at the bias, and are added at the end.
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    float4v c0, c1;
+    if constexpr (OUT) {
+      c0 = float4v{0.f, 0.f, 0.f, 0.f};
+      c1 = c0;
+    } else {
+      const float b24 = bias * kTwoM24;
+      c0 = float4v{b24, b24, b24, b24};
+      c1 = c0;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c0 = mfma16x16x32(unpack_sub(r.w[0][j], nc), qh[j], c0);
+      c1 = mfma16x16x32(unpack_sub(r.w[1][j], nc), qh[j], c1);
+    }
+    if constexpr (OUT) {
+      const float4v b4 = {bias, bias, bias, bias};
+      const float4v o0 = mfma16x16x32(pack8(olo ? r.o : 0u, 0u, 0u, 0u), qo, b4);
+      const float4v o1 = mfma16x16x32(pack8(olo ? 0u : r.o, 0u, 0u, 0u), qo, b4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c0[i] = fmaf(o0[i], kTwoM24, c0[i]);
+        c1[i] = fmaf(o1[i], kTwoM24, c1[i]);
+      }
+    }
+    x0 = c0;
+    x1 = c1;
+  }
+};
+
+// INT4 asymmetric V in the TILE32 layout.  acc[c] (c < 8) accumulates sum_t p * x for
+// channel 8 col + c of the lane's d-row col, with the codes as the exact fp16 subnormals
+// x = 16 n 2^-24 (even c, high nibble) or n 2^-24 (odd c) and p the hi + lo probability
+// operands (softmax_tile); the epilogue applies out = s (acc / l * 2^20 or 2^24 - 8) + z.
+struct VAsymT {
+  static constexpr bool kResidual = false;  // merges an fp16 residual window
+  static constexpr bool kTile32 = true;
+  static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
+  // hooks of formats with per-token parameters (none here)
+  template <class Raw>
+  __device__ __forceinline__ void mask(Raw&, int, int, int) const {}
+  __device__ __forceinline__ void finalize(float4v*, int) const {}
+  __device__ __forceinline__ float* extra() { return nullptr; }
+  rsrc_t rv;
+  uint32_t vv;
+  struct Raw {
+    u32x4 w[2];
+  };
+  // the V scale / zero-point of group lane / 16 for the output epilogue
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    const int g = lane >> 4;
+    s = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
+    z = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
+  }
+  // channels 2 lane, 2 lane + 1 from the merged acc / l: 2^20 r0 and 2^24 r1 are n = c + 8
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    return half2v{(half_t)fmaf(s, fmaf(r0, 1048576.0f, -8.0f), z),
+                  (half_t)fmaf(s, fmaf(r1, 16777216.0f, -8.0f), z)};
+  }
+
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(((a.cap + kTile - 1) / kTile) * kTile * (kD / 2)));
+    vv = (uint32_t)lane * 32u;
+  }
+  // whole tiles only: the descriptor spans ceil(capacity / 32) tiles; with !valid
+  // (wave-uniform) voffset is out of range, so the loads read 0 and touch no memory
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t soff = valid ? (uint32_t)tok * (kD / 2) : 0u;  // tile index * 2048
+    const uint32_t v = vv + (valid ? 0u : kOutOfRange);
+    r.w[0] = bload4(rv, v, soff);
+    r.w[1] = bload4(rv, v + 16u, soff);
+  }
+  template <bool ONE = false>
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
+                                      const NibConsts& nc) const {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      // dword 2p + k of the lane: bytes (2k, 2k+1) of the two tokens of k-slot pair p
+      const uint32_t a0 = k ? r.w[0].y : r.w[0].x, a1 = k ? r.w[0].w : r.w[0].z;
+      const uint32_t a2 = k ? r.w[1].y : r.w[1].x, a3 = k ? r.w[1].w : r.w[1].z;
+      const uint32_t s0 = a0 >> 8, s1 = a1 >> 8, s2 = a2 >> 8, s3 = a3 >> 8;
+      const half8v c0 = pack8(a0 & nc.m_hi, a1 & nc.m_hi, a2 & nc.m_hi, a3 & nc.m_hi);
+      const half8v c1 = pack8(a0 & nc.m_lo, a1 & nc.m_lo, a2 & nc.m_lo, a3 & nc.m_lo);
+      const half8v c2 = pack8(s0 & nc.m_hi, s1 & nc.m_hi, s2 & nc.m_hi, s3 & nc.m_hi);
+      const half8v c3 = pack8(s0 & nc.m_lo, s1 & nc.m_lo, s2 & nc.m_lo, s3 & nc.m_lo);
+      acc[4 * k] = mfma16x16x32(c0, pb, acc[4 * k]);
+      acc[4 * k + 1] = mfma16x16x32(c1, pb, acc[4 * k + 1]);
+      acc[4 * k + 2] = mfma16x16x32(c2, pb, acc[4 * k + 2]);
+      acc[4 * k + 3] = mfma16x16x32(c3, pb, acc[4 * k + 3]);
+      if constexpr (!ONE) {
+        acc[4 * k] = mfma16x16x32(c0, pl, acc[4 * k]);
+        acc[4 * k + 1] = mfma16x16x32(c1, pl, acc[4 * k + 1]);
+        acc[4 * k + 2] = mfma16x16x32(c2, pl, acc[4 * k + 2]);
+        acc[4 * k + 3] = mfma16x16x32(c3, pl, acc[4 * k + 3]);
+      }
+    }
+  }
+  // one MFMA per block: pb is softmax_tile8c's combined hi / lo operand
+  __device__ __forceinline__ void mma1(const Raw& r, half8v pc, float4v acc[8],
+                                       const NibConsts& nc) const {
+    mma<true>(r, pc, pc, acc, nc);
+  }
+};
+
+// fp16 scale of (kv head, group g) from a scale view that is static over b and t
+// (stride-0 view of per-token scales, fp16 or fp32; an fp32 scale is rounded to fp16)
+__device__ __forceinline__ half_t static_scale16(const KvDev& v, int hkv, int g) {
+  const int64_t i = (int64_t)hkv * v.ssh + (int64_t)g * v.ssg;
+  return v.scale_f32 ? (half_t)reinterpret_cast<const float*>(v.scale)[i]
+                     : reinterpret_cast<const half_t*>(v.scale)[i];
+}
+
+// Two INT8 codes (the low bytes of the two halves of x, the high bytes zero) -> the fp16
+// pair fp16(c * s16), rounded once as the reference's dequantisation (int8 -> fp16, times
+// the fp16 scale, src/engine/patch_model.py:355-362): x ^ 0x64806480 gives 1024 + (c + 128)
+// exactly, minus 1152 gives c, and the packed fp16 product with s16 rounds to nearest even.
+__device__ __forceinline__ uint32_t i8pair_deq(uint32_t x, half2v s2) {
+  const half2v off = {(half_t)1152.0f, (half_t)1152.0f};
+  return as_u32((as_h2(x ^ 0x64806480u) - off) * s2);
+}
+
+// INT8 symmetric K with a static fp16 scale s per (kv head, group), i.e. per-token scales
+// given as a view with stride 0 over b and t (the reference's static-scale cache,
+// src/cache/int8_cache.py:298-488).  Lane (row, lg) of row block rb reads bytes
+// [32 lg, 32 lg + 32) of token 16 rb + row.  GS_ANY = false: groups of 32, so those 32
+// channels are group lg and share one scale.  GS_ANY = true: any group size (8 .. 128,
+// a.gs); each 8-channel slice j takes the scale of its own group (3 more VGPRs; the group
+// index comes from a.gs at run time, which costs the groups-of-32 kernel 0.2 us of set-up
+// at config 1, hence two instantiations).  The A operand is the reference's
+// dequantised k = fp16(c * s16) (i8pair_deq), the B operand q', so the logits are the
+// reference's fp32 dot products of fp16 k and q up to the summation order.
+template <bool GS_ANY>
+struct KI8T {
+  static constexpr bool kGsAny = GS_ANY;
+  static constexpr int kMergeBatch = 32;
+  static constexpr bool kPackPV = false;
+  using QInT = QIn;
+  static constexpr bool kAppend = true;
+  static constexpr bool kAppendRow = false;
+  static constexpr bool kAsym = false;
+  static constexpr bool kOut = false;
+  static constexpr bool kSub24 = false;  // logits at unit scale
+  static constexpr int kNS = GS_ANY ? 4 : 1;
+  half8v qh[4];
+  half2v s2[kNS];  // the scale of channel slice 32 lg + 8 j .. + 7 (its group), twice
+  rsrc_t rk;
+  uint32_t vk;
+  struct Raw {
+    u32x4 w[4];  // [2 rb + i]: bytes [32 lg + 16 i, 32 lg + 16 i + 16) of token 16 rb + row
+  };
+
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kD));
+    vk = (uint32_t)(col * kD + 32 * lg);
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    if constexpr (GS_ANY) {
+      // slice j of the lane's 32 channels lies in group (32 lg + 8 j) / gs (gs = 8 .. 128)
+      const int sh = __builtin_ctz((unsigned)a.gs);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) in.sj[j] = static_scale16(a.k, hkv, (32 * lg + 8 * j) >> sh);
+    } else {
+      in.sj[0] = static_scale16(a.k, hkv, lg);
+    }
+    in.s = in.sj[0];
+    in.z = (half_t)0.0f;
+    in.oc = int4{-1, -1, -1, -1};
+  }
+  // channel slice j (channels 32 lg + 8 j + e) of the q operand q' = fp16(q * inv_tau),
+  // shared through LDS
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    half_t vh[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      vh[e] = valid ? qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+  }
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+#pragma unroll
+    for (int j = 0; j < kNS; ++j) s2[j] = half2v{in.sj[j], in.sj[j]};
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kD : kOutOfRange);
+    r.w[0] = bload4(rk, v, 0);
+    r.w[1] = bload4(rk, v + 16, 0);
+    r.w[2] = bload4(rk, v + 16 * kD, 0);
+    r.w[3] = bload4(rk, v + 16 * kD + 16, 0);
+  }
+  // 8 codes of slice j (dwords lo = channels 0..3, hi = 4..7) -> fp16(c * s16) in channel
+  // order
+  __device__ __forceinline__ half8v deq8(uint32_t lo, uint32_t hi, int j) const {
+    const half2v s = s2[GS_ANY ? j : 0];
+    return pack8(i8pair_deq(perm_b32(0u, lo, 0x0C010C00u), s), i8pair_deq(perm_b32(0u, lo, 0x0C030C02u), s),
+                 i8pair_deq(perm_b32(0u, hi, 0x0C010C00u), s), i8pair_deq(perm_b32(0u, hi, 0x0C030C02u), s));
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    (void)nc;
+    float4v c0 = {0.f, 0.f, 0.f, 0.f};
+    float4v c1 = c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 w0 = r.w[j >> 1], w1 = r.w[2 + (j >> 1)];
+      const uint32_t l0 = (j & 1) ? w0.z : w0.x, h0 = (j & 1) ? w0.w : w0.y;
+      const uint32_t l1 = (j & 1) ? w1.z : w1.x, h1 = (j & 1) ? w1.w : w1.y;
+      c0 = mfma16x16x32(deq8(l0, h0, j), qh[j], c0);
+      c1 = mfma16x16x32(deq8(l1, h1, j), qh[j], c1);
+    }
+    x0 = c0;
+    x1 = c1;
+  }
+};
+
+// INT8 symmetric V in token rows (the reference layout) with a static scale per (kv head,
+// group): groups of 32 (GS_ANY = false) or any group size a.gs (8 .. 128).  Lane (col, lg) reads the 8 bytes of channels 8 col .. 8 col + 7 of its 8
+// PV k-slot tokens T(k) = 4 lg + k (k < 4), 16 + 4 lg + k - 4: each load instruction reads
+// four whole 128-byte rows.  The A operand of MFMA c (channel 8 col + c) is the reference's
+// v = fp16(c * s16) of the 8 tokens (one v_perm_b32 per pair of tokens, then i8pair_deq), so
+// acc / l is the output.
+template <bool GS_ANY>
+struct VI8RowT {
+  static constexpr bool kResidual = false;  // merges an fp16 residual window
+  static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
+  static constexpr bool kTile32 = false;
+  // hooks of formats with per-token parameters (none here)
+  template <class Raw>
+  __device__ __forceinline__ void mask(Raw&, int, int, int) const {}
+  __device__ __forceinline__ void finalize(float4v*, int) const {}
+  __device__ __forceinline__ float* extra() { return nullptr; }
+  rsrc_t rv;
+  uint32_t vv;
+  half2v s2;  // the scale of the group of channels 8 col .. 8 col + 7, twice
+  struct Raw {
+    u32x2 w[8];  // token T(k)
+  };
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * kD));
+    vv = (uint32_t)((4 * lg) * kD + 8 * col);
+    const half_t sv =
+        static_scale16(a.v, hkv, GS_ANY ? (8 * col) >> __builtin_ctz((unsigned)a.gs) : col >> 2);
+    s2 = half2v{sv, sv};
+  }
+  // rows of a partial last tile past the capacity read 0; !valid: every load out of range
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * kD : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      r.w[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(v + t * kD), 0, kBufNT));
+    }
+  }
+  template <bool ONE = false>
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
+                                      const NibConsts& nc) const {
+    (void)nc;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      // byte c % 4 of the tokens T(2p) and T(2p + 1) into the low bytes of the two halves
+      const uint32_t sel = (uint32_t)(c & 3) | 0x0C00u | ((uint32_t)(4 + (c & 3)) << 16) | 0x0C000000u;
+      uint32_t R[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t lo = (c >> 2) ? r.w[2 * p].y : r.w[2 * p].x;
+        const uint32_t hi = (c >> 2) ? r.w[2 * p + 1].y : r.w[2 * p + 1].x;
+        R[p] = i8pair_deq(perm_b32(hi, lo, sel), s2);
+      }
+      const half8v av = pack8(R[0], R[1], R[2], R[3]);
+      acc[c] = mfma16x16x32(av, pb, acc[c]);
+      if constexpr (!ONE) acc[c] = mfma16x16x32(av, pl, acc[c]);
+    }
+  }
+  // one MFMA per block: pb is softmax_tile8c's combined hi / lo operand
+  __device__ __forceinline__ void mma1(const Raw& r, half8v pc, float4v acc[8],
+                                       const NibConsts& nc) const {
+    mma<true>(r, pc, pc, acc, nc);
+  }
+};
+
+// ---- KIVI layout (the reference's asymmetric INT4 kernels,
+// src/kernels/triton_decode_attn_int4_asym.py:28-277 and its v2 / GQA variants): packed
+// nibbles in token rows, K value (n - 8) s_d + z_d with fp32 s, z per (b, h, channel), V
+// value (n - 8) s_t + z_t with fp32 s, z per (b, h, token).
+
+// q-side inputs of KKiviT: the lane's 8 channels' K scale and zero-point
+struct KiviQIn {
+  u32x4 q;
+  half_t tau, s, z;  // s, z unused (the fused append is not built for this format)
+  int4 oc;
+  float4v ks[2], kz[2];
+};
+
+// K of the KIVI layout: as KAsymT<false> (subnormal nibbles, logits x 2^-24) with
+// per-channel parameters.  The q operand q'_d s_d (/ 16 for a high nibble) is a hi + lo
+// pair of fp16 values (split_h), each multiplied by the codes in its own MFMA, so the
+// product is carried to about 2^-22 of itself: the reference computes k = (n - 8) s_d + z_d
+// and q . k in fp32, and per-channel scales of K outlier channels can be two orders of
+// magnitude above the rest, where one fp16 rounding of q'_d s_d (2^-11 of the term) would
+// show in the logits.  The constant term sum_d q'_d (z_d - 8 s_d) is summed in fp32.
+struct KKiviT : KAsymT<false> {
+  using QInT = KiviQIn;
+  static constexpr bool kAppend = false;
+  static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
+  static constexpr bool kRescue = false;     // (no INT4_SYM side)
+  half8v ql[4];
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, KiviQIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.oc = int4{-1, -1, -1, -1};
+    const int64_t o = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh + 32 * lg + 8 * (wave & 3);
+    const float* ps = reinterpret_cast<const float*>(a.k.scale) + o;
+    const float* pz = reinterpret_cast<const float*>(a.k.zp) + o;
+    in.ks[0] = *reinterpret_cast<const float4v*>(ps);
+    in.ks[1] = *reinterpret_cast<const float4v*>(ps + 4);
+    in.kz[0] = *reinterpret_cast<const float4v*>(pz);
+    in.kz[1] = *reinterpret_cast<const float4v*>(pz + 4);
+  }
+  __device__ void setup_q(const DecodeArgs& a, const KiviQIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15, lg = lane >> 4;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    float part = 0.f;
+    half_t vh[8], vl[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = slot_elem(k);
+      const half2v h2 = as_h2(qw[e >> 1]);
+      const float qd = valid ? (float)qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : 0.f;
+      const float sd = in.ks[e >> 2][e & 3], zd = in.kz[e >> 2][e & 3];
+      const float P = qd * sd;
+      split_h(slot_high(k) ? P * 0.0625f : P, vh[k], vl[k]);
+      part += qd * fmaf(-8.0f, sd, zd);
+    }
+    part = wave_sum_xor_groups(part);
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+    sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
+    if (lg == 0) sh.bias[j][col] = part;
+  }
+  __device__ void finish_setup(const QShareLds& sh, const KiviQIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+      ql[j] = __builtin_bit_cast(half8v, sh.ql[j][lane]);
+    }
+    const int col = lane & 15;
+    bias = (sh.bias[0][col] + sh.bias[1][col]) + (sh.bias[2][col] + sh.bias[3][col]);
+  }
+  // logits x 2^-24 of the tile's two row blocks: the codes times the hi and the lo operand
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    const float b24 = bias * kTwoM24;
+    float4v c0 = {b24, b24, b24, b24};
+    float4v c1 = c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const half8v a0 = unpack_sub(r.w[0][j], nc), a1 = unpack_sub(r.w[1][j], nc);
+      c0 = mfma16x16x32(a0, qh[j], c0);
+      c1 = mfma16x16x32(a1, qh[j], c1);
+      c0 = mfma16x16x32(a0, ql[j], c0);
+      c1 = mfma16x16x32(a1, ql[j], c1);
+    }
+    x0 = c0;
+    x1 = c1;
+  }
+};
+
+// V of the KIVI layout in token rows (64 bytes).  Lane (col, lg) reads the dword of
+// channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens T(k) (four 64-byte rows
+// per load instruction) and their fp32 scale / zero-point.  The codes enter the MFMA as
+// the exact fp16 subnormals n 2^-24 (odd channel, low nibble) and 16 n 2^-24 (even
+// channel, high nibble), and the B operand is w = p s_t (fp32) carried as a hi + lo pair of
+// fp16 values (split_h, two MFMAs per operand), so
+//   sum_t p v = sum_t w (n - 8) + sum_t p z_t = 2^24 acc (/ 16 for an even channel)
+//               - 8 Lp + Cz,   Lp = sum_t (hi + lo),  Cz = sum_t p z_t (fp32),
+// with w rounded to about 2^-22 of itself instead of the 2^-11 of one fp16 operand (the
+// reference dequantises V in fp32).  The wave keeps Lp and Cz beside l (the softmax
+// rescales them with l) and finalize() folds them into acc before the merge (out = acc / l).
+struct VKiviRowT {
+  static constexpr bool kResidual = true;  // merges an fp16 residual window
+  static constexpr bool kPackedPV = false;
+  static constexpr bool kTile32 = false;
+  rsrc_t rv, rs, rz;
+  uint32_t vv, vp;
+  float ex[2];  // Lp, Cz (rescaled with l by the softmax)
+  struct Raw {
+    uint32_t w[8];     // token T(k): bytes 4 col .. 4 col + 3
+    float4v s[2], z[2];  // tokens 4 lg + i, 16 + 4 lg + i
+  };
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * (kD / 2)));
+    vv = (uint32_t)((4 * lg) * (kD / 2) + 4 * col);
+    const int64_t po = (int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh;
+    rs = buffer_rsrc(reinterpret_cast<const float*>(a.v.scale) + po, (uint32_t)(a.cap * 4));
+    rz = buffer_rsrc(reinterpret_cast<const float*>(a.v.zp) + po, (uint32_t)(a.cap * 4));
+    vp = (uint32_t)(4 * lg) * 4u;
+    ex[0] = ex[1] = 0.f;
+  }
+  __device__ __forceinline__ float* extra() { return ex; }
+  // rows of a partial last tile past the capacity read 0; !valid: every load out of range
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * (kD / 2) : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      r.w[k] = bload1(rv, v + t * (kD / 2), 0);
+    }
+    const uint32_t p = vp + (valid ? (uint32_t)tok * 4u : kOutOfRange);
+    r.s[0] = __builtin_bit_cast(float4v, bload4(rs, p, 0));
+    r.s[1] = __builtin_bit_cast(float4v, bload4(rs, p + 64u, 0));
+    r.z[0] = __builtin_bit_cast(float4v, bload4(rz, p, 0));
+    r.z[1] = __builtin_bit_cast(float4v, bload4(rz, p + 64u, 0));
+  }
+  // tokens at or past the context in the last, partial tile: parameters 0 (their memory
+  // may hold anything; p is 0 there)
+  __device__ __forceinline__ void mask(Raw& r, int tt, int ctx, int lg) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (tt + 4 * lg + i >= ctx) r.s[0][i] = r.z[0][i] = 0.f;
+      if (tt + 16 + 4 * lg + i >= ctx) r.s[1][i] = r.z[1][i] = 0.f;
+    }
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v plo, float4v acc[8],
+                                      const NibConsts& nc) {
+    float sk[8], wk[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sk[i] = r.s[0][i];
+      sk[4 + i] = r.s[1][i];
+      wk[i] = r.z[0][i];
+      wk[4 + i] = r.z[1][i];
+    }
+    float cz = ex[1];
+    uint32_t ph[4], pl[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float p0 = (float)pb[2 * q] + (float)plo[2 * q];
+      const float p1 = (float)pb[2 * q + 1] + (float)plo[2 * q + 1];
+      cz = fmaf(p0, wk[2 * q], cz);
+      cz = fmaf(p1, wk[2 * q + 1], cz);
+      half_t h0, l0, h1, l1;
+      split_h(p0 * sk[2 * q], h0, l0);
+      split_h(p1 * sk[2 * q + 1], h1, l1);
+      ph[q] = as_u32(half2v{h0, h1});
+      pl[q] = as_u32(half2v{l0, l1});
+    }
+    ex[1] = cz;
+    const half2v ones = {(half_t)1.0f, (half_t)1.0f};
+    float lp = ex[0];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      lp = __builtin_amdgcn_fdot2(as_h2(ph[q]), ones, lp, false);
+      lp = __builtin_amdgcn_fdot2(as_h2(pl[q]), ones, lp, false);
+    }
+    ex[0] = lp;
+    const half8v wh = pack8(ph[0], ph[1], ph[2], ph[3]);
+    const half8v wl = pack8(pl[0], pl[1], pl[2], pl[3]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // byte j of the tokens T(2p), T(2p + 1) into the low bytes of the two halves
+      const uint32_t sel = (uint32_t)j | 0x0C00u | ((uint32_t)(4 + j) << 16) | 0x0C000000u;
+      uint32_t R[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) R[p] = perm_b32(r.w[2 * p + 1], r.w[2 * p], sel);
+      const half8v ahi = pack8(R[0] & nc.m_hi, R[1] & nc.m_hi, R[2] & nc.m_hi, R[3] & nc.m_hi);
+      const half8v alo = pack8(R[0] & nc.m_lo, R[1] & nc.m_lo, R[2] & nc.m_lo, R[3] & nc.m_lo);
+      acc[2 * j] = mfma16x16x32(ahi, wh, acc[2 * j]);
+      acc[2 * j + 1] = mfma16x16x32(alo, wh, acc[2 * j + 1]);
+      acc[2 * j] = mfma16x16x32(ahi, wl, acc[2 * j]);
+      acc[2 * j + 1] = mfma16x16x32(alo, wl, acc[2 * j + 1]);
+    }
+  }
+  // acc[mb][r] (channel 32 lg + 8 r + mb) = 2^24 acc (2^20 for an even channel, whose codes
+  // entered as 16 n 2^-24) - 8 Lp + Cz, with Lp, Cz summed over the lane groups (the k-slots
+  // of a head)
+  __device__ __forceinline__ void finalize(float4v acc[8], int lane) {
+    (void)lane;
+    const float lp = wave_sum_xor_groups(ex[0]), cz = wave_sum_xor_groups(ex[1]);
+    const float d = fmaf(-8.0f, lp, cz);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const float f = (mb & 1) ? kTwo24 : kTwo24 * 0.0625f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mb][r] = fmaf(acc[mb][r], f, d);
+    }
+  }
+};
+
+// ---- The KIVI family with 8-bit codes and 16-bit sides: the reference's quant_bits=8 KIVI
+// cache (src/cache/kivi_style_cache.py) and the per-layer (k_bits, v_bits) pairs of its
+// allocator and mixed caches (src/cache/role_aware_allocator_cache.py,
+// src/cache/mixed_kv_cache.py), where a 16-bit side stores fp16 values as they come.
+
+// Two int8 codes (the low bytes of the two halves of x, the high bytes zero) -> the exact
+// fp16 pair: x ^ 0x64806480 gives 1024 + (c + 128), minus 1152 gives c.
+__device__ __forceinline__ uint32_t i8pair_exact(uint32_t x) {
+  const half2v off = {(half_t)1152.0f, (half_t)1152.0f};
+  return as_u32(as_h2(x ^ 0x64806480u) - off);
+}
+
+// K of the 8-bit KIVI layout: int8 codes in 128-byte token rows with per-channel fp32 scale
+// s_d and zero-point z_d per (b, kv head).  logit = sum_d q'_d (c_d s_d + z_d): the codes
+// enter the MFMA exactly (i8pair_exact), q'_d s_d as a hi + lo pair of fp16 operands (two
+// MFMAs per slice, as KKiviT), and the constant sum_d q'_d z_d starts the accumulator.
+// Lane (row, lg) of row block rb reads bytes [32 lg, 32 lg + 32) of token 16 rb + row.
+struct KKivi8T {
+  static constexpr int kMergeBatch = 8;
+  static constexpr bool kPackPV = false;
+  using QInT = KiviQIn;
+  static constexpr bool kAppend = false;
+  static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
+  static constexpr bool kRescue = false;     // (no INT4_SYM side)
+  static constexpr bool kAsym = false;
+  static constexpr bool kGsAny = false;
+  static constexpr bool kOut = false;
+  static constexpr bool kSub24 = false;  // logits at unit scale
+  half8v qh[4], ql[4];
+  float bias;
+  rsrc_t rk;
+  uint32_t vk;
+  struct Raw {
+    u32x4 w[4];  // [2 rb + i]: bytes [32 lg + 16 i, + 16) of token 16 rb + row
+  };
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kD));
+    vk = (uint32_t)(col * kD + 32 * lg);
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, KiviQIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.oc = int4{-1, -1, -1, -1};
+    const int64_t o = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh + 32 * lg + 8 * (wave & 3);
+    const float* ps = reinterpret_cast<const float*>(a.k.scale) + o;
+    const float* pz = reinterpret_cast<const float*>(a.k.zp) + o;
+    in.ks[0] = *reinterpret_cast<const float4v*>(ps);
+    in.ks[1] = *reinterpret_cast<const float4v*>(ps + 4);
+    in.kz[0] = *reinterpret_cast<const float4v*>(pz);
+    in.kz[1] = *reinterpret_cast<const float4v*>(pz + 4);
+  }
+  // channel slice j (channels 32 lg + 8 j + e, in channel order)
+  __device__ void setup_q(const DecodeArgs& a, const KiviQIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15, lg = lane >> 4;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    float part = 0.f;
+    half_t vh[8], vl[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      const float qd = valid ? (float)qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : 0.f;
+      split_h(qd * in.ks[e >> 2][e & 3], vh[e], vl[e]);
+      part = fmaf(qd, in.kz[e >> 2][e & 3], part);
+    }
+    part = wave_sum_xor_groups(part);
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+    sh.ql[j][lane] = __builtin_bit_cast(u32x4, half8v{vl[0], vl[1], vl[2], vl[3], vl[4], vl[5], vl[6], vl[7]});
+    if (lg == 0) sh.bias[j][col] = part;
+  }
+  __device__ void finish_setup(const QShareLds& sh, const KiviQIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+      ql[j] = __builtin_bit_cast(half8v, sh.ql[j][lane]);
+    }
+    const int col = lane & 15;
+    bias = (sh.bias[0][col] + sh.bias[1][col]) + (sh.bias[2][col] + sh.bias[3][col]);
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kD : kOutOfRange);
+    r.w[0] = bload4(rk, v, 0);
+    r.w[1] = bload4(rk, v + 16, 0);
+    r.w[2] = bload4(rk, v + 16 * kD, 0);
+    r.w[3] = bload4(rk, v + 16 * kD + 16, 0);
+  }
+  __device__ __forceinline__ static half8v codes8(uint32_t lo, uint32_t hi) {
+    return pack8(i8pair_exact(perm_b32(0u, lo, 0x0C010C00u)), i8pair_exact(perm_b32(0u, lo, 0x0C030C02u)),
+                 i8pair_exact(perm_b32(0u, hi, 0x0C010C00u)), i8pair_exact(perm_b32(0u, hi, 0x0C030C02u)));
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    (void)nc;
+    float4v c0 = {bias, bias, bias, bias};
+    float4v c1 = c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 w0 = r.w[j >> 1], w1 = r.w[2 + (j >> 1)];
+      const half8v a0 = codes8((j & 1) ? w0.z : w0.x, (j & 1) ? w0.w : w0.y);
+      const half8v a1 = codes8((j & 1) ? w1.z : w1.x, (j & 1) ? w1.w : w1.y);
+      c0 = mfma16x16x32(a0, qh[j], c0);
+      c1 = mfma16x16x32(a1, qh[j], c1);
+      c0 = mfma16x16x32(a0, ql[j], c0);
+      c1 = mfma16x16x32(a1, ql[j], c1);
+    }
+    x0 = c0;
+    x1 = c1;
+  }
+};
+
+// fp16 K in 256-byte token rows (a 16-bit K side): the logits are the fp32 dot products of
+// the stored fp16 k with q' = fp16(q * inv_tau).  Lane (row, lg) of row block rb reads bytes
+// [64 lg, 64 lg + 64) of token 16 rb + row: channels 32 lg + 8 j .. + 7 are slice j.
+struct KF16T {
+  static constexpr int kMergeBatch = 8;
+  static constexpr bool kPackPV = false;
+  using QInT = QIn;
+  static constexpr bool kAppend = false;
+  static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
+  static constexpr bool kRescue = false;     // (no INT4_SYM side)
+  static constexpr bool kAsym = false;
+  static constexpr bool kGsAny = false;
+  static constexpr bool kOut = false;
+  static constexpr bool kSub24 = false;
+  static constexpr int kRow = 2 * kD;
+  half8v qh[4];
+  rsrc_t rk;
+  uint32_t vk;
+  struct Raw {
+    u32x4 w[8];  // [4 rb + j]: slice j of token 16 rb + row
+  };
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kRow));
+    vk = (uint32_t)(col * kRow + 64 * lg);
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.s = (half_t)1.0f;
+    in.z = (half_t)0.0f;
+    in.oc = int4{-1, -1, -1, -1};
+  }
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    half_t vh[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      vh[e] = valid ? qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+  }
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kRow : kOutOfRange);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      r.w[j] = bload4(rk, v + 16 * j, 0);
+      r.w[4 + j] = bload4(rk, v + 16 * kRow + 16 * j, 0);
+    }
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    (void)nc;
+    float4v c0 = {0.f, 0.f, 0.f, 0.f};
+    float4v c1 = c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c0 = mfma16x16x32(__builtin_bit_cast(half8v, r.w[j]), qh[j], c0);
+      c1 = mfma16x16x32(__builtin_bit_cast(half8v, r.w[4 + j]), qh[j], c1);
+    }
+    x0 = c0;
+    x1 = c1;
+  }
+};
+
+// V of the 8-bit KIVI layout in 128-byte token rows, per-token fp32 s_t, z_t: lane (col, lg)
+// reads the 8 bytes of channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens T(k)
+// (as VI8RowT) and the tokens' s, z (as VKiviRowT).  The codes enter the MFMA exactly
+// (i8pair_exact), the B operand is w = p s_t as a hi + lo pair (two MFMAs per channel), and
+//   sum_t p v = sum_t w c + Cz,   Cz = sum_t p z_t (fp32, rescaled with l by the softmax).
+struct VKivi8RowT {
+  static constexpr bool kResidual = true;  // merges an fp16 residual window
+  static constexpr bool kPackedPV = false;
+  static constexpr bool kTile32 = false;
+  rsrc_t rv, rs, rz;
+  uint32_t vv, vp;
+  float ex[2];  // unused, Cz
+  struct Raw {
+    u32x2 w[8];          // token T(k): bytes 8 col .. 8 col + 7
+    float4v s[2], z[2];  // tokens 4 lg + i, 16 + 4 lg + i
+  };
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * kD));
+    vv = (uint32_t)((4 * lg) * kD + 8 * col);
+    const int64_t po = (int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh;
+    rs = buffer_rsrc(reinterpret_cast<const float*>(a.v.scale) + po, (uint32_t)(a.cap * 4));
+    rz = buffer_rsrc(reinterpret_cast<const float*>(a.v.zp) + po, (uint32_t)(a.cap * 4));
+    vp = (uint32_t)(4 * lg) * 4u;
+    ex[0] = ex[1] = 0.f;
+  }
+  __device__ __forceinline__ float* extra() { return ex; }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * kD : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      r.w[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(v + t * kD), 0, kBufNT));
+    }
+    const uint32_t p = vp + (valid ? (uint32_t)tok * 4u : kOutOfRange);
+    r.s[0] = __builtin_bit_cast(float4v, bload4(rs, p, 0));
+    r.s[1] = __builtin_bit_cast(float4v, bload4(rs, p + 64u, 0));
+    r.z[0] = __builtin_bit_cast(float4v, bload4(rz, p, 0));
+    r.z[1] = __builtin_bit_cast(float4v, bload4(rz, p + 64u, 0));
+  }
+  // tokens at or past the context in the last, partial tile: parameters 0
+  __device__ __forceinline__ void mask(Raw& r, int tt, int ctx, int lg) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (tt + 4 * lg + i >= ctx) r.s[0][i] = r.z[0][i] = 0.f;
+      if (tt + 16 + 4 * lg + i >= ctx) r.s[1][i] = r.z[1][i] = 0.f;
+    }
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v plo, float4v acc[8],
+                                      const NibConsts& nc) {
+    (void)nc;
+    float sk[8], wk[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sk[i] = r.s[0][i];
+      sk[4 + i] = r.s[1][i];
+      wk[i] = r.z[0][i];
+      wk[4 + i] = r.z[1][i];
+    }
+    float cz = ex[1];
+    uint32_t ph[4], pl[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float p0 = (float)pb[2 * q] + (float)plo[2 * q];
+      const float p1 = (float)pb[2 * q + 1] + (float)plo[2 * q + 1];
+      cz = fmaf(p0, wk[2 * q], cz);
+      cz = fmaf(p1, wk[2 * q + 1], cz);
+      half_t h0, l0, h1, l1;
+      split_h(p0 * sk[2 * q], h0, l0);
+      split_h(p1 * sk[2 * q + 1], h1, l1);
+      ph[q] = as_u32(half2v{h0, h1});
+      pl[q] = as_u32(half2v{l0, l1});
+    }
+    ex[1] = cz;
+    const half8v wh = pack8(ph[0], ph[1], ph[2], ph[3]);
+    const half8v wl = pack8(pl[0], pl[1], pl[2], pl[3]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      // byte c % 4 of the tokens T(2p) and T(2p + 1) into the low bytes of the two halves
+      const uint32_t sel = (uint32_t)(c & 3) | 0x0C00u | ((uint32_t)(4 + (c & 3)) << 16) | 0x0C000000u;
+      uint32_t R[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t lo = (c >> 2) ? r.w[2 * p].y : r.w[2 * p].x;
+        const uint32_t hi = (c >> 2) ? r.w[2 * p + 1].y : r.w[2 * p + 1].x;
+        R[p] = i8pair_exact(perm_b32(hi, lo, sel));
+      }
+      const half8v av = pack8(R[0], R[1], R[2], R[3]);
+      acc[c] = mfma16x16x32(av, wh, acc[c]);
+      acc[c] = mfma16x16x32(av, wl, acc[c]);
+    }
+  }
+  // acc[mb][r] += Cz, summed over the lane groups (the k-slots of a head)
+  __device__ __forceinline__ void finalize(float4v acc[8], int lane) {
+    (void)lane;
+    const float cz = wave_sum_xor_groups(ex[1]);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mb][r] += cz;
+  }
+};
+
+// fp16 V in 256-byte token rows (a 16-bit V side): lane (col, lg) reads the 16 bytes of
+// channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens; the A operand of channel
+// 8 col + c is the stored v of the 8 tokens (one v_perm_b32 per token pair), so acc / l is
+// the output.
+struct VF16RowT {
+  static constexpr bool kResidual = true;  // merges an fp16 residual window
+  static constexpr bool kPackedPV = false;
+  static constexpr bool kTile32 = false;
+  static constexpr int kRow = 2 * kD;
+  __device__ __forceinline__ void finalize(float4v*, int) const {}
+  __device__ __forceinline__ float* extra() { return nullptr; }
+  rsrc_t rv;
+  uint32_t vv;
+  struct Raw {
+    u32x4 w[8];  // token T(k): channels 8 col .. 8 col + 7
+  };
+  // tokens at or past the context in the last, partial tile read as 0: their probability is
+  // 0, but the memory may hold any fp16 bits, and 0 x inf or 0 x NaN would reach acc
+  __device__ __forceinline__ void mask(Raw& r, int tt, int ctx, int lg) const {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int t = tt + (k < 4 ? 4 * lg + k : 12 + 4 * lg + k);
+      if (t >= ctx) r.w[k] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * kRow));
+    vv = (uint32_t)((4 * lg) * kRow + 16 * col);
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * kRow : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      r.w[k] = bload4(rv, v + t * kRow, 0);
+    }
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
+                                      const NibConsts& nc) const {
+    (void)nc;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      // half c % 2 of dword c / 2 of the tokens T(2p), T(2p + 1) -> the two halves
+      const uint32_t b0 = 2u * (uint32_t)(c & 1);
+      const uint32_t sel = b0 | ((b0 + 1) << 8) | ((b0 + 4) << 16) | ((b0 + 5) << 24);
+      uint32_t R[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) R[p] = perm_b32(r.w[2 * p + 1][c >> 1], r.w[2 * p][c >> 1], sel);
+      const half8v av = pack8(R[0], R[1], R[2], R[3]);
+      acc[c] = mfma16x16x32(av, pb, acc[c]);
+      acc[c] = mfma16x16x32(av, pl, acc[c]);
+    }
+  }
+};
+
+// ---- Per-token scales: INT8 codes with fp16 scales or packed INT4-symmetric codes with fp32
+// scales per (b, kv head, token, group), in token rows (the reference's dynamic, adaptive and
+// group-rescue caches, src/cache/int8_cache.py:298-488, src/cache/int4_cache.py:298-590, read
+// by src/kernels/triton_decode_attn_int8.py:306-519 and triton_decode_attn_int4.py:62-121).
+// Both sides are dequantised as the reference's torch path does, k = fp16(c * fp16(s)), and
+// enter the MFMAs as fp16 values (the arithmetic of the row kernel's KTok / VTok).  A static
+// table given as a stride-0 view reads like per-token scales (every token one line).
+// NS = scales of a K lane's 32 channels: 1 for groups of 32 or more, 2 for groups of 16.
+// bytes of a (b, kv head)'s per-token scale rows: cap rows of stride sst elements, or one
+// row of 128 / gs groups for a stride-0 (static) view
+__device__ __forceinline__ uint32_t scale_bytes(int64_t cap, int64_t sst, int gs, int es) {
+  return (uint32_t)(sst > 0 ? cap * sst * es : (int64_t)(kD / gs) * es);
+}
+
+template <bool I4, int NS>
+struct KTokT {
+  static_assert(NS == 1 || NS == 2, "groups of 16 or more");
+  static constexpr int kMergeBatch = 16;
+  static constexpr bool kPackPV = false;
+  using QInT = QIn;
+  static constexpr bool kAppend = false;
+  // the writer runs quant_row_x (fused step); with INT4_SYM sides it also finds the group
+  // rescue's threshold over every row of the append (rescue_thr_wave)
+  static constexpr bool kAppendRow = true;
+  static constexpr bool kRescue = I4;
+  static constexpr bool kAsym = false;
+  static constexpr bool kGsAny = true;
+  static constexpr bool kOut = false;
+  static constexpr bool kSub24 = false;  // logits at unit scale
+  static constexpr int kRow = I4 ? kD / 2 : kD;  // code bytes per token
+  static constexpr int kEs = I4 ? 4 : 2;         // scale bytes (fp32 / fp16)
+  half8v qh[4];
+  rsrc_t rk, rs;
+  uint32_t vk, vs, sst;  // lane code offset, lane scale offset, scale bytes per token
+  struct Raw {
+    u32x4 w[I4 ? 2 : 4];  // I4: [rb] = bytes [16 lg, 16 lg + 16) of token 16 rb + row;
+                          // INT8: [2 rb + i] = bytes [32 lg + 16 i, + 16)
+    uint32_t s[2];        // the NS scales of row block rb (fp16 pair, fp16 or fp32 bits)
+    uint32_t s2[I4 && NS == 2 ? 2 : 1];  // the second fp32 scale of row block rb (NS = 2)
+  };
+
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    rk = buffer_rsrc(kb, (uint32_t)(a.cap * kRow));
+    vk = (uint32_t)(col * kRow + (kRow / 4) * lg);
+    // the lane's first group: 32 lg / gs; with NS = 2 the next one follows (stride_g = 1)
+    const int g0 = (32 * lg) >> __builtin_ctz((unsigned)a.gs);
+    const char* sb = reinterpret_cast<const char*>(a.k.scale) +
+                     ((int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh) * kEs;
+    sst = (uint32_t)(a.k.sst * kEs);
+    rs = buffer_rsrc(sb, scale_bytes(a.cap, a.k.sst, a.gs, kEs));
+    vs = (uint32_t)(col * sst + g0 * a.k.ssg * kEs);
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.s = (half_t)1.0f;
+    in.z = (half_t)0.0f;
+    in.oc = int4{-1, -1, -1, -1};
+  }
+  // channel slice j of the q operand q' = fp16(q * inv_tau), in the k-slot order of the
+  // codes (INT4: unpack_dword_64pn's), shared through LDS
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    half_t vh[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int el = I4 ? kNibSlotElem(e) : e;
+      const half2v h2 = as_h2(qw[el >> 1]);
+      vh[e] = valid ? qscale((el & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+  }
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+  }
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kRow : kOutOfRange);
+    if constexpr (I4) {
+      r.w[0] = bload4(rk, v, 0);
+      r.w[1] = bload4(rk, v + 16 * kRow, 0);
+    } else {
+      r.w[0] = bload4(rk, v, 0);
+      r.w[1] = bload4(rk, v + 16, 0);
+      r.w[2] = bload4(rk, v + 16 * kRow, 0);
+      r.w[3] = bload4(rk, v + 16 * kRow + 16, 0);
+    }
+    const uint32_t p = vs + (valid ? (uint32_t)tok * sst : kOutOfRange);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const uint32_t o = p + (uint32_t)rb * 16u * sst;
+      if constexpr (I4 && NS == 2) {
+        const u32x2 s = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, (int)o, 0, kBufNT));
+        r.s[rb] = s.x;
+        r.s2[rb] = s.y;
+      } else if constexpr (I4 || NS == 2) {
+        r.s[rb] = bload1(rs, o, 0);  // one fp32, or two fp16
+      } else {
+        r.s[rb] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)o, 0, kBufNT);
+      }
+    }
+  }
+  // the fp16 scale of slice j in row block rb, twice
+  __device__ __forceinline__ uint32_t scale2(const Raw& r, int rb, int j) const {
+    half_t s;
+    if constexpr (I4) {
+      const uint32_t bits = (NS == 2 && j >= 2) ? r.s2[rb] : r.s[rb];
+      s = (half_t)__builtin_bit_cast(float, bits);
+    } else {
+      const half2v h = as_h2(r.s[rb]);
+      s = (NS == 2 && j >= 2) ? h.y : h.x;
+    }
+    return splat_h2(s);
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    float4v c[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t s2 = scale2(r, rb, j);
+        uint32_t u[4];
+        if constexpr (I4) {
+          const u32x4 w = r.w[rb];
+          const uint32_t d = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+          unpack_dword_64pn(d, nc, u);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) u[i] = deq_pair(u[i], (half_t)72.0f, s2);
+        } else {
+          const u32x4 w = r.w[2 * rb + (j >> 1)];
+          const uint32_t lo = (j & 1) ? w.z : w.x, hi = (j & 1) ? w.w : w.y;
+          u[0] = i8pair_deq(perm_b32(0u, lo, 0x0C010C00u), as_h2(s2));
+          u[1] = i8pair_deq(perm_b32(0u, lo, 0x0C030C02u), as_h2(s2));
+          u[2] = i8pair_deq(perm_b32(0u, hi, 0x0C010C00u), as_h2(s2));
+          u[3] = i8pair_deq(perm_b32(0u, hi, 0x0C030C02u), as_h2(s2));
+        }
+        c[rb] = mfma16x16x32(pack8(u[0], u[1], u[2], u[3]), qh[j], c[rb]);
+      }
+    }
+    x0 = c[0];
+    x1 = c[1];
+  }
+};
+
+// V with per-token scales in token rows: lane (col, lg) reads channels 8 col .. 8 col + 7
+// (8 INT8 bytes or 4 packed INT4 bytes) of its 8 PV k-slot tokens T(k) = 4 lg + k (k < 4),
+// 16 + 4 lg + k - 4, and the scale of their group (8 col) / gs.  The A operand of MFMA c
+// (channel 8 col + c) is vhat = fp16(c * fp16(s)) of the 8 tokens, so acc / l is the output.
+template <bool I4>
+struct VTokT {
+  static constexpr bool kResidual = false;  // merges an fp16 residual window
+  static constexpr bool kPackedPV = false;
+  static constexpr bool kTile32 = false;
+  static constexpr int kRow = I4 ? kD / 2 : kD;
+  static constexpr int kEs = I4 ? 4 : 2;
+  __device__ __forceinline__ void finalize(float4v*, int) const {}
+  __device__ __forceinline__ float* extra() { return nullptr; }
+  rsrc_t rv, rs;
+  uint32_t vv, vs, sst;
+  struct Raw {
+    uint32_t w[8][I4 ? 1 : 2];  // token T(k)
+    uint32_t s[8];              // token T(k)'s scale (fp32 or fp16 bits)
+  };
+  __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
+    (void)a; (void)hkv; (void)lane;
+    s = 1.f;
+    z = 0.f;
+  }
+  __device__ static half2v epilogue(float r0, float r1, float s, float z) {
+    (void)s; (void)z;
+    return half2v{(half_t)r0, (half_t)r1};
+  }
+  __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    rv = buffer_rsrc(vb, (uint32_t)(a.cap * kRow));
+    vv = (uint32_t)((4 * lg) * kRow + (I4 ? 4 : 8) * col);
+    const int gi = (8 * col) >> __builtin_ctz((unsigned)a.gs);
+    const char* sb = reinterpret_cast<const char*>(a.v.scale) +
+                     ((int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh) * kEs;
+    sst = (uint32_t)(a.v.sst * kEs);
+    rs = buffer_rsrc(sb, scale_bytes(a.cap, a.v.sst, a.gs, kEs));
+    vs = (uint32_t)((4 * lg) * sst + gi * a.v.ssg * kEs);
+  }
+  // rows of a partial last tile past the capacity read 0; !valid: every load out of range
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vv + (valid ? (uint32_t)tok * kRow : kOutOfRange);
+    const uint32_t p = vs + (valid ? (uint32_t)tok * sst : kOutOfRange);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+      if constexpr (I4) {
+        r.w[k][0] = bload1(rv, v + t * kRow, 0);
+        r.s[k] = bload1(rs, p + t * sst, 0);
+      } else {
+        const u32x2 x = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(v + t * kRow), 0, kBufNT));
+        r.w[k][0] = x.x;
+        r.w[k][1] = x.y;
+        r.s[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(p + t * sst), 0, kBufNT);
+      }
+    }
+  }
+  // tokens at or past the context in the last, partial tile: scale 0 (their memory may
+  // hold anything; p is 0 there)
+  __device__ __forceinline__ void mask(Raw& r, int tt, int ctx, int lg) const {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int t = tt + 4 * lg + ((k < 4) ? k : 12 + k);
+      if (t >= ctx) r.s[k] = 0u;
+    }
+  }
+  __device__ __forceinline__ uint32_t spair(const Raw& r, int p) const {
+    if constexpr (I4)
+      return pair_h2((half_t)__builtin_bit_cast(float, r.s[2 * p]),
+                     (half_t)__builtin_bit_cast(float, r.s[2 * p + 1]));
+    else
+      return (r.s[2 * p] & 0xFFFFu) | (r.s[2 * p + 1] << 16);
+  }
+  __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
+                                      const NibConsts& nc) const {
+    uint32_t sp[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) sp[p] = spair(r, p);
+    if constexpr (I4) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        // byte k of the tokens T(2p), T(2p + 1) into the low bytes of the two halves
+        const uint32_t sel = (uint32_t)k | 0x0C00u | ((uint32_t)(4 + k) << 16) | 0x0C000000u;
+        uint32_t h[4], o[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t R = perm_b32(r.w[2 * p + 1][0], r.w[2 * p][0], sel);
+          h[p] = deq_pair(and_or(R, nc.m_hi, nc.c64), (half_t)72.0f, sp[p]);
+          o[p] = deq_pair(and_or(R, nc.m_lo, nc.c1024), (half_t)1032.0f, sp[p]);
+        }
+        const half8v ah = pack8(h[0], h[1], h[2], h[3]), ao = pack8(o[0], o[1], o[2], o[3]);
+        acc[2 * k] = mfma16x16x32(ah, pb, acc[2 * k]);
+        acc[2 * k + 1] = mfma16x16x32(ao, pb, acc[2 * k + 1]);
+        acc[2 * k] = mfma16x16x32(ah, pl, acc[2 * k]);
+        acc[2 * k + 1] = mfma16x16x32(ao, pl, acc[2 * k + 1]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t sel = (uint32_t)(c & 3) | 0x0C00u | ((uint32_t)(4 + (c & 3)) << 16) | 0x0C000000u;
+        uint32_t R[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          R[p] = i8pair_deq(perm_b32(r.w[2 * p + 1][c >> 2], r.w[2 * p][c >> 2], sel), as_h2(sp[p]));
+        const half8v av = pack8(R[0], R[1], R[2], R[3]);
+        acc[c] = mfma16x16x32(av, pb, acc[c]);
+        acc[c] = mfma16x16x32(av, pl, acc[c]);
+      }
+    }
+  }
+};
+
+// Fused quantize-on-append of the new token of (b, kv head): one wave (the writer), two
+// values per lane, the arithmetic of the append kernel: asym_pack_pair with the decode's
+// static tables for INT4_ASYM, int8_pack_pair with the append's static table for INT8.  K
+// goes to row wpos (INT4_ASYM: its outlier channels verbatim to the side-band), V to its
+// TILE32 bytes or its row.  The other waves issue nothing for it (even out-of-range memory
+// operations would occupy their address unit ahead of their first cache loads).  NaN / Inf
+// set status[0] and clamped elements are added to status[1] (per side).
+struct AppendIn {
+  uint32_t k2, v2;  // fp16 pair of channels 2 lane, 2 lane + 1
+  uint32_t o;       // lanes < 4: fp16 K value of outlier channel lane (INT4_ASYM K)
+  float ks;         // INT8 K: the fp16 scale of the group of channels 2 lane, 2 lane + 1
+  float vs, vz;     // V: INT8 fp16 scale of that group, or INT4_ASYM scale / zero-point of
+                    // group lane / 16
+};
+struct AppendFlags {
+  bool kbad = false, vbad = false;
+  int kclip = 0, vclip = 0;
+};
+
+// fp16 scale of group g of the append's static INT8 table tab (fp32 when f32)
+__device__ __forceinline__ float app_int8_scale(const void* tab, int f32, int64_t sh, int64_t sg,
+                                                int hkv, int g) {
+  const int64_t i = (int64_t)hkv * sh + (int64_t)g * sg;
+  const float s = f32 ? reinterpret_cast<const float*>(tab)[i] : (float)reinterpret_cast<const half_t*>(tab)[i];
+  return (float)int8_static_scale16(s, f32 != 0);
+}
+
+// oc: the kv head's 4 outlier channels (from the q set-up's inputs); called by the writer
+template <class KF, class VF>
+__device__ __forceinline__ void append_fetch(const DecodeArgs& a, int b, int hkv, int lane,
+                                             int4 oc, AppendIn& in) {
+  const FusedAppend& f = a.app;
+  const half_t* xk = f.kx + (int64_t)b * f.ksb + (int64_t)hkv * f.ksh;
+  const half_t* xv = f.vx + (int64_t)b * f.vsb + (int64_t)hkv * f.vsh;
+  const rsrc_t rk = buffer_rsrc(xk, kD * 2), rv = buffer_rsrc(xv, kD * 2);
+  in.k2 = bload1(rk, 4u * lane, 0);
+  in.v2 = bload1(rv, 4u * lane, 0);
+  in.o = 0;
+  if constexpr (KF::kOut) {
+    const int ch = lane == 0 ? oc.x : lane == 1 ? oc.y : lane == 2 ? oc.z : oc.w;
+    in.o = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+        rk, (int)(lane < 4 ? 2u * (uint32_t)ch : kOutOfRange), 0, kBufNT);
+  }
+  const int g = lane >> 4;  // group of 32
+  int g8 = g;               // INT8 sides: the group of channels 2 lane, 2 lane + 1
+  if constexpr (KF::kGsAny) g8 = (2 * lane) >> __builtin_ctz((unsigned)a.gs);
+  in.ks = 0.f;
+  if constexpr (!KF::kAsym) in.ks = app_int8_scale(f.kst, f.kst_f32, f.kst_sh, f.kst_sg, hkv, g8);
+  if constexpr (VF::kTile32) {
+    // V scale / zero-point of group lane / 16 (fp16, element offsets hkv * ssh + g * ssg)
+    in.vs = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
+    in.vz = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
+  } else {
+    in.vs = app_int8_scale(f.vst, f.vst_f32, f.vst_sh, f.vst_sg, hkv, g8);
+    in.vz = 0.f;
+  }
+}
+
+// ks / kz: the INT4_ASYM K scale / zero-point of group lane / 16 (the q set-up reads the same)
+template <class KF, class VF>
+__device__ __forceinline__ void append_store(const DecodeArgs& a, const KF& kf, const VF& vf,
+                                             int lane, const AppendIn& in, float ks, float kz,
+                                             AppendFlags& fl) {
+  const int64_t t = a.app.wpos;
+  const half2v k2 = as_h2(in.k2), v2 = as_h2(in.v2);
+  int kclip = 0, vclip = 0;
+  if constexpr (KF::kAsym) {
+    const uint32_t kb = asym_pack_pair((float)k2.x, (float)k2.y, ks, kz, kclip);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)kb, kf.rk, (int)(uint32_t)(t * kRowK + lane), 0, 0);
+  } else {
+    const uint16_t kp = int8_pack_pair((float)k2.x, (float)k2.y, (half_t)in.ks, kclip);
+    __builtin_amdgcn_raw_buffer_store_b16(kp, kf.rk, (int)(uint32_t)(t * kD + 2 * lane), 0, 0);
+  }
+  if constexpr (VF::kTile32) {
+    const uint32_t vb = asym_pack_pair((float)v2.x, (float)v2.y, in.vs, in.vz, vclip);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)vb, vf.rv, (int)(uint32_t)tile32_offset(t, lane), 0, 0);
+  } else {
+    const uint16_t vp = int8_pack_pair((float)v2.x, (float)v2.y, (half_t)in.vs, vclip);
+    __builtin_amdgcn_raw_buffer_store_b16(vp, vf.rv, (int)(uint32_t)(t * kD + 2 * lane), 0, 0);
+  }
+  if constexpr (KF::kOut)
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)in.o, kf.ro,
+                                          (int)(lane < 4 ? (uint32_t)(t * kRowO + 2 * lane) : kOutOfRange), 0, 0);
+  fl.kbad |= __ballot(!(__builtin_isfinite((float)k2.x) && __builtin_isfinite((float)k2.y))) != 0;
+  fl.vbad |= __ballot(!(__builtin_isfinite((float)v2.x) && __builtin_isfinite((float)v2.y))) != 0;
+  fl.kclip += wave_sum_int(kclip);
+  fl.vclip += wave_sum_int(vclip);
+}
+
+// The fused append of the row formats: the writer quantises the (b, kv head) row of each
+// side of the one-token append exactly as kvq_quant_append's kernel does (quant_row_x on
+// row b * H + h), codes, per-token scales and status words included.  An INT4 side with the
+// group rescue first finds its threshold over every row of the append on its own
+// (rescue_thr_wave: the host admits only thresholds within the walk's reach of the top).
+__device__ __forceinline__ bool rescue_side(const AppendDev& d) {
+  return d.fmt == KVQ_FMT_INT4_SYM && d.st != nullptr && d.rq > 0.f && !d.rescue_all;
+}
+// The writer's inputs, requested at the start of the kernel (under the streaming that
+// follows, a load issued at the store would wait a loaded round trip): its own new rows and
+// their static scales, and with the group rescue every new row of the append.
+struct RowPre {
+  half2v k, v;
+  float sk, sv;
+};
+__device__ __forceinline__ void append_row_fetch(const DecodeArgs& a, int b, int hkv, int lane,
+                                                 RowPre& p) {
+  const int row = b * a.ark.H + hkv;
+  p.k = load_x(a.ark, row, lane);
+  p.sk = row_static(a.ark, row, lane);
+  p.v = load_x(a.arv, row, lane);
+  p.sv = row_static(a.arv, row, lane);
+}
+// (the rescue is compiled only where it can occur: INT4_SYM K and V, RESCUE)
+template <bool RESCUE>
+__device__ __forceinline__ void append_row_pair(const DecodeArgs& a, int b, int hkv, int lane,
+                                                const RowPre& p, const RescueRows& rk,
+                                                const RescueRows& rv) {
+  const int row = b * a.ark.H + hkv;
+  float tk = 0.f, tv = 0.f;
+  if constexpr (RESCUE) {
+    __shared__ float rdyn[kRescueRows * 8];  // the writer's scales (one writer per work-group)
+    if (rescue_side(a.ark)) tk = rescue_thr_rows(a.ark, lane, rk, rdyn);
+    quant_row_x(a.ark, row, lane, tk, p.k, p.sk);
+    if (rescue_side(a.arv)) tv = rescue_thr_rows(a.arv, lane, rv, rdyn);
+  } else {
+    quant_row_x(a.ark, row, lane, tk, p.k, p.sk);
+  }
+  quant_row_x(a.arv, row, lane, tv, p.v, p.sv);
+}
+
+__device__ __forceinline__ void append_status(const FusedAppend& f, const AppendFlags& fl) {
+  if (f.kstatus) {
+    if (fl.kbad) atomicOr(&f.kstatus[0], 1);
+    if (fl.kclip) atomicAdd(&f.kstatus[1], fl.kclip);
+  }
+  if (f.vstatus) {
+    if (fl.vbad) atomicOr(&f.vstatus[0], 1);
+    if (fl.vclip) atomicAdd(&f.vstatus[1], fl.vclip);
+  }
+}
+
+// One-dimensional split per kv head (a.share).  Rows of equal context length: row b takes
+// work-groups [b u, (b + 1) u) as the chunks of the uniform split (u = a.u_chunks).  A
+// ragged batch: C = a.share_c work-groups are shared out over the rows by context length.
+// Row b (t_b tiles) gets c_b = min(ceil(t_b / T), ceil(t_b / kTW), kUnitChunks) of them, or
+// one if it is empty (that one writes its zero output), with T the first of
+// ceil(total / C), ceil(total / (C - 1)), .. for which the shares fit C (C >= the row
+// count, so T = total always fits).  Work-group g of the kv head takes chunk g - start_b of
+// the row whose range [start_b, start_b + c_b) holds g; n = 0: past every row's share.  Every wave
+// of every work-group computes the same shares (lane b handles row b), so the assignment
+// is fixed by the context lengths alone.
+struct RowShare {
+  int hkv, b, chunk, n;
+  int64_t ctx;  // row b's context length (clamped to the capacity)
+};
+__device__ __forceinline__ int ceil_div_pos(int x, int y) {  // x >= 0, y >= 1, x < 2^24
+  int q = (int)((float)x / (float)y);
+  q += q * y < x;
+  q -= q > 0 && (q - 1) * y >= x;
+  return q;
+}
+// lin: the work-group's index over the whole grid (x fastest); the work-groups that do work
+// come first in it, so they are the first dispatched.
+__device__ RowShare share_rows(const DecodeArgs& a, int lin) {
+  const int lane = threadIdx.x & 63;
+  const bool row = lane < a.B;
+  const int len = row ? (int)row_context(a, lane) : 0;
+  const int t = (len + kTile - 1) / kTile;
+  RowShare rs{0, 0, 0, 0, 0};
+  const int t0 = __builtin_amdgcn_readlane(t, 0);
+  if (__ballot(row && t != t0) == 0) {  // equal lengths: the uniform split
+    const int per_head = a.u_chunks * a.B;
+    if (lin < per_head * a.Hkv) {
+      rs.hkv = lin / per_head;
+      const int g = lin - rs.hkv * per_head;
+      rs.b = g / a.u_chunks;
+      rs.chunk = g - rs.b * a.u_chunks;
+      rs.n = a.u_chunks;
+      rs.ctx = __builtin_amdgcn_readlane(len, rs.b);
+    }
+    return rs;
+  }
+  const int C = a.share_c;
+  if (lin >= C * a.Hkv) return rs;
+  rs.hkv = lin / C;
+  const int g = lin - rs.hkv * C;
+  const int cap = t == 0 ? (row ? 1 : 0) : min(ceil_div_pos(t, kTW), kUnitChunks);
+  const int total = (int)wave_sum64((float)t);
+  int c = cap;
+  for (int k = 0; k < C; ++k) {
+    const int T = total > 0 ? max(1, (total + (C - k) - 1) / (C - k)) : 1;
+    c = t == 0 ? cap : min(ceil_div_pos(t, T), cap);
+    if ((int)wave_sum64((float)c) <= C) break;
+  }
+  int start = 0;
+  for (int r = 0; r < a.B; ++r) {
+    const int cr = __builtin_amdgcn_readlane(c, r);
+    if (g < start + cr) {
+      rs.b = r;
+      rs.chunk = g - start;
+      rs.n = cr;
+      rs.ctx = __builtin_amdgcn_readlane(len, r);
+      break;
+    }
+    start += cr;
+  }
+  return rs;
+}
+
+template <class KF, class VF, int LOOK, bool PACK8, int WPE = 2>
+__global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+void decode_tiled_kernel(DecodeArgs a) {
+  // One field of each kernel-argument line the prologue reads, so that the first batch of
+  // scalar loads fetches every such line (a line first touched later costs one more
+  // round trip before the first cache load; measured 0.15-0.25 us per launch).
+  asm volatile("" ::"s"(a.v.scale), "s"(a.ctx), "s"(a.app.kx), "s"(a.app.wpos));
+  constexpr bool APP = KF::kAppend || KF::kAppendRow;  // a fused append (the writer's code) is built
+  constexpr bool OUT = KF::kOut;
+  int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z, n_ch = a.n_chunks;  // n_ch: the row's chunks
+  int64_t share_ctx = 0;
+  if (a.share) {
+    const RowShare rs = share_rows(a, (int)(blockIdx.y * gridDim.x + blockIdx.x));
+    if (rs.n == 0) return;  // past every row's share (uniform over the work-group)
+    hkv = __builtin_amdgcn_readfirstlane(rs.hkv);
+    b = __builtin_amdgcn_readfirstlane(rs.b);
+    chunk = __builtin_amdgcn_readfirstlane(rs.chunk);
+    n_ch = __builtin_amdgcn_readfirstlane(rs.n);
+    share_ctx = __builtin_amdgcn_readfirstlane((int)rs.ctx);
+  }
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, lg = lane >> 4;
+
+  // Fused quantize-on-append.  The writer is the wave whose schedule (below) holds the new
+  // token's tile wt: its stores precede, in program order, its loads of that tile.  They
+  // are issued after the set-up, when the new rows (requested with q) have arrived, or
+  // before the first cache loads when wt is one of the wave's first LOOK + 1 tiles.  A
+  // writer whose work-group has no tile of the context stores before it leaves.
+  const bool app_on = APP && a.app.kx != nullptr;
+  const int stride_all = n_ch * kTW;
+  const int wt = app_on ? (int)(a.app.wpos / kTile) : 0;
+  const bool writer = app_on && chunk * kTW + wave == wt % stride_all;
+  AppendIn ain;
+  AppendFlags afl;
+  [[maybe_unused]] RowPre rpre;
+  [[maybe_unused]] RescueRows rxk, rxv;
+
+  __shared__ QShareLds qsh;
+  __shared__ TiledMergeLds msh;
+  // Waves w and w + 4 share a SIMD, which issues the older of two ready waves first;
+  // each publishes its step count and, when ahead of its partner, lowers its priority,
+  // so the two stay in step (the tile schedule, and so every result bit, is fixed).
+  __shared__ int progress[kTW];
+  progress[wave] = 0;
+  KF kf;
+  // the q-side inputs are requested first: the wait for them then does not include the
+  // cache tiles requested next
+  typename KF::QInT qin;
+  kf.fetch_q(a, b, hkv, lane, wave, qin);
+  if constexpr (KF::kAppendRow) {
+    if (writer) {
+      append_row_fetch(a, b, hkv, lane, rpre);
+      if constexpr (KF::kRescue)
+        if (rescue_side(a.ark) || rescue_side(a.arv)) {
+          rescue_fetch(a.ark, lane, rxk);
+          rescue_fetch(a.arv, lane, rxv);
+        }
+    }
+  }
+  kf.setup_addr(a, b, hkv, lane);
+  VF vf;
+  vf.setup(a, b, hkv, lane);
+  // the fused append's two steps (compiled only for the format that has it)
+  auto app_fetch = [&]() {
+    if constexpr (KF::kAppend) append_fetch<KF, VF>(a, b, hkv, lane, qin.oc, ain);
+  };
+  auto app_store = [&]() {
+    if constexpr (KF::kAppend) append_store(a, kf, vf, lane, ain, (float)qin.s, (float)qin.z, afl);
+    else if constexpr (KF::kAppendRow) append_row_pair<KF::kRescue>(a, b, hkv, lane, rpre, rxk, rxv);
+  };
+
+  // Tile schedule: the n_ch work-groups of a (b, kv head) interleave, so at step i the
+  // waves of all of them read one contiguous run of n_ch * kTW tiles and the device
+  // streams each slab front to back.  Wave w of work-group c takes tiles c * kTW + w +
+  // i * stride (tile = 32 tokens; only the context's last tile, ntot - 1, may be partial).
+  // The schedule is static, so results do not depend on timing.
+  const int first = chunk * kTW + wave;
+  const int stride = n_ch * kTW;
+  // tile[j] = tile of step i + j (j <= LOOK + 1)
+  int tile[LOOK + 2];
+#pragma unroll
+  for (int j = 0; j <= LOOK; ++j) tile[j] = first + j * stride;
+  constexpr int R = LOOK + 1;                 // ring slots per stream
+  constexpr int U = (R % 2 == 0) ? R : 2 * R;  // unroll: ring slot and x buffer are static
+  typename KF::Raw kr[R];
+  typename VF::Raw vr[R];
+  // The context length is read here, ahead of every cache load: before the barrier below
+  // the compiler reads it through the scalar cache, whose wait does not include the cache
+  // tiles (after it, a vector load whose vmcnt wait also waited for the first tiles cost
+  // about 0.5 us per launch).  The K and V tiles of step 0 are then requested before the q
+  // set-up (bounded by the capacity; tiles past the context are never used), so the memory
+  // system is busy from the start of the kernel; the rest of the ring (K of steps 1..LOOK,
+  // V of steps 1..LOOK-1) after the set-up.  A larger first burst delays the q loads
+  // queued with it, and the set-up waits for those (measured: the whole ring up front
+  // costs about 0.4 us per launch at the headline shape; warming loads of the next tiles
+  // during the set-up cost 1.4 us).  Every ring load is issued unconditionally (out of
+  // range for a tile past the bound): conditional loads would make the compiler's vmcnt
+  // waits conservative at the joins, i.e. wait for the tiles just requested.
+  // (the shared split has every row's length already)
+  const int64_t ctx64 = a.share ? share_ctx : row_context(a, b);
+  asm volatile("" ::: "memory");
+  const bool early_write = writer && wt / stride_all <= LOOK;
+  if (early_write) {
+    app_fetch();
+    app_store();
+  }
+  const int ncap = (a.cap + kTile - 1) / kTile;
+  kf.load(kTile * tile[0], tile[0] < ncap, kr[0]);
+  vf.load(kTile * tile[0], tile[0] < ncap, vr[0]);
+
+  const int ctx = (int)ctx64;
+  const int ntot = (ctx + kTile - 1) / kTile;
+  const bool partial = (ctx & (kTile - 1)) != 0;
+  if (ntot == 0 || chunk * kTW >= ntot) {  // no tile for this work-group (uniform)
+    if (writer) {
+      if (!early_write) {
+        app_fetch();
+        app_store();
+      }
+      if (lane == 0) append_status(a.app, afl);
+    }
+    if (ntot == 0 && chunk == 0 && a.fused) {
+      if (VF::kResidual && a.res_n > 0) {  // empty quantized context: the residual window alone
+        merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, 0, wave, lane);
+      } else {  // empty context: zero rows
+        for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
+          a.out[(int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + (idx >> 7)) * a.o_sh +
+                (idx & (kD - 1))] = (half_t)0.0f;
+      }
+    }
+    return;
+  }
+  // The writer fetches the new rows now and stores their codes in the loop, at the last
+  // step that precedes its loads of tile wt (step wt_step - LOOK - 1), or right after the
+  // set-up when wt lies past the wave's tiles.
+  const bool late_write = writer && !early_write;
+  const int wt_step = (wt - (chunk * kTW + wave)) / stride_all;
+  const int store_step = late_write ? wt_step - LOOK - 1 : -1;
+  if (late_write) app_fetch();
+  if (wave < 4) kf.setup_q(a, qin, lane, wave, qsh);  // waves 4..7 would build the same
+  NibConsts nc;
+  nc.init();
+  __syncthreads();
+#pragma unroll
+  for (int s = 1; s <= LOOK; ++s) {
+    kf.load(kTile * tile[s], tile[s] < ntot, kr[s]);
+    if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ntot, vr[s]);
+  }
+  kf.finish_setup(qsh, qin, lane);
+  // (wt past the context: the wave may have fewer steps than store_step; the row formats'
+  // writer always stores here, outside the loop)
+  const bool store_now = late_write && (KF::kAppendRow || wt >= ntot || store_step <= 0);
+  if (store_now) app_store();
+
+  float4v acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
+  float m = kNegInf, l = 0.f;
+  const float sm = KF::kSub24 ? a.sm_log2e * kTwo24 : a.sm_log2e;  // logits of KAsymT: x 2^-24
+  int steps = 0;
+  if (tile[0] < ntot) {
+    float4v x[2][2];
+    kf.qk(kr[0], nc, x[0][0], x[0][1]);
+    while (tile[0] < ntot) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        // step i (i % U == u): the tiles of this wave form a prefix of its schedule
+        if (tile[0] >= ntot) break;
+        if constexpr (!KF::kAppendRow)
+          if (late_write && !store_now && steps == store_step) app_store();
+        tile[LOOK + 1] = tile[LOOK] + stride;
+        // fetch K of step i + LOOK + 1 (into the slot K of step i used) and V of step
+        // i + LOOK (into the slot V of step i - 1 used), QK of step i + 1, then softmax
+        // and PV of step i
+        kf.load(kTile * tile[LOOK + 1], tile[LOOK + 1] < ntot, kr[u % R]);
+        vf.load(kTile * tile[LOOK], tile[LOOK] < ntot, vr[(u + LOOK) % R]);
+        if (tile[1] < ntot) kf.qk(kr[(u + 1) % R], nc, x[(u + 1) & 1][0], x[(u + 1) & 1][1]);
+        float4v x0 = x[u & 1][0], x1 = x[u & 1][1];
+        if (partial && tile[0] == ntot - 1) {
+          mask_tile(x0, x1, kTile * tile[0], ctx, lg);
+          vf.mask(vr[u % R], kTile * tile[0], ctx, lg);
+        }
+        if constexpr (PACK8 && KF::kPackPV && VF::kPackedPV) {
+          half8v pc;
+          softmax_tile8c(x0, x1, sm, m, l, acc, pc, col < 8);
+          vf.mma1(vr[u % R], pc, acc, nc);
+        } else {
+          half8v pb, pl;
+          if constexpr (PACK8) softmax_tile8(x0, x1, sm, m, l, acc, pb, pl, vf.extra());
+          else softmax_tile(x0, x1, sm, m, l, acc, pb, pl, vf.extra());
+          vf.mma(vr[u % R], pb, pl, acc, nc);
+        }
+        ++steps;
+        progress[wave] = steps;
+        if (__builtin_amdgcn_readfirstlane(progress[wave ^ 4]) < steps)
+          __builtin_amdgcn_s_setprio(0);
+        else
+          __builtin_amdgcn_s_setprio(2);
+#pragma unroll
+        for (int j = 0; j <= LOOK; ++j) tile[j] = tile[j + 1];
+      }
+    }
+  }
+  __builtin_amdgcn_s_setprio(0);
+  if constexpr (PACK8 && KF::kPackPV && VF::kPackedPV) fold_lo(acc);
+  if (writer && lane == 0) append_status(a.app, afl);
+
+  // Merge.  The waves' states are merged in LDS and the work-group's partial is stored
+  // write-through (combine_kernel merges them when a.fused == 0).  Once every store of the
+  // work-group has completed, one thread counts it in (word 0 of the (b, kv head)'s
+  // counter slot); the last of the (b, kv head)'s work-groups merges every partial, writes
+  // the output and resets the counter.
+  const int nvalid = min(n_ch, (ntot + kTW - 1) / kTW);  // chunks holding a tile
+  uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
+  __shared__ int is_last;
+  vf.finalize(acc, lane);
+  merge_store_partial<PACK8>(a, msh, wave, lane, m, l, acc, b, hkv, chunk);
+  if (!a.fused) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nvalid - 1);
+  __syncthreads();
+  if (!is_last) return;
+  merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, nvalid, wave, lane);
+  if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class KF, class VF, bool PACK8>
+const void* tiled_ptr() {
+  return reinterpret_cast<const void*>(&decode_tiled_kernel<KF, VF, 1, PACK8>);
+}
+// the kernels for n_rep <= 8 (pack8) pack the second row block's softmax into the padding
+// lanes
+template <class KF, class VF>
+const void* tiled_pick(bool pack8) {
+  return pack8 ? tiled_ptr<KF, VF, true>() : tiled_ptr<KF, VF, false>();
+}
+
+}  // namespace
+}  // namespace kvq
