@@ -21,7 +21,11 @@ Where the layout differs from the reference:
   ``.to(torch.float16)`` is therefore free.
 * Host synchronisation is optional.  With ``check_numerics=True`` (the default)
   ``append`` reads a device status word back, like the reference's
-  NaN/Inf/clip checks, and raises/warns the same way.  With
+  NaN/Inf/clip checks, and raises/warns the same way.  The decode step
+  (``append_decode_attn``) reads the status words of all layers once per step,
+  after the step's last layer, instead of once per layer: a NaN / Inf then raises
+  ValueError there and every layer of the step goes back to its length before the
+  step, so the cache does not advance (``flush_status`` reads them earlier).  With
   ``check_numerics=False`` nothing synchronises.  :class:`KIVIStyleKVCache` reads it
   at prefill only, and on the decode steps its frozen-K range check selects
   (``KV_OOR_CHECK_INTERVAL``, off by default as in the reference).
@@ -108,6 +112,10 @@ class _EngineBase:
         self._seq_len = 0
         self.decode_stats: Dict[str, object] = _new_decode_stats()
         self._status: Optional[Tensor] = None
+        # the decode step's per-layer status rows and the appends not read yet
+        self._step_status: Optional[Tensor] = None
+        self._step_pending: List[tuple] = []
+        self._step_seq_len0 = 0
         # per layer: the LayerStep over the layer's buffers and the fused append's parameter
         # blocks, rebuilt when the buffers are reallocated
         self._steps: List[Optional[object]] = [None] * num_layers
@@ -189,6 +197,68 @@ class _EngineBase:
             self._status = torch.zeros(4, dtype=torch.int32, device=device)
         return self._status
 
+    # -- the decode step's status words, read once per step.  ``append`` checks its input
+    # as the reference does, with one host read per call; the decode step
+    # (``append_decode_attn``) instead writes each layer's status words to a row of a
+    # [num_layers, 4] device buffer and reads the whole buffer once, after the step's last
+    # layer (layer num_layers - 1) or before a layer is appended a second time.  A NaN / Inf
+    # then raises ValueError and every layer appended since the previous read goes back to
+    # its length before the step, so the cache does not advance; clip warnings are issued
+    # per layer at the same point.
+    def _step_status_ptr(self, layer_id: int, device) -> int:
+        """Address of layer layer_id's status row for a decode-step append (the pending
+        rows are read first if this layer already has one)."""
+        buf = self._step_status
+        if buf is None or buf.device != device:
+            self._flush_step_status()
+            buf = self._step_status = torch.zeros(self.num_layers, 4, dtype=torch.int32,
+                                                  device=device)
+        elif any(e[0] == layer_id for e in self._step_pending):
+            self._flush_step_status()
+        return buf.data_ptr() + 16 * layer_id
+
+    def _defer_status(self, layer_id: int, n_elem: int, kind: str, qrange: str,
+                      clip_warn: bool = True) -> None:
+        """Records a decode-step append of layer_id (already advanced) whose status row is
+        read later; reads every pending row after the step's last layer."""
+        if not self._step_pending:
+            self._step_seq_len0 = self._seq_len
+        self._step_pending.append((layer_id, n_elem, kind, qrange, clip_warn))
+        if layer_id == self.num_layers - 1:
+            self._flush_step_status()
+
+    def flush_status(self) -> None:
+        """Reads the status rows of the decode-step appends not read yet (one host sync):
+        raises ValueError, after undoing those appends, if one of them had NaN / Inf input,
+        and issues their clip warnings."""
+        self._flush_step_status()
+
+    def _flush_step_status(self) -> None:
+        pending = self._step_pending
+        if not pending:
+            return
+        self._step_pending = []
+        rows = self._step_status.cpu()
+        self._step_status.zero_()
+        bad = None
+        for layer_id, n_elem, kind, qrange, clip_warn in pending:
+            st = rows[layer_id].tolist()
+            if bad is None and (st[0] & 1 or st[2] & 1):
+                bad = (kind, "K" if st[0] & 1 else "V")
+            if clip_warn:
+                self._clip_warnings(layer_id, n_elem, qrange, st)
+        if bad is not None:
+            for layer_id, *_ in pending:
+                self._layer_seq_lens[layer_id] -= 1
+            self._seq_len = self._step_seq_len0
+            raise ValueError(f"{bad[0]} append: {bad[1]} input contains NaN or Inf — refusing "
+                             "to quantize corrupt data")
+
+    def _discard_step_status(self) -> None:
+        self._step_pending = []
+        if self._step_status is not None:
+            self._step_status.zero_()
+
     def _read_status(self) -> List[int]:
         """The append kernel's status words (NaN flags and clip counts of K and V), then
         cleared for the next append."""
@@ -202,6 +272,9 @@ class _EngineBase:
             raise ValueError(f"{kind} append: K input contains NaN or Inf — refusing to quantize corrupt data")
         if st[2] & 1:
             raise ValueError(f"{kind} append: V input contains NaN or Inf — refusing to quantize corrupt data")
+        self._clip_warnings(layer_id, n_elem, qrange, st)
+
+    def _clip_warnings(self, layer_id: int, n_elem: int, qrange: str, st: List[int]) -> None:
         for side, cnt in (("K", st[1]), ("V", st[3])):
             ratio = cnt / max(n_elem, 1)
             if ratio > _CLIP_WARN_THRESHOLD:
@@ -443,9 +516,10 @@ class _SymCacheBase(_EngineBase):
         self._steps[layer_id] = st
         return st
 
-    def _fused_apps(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status):
+    def _fused_apps(self, layer_id: int, k: Tensor, v: Tensor, pos: int, status: Optional[int]):
         """The decode step's kvq_append_params of K and V for one new token (built once per
-        layer buffers; per call the rows, the slot and the status words change)."""
+        layer buffers; per call the rows, the slot and the status words (the device address
+        of the layer's status row, or None) change)."""
         B, H, S, D = k.shape
         ent = self._apps[layer_id]
         if ent is None or ent[2] != (B, H):
@@ -456,7 +530,7 @@ class _SymCacheBase(_EngineBase):
             ent = (pk, pv, (B, H))
             self._apps[layer_id] = ent
         pk, pv = ent[0], ent[1]
-        sptr = None if status is None else status.data_ptr()
+        sptr = status
         for p, x, off in ((pk, k, 0), (pv, v, 8)):
             if x.stride(-1) != 1:
                 x = x.contiguous()
@@ -501,22 +575,26 @@ class _SymCacheBase(_EngineBase):
         old = self._layer_seq_lens[layer_id]
         n = old + 1
         self._ensure_capacity(layer_id, B, H, D, G, n)
-        status = self._status_buf(k.device) if self.check_numerics else None
+        status = self._step_status_ptr(layer_id, k.device) if self.check_numerics else None
         # the append's parameter blocks are kept per layer (as ``append`` would build them)
         pk, pv = self._fused_apps(layer_id, k, v, old, status)
         step = self._step_for(layer_id, q.shape[1])
+        out = None
         if self._fused_step_ok(D, B, H):
-            out = step.append_attend(q, n, sm_scale, inv_tau, pk, pv)
-            if status is not None:
-                self._check_status(layer_id, k.numel(), self._kind, self._qrange)
-        else:
+            try:
+                out = step.append_attend(q, n, sm_scale, inv_tau, pk, pv)
+            except NotImplementedError:
+                # the library declined the one-launch step for these buffers (it enqueues
+                # nothing then): the two launches below give the same bits
+                out = None
+        if out is None:
             self._launch_append(pk, pv, k.device)
-            if status is not None:
-                self._check_status(layer_id, k.numel(), self._kind, self._qrange)
             out = step.attend(q, n, sm_scale, inv_tau)
         self._layer_seq_lens[layer_id] = n
         if layer_id == 0:
             self._seq_len = n
+        if status is not None:
+            self._defer_status(layer_id, k.numel(), self._kind, self._qrange)
         return out
 
     def _raw_views(self, layer_id: int, n: Optional[int] = None):
@@ -539,6 +617,7 @@ class _SymCacheBase(_EngineBase):
             sv(self._v_scale[layer_id], self._v_tok[layer_id])
 
     def clear(self) -> None:
+        self._discard_step_status()
         self._layer_seq_lens = [0] * self.num_layers
         self._seq_len = 0
 
@@ -985,14 +1064,13 @@ class _StaticG32Cache(_EngineBase):
         n = old + 1
         if sm_scale is None:
             sm_scale = 1.0 / math.sqrt(D)
-        status = self._status_buf(k.device) if self.check_numerics else None
+        sptr = self._step_status_ptr(layer_id, k.device) if self.check_numerics else None
         ent = self._apps[layer_id]
         if ent is None:
             pk, pv, _ = self._append_params(layer_id, k, v, old, None)
             ent = (pk, pv)
             self._apps[layer_id] = ent
         pk, pv = ent
-        sptr = None if status is None else status.data_ptr()
         for p, x, off in ((pk, k, 0), (pv, v, 8)):
             if x.stride(-1) != 1:
                 x = x.contiguous()
@@ -1002,12 +1080,12 @@ class _StaticG32Cache(_EngineBase):
             p.status = None if sptr is None else sptr + off
             p._keep = (x,)
         out = self._step_for(layer_id, q.shape[1]).append_attend(q, n, sm_scale, inv_tau, pk, pv)
-        if status is not None:
-            self._check_status(layer_id, k.numel(), "K8V4" if self._k_int8 else "INT4-asym",
-                               "the code range")
         self._layer_seq_lens[layer_id] = n
         if layer_id == 0:
             self._seq_len = n
+        if sptr is not None:
+            self._defer_status(layer_id, k.numel(), "K8V4" if self._k_int8 else "INT4-asym",
+                               "the code range")
         return out
 
     def _check_layer(self, layer_id: int) -> int:
@@ -1016,6 +1094,7 @@ class _StaticG32Cache(_EngineBase):
         return self._layer_seq_lens[layer_id]
 
     def clear(self) -> None:
+        self._discard_step_status()
         self._layer_seq_lens = [0] * self.num_layers
         self._seq_len = 0
 
@@ -1510,6 +1589,7 @@ class _KiviFamily(_EngineBase):
         return pk, pv
 
     def clear(self) -> None:
+        self._discard_step_status()
         self._layer_seq_lens = [0] * self.num_layers
         self._seq_len = 0
         self._steps = [None] * self.num_layers
@@ -1829,7 +1909,8 @@ class MixedKVCache(_EngineBase):
             if S == 1:
                 self._apps[layer_id] = {**(ents or {}), fp16: ent}
         pk, pv = ent
-        sptr = None if status is None else status.data_ptr()
+        # status: the status words (a tensor), or the address of a decode-step status row
+        sptr = status if status is None or isinstance(status, int) else status.data_ptr()
         for p, x, off in ((pk, k, 0), (pv, v, 8)):
             if p is None:
                 continue
@@ -1978,19 +2059,17 @@ class MixedKVCache(_EngineBase):
             v = v.contiguous()
         old = self._layer_seq_lens[layer_id]
         self._ensure(layer_id, B, H, old + 1, k.device)
-        status = self._status_buf(k.device) if self.check_numerics else None
+        status = self._step_status_ptr(layer_id, k.device) if self.check_numerics else None
         pk, pv = self._params(layer_id, k, v, old, status, fp16=True)
         out = self._step_for(layer_id, q.shape[1]).append_attend(q, old + 1, sm, inv_tau, pk, pv)
-        if status is not None:
-            st = self._read_status()
-            if st[0] & 1 or st[2] & 1:
-                raise ValueError(f"MixedKVCache append: {'K' if st[0] & 1 else 'V'} input contains "
-                                 "NaN or Inf — refusing to quantize corrupt data")
         self._layer_seq_lens[layer_id] = old + 1
         self._seq_len = max(self._layer_seq_lens)
+        if status is not None:
+            self._defer_status(layer_id, k.numel(), "MixedKVCache", "", clip_warn=False)
         return out
 
     def clear(self) -> None:
+        self._discard_step_status()
         self._layer_seq_lens = [0] * self.num_layers
         self._seq_len = 0
 

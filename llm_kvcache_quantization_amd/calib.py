@@ -1,8 +1,12 @@
 """Static quantization tables from calibration samples, and the calibration-JSON loader.
 
-Scale production follows scripts/calibrate_behavior.py:784-811 with percentile 100:
-per (kv head, group) absmax over every sampled token, clamped to 1e-5 and divided by
-qmax.  The JSON schema is the one read by src/engine/generate_loop.py:751-889:
+Scale production follows scripts/calibrate_behavior.py:228-259 and 764-811: per
+calibration sample, the absmax of every (kv head, group) over the sample's tokens
+(``compute_absmax_per_group``); per layer, torch.quantile of those sample maxima at
+``clip_percentile / 100`` over the samples, clamped to 1e-5 and divided by qmax
+(``scales_from_absmax_samples``).  ``absmax_scale`` is the percentile-100 case over one
+pooled sample.  ``calibration_json`` writes the tables in the schema read by
+src/engine/generate_loop.py:751-889:
 
 * ``k_scale`` / ``v_scale`` [L, Hkv, G];
 * ``inv_tau`` [L, Hq];
@@ -39,6 +43,71 @@ def absmax_scale(sample: torch.Tensor, group_size: int, qmax: float) -> torch.Te
     """fp32 [Hkv, G]: absmax over calibration tokens / qmax (calibrate_behavior.py:784-811)."""
     am = _groups(sample.float(), group_size).abs().amax(dim=(1, 3))
     return am.clamp(min=1e-5) / qmax
+
+
+def compute_absmax_per_group(tensor: torch.Tensor, group_size: int) -> torch.Tensor:
+    """[heads, seq, head_dim] -> [heads, head_dim // group_size]: per (head, group) absmax
+    over the whole sequence (scripts/calibrate_behavior.py:228-259)."""
+    if tensor.ndim != 3:
+        raise ValueError(f"expected [heads, seq, head_dim], got {tuple(tensor.shape)}")
+    heads, seq_len, head_dim = tensor.shape
+    if group_size <= 0 or head_dim % group_size != 0:
+        raise ValueError(f"head_dim ({head_dim}) must be divisible by group_size ({group_size})")
+    view = tensor.reshape(heads, seq_len, head_dim // group_size, group_size)
+    return view.abs().amax(dim=3).amax(dim=1)
+
+
+def collect_absmax_samples(kv_samples, group_size: int):
+    """kv_samples: list over samples -> list over layers -> [kv_heads, seq, head_dim].
+    Returns list over layers -> list over samples -> [kv_heads, num_groups]
+    (scripts/calibrate_behavior.py:764-781)."""
+    if not kv_samples:
+        return []
+    num_layers = len(kv_samples[0])
+    out = [[] for _ in range(num_layers)]
+    for sample in kv_samples:
+        for layer_idx in range(num_layers):
+            out[layer_idx].append(compute_absmax_per_group(sample[layer_idx], group_size))
+    return out
+
+
+def scales_from_absmax_samples(absmax_samples, clip_percentile: float, qmax: float):
+    """Per-layer static scales fp32 [kv_heads, num_groups]: torch.quantile of the
+    sample-level absmax at clip_percentile / 100 over the samples, clamped to 1e-5, divided
+    by qmax (scripts/calibrate_behavior.py:784-811).  An empty layer raises ValueError."""
+    scales = []
+    for layer_idx, layer in enumerate(absmax_samples):
+        if not layer:
+            raise ValueError(f"absmax_samples[{layer_idx}] is empty — no calibration samples "
+                             f"collected for layer {layer_idx}. Check that num_layers matches "
+                             "the model.")
+        stack = torch.stack(list(layer), dim=0).float()
+        absmax = torch.quantile(stack, clip_percentile / 100.0, dim=0)
+        scales.append(absmax.clamp(min=1e-5) / float(qmax))
+    return scales
+
+
+def calibration_json(k_scales, v_scales, *, group_size: int, clip_percentile_k: float,
+                     clip_percentile_v: Optional[float] = None, inv_tau=None,
+                     quant_bits: int = 8, outlier_ratio: float = 0.0,
+                     mixed_rescue: bool = False) -> dict:
+    """The calibration JSON (as a dict) that ``load_calibration_json`` and the reference's
+    loader read (src/engine/generate_loop.py:769-849): k_scale / v_scale [L, Hkv, G],
+    optional inv_tau [L, Hq], the group size and clip percentiles, and for INT4 the rescue
+    settings."""
+    ks = torch.stack([t.float() for t in k_scales]).tolist()
+    vs = torch.stack([t.float() for t in v_scales]).tolist()
+    out = {"version": 2, "quant_bits": int(quant_bits), "k_scale": ks, "v_scale": vs,
+           "group_size_k": int(group_size), "group_size_v": int(group_size),
+           "clip_percentile_k": float(clip_percentile_k),
+           "clip_percentile_v": float(clip_percentile_k if clip_percentile_v is None
+                                      else clip_percentile_v)}
+    if inv_tau is not None:
+        out["inv_tau"] = torch.as_tensor(inv_tau).float().tolist()
+    if quant_bits == 4:
+        out["int4_outlier_ratio"] = float(outlier_ratio)
+        out["int4_mixed_rescue"] = bool(mixed_rescue)
+    return out
 
 
 def int8_static_scale(sample: torch.Tensor, group_size: int) -> torch.Tensor:

@@ -401,8 +401,9 @@ __host__ __device__ inline bool rescue_walk_ok(float q, int n) {
 // decode step's writer), over at most kRescueRows rows (rows = B * H) in groups of 16 or more.
 // rescue_fetch issues the rows' loads early (lane l: the 32 dwords of channels
 // 64 (l % 2) .. + 63 of row l / 2); rescue_thr_rows then takes each lane's group maxima (a
-// group of 128 with its partner lane), writes the scales fmax(absmax, 1e-5) / 7 to dyn (LDS;
-// one wave, whose own writes its reads see in order) and walks from the top.  Needs
+// group of 128 with its partner lane), writes the scales fmax(absmax, 1e-5) / 7 to dyn (LDS
+// of this wave alone; a wave barrier orders the writes before the walk's reads) and walks
+// from the top.  Needs
 // rescue_walk_ok(a.rq, rows * 128 / gs).
 constexpr int kRescueRows = 32;
 struct RescueRows {
@@ -448,6 +449,12 @@ __device__ __forceinline__ float rescue_thr_rows(const AppendDev& a, int lane, c
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       if (k < ng) dyn[r * G + hh * ng + k] = __fdiv_rn(fmaxf(mm[k], 1e-5f), 7.0f);
+  // the walk below reads other lanes' writes: a wave-scope fence and barrier keep the
+  // compiler from moving those reads above the writes (the LDS executes one wave's
+  // instructions in order)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const float rank = a.rq * (float)(n - 1);
   const int lo = (int)floorf(rank), hi = (int)ceilf(rank);
   const float w = rank - (float)lo;

@@ -893,6 +893,21 @@ static int64_t counter_bytes(const kvq_decode_params* p) {
   return (((int64_t)p->batch * p->kv_heads * kCtrSlotWords * 4 + 255) / 256) * 256;
 }
 
+// the n counter slots at ctr set to zero (a fill kernel rather than a memset, so that a
+// call can be captured into a HIP graph)
+static __global__ void clear_counts_kernel(uint32_t* ctr, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n * kCtrSlotWords;
+       i += (int64_t)gridDim.x * blockDim.x)
+    ctr[i] = 0u;
+}
+static int clear_arrival_counts(uint32_t* ctr, int64_t n, hipStream_t s) {
+  const int64_t words = n * kCtrSlotWords;
+  const int64_t blocks = (words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024;
+  hipLaunchKernelGGL(clear_counts_kernel, dim3((unsigned)blocks), dim3(256), 0, s, ctr, n);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? KVQ_OK : fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
+}
+
 extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
   if (!p) return 0;
   const int64_t rows = (int64_t)p->batch * p->q_heads * plan_split(p).pitch;
@@ -903,7 +918,7 @@ extern "C" int64_t kvq_decode_workspace_bytes(const kvq_decode_params* p) {
 // row formats pass their two append sides in rk / rv)
 static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_stream_t stream,
                        const AppendDev* rk = nullptr, const AppendDev* rv = nullptr,
-                       int fam_override = -1) {
+                       int fam_override = -1, bool clear_counts = false) {
   if (!p) return fail(KVQ_ERR_INVALID, "params is NULL");
   if (p->head_dim != kD) return fail(KVQ_ERR_UNSUPPORTED, "head_dim must be 128");
   if (p->batch <= 0 || p->q_heads <= 0 || p->kv_heads <= 0)
@@ -1025,6 +1040,10 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   a.fused = tiled && nch64 <= kUnitChunks;
+  if (clear_counts) {  // kvq_decode_attn_noalloc, after every check above has passed
+    const int rc2 = clear_arrival_counts(a.counters, (int64_t)p->batch * p->kv_heads, s);
+    if (rc2) return rc2;
+  }
   if (tiled) {
     const dim3 grid = sp.share ? dim3((unsigned)sp.grid_x, (unsigned)p->kv_heads, 1u)
                                : dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch);
@@ -1071,14 +1090,6 @@ static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 namespace {
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, or null
-
-// the counter words of the merge start at zero on every call (the array keeps whatever
-// the previous call, of any shape, left there)
-__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = 0u;
-}
 
 // device address of `scratch` on device dev (looked up on the first call for dev)
 int scratch_ptr(int dev, void** out) {
@@ -1128,18 +1139,11 @@ extern "C" int kvq_decode_attn_noalloc(const kvq_decode_params* p, kvq_stream_t 
   kvq_decode_params q = *p;
   q.workspace = ws;
   q.workspace_bytes = kNoallocScratchBytes;
-  // clear the counter slots this call's merge uses (a fill kernel rather than a memset,
-  // so that the call can be captured into a HIP graph)
-  // the counter slots are the first B x Hkv x 128 bytes of the workspace
-  const int64_t words = (int64_t)p->batch * p->kv_heads * kCtrSlotWords;
-  if (words * 4 > kNoallocScratchBytes)
-    return fail(KVQ_ERR_INVALID, "kvq_decode_attn_noalloc: counter slots outside the scratch");
-  uint32_t* ctr = static_cast<uint32_t*>(ws);
-  const int64_t blocks = (words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024;
-  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)blocks), dim3(256), 0, s, ctr, words);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
-  return decode_impl(&q, nullptr, stream);
+  // The counter slots this call's merge uses (the first B x Hkv x 128 bytes of the
+  // workspace) are cleared by a fill kernel, enqueued by decode_impl once every argument
+  // check has passed: a rejected call enqueues nothing.  (The array keeps what the previous
+  // call, of any shape, left there.)
+  return decode_impl(&q, nullptr, stream, nullptr, nullptr, -1, true);
 }
 
 // One new token per (b, kv head) appended to the cache p attends over, in the same launch.

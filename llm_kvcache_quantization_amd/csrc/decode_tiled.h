@@ -1739,10 +1739,12 @@ __device__ __forceinline__ void append_row_pair(const DecodeArgs& a, int b, int 
   const int row = b * a.ark.H + hkv;
   float tk = 0.f, tv = 0.f;
   if constexpr (RESCUE) {
-    __shared__ float rdyn[kRescueRows * 8];  // the writer's scales (one writer per work-group)
-    if (rescue_side(a.ark)) tk = rescue_thr_rows(a.ark, lane, rk, rdyn);
+    // the writer's scales of each side (one writer per work-group; one array per side, so the
+    // V side's writes cannot pass the K side's reads)
+    __shared__ float rdyn_k[kRescueRows * 8], rdyn_v[kRescueRows * 8];
+    if (rescue_side(a.ark)) tk = rescue_thr_rows(a.ark, lane, rk, rdyn_k);
     quant_row_x(a.ark, row, lane, tk, p.k, p.sk);
-    if (rescue_side(a.arv)) tv = rescue_thr_rows(a.arv, lane, rv, rdyn);
+    if (rescue_side(a.arv)) tv = rescue_thr_rows(a.arv, lane, rv, rdyn_v);
   } else {
     quant_row_x(a.ark, row, lane, tk, p.k, p.sk);
   }

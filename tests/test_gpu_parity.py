@@ -907,6 +907,58 @@ def test_fused_append_decode_nan_raises_and_does_not_advance():
     assert cache.get_seq_len() == 65 and torch.isfinite(out.float()).all()
 
 
+def test_decode_step_status_read_once_per_step_and_rolled_back():
+    """check_numerics on the decode step: the status words of all layers are read once,
+    after the step's last layer.  A NaN in a middle layer's new token raises there and every
+    layer of the step goes back to its length before the step (the reference's "raise and do
+    not advance": src/quant/_common.py:13-20 raises before src/cache/int8_cache.py:350-488
+    writes); the next step then runs normally."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[3]
+    t = SY.calibrate(cfg, 0)
+    L = 3
+    g = gen(78)
+    k, v = SY.draw_kv(cfg, 0, 2, 66, g)
+    q = SY.draw_q(cfg, 2, g).to(DEV)
+    rep = lambda x: x[None].expand(L, *x.shape).contiguous()
+    cache = K.INT4AsymKVCache(L, rep(t.k_scale), rep(t.k_zp), rep(t.v_scale), rep(t.v_zp),
+                              device=DEV, k_outlier_idx=rep(t.k_outlier_idx), check_numerics=True)
+    for layer in range(L):
+        cache.append(layer, k[:, :, :64].to(DEV), v[:, :, :64].to(DEV))
+    k1, v1 = k[:, :, 64:65].to(DEV), v[:, :, 64:65].to(DEV)
+    bad = v1.clone()
+    bad[0, 1, 0, 5] = float("inf")
+    cache.append_decode_attn(0, q, k1, v1)
+    cache.append_decode_attn(1, q, k1, bad)  # not read yet: no host sync per layer
+    assert cache._layer_seq_lens == [65, 65, 64]
+    with pytest.raises(ValueError, match="NaN or Inf"):
+        cache.append_decode_attn(2, q, k1, v1)
+    assert cache._layer_seq_lens == [64, 64, 64] and cache.get_seq_len() == 64
+    # the step again with good data, then one more step: every layer matches a fresh cache
+    ref = K.INT4AsymKVCache(L, rep(t.k_scale), rep(t.k_zp), rep(t.v_scale), rep(t.v_zp),
+                            device=DEV, k_outlier_idx=rep(t.k_outlier_idx), check_numerics=False)
+    for layer in range(L):
+        ref.append(layer, k[:, :, :64].to(DEV), v[:, :, :64].to(DEV))
+    k2, v2 = k[:, :, 65:66].to(DEV), v[:, :, 65:66].to(DEV)
+    for kk, vv in ((k1, v1), (k2, v2)):
+        for layer in range(L):
+            out = cache.append_decode_attn(layer, q, kk, vv)
+            ro = ref.append_decode_attn(layer, q, kk, vv)
+            assert torch.equal(out, ro), layer
+    assert cache._layer_seq_lens == [66, 66, 66] and cache.get_seq_len() == 66
+    for layer in range(L):
+        assert torch.equal(cache.get_int4_g32_tensors(layer)[0], ref.get_int4_g32_tensors(layer)[0])
+    # a partial step read explicitly
+    bad2 = k2.clone()
+    bad2[1, 0, 0, 0] = float("nan")
+    cache.append_decode_attn(0, q, bad2, v2)
+    with pytest.raises(ValueError, match="K input contains NaN"):
+        cache.flush_status()
+    assert cache._layer_seq_lens == [66, 66, 66]
+
+
 # ---------------------------------------------------------------- KIVI layout
 
 
