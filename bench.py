@@ -77,6 +77,14 @@ def parse():
     ap.add_argument("--kv-mode", choices=sorted(MODE_SETTINGS), default=None,
                     help="time one of the reference's kv_modes through its cache engine at the "
                          "configuration's shape (shipped calibration settings) and exit")
+    ap.add_argument("--e2e", default=None, metavar="MODEL",
+                    help="end-to-end decode through generate_from_ids on a random-weight "
+                         "model of this shape (qwen2.5-1.5b or qwen2.5-7b): TTFT / TPOT per "
+                         "kv_mode, one JSON line per mode")
+    ap.add_argument("--prompt", type=int, default=4096, help="--e2e prompt length")
+    ap.add_argument("--new-tokens", type=int, default=32, help="--e2e generated tokens")
+    ap.add_argument("--e2e-modes", default="fp16,int8_ours,int4_fused",
+                    help="--e2e kv_modes (comma separated)")
     ap.add_argument("--kivi-probe", action="store_true",
                     help="only time kvq_decode_attn over the KIVI layout at config 3's shape "
                          "(B 8, 28 / 4 heads, 32k tokens; random codes and parameters)")
@@ -648,6 +656,107 @@ def cpu_baseline(cfg, layers_dev):
     }
 
 
+# Qwen2.5 decoder shapes for the end-to-end leg (the models' published configurations)
+E2E_MODELS = {
+    "qwen2.5-1.5b": dict(hidden_size=1536, intermediate_size=8960, num_hidden_layers=28,
+                         num_attention_heads=12, num_key_value_heads=2, vocab_size=151936,
+                         tie_word_embeddings=True),
+    "qwen2.5-7b": dict(hidden_size=3584, intermediate_size=18944, num_hidden_layers=28,
+                       num_attention_heads=28, num_key_value_heads=4, vocab_size=152064,
+                       tie_word_embeddings=False),
+}
+# the shipped calibration settings of the reference's tables
+# (artifacts/kv_calib_mse_1p5b_int8.json / _int4.json): group 16, K clip percentile 99.5,
+# INT4 group rescue ratio 0.01
+E2E_CALIB = dict(group_size=16, clip_percentile=99.5, outlier_ratio=0.01)
+
+
+def e2e_leg(model_name, prompt, new_tokens, modes, device="cuda:0"):
+    """End-to-end greedy decode through ``modes.generate_from_ids`` (prefill through the
+    model, then one token per step through the attention hook; the reference's TTFT / TPOT
+    protocol, src/engine/generate_loop.py:1320-1529: a device synchronisation around every
+    step) on a randomly initialised fp16 Qwen2 model of the named shape, batch 1, random
+    prompt ids, ``stop_on_eos=False``.  The int8_ours / int4_fused tables come from the
+    model's own prefill K/V over 4 calibration prompts of 512 tokens
+    (calib.scales_from_absmax_samples at the shipped settings), with per-head inverse
+    temperatures drawn in [0.8, 1.2].  Returns one dict per mode."""
+    import tempfile
+
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from llm_kvcache_quantization_amd import calib as CB
+    from llm_kvcache_quantization_amd import modes as M
+    from llm_kvcache_quantization_amd.modes import _past_layers
+
+    shape = E2E_MODELS[model_name]
+    cfg = Qwen2Config(**shape, max_position_embeddings=max(prompt + new_tokens + 64, 32768),
+                      rope_theta=1000000.0, rms_norm_eps=1e-6)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(1234)
+    t0 = time.time()
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(device):
+            model = Qwen2ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    model.eval()
+    print(f"[e2e] {model_name}: random fp16 weights in {time.time() - t0:.1f}s", file=sys.stderr,
+          flush=True)
+    L, Hq = shape["num_hidden_layers"], shape["num_attention_heads"]
+    gen = torch.Generator(device=device).manual_seed(4321)
+    vocab = shape["vocab_size"]
+    # calibration samples: the model's own K / V
+    ks_samples, vs_samples = [], []
+    with torch.no_grad():
+        for _ in range(4):
+            ids = torch.randint(0, vocab, (1, 512), device=device, generator=gen)
+            pkv = model(input_ids=ids, use_cache=True).past_key_values
+            layers = _past_layers(pkv)
+            ks_samples.append([k[0].float() for k, _ in layers])
+            vs_samples.append([v[0].float() for _, v in layers])
+    gs = E2E_CALIB["group_size"]
+    ab_k = CB.collect_absmax_samples(ks_samples, gs)
+    ab_v = CB.collect_absmax_samples(vs_samples, gs)
+    tau = torch.empty(L, Hq).uniform_(0.8, 1.2, generator=torch.Generator().manual_seed(7))
+    tmp = tempfile.mkdtemp(prefix="kvq_e2e_")
+    files = {}
+    for bits, qmax in ((8, 127), (4, 7)):
+        d = CB.calibration_json(CB.scales_from_absmax_samples(ab_k, E2E_CALIB["clip_percentile"], qmax),
+                                CB.scales_from_absmax_samples(ab_v, E2E_CALIB["clip_percentile"], qmax),
+                                group_size=gs, clip_percentile_k=E2E_CALIB["clip_percentile"],
+                                inv_tau=tau, quant_bits=bits,
+                                outlier_ratio=E2E_CALIB["outlier_ratio"])
+        files[bits] = os.path.join(tmp, f"calib_int{bits}.json")
+        with open(files[bits], "w") as f:
+            json.dump(d, f)
+    ids = torch.randint(0, vocab, (1, prompt), device=device, generator=gen)
+    out = []
+    for mode in modes:
+        calib_file = files[4] if mode.startswith("int4") else files[8] if mode.startswith("int8") else None
+        kw = dict(kv_mode=mode, calib_file=calib_file, stop_on_eos=False,
+                  decode_attn_impl="triton_fused")
+        # untimed warm-up (kernels, allocator), then the measured generation
+        M.generate_from_ids(model, None, ids[:, :256], max_new_tokens=4, **kw)
+        r = M.generate_from_ids(model, None, ids, max_new_tokens=new_tokens, **kw)
+        dts = sorted(r.decode_times_ms)
+        line = {
+            "metric": "end-to-end TTFT / TPOT (generate_from_ids)",
+            "model": f"{model_name} (random fp16 weights)", "kv_mode": mode,
+            "batch": 1, "prompt": prompt, "new_tokens": new_tokens,
+            "ttft_ms": round(r.ttft_ms, 3), "tpot_ms": round(r.tpot_ms, 3),
+            "tpot_median_ms": round(dts[len(dts) // 2], 3) if dts else None,
+            "kv_cache_mb": round(r.kv_cache_mem_mb, 1),
+            "decode_attn_impl": r.decode_attn_impl,
+            "fused_decode_calls": (r.decode_stats or {}).get("fused_decode_calls"),
+            "check_numerics": True,
+        }
+        print(f"[e2e] {line}", file=sys.stderr, flush=True)
+        out.append(line)
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -661,6 +770,15 @@ def main():
         return
     if args.kivi_probe:
         kivi_probe("cuda:0", max(args.steps, 200), max(args.warmup, 20))
+        return
+    if args.e2e:
+        from llm_kvcache_quantization_amd import _capi as C
+
+        C.lib()
+        torch.cuda.set_device(0)
+        for line in e2e_leg(args.e2e, args.prompt, args.new_tokens,
+                            [m for m in args.e2e_modes.split(",") if m]):
+            print(json.dumps(line), flush=True)
         return
     if args.kv_mode:
         from llm_kvcache_quantization_amd import _capi as C

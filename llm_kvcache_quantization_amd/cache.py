@@ -215,14 +215,14 @@ class _EngineBase:
                                                   device=device)
         elif any(e[0] == layer_id for e in self._step_pending):
             self._flush_step_status()
+        if not self._step_pending:  # the first append of a step: its length before the step
+            self._step_seq_len0 = self._seq_len
         return buf.data_ptr() + 16 * layer_id
 
     def _defer_status(self, layer_id: int, n_elem: int, kind: str, qrange: str,
                       clip_warn: bool = True) -> None:
         """Records a decode-step append of layer_id (already advanced) whose status row is
         read later; reads every pending row after the step's last layer."""
-        if not self._step_pending:
-            self._step_seq_len0 = self._seq_len
         self._step_pending.append((layer_id, n_elem, kind, qrange, clip_warn))
         if layer_id == self.num_layers - 1:
             self._flush_step_status()

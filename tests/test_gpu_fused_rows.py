@@ -213,7 +213,8 @@ def test_fused_rows_mixed(kb, vb, gs):
 def test_fused_rows_group_rescue_far_from_top_keeps_two_launches():
     """A group rescue threshold far from the top of the append's scales (here the median)
     is beyond the writer's walk: the engine keeps two launches, and the entry point refuses
-    the fused call."""
+    the fused call (enqueueing nothing), after which an engine that asked for it anyway makes
+    the two launches itself with the same bits."""
     K = _k()
     st = torch.rand(1, 2, 4) * 0.3 + 0.1
     c = K.INT4KVCache(1, device=DEV, group_size=32, static_k_scale=st, static_v_scale=st,
@@ -228,9 +229,23 @@ def test_fused_rows_group_rescue_far_from_top_keeps_two_launches():
     q = torch.randn(16, 12, 128, generator=g).to(torch.float16).to(DEV)
     out = c.append_decode_attn(0, q, k[:, :, 8:].to(DEV), v[:, :, 8:].to(DEV))  # two launches
     assert out.shape == q.shape and c.get_seq_len() == 9
-    c._fused_step_ok = lambda *args: True
+    twin = K.INT4KVCache(1, device=DEV, group_size=32, static_k_scale=st, static_v_scale=st,
+                         outlier_rescue_ratio=0.5, check_numerics=False)
+    twin.append(0, k[:, :, :8].to(DEV), v[:, :, :8].to(DEV))
+    twin.append_decode_attn(0, q, k[:, :, 8:].to(DEV), v[:, :, 8:].to(DEV))
+    k2, v2 = _kv(16, 2, 1, g)
+    k2, v2 = k2.to(DEV), v2.to(DEV)
+    pk, pv = c._fused_apps(0, k2, v2, 9, None)
     with pytest.raises(NotImplementedError, match="group rescue"):
-        c.append_decode_attn(0, q, k[:, :, 8:].to(DEV), v[:, :, 8:].to(DEV))
+        c._step_for(0, 12).append_attend(q, 10, 1.0 / math.sqrt(128), None, pk, pv)
+    assert c.get_seq_len() == 9
+    c._fused_step_ok = lambda *args: True
+    out = c.append_decode_attn(0, q, k2, v2)
+    ref = twin.append_decode_attn(0, q, k2, v2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref) and c.get_seq_len() == twin.get_seq_len() == 10
+    for a, b in zip(c.get_int4_tensors(0), twin.get_int4_tensors(0)):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("eng", ["int8", "mixed88", "int4"])
