@@ -1,5 +1,5 @@
 /*
- * kvq.h -- C ABI (version 5) of the MI355X (gfx950) quantized-KV decode path.
+ * kvq.h -- C ABI (version 6) of the MI355X (gfx950) quantized-KV decode path.
  *
  * libkvq.so exports three groups of entry points: quantize-on-append, split-K
  * decode attention and error reporting.  Every entry point
@@ -47,9 +47,12 @@ typedef struct ihipStream_t* kvq_stream_t; /* == hipStream_t */
 #define KVQ_FMT_INT4_KIVI 4  /* packed nibbles as INT4_SYM, codes in [-8,7], value c * s + z
                                with fp32 s, z (src/quant/asymmetric_quant.py:24-196,
                                src/cache/kivi_style_cache.py): K per (b, h, channel)
-                               [B,H,D] (scale_stride_b/_h/_g, channels contiguous), V per
-                               (b, h, token) [B,H,T] (scale_stride_b/_h/_t, tokens
-                               contiguous); zero_point has the scale's strides */
+                               [B,H,D] (scale_stride_b/_h/_g, channels contiguous) or, ABI 6,
+                               per (b, h, token) [B,H,T] like V (scale_stride_t 1,
+                               scale_stride_g 0: the reference's MixedKVCache K at 4 bits,
+                               src/cache/mixed_kv_cache.py:159-162); V per (b, h, token)
+                               [B,H,T] (scale_stride_b/_h/_t, tokens contiguous); zero_point
+                               has the scale's strides */
 #define KVQ_FMT_INT8_KIVI 5  /* int8 codes [..., D] in [-128,127], value c * s + z, the
                                 parameters as INT4_KIVI (the reference's quant_bits=8 KIVI
                                 cache); append: range floor 255 * 2^-14, s = range / 255,
@@ -138,7 +141,9 @@ typedef struct kvq_decode_params {
   void* out;              /* fp16 [B, Hq, D], d contiguous */
   int64_t out_stride_b, out_stride_h; /* elements */
   int32_t context_len;    /* context of every row when context_lens is NULL (ABI 4) */
-  int32_t pad0;           /* 0 */
+  int32_t v_group_size;   /* ABI 6: the group size of INT8_SYM / INT4_SYM V when it differs from
+                             group_size (the reference's MixedKVCache v_group_size); 0 = the
+                             same as group_size.  Tiled per-token kernels only */
   /* fp16 residual window (ABI 5; src/cache/kivi_style_cache.py:102-113, 354-404): the
      res_tokens most recent tokens of every row kept unquantized, fp16 [B, kv_heads, >=
      res_tokens, D] with dense 256-byte token rows, attended together with the row's
@@ -288,7 +293,7 @@ int kvq_stream_read(const void* buf, int64_t bytes, uint32_t* sink, int32_t work
 
 /* message for the last non-OK return on this thread ("" if none) */
 const char* kvq_last_error(void);
-/* ABI version (increments on incompatible changes to the structs above); this is 5 */
+/* ABI version (increments on incompatible changes to the structs above); this is 6 */
 int32_t kvq_abi_version(void);
 
 #ifdef __cplusplus

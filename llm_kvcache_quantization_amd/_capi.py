@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before libkvq.so, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 KVQ_OK = 0
 KVQ_ERR_INVALID = 1
@@ -79,7 +79,7 @@ class DecodeParams(ctypes.Structure):
         ("workspace_bytes", c_i64),
         ("out", c_vp),
         ("out_stride_b", c_i64), ("out_stride_h", c_i64),
-        ("context_len", c_i32), ("pad0", c_i32),
+        ("context_len", c_i32), ("v_group_size", c_i32),
         ("res_k", c_vp), ("res_v", c_vp),
         ("res_stride_b", c_i64), ("res_stride_h", c_i64),
         ("res_tokens", c_i32), ("pad1", c_i32),

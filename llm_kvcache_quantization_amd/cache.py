@@ -1748,21 +1748,24 @@ class MixedKVCache(_EngineBase):
     * K 8: INT8 symmetric per (token, group of k_group_size) with a dynamic percentile-clipped
       scale (src/quant/int8_basic.py:18-108): codes int8 [B, H, cap, 128], fp16 scales
       [B, H, cap, Gk] (the reference keeps the same fp16-valued scales as fp32);
-    * V 4: INT4 asymmetric per token (src/quant/asymmetric_quant.py:246-270, v_percentile
-      clipping): packed nibbles [B, H, cap, 64] (byte = ((c[2i]+8) << 4) | (c[2i+1]+8); the
-      reference keeps one code per byte), fp32 scale / zero-point [B, H, cap];
+    * K 4: INT4 asymmetric per token (src/quant/asymmetric_quant.py:246-270,
+      k_clip_percentile clipping; src/cache/mixed_kv_cache.py:159-162): packed nibbles
+      [B, H, cap, 64], fp32 scale / zero-point [B, H, cap] (rows padded to 4 tokens);
+    * V 4: INT4 asymmetric per token (v_percentile clipping): packed nibbles [B, H, cap, 64]
+      (byte = ((c[2i]+8) << 4) | (c[2i+1]+8); the reference keeps one code per byte), fp32
+      scale / zero-point [B, H, cap];
     * V 8: as K 8 with v_group_size and v_percentile;
     * 16 (either side): fp16 values as they come.
 
     The buffers are preallocated and grow by doubling (the reference concatenates per
     append).  The quantized sides of an append are one kvq_quant_append launch; decode
-    attention reads the cache in place through the tiled kernel of the layer's pair.  Built
-    pairs: (8, 4) (the default), (8, 8) with k_group_size == v_group_size, (8, 16), (16, 4),
-    (16, 16); K 4 (asymmetric per token) and (16, 8) raise NotImplementedError.
+    attention reads the cache in place through the tiled kernel of the layer's pair, every
+    (k_bits, v_bits) pair of {4, 8, 16} (the decode call carries V's group size apart from
+    K's, kvq_decode_params.v_group_size).
     """
 
     _min_capacity = 256
-    _BUILT = {(8, 4), (8, 8), (8, 16), (16, 4), (16, 16)}
+    _BUILT = {(kb, vb) for kb in (4, 8, 16) for vb in (4, 8, 16)}
 
     def __init__(self, num_layers: int, device: str = "cuda", dtype: torch.dtype = torch.float16,
                  max_seq_len: Optional[int] = None, k_group_size: int = 128,
@@ -1794,12 +1797,12 @@ class MixedKVCache(_EngineBase):
             if (kb, vb) not in self._BUILT:
                 raise NotImplementedError(f"MixedKVCache: the ({kb}, {vb}) layer is not built (built: "
                                           f"{sorted(self._BUILT)})")
-            if (kb, vb) == (8, 8) and k_group_size != v_group_size:
-                raise NotImplementedError("MixedKVCache (8, 8) needs k_group_size == v_group_size")
         for gs in (k_group_size, v_group_size):
             if gs not in (16, 32, 64, 128):
                 raise NotImplementedError(f"group sizes must be 16, 32, 64 or 128, got {gs}")
         _dyn_quantile(k_clip_percentile)  # (0, 100]
+        if any(kb == 4 for kb, _ in bits):
+            _kivi_levels(k_clip_percentile)
         if any(vb == 4 for _, vb in bits):
             _kivi_levels(v_percentile)
         elif any(vb == 8 for _, vb in bits):
@@ -1818,6 +1821,7 @@ class MixedKVCache(_EngineBase):
         n = num_layers
         self._k_cache: List[Optional[Tensor]] = [None] * n
         self._k_scale: List[Optional[Tensor]] = [None] * n
+        self._k_zp: List[Optional[Tensor]] = [None] * n
         self._v_cache: List[Optional[Tensor]] = [None] * n
         self._v_scale: List[Optional[Tensor]] = [None] * n
         self._v_zp: List[Optional[Tensor]] = [None] * n
@@ -1839,10 +1843,19 @@ class MixedKVCache(_EngineBase):
         kb, vb = self._bits[layer_id]
         new_cap = self._new_capacity(layer_id, target, cap if kc is not None else 0)
         old = self._layer_seq_lens[layer_id]
+        # per-token K parameters: rows of a multiple of 4 tokens (the kernel reads 4 tokens'
+        # parameters as one 16-byte vector)
+        kpitch = (new_cap + 3) // 4 * 4
         new = {
-            "k": torch.empty(B, H, new_cap, 128, dtype=torch.int8 if kb == 8 else torch.float16, device=device),
+            "k": (torch.empty(B, H, new_cap, 64, dtype=torch.int8, device=device) if kb == 4 else
+                  torch.empty(B, H, new_cap, 128, dtype=torch.int8 if kb == 8 else torch.float16,
+                              device=device)),
             "ks": (torch.empty(B, H, new_cap, 128 // self.k_group_size, dtype=torch.float16, device=device)
-                   if kb == 8 else None),
+                   if kb == 8 else
+                   torch.empty(B, H, kpitch, dtype=torch.float32, device=device)[:, :, :new_cap]
+                   if kb == 4 else None),
+            "kz": (torch.empty(B, H, kpitch, dtype=torch.float32, device=device)[:, :, :new_cap]
+                   if kb == 4 else None),
             "v": torch.empty(B, H, new_cap, 64 if vb == 4 else 128,
                              dtype=torch.float16 if vb == 16 else torch.int8, device=device),
             "vs": (torch.empty(B, H, new_cap, dtype=torch.float32, device=device) if vb == 4 else
@@ -1850,13 +1863,14 @@ class MixedKVCache(_EngineBase):
                    if vb == 8 else None),
             "vz": torch.empty(B, H, new_cap, dtype=torch.float32, device=device) if vb == 4 else None,
         }
-        olds = {"k": kc, "ks": self._k_scale[layer_id], "v": self._v_cache[layer_id],
-                "vs": self._v_scale[layer_id], "vz": self._v_zp[layer_id]}
+        olds = {"k": kc, "ks": self._k_scale[layer_id], "kz": self._k_zp[layer_id],
+                "v": self._v_cache[layer_id], "vs": self._v_scale[layer_id], "vz": self._v_zp[layer_id]}
         if kc is not None and old > 0:
             for key, t in new.items():
                 if t is not None:
                     t[:, :, :old] = olds[key][:, :, :old]
         self._k_cache[layer_id], self._k_scale[layer_id] = new["k"], new["ks"]
+        self._k_zp[layer_id] = new["kz"]
         self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id] = new["v"], new["vs"], new["vz"]
         self._layer_capacity[layer_id] = new_cap
         self._steps[layer_id] = self._apps[layer_id] = None
@@ -1891,6 +1905,13 @@ class MixedKVCache(_EngineBase):
                 pk.dyn_quantile = _dyn_quantile(self.k_clip_percentile)
                 pk.scale_out, pk.scale_out_dtype = ks.data_ptr(), C.KVQ_DTYPE_F16
                 pk.so_stride_b, pk.so_stride_h, pk.so_stride_t, pk.so_stride_g = ks.stride()
+            elif kb == 4:  # per-token asymmetric, the same arithmetic as a 4-bit V
+                pk = C.AppendParams()
+                ks, kz = self._k_scale[layer_id], self._k_zp[layer_id]
+                _fill_append(pk, C.KVQ_FMT_INT4_KIVI, k, 32, self._k_cache[layer_id], pos, None)
+                pk.scale_out, pk.zp_out, pk.scale_out_dtype = ks.data_ptr(), kz.data_ptr(), C.KVQ_DTYPE_F32
+                pk.so_stride_b, pk.so_stride_h, pk.so_stride_t = ks.stride()
+                pk.dyn_quantile_lo, pk.dyn_quantile = _kivi_levels(self.k_clip_percentile)
             if vb == 4:
                 pv = C.AppendParams()
                 vc, vs, vz = self._v_cache[layer_id], self._v_scale[layer_id], self._v_zp[layer_id]
@@ -1968,9 +1989,10 @@ class MixedKVCache(_EngineBase):
         return self._layer_seq_lens[layer_id]
 
     def get_mixed_tensors(self, layer_id: int):
-        """(k_store, k_scale16, v_store, v_scale, v_zp) over the stored tokens: K int8 codes or
-        fp16 values, V packed / int8 codes or fp16 values; None where a side has no such
-        parameter."""
+        """(k_store, k_scale, v_store, v_scale, v_zp) over the stored tokens: K int8 codes
+        (fp16 group scales), packed 4-bit codes (fp32 per-token scales; the zero-points are
+        ``get_k_zero_points``) or fp16 values, V packed / int8 codes or fp16 values; None
+        where a side has no such parameter."""
         n = self._check_layer(layer_id)
 
         def sl(t):
@@ -1979,13 +2001,25 @@ class MixedKVCache(_EngineBase):
         return (sl(self._k_cache[layer_id]), sl(self._k_scale[layer_id]), sl(self._v_cache[layer_id]),
                 sl(self._v_scale[layer_id]), sl(self._v_zp[layer_id]))
 
+    def get_k_zero_points(self, layer_id: int) -> Optional[Tensor]:
+        """fp32 [B, H, S] per-token zero-points of a 4-bit K layer (None otherwise)."""
+        n = self._check_layer(layer_id)
+        kz = self._k_zp[layer_id]
+        return None if kz is None else kz[:, :, :n]
+
     def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
         """Dequantised K, V in self.dtype (mixed_kv_cache.py:170-190, 242-254): a symmetric
-        side is code x the scale of its group, the asymmetric V code x s + z of its token, in
-        fp32, then cast."""
+        side is code x the scale of its group, an asymmetric side code x s + z of its token,
+        in fp32, then cast."""
         kc, ks, vc, vs, vz = self.get_mixed_tensors(layer_id)
         kb, vb = self._bits[layer_id]
-        k = kc.to(self.dtype) if kb == 16 else _deq_sym(kc, ks.float()).to(self.dtype)
+        if kb == 16:
+            k = kc.to(self.dtype)
+        elif kb == 8:
+            k = _deq_sym(kc, ks.float()).to(self.dtype)
+        else:
+            kz = self.get_k_zero_points(layer_id)
+            k = (_unpack(kc).float() * ks.unsqueeze(-1) + kz.unsqueeze(-1)).to(self.dtype)
         if vb == 16:
             v = vc.to(self.dtype)
         elif vb == 8:
@@ -2005,8 +2039,11 @@ class MixedKVCache(_EngineBase):
         B, H = kc.shape[0], kc.shape[1]
         ks, vc, vs, vz = self._k_scale[layer_id], self._v_cache[layer_id], self._v_scale[layer_id], \
             self._v_zp[layer_id]
+        kz = self._k_zp[layer_id]
         if kb == 8:
             kf, kview = C.KVQ_FMT_INT8_SYM, kv_view_tok(kc, ks)
+        elif kb == 4:  # per-token parameters, the layout of a 4-bit V
+            kf, kview = C.KVQ_FMT_INT4_KIVI, kv_view_kivi(kc, ks, kz, False)
         else:
             kf, kview = C.KVQ_FMT_FP16, kv_view_fp16(kc)
         if vb == 4:
@@ -2015,8 +2052,12 @@ class MixedKVCache(_EngineBase):
             vf, vview = C.KVQ_FMT_INT8_SYM, kv_view_tok(vc, vs)
         else:
             vf, vview = C.KVQ_FMT_FP16, kv_view_fp16(vc)
-        st = LayerStep(kf, kview, vf, vview, B, q_heads, H, self.k_group_size if kb == 8 else 32,
-                       kc.device, keepalive=(kc, ks, vc, vs, vz))
+        # one group size per decode call for K; V's goes apart when both sides have groups
+        gs = self.k_group_size if kb == 8 else self.v_group_size if vb == 8 else 32
+        st = LayerStep(kf, kview, vf, vview, B, q_heads, H, gs, kc.device,
+                       keepalive=(kc, ks, kz, vc, vs, vz))
+        if kb == 8 and vb == 8 and self.v_group_size != self.k_group_size:
+            st.params.v_group_size = self.v_group_size
         st.key = (q_heads, kc.data_ptr())
         self._steps[layer_id] = st
         return st
@@ -2048,10 +2089,6 @@ class MixedKVCache(_EngineBase):
             q = q.to(torch.float16).contiguous()
         sm = 1.0 / math.sqrt(128) if sm_scale is None else sm_scale
         self._validate_kv(layer_id, k, v)
-        kb, vb = self._bits[layer_id]
-        if kb == 8 and vb == 8 and self.v_group_size != self.k_group_size:
-            n = self._append(layer_id, k, v)  # the decode call has one group size
-            return self._step_for(layer_id, q.shape[1]).attend(q, n, sm, inv_tau)
         B, H = k.shape[0], k.shape[1]
         if k.stride(-1) != 1:
             k = k.contiguous()
@@ -2075,7 +2112,7 @@ class MixedKVCache(_EngineBase):
 
     def release(self) -> None:
         n = self.num_layers
-        self._k_cache, self._k_scale = [None] * n, [None] * n
+        self._k_cache, self._k_scale, self._k_zp = [None] * n, [None] * n, [None] * n
         self._v_cache, self._v_scale, self._v_zp = [None] * n, [None] * n, [None] * n
         self._steps, self._apps = [None] * n, [None] * n
         self._layer_capacity = [0] * n
@@ -2083,7 +2120,7 @@ class MixedKVCache(_EngineBase):
 
     def get_memory_mb(self) -> float:
         total = 0
-        for lst in (self._k_cache, self._k_scale, self._v_cache, self._v_scale, self._v_zp):
+        for lst in (self._k_cache, self._k_scale, self._k_zp, self._v_cache, self._v_scale, self._v_zp):
             total += sum(t.numel() * t.element_size() for t in lst if t is not None)
         return total / (1024 * 1024)
 

@@ -558,7 +558,7 @@ static const void* selected_kernel() {
 
 // (k_format, v_format, scale dtype) -> kernel family; 0 means unsupported
 enum Family { kNone = 0, kI8I8_16, kI8I8_32, kI4I4_16, kI4I4_32, kA4A4, kA4A4o, kI8A4_16, kI8A4_32,
-              kKivi, kI8Kv };
+              kKivi, kI8Kv, kMixedT8 };
 
 // the KIVI family's formats: per-channel K / per-token V asymmetric codes, or fp16 values
 static bool kivi_fmt(int f) {
@@ -579,6 +579,9 @@ static Family family(int kf, int vf, int ksf32, int vsf32, int kout) {
   if (kivi_fmt(kf) && kivi_fmt(vf)) return kKivi;  // tiled kernel only
   if (kf == KVQ_FMT_INT8_SYM && (vf == KVQ_FMT_INT4_KIVI || vf == KVQ_FMT_FP16))
     return kI8Kv;  // tiled kernel only
+  // the reference's MixedKVCache (K INT4 per token, or fp16 K) with INT8 V: tiled kernel only
+  if ((kf == KVQ_FMT_INT4_KIVI || kf == KVQ_FMT_FP16) && vf == KVQ_FMT_INT8_SYM && !vsf32)
+    return kMixedT8;
   return kNone;
 }
 
@@ -634,6 +637,17 @@ static bool static_over_bt(const kvq_kv_view& v, const kvq_decode_params* p) {
 // INT8 K with per-token fp16 scales may also pair with per-token asymmetric INT4 V in the
 // KIVI layout (the reference's MixedKVCache: K INT8 symmetric per group, V INT4 asymmetric
 // per token).
+// the group size of the V side's per-token scales (kvq_decode_params.v_group_size, ABI 6)
+static int v_group(const kvq_decode_params* p) {
+  return p->v_group_size > 0 ? p->v_group_size : p->group_size;
+}
+
+// a per-token INT4_KIVI K view (the reference's MixedKVCache K at 4 bits): fp32 parameters
+// [B, H, T], tokens contiguous, no channel stride
+static bool kivi_k_per_token(const kvq_kv_view& v) {
+  return v.scale_stride_t == 1 && v.scale_stride_g == 0;
+}
+
 static int tok_family(const kvq_decode_params* p) {
   if (p->v.layout != KVQ_LAYOUT_ROWS) return kTiledNone;
   const bool kivi_v = p->k_format == KVQ_FMT_INT8_SYM &&
@@ -641,33 +655,56 @@ static int tok_family(const kvq_decode_params* p) {
   if (p->k_format != p->v_format && !kivi_v) return kTiledNone;
   const bool i4 = p->k_format == KVQ_FMT_INT4_SYM;
   if (!i4 && p->k_format != KVQ_FMT_INT8_SYM) return kTiledNone;
-  const int gs = p->group_size;
-  if (gs < 16) return kTiledNone;
+  const int gs = p->group_size, vgs = v_group(p);
+  if (gs < 16 || vgs < 16) return kTiledNone;
+  if (vgs != gs && (i4 || p->v_format != KVQ_FMT_INT8_SYM)) return kTiledNone;
   const int64_t row = i4 ? kD / 2 : kD;
   const int dt = i4 ? KVQ_DTYPE_F32 : KVQ_DTYPE_F16;
   const int64_t es = i4 ? 4 : 2;
-  const int64_t w = (!i4 && gs == 16) ? 2 : 1;  // elements per aligned load
-  auto ok = [&](const kvq_kv_view& v) {
+  // w: elements per aligned scale load (INT8 K with groups of 16 reads two fp16 at once)
+  auto ok = [&](const kvq_kv_view& v, int g, int64_t w) {
     return v.stride_t == row && v.scale_dtype == dt && v.scale != nullptr &&
-           (v.scale_stride_g == 1 || gs == kD) && ((uintptr_t)v.scale % (w * es)) == 0 &&
+           (v.scale_stride_g == 1 || g == kD) && ((uintptr_t)v.scale % (w * es)) == 0 &&
            v.scale_stride_b % w == 0 && v.scale_stride_h % w == 0 && v.scale_stride_t % w == 0 &&
            v.scale_stride_b >= 0 && v.scale_stride_h >= 0 && v.scale_stride_t >= 0;
   };
+  const int64_t wk = (!i4 && gs == 16) ? 2 : 1;
   if (kivi_v) {
-    if (!ok(p->k)) return kTiledNone;
+    if (!ok(p->k, gs, wk)) return kTiledNone;
     if (p->v_format == KVQ_FMT_FP16)  // fp16 V in dense 256-byte rows
       return p->v.stride_t == 2 * kD ? (gs == 16 ? kTiledT8Fg16 : kTiledT8F) : kTiledNone;
     // V codes in dense 64-byte rows, fp32 scale / zero-point per token (checked by check_view)
     if (p->v.stride_t != kD / 2 || p->v.scale_stride_t != 1) return kTiledNone;
     return gs == 16 ? kTiledT8Kvg16 : kTiledT8Kv;
   }
-  if (!ok(p->k) || !ok(p->v)) return kTiledNone;
+  if (!ok(p->k, gs, wk) || !ok(p->v, vgs, i4 ? 1 : 1)) return kTiledNone;
   if (i4) return gs == 16 ? kTiledT4g16 : kTiledT4;
   return gs == 16 ? kTiledT8g16 : kTiledT8;
 }
 
+// INT8_SYM V with per-token fp16 scales in dense rows (groups of 16 or more, contiguous) on
+// the tiled kernel's VTokT, next to a K of another format
+static bool tok8_v_ok(const kvq_decode_params* p) {
+  const kvq_kv_view& v = p->v;
+  const int vgs = v_group(p);
+  return p->v_format == KVQ_FMT_INT8_SYM && v.layout == KVQ_LAYOUT_ROWS && v.stride_t == kD &&
+         v.scale != nullptr && v.scale_dtype == KVQ_DTYPE_F16 && vgs >= 16 &&
+         (v.scale_stride_g == 1 || vgs == kD) && v.scale_stride_b >= 0 && v.scale_stride_h >= 0 &&
+         v.scale_stride_t >= 0;
+}
+
 static int tiled_family(const kvq_decode_params* p) {
   const bool vt = p->v.layout == KVQ_LAYOUT_TILE32;
+  // the reference's MixedKVCache pairs with a per-token INT4 K, or fp16 K with INT8 V
+  if (p->k_format == KVQ_FMT_INT4_KIVI && kivi_k_per_token(p->k)) {
+    if (vt || p->k.stride_t != kD / 2) return kTiledNone;
+    if (p->v_format == KVQ_FMT_INT4_KIVI)
+      return (p->v.stride_t == kD / 2 && p->v.scale_stride_t == 1) ? kTiledKtKv : kTiledNone;
+    if (p->v_format == KVQ_FMT_FP16) return p->v.stride_t == 2 * kD ? kTiledKtF : kTiledNone;
+    return tok8_v_ok(p) ? kTiledKtT8 : kTiledNone;
+  }
+  if (p->k_format == KVQ_FMT_FP16 && p->v_format == KVQ_FMT_INT8_SYM)
+    return (!vt && p->k.stride_t == 2 * kD && tok8_v_ok(p)) ? kTiledFT8 : kTiledNone;
   if (kivi_fmt(p->k_format)) {
     if (!kivi_fmt(p->v_format) || vt || p->k.stride_t != row_bytes_of(p->k_format) ||
         p->v.stride_t != row_bytes_of(p->v_format))
@@ -786,7 +823,12 @@ static int check_view(const kvq_kv_view& v, int fmt, bool is_k, const char* name
     if (v.scale_dtype != KVQ_DTYPE_F32 || !v.zero_point)
       return fail(KVQ_ERR_INVALID, n + ": KIVI needs fp32 scale and zero_point");
     if (v.n_outlier != 0) return fail(KVQ_ERR_UNSUPPORTED, n + ": outlier channels need INT4_ASYM");
-    if (is_k) {
+    if (is_k && fmt == KVQ_FMT_INT4_KIVI && kivi_k_per_token(v)) {
+      // per-token K: 4 tokens' parameters are read as one 16-byte vector
+      if (!aligned(v.scale, 16) || !aligned(v.zero_point, 16) || v.scale_stride_b % 4 ||
+          v.scale_stride_h % 4)
+        return fail(KVQ_ERR_UNSUPPORTED, n + ": per-token K parameter rows must be 16-byte aligned");
+    } else if (is_k) {
       // the 8 channels of a lane are read as two 16-byte vectors
       if (v.scale_stride_g != 1)
         return fail(KVQ_ERR_UNSUPPORTED, n + ": KIVI K parameters need contiguous channels");
@@ -932,6 +974,9 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   const int gs = p->group_size;
   if (gs != 8 && gs != 16 && gs != 32 && gs != 64 && gs != 128)
     return fail(KVQ_ERR_UNSUPPORTED, "group_size must be 8, 16, 32, 64 or 128");
+  const int vgs = v_group(p);
+  if (p->v_group_size < 0 || (vgs != 8 && vgs != 16 && vgs != 32 && vgs != 64 && vgs != 128))
+    return fail(KVQ_ERR_UNSUPPORTED, "v_group_size must be 0, 8, 16, 32, 64 or 128");
   if (p->capacity < 0 || p->capacity > (int64_t)1 << 30)
     return fail(KVQ_ERR_INVALID, "capacity out of range");
   if (!p->q || !p->out) return fail(KVQ_ERR_INVALID, "q/out is NULL");
@@ -953,6 +998,10 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   if (fam == kKivi && !tiled)
     return fail(KVQ_ERR_UNSUPPORTED,
                 "KIVI-family K and V (INT4_KIVI, INT8_KIVI, FP16) need dense token rows");
+  if (fam == kMixedT8 && !tiled)
+    return fail(KVQ_ERR_UNSUPPORTED,
+                "INT8 V with a per-token INT4 K or an fp16 K needs dense rows (per-token K "
+                "parameters [B, H, T], fp16 V scales in groups of 16 or more)");
   if (fam == kI8Kv && !tiled)
     return fail(KVQ_ERR_UNSUPPORTED,
                 "INT8 K with INT4_KIVI or FP16 V needs dense K rows with fp16 per-token scales "
@@ -966,8 +1015,11 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
     return fail(KVQ_ERR_UNSUPPORTED, "capacity too large for one (b, head) slab");
   int rc = check_view(p->k, kf, true, "k", gs);
   if (rc) return rc;
-  rc = check_view(p->v, vf, false, "v", gs);
+  rc = check_view(p->v, vf, false, "v", vgs);
   if (rc) return rc;
+  if (vgs != gs && !tiled)
+    return fail(KVQ_ERR_UNSUPPORTED, "a V group size apart from K's needs per-token INT8 V on the "
+                                     "tiled kernel (dense rows, groups of 16 or more)");
 
   const Split sp = plan_split(p);
   const int32_t chunk = sp.chunk;
@@ -988,7 +1040,7 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   a.v = to_dev(p->v);
   a.ctx = p->context_lens;
   a.ctx_uniform = p->context_len;
-  a.B = p->batch; a.Hq = p->q_heads; a.Hkv = p->kv_heads; a.n_rep = n_rep; a.gs = gs;
+  a.B = p->batch; a.Hq = p->q_heads; a.Hkv = p->kv_heads; a.n_rep = n_rep; a.gs = gs; a.vgs = vgs;
   a.cap = p->capacity;
   a.sm_log2e = p->sm_scale * kLog2e;
   a.chunk = chunk;
@@ -1202,7 +1254,8 @@ static int check_row_side(const kvq_append_params* x, const kvq_kv_view& v, int 
     return fail(KVQ_ERR_UNSUPPORTED, n + ": format differs from the decode call's");
   if (x->seq_new != 1) return fail(KVQ_ERR_UNSUPPORTED, n + ": the fused append takes one token");
   if (x->batch != p->batch || x->heads != p->kv_heads || x->head_dim != kD ||
-      ((fmt == KVQ_FMT_INT8_SYM || fmt == KVQ_FMT_INT4_SYM) && x->group_size != p->group_size))
+      ((fmt == KVQ_FMT_INT8_SYM || fmt == KVQ_FMT_INT4_SYM) &&
+       x->group_size != (is_k ? p->group_size : v_group(p))))
     return fail(KVQ_ERR_INVALID, n + ": shape does not match the decode call");
   if (x->write_pos < 0 || x->write_pos >= p->capacity)
     return fail(KVQ_ERR_INVALID, n + ": write_pos outside the cache capacity");
@@ -1303,4 +1356,4 @@ extern "C" int kvq_append_decode_attn(const kvq_decode_params* p, const kvq_appe
 }
 
 extern "C" const char* kvq_last_error(void) { return g_last_error.c_str(); }
-extern "C" int32_t kvq_abi_version(void) { return 5; }
+extern "C" int32_t kvq_abi_version(void) { return 6; }

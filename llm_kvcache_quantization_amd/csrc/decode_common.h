@@ -62,6 +62,7 @@ struct DecodeArgs {
   const int32_t* ctx;  // context length per batch row, or null: every row has ctx_uniform
   int ctx_uniform;
   int B, Hq, Hkv, n_rep, gs;
+  int vgs;          // the group size of per-token INT8 / INT4 V scales (gs unless set apart)
   int64_t cap;
   float sm_log2e;
   int chunk, n_chunks;
@@ -440,6 +441,10 @@ enum TiledFam {
   kTiledKv48, kTiledKv4F, kTiledKv84, kTiledKv88, kTiledKv8F, kTiledKvF4, kTiledKvF8, kTiledKvFF,
   kTiledT8F,    // INT8_SYM K with per-token fp16 scales, FP16 V
   kTiledT8Fg16,  // the same with K groups of 16
+  // INT4 asymmetric K per token (INT4_KIVI with per-token parameters), with V INT4_KIVI,
+  // INT8_SYM with per-token fp16 scales, or FP16 (the reference's MixedKVCache at K 4 bits)
+  kTiledKtKv, kTiledKtT8, kTiledKtF,
+  kTiledFT8,    // FP16 K, INT8_SYM V with per-token fp16 scales (MixedKVCache (16, 8))
 };
 // kernel of family fam for n_rep query heads per kv head, or nullptr
 const void* tiled_kernel(int fam, int n_rep);
@@ -448,6 +453,7 @@ const void* tiled_kernel_a4(int fam, bool pack8);
 const void* tiled_kernel_tok(int fam, bool pack8);
 const void* tiled_kernel_kv4(int fam, bool pack8);
 const void* tiled_kernel_kv16(int fam, bool pack8);
+const void* tiled_kernel_kt(int fam, bool pack8);
 hipError_t launch_tiled(const DecodeArgs& a, int fam, dim3 grid, hipStream_t s);
 
 }  // namespace kvq

@@ -847,6 +847,103 @@ struct KKiviT : KAsymT<false> {
   }
 };
 
+// K of the reference's MixedKVCache at 4 bits: INT4 asymmetric per token
+// (src/quant/asymmetric_quant.py:246-270, src/cache/mixed_kv_cache.py:159-162): packed
+// nibbles n = c + 8 in dense 64-byte rows and an fp32 scale s_t / zero-point z_t per token
+// ([B, H, T], tokens contiguous; INT4_KIVI with per-token K parameters).  The reference
+// dequantises K to fp16 before its attention (mixed_kv_cache.py:186-188: (n - 8) s + z in fp32,
+// then .to(fp16)), and with outlier channels in the token's range that rounding moves the
+// logits by more than the output tolerance allows, so the A operand is exactly that fp16
+// value: lane (row, lg) of row block rb dequantises its 32 channels of token 16 rb + row with
+// the token's s and z (one dword each per row block), byte to float by v_cvt_f32_ubyte, one
+// fma, round to nearest fp16.  The B operand is q' in channel order.  Logits at unit scale.
+struct KTokAsymT : KAsymT<false> {
+  static constexpr bool kAppend = false;
+  static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
+  static constexpr bool kRescue = false;     // (no INT4_SYM side)
+  static constexpr bool kSub24 = false;
+  static constexpr bool kPackPV = false;
+  rsrc_t rs, rz;
+  uint32_t vs;  // lane byte offset of token row (lane & 15) in the parameter rows
+  struct Raw {
+    u32x4 w[2];
+    float s[2], z[2];  // [rb]: the parameters of token 16 rb + row
+  };
+  __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
+    KAsymT<false>::setup_addr(a, b, hkv, lane);
+    const int64_t o = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh;
+    rs = buffer_rsrc(reinterpret_cast<const float*>(a.k.scale) + o, (uint32_t)(a.cap * 4));
+    rz = buffer_rsrc(reinterpret_cast<const float*>(a.k.zp) + o, (uint32_t)(a.cap * 4));
+    vs = (uint32_t)(4 * (lane & 15));
+  }
+  __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
+    const int col = lane & 15, lg = lane >> 4;
+    const int hq = hkv * a.n_rep + (col < a.n_rep ? col : 0);
+    in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
+    in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
+    in.s = (half_t)1.0f;
+    in.z = (half_t)0.0f;
+    in.oc = int4{-1, -1, -1, -1};
+  }
+  // channel slice j: q' = fp16(q * inv_tau) in channel order
+  __device__ void setup_q(const DecodeArgs& a, const QIn& in, int lane, int j, QShareLds& sh) {
+    const int col = lane & 15;
+    const bool valid = col < a.n_rep;
+    const bool has_tau = a.inv_tau != nullptr;
+    const uint32_t qw[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
+    half_t vh[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half2v h2 = as_h2(qw[e >> 1]);
+      vh[e] = valid ? qscale((e & 1) ? h2.y : h2.x, in.tau, has_tau) : (half_t)0.0f;
+    }
+    sh.qh[j][lane] = __builtin_bit_cast(u32x4, half8v{vh[0], vh[1], vh[2], vh[3], vh[4], vh[5], vh[6], vh[7]});
+  }
+  __device__ void finish_setup(const QShareLds& sh, const QIn& in, int lane) {
+    (void)in;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
+  }
+  // codes as KAsymT; the parameters of the lane's tokens (0 past the capacity, and for a
+  // !valid tile, which touches no memory)
+  __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    const uint32_t v = vk + (valid ? (uint32_t)tok * kRowK : kOutOfRange);
+    r.w[0] = bload4(rk, v, 0);
+    r.w[1] = bload4(rk, v + 16 * kRowK, 0);
+    const uint32_t p = vs + (valid ? (uint32_t)tok * 4u : kOutOfRange);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      r.s[rb] = __builtin_bit_cast(float, bload1(rs, p + 64u * rb, 0));
+      r.z[rb] = __builtin_bit_cast(float, bload1(rz, p + 64u * rb, 0));
+    }
+  }
+  // fp16((n - 8) s + z) of the 8 codes of dword w (byte b: channel 2 b in the high nibble,
+  // 2 b + 1 in the low one), in channel order
+  __device__ __forceinline__ static half8v deq8(uint32_t w, float s, float z) {
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu, lo = w & 0x0F0F0F0Fu;
+    half_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // (float) of a byte lane compiles to v_cvt_f32_ubyte<k>
+      const float n = (float)(((e & 1) ? lo : hi) >> (8 * (e >> 1)) & 0xFFu);
+      // the reference's codes.to(fp32) * s + z: a rounded product, then a rounded sum
+      h[e] = (half_t)__fadd_rn(__fmul_rn(n - 8.0f, s), z);
+    }
+    return half8v{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+  }
+  __device__ __forceinline__ void qk(const Raw& r, const NibConsts& nc, float4v& x0,
+                                     float4v& x1) const {
+    (void)nc;
+    float4v c[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[rb] = mfma16x16x32(deq8(r.w[rb][j], r.s[rb], r.z[rb]), qh[j], c[rb]);
+    x0 = c[0];
+    x1 = c[1];
+  }
+};
+
 // V of the KIVI layout in token rows (64 bytes).  Lane (col, lg) reads the dword of
 // channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens T(k) (four 64-byte rows
 // per load instruction) and their fp32 scale / zero-point.  The codes enter the MFMA as
@@ -1538,11 +1635,11 @@ struct VTokT {
     const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
     rv = buffer_rsrc(vb, (uint32_t)(a.cap * kRow));
     vv = (uint32_t)((4 * lg) * kRow + (I4 ? 4 : 8) * col);
-    const int gi = (8 * col) >> __builtin_ctz((unsigned)a.gs);
+    const int gi = (8 * col) >> __builtin_ctz((unsigned)a.vgs);
     const char* sb = reinterpret_cast<const char*>(a.v.scale) +
                      ((int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh) * kEs;
     sst = (uint32_t)(a.v.sst * kEs);
-    rs = buffer_rsrc(sb, scale_bytes(a.cap, a.v.sst, a.gs, kEs));
+    rs = buffer_rsrc(sb, scale_bytes(a.cap, a.v.sst, a.vgs, kEs));
     vs = (uint32_t)((4 * lg) * sst + gi * a.v.ssg * kEs);
   }
   // rows of a partial last tile past the capacity read 0; !valid: every load out of range

@@ -1,5 +1,5 @@
 // Dispatch of the tiled decode kernel (decode_tiled.h): the format family's instantiation,
-// looked up in the translation unit that holds it (decode_tiled_{a4,tok,kv4,kv16}.hip), and
+// looked up in the translation unit that holds it (decode_tiled_{a4,tok,kv4,kv16,kt}.hip), and
 // its launch.
 #include "decode_common.h"
 
@@ -7,7 +7,8 @@ namespace kvq {
 
 const void* tiled_kernel(int fam, int n_rep) {
   const bool pack8 = n_rep <= 8;
-  for (auto pick : {tiled_kernel_a4, tiled_kernel_tok, tiled_kernel_kv4, tiled_kernel_kv16})
+  for (auto pick : {tiled_kernel_a4, tiled_kernel_tok, tiled_kernel_kv4, tiled_kernel_kv16,
+                    tiled_kernel_kt})
     if (const void* fn = pick(fam, pack8)) return fn;
   return nullptr;
 }

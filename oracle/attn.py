@@ -126,12 +126,18 @@ def decode_attn_mixed_ref(q, k_int8, k_scale, v_codes, v_scale, v_zp, context_le
 
 
 def decode_attn_mixed_bits_ref(q, k_store, k_bits, k_scale, v_store, v_bits, v_scale, v_zp,
-                               context_lens, sm_scale, inv_tau=None):
-    """MixedKVCache of any built (k_bits, v_bits) pair (src/cache/mixed_kv_cache.py:150-254),
-    decoded as get_kv then attention: an 8-bit side is code x its group's scale in fp32, the
-    4-bit V code x s + z of its token in fp32 (v_store packed), a 16-bit side the stored fp16
-    values; each side cast to fp16, then fp32 attention."""
-    k = k_store if k_bits == 16 else dequantize_symmetric(k_store, k_scale.float()).to(torch.float16)
+                               context_lens, sm_scale, inv_tau=None, k_zp=None):
+    """MixedKVCache of any (k_bits, v_bits) pair of {4, 8, 16} (src/cache/mixed_kv_cache.py:
+    150-254), decoded as get_kv then attention: an 8-bit side is code x its group's scale in
+    fp32, a 4-bit side (packed) code x s + z of its token in fp32 (K: k_scale / k_zp
+    [B, H, S]), a 16-bit side the stored fp16 values; each side cast to fp16, then fp32
+    attention."""
+    if k_bits == 16:
+        k = k_store
+    elif k_bits == 8:
+        k = dequantize_symmetric(k_store, k_scale.float()).to(torch.float16)
+    else:
+        k = dequantize_kivi(unpack_int4(k_store), k_scale, k_zp, per_channel=False).to(torch.float16)
     if v_bits == 16:
         v = v_store
     elif v_bits == 8:

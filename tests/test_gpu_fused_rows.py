@@ -180,14 +180,17 @@ def test_fused_rows_kivi_family(eng, kw, B, H, Hq, S0, steps):
         assert_close_ulp(out1, ref, f"{eng} ({kb},{vb}) {n}")
 
 
-@pytest.mark.parametrize("kb,vb,gs", [(8, 4, 128), (8, 4, 16), (8, 8, 32), (8, 16, 64), (16, 4, 128),
-                                      (16, 16, 128)])
-def test_fused_rows_mixed(kb, vb, gs):
+@pytest.mark.parametrize("kb,vb,gs,vgs", [(8, 4, 128, 128), (8, 4, 16, 16), (8, 8, 32, 32), (8, 16, 64, 64),
+                                          (16, 4, 128, 128), (16, 16, 128, 128), (4, 4, 128, 128),
+                                          (4, 8, 128, 64), (4, 16, 128, 128), (16, 8, 128, 32),
+                                          (8, 8, 128, 16)])
+def test_fused_rows_mixed(kb, vb, gs, vgs):
     K = _k()
-    print(f"[case] mixed ({kb},{vb}) gs={gs}", flush=True)
-    g = gen(90 + kb + vb + gs)
+    print(f"[case] mixed ({kb},{vb}) gs={gs} vgs={vgs}", flush=True)
+    g = gen(90 + kb + vb + gs + vgs)
     B, H, Hq, S0, steps = 2, 2, 10, 95, 3
-    mk = lambda: K.MixedKVCache(1, device=DEV, k_group_size=gs, k_bits=kb, v_bits=vb, v_percentile=99.9)
+    mk = lambda: K.MixedKVCache(1, device=DEV, k_group_size=gs, v_group_size=vgs, k_bits=kb, v_bits=vb,
+                                v_percentile=99.9)
     one, two = mk(), mk()
     k, v = _kv(B, H, S0 + steps, g)
     for c in (one, two):
@@ -205,8 +208,12 @@ def test_fused_rows_mixed(kb, vb, gs):
         _equal(t1, two.get_mixed_tensors(0), f"mixed step {i}")
         assert torch.equal(out1, out2), f"mixed step {i}: fused output differs from two launches"
         kc, ksc, vc, vsc, vz = [None if t is None else t.cpu() for t in t1]
+        kz = one.get_k_zero_points(0)
+        if kz is not None:
+            assert torch.equal(kz, two.get_k_zero_points(0))
+            kz = kz.cpu()
         ref = OA.decode_attn_mixed_bits_ref(q, kc, kb, ksc, vc, vb, vsc, vz, torch.full((B,), n), sm,
-                                            inv_tau=tau)
+                                            inv_tau=tau, k_zp=kz)
         assert_close_ulp(out1, ref, f"mixed ({kb},{vb}) {n}")
 
 

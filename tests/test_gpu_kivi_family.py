@@ -175,14 +175,20 @@ def test_allocator_every_bit_pair():
     assert len(cache.to_tuple()) == L
 
 
-@pytest.mark.parametrize("kb,vb,gs,vp", [(8, 8, 32, 99.9), (8, 16, 64, 100.0), (16, 4, 128, 99.9),
-                                         (16, 16, 128, 100.0), (8, 4, 128, 99.9)])
-def test_mixed_cache_bit_pairs(kb, vb, gs, vp):
+@pytest.mark.parametrize("kb,vb,gs,vgs,vp,kp", [
+    (8, 8, 32, 32, 99.9, 99.9), (8, 16, 64, 64, 100.0, 99.9), (16, 4, 128, 128, 99.9, 99.9),
+    (16, 16, 128, 128, 100.0, 99.9), (8, 4, 128, 128, 99.9, 99.9),
+    # K at 4 bits (asymmetric per token, k_clip_percentile), fp16 K with INT8 V, and INT8 K and
+    # V with their own group sizes
+    (4, 4, 128, 128, 99.9, 99.9), (4, 8, 128, 32, 100.0, 99.0), (4, 16, 128, 128, 99.9, 100.0),
+    (16, 8, 128, 16, 99.9, 99.9), (8, 8, 128, 32, 99.9, 99.5), (8, 8, 16, 64, 100.0, 99.9)])
+def test_mixed_cache_bit_pairs(kb, vb, gs, vgs, vp, kp):
     K = _k()
-    print(f"[case] mixed ({kb},{vb}) gs={gs} vp={vp}", flush=True)
-    g = gen(900 + kb + vb + gs)
+    print(f"[case] mixed ({kb},{vb}) gs={gs} vgs={vgs} vp={vp} kp={kp}", flush=True)
+    g = gen(900 + kb + vb + gs + vgs)
     B, H, Hq, S0, steps = 2, 2, 10, 70, 3
-    cache = K.MixedKVCache(1, device=DEV, k_group_size=gs, k_bits=kb, v_bits=vb, v_percentile=vp)
+    cache = K.MixedKVCache(1, device=DEV, k_group_size=gs, v_group_size=vgs, k_bits=kb, v_bits=vb,
+                           v_percentile=vp, k_clip_percentile=kp)
     ks_, vs_ = [], []
     k0, v0 = _kv(B, H, S0, g)
     cache.append(0, k0.to(DEV), v0.to(DEV))
@@ -195,10 +201,16 @@ def test_mixed_cache_bit_pairs(kb, vb, gs, vp):
         vs_.append(v1)
     torch.cuda.synchronize()
     kc, ksc, vc, vsc, vz = [None if t is None else t.cpu() for t in cache.get_mixed_tensors(0)]
+    kz = None
     if kb == 8:
-        parts = [OQ.quantize_symmetric_int8(k, 99.9, gs) for k in ks_]
+        parts = [OQ.quantize_symmetric_int8(k, kp, gs) for k in ks_]
         assert torch.equal(kc, torch.cat([p[0] for p in parts], 2))
         assert torch.equal(ksc.float(), torch.cat([p[1] for p in parts], 2).float())
+    elif kb == 4:
+        kz = cache.get_k_zero_points(0).cpu()
+        parts = [OQ.quantize_asymmetric_per_token(k, 4, kp) for k in ks_]
+        assert torch.equal(kc, OQ.pack_int4(torch.cat([p[0] for p in parts], 2)))
+        assert torch.equal(ksc, torch.cat([p[1] for p in parts], 2)) and torch.equal(kz, torch.cat([p[2] for p in parts], 2))
     else:
         assert torch.equal(kc, torch.cat(ks_, 2))
     if vb == 4:
@@ -206,7 +218,7 @@ def test_mixed_cache_bit_pairs(kb, vb, gs, vp):
         assert torch.equal(vc, OQ.pack_int4(torch.cat([p[0] for p in parts], 2)))
         assert torch.equal(vsc, torch.cat([p[1] for p in parts], 2)) and torch.equal(vz, torch.cat([p[2] for p in parts], 2))
     elif vb == 8:
-        parts = [OQ.quantize_symmetric_int8(v, vp, gs) for v in vs_]
+        parts = [OQ.quantize_symmetric_int8(v, vp, vgs) for v in vs_]
         assert torch.equal(vc, torch.cat([p[0] for p in parts], 2))
         assert torch.equal(vsc.float(), torch.cat([p[1] for p in parts], 2).float())
     else:
@@ -217,7 +229,7 @@ def test_mixed_cache_bit_pairs(kb, vb, gs, vp):
     out = cache.decode_attn(0, q.to(DEV), inv_tau=tau.to(DEV))
     torch.cuda.synchronize()
     ref = OA.decode_attn_mixed_bits_ref(q, kc, kb, ksc, vc, vb, vsc, vz, torch.full((B,), n),
-                                        1 / math.sqrt(128), inv_tau=tau)
+                                        1 / math.sqrt(128), inv_tau=tau, k_zp=kz)
     assert_close_ulp(out, ref, f"mixed ({kb},{vb})")
     k_deq, v_deq = cache.get_kv(0)
     assert k_deq.shape == (B, H, n, 128) and v_deq.shape == (B, H, n, 128)

@@ -10,6 +10,7 @@ independent float64 brute force that unpacks the nibbles with integer arithmetic
 """
 import math
 
+import numpy as np
 import torch
 
 from oracle import attn as OA
@@ -203,3 +204,51 @@ def test_kivi_family_ref_brute_force_mixed_bits():
                         vv = (nib - 8) * float(vs[0, kh, t]) + float(vz[0, kh, t])
                     o += w[t] * vv
                 assert abs(o / tot - float(out[0, h, d])) <= 2e-3, (kb, vb, h, d)
+
+
+def test_mixed_bits_ref_k4_brute_force():
+    """decode_attn_mixed_bits_ref with a 4-bit K (MixedKVCache K at 4 bits: asymmetric per
+    token, src/cache/mixed_kv_cache.py:159-162, 186-188) against a float64 brute force that
+    unpacks the nibbles with integer arithmetic and rounds each dequantised K element to
+    fp16, with V at 8 bits (per-group scales) and at 16 bits.  A K dequantised per channel,
+    or without the zero-point, misses it."""
+    g = torch.Generator().manual_seed(45)
+    B, Hq, Hkv, S, D = 1, 4, 2, 9, 128
+    q = torch.randn(B, Hq, D, generator=g).to(torch.float16)
+    kp = torch.randint(0, 256, (B, Hkv, S, D // 2), generator=g, dtype=torch.uint8).view(torch.int8)
+    ks, kz = torch.rand(B, Hkv, S, generator=g) * 0.4 + 0.05, torch.randn(B, Hkv, S, generator=g)
+    v8 = torch.randint(-127, 128, (B, Hkv, S, D), generator=g, dtype=torch.int8)
+    vs8 = (torch.rand(B, Hkv, S, 4, generator=g) * 0.02 + 0.001).to(torch.float16)
+    v16 = torch.randn(B, Hkv, S, D, generator=g).to(torch.float16)
+    ctx = torch.tensor([8], dtype=torch.int32)
+    sm = 1 / math.sqrt(D)
+    for vb in (8, 16):
+        out = OA.decode_attn_mixed_bits_ref(q, kp, 4, ks, v8 if vb == 8 else v16, vb,
+                                            vs8 if vb == 8 else None, None, ctx, sm, k_zp=kz)
+        for h in range(Hq):
+            kh = h // 2
+            n = int(ctx[0])
+            logits = []
+            for t in range(n):
+                acc = 0.0
+                for d in range(D):
+                    byte = int(kp[0, kh, t, d // 2]) & 0xFF
+                    nib = (byte >> 4) if d % 2 == 0 else (byte & 15)
+                    kv = float(np.float16(np.float32((nib - 8) * np.float32(ks[0, kh, t]) +
+                                                     np.float32(kz[0, kh, t]))))
+                    acc += float(q[0, h, d]) * kv
+                logits.append(acc * sm)
+            mx = max(logits)
+            w = [math.exp(x - mx) for x in logits]
+            tot = sum(w)
+            for d in range(0, D, 11):
+                o = 0.0
+                for t in range(n):
+                    vv = (int(v8[0, kh, t, d]) * float(vs8[0, kh, t, d // 32])) if vb == 8 \
+                        else float(v16[0, kh, t, d])
+                    o += w[t] * vv
+                assert abs(o / tot - float(out[0, h, d])) <= 2e-3, (vb, h, d)
+    # the plausible mistakes: no zero-point, or the parameters taken per channel
+    bad = OA.decode_attn_mixed_bits_ref(q, kp, 4, ks, v16, 16, None, None, ctx, sm, k_zp=torch.zeros_like(kz))
+    good = OA.decode_attn_mixed_bits_ref(q, kp, 4, ks, v16, 16, None, None, ctx, sm, k_zp=kz)
+    assert (bad.float() - good.float()).abs().max() > 1e-2
