@@ -149,7 +149,8 @@ typedef struct kvq_decode_params {
      res_tokens, D] with dense 256-byte token rows, attended together with the row's
      quantized context (any order within the window).  0 = none.  KIVI-family formats
      (INT4_KIVI, INT8_KIVI, FP16) on the tiled kernel with at most 64 work-groups per
-     (b, kv head); at most 4096 tokens. */
+     (b, kv head); at most 65536 tokens (the merging work-group attends the window with VALU
+     dot products, so a long window lengthens the launch). */
   const void* res_k;
   const void* res_v;
   int64_t res_stride_b, res_stride_h;   /* elements */

@@ -763,13 +763,14 @@ class INT4KVCache(_SymCacheBase):
     ):
         if outlier_rescue_ratio < 0.0 or outlier_rescue_ratio > 1.0:
             raise ValueError(f"outlier_rescue_ratio must be in [0, 1], got {outlier_rescue_ratio}")
-        if not bit_packed:
-            raise NotImplementedError("the HIP INT4 engine stores bit-packed codes only")
         self._init_sym(num_layers, device, clip_percentile, group_size, dtype, max_seq_len,
                        decode_attn_impl, static_k_scale, static_v_scale, inv_tau,
                        use_attn_temperature, adaptive_static_scales, adaptive_static_margin,
                        adaptive_static_k, adaptive_static_v, check_numerics)
-        self.bit_packed = True
+        # The codes are stored packed either way (the kernels read them so); with
+        # bit_packed=False get_int4_tensors returns them unpacked, one int8 code per channel,
+        # as the reference's unpacked cache does (src/cache/int4_cache.py:531-537, 623-625).
+        self.bit_packed = bool(bit_packed)
         self.outlier_rescue_ratio = float(outlier_rescue_ratio)
         self.mixed_rescue = bool(mixed_rescue)
 
@@ -837,8 +838,14 @@ class INT4KVCache(_SymCacheBase):
                     f"because no static {side} scale is provided.", RuntimeWarning)
 
     def get_int4_tensors(self, layer_id: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
-        """(k_packed, v_packed, k_scale, v_scale): packed [B,H,S,D/2], fp32 scales [B,H,S,G]."""
-        return self._raw_views(layer_id)
+        """(k, v, k_scale, v_scale) over the stored tokens, fp32 scales [B,H,S,G]: with
+        bit_packed the packed codes [B,H,S,D/2] (views of the cache), else the codes unpacked
+        to int8 [B,H,S,D] in [-8, 7] (new tensors, which decode_attn_int4(bit_packed=False)
+        takes)."""
+        kc, vc, ks, vs = self._raw_views(layer_id)
+        if self.bit_packed:
+            return kc, vc, ks, vs
+        return _unpack(kc), _unpack(vc), ks, vs
 
     def get_kv(self, layer_id: int) -> Tuple[Tensor, Tensor]:
         kc, vc, ks, vs = self._raw_views(layer_id)
@@ -1244,8 +1251,9 @@ class _KiviFamily(_EngineBase):
         self.dtype = dtype
         self.k_percentile, self.v_percentile = float(k_percentile), float(v_percentile)
         self.residual_length = max(0, int(residual_length))
-        if self.residual_length > 4096:
-            raise NotImplementedError("residual_length above 4096 is not built")
+        if self.residual_length > 65536:
+            raise NotImplementedError("residual_length above 65536 is not built (the decode "
+                                      "kernel attends the fp16 window in one work-group)")
         # fp16 residual window (kivi_style_cache.py:102-113): per layer a ring of the
         # residual_length most recent decode tokens, _res_len of them valid, the oldest at
         # _res_start once the ring is full

@@ -648,6 +648,10 @@ static bool kivi_k_per_token(const kvq_kv_view& v) {
   return v.scale_stride_t == 1 && v.scale_stride_g == 0;
 }
 
+// the longest fp16 residual window: the merging work-group attends it with VALU dot products
+// (16 tokens per batch), so its time grows with the window (about 1 us per 256 tokens)
+constexpr int kMaxResidual = 65536;
+
 static int tok_family(const kvq_decode_params* p) {
   if (p->v.layout != KVQ_LAYOUT_ROWS) return kTiledNone;
   const bool kivi_v = p->k_format == KVQ_FMT_INT8_SYM &&
@@ -1063,8 +1067,8 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   a.rsb = a.rsh = 0;
   a.res_n = 0;
   if (p->res_tokens != 0) {
-    if (p->res_tokens < 0 || p->res_tokens > 4096)
-      return fail(KVQ_ERR_INVALID, "res_tokens must lie in [0, 4096]");
+    if (p->res_tokens < 0 || p->res_tokens > kMaxResidual)
+      return fail(KVQ_ERR_INVALID, "res_tokens must lie in [0, " + std::to_string(kMaxResidual) + "]");
     if (!tiled || !kivi_fmt(kf) || !kivi_fmt(vf))
       return fail(KVQ_ERR_UNSUPPORTED,
                   "the fp16 residual window needs KIVI-family formats (INT4_KIVI, INT8_KIVI, FP16)");

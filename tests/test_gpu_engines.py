@@ -429,3 +429,39 @@ def test_mixed_cache_append_bitexact_and_decode(k_gs, pct, S0, Hq):
     ref = OA.decode_attn_mixed_ref(q, kc, ksc, OQ.unpack_int4(vp), vsc, vz, torch.full((B,), n), 1 / math.sqrt(128),
                                    inv_tau=tau)
     assert_close_ulp(out, ref, f"mixed gs{k_gs} S{n}")
+
+
+def test_int4_engine_unpacked_view():
+    """INT4KVCache(bit_packed=False) (src/cache/int4_cache.py:55, 531-537, 623-625): the same
+    codes as the packed engine, returned unpacked by get_int4_tensors (int8 codes in [-7, 7],
+    [B, H, S, D]), which decode_attn_int4(bit_packed=False) takes; the decode step gives the
+    packed engine's bits."""
+    K = _k()
+    g = gen(410)
+    B, H, Hq, S = 2, 2, 12, 90
+    st = torch.rand(1, H, 4, generator=g) * 0.5 + 0.05
+    caches = [K.INT4KVCache(1, device=DEV, group_size=32, static_k_scale=st.to(DEV), static_v_scale=st.to(DEV),
+                            bit_packed=bp, check_numerics=False) for bp in (True, False)]
+    k, v = _kv(B, H, S + 1, g)
+    for c in caches:
+        c.append(0, k[:, :, :S].to(DEV), v[:, :, :S].to(DEV))
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.float16).to(DEV)
+    outs = [c.append_decode_attn(0, q, k[:, :, S:].to(DEV), v[:, :, S:].to(DEV)) for c in caches]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    kp, vp, ks, vs = caches[0].get_int4_tensors(0)
+    ku, vu, ks2, vs2 = caches[1].get_int4_tensors(0)
+    assert ku.dtype == torch.int8 and ku.shape == (B, H, S + 1, 128) and caches[1].bit_packed is False
+    assert torch.equal(ku.cpu(), OQ.unpack_int4(kp.cpu())) and torch.equal(vu.cpu(), OQ.unpack_int4(vp.cpu()))
+    assert int(ku.abs().max()) <= 7 and torch.equal(ks, ks2) and torch.equal(vs, vs2)
+    ctx = torch.full((B,), S + 1, dtype=torch.int32, device=DEV)
+    # the kernel wrappers take fp16 scales, as the reference's (the hook casts the engines' fp32)
+    ks16, vs16 = ks.half(), vs.half()
+    a = K.decode_attn_int4(q, kp, vp, ks16, vs16, ctx, 1 / math.sqrt(128), bit_packed=True)
+    b = K.decode_attn_int4(q, ku, vu, ks2.half(), vs2.half(), ctx, 1 / math.sqrt(128), bit_packed=False)
+    torch.cuda.synchronize()
+    ref = OA.decode_attn_int4_torch_ref(q.cpu(), kp.cpu(), vp.cpu(), ks16.cpu(), vs16.cpu(), ctx.cpu(),
+                                        1 / math.sqrt(128))
+    assert_close_ulp(a, ref, "int4 packed")
+    assert_close_ulp(b, ref, "int4 unpacked")
+    assert torch.equal(caches[0].get_kv(0)[0], caches[1].get_kv(0)[0])

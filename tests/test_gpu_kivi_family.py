@@ -253,7 +253,7 @@ def test_fp16_pair_partial_tile_ignores_stale_rows():
     assert_close_ulp(out, ref, "fp16 stale tail")
 
 
-@pytest.mark.parametrize("bits,R,extra", [(4, 32, 5), (8, 16, 40), (4, 128, 0)])
+@pytest.mark.parametrize("bits,R,extra", [(4, 32, 5), (8, 16, 40), (4, 128, 0), (4, 4200, 3)])
 def test_kivi_residual_window(bits, R, extra):
     """residual_length R (src/cache/kivi_style_cache.py:102-113, 354-404): after the prefill,
     decode tokens fill an fp16 window of R; each later token evicts the oldest into the
