@@ -114,10 +114,16 @@ typedef struct kvq_kv_view {
  * require group_size in {8, 16, 32, 64, 128}.
  *
  * Kernel choice (the same results either way, within the stated tolerance): the tiled
- * kernel (8-wave work-groups, single-launch merge of the split partials) serves INT4_ASYM K
- * with TILE32 V, and INT8_SYM K whose scale view is static (stride 0, or size 1, over b and
- * t; group 32; 128-byte dense rows) with TILE32 INT4_ASYM V or a static INT8_SYM V in dense
- * rows.  Every other combination runs the row-layout split-K kernel and a combine launch.
+ * kernel (8-wave work-groups, single-launch merge of the split partials) serves
+ *  - INT4_ASYM K with TILE32 V;
+ *  - INT8_SYM K whose scale view is static (stride 0, or size 1, over b and t; 128-byte dense
+ *    rows) with TILE32 INT4_ASYM V (group 32) or a static INT8_SYM V in dense rows (any
+ *    group size);
+ *  - per-token INT8_SYM / INT4_SYM scales on both sides in dense rows (groups of 16 or more),
+ *    INT8_SYM K with per-token scales and INT4_KIVI or FP16 V;
+ *  - the KIVI family (INT4_KIVI, INT8_KIVI, FP16 on either side), per-token INT4_KIVI K with
+ *    INT4_KIVI, INT8_SYM or FP16 V, and FP16 K with INT8_SYM V.
+ * Every other combination runs the row-layout split-K kernel and a combine launch.
  */
 typedef struct kvq_decode_params {
   const void* q;          /* fp16 [B, Hq, D], d contiguous */

@@ -326,6 +326,39 @@ def test_decode_int8_static_tiled(B, Hq, Hkv, S, ctx):
             assert torch.all(out[b] == 0)
 
 
+def test_cfg1_every_layer():
+    """Configuration 1 (Qwen2.5-1.5B shape, INT8 static g32 tables, B 4, 8k) on each of its 28
+    layers: that layer's seeded K / V and calibration tables, the cache built by the HIP
+    append (INT8KVCache), then one fused decode step (append of token 8192 + attention) with
+    the layer's inverse temperatures.  Codes of the new token bit-exact with the oracle's
+    quantizer; outputs of rows 0 and 3 within the bound of the oracle's attention."""
+    K = _lib()
+    from llm_kvcache_quantization_amd import synthetic as SY
+
+    cfg = SY.CONFIGS[1]
+    taus = SY.inv_tau(cfg)
+    S, B = cfg.context, cfg.batch
+    sm = 1 / math.sqrt(128)
+    for layer in range(cfg.layers):
+        t = SY.calibrate(cfg, layer)
+        g = gen(SY.seed_for(1, layer))
+        k, v = SY.draw_kv(cfg, layer, B, S, g)
+        q = SY.draw_q(cfg, B, g)
+        cache = K.INT8KVCache(1, device=DEV, group_size=32, static_k_scale=t.k_scale[None].to(DEV),
+                              static_v_scale=t.v_scale[None].to(DEV), check_numerics=False)
+        cache.append(0, k[:, :, :S - 1].to(DEV), v[:, :, :S - 1].to(DEV))
+        out = cache.append_decode_attn(0, q.to(DEV), k[:, :, S - 1:].to(DEV), v[:, :, S - 1:].to(DEV),
+                                       sm, inv_tau=taus[layer].to(DEV))
+        kc, vc, ks, vs = [x.cpu() for x in cache.get_int8_tensors(0)]
+        rk, _ = OQ.quantize_symmetric_int8_with_scale(k[:, :, S - 1:], t.k_scale, 32)
+        rv, _ = OQ.quantize_symmetric_int8_with_scale(v[:, :, S - 1:], t.v_scale, 32)
+        assert torch.equal(kc[:, :, S - 1:], rk) and torch.equal(vc[:, :, S - 1:], rv), layer
+        rows = [0, 3]
+        ref = OA.decode_attn_int8_torch_ref(OA.prescale_q(q[rows], taus[layer]), kc[rows], vc[rows],
+                                            ks[rows], vs[rows], torch.full((2,), S, dtype=torch.int32), sm)
+        assert_close(out[rows], ref, f"cfg1 layer {layer}")
+
+
 @pytest.mark.parametrize("G,B,Hq,Hkv,S,ctx", [
     (8, 4, 12, 2, 8192, [8192, 8191, 4097, 33]),   # group 16 (the shipped int8_ours tables)
     (16, 3, 12, 2, 700, [700, 1, 0]),              # group 8
