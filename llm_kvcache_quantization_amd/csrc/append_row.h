@@ -216,14 +216,15 @@ __device__ __forceinline__ float row_static(const AppendDev& a, int row, int lan
   return ld_static(a, (row / a.S) % a.H, (2 * lane) / a.gs);
 }
 
-// Quantizes append row `row` whose lane values xv (and static scale stv, row_static) were
-// loaded by the caller.
-__device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lane, float thr,
-                                            half2v xv, float stv) {
+// Quantizes append row `row` = (b * H + h) * S + s_idx whose lane values xv (and static
+// scale stv, row_static) were loaded by the caller.  FMT: the side's format when the caller
+// knows it at compile time (the fused decode step's writer: only that format's code is
+// built into its kernel), or -1 for a.fmt.
+template <int FMT = -1>
+__device__ __forceinline__ void quant_row_bhs(const AppendDev& a, int b, int h, int s_idx, int row,
+                                              int lane, float thr, half2v xv, float stv) {
 #pragma clang fp contract(off)
-  const int s_idx = row % a.S;
-  const int bh = row / a.S;
-  const int h = bh % a.H, b = bh / a.H;
+  const int fmt = FMT >= 0 ? FMT : a.fmt;
   const int64_t t = a.wpos + s_idx;
   const half_t* xr = row_x(a, row);
   const float x0 = (float)xv.x, x1 = (float)xv.y;
@@ -237,13 +238,13 @@ __device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lan
 
   // the group's absmax, or for a percentile-clipped dynamic scale its quantile of |x|
   const bool pct = a.st == nullptr && a.dq > 0.f &&
-                   (a.fmt == KVQ_FMT_INT8_SYM || a.fmt == KVQ_FMT_INT4_SYM);
+                   (fmt == KVQ_FMT_INT8_SYM || fmt == KVQ_FMT_INT4_SYM);
   const float am = pct ? group_quantile(fabsf(x0), fabsf(x1), a.gs, a.dq, lane)
                        : group_max(fmaxf(fabsf(x0), fabsf(x1)), a.gs);
   uint8_t* crow = a.codes + (int64_t)b * a.csb + (int64_t)h * a.csh + t * a.cst;
   int clipped = 0;
 
-  if (a.fmt == KVQ_FMT_INT8_SYM) {
+  if (fmt == KVQ_FMT_INT8_SYM) {
     const half_t s16 = int8_scale16(a, stv, am);
     const float sf = (float)s16;
     *reinterpret_cast<uint16_t*>(crow + d0) = int8_pack_pair(x0, x1, s16, clipped);
@@ -254,7 +255,7 @@ __device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lan
       if (a.so_f32) reinterpret_cast<float*>(a.so)[off] = sf;
       else reinterpret_cast<half_t*>(a.so)[off] = s16;
     }
-  } else if (a.fmt == KVQ_FMT_INT4_SYM) {
+  } else if (fmt == KVQ_FMT_INT4_SYM) {
     float s;
     if (a.st == nullptr) {
       // the fp16 absmax clamped in fp16, or the fp32 quantile clamped in fp32, then divided
@@ -275,9 +276,9 @@ __device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lan
       if (a.so_f32) reinterpret_cast<float*>(a.so)[off] = s;
       else reinterpret_cast<half_t*>(a.so)[off] = (half_t)s;
     }
-  } else if (a.fmt == KVQ_FMT_INT4_KIVI || a.fmt == KVQ_FMT_INT8_KIVI) {
+  } else if (fmt == KVQ_FMT_INT4_KIVI || fmt == KVQ_FMT_INT8_KIVI) {
     // asymmetric_quant.py:24-141 with qmin, qmax = -8, 7 (4 bits) or -128, 127 (8 bits)
-    const bool b8 = a.fmt == KVQ_FMT_INT8_KIVI;
+    const bool b8 = fmt == KVQ_FMT_INT8_KIVI;
     const float qmin = b8 ? -128.f : -8.f, qmax = b8 ? 127.f : 7.f;
     float s0, s1, z0, z1;
     if (a.st != nullptr) {
@@ -322,7 +323,7 @@ __device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lan
       *reinterpret_cast<uint16_t*>(crow + d0) = (uint16_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8));
     else
       crow[lane] = (uint8_t)(((q0 + 8) << 4) | (q1 + 8));
-  } else if (a.fmt == KVQ_FMT_FP16) {  // a 16-bit side stores the row as it comes
+  } else if (fmt == KVQ_FMT_FP16) {  // a 16-bit side stores the row as it comes
     *reinterpret_cast<half2v*>(crow + 4 * lane) = xv;
   } else {  // KVQ_FMT_INT4_ASYM, static parameters
     const int64_t off = (int64_t)h * a.st_sh + (int64_t)g * a.st_sg;
@@ -342,6 +343,14 @@ __device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lan
   // clipped-element count (int8_cache.py:407-419, int4_cache.py:468-485)
   for (int o = 32; o > 0; o >>= 1) clipped += __shfl_xor(clipped, o, 64);
   if (lane == 0 && a.status && clipped) atomicAdd(&a.status[1], clipped);
+}
+
+template <int FMT = -1>
+__device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lane, float thr,
+                                            half2v xv, float stv) {
+  const int s_idx = row % a.S;
+  const int bh = row / a.S;
+  quant_row_bhs<FMT>(a, bh / a.H, bh % a.H, s_idx, row, lane, thr, xv, stv);
 }
 
 // group_max for values >= +0 (absolute values: the order of the maxima cannot change a bit)

@@ -735,7 +735,7 @@ static int tiled_family(const kvq_decode_params* p) {
 // the split-K kernel kvq_decode_attn launches for p (nullptr if unsupported)
 static const void* kernel_for(const kvq_decode_params* p) {
   const int fam = tiled_family(p);
-  if (fam != kTiledNone) return tiled_kernel(fam, p->q_heads / p->kv_heads);
+  if (fam != kTiledNone) return tiled_kernel(fam, p->q_heads / p->kv_heads).fn;
   if (p->v.layout == KVQ_LAYOUT_TILE32) return nullptr;
   return select_kernel(family(p->k_format, p->v_format, p->k.scale_dtype == KVQ_DTYPE_F32,
                               p->v.scale_dtype == KVQ_DTYPE_F32, p->k.n_outlier > 0));
@@ -1103,7 +1103,11 @@ static int decode_impl(const kvq_decode_params* p, const FusedAppend* app, kvq_s
   if (tiled) {
     const dim3 grid = sp.share ? dim3((unsigned)sp.grid_x, (unsigned)p->kv_heads, 1u)
                                : dim3((unsigned)nch64, (unsigned)p->kv_heads, (unsigned)p->batch);
-    const hipError_t e = launch_tiled(a, tfam, grid, s);
+    const TiledFn k = tiled_kernel(tfam, a.n_rep);
+    // the kernel's writer quantizes the formats it was built for
+    if (rk && k.fn && (rk->fmt != k.kfmt || rv->fmt != k.vfmt))
+      return fail(KVQ_ERR_UNSUPPORTED, "the fused append's formats differ from the kernel's");
+    const hipError_t e = launch_tiled(a, k, grid, s);
     if (e != hipSuccess) return fail(KVQ_ERR_LAUNCH, std::string("launch: ") + hipGetErrorString(e));
     if (a.fused) return KVQ_OK;  // one launch: the last work-group of each (b, kv head) merged
   } else if (p->capacity > 0) {

@@ -94,8 +94,13 @@ struct DecodeArgs {
 };
 
 // context length of batch row b, clamped to [0, capacity]
+// b uniform: the length is read through the scalar cache (a constant-address load), whose
+// wait does not include the vector loads issued before it (a vector load here would make
+// the wave wait for the q-side loads before it requests its first cache tiles).  Nothing
+// in a launch writes the lengths.
 __device__ __forceinline__ int64_t row_context(const DecodeArgs& a, int b) {
-  const int64_t c = a.ctx != nullptr ? (int64_t)a.ctx[b] : (int64_t)a.ctx_uniform;
+  using cint = const __attribute__((address_space(4))) int32_t;
+  const int64_t c = a.ctx != nullptr ? (int64_t)((cint*)a.ctx)[b] : (int64_t)a.ctx_uniform;
   return c < 0 ? 0 : (c > a.cap ? a.cap : c);
 }
 
@@ -446,14 +451,19 @@ enum TiledFam {
   kTiledKtKv, kTiledKtT8, kTiledKtF,
   kTiledFT8,    // FP16 K, INT8_SYM V with per-token fp16 scales (MixedKVCache (16, 8))
 };
-// kernel of family fam for n_rep query heads per kv head, or nullptr
-const void* tiled_kernel(int fam, int n_rep);
-// the instantiations, one lookup per translation unit (nullptr: not one of its families)
-const void* tiled_kernel_a4(int fam, bool pack8);
-const void* tiled_kernel_tok(int fam, bool pack8);
-const void* tiled_kernel_kv4(int fam, bool pack8);
-const void* tiled_kernel_kv16(int fam, bool pack8);
-const void* tiled_kernel_kt(int fam, bool pack8);
-hipError_t launch_tiled(const DecodeArgs& a, int fam, dim3 grid, hipStream_t s);
+// a tiled kernel and the formats of the fused row append built into it (-1: none)
+struct TiledFn {
+  const void* fn;
+  int kfmt, vfmt;
+};
+// the instantiations, one lookup per translation unit (fn nullptr: not one of its families)
+TiledFn tiled_kernel_a4(int fam, bool pack8);
+TiledFn tiled_kernel_tok(int fam, bool pack8);
+TiledFn tiled_kernel_kv4(int fam, bool pack8);
+TiledFn tiled_kernel_kv16(int fam, bool pack8);
+TiledFn tiled_kernel_kt(int fam, bool pack8);
+// kernel of family fam for n_rep query heads per kv head (fn nullptr if none)
+TiledFn tiled_kernel(int fam, int n_rep);
+hipError_t launch_tiled(const DecodeArgs& a, const TiledFn& k, dim3 grid, hipStream_t s);
 
 }  // namespace kvq

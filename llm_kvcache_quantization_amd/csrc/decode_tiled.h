@@ -316,6 +316,10 @@ __device__ __forceinline__ void split_h(float x, half_t& hi, half_t& lo) {
 // inverse temperature and the K scale / zero-point of group lg.  They are fetched before
 // the first cache loads, so waiting for them does not wait for those (vmcnt counts loads
 // in issue order).
+__device__ __forceinline__ int4 clamp_ch4(int4 o) {
+  return int4{min(max(o.x, 0), kD - 1), min(max(o.y, 0), kD - 1), min(max(o.z, 0), kD - 1),
+              min(max(o.w, 0), kD - 1)};
+}
 struct QIn {
   u32x4 q;
   half_t tau, s, z;
@@ -333,6 +337,7 @@ struct QIn {
 // and q' of those channels in the first two k-slots of each lane group.
 template <bool OUT>
 struct KAsymT {
+  static constexpr int kRowFmt = -1;  // no row append
   static constexpr int kMergeBatch = 8;
   // hi / lo probabilities in one PV MFMA (softmax_tile8c) when the V format allows it:
   // measured 0.2 us faster at configs 2-3; with static INT8 K (short per-wave runs at
@@ -379,11 +384,9 @@ struct KAsymT {
     in.s = reinterpret_cast<const half_t*>(a.k.scale)[hkv * a.k.ssh + lg * a.k.ssg];
     in.z = a.k.zp[hkv * a.k.ssh + lg * a.k.ssg];
     in.oc = int4{-1, -1, -1, -1};
-    if constexpr (OUT) {
-      const int4 o = *reinterpret_cast<const int4*>(a.k.oidx + hkv * 4);
-      in.oc = int4{min(max(o.x, 0), kD - 1), min(max(o.y, 0), kD - 1), min(max(o.z, 0), kD - 1),
-                   min(max(o.w, 0), kD - 1)};
-    }
+    // raw indices: each use clamps them to [0, kD - 1] (arithmetic on a loaded value here
+    // would make every wave wait for the q loads before it requests its first tiles)
+    if constexpr (OUT) in.oc = *reinterpret_cast<const int4*>(a.k.oidx + hkv * 4);
   }
 
   // q-dependent operands of channel slice j = 0..3 (channels 32 lg + 8 j + e), shared
@@ -399,6 +402,7 @@ struct KAsymT {
     const float s = (float)in.s;
     const float z = (float)in.z;
     float part = 0.f;
+    const int4 oc = clamp_ch4(in.oc);
     half_t vh[8], qs[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -409,7 +413,7 @@ struct KAsymT {
     for (int k = 0; k < 8; ++k) {
       const int e = slot_elem(k);
       const int d = 32 * lg + 8 * j + e;
-      const bool use = d != in.oc.x && d != in.oc.y && d != in.oc.z && d != in.oc.w;
+      const bool use = !OUT || (d != oc.x && d != oc.y && d != oc.z && d != oc.w);
       const float qd = use ? (float)qs[e] : 0.f;
       const float P = qd * s;  // exact: 11-bit x 11-bit significands
       const half_t h = (half_t)(slot_high(k) ? P * 0.0625f : P);
@@ -434,7 +438,8 @@ struct KAsymT {
     if constexpr (OUT) {
       // lane group lg supplies outlier channels 2 (lg & 1) and 2 (lg & 1) + 1
       const bool odd = ((lane >> 4) & 1) != 0;
-      qo = half8v{sh.qv[col][odd ? in.oc.z : in.oc.x], sh.qv[col][odd ? in.oc.w : in.oc.y],
+      const int4 oc = clamp_ch4(in.oc);
+      qo = half8v{sh.qv[col][odd ? oc.z : oc.x], sh.qv[col][odd ? oc.w : oc.y],
                   h0, h0, h0, h0, h0, h0};
     }
   }
@@ -487,6 +492,7 @@ struct KAsymT {
 // x = 16 n 2^-24 (even c, high nibble) or n 2^-24 (odd c) and p the hi + lo probability
 // operands (softmax_tile); the epilogue applies out = s (acc / l * 2^20 or 2^24 - 8) + z.
 struct VAsymT {
+  static constexpr int kRowFmt = -1;  // no row append
   static constexpr bool kResidual = false;  // merges an fp16 residual window
   static constexpr bool kTile32 = true;
   static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
@@ -586,6 +592,7 @@ __device__ __forceinline__ uint32_t i8pair_deq(uint32_t x, half2v s2) {
 // reference's fp32 dot products of fp16 k and q up to the summation order.
 template <bool GS_ANY>
 struct KI8T {
+  static constexpr int kRowFmt = -1;  // no row append
   static constexpr bool kGsAny = GS_ANY;
   static constexpr int kMergeBatch = 32;
   static constexpr bool kPackPV = false;
@@ -688,6 +695,7 @@ struct KI8T {
 // acc / l is the output.
 template <bool GS_ANY>
 struct VI8RowT {
+  static constexpr int kRowFmt = -1;  // no row append
   static constexpr bool kResidual = false;  // merges an fp16 residual window
   static constexpr bool kPackedPV = true;  // mma1 with softmax_tile8c's operand
   static constexpr bool kTile32 = false;
@@ -777,6 +785,7 @@ struct KiviQIn {
 // magnitude above the rest, where one fp16 rounding of q'_d s_d (2^-11 of the term) would
 // show in the logits.  The constant term sum_d q'_d (z_d - 8 s_d) is summed in fp32.
 struct KKiviT : KAsymT<false> {
+  static constexpr int kRowFmt = KVQ_FMT_INT4_KIVI;  // the fused append's K format
   using QInT = KiviQIn;
   static constexpr bool kAppend = false;
   static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
@@ -858,6 +867,7 @@ struct KKiviT : KAsymT<false> {
 // the token's s and z (one dword each per row block), byte to float by v_cvt_f32_ubyte, one
 // fma, round to nearest fp16.  The B operand is q' in channel order.  Logits at unit scale.
 struct KTokAsymT : KAsymT<false> {
+  static constexpr int kRowFmt = KVQ_FMT_INT4_KIVI;  // the fused append's K format
   static constexpr bool kAppend = false;
   static constexpr bool kAppendRow = true;  // the writer runs quant_row_x (fused step)
   static constexpr bool kRescue = false;     // (no INT4_SYM side)
@@ -956,6 +966,7 @@ struct KTokAsymT : KAsymT<false> {
 // reference dequantises V in fp32).  The wave keeps Lp and Cz beside l (the softmax
 // rescales them with l) and finalize() folds them into acc before the merge (out = acc / l).
 struct VKiviRowT {
+  static constexpr int kRowFmt = KVQ_FMT_INT4_KIVI;  // the fused append's V format
   static constexpr bool kResidual = true;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
@@ -1094,6 +1105,7 @@ __device__ __forceinline__ uint32_t i8pair_exact(uint32_t x) {
 // MFMAs per slice, as KKiviT), and the constant sum_d q'_d z_d starts the accumulator.
 // Lane (row, lg) of row block rb reads bytes [32 lg, 32 lg + 32) of token 16 rb + row.
 struct KKivi8T {
+  static constexpr int kRowFmt = KVQ_FMT_INT8_KIVI;  // the fused append's K format
   static constexpr int kMergeBatch = 8;
   static constexpr bool kPackPV = false;
   using QInT = KiviQIn;
@@ -1196,6 +1208,7 @@ struct KKivi8T {
 // the stored fp16 k with q' = fp16(q * inv_tau).  Lane (row, lg) of row block rb reads bytes
 // [64 lg, 64 lg + 64) of token 16 rb + row: channels 32 lg + 8 j .. + 7 are slice j.
 struct KF16T {
+  static constexpr int kRowFmt = KVQ_FMT_FP16;  // the fused append's K format
   static constexpr int kMergeBatch = 8;
   static constexpr bool kPackPV = false;
   using QInT = QIn;
@@ -1275,6 +1288,7 @@ struct KF16T {
 // (i8pair_exact), the B operand is w = p s_t as a hi + lo pair (two MFMAs per channel), and
 //   sum_t p v = sum_t w c + Cz,   Cz = sum_t p z_t (fp32, rescaled with l by the softmax).
 struct VKivi8RowT {
+  static constexpr int kRowFmt = KVQ_FMT_INT8_KIVI;  // the fused append's V format
   static constexpr bool kResidual = true;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
@@ -1387,6 +1401,7 @@ struct VKivi8RowT {
 // 8 col + c is the stored v of the 8 tokens (one v_perm_b32 per token pair), so acc / l is
 // the output.
 struct VF16RowT {
+  static constexpr int kRowFmt = KVQ_FMT_FP16;  // the fused append's V format
   static constexpr bool kResidual = true;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
@@ -1464,6 +1479,7 @@ __device__ __forceinline__ uint32_t scale_bytes(int64_t cap, int64_t sst, int gs
 
 template <bool I4, int NS>
 struct KTokT {
+  static constexpr int kRowFmt = I4 ? KVQ_FMT_INT4_SYM : KVQ_FMT_INT8_SYM;  // the fused append's K format
   static_assert(NS == 1 || NS == 2, "groups of 16 or more");
   static constexpr int kMergeBatch = 16;
   static constexpr bool kPackPV = false;
@@ -1608,6 +1624,7 @@ struct KTokT {
 // (channel 8 col + c) is vhat = fp16(c * fp16(s)) of the 8 tokens, so acc / l is the output.
 template <bool I4>
 struct VTokT {
+  static constexpr int kRowFmt = I4 ? KVQ_FMT_INT4_SYM : KVQ_FMT_INT8_SYM;  // the fused append's V format
   static constexpr bool kResidual = false;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
@@ -1723,24 +1740,35 @@ struct VTokT {
 // TILE32 bytes or its row.  The other waves issue nothing for it (even out-of-range memory
 // operations would occupy their address unit ahead of their first cache loads).  NaN / Inf
 // set status[0] and clamped elements are added to status[1] (per side).
+// Loaded bits only: a conversion at the fetch would make the writer wait there for every
+// load issued before (the first cache tiles), ahead of the work-group's set-up barrier.
 struct AppendIn {
   uint32_t k2, v2;  // fp16 pair of channels 2 lane, 2 lane + 1
   uint32_t o;       // lanes < 4: fp16 K value of outlier channel lane (INT4_ASYM K)
-  float ks;         // INT8 K: the fp16 scale of the group of channels 2 lane, 2 lane + 1
-  float vs, vz;     // V: INT8 fp16 scale of that group, or INT4_ASYM scale / zero-point of
-                    // group lane / 16
+  uint32_t ks;      // INT8 K: the table entry of the group of channels 2 lane, 2 lane + 1
+  uint32_t vs, vz;  // V: INT8 table entry of that group, or INT4_ASYM fp16 scale /
+                    // zero-point of group lane / 16
 };
 struct AppendFlags {
   bool kbad = false, vbad = false;
   int kclip = 0, vclip = 0;
 };
 
-// fp16 scale of group g of the append's static INT8 table tab (fp32 when f32)
-__device__ __forceinline__ float app_int8_scale(const void* tab, int f32, int64_t sh, int64_t sg,
-                                                int hkv, int g) {
+// entry of group g of the append's static INT8 table tab (fp32 bits when f32, else fp16)
+__device__ __forceinline__ uint32_t app_int8_entry(const void* tab, int f32, int64_t sh,
+                                                   int64_t sg, int hkv, int g) {
   const int64_t i = (int64_t)hkv * sh + (int64_t)g * sg;
-  const float s = f32 ? reinterpret_cast<const float*>(tab)[i] : (float)reinterpret_cast<const half_t*>(tab)[i];
+  return f32 ? reinterpret_cast<const uint32_t*>(tab)[i]
+             : (uint32_t)reinterpret_cast<const uint16_t*>(tab)[i];
+}
+// its fp16 scale
+__device__ __forceinline__ float app_int8_scale(uint32_t e, int f32) {
+  const float s = f32 ? __builtin_bit_cast(float, e)
+                      : (float)__builtin_bit_cast(half_t, (uint16_t)e);
   return (float)int8_static_scale16(s, f32 != 0);
+}
+__device__ __forceinline__ float h16(uint32_t e) {
+  return (float)__builtin_bit_cast(half_t, (uint16_t)e);
 }
 
 // oc: the kv head's 4 outlier channels (from the q set-up's inputs); called by the writer
@@ -1755,22 +1783,23 @@ __device__ __forceinline__ void append_fetch(const DecodeArgs& a, int b, int hkv
   in.v2 = bload1(rv, 4u * lane, 0);
   in.o = 0;
   if constexpr (KF::kOut) {
-    const int ch = lane == 0 ? oc.x : lane == 1 ? oc.y : lane == 2 ? oc.z : oc.w;
+    const int4 c4 = clamp_ch4(oc);
+    const int ch = lane == 0 ? c4.x : lane == 1 ? c4.y : lane == 2 ? c4.z : c4.w;
     in.o = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
         rk, (int)(lane < 4 ? 2u * (uint32_t)ch : kOutOfRange), 0, kBufNT);
   }
   const int g = lane >> 4;  // group of 32
   int g8 = g;               // INT8 sides: the group of channels 2 lane, 2 lane + 1
   if constexpr (KF::kGsAny) g8 = (2 * lane) >> __builtin_ctz((unsigned)a.gs);
-  in.ks = 0.f;
-  if constexpr (!KF::kAsym) in.ks = app_int8_scale(f.kst, f.kst_f32, f.kst_sh, f.kst_sg, hkv, g8);
+  in.ks = 0;
+  if constexpr (!KF::kAsym) in.ks = app_int8_entry(f.kst, f.kst_f32, f.kst_sh, f.kst_sg, hkv, g8);
   if constexpr (VF::kTile32) {
     // V scale / zero-point of group lane / 16 (fp16, element offsets hkv * ssh + g * ssg)
-    in.vs = (float)reinterpret_cast<const half_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
-    in.vz = (float)a.v.zp[hkv * a.v.ssh + g * a.v.ssg];
+    in.vs = reinterpret_cast<const uint16_t*>(a.v.scale)[hkv * a.v.ssh + g * a.v.ssg];
+    in.vz = reinterpret_cast<const uint16_t*>(a.v.zp)[hkv * a.v.ssh + g * a.v.ssg];
   } else {
-    in.vs = app_int8_scale(f.vst, f.vst_f32, f.vst_sh, f.vst_sg, hkv, g8);
-    in.vz = 0.f;
+    in.vs = app_int8_entry(f.vst, f.vst_f32, f.vst_sh, f.vst_sg, hkv, g8);
+    in.vz = 0;
   }
 }
 
@@ -1786,14 +1815,16 @@ __device__ __forceinline__ void append_store(const DecodeArgs& a, const KF& kf, 
     const uint32_t kb = asym_pack_pair((float)k2.x, (float)k2.y, ks, kz, kclip);
     __builtin_amdgcn_raw_buffer_store_b8((uint8_t)kb, kf.rk, (int)(uint32_t)(t * kRowK + lane), 0, 0);
   } else {
-    const uint16_t kp = int8_pack_pair((float)k2.x, (float)k2.y, (half_t)in.ks, kclip);
+    const float ks = app_int8_scale(in.ks, a.app.kst_f32);
+    const uint16_t kp = int8_pack_pair((float)k2.x, (float)k2.y, (half_t)ks, kclip);
     __builtin_amdgcn_raw_buffer_store_b16(kp, kf.rk, (int)(uint32_t)(t * kD + 2 * lane), 0, 0);
   }
   if constexpr (VF::kTile32) {
-    const uint32_t vb = asym_pack_pair((float)v2.x, (float)v2.y, in.vs, in.vz, vclip);
+    const uint32_t vb = asym_pack_pair((float)v2.x, (float)v2.y, h16(in.vs), h16(in.vz), vclip);
     __builtin_amdgcn_raw_buffer_store_b8((uint8_t)vb, vf.rv, (int)(uint32_t)tile32_offset(t, lane), 0, 0);
   } else {
-    const uint16_t vp = int8_pack_pair((float)v2.x, (float)v2.y, (half_t)in.vs, vclip);
+    const float vs = app_int8_scale(in.vs, a.app.vst_f32);
+    const uint16_t vp = int8_pack_pair((float)v2.x, (float)v2.y, (half_t)vs, vclip);
     __builtin_amdgcn_raw_buffer_store_b16(vp, vf.rv, (int)(uint32_t)(t * kD + 2 * lane), 0, 0);
   }
   if constexpr (KF::kOut)
@@ -1829,7 +1860,10 @@ __device__ __forceinline__ void append_row_fetch(const DecodeArgs& a, int b, int
   p.sv = row_static(a.arv, row, lane);
 }
 // (the rescue is compiled only where it can occur: INT4_SYM K and V, RESCUE)
-template <bool RESCUE>
+// KFMT / VFMT: the sides' formats (the kernel's operand types; the host admits only appends
+// of those formats), so the writer's kernel holds only their quantizer code.  One token:
+// row b * H + hkv.
+template <bool RESCUE, int KFMT, int VFMT>
 __device__ __forceinline__ void append_row_pair(const DecodeArgs& a, int b, int hkv, int lane,
                                                 const RowPre& p, const RescueRows& rk,
                                                 const RescueRows& rv) {
@@ -1840,12 +1874,12 @@ __device__ __forceinline__ void append_row_pair(const DecodeArgs& a, int b, int 
     // V side's writes cannot pass the K side's reads)
     __shared__ float rdyn_k[kRescueRows * 8], rdyn_v[kRescueRows * 8];
     if (rescue_side(a.ark)) tk = rescue_thr_rows(a.ark, lane, rk, rdyn_k);
-    quant_row_x(a.ark, row, lane, tk, p.k, p.sk);
+    quant_row_bhs<KFMT>(a.ark, b, hkv, 0, row, lane, tk, p.k, p.sk);
     if (rescue_side(a.arv)) tv = rescue_thr_rows(a.arv, lane, rv, rdyn_v);
   } else {
-    quant_row_x(a.ark, row, lane, tk, p.k, p.sk);
+    quant_row_bhs<KFMT>(a.ark, b, hkv, 0, row, lane, tk, p.k, p.sk);
   }
-  quant_row_x(a.arv, row, lane, tv, p.v, p.sv);
+  quant_row_bhs<VFMT>(a.arv, b, hkv, 0, row, lane, tv, p.v, p.sv);
 }
 
 __device__ __forceinline__ void append_status(const FusedAppend& f, const AppendFlags& fl) {
@@ -1931,9 +1965,18 @@ template <class KF, class VF, int LOOK, bool PACK8, int WPE = 2>
 __global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
   // One field of each kernel-argument line the prologue reads, so that the first batch of
-  // scalar loads fetches every such line (a line first touched later costs one more
-  // round trip before the first cache load; measured 0.15-0.25 us per launch).
-  asm volatile("" ::"s"(a.v.scale), "s"(a.ctx), "s"(a.app.kx), "s"(a.app.wpos));
+  // scalar loads fetches every such line: a line first touched later costs one more round
+  // trip before the first cache load (measured 0.15-0.25 us per launch).  The row formats'
+  // prologue reads most of the arguments (the append's two row sides): one dword of every
+  // 64-byte line (it touched about 20 lines one after another, 2 us per launch); the
+  // others read four lines (touching all costs them 0.2 us).
+  if constexpr (KF::kAppendRow) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&a);
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(DecodeArgs) / 4); i += 16) asm volatile("" ::"s"(w[i]));
+  } else {
+    asm volatile("" ::"s"(a.v.scale), "s"(a.ctx), "s"(a.app.kx), "s"(a.app.wpos));
+  }
   constexpr bool APP = KF::kAppend || KF::kAppendRow;  // a fused append (the writer's code) is built
   constexpr bool OUT = KF::kOut;
   int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z, n_ch = a.n_chunks;  // n_ch: the row's chunks
@@ -1996,7 +2039,8 @@ void decode_tiled_kernel(DecodeArgs a) {
   };
   auto app_store = [&]() {
     if constexpr (KF::kAppend) append_store(a, kf, vf, lane, ain, (float)qin.s, (float)qin.z, afl);
-    else if constexpr (KF::kAppendRow) append_row_pair<KF::kRescue>(a, b, hkv, lane, rpre, rxk, rxv);
+    else if constexpr (KF::kAppendRow)
+      append_row_pair<KF::kRescue, KF::kRowFmt, VF::kRowFmt>(a, b, hkv, lane, rpre, rxk, rxv);
   };
 
   // Tile schedule: the n_ch work-groups of a (b, kv head) interleave, so at step i the
@@ -2156,15 +2200,16 @@ void decode_tiled_kernel(DecodeArgs a) {
   if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <class KF, class VF, bool PACK8>
+template <class KF, class VF, bool PACK8, int LOOK = 1>
 const void* tiled_ptr() {
-  return reinterpret_cast<const void*>(&decode_tiled_kernel<KF, VF, 1, PACK8>);
+  return reinterpret_cast<const void*>(&decode_tiled_kernel<KF, VF, LOOK, PACK8>);
 }
 // the kernels for n_rep <= 8 (pack8) pack the second row block's softmax into the padding
 // lanes
-template <class KF, class VF>
-const void* tiled_pick(bool pack8) {
-  return pack8 ? tiled_ptr<KF, VF, true>() : tiled_ptr<KF, VF, false>();
+template <class KF, class VF, int LOOK = 1>
+TiledFn tiled_pick(bool pack8) {
+  return TiledFn{pack8 ? tiled_ptr<KF, VF, true, LOOK>() : tiled_ptr<KF, VF, false, LOOK>(),
+                 KF::kRowFmt, VF::kRowFmt};
 }
 
 }  // namespace

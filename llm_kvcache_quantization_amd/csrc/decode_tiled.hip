@@ -5,20 +5,21 @@
 
 namespace kvq {
 
-const void* tiled_kernel(int fam, int n_rep) {
+TiledFn tiled_kernel(int fam, int n_rep) {
   const bool pack8 = n_rep <= 8;
   for (auto pick : {tiled_kernel_a4, tiled_kernel_tok, tiled_kernel_kv4, tiled_kernel_kv16,
-                    tiled_kernel_kt})
-    if (const void* fn = pick(fam, pack8)) return fn;
-  return nullptr;
+                    tiled_kernel_kt}) {
+    const TiledFn k = pick(fam, pack8);
+    if (k.fn) return k;
+  }
+  return TiledFn{nullptr, -1, -1};
 }
 
-hipError_t launch_tiled(const DecodeArgs& a, int fam, dim3 grid, hipStream_t s) {
-  const void* fn = tiled_kernel(fam, a.n_rep);
-  if (!fn) return hipErrorInvalidValue;
+hipError_t launch_tiled(const DecodeArgs& a, const TiledFn& k, dim3 grid, hipStream_t s) {
+  if (!k.fn) return hipErrorInvalidValue;
   DecodeArgs args = a;
   void* kargs[] = {&args};
-  return hipLaunchKernel(fn, grid, dim3(kTiledWaves * 64), kargs, 0, s);
+  return hipLaunchKernel(k.fn, grid, dim3(kTiledWaves * 64), kargs, 0, s);
 }
 
 }  // namespace kvq

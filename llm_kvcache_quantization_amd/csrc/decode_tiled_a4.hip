@@ -4,14 +4,14 @@
 
 namespace kvq {
 
-const void* tiled_kernel_a4(int fam, bool pack8) {
+TiledFn tiled_kernel_a4(int fam, bool pack8) {
   switch (fam) {
     case kTiledA4A4: return tiled_pick<KAsymT<false>, VAsymT>(pack8);
     case kTiledA4A4o: return tiled_pick<KAsymT<true>, VAsymT>(pack8);
     case kTiledI8A4: return tiled_pick<KI8T<false>, VAsymT>(pack8);
     case kTiledI8I8: return tiled_pick<KI8T<false>, VI8RowT<false>>(pack8);
     case kTiledI8I8g: return tiled_pick<KI8T<true>, VI8RowT<true>>(pack8);
-    default: return nullptr;
+    default: return TiledFn{nullptr, -1, -1};
   }
 }
 

@@ -5,12 +5,12 @@
 
 namespace kvq {
 
-const void* tiled_kernel_kt(int fam, bool pack8) {
+TiledFn tiled_kernel_kt(int fam, bool pack8) {
   switch (fam) {
     case kTiledKtKv: return tiled_pick<KTokAsymT, VKiviRowT>(pack8);
     case kTiledKtT8: return tiled_pick<KTokAsymT, VTokT<false>>(pack8);
     case kTiledKtF: return tiled_pick<KTokAsymT, VF16RowT>(pack8);
-    default: return nullptr;
+    default: return TiledFn{nullptr, -1, -1};
   }
 }
 

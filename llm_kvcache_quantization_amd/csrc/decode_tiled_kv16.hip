@@ -4,14 +4,14 @@
 
 namespace kvq {
 
-const void* tiled_kernel_kv16(int fam, bool pack8) {
+TiledFn tiled_kernel_kv16(int fam, bool pack8) {
   switch (fam) {
     case kTiledKv8F: return tiled_pick<KKivi8T, VF16RowT>(pack8);
     case kTiledKvF4: return tiled_pick<KF16T, VKiviRowT>(pack8);
     case kTiledKvF8: return tiled_pick<KF16T, VKivi8RowT>(pack8);
     case kTiledKvFF: return tiled_pick<KF16T, VF16RowT>(pack8);
     case kTiledFT8: return tiled_pick<KF16T, VTokT<false>>(pack8);
-    default: return nullptr;
+    default: return TiledFn{nullptr, -1, -1};
   }
 }
 

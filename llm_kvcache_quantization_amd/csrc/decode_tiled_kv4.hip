@@ -4,14 +4,14 @@
 
 namespace kvq {
 
-const void* tiled_kernel_kv4(int fam, bool pack8) {
+TiledFn tiled_kernel_kv4(int fam, bool pack8) {
   switch (fam) {
     case kTiledKivi: return tiled_pick<KKiviT, VKiviRowT>(pack8);
     case kTiledKv48: return tiled_pick<KKiviT, VKivi8RowT>(pack8);
     case kTiledKv4F: return tiled_pick<KKiviT, VF16RowT>(pack8);
     case kTiledKv84: return tiled_pick<KKivi8T, VKiviRowT>(pack8);
     case kTiledKv88: return tiled_pick<KKivi8T, VKivi8RowT>(pack8);
-    default: return nullptr;
+    default: return TiledFn{nullptr, -1, -1};
   }
 }
 

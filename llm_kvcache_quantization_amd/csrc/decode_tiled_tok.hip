@@ -4,7 +4,7 @@
 
 namespace kvq {
 
-const void* tiled_kernel_tok(int fam, bool pack8) {
+TiledFn tiled_kernel_tok(int fam, bool pack8) {
   switch (fam) {
     case kTiledT8: return tiled_pick<KTokT<false, 1>, VTokT<false>>(pack8);
     case kTiledT8g16: return tiled_pick<KTokT<false, 2>, VTokT<false>>(pack8);
@@ -14,7 +14,7 @@ const void* tiled_kernel_tok(int fam, bool pack8) {
     case kTiledT8Kvg16: return tiled_pick<KTokT<false, 2>, VKiviRowT>(pack8);
     case kTiledT8F: return tiled_pick<KTokT<false, 1>, VF16RowT>(pack8);
     case kTiledT8Fg16: return tiled_pick<KTokT<false, 2>, VF16RowT>(pack8);
-    default: return nullptr;
+    default: return TiledFn{nullptr, -1, -1};
   }
 }
 
