@@ -26,9 +26,12 @@ attention).  The line also carries:
 - ``attention_us_per_layer_step`` / ``append_us_per_layer_step``: each half timed alone
   (its own HIP graph), as a breakdown;
 - ``stream_ceiling``: the library's streaming-read probe (kvq_stream_read) over the same
-  bytes per launch, the read rate this GPU sustains for a launch of that size;
+  bytes per launch, replayed from a HIP graph (device time), the read rate this GPU
+  sustains for a launch of that size;
 - ``engine_api``: the same step through the cache engine a caller uses
   (``cache.append_decode_attn`` per layer, Python included);
+- ``int4_fused`` (configuration 3): the reference's ``int4_fused`` kv_mode (group 16,
+  outlier rescue 0.01, static tables) through INT4KVCache at the same shape;
 - ``cpu_baseline``: the CPU oracle (the reference's torch path restated) timed on a
   bounded sample on this host's cores.
 
@@ -61,6 +64,9 @@ def parse():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine-API leg")
+    ap.add_argument("--no-modes", action="store_true",
+                    help="skip the int4_fused leg (the reference's kv_mode through INT4KVCache "
+                         "at configuration 3's shape, reported as the line's int4_fused key)")
     ap.add_argument("--no-ceiling", action="store_true",
                     help="skip the streaming-read ceiling (counter runs)")
     ap.add_argument("--launch", choices=["auto", "graph", "stream"], default="auto",
@@ -270,7 +276,10 @@ def stream_ceiling(device, nbytes, reps=28):
       each reading the next window of a 4 GiB buffer, so that, as in the decode step, no
       launch is served from the 256 MB MALL;
     - ``read_GBps_4GiB``: one launch over the whole buffer.
-    Each is the best over 1 to 64 work-groups (512 threads, one contiguous slab each) per CU."""
+    Each is the best over 1 to 64 work-groups (512 threads, one contiguous slab each) per CU.
+    The same-bytes launches are replayed from a HIP graph of `reps` launches, so that the
+    figure is device time: from Python, launches of a few MB are host-bound (about 10 us per
+    ctypes call)."""
     from llm_kvcache_quantization_amd import _capi as C
 
     L = C.lib()
@@ -286,20 +295,28 @@ def stream_ceiling(device, nbytes, reps=28):
         wgs = per_cu * cus
         sink = torch.zeros(wgs, dtype=torch.int32, device=device)
 
-        def launch(off, n):
+        def launch(off, n, stream=s):
             C.check(L.kvq_stream_read(ctypes.c_void_p(buf.data_ptr() + off), n,
-                                      ctypes.c_void_p(sink.data_ptr()), wgs, ctypes.c_void_p(s)))
+                                      ctypes.c_void_p(sink.data_ptr()), wgs,
+                                      ctypes.c_void_p(stream)))
 
         for w in range(nwins):
             launch(w * nwin, nwin)
         torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            cs = torch.cuda.current_stream().cuda_stream
+            for r in range(reps):
+                launch((r % nwins) * nwin, nwin, cs)
+        graph.replay()
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for r in range(reps):
-            launch((r % nwins) * nwin, nwin)
+        graph.replay()
         e1.record()
         torch.cuda.synchronize()
         gbps = nwin * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        del graph
         best_same = max(best_same, (gbps, wgs))
         e0.record()
         for _ in range(3):
@@ -860,6 +877,11 @@ def main():
         print("[bench] timing the engine API", file=sys.stderr, flush=True)
         eng = engine_leg(cfg, device, args.steps, args.warmup)
         print(f"[bench] engine API {eng}", file=sys.stderr, flush=True)
+    fused_mode = None
+    if not args.no_modes and cfg.index == 3:
+        print("[bench] timing the int4_fused kv_mode at this shape", file=sys.stderr, flush=True)
+        fused_mode = modes_leg(cfg, "int4_fused", device, args.steps, args.warmup)
+        print(f"[bench] int4_fused {fused_mode}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
@@ -912,6 +934,7 @@ def main():
         },
         "stream_ceiling": ceiling,
         "engine_api": eng,
+        "int4_fused": fused_mode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
