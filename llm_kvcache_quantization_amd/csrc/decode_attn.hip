@@ -887,11 +887,13 @@ static int64_t n_chunks_for(const kvq_decode_params* p, int32_t chunk) {
 // (grid (u, Hkv, B)).  With the tiled kernels, context lengths given per row (2..64 rows),
 // no explicit chunk_tokens and u <= kUnitChunks, the grid is one dimension per kv head
 // instead: rows of equal length still take u work-groups each, in the same chunks (so
-// their bits are those of the uniform split), while a ragged batch shares share_c work-
-// groups of the kv head, about one per resident slot, out by length: row b gets
-// ceil(t_b / T) of them (t_b its tiles, T the smallest step that fits; see share_rows in
-// decode_tiled.h), so it runs in one round of equally long work-groups instead of
-// rounds of work-groups as long as their row.  pitch: partial slots per (b, query head).
+// their bits are those of the uniform split), while a ragged batch shares the waves of
+// share_c work-groups of the kv head, about one work-group per resident slot, out by
+// length: row b gets a run of about t_b / T waves (at least one work-group's worth; t_b
+// its tiles, T the smallest per-wave load that fits; see share_waves in decode_tiled.h),
+// so every wave streams about the same number of tiles in one round.  pitch: partial
+// slots per (b, query head): a run touches at most one work-group more than its length
+// in work-groups (it need not start at a work-group boundary).
 struct Split {
   int32_t chunk;
   int64_t grid_x, pitch, u, share_c;
@@ -906,13 +908,15 @@ static Split plan_split(const kvq_decode_params* p) {
   sp.share = false;
   if (tiled_family(p) != kTiledNone && p->context_lens != nullptr && p->chunk_tokens <= 0 &&
       p->batch >= 2 && p->batch <= kShareMaxRows && p->capacity > 0 && sp.u <= kUnitChunks) {
-    const void* fn = kernel_for(p);
+    const void* fn = tiled_kernel(tiled_family(p), p->q_heads / p->kv_heads).fn_share;
     const int64_t slots = fn ? resident_slots(fn, kTiledWaves * 64) : 256;
     int64_t c = slots / p->kv_heads;
     if (c < p->batch) c = p->batch;
     if (c > (int64_t)kUnitChunks * p->batch) c = (int64_t)kUnitChunks * p->batch;
-    // a row has at most one chunk per kTiledWaves tiles (every chunk holds a tile)
-    const int64_t row_max = ((p->capacity + kTile - 1) / kTile + kTiledWaves - 1) / kTiledWaves;
+    // a row's partials: one per work-group whose part of the row's run holds a tile, so at
+    // most one per kTiledWaves tiles plus one, at most c, at most kUnitChunks (the device
+    // caps a run at kTiledWaves * (kUnitChunks - 1) waves)
+    const int64_t row_max = ((p->capacity + kTile - 1) / kTile + kTiledWaves - 1) / kTiledWaves + 1;
     int64_t share_pitch = c < kUnitChunks ? c : kUnitChunks;
     if (share_pitch > row_max) share_pitch = row_max;
     sp.share_c = c;

@@ -453,7 +453,8 @@ enum TiledFam {
 };
 // a tiled kernel and the formats of the fused row append built into it (-1: none)
 struct TiledFn {
-  const void* fn;
+  const void* fn;        // the grid split's instantiation
+  const void* fn_share;  // the shared split's (a.share)
   int kfmt, vfmt;
 };
 // the instantiations, one lookup per translation unit (fn nullptr: not one of its families)

@@ -103,17 +103,17 @@ struct TiledMergeLds {
   float4v acc[kTW][16][kD / 4 + 1];
 };
 
-// Merges the (m, l, acc) states of the kTW waves (through LDS) into the work-group's
-// partial and stores it write-through at device scope, so another work-group of the launch,
-// on any XCD, can read it once the stores have completed.  acc[mb][r] of lane (head, lg)
-// holds channel d = 32 lg + 8 r + mb.  Wave w merges heads w, w + kTW, ..; lane l
-// channels 2 l and 2 l + 1: partial = sum_w e_w acc_w with e_w = exp2(m_w - M), (M,
-// sum_w e_w l_w) for the head's (m, l) pair.
+// Merges the (m, l, acc) states of the work-group's waves (through LDS) into its partial
+// of each row and stores it write-through at device scope, so another work-group of the
+// launch, on any XCD, can read it once the stores have completed.  acc[mb][r] of lane
+// (head, lg) holds channel d = 32 lg + 8 r + mb.  First every wave writes its state
+// (merge_to_lds, ending with a barrier); then, per row, waves [lo, hi) of the work-group
+// are merged (merge_partial): wave w merges heads w, w + kTW, ..; lane l channels 2 l and
+// 2 l + 1: partial = sum_w e_w acc_w with e_w = exp2(m_w - M), (M, sum_w e_w l_w) for the
+// head's (m, l) pair.  A wave without a tile has m = -inf, weight 0.
 template <bool PACK8>
-__device__ __forceinline__ void merge_store_partial(const DecodeArgs& a, TiledMergeLds& sh,
-                                                    int wave, int lane, float m, float l,
-                                                    const float4v acc[8], int b, int hkv,
-                                                    int chunk) {
+__device__ __forceinline__ void merge_to_lds(const DecodeArgs& a, TiledMergeLds& sh, int wave,
+                                             int lane, float m, float l, const float4v acc[8]) {
   const int col = lane & 15, lg = lane >> 4;
   if constexpr (PACK8) l += dpp_ror8f<0xF>(l, l);  // add the block-1 part from lane h + 8
   l = wave_sum_xor_groups(l);
@@ -129,23 +129,30 @@ __device__ __forceinline__ void merge_store_partial(const DecodeArgs& a, TiledMe
     }
   }
   __syncthreads();
+}
+__device__ __forceinline__ void merge_partial(const DecodeArgs& a, const TiledMergeLds& sh,
+                                              int wave, int lane, int lo, int hi, int b, int hkv,
+                                              int slot) {
   for (int h = wave; h < a.n_rep; h += kTW) {
     float mw[kTW];
 #pragma unroll
-    for (int w = 0; w < kTW; ++w) mw[w] = sh.m[w][h];
+    for (int w = 0; w < kTW; ++w) mw[w] = (w >= lo && w < hi) ? sh.m[w][h] : kNegInf;
     float M = mw[0];
 #pragma unroll
     for (int w = 1; w < kTW; ++w) M = fmaxf(M, mw[w]);
+    // (selects, not branches: the LDS reads of all kTW waves are issued together)
     float n0 = 0.f, n1 = 0.f, den = 0.f;
 #pragma unroll
     for (int w = 0; w < kTW; ++w) {
+      const bool in = w >= lo && w < hi;
       const float e = fast_exp2(mw[w] - M);
       const float2 v2 = reinterpret_cast<const float2*>(&sh.acc[w][h][0])[lane];
-      n0 = fmaf(e, v2.x, n0);
-      n1 = fmaf(e, v2.y, n1);
-      den = fmaf(e, sh.l[w][h], den);
+      const float lw = sh.l[w][h];
+      n0 = in ? fmaf(e, v2.x, n0) : n0;
+      n1 = in ? fmaf(e, v2.y, n1) : n1;
+      den = in ? fmaf(e, lw, den) : den;
     }
-    const int64_t pi = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks + chunk;
+    const int64_t pi = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks + slot;
     __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_acc + pi * kD + 2 * lane),
                        __builtin_bit_cast(uint64_t, float2{n0, n1}), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
@@ -1893,19 +1900,33 @@ __device__ __forceinline__ void append_status(const FusedAppend& f, const Append
   }
 }
 
-// One-dimensional split per kv head (a.share).  Rows of equal context length: row b takes
-// work-groups [b u, (b + 1) u) as the chunks of the uniform split (u = a.u_chunks).  A
-// ragged batch: C = a.share_c work-groups are shared out over the rows by context length.
-// Row b (t_b tiles) gets c_b = min(ceil(t_b / T), ceil(t_b / kTW), kUnitChunks) of them, or
-// one if it is empty (that one writes its zero output), with T the first of
-// ceil(total / C), ceil(total / (C - 1)), .. for which the shares fit C (C >= the row
-// count, so T = total always fits).  Work-group g of the kv head takes chunk g - start_b of
-// the row whose range [start_b, start_b + c_b) holds g; n = 0: past every row's share.  Every wave
-// of every work-group computes the same shares (lane b handles row b), so the assignment
-// is fixed by the context lengths alone.
-struct RowShare {
-  int hkv, b, chunk, n;
-  int64_t ctx;  // row b's context length (clamped to the capacity)
+// The rows of one work-group: runs of waves in its kv head's wave space.  Row b's run is
+// waves [p, p + w) of that space, wave k of the run (k = v - p for wave v) taking tiles
+// k, k + w, k + 2 w, ..  (tile = 32 tokens; only the row's last tile, t - 1, may be
+// partial), so at step i the run reads one contiguous stretch of w tiles and the device
+// streams each slab front to back.  The work-group's waves are v0 .. v0 + kTW - 1: waves
+// [0, x) of it are row r[0]'s, [x, nact) row r[1]'s (nrows = 2), waves from nact on have
+// no row.  Its partial of row r sits in slot v0 / kTW - p / kTW of the row; the row has
+// one partial per work-group whose part of the run holds a tile.
+struct ShareRow {
+  int b;     // the batch row
+  int p, w;  // its run of waves
+  int t;     // its tiles
+  int ctx;   // its context length (clamped to the capacity)
+};
+struct WgRows {
+  int hkv, v0, nrows, x, nact;
+  ShareRow r[2];
+  uint64_t empty;  // shared split, work-group 0: the rows with an empty context
+};
+// what the merge needs of the work-group's rows, kept in LDS over the main loop (held in
+// scalar registers there, they pushed the loop's own scalars into spills)
+struct SegInfo {
+  int b[2];     // the rows
+  int lo[2], hi[2];  // their waves [lo, hi)
+  int slot[2];  // the work-group's partial slot of each
+  int n[2];     // each row's partial count
+  int tile[2];  // whether the work-group's part holds a tile
 };
 __device__ __forceinline__ int ceil_div_pos(int x, int y) {  // x >= 0, y >= 1, x < 2^24
   int q = (int)((float)x / (float)y);
@@ -1913,55 +1934,96 @@ __device__ __forceinline__ int ceil_div_pos(int x, int y) {  // x >= 0, y >= 1, 
   q -= q > 0 && (q - 1) * y >= x;
   return q;
 }
-// lin: the work-group's index over the whole grid (x fastest); the work-groups that do work
-// come first in it, so they are the first dispatched.
-__device__ RowShare share_rows(const DecodeArgs& a, int lin) {
+// exclusive prefix sum over the wave's 64 lanes (DPP within rows of 16, then the rows'
+// totals by readlane)
+__device__ __forceinline__ int wave_excl_scan(int x) {
+  int v = x;
+  int t = __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += t;
+  t = __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += t;
+  t = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += t;
+  t = __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += t;
+  // v = inclusive sum within the row of 16 lanes
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+            r2 = __builtin_amdgcn_readlane(v, 47);
+  const int lane = threadIdx.x & 63;
+  const int base = lane < 16 ? 0 : lane < 32 ? r0 : lane < 48 ? r0 + r1 : r0 + r1 + r2;
+  return v + base - x;
+}
+// the most waves a row's run takes: its partials (one per work-group its run touches) fit
+// the merge's kUnitChunks
+constexpr int kShareWaveCap = kTW * (kUnitChunks - 1);
+// One-dimensional split per kv head (a.share): grid x = the kv head's work-groups.  Rows of
+// equal context length: the uniform split (row b takes work-groups [b u, (b + 1) u), u =
+// a.u_chunks, waves as in the non-shared split, so the bits are the same).  A ragged batch:
+// the W = kTW C waves of C = a.share_c work-groups are shared out over the rows by length.
+// Nonempty row b (t_b tiles) takes a run of w_b = min(kShareWaveCap, max(kTW, ceil(t_b /
+// T))) waves, runs in row order, with T found from ceil(total / W) upwards so that the runs
+// fit W (T = max t_b always fits: C >= the row count).  Runs of at least kTW waves give
+// every work-group at most two rows.  Empty rows take no waves; work-group 0 writes their
+// outputs.  Every wave of every work-group computes the same shares (lane b handles row b),
+// so the assignment is fixed by the context lengths alone.  lin: the work-group's index over
+// the whole grid (x fastest); kv head lin / n and work-group lin % n of it (n work-groups per
+// kv head), so the work-groups that do work come first and are the first dispatched.
+__device__ WgRows share_waves(const DecodeArgs& a, int lin) {
   const int lane = threadIdx.x & 63;
   const bool row = lane < a.B;
   const int len = row ? (int)row_context(a, lane) : 0;
   const int t = (len + kTile - 1) / kTile;
-  RowShare rs{0, 0, 0, 0, 0};
+  WgRows wr{};
+  wr.nrows = 0;
   const int t0 = __builtin_amdgcn_readlane(t, 0);
-  if (__ballot(row && t != t0) == 0) {  // equal lengths: the uniform split
-    const int per_head = a.u_chunks * a.B;
-    if (lin < per_head * a.Hkv) {
-      rs.hkv = lin / per_head;
-      const int g = lin - rs.hkv * per_head;
-      rs.b = g / a.u_chunks;
-      rs.chunk = g - rs.b * a.u_chunks;
-      rs.n = a.u_chunks;
-      rs.ctx = __builtin_amdgcn_readlane(len, rs.b);
+  const bool equal = __ballot(row && t != t0) == 0;
+  const int n = equal ? a.u_chunks * a.B : a.share_c;  // work-groups per kv head
+  wr.hkv = lin / n;
+  const int g = lin - wr.hkv * n;
+  wr.v0 = g * kTW;
+  if (wr.hkv >= a.Hkv) return wr;  // past every kv head's work-groups
+  int w;
+  if (equal) {  // equal lengths: the uniform split
+    w = row && t0 > 0 ? a.u_chunks * kTW : 0;
+    wr.empty = t0 == 0 ? __ballot(row) : 0;
+  } else {
+    const int W = a.share_c * kTW;
+    const int total = (int)wave_sum64((float)t);
+    auto runs = [&](int T) {
+      const int c = t == 0 ? 0 : min(kShareWaveCap, max(kTW, ceil_div_pos(t, T)));
+      return c;
+    };
+    // (float steps: T is only a start and a stride; the loop's test is exact)
+    int T = max(1, (int)ceilf((float)total / (float)W));
+    int S = (int)wave_sum64((float)runs(T));
+    while (S > W) {  // S(T) falls as T grows; S(max t_b) <= W
+      T = max(T + 1, (int)ceilf((float)T * ((float)S / (float)W)));
+      S = (int)wave_sum64((float)runs(T));
     }
-    return rs;
+    w = runs(T);
+    wr.empty = __ballot(row && t == 0);
   }
-  const int C = a.share_c;
-  if (lin >= C * a.Hkv) return rs;
-  rs.hkv = lin / C;
-  const int g = lin - rs.hkv * C;
-  const int cap = t == 0 ? (row ? 1 : 0) : min(ceil_div_pos(t, kTW), kUnitChunks);
-  const int total = (int)wave_sum64((float)t);
-  int c = cap;
-  for (int k = 0; k < C; ++k) {
-    const int T = total > 0 ? max(1, (total + (C - k) - 1) / (C - k)) : 1;
-    c = t == 0 ? cap : min(ceil_div_pos(t, T), cap);
-    if ((int)wave_sum64((float)c) <= C) break;
-  }
-  int start = 0;
-  for (int r = 0; r < a.B; ++r) {
-    const int cr = __builtin_amdgcn_readlane(c, r);
-    if (g < start + cr) {
-      rs.b = r;
-      rs.chunk = g - start;
-      rs.n = cr;
-      rs.ctx = __builtin_amdgcn_readlane(len, r);
-      break;
-    }
-    start += cr;
-  }
-  return rs;
+  const int p = wave_excl_scan(w);
+  const int S = __builtin_amdgcn_readlane(p + w, 63);
+  const int v0 = wr.v0;
+  if (v0 >= S) return wr;
+  const int v1 = min(v0 + kTW, S) - 1;
+  const uint64_t ha = __ballot(row && p <= v0 && v0 < p + w);
+  const uint64_t hb = __ballot(row && p <= v1 && v1 < p + w);
+  const int ba = __builtin_ctzll(ha), bb = __builtin_ctzll(hb);
+  wr.r[0] = ShareRow{ba, __builtin_amdgcn_readlane(p, ba), __builtin_amdgcn_readlane(w, ba),
+                     __builtin_amdgcn_readlane(t, ba), __builtin_amdgcn_readlane(len, ba)};
+  wr.r[1] = ShareRow{bb, __builtin_amdgcn_readlane(p, bb), __builtin_amdgcn_readlane(w, bb),
+                     __builtin_amdgcn_readlane(t, bb), __builtin_amdgcn_readlane(len, bb)};
+  wr.nrows = ba == bb ? 1 : 2;
+  wr.nact = v1 - v0 + 1;
+  wr.x = ba == bb ? wr.nact : wr.r[0].p + wr.r[0].w - v0;
+  return wr;
 }
 
-template <class KF, class VF, int LOOK, bool PACK8, int WPE = 2>
+// SHARE: the instantiation for the shared split (a.share); the other one carries none of
+// its code (it cost the grid split 0.2 us per launch at the headline shape).
+template <class KF, class VF, int LOOK, bool PACK8, bool SHARE, int WPE = 2>
 __global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
   // One field of each kernel-argument line the prologue reads, so that the first batch of
@@ -1979,20 +2041,50 @@ void decode_tiled_kernel(DecodeArgs a) {
   }
   constexpr bool APP = KF::kAppend || KF::kAppendRow;  // a fused append (the writer's code) is built
   constexpr bool OUT = KF::kOut;
-  int chunk = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z, n_ch = a.n_chunks;  // n_ch: the row's chunks
-  int64_t share_ctx = 0;
-  if (a.share) {
-    const RowShare rs = share_rows(a, (int)(blockIdx.y * gridDim.x + blockIdx.x));
-    if (rs.n == 0) return;  // past every row's share (uniform over the work-group)
-    hkv = __builtin_amdgcn_readfirstlane(rs.hkv);
-    b = __builtin_amdgcn_readfirstlane(rs.b);
-    chunk = __builtin_amdgcn_readfirstlane(rs.chunk);
-    n_ch = __builtin_amdgcn_readfirstlane(rs.n);
-    share_ctx = __builtin_amdgcn_readfirstlane((int)rs.ctx);
-  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, lg = lane >> 4;
+  // This work-group's rows (WgRows): the shared split's, or the grid's (chunk, kv head, b)
+  // with the row's run of n_chunks * kTW waves from wave 0 (its length read below).
+  WgRows wr;
+  if constexpr (SHARE) {
+    wr = share_waves(a, (int)(blockIdx.y * gridDim.x + blockIdx.x));
+    if (wr.hkv >= a.Hkv) return;  // past every kv head's work-groups
+    // the rows with an empty context: work-group 0 of the kv head writes their outputs
+    // (zero rows, or the residual window alone)
+    if (wr.v0 == 0 && wr.empty != 0) {
+      const int eh = __builtin_amdgcn_readfirstlane(wr.hkv);
+      for (uint64_t e = wr.empty; e != 0; e &= e - 1) {
+        const int rb = __builtin_amdgcn_readfirstlane(__builtin_ctzll(e));
+        if (VF::kResidual && a.res_n > 0) {
+          merge_chunks<VF, KF::kMergeBatch>(a, rb, eh, 0, wave, lane);
+        } else {
+          for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
+            a.out[(int64_t)rb * a.o_sb + (int64_t)(eh * a.n_rep + (idx >> 7)) * a.o_sh +
+                  (idx & (kD - 1))] = (half_t)0.0f;
+        }
+      }
+    }
+    if (wr.nrows == 0) return;  // past every row's run (uniform over the work-group)
+  } else {
+    wr.hkv = blockIdx.y;
+    wr.v0 = blockIdx.x * kTW;
+    wr.nrows = 1;
+    wr.x = wr.nact = kTW;
+    wr.empty = 0;
+    wr.r[0] = ShareRow{(int)blockIdx.z, 0, a.n_chunks * kTW, 0, 0};
+    wr.r[1] = wr.r[0];
+  }
+  const int hkv = __builtin_amdgcn_readfirstlane(wr.hkv);
+  // the wave's row: waves [0, x) row r[0]'s, [x, nact) row r[1]'s; waves from nact on have
+  // none and take no tile (first at the capacity)
+  const bool rowless = wave >= wr.nact;
+  const int ri = wave < wr.x ? 0 : 1;
+  const int b = __builtin_amdgcn_readfirstlane(ri == 0 ? wr.r[0].b : wr.r[1].b);
+  const int rp = __builtin_amdgcn_readfirstlane(ri == 0 ? wr.r[0].p : wr.r[1].p);
+  const int stride = __builtin_amdgcn_readfirstlane(ri == 0 ? wr.r[0].w : wr.r[1].w);
+  const int ncap = (a.cap + kTile - 1) / kTile;
+  const int first = rowless ? ncap : wr.v0 + wave - rp;  // the wave's first tile
 
   // Fused quantize-on-append.  The writer is the wave whose schedule (below) holds the new
   // token's tile wt: its stores precede, in program order, its loads of that tile.  They
@@ -2000,15 +2092,14 @@ void decode_tiled_kernel(DecodeArgs a) {
   // before the first cache loads when wt is one of the wave's first LOOK + 1 tiles.  A
   // writer whose work-group has no tile of the context stores before it leaves.
   const bool app_on = APP && a.app.kx != nullptr;
-  const int stride_all = n_ch * kTW;
   const int wt = app_on ? (int)(a.app.wpos / kTile) : 0;
-  const bool writer = app_on && chunk * kTW + wave == wt % stride_all;
+  const bool writer = app_on && !rowless && first == wt % stride;
   AppendIn ain;
   AppendFlags afl;
   [[maybe_unused]] RowPre rpre;
   [[maybe_unused]] RescueRows rxk, rxv;
 
-  __shared__ QShareLds qsh;
+  __shared__ QShareLds qsh[2];  // the q operands of the work-group's rows
   __shared__ TiledMergeLds msh;
   // Waves w and w + 4 share a SIMD, which issues the older of two ready waves first;
   // each publishes its step count and, when ahead of its partner, lowers its priority,
@@ -2018,8 +2109,11 @@ void decode_tiled_kernel(DecodeArgs a) {
   KF kf;
   // the q-side inputs are requested first: the wait for them then does not include the
   // cache tiles requested next
+  // (waves 0..3 build the operands of row r[0], waves 4..7 those of r[1]; the q-side fields
+  // every wave reads itself are the kv head's)
   typename KF::QInT qin;
-  kf.fetch_q(a, b, hkv, lane, wave, qin);
+  const int bq = __builtin_amdgcn_readfirstlane(wr.nrows == 2 && wave >= 4 ? wr.r[1].b : wr.r[0].b);
+  kf.fetch_q(a, bq, hkv, lane, wave, qin);
   if constexpr (KF::kAppendRow) {
     if (writer) {
       append_row_fetch(a, b, hkv, lane, rpre);
@@ -2043,13 +2137,8 @@ void decode_tiled_kernel(DecodeArgs a) {
       append_row_pair<KF::kRescue, KF::kRowFmt, VF::kRowFmt>(a, b, hkv, lane, rpre, rxk, rxv);
   };
 
-  // Tile schedule: the n_ch work-groups of a (b, kv head) interleave, so at step i the
-  // waves of all of them read one contiguous run of n_ch * kTW tiles and the device
-  // streams each slab front to back.  Wave w of work-group c takes tiles c * kTW + w +
-  // i * stride (tile = 32 tokens; only the context's last tile, ntot - 1, may be partial).
-  // The schedule is static, so results do not depend on timing.
-  const int first = chunk * kTW + wave;
-  const int stride = n_ch * kTW;
+  // Tile schedule (WgRows): the wave takes tiles first + i * stride of its row.  The
+  // schedule is static, so results do not depend on timing.
   // tile[j] = tile of step i + j (j <= LOOK + 1)
   int tile[LOOK + 2];
 #pragma unroll
@@ -2058,11 +2147,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   constexpr int U = (R % 2 == 0) ? R : 2 * R;  // unroll: ring slot and x buffer are static
   typename KF::Raw kr[R];
   typename VF::Raw vr[R];
-  // The context length is read here, ahead of every cache load: before the barrier below
-  // the compiler reads it through the scalar cache, whose wait does not include the cache
-  // tiles (after it, a vector load whose vmcnt wait also waited for the first tiles cost
-  // about 0.5 us per launch).  The K and V tiles of step 0 are then requested before the q
-  // set-up (bounded by the capacity; tiles past the context are never used), so the memory
+  // The K and V tiles of step 0 are requested before the q set-up (bounded by the capacity; tiles past the context are never used), so the memory
   // system is busy from the start of the kernel; the rest of the ring (K of steps 1..LOOK,
   // V of steps 1..LOOK-1) after the set-up.  A larger first burst delays the q loads
   // queued with it, and the set-up waits for those (measured: the whole ring up front
@@ -2070,22 +2155,54 @@ void decode_tiled_kernel(DecodeArgs a) {
   // during the set-up cost 1.4 us).  Every ring load is issued unconditionally (out of
   // range for a tile past the bound): conditional loads would make the compiler's vmcnt
   // waits conservative at the joins, i.e. wait for the tiles just requested.
-  // (the shared split has every row's length already)
-  const int64_t ctx64 = a.share ? share_ctx : row_context(a, b);
   asm volatile("" ::: "memory");
-  const bool early_write = writer && wt / stride_all <= LOOK;
+  const bool early_write = writer && wt / stride <= LOOK;
   if (early_write) {
     app_fetch();
     app_store();
   }
-  const int ncap = (a.cap + kTile - 1) / kTile;
   kf.load(kTile * tile[0], tile[0] < ncap, kr[0]);
   vf.load(kTile * tile[0], tile[0] < ncap, vr[0]);
 
-  const int ctx = (int)ctx64;
-  const int ntot = (ctx + kTile - 1) / kTile;
+  // The context length of the grid's row is read here, after the first tiles are requested
+  // (bounded by the capacity; tiles past the context are never used) but ahead of every
+  // wait: through the scalar cache, whose wait does not include the cache tiles (a vector
+  // load whose vmcnt wait also waited for the first tiles cost about 0.5 us per launch).
+  if constexpr (!SHARE) {
+    const int c = (int)row_context(a, b);
+    wr.r[0].t = wr.r[1].t = (c + kTile - 1) / kTile;
+    wr.r[0].ctx = wr.r[1].ctx = c;
+  }
+  const int ntot = __builtin_amdgcn_readfirstlane(ri == 0 ? wr.r[0].t : wr.r[1].t);
+  const int ctx = __builtin_amdgcn_readfirstlane(ri == 0 ? wr.r[0].ctx : wr.r[1].ctx);
   const bool partial = (ctx & (kTile - 1)) != 0;
-  if (ntot == 0 || chunk * kTW >= ntot) {  // no tile for this work-group (uniform)
+  // the work-group's part of each of its rows: waves [lo, hi), its slot among the row's
+  // partials, whether it holds a tile (its first wave's first tile is in the row), and the
+  // row's partial count (one per work-group of its run up to the last wave with a tile)
+  int seg_lo[2], seg_hi[2], seg_slot[2], seg_n[2];
+  bool seg_tile[2];
+#pragma unroll
+  for (int sgi = 0; sgi < 2; ++sgi) {
+    const ShareRow& r = wr.r[sgi];
+    seg_lo[sgi] = sgi == 0 ? 0 : wr.x;
+    seg_hi[sgi] = sgi == 0 ? wr.x : wr.nact;
+    seg_slot[sgi] = wr.v0 / kTW - r.p / kTW;
+    seg_n[sgi] = (r.p + min(r.w, r.t) - 1) / kTW - r.p / kTW + 1;
+    seg_tile[sgi] = sgi < wr.nrows && seg_lo[sgi] < seg_hi[sgi] && wr.v0 + seg_lo[sgi] - r.p < r.t;
+  }
+  __shared__ SegInfo seg;
+  if (SHARE && threadIdx.x == 0) {
+#pragma unroll
+    for (int sgi = 0; sgi < 2; ++sgi) {
+      seg.b[sgi] = wr.r[sgi].b;
+      seg.lo[sgi] = seg_lo[sgi];
+      seg.hi[sgi] = seg_hi[sgi];
+      seg.slot[sgi] = seg_slot[sgi];
+      seg.n[sgi] = seg_n[sgi];
+      seg.tile[sgi] = seg_tile[sgi];
+    }
+  }  // (read after the main loop; the set-up barrier orders the writes before)
+  if (!seg_tile[0] && !seg_tile[1]) {  // no tile for this work-group (uniform)
     if (writer) {
       if (!early_write) {
         app_fetch();
@@ -2093,7 +2210,7 @@ void decode_tiled_kernel(DecodeArgs a) {
       }
       if (lane == 0) append_status(a.app, afl);
     }
-    if (ntot == 0 && chunk == 0 && a.fused) {
+    if (!SHARE && ntot == 0 && wr.v0 == 0 && a.fused) {
       if (VF::kResidual && a.res_n > 0) {  // empty quantized context: the residual window alone
         merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, 0, wave, lane);
       } else {  // empty context: zero rows
@@ -2108,10 +2225,11 @@ void decode_tiled_kernel(DecodeArgs a) {
   // step that precedes its loads of tile wt (step wt_step - LOOK - 1), or right after the
   // set-up when wt lies past the wave's tiles.
   const bool late_write = writer && !early_write;
-  const int wt_step = (wt - (chunk * kTW + wave)) / stride_all;
+  const int wt_step = (wt - first) / stride;
   const int store_step = late_write ? wt_step - LOOK - 1 : -1;
   if (late_write) app_fetch();
-  if (wave < 4) kf.setup_q(a, qin, lane, wave, qsh);  // waves 4..7 would build the same
+  // (one row: waves 4..7 would build the same)
+  if (wave < 4 || wr.nrows == 2) kf.setup_q(a, qin, lane, wave & 3, qsh[wave >> 2]);
   NibConsts nc;
   nc.init();
   __syncthreads();
@@ -2120,7 +2238,7 @@ void decode_tiled_kernel(DecodeArgs a) {
     kf.load(kTile * tile[s], tile[s] < ntot, kr[s]);
     if (s < LOOK) vf.load(kTile * tile[s], tile[s] < ntot, vr[s]);
   }
-  kf.finish_setup(qsh, qin, lane);
+  kf.finish_setup(qsh[ri], qin, lane);
   // (wt past the context: the wave may have fewer steps than store_step; the row formats'
   // writer always stores here, outside the loop)
   const bool store_now = late_write && (KF::kAppendRow || wt >= ntot || store_step <= 0);
@@ -2184,31 +2302,65 @@ void decode_tiled_kernel(DecodeArgs a) {
   // work-group has completed, one thread counts it in (word 0 of the (b, kv head)'s
   // counter slot); the last of the (b, kv head)'s work-groups merges every partial, writes
   // the output and resets the counter.
-  const int nvalid = min(n_ch, (ntot + kTW - 1) / kTW);  // chunks holding a tile
-  uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
-  __shared__ int is_last;
+  __shared__ int is_last[2];
   vf.finalize(acc, lane);
-  merge_store_partial<PACK8>(a, msh, wave, lane, m, l, acc, b, hkv, chunk);
+  merge_to_lds<PACK8>(a, msh, wave, lane, m, l, acc);
+  if constexpr (!SHARE) {  // one row, all kTW waves (constant descriptors: no LDS reads)
+    const int nvalid = min(a.n_chunks, (ntot + kTW - 1) / kTW);  // chunks holding a tile
+    uint32_t* slot = a.counters + ((int64_t)b * a.Hkv + hkv) * kCtrSlotWords;
+    merge_partial(a, msh, wave, lane, 0, kTW, b, hkv, (int)blockIdx.x);
+    if (!a.fused) return;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      is_last[0] = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)(nvalid - 1);
+    __syncthreads();
+    if (!is_last[0]) return;
+    merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, nvalid, wave, lane);
+    if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  auto sgv = [](const int& x) { return __builtin_amdgcn_readfirstlane(x); };
+#pragma unroll
+  for (int sgi = 0; sgi < 2; ++sgi)
+    if (sgv(seg.tile[sgi]))
+      merge_partial(a, msh, wave, lane, sgv(seg.lo[sgi]), sgv(seg.hi[sgi]), sgv(seg.b[sgi]), hkv,
+                    sgv(seg.slot[sgi]));
   if (!a.fused) return;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nvalid - 1);
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int sgi = 0; sgi < 2; ++sgi) {
+      uint32_t* slot = a.counters + ((int64_t)seg.b[sgi] * a.Hkv + hkv) * kCtrSlotWords;
+      is_last[sgi] = seg.tile[sgi] &&
+                     __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         (uint32_t)(seg.n[sgi] - 1);
+    }
+  }
   __syncthreads();
-  if (!is_last) return;
-  merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, nvalid, wave, lane);
-  if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int sgi = 0; sgi < 2; ++sgi) {
+    if (!is_last[sgi]) continue;
+    const int rb = sgv(seg.b[sgi]);
+    merge_chunks<VF, KF::kMergeBatch>(a, rb, hkv, sgv(seg.n[sgi]), wave, lane);
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.counters + ((int64_t)rb * a.Hkv + hkv) * kCtrSlotWords, 0u,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
-template <class KF, class VF, bool PACK8, int LOOK = 1>
+template <class KF, class VF, bool PACK8, bool SHARE, int LOOK = 1>
 const void* tiled_ptr() {
-  return reinterpret_cast<const void*>(&decode_tiled_kernel<KF, VF, LOOK, PACK8>);
+  return reinterpret_cast<const void*>(&decode_tiled_kernel<KF, VF, LOOK, PACK8, SHARE>);
 }
 // the kernels for n_rep <= 8 (pack8) pack the second row block's softmax into the padding
 // lanes
 template <class KF, class VF, int LOOK = 1>
 TiledFn tiled_pick(bool pack8) {
-  return TiledFn{pack8 ? tiled_ptr<KF, VF, true, LOOK>() : tiled_ptr<KF, VF, false, LOOK>(),
+  return TiledFn{pack8 ? tiled_ptr<KF, VF, true, false, LOOK>() : tiled_ptr<KF, VF, false, false, LOOK>(),
+                 pack8 ? tiled_ptr<KF, VF, true, true, LOOK>() : tiled_ptr<KF, VF, false, true, LOOK>(),
                  KF::kRowFmt, VF::kRowFmt};
 }
 

@@ -12,14 +12,14 @@ TiledFn tiled_kernel(int fam, int n_rep) {
     const TiledFn k = pick(fam, pack8);
     if (k.fn) return k;
   }
-  return TiledFn{nullptr, -1, -1};
+  return TiledFn{nullptr, nullptr, -1, -1};
 }
 
 hipError_t launch_tiled(const DecodeArgs& a, const TiledFn& k, dim3 grid, hipStream_t s) {
   if (!k.fn) return hipErrorInvalidValue;
   DecodeArgs args = a;
   void* kargs[] = {&args};
-  return hipLaunchKernel(k.fn, grid, dim3(kTiledWaves * 64), kargs, 0, s);
+  return hipLaunchKernel(a.share ? k.fn_share : k.fn, grid, dim3(kTiledWaves * 64), kargs, 0, s);
 }
 
 }  // namespace kvq

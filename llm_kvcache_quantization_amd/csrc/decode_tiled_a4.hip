@@ -11,7 +11,7 @@ TiledFn tiled_kernel_a4(int fam, bool pack8) {
     case kTiledI8A4: return tiled_pick<KI8T<false>, VAsymT>(pack8);
     case kTiledI8I8: return tiled_pick<KI8T<false>, VI8RowT<false>>(pack8);
     case kTiledI8I8g: return tiled_pick<KI8T<true>, VI8RowT<true>>(pack8);
-    default: return TiledFn{nullptr, -1, -1};
+    default: return TiledFn{nullptr, nullptr, -1, -1};
   }
 }
 

@@ -10,7 +10,7 @@ TiledFn tiled_kernel_kt(int fam, bool pack8) {
     case kTiledKtKv: return tiled_pick<KTokAsymT, VKiviRowT>(pack8);
     case kTiledKtT8: return tiled_pick<KTokAsymT, VTokT<false>>(pack8);
     case kTiledKtF: return tiled_pick<KTokAsymT, VF16RowT>(pack8);
-    default: return TiledFn{nullptr, -1, -1};
+    default: return TiledFn{nullptr, nullptr, -1, -1};
   }
 }
 

@@ -11,7 +11,7 @@ TiledFn tiled_kernel_kv16(int fam, bool pack8) {
     case kTiledKvF8: return tiled_pick<KF16T, VKivi8RowT>(pack8);
     case kTiledKvFF: return tiled_pick<KF16T, VF16RowT>(pack8);
     case kTiledFT8: return tiled_pick<KF16T, VTokT<false>>(pack8);
-    default: return TiledFn{nullptr, -1, -1};
+    default: return TiledFn{nullptr, nullptr, -1, -1};
   }
 }
 

@@ -11,7 +11,7 @@ TiledFn tiled_kernel_kv4(int fam, bool pack8) {
     case kTiledKv4F: return tiled_pick<KKiviT, VF16RowT>(pack8);
     case kTiledKv84: return tiled_pick<KKivi8T, VKiviRowT>(pack8);
     case kTiledKv88: return tiled_pick<KKivi8T, VKivi8RowT>(pack8);
-    default: return TiledFn{nullptr, -1, -1};
+    default: return TiledFn{nullptr, nullptr, -1, -1};
   }
 }
 

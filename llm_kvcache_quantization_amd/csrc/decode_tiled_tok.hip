@@ -14,7 +14,7 @@ TiledFn tiled_kernel_tok(int fam, bool pack8) {
     case kTiledT8Kvg16: return tiled_pick<KTokT<false, 2>, VKiviRowT>(pack8);
     case kTiledT8F: return tiled_pick<KTokT<false, 1>, VF16RowT>(pack8);
     case kTiledT8Fg16: return tiled_pick<KTokT<false, 2>, VF16RowT>(pack8);
-    default: return TiledFn{nullptr, -1, -1};
+    default: return TiledFn{nullptr, nullptr, -1, -1};
   }
 }
 
