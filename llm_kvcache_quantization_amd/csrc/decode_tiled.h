@@ -287,6 +287,98 @@ __device__ __forceinline__ void merge_chunks(const DecodeArgs& a, int b, int hkv
   }
 }
 
+// merge_chunks' steps for one (row, head) pair, split so that a wave can request the loads
+// of two pairs before it combines either: merge_pair_issue requests the (m, l) pairs and the
+// first batch of chunk partials, merge_pair_finish combines them (and any further batch)
+// with the same arithmetic and writes the output row.
+template <int kB>
+struct PairLoads {
+  rsrc_t racc;
+  u32x2 ml;
+  u32x2 av[kB];
+};
+template <int kB>
+__device__ __forceinline__ void merge_pair_issue(const DecodeArgs& a, int b, int hkv, int h,
+                                                 int nvalid, int lane, PairLoads<kB>& L) {
+  const int64_t row = ((int64_t)b * a.Hq + hkv * a.n_rep + h) * a.n_chunks;
+  const rsrc_t rml = buffer_rsrc(a.part_ml + row, (uint32_t)nvalid * 8u);
+  L.racc = buffer_rsrc(a.part_acc + row * kD, (uint32_t)nvalid * (kD * 4u));
+  L.ml = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, (int)(lane * 8), 0, kBufSC1));
+#pragma unroll
+  for (int c = 0; c < kB; ++c)
+    L.av[c] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                            L.racc, (int)((uint32_t)lane * 8u + (uint32_t)c * (kD * 4u)), 0, kBufSC1));
+}
+template <class VF, int kB>
+__device__ __forceinline__ void merge_pair_finish(const DecodeArgs& a, int b, int hkv, int h,
+                                                  int nvalid, int lane, PairLoads<kB>& L,
+                                                  float s, float z) {
+  float mr = kNegInf, lr = 0.f, rr0 = 0.f, rr1 = 0.f;
+  if constexpr (VF::kResidual)
+    if (a.res_n > 0) residual_partial(a, b, hkv, hkv * a.n_rep + h, lane, mr, lr, rr0, rr1);
+  const float mc = lane < nvalid ? __builtin_bit_cast(float, (uint32_t)L.ml.x) : kNegInf;
+  float M = wave_max64(mc);
+  if constexpr (VF::kResidual) M = fmaxf(M, mr);
+  const float e = fast_exp2(mc - M);
+  float den = wave_sum64(e * __builtin_bit_cast(float, (uint32_t)L.ml.y));
+  float er = 0.f;
+  if constexpr (VF::kResidual) {
+    er = fast_exp2(mr - M);
+    den = fmaf(er, lr, den);
+  }
+  float n0 = 0.f, n1 = 0.f;
+  for (int c0 = 0;;) {
+#pragma unroll
+    for (int c = 0; c < kB; ++c) {
+      const float ec = row_lane(e, c0 + c);
+      n0 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)L.av[c].x), n0);
+      n1 = fmaf(ec, __builtin_bit_cast(float, (uint32_t)L.av[c].y), n1);
+    }
+    c0 += kB;
+    if (c0 >= nvalid) {
+      if constexpr (VF::kResidual) {
+        n0 = fmaf(er, rr0, n0);
+        n1 = fmaf(er, rr1, n1);
+      }
+      break;
+    }
+#pragma unroll
+    for (int c = 0; c < kB; ++c)
+      L.av[c] = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                     L.racc, (int)((uint32_t)lane * 8u + (uint32_t)(c0 + c) * (kD * 4u)), 0, kBufSC1));
+  }
+  const half2v o = VF::epilogue(n0 / den, n1 / den, s, z);
+  *reinterpret_cast<half2v*>(a.out + (int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + h) * a.o_sh +
+                             2 * lane) = o;
+}
+// The shared split's merge of the rows whose last work-group this is (nr = 1 or 2: rows
+// b0 (n0 partials) and b1 (n1)).  Pair p is (row p / n_rep, head p % n_rep); wave w takes
+// pairs w, w + kTW, ..; a wave with two pairs requests the loads of both before it combines
+// the first (one memory latency for the two rows, where merging them one after the other
+// took two).
+template <class VF, int kB>
+__device__ __forceinline__ void merge_rows(const DecodeArgs& a, int hkv, int b0, int n0, int b1,
+                                           int n1, int nr, int wave, int lane) {
+  float s, z;
+  VF::epi_params(a, hkv, lane, s, z);
+  const int np = nr * a.n_rep;
+  for (int p = wave; p < np; p += 2 * kTW) {
+    const int q = p + kTW;
+    const bool two = q < np;
+    const int r0 = p >= a.n_rep, r1 = q >= a.n_rep;
+    const int h0 = p - r0 * a.n_rep, h1 = two ? q - r1 * a.n_rep : 0;
+    const int bb0 = r0 ? b1 : b0, nn0 = r0 ? n1 : n0;
+    const int bb1 = r1 ? b1 : b0, nn1 = r1 ? n1 : n0;
+    PairLoads<kB> L0, L1;
+    merge_pair_issue<kB>(a, bb0, hkv, h0, nn0, lane, L0);
+    if (two) merge_pair_issue<kB>(a, bb1, hkv, h1, nn1, lane, L1);
+    asm volatile("" ::: "memory");
+    merge_pair_finish<VF, kB>(a, bb0, hkv, h0, nn0, lane, L0, s, z);
+    if (two) merge_pair_finish<VF, kB>(a, bb1, hkv, h1, nn1, lane, L1, s, z);
+  }
+}
+
 // 8 packed codes -> 8 fp16 operands in k-slot order [e0, e4, e1, e5, e2, e6, e3, e7]
 // (e = element within the dword; byte k holds e = 2k in its high nibble), read as fp16
 // subnormals: a nibble in bits 4..7 of a 16-bit half is 16 n * 2^-24, one in bits 0..3 is
@@ -2030,9 +2122,10 @@ void decode_tiled_kernel(DecodeArgs a) {
   // scalar loads fetches every such line: a line first touched later costs one more round
   // trip before the first cache load (measured 0.15-0.25 us per launch).  The row formats'
   // prologue reads most of the arguments (the append's two row sides): one dword of every
-  // 64-byte line (it touched about 20 lines one after another, 2 us per launch); the
-  // others read four lines (touching all costs them 0.2 us).
-  if constexpr (KF::kAppendRow) {
+  // 64-byte line (it touched about 20 lines one after another, 2 us per launch); so does the
+  // shared split, whose prologue reads the split's fields before the cache descriptors (1.1
+  // us per launch at config 4); the others read four lines (touching all costs them 0.2 us).
+  if constexpr (KF::kAppendRow || SHARE) {
     const uint32_t* w = reinterpret_cast<const uint32_t*>(&a);
 #pragma unroll
     for (int i = 0; i < (int)(sizeof(DecodeArgs) / 4); i += 16) asm volatile("" ::"s"(w[i]));
@@ -2330,25 +2423,25 @@ void decode_tiled_kernel(DecodeArgs a) {
   if (!a.fused) return;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int sgi = 0; sgi < 2; ++sgi) {
+  // lane r of wave 0 counts the work-group in on row r's counter (both rows in one atomic
+  // instruction); the last arriver resets it (every work-group of the row has counted)
+  if (threadIdx.x < 2) {
+    const int sgi = threadIdx.x;
+    bool last = false;
+    if (seg.tile[sgi]) {
       uint32_t* slot = a.counters + ((int64_t)seg.b[sgi] * a.Hkv + hkv) * kCtrSlotWords;
-      is_last[sgi] = seg.tile[sgi] &&
-                     __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                         (uint32_t)(seg.n[sgi] - 1);
+      last = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (uint32_t)(seg.n[sgi] - 1);
+      if (last) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    is_last[sgi] = last;
   }
   __syncthreads();
-#pragma unroll
-  for (int sgi = 0; sgi < 2; ++sgi) {
-    if (!is_last[sgi]) continue;
-    const int rb = sgv(seg.b[sgi]);
-    merge_chunks<VF, KF::kMergeBatch>(a, rb, hkv, sgv(seg.n[sgi]), wave, lane);
-    if (threadIdx.x == 0)
-      __hip_atomic_store(a.counters + ((int64_t)rb * a.Hkv + hkv) * kCtrSlotWords, 0u,
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  const int l0 = sgv(is_last[0]), l1 = sgv(is_last[1]);
+  if (!l0 && !l1) return;
+  constexpr int kB = KF::kMergeBatch < 16 ? KF::kMergeBatch : 16;
+  merge_rows<VF, kB>(a, hkv, sgv(seg.b[l0 ? 0 : 1]), sgv(seg.n[l0 ? 0 : 1]), sgv(seg.b[1]),
+                     sgv(seg.n[1]), l0 && l1 ? 2 : 1, wave, lane);
 }
 
 template <class KF, class VF, bool PACK8, bool SHARE, int LOOK = 1>
