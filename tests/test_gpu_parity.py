@@ -5,6 +5,7 @@ max-abs 2e-3 of the dequantise-then-attention oracle with cosine >= 0.9999 (the
 tolerance BASELINE.json's north star states for fp16 outputs).
 """
 import ctypes
+import dataclasses
 import math
 
 import pytest
@@ -535,10 +536,12 @@ def test_decode_per_token_scales_tiled(bits, G, B, Hq, Hkv, S, ctx, static):
             assert torch.all(out[b] == 0)
 
 
-def _asym_case(cfg_idx, B, S, ctx, seed, outliers=True):
+def _asym_case(cfg_idx, B, S, ctx, seed, outliers=True, heads=None):
     from llm_kvcache_quantization_amd import synthetic as SY
 
     cfg = SY.CONFIGS[cfg_idx]
+    if heads is not None:  # (q heads, kv heads) in place of the configuration's
+        cfg = dataclasses.replace(cfg, q_heads=heads[0], kv_heads=heads[1])
     t = SY.calibrate(cfg, 0)
     g = gen(seed)
     k, v = SY.draw_kv(cfg, 0, B, S, g)
@@ -1141,3 +1144,29 @@ def test_decode_shared_split_ragged(B, S, ctx):
     for b, c in enumerate(ctx):
         if c == 0:
             assert torch.all(out[b] == 0)
+
+
+@pytest.mark.parametrize("heads,ctx", [
+    ((32, 2), [4000, 90, 2500, 33, 4096, 1200, 700, 3001, 64, 1900]),  # 16 query heads per kv head
+    ((4, 4), [4096, 1, 2049, 300, 3999, 1024, 77, 2600]),              # one query head per kv head
+    ((20, 2), [4096, 4095, 100, 3000, 31, 2222]),                      # 10: three pairs on some waves
+])
+def test_decode_shared_split_two_row_merge(heads, ctx):
+    """The shared split's merge of work-groups that hold two rows and arrive last for both:
+    (row, head) pairs shared out over the 8 waves, two pairs per wave with their loads
+    issued together, for query heads per kv head from 1 to 16.  Against the oracle, and two
+    launches bit-identical."""
+    K = _lib()
+    B, S = len(ctx), 4096
+    cfg, t, q, tau, kq, vq, oidx, oval, cl = _asym_case(3, B, S, ctx, 90 + heads[0], True, heads)
+    sm = 1 / math.sqrt(128)
+    ref = OA.decode_attn_asym_ref(q, kq, vq, t.k_scale, t.k_zp, t.v_scale, t.v_zp, cl, sm,
+                                  inv_tau=tau, k_outlier_idx=oidx, k_outlier_val=oval)
+    args = (q.to(DEV), kq.to(DEV), K.tile_v(vq.to(DEV)), t.k_scale.to(DEV), t.k_zp.to(DEV),
+            t.v_scale.to(DEV), t.v_zp.to(DEV), cl.to(DEV), sm)
+    kw = dict(inv_tau=tau.to(DEV), k_outlier_idx=oidx.to(DEV), k_outlier_val=oval.to(DEV))
+    out = K.decode_attn_int4_asym(*args, **kw).clone()
+    again = K.decode_attn_int4_asym(*args, **kw)
+    assert torch.equal(out, again)
+    assert_close(out, ref, f"two-row merge heads {heads}")
+
