@@ -423,7 +423,8 @@ struct QIn {
   u32x4 q;
   half_t tau, s, z;
   int4 oc;
-  half_t sj[4];  // static INT8 K: the scale of channel slice 32 lg + 8 j (any group size)
+  uint32_t sj[4];  // static INT8 K: the loaded bits (static_scale_bits) of the scale of
+                   // channel slice 32 lg + 8 j (any group size)
 };
 
 // INT4 asymmetric K with static scale s / zero-point z per (kv head, group of 32).  With
@@ -662,12 +663,18 @@ struct VAsymT {
   }
 };
 
-// fp16 scale of (kv head, group g) from a scale view that is static over b and t
-// (stride-0 view of per-token scales, fp16 or fp32; an fp32 scale is rounded to fp16)
-__device__ __forceinline__ half_t static_scale16(const KvDev& v, int hkv, int g) {
+// The scale of (kv head, group g) from a scale view that is static over b and t (stride-0
+// view of per-token scales, fp16 or fp32): static_scale_bits loads its bits (fp32, or fp16
+// in the low half), static_scale16 gives the fp16 scale (an fp32 scale rounded to fp16).
+// They are split so that the set-up converts after the first cache tiles are requested:
+// converting at the load made every wave wait for it before its first tile load.
+__device__ __forceinline__ uint32_t static_scale_bits(const KvDev& v, int hkv, int g) {
   const int64_t i = (int64_t)hkv * v.ssh + (int64_t)g * v.ssg;
-  return v.scale_f32 ? (half_t)reinterpret_cast<const float*>(v.scale)[i]
-                     : reinterpret_cast<const half_t*>(v.scale)[i];
+  return v.scale_f32 ? reinterpret_cast<const uint32_t*>(v.scale)[i]
+                     : (uint32_t)reinterpret_cast<const uint16_t*>(v.scale)[i];
+}
+__device__ __forceinline__ half_t static_scale16(uint32_t bits, int f32) {
+  return f32 ? (half_t)__builtin_bit_cast(float, bits) : __builtin_bit_cast(half_t, (uint16_t)bits);
 }
 
 // Two INT8 codes (the low bytes of the two halves of x, the high bytes zero) -> the fp16
@@ -706,6 +713,7 @@ struct KI8T {
   half2v s2[kNS];  // the scale of channel slice 32 lg + 8 j .. + 7 (its group), twice
   rsrc_t rk;
   uint32_t vk;
+  int sf32;  // the scale view holds fp32
   struct Raw {
     u32x4 w[4];  // [2 rb + i]: bytes [32 lg + 16 i, 32 lg + 16 i + 16) of token 16 rb + row
   };
@@ -715,6 +723,7 @@ struct KI8T {
     const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
     rk = buffer_rsrc(kb, (uint32_t)(a.cap * kD));
     vk = (uint32_t)(col * kD + 32 * lg);
+    sf32 = a.k.scale_f32;
   }
   __device__ void fetch_q(const DecodeArgs& a, int b, int hkv, int lane, int wave, QIn& in) const {
     const int col = lane & 15, lg = lane >> 4;
@@ -725,11 +734,11 @@ struct KI8T {
       // slice j of the lane's 32 channels lies in group (32 lg + 8 j) / gs (gs = 8 .. 128)
       const int sh = __builtin_ctz((unsigned)a.gs);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) in.sj[j] = static_scale16(a.k, hkv, (32 * lg + 8 * j) >> sh);
+      for (int j = 0; j < 4; ++j) in.sj[j] = static_scale_bits(a.k, hkv, (32 * lg + 8 * j) >> sh);
     } else {
-      in.sj[0] = static_scale16(a.k, hkv, lg);
+      in.sj[0] = static_scale_bits(a.k, hkv, lg);
     }
-    in.s = in.sj[0];
+    in.s = (half_t)1.0f;  // (the fused append quantizes with its own table)
     in.z = (half_t)0.0f;
     in.oc = int4{-1, -1, -1, -1};
   }
@@ -752,7 +761,10 @@ struct KI8T {
 #pragma unroll
     for (int j = 0; j < 4; ++j) qh[j] = __builtin_bit_cast(half8v, sh.qh[j][lane]);
 #pragma unroll
-    for (int j = 0; j < kNS; ++j) s2[j] = half2v{in.sj[j], in.sj[j]};
+    for (int j = 0; j < kNS; ++j) {
+      const half_t sv = static_scale16(in.sj[j], sf32);
+      s2[j] = half2v{sv, sv};
+    }
   }
   __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
     const uint32_t v = vk + (valid ? (uint32_t)tok * kD : kOutOfRange);
@@ -805,7 +817,8 @@ struct VI8RowT {
   __device__ __forceinline__ float* extra() { return nullptr; }
   rsrc_t rv;
   uint32_t vv;
-  half2v s2;  // the scale of the group of channels 8 col .. 8 col + 7, twice
+  uint32_t sbits;  // the scale of the group of channels 8 col .. 8 col + 7 (static_scale_bits)
+  int sf32;
   struct Raw {
     u32x2 w[8];  // token T(k)
   };
@@ -823,9 +836,8 @@ struct VI8RowT {
     const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
     rv = buffer_rsrc(vb, (uint32_t)(a.cap * kD));
     vv = (uint32_t)((4 * lg) * kD + 8 * col);
-    const half_t sv =
-        static_scale16(a.v, hkv, GS_ANY ? (8 * col) >> __builtin_ctz((unsigned)a.gs) : col >> 2);
-    s2 = half2v{sv, sv};
+    sbits = static_scale_bits(a.v, hkv, GS_ANY ? (8 * col) >> __builtin_ctz((unsigned)a.gs) : col >> 2);
+    sf32 = a.v.scale_f32;
   }
   // rows of a partial last tile past the capacity read 0; !valid: every load out of range
   __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
@@ -840,6 +852,9 @@ struct VI8RowT {
   __device__ __forceinline__ void mma(const Raw& r, half8v pb, half8v pl, float4v acc[8],
                                       const NibConsts& nc) const {
     (void)nc;
+    // (converted here, loop-invariant: the set-up does not wait for the table load)
+    const half_t sv = static_scale16(sbits, sf32);
+    const half2v s2 = {sv, sv};
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       // byte c % 4 of the tokens T(2p) and T(2p + 1) into the low bytes of the two halves
