@@ -682,7 +682,19 @@ static int tok_family(const kvq_decode_params* p) {
     return gs == 16 ? kTiledT8Kvg16 : kTiledT8Kv;
   }
   if (!ok(p->k, gs, wk) || !ok(p->v, vgs, i4 ? 1 : 1)) return kTiledNone;
-  if (i4) return gs == 16 ? kTiledT4g16 : kTiledT4;
+  if (i4) {
+    // groups of 16 or 32 in dense V scale rows (128 / gs fp32 per token, contiguous, rows
+    // 16-byte aligned) and 16-byte aligned code rows: the tile is read with 16-byte loads and
+    // gathered in LDS
+    const kvq_kv_view& v = p->v;
+    const int64_t ng = kD / vgs;
+    const bool staged = vgs <= 32 && v.scale_stride_t == ng && v.scale_stride_g == 1 &&
+                        ((uintptr_t)v.scale % 16) == 0 && (v.scale_stride_b * 4) % 16 == 0 &&
+                        (v.scale_stride_h * 4) % 16 == 0 && ((uintptr_t)v.codes % 16) == 0 &&
+                        v.stride_b % 16 == 0 && v.stride_h % 16 == 0;
+    if (staged) return gs == 16 ? kTiledT4g16s : kTiledT4s;
+    return gs == 16 ? kTiledT4g16 : kTiledT4;
+  }
   return gs == 16 ? kTiledT8g16 : kTiledT8;
 }
 

@@ -450,6 +450,9 @@ enum TiledFam {
   // INT8_SYM with per-token fp16 scales, or FP16 (the reference's MixedKVCache at K 4 bits)
   kTiledKtKv, kTiledKtT8, kTiledKtF,
   kTiledFT8,    // FP16 K, INT8_SYM V with per-token fp16 scales (MixedKVCache (16, 8))
+  // kTiledT4 / kTiledT4g16 whose V scale rows are dense and 16-byte aligned: V tiles read with
+  // 16-byte loads and gathered through LDS (VTokT<true, true>)
+  kTiledT4s, kTiledT4g16s,
 };
 // a tiled kernel and the formats of the fused row append built into it (-1: none)
 struct TiledFn {

@@ -54,6 +54,17 @@
 #include "decode_common.h"
 
 #include <cstdlib>
+#include <type_traits>
+
+// Tiles a row format's fused-append writer hands to its SIMD partner (decode_tiled_kernel):
+// with the INT4 group rescue (the writer also finds the rescue threshold), and for the other
+// row formats.
+#ifndef KVQ_SHED_RESCUE
+#define KVQ_SHED_RESCUE 3
+#endif
+#ifndef KVQ_SHED_ROW
+#define KVQ_SHED_ROW 1
+#endif
 
 namespace kvq {
 namespace {
@@ -1736,8 +1747,21 @@ struct KTokT {
 // (8 INT8 bytes or 4 packed INT4 bytes) of its 8 PV k-slot tokens T(k) = 4 lg + k (k < 4),
 // 16 + 4 lg + k - 4, and the scale of their group (8 col) / gs.  The A operand of MFMA c
 // (channel 8 col + c) is vhat = fp16(c * fp16(s)) of the 8 tokens, so acc / l is the output.
-template <bool I4>
+// STAGE (INT4 only; groups of 16 or 32 in dense scale rows, 16-byte aligned): the tile's 2 KB of code rows and its
+// block of scales are read with 16-byte loads (lane l: bytes [16 l, 16 l + 16) of each) and
+// passed through the wave's own LDS (stage()), from which each lane reads its gathered
+// operands with ds_read2_b32; the same operands reach the MFMAs as with the 8 + 8 dword
+// gathers per lane and tile that the other instantiation issues.
+template <bool I4, bool STAGE = false>
 struct VTokT {
+  static constexpr bool kStage = I4 && STAGE;
+  // LDS layout of a staged tile (per wave): 32 code rows, 80 bytes apart (64 + 16 of padding,
+  // so that the 4 token rows one read touches per lane group fall in distinct banks), then
+  // the 32 scale rows (16 or 32 bytes: groups of 32 or 16), 48 bytes apart (the same reason)
+  static constexpr int kCRow = 80;
+  static constexpr int kSRow = 48;
+  static constexpr int kSOff = 32 * kCRow;
+  static constexpr int kStageBytes = kSOff + 32 * kSRow;
   static constexpr int kRowFmt = I4 ? KVQ_FMT_INT4_SYM : KVQ_FMT_INT8_SYM;  // the fused append's V format
   static constexpr bool kResidual = false;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
@@ -1748,9 +1772,12 @@ struct VTokT {
   __device__ __forceinline__ float* extra() { return nullptr; }
   rsrc_t rv, rs;
   uint32_t vv, vs, sst;
+  // kStage: the lane's load offsets (code rows, scale block), LDS write offsets and read bases
+  uint32_t lc, ls, wc, ws, rc, rsb;
   struct Raw {
     uint32_t w[8][I4 ? 1 : 2];  // token T(k)
     uint32_t s[8];              // token T(k)'s scale (fp32 or fp16 bits)
+    u32x4 c0, c1, sc;           // kStage: the tile as loaded (16 bytes per lane of each)
   };
   __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
     (void)a; (void)hkv; (void)lane;
@@ -1772,9 +1799,51 @@ struct VTokT {
     sst = (uint32_t)(a.v.sst * kEs);
     rs = buffer_rsrc(sb, scale_bytes(a.cap, a.v.sst, a.vgs, kEs));
     vs = (uint32_t)((4 * lg) * sst + gi * a.v.ssg * kEs);
+    if constexpr (kStage) {
+      // a token's scale row: sst = 4 * (128 / gs) bytes, 32 (groups of 16) or 16 (of 32)
+      const uint32_t byte = (uint32_t)lane * 16u;
+      lc = byte;
+      ls = byte < 32u * sst ? byte : kOutOfRange;
+      wc = (uint32_t)(lane >> 2) * kCRow + (uint32_t)(lane & 3) * 16u;
+      ws = kSOff + (byte / sst) * kSRow + byte % sst;
+      // pair p reads tokens T(2 p), T(2 p) + 1 = 4 lg + {0, 2, 16, 18}[p] and the next row
+      rc = (uint32_t)(4 * lg) * kCRow + (uint32_t)col * 4u;
+      rsb = kSOff + (uint32_t)(4 * lg) * kSRow + (uint32_t)gi * 4u;
+    }
+  }
+  // kStage: write the tile's rows and scales to the wave's LDS and read back the lane's
+  // gathered operands (LDS operations of one wave execute in order: no barrier)
+  __device__ __forceinline__ void stage(Raw& r, int wave) const {
+    if constexpr (kStage) {
+      __shared__ __attribute__((aligned(16))) uint8_t vst[kTW][kStageBytes];
+      uint8_t* base = vst[wave];
+      *reinterpret_cast<u32x4*>(base + wc) = r.c0;
+      *reinterpret_cast<u32x4*>(base + wc + 16 * kCRow) = r.c1;
+      if (ls != kOutOfRange) *reinterpret_cast<u32x4*>(base + ws) = r.sc;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t dt = p == 0 ? 0u : p == 1 ? 2u : p == 2 ? 16u : 18u;
+        const uint32_t* cr = reinterpret_cast<const uint32_t*>(base + rc + dt * kCRow);
+        r.w[2 * p][0] = cr[0];
+        r.w[2 * p + 1][0] = cr[kCRow / 4];
+        const uint32_t* sr = reinterpret_cast<const uint32_t*>(base + rsb + dt * kSRow);
+        r.s[2 * p] = sr[0];
+        r.s[2 * p + 1] = sr[kSRow / 4];
+      }
+    } else {
+      (void)r;
+      (void)wave;
+    }
   }
   // rows of a partial last tile past the capacity read 0; !valid: every load out of range
   __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
+    if constexpr (kStage) {
+      const uint32_t o = valid ? (uint32_t)tok * kRow : kOutOfRange;
+      r.c0 = bload4(rv, lc + o, 0);
+      r.c1 = bload4(rv, lc + o + 16u * kRow, 0);
+      r.sc = bload4(rs, ls + (valid ? (uint32_t)tok * sst : kOutOfRange), 0);
+      return;
+    }
     const uint32_t v = vv + (valid ? (uint32_t)tok * kRow : kOutOfRange);
     const uint32_t p = vs + (valid ? (uint32_t)tok * sst : kOutOfRange);
 #pragma unroll
@@ -2130,6 +2199,12 @@ __device__ WgRows share_waves(const DecodeArgs& a, int lin) {
 
 // SHARE: the instantiation for the shared split (a.share); the other one carries none of
 // its code (it cost the grid split 0.2 us per launch at the headline shape).
+// V operand types that pass their tiles through LDS (VTokT<true, true>) have kStage
+template <class T, class = void>
+struct v_staged : std::false_type {};
+template <class T>
+struct v_staged<T, std::void_t<decltype(T::kStage)>> : std::bool_constant<T::kStage> {};
+
 template <class KF, class VF, int LOOK, bool PACK8, bool SHARE, int WPE = 2>
 __global__ __launch_bounds__(kTW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void decode_tiled_kernel(DecodeArgs a) {
@@ -2202,6 +2277,37 @@ void decode_tiled_kernel(DecodeArgs a) {
   const bool app_on = APP && a.app.kx != nullptr;
   const int wt = app_on ? (int)(a.app.wpos / kTile) : 0;
   const bool writer = app_on && !rowless && first == wt % stride;
+  // Tiles shed by the writer.  A row format's writer quantizes its row pair before its loop
+  // (with the group rescue it also finds the threshold over every new row), so its stream
+  // starts late and it used to end its loop several us after every other wave of its
+  // (b, kv head); its SIMD partner, which has the SIMD to itself meanwhile, takes the
+  // writer's first kShed tiles before its own.  The schedule stays static (results do not
+  // depend on timing), and the writer keeps tile wt: shedding applies only when the writer
+  // holds at least kShed + LOOK + 2 tiles, so wt is neither shed nor one of its early loads.
+  int t_first = first;        // the wave's first tile
+  int sw_at = -1, sw_to = 0;  // the partner continues at sw_to after tile sw_at
+  int extra = 0;              // tiles taken (+) or shed (-): the pacing compares remainders
+  if constexpr (KF::kAppendRow && !SHARE) {
+    constexpr int kShed = KF::kRescue ? KVQ_SHED_RESCUE : KVQ_SHED_ROW;
+    const int wfirst = wt % stride;              // the writer's first tile
+    const int ww = wfirst - wr.v0;               // its wave, when in this work-group
+    const int nw = (wt - wfirst) / stride + 1;   // its tiles up to wt
+    if (kShed > 0 && app_on && ww >= 0 && ww < kTW && nw >= kShed + LOOK + 2) {
+      if (wave == ww) {
+        t_first = first + kShed * stride;
+        extra = -kShed;
+      } else if (wave == (ww ^ 4)) {
+        t_first = wfirst;
+        sw_at = wfirst + (kShed - 1) * stride;
+        sw_to = first;
+        extra = kShed;
+      }
+    }
+  }
+  auto tnext = [&](int t) {
+    if constexpr (KF::kAppendRow && !SHARE) return t == sw_at ? sw_to : t + stride;
+    else return t + stride;
+  };
   AppendIn ain;
   AppendFlags afl;
   [[maybe_unused]] RowPre rpre;
@@ -2213,7 +2319,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   // each publishes its step count and, when ahead of its partner, lowers its priority,
   // so the two stay in step (the tile schedule, and so every result bit, is fixed).
   __shared__ int progress[kTW];
-  progress[wave] = 0;
+  progress[wave] = -extra;
   KF kf;
   // the q-side inputs are requested first: the wait for them then does not include the
   // cache tiles requested next
@@ -2250,7 +2356,7 @@ void decode_tiled_kernel(DecodeArgs a) {
   // tile[j] = tile of step i + j (j <= LOOK + 1)
   int tile[LOOK + 2];
 #pragma unroll
-  for (int j = 0; j <= LOOK; ++j) tile[j] = first + j * stride;
+  for (int j = 0; j <= LOOK; ++j) tile[j] = j == 0 ? t_first : tnext(tile[j - 1]);
   constexpr int R = LOOK + 1;                 // ring slots per stream
   constexpr int U = (R % 2 == 0) ? R : 2 * R;  // unroll: ring slot and x buffer are static
   typename KF::Raw kr[R];
@@ -2368,12 +2474,14 @@ void decode_tiled_kernel(DecodeArgs a) {
         if (tile[0] >= ntot) break;
         if constexpr (!KF::kAppendRow)
           if (late_write && !store_now && steps == store_step) app_store();
-        tile[LOOK + 1] = tile[LOOK] + stride;
+        tile[LOOK + 1] = tnext(tile[LOOK]);
         // fetch K of step i + LOOK + 1 (into the slot K of step i used) and V of step
         // i + LOOK (into the slot V of step i - 1 used), QK of step i + 1, then softmax
         // and PV of step i
         kf.load(kTile * tile[LOOK + 1], tile[LOOK + 1] < ntot, kr[u % R]);
         vf.load(kTile * tile[LOOK], tile[LOOK] < ntot, vr[(u + LOOK) % R]);
+        // (staged V: this step's tile through the wave's LDS, while QK and the softmax run)
+        if constexpr (v_staged<VF>::value) vf.stage(vr[u % R], wave);
         if (tile[1] < ntot) kf.qk(kr[(u + 1) % R], nc, x[(u + 1) & 1][0], x[(u + 1) & 1][1]);
         float4v x0 = x[u & 1][0], x1 = x[u & 1][1];
         if (partial && tile[0] == ntot - 1) {
@@ -2391,8 +2499,8 @@ void decode_tiled_kernel(DecodeArgs a) {
           vf.mma(vr[u % R], pb, pl, acc, nc);
         }
         ++steps;
-        progress[wave] = steps;
-        if (__builtin_amdgcn_readfirstlane(progress[wave ^ 4]) < steps)
+        progress[wave] = steps - extra;
+        if (__builtin_amdgcn_readfirstlane(progress[wave ^ 4]) < steps - extra)
           __builtin_amdgcn_s_setprio(0);
         else
           __builtin_amdgcn_s_setprio(2);

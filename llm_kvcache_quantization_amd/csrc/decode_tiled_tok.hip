@@ -10,6 +10,8 @@ TiledFn tiled_kernel_tok(int fam, bool pack8) {
     case kTiledT8g16: return tiled_pick<KTokT<false, 2>, VTokT<false>>(pack8);
     case kTiledT4: return tiled_pick<KTokT<true, 1>, VTokT<true>>(pack8);
     case kTiledT4g16: return tiled_pick<KTokT<true, 2>, VTokT<true>>(pack8);
+    case kTiledT4s: return tiled_pick<KTokT<true, 1>, VTokT<true, true>>(pack8);
+    case kTiledT4g16s: return tiled_pick<KTokT<true, 2>, VTokT<true, true>>(pack8);
     case kTiledT8Kv: return tiled_pick<KTokT<false, 1>, VKiviRowT>(pack8);
     case kTiledT8Kvg16: return tiled_pick<KTokT<false, 2>, VKiviRowT>(pack8);
     case kTiledT8F: return tiled_pick<KTokT<false, 1>, VF16RowT>(pack8);

@@ -8,6 +8,12 @@ through append and then the decode kernel (two launches).  At every step, codes,
 zero-points and outputs must be bit-identical.  The fused output must also be within
 max-abs 2e-3 (one fp16 ulp where |out| >= 4) and cosine 0.9999 of the oracle's attention
 over the stored cache.
+
+When a wave runs long enough (the writer of a per-token INT4 / INT8 step holds at least
+kShed + 3 tiles: KVQ_SHED_ROW = 1, KVQ_SHED_RESCUE = 3), the fused kernel's writer hands
+its first tiles to its SIMD partner; the two paths then sum the same tiles in different
+waves, so their outputs agree within the oracle bound rather than bit for bit
+(test_fused_rows_writer_sheds_tiles).  The cases above stay below that length.
 """
 import math
 
@@ -288,3 +294,61 @@ def test_fused_rows_one_row_first_token(eng):
         torch.cuda.synchronize()
         _equal(t1, t2, f"{eng} step {i}")
         assert torch.equal(out1, out2), f"{eng} step {i}"
+
+
+SHED = [
+    # kind, engine arguments (per-token formats whose writer sheds tiles at long runs)
+    ("int4", dict(group_size=16, static=True, outlier_rescue_ratio=0.01)),  # int4_fused: 3 tiles
+    ("int4", dict(group_size=32)),                                          # int4_baseline: 1 tile
+    ("int8", dict(group_size=16)),                                          # int8_baseline-like
+]
+
+
+@pytest.mark.parametrize("kind,kw", SHED)
+def test_fused_rows_writer_sheds_tiles(kind, kw, monkeypatch):
+    """Chunks of 4096 tokens over an 8.3k context: every wave holds about 11 tiles, so the
+    fused writer sheds its first tiles to its SIMD partner.  Codes and scales stay
+    bit-identical to the two-launch path; the outputs agree with each other within 2e-3 and
+    with the oracle within the bound."""
+    monkeypatch.setenv("KVQ_CHUNK_TOKENS", "4096")
+    K = _k()
+    B, H, Hq, S0, steps = 2, 2, 12, 8290, 2
+    print(f"[case] shed {kind} {kw}", flush=True)
+    kw = dict(kw)
+    g = gen(99 + len(kw))
+    G = 128 // kw["group_size"]
+    if kw.pop("static", False):
+        st = torch.rand(1, H, G, generator=g) * 0.3 + 0.1
+        kw["static_k_scale"], kw["static_v_scale"] = st, st * 0.8
+    cls = K.INT8KVCache if kind == "int8" else K.INT4KVCache
+    one = cls(1, device=DEV, check_numerics=False, **kw)
+    two = cls(1, device=DEV, check_numerics=False, **kw)
+    assert one._fused_step_ok(128, B, H)
+    two._fused_step_ok = lambda *args: False
+    k, v = _kv(B, H, S0 + steps, g)
+    for c in (one, two):
+        c.append(0, k[:, :, :S0].to(DEV), v[:, :, :S0].to(DEV))
+    assert one._step_for(0, Hq).params.chunk_tokens == 4096
+    sm = 1 / math.sqrt(128)
+    tau = (torch.rand(Hq, generator=g) * 0.4 + 0.8).to(torch.float16)
+    get = (lambda c: c.get_int8_tensors(0)) if kind == "int8" else (lambda c: c.get_int4_tensors(0))
+    for i in range(steps):
+        kn, vn = k[:, :, S0 + i:S0 + i + 1].to(DEV), v[:, :, S0 + i:S0 + i + 1].to(DEV)
+        q = torch.randn(B, Hq, 128, generator=g).to(torch.float16)
+        out1 = one.append_decode_attn(0, q.to(DEV), kn, vn, sm_scale=sm, inv_tau=tau.to(DEV))
+        out2 = two.append_decode_attn(0, q.to(DEV), kn, vn, sm_scale=sm, inv_tau=tau.to(DEV))
+        torch.cuda.synchronize()
+        t1 = get(one)
+        _equal(t1, get(two), f"shed {kind} step {i}")
+        d = (out1.float() - out2.float()).abs().max().item()
+        assert d <= ATOL, (kind, i, d)
+        kc, vc, ks, vs = [t.cpu() for t in t1]
+        n = S0 + i + 1
+        cl = torch.full((B,), n, dtype=torch.int32)
+        qq = OA.prescale_q(q, tau)
+        if kind == "int8":
+            ref = OA.decode_attn_int8_torch_ref(qq, kc, vc, ks.half(), vs.half(), cl, sm)
+        else:
+            ref = OA.decode_attn_int4_torch_ref(qq, kc, vc, ks.half(), vs.half(), cl, sm)
+        assert_close_ulp(out1, ref, f"shed {kind} {n}")
+        assert_close_ulp(out2, ref, f"shed two {kind} {n}")

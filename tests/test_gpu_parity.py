@@ -528,6 +528,15 @@ def test_decode_per_token_scales_tiled(bits, G, B, Hq, Hkv, S, ctx, static):
     out = plan.launch().clone()
     assert torch.equal(out, plan.launch()), "repeated launches differ"
     assert_close(out, ref, f"per-token int{bits} G{G} B{B} Hq{Hq} Hkv{Hkv} S{S} static={static}")
+    if bits == 4 and not static:
+        # the same V scales in rows padded to G + 4 values (not dense): the kernel then gathers
+        # the V operands with per-lane dword loads instead of 16-byte loads through LDS; the
+        # operands, and so the bits, are the same
+        vpad = torch.full((B, Hkv, S, G + 4), float("nan"), dtype=sdt, device=DEV)
+        vpad[..., :G] = vsd
+        plan2 = DecodePlan(d(q), fmt, kv_view_tok(d(kx), ksd), fmt, kv_view_tok(d(vx), vpad[..., :G]),
+                           d(cl), Hkv, S, sm, 128 // G, inv_tau=d(tau))
+        assert torch.equal(plan2.launch(), out), "V gathered through LDS and by dword loads differ"
     if bits == 8 and not static:  # the public entry point takes the same kernel
         pub = K.decode_attn_int8(d(qs), d(kc), d(vc), d(ks), d(vs), d(cl), sm_scale=sm)
         assert_close(pub, ref, f"decode_attn_int8 per-token G{G}")
