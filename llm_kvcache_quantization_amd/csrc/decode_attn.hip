@@ -652,6 +652,12 @@ static bool kivi_k_per_token(const kvq_kv_view& v) {
 // (16 tokens per batch), so its time grows with the window (about 1 us per 256 tokens)
 constexpr int kMaxResidual = 65536;
 
+// code rows whose every (b, head) slab starts 16-byte aligned: the V tiles can be read with
+// 16-byte loads (the staged V operand types)
+static bool rows16_aligned(const kvq_kv_view& v) {
+  return ((uintptr_t)v.codes % 16) == 0 && v.stride_b % 16 == 0 && v.stride_h % 16 == 0;
+}
+
 static int tok_family(const kvq_decode_params* p) {
   if (p->v.layout != KVQ_LAYOUT_ROWS) return kTiledNone;
   const bool kivi_v = p->k_format == KVQ_FMT_INT8_SYM &&
@@ -679,6 +685,7 @@ static int tok_family(const kvq_decode_params* p) {
       return p->v.stride_t == 2 * kD ? (gs == 16 ? kTiledT8Fg16 : kTiledT8F) : kTiledNone;
     // V codes in dense 64-byte rows, fp32 scale / zero-point per token (checked by check_view)
     if (p->v.stride_t != kD / 2 || p->v.scale_stride_t != 1) return kTiledNone;
+    if (rows16_aligned(p->v)) return gs == 16 ? kTiledT8Kvg16s : kTiledT8Kvs;
     return gs == 16 ? kTiledT8Kvg16 : kTiledT8Kv;
   }
   if (!ok(p->k, gs, wk) || !ok(p->v, vgs, i4 ? 1 : 1)) return kTiledNone;
@@ -690,8 +697,7 @@ static int tok_family(const kvq_decode_params* p) {
     const int64_t ng = kD / vgs;
     const bool staged = vgs <= 32 && v.scale_stride_t == ng && v.scale_stride_g == 1 &&
                         ((uintptr_t)v.scale % 16) == 0 && (v.scale_stride_b * 4) % 16 == 0 &&
-                        (v.scale_stride_h * 4) % 16 == 0 && ((uintptr_t)v.codes % 16) == 0 &&
-                        v.stride_b % 16 == 0 && v.stride_h % 16 == 0;
+                        (v.scale_stride_h * 4) % 16 == 0 && rows16_aligned(v);
     if (staged) return gs == 16 ? kTiledT4g16s : kTiledT4s;
     return gs == 16 ? kTiledT4g16 : kTiledT4;
   }
@@ -729,7 +735,8 @@ static int tiled_family(const kvq_decode_params* p) {
     static const int fams[3][3] = {{kTiledKivi, kTiledKv48, kTiledKv4F},
                                    {kTiledKv84, kTiledKv88, kTiledKv8F},
                                    {kTiledKvF4, kTiledKvF8, kTiledKvFF}};
-    return fams[idx(p->k_format)][idx(p->v_format)];
+    const int fam = fams[idx(p->k_format)][idx(p->v_format)];
+    return (fam == kTiledKivi && rows16_aligned(p->v)) ? kTiledKivis : fam;
   }
   if (p->k_format == KVQ_FMT_INT4_ASYM)
     return (p->v_format == KVQ_FMT_INT4_ASYM && vt) ? (p->k.n_outlier > 0 ? kTiledA4A4o : kTiledA4A4)

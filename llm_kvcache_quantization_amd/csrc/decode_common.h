@@ -453,6 +453,9 @@ enum TiledFam {
   // kTiledT4 / kTiledT4g16 whose V scale rows are dense and 16-byte aligned: V tiles read with
   // 16-byte loads and gathered through LDS (VTokT<true, true>)
   kTiledT4s, kTiledT4g16s,
+  // kTiledKivi / kTiledT8Kv / kTiledT8Kvg16 with 16-byte aligned V code rows: the V rows read
+  // with 16-byte loads and gathered through LDS (VKiviRowTS)
+  kTiledKivis, kTiledT8Kvs, kTiledT8Kvg16s,
 };
 // a tiled kernel and the formats of the fused row append built into it (-1: none)
 struct TiledFn {

@@ -1079,6 +1079,45 @@ struct KTokAsymT : KAsymT<false> {
   }
 };
 
+// A tile's 32 packed INT4 token rows (64 bytes each, contiguous) passed through the wave's
+// own LDS, for the V operand types that read token rows: lane l loads bytes [16 l, 16 l + 16)
+// of each KB half with one 16-byte load (2 per tile instead of 8 dword gathers), writes them
+// to rows kRowB = 80 bytes apart (16 bytes of padding put the 4 token rows one read touches
+// per lane group in distinct banks), and reads back dword col of its 8 k-slot tokens T(k) =
+// 4 lg + {0, 1, 2, 3, 16, 17, 18, 19}, two rows per ds_read2_b32.  LDS operations of one
+// wave execute in order, so no barrier is needed.
+struct Rows64Lds {
+  static constexpr int kRowB = 80;
+  static constexpr int kBytes = 32 * kRowB;
+  uint32_t lc, wc, rc;
+  __device__ void setup(int lane) {
+    const int col = lane & 15, lg = lane >> 4;
+    lc = (uint32_t)lane * 16u;
+    wc = (uint32_t)(lane >> 2) * kRowB + (uint32_t)(lane & 3) * 16u;
+    rc = (uint32_t)(4 * lg) * kRowB + (uint32_t)col * 4u;
+  }
+  // o: the tile's byte offset in the slab (kOutOfRange: nothing loaded)
+  __device__ __forceinline__ void load(rsrc_t r, uint32_t o, u32x4& c0, u32x4& c1) const {
+    c0 = bload4(r, lc + o, 0);
+    c1 = bload4(r, lc + o + 16u * (kD / 2), 0);
+  }
+  __device__ __forceinline__ void write(uint8_t* base, const u32x4& c0, const u32x4& c1) const {
+    *reinterpret_cast<u32x4*>(base + wc) = c0;
+    *reinterpret_cast<u32x4*>(base + wc + 16 * kRowB) = c1;
+  }
+  // w[k]: dword col of token T(k)
+  __device__ __forceinline__ void gather(const uint8_t* base, uint32_t w[8]) const {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t dt = p == 0 ? 0u : p == 1 ? 2u : p == 2 ? 16u : 18u;
+      const uint32_t* cr = reinterpret_cast<const uint32_t*>(base + rc + dt * kRowB);
+      w[2 * p] = cr[0];
+      w[2 * p + 1] = cr[kRowB / 4];
+    }
+  }
+};
+
+
 // V of the KIVI layout in token rows (64 bytes).  Lane (col, lg) reads the dword of
 // channels 8 col .. 8 col + 7 of each of its 8 PV k-slot tokens T(k) (four 64-byte rows
 // per load instruction) and their fp32 scale / zero-point.  The codes enter the MFMA as
@@ -1090,17 +1129,21 @@ struct KTokAsymT : KAsymT<false> {
 // with w rounded to about 2^-22 of itself instead of the 2^-11 of one fp16 operand (the
 // reference dequantises V in fp32).  The wave keeps Lp and Cz beside l (the softmax
 // rescales them with l) and finalize() folds them into acc before the merge (out = acc / l).
-struct VKiviRowT {
+template <bool STAGE>
+struct VKiviRowTT {
+  static constexpr bool kStage = STAGE;  // code rows through LDS (Rows64Lds)
   static constexpr int kRowFmt = KVQ_FMT_INT4_KIVI;  // the fused append's V format
   static constexpr bool kResidual = true;  // merges an fp16 residual window
   static constexpr bool kPackedPV = false;
   static constexpr bool kTile32 = false;
   rsrc_t rv, rs, rz;
   uint32_t vv, vp;
+  Rows64Lds cst;  // STAGE
   float ex[2];  // Lp, Cz (rescaled with l by the softmax)
   struct Raw {
     uint32_t w[8];     // token T(k): bytes 4 col .. 4 col + 3
     float4v s[2], z[2];  // tokens 4 lg + i, 16 + 4 lg + i
+    u32x4 c0, c1;      // STAGE: the tile's code rows as loaded
   };
   __device__ static void epi_params(const DecodeArgs& a, int hkv, int lane, float& s, float& z) {
     (void)a; (void)hkv; (void)lane;
@@ -1121,15 +1164,31 @@ struct VKiviRowT {
     rz = buffer_rsrc(reinterpret_cast<const float*>(a.v.zp) + po, (uint32_t)(a.cap * 4));
     vp = (uint32_t)(4 * lg) * 4u;
     ex[0] = ex[1] = 0.f;
+    if constexpr (STAGE) cst.setup(lane);
+  }
+  // STAGE: the tile's code rows through the wave's LDS into w (Rows64Lds)
+  __device__ __forceinline__ void stage(Raw& r, int wave) const {
+    if constexpr (STAGE) {
+      __shared__ __attribute__((aligned(16))) uint8_t vst[kTW][Rows64Lds::kBytes];
+      cst.write(vst[wave], r.c0, r.c1);
+      cst.gather(vst[wave], r.w);
+    } else {
+      (void)r;
+      (void)wave;
+    }
   }
   __device__ __forceinline__ float* extra() { return ex; }
   // rows of a partial last tile past the capacity read 0; !valid: every load out of range
   __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
-    const uint32_t v = vv + (valid ? (uint32_t)tok * (kD / 2) : kOutOfRange);
+    if constexpr (STAGE) {
+      cst.load(rv, valid ? (uint32_t)tok * (kD / 2) : kOutOfRange, r.c0, r.c1);
+    } else {
+      const uint32_t v = vv + (valid ? (uint32_t)tok * (kD / 2) : kOutOfRange);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
-      r.w[k] = bload1(rv, v + t * (kD / 2), 0);
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t t = (k < 4) ? (uint32_t)k : (uint32_t)(12 + k);  // 16 + k - 4
+        r.w[k] = bload1(rv, v + t * (kD / 2), 0);
+      }
     }
     const uint32_t p = vp + (valid ? (uint32_t)tok * 4u : kOutOfRange);
     r.s[0] = __builtin_bit_cast(float4v, bload4(rs, p, 0));
@@ -1211,6 +1270,10 @@ struct VKiviRowT {
     }
   }
 };
+using VKiviRowT = VKiviRowTT<false>;
+// the same with the code rows read by 16-byte loads and gathered through LDS (16-byte aligned
+// code rows)
+using VKiviRowTS = VKiviRowTT<true>;
 
 // ---- The KIVI family with 8-bit codes and 16-bit sides: the reference's quant_bits=8 KIVI
 // cache (src/cache/kivi_style_cache.py) and the per-layer (k_bits, v_bits) pairs of its
@@ -1755,12 +1818,11 @@ struct KTokT {
 template <bool I4, bool STAGE = false>
 struct VTokT {
   static constexpr bool kStage = I4 && STAGE;
-  // LDS layout of a staged tile (per wave): 32 code rows, 80 bytes apart (64 + 16 of padding,
-  // so that the 4 token rows one read touches per lane group fall in distinct banks), then
-  // the 32 scale rows (16 or 32 bytes: groups of 32 or 16), 48 bytes apart (the same reason)
-  static constexpr int kCRow = 80;
+  // LDS layout of a staged tile (per wave): the 32 code rows (Rows64Lds), then the 32 scale
+  // rows (16 or 32 bytes: groups of 32 or 16), 48 bytes apart (so that the 4 rows one read
+  // touches per lane group fall in distinct banks)
   static constexpr int kSRow = 48;
-  static constexpr int kSOff = 32 * kCRow;
+  static constexpr int kSOff = Rows64Lds::kBytes;
   static constexpr int kStageBytes = kSOff + 32 * kSRow;
   static constexpr int kRowFmt = I4 ? KVQ_FMT_INT4_SYM : KVQ_FMT_INT8_SYM;  // the fused append's V format
   static constexpr bool kResidual = false;  // merges an fp16 residual window
@@ -1772,8 +1834,10 @@ struct VTokT {
   __device__ __forceinline__ float* extra() { return nullptr; }
   rsrc_t rv, rs;
   uint32_t vv, vs, sst;
-  // kStage: the lane's load offsets (code rows, scale block), LDS write offsets and read bases
-  uint32_t lc, ls, wc, ws, rc, rsb;
+  // kStage: the code rows' staging, the lane's scale-block load offset, LDS write offset and
+  // read base
+  Rows64Lds cst;
+  uint32_t ls, ws, rsb;
   struct Raw {
     uint32_t w[8][I4 ? 1 : 2];  // token T(k)
     uint32_t s[8];              // token T(k)'s scale (fp32 or fp16 bits)
@@ -1802,12 +1866,10 @@ struct VTokT {
     if constexpr (kStage) {
       // a token's scale row: sst = 4 * (128 / gs) bytes, 32 (groups of 16) or 16 (of 32)
       const uint32_t byte = (uint32_t)lane * 16u;
-      lc = byte;
+      cst.setup(lane);
       ls = byte < 32u * sst ? byte : kOutOfRange;
-      wc = (uint32_t)(lane >> 2) * kCRow + (uint32_t)(lane & 3) * 16u;
       ws = kSOff + (byte / sst) * kSRow + byte % sst;
-      // pair p reads tokens T(2 p), T(2 p) + 1 = 4 lg + {0, 2, 16, 18}[p] and the next row
-      rc = (uint32_t)(4 * lg) * kCRow + (uint32_t)col * 4u;
+      // pair p reads the scales of tokens T(2 p), T(2 p) + 1 = 4 lg + {0, 2, 16, 18}[p] + {0, 1}
       rsb = kSOff + (uint32_t)(4 * lg) * kSRow + (uint32_t)gi * 4u;
     }
   }
@@ -1817,15 +1879,15 @@ struct VTokT {
     if constexpr (kStage) {
       __shared__ __attribute__((aligned(16))) uint8_t vst[kTW][kStageBytes];
       uint8_t* base = vst[wave];
-      *reinterpret_cast<u32x4*>(base + wc) = r.c0;
-      *reinterpret_cast<u32x4*>(base + wc + 16 * kCRow) = r.c1;
+      cst.write(base, r.c0, r.c1);
       if (ls != kOutOfRange) *reinterpret_cast<u32x4*>(base + ws) = r.sc;
+      uint32_t w[8];
+      cst.gather(base, w);
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
         const uint32_t dt = p == 0 ? 0u : p == 1 ? 2u : p == 2 ? 16u : 18u;
-        const uint32_t* cr = reinterpret_cast<const uint32_t*>(base + rc + dt * kCRow);
-        r.w[2 * p][0] = cr[0];
-        r.w[2 * p + 1][0] = cr[kCRow / 4];
+        r.w[2 * p][0] = w[2 * p];
+        r.w[2 * p + 1][0] = w[2 * p + 1];
         const uint32_t* sr = reinterpret_cast<const uint32_t*>(base + rsb + dt * kSRow);
         r.s[2 * p] = sr[0];
         r.s[2 * p + 1] = sr[kSRow / 4];
@@ -1838,9 +1900,7 @@ struct VTokT {
   // rows of a partial last tile past the capacity read 0; !valid: every load out of range
   __device__ __forceinline__ void load(int tok, bool valid, Raw& r) const {
     if constexpr (kStage) {
-      const uint32_t o = valid ? (uint32_t)tok * kRow : kOutOfRange;
-      r.c0 = bload4(rv, lc + o, 0);
-      r.c1 = bload4(rv, lc + o + 16u * kRow, 0);
+      cst.load(rv, valid ? (uint32_t)tok * kRow : kOutOfRange, r.c0, r.c1);
       r.sc = bload4(rs, ls + (valid ? (uint32_t)tok * sst : kOutOfRange), 0);
       return;
     }

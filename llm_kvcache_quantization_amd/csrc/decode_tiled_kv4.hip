@@ -7,6 +7,7 @@ namespace kvq {
 TiledFn tiled_kernel_kv4(int fam, bool pack8) {
   switch (fam) {
     case kTiledKivi: return tiled_pick<KKiviT, VKiviRowT>(pack8);
+    case kTiledKivis: return tiled_pick<KKiviT, VKiviRowTS>(pack8);
     case kTiledKv48: return tiled_pick<KKiviT, VKivi8RowT>(pack8);
     case kTiledKv4F: return tiled_pick<KKiviT, VF16RowT>(pack8);
     case kTiledKv84: return tiled_pick<KKivi8T, VKiviRowT>(pack8);
