@@ -56,9 +56,9 @@
 #include <cstdlib>
 #include <type_traits>
 
-// Tiles a row format's fused-append writer hands to its SIMD partner (decode_tiled_kernel):
-// with the INT4 group rescue (the writer also finds the rescue threshold), and for the other
-// row formats.
+// Tiles a row format's fused-append writer hands to waves of the other SIMDs (at most 6;
+// decode_tiled_kernel): with the INT4 group rescue (the writer also finds the rescue
+// threshold), and for the other row formats.
 #ifndef KVQ_SHED_RESCUE
 #define KVQ_SHED_RESCUE 3
 #endif
@@ -2340,27 +2340,33 @@ void decode_tiled_kernel(DecodeArgs a) {
   // Tiles shed by the writer.  A row format's writer quantizes its row pair before its loop
   // (with the group rescue it also finds the threshold over every new row), so its stream
   // starts late and it used to end its loop several us after every other wave of its
-  // (b, kv head); its SIMD partner, which has the SIMD to itself meanwhile, takes the
-  // writer's first kShed tiles before its own.  The schedule stays static (results do not
-  // depend on timing), and the writer keeps tile wt: shedding applies only when the writer
-  // holds at least kShed + LOOK + 2 tiles, so wt is neither shed nor one of its early loads.
+  // (b, kv head).  Its first kShed tiles go one each to waves of the other three SIMDs
+  // (giving them to its SIMD partner, which shares the writer's issue slots, gained less),
+  // which take them before their own.  The schedule stays static (results do not depend on
+  // timing), and the writer keeps tile wt: shedding applies only when the writer holds at
+  // least kShed + LOOK + 2 tiles, so wt is neither shed nor one of its early loads.
   int t_first = first;        // the wave's first tile
-  int sw_at = -1, sw_to = 0;  // the partner continues at sw_to after tile sw_at
+  int sw_at = -1, sw_to = 0;  // a receiver continues at sw_to after tile sw_at
   int extra = 0;              // tiles taken (+) or shed (-): the pacing compares remainders
   if constexpr (KF::kAppendRow && !SHARE) {
     constexpr int kShed = KF::kRescue ? KVQ_SHED_RESCUE : KVQ_SHED_ROW;
+    static_assert(kShed >= 0 && kShed <= 6, "one shed tile per wave of the other SIMDs");
     const int wfirst = wt % stride;              // the writer's first tile
     const int ww = wfirst - wr.v0;               // its wave, when in this work-group
     const int nw = (wt - wfirst) / stride + 1;   // its tiles up to wt
     if (kShed > 0 && app_on && ww >= 0 && ww < kTW && nw >= kShed + LOOK + 2) {
+      // receiver i (i < kShed <= 6) of the writer's tile i: the waves of the other three SIMDs,
+      // in the order (ww + 1) % 4, its partner, (ww + 2) % 4, ..
+      const int sd = (wave - ww) & 3;                 // SIMD distance from the writer's
+      const int ri = sd == 0 ? -1 : 2 * (sd - 1) + (((wave ^ ww) & 4) ? 1 : 0);
       if (wave == ww) {
         t_first = first + kShed * stride;
         extra = -kShed;
-      } else if (wave == (ww ^ 4)) {
-        t_first = wfirst;
-        sw_at = wfirst + (kShed - 1) * stride;
+      } else if (ri >= 0 && ri < kShed) {
+        t_first = wfirst + ri * stride;
+        sw_at = t_first;
         sw_to = first;
-        extra = kShed;
+        extra = 1;
       }
     }
   }

@@ -11,7 +11,7 @@ over the stored cache.
 
 When a wave runs long enough (the writer of a per-token INT4 / INT8 step holds at least
 kShed + 3 tiles: KVQ_SHED_ROW = 1, KVQ_SHED_RESCUE = 3), the fused kernel's writer hands
-its first tiles to its SIMD partner; the two paths then sum the same tiles in different
+its first tiles to waves of the other SIMDs; the two paths then sum the same tiles in different
 waves, so their outputs agree within the oracle bound rather than bit for bit
 (test_fused_rows_writer_sheds_tiles).  The cases above stay below that length.
 """
@@ -307,7 +307,7 @@ SHED = [
 @pytest.mark.parametrize("kind,kw", SHED)
 def test_fused_rows_writer_sheds_tiles(kind, kw, monkeypatch):
     """Chunks of 4096 tokens over an 8.3k context: every wave holds about 11 tiles, so the
-    fused writer sheds its first tiles to its SIMD partner.  Codes and scales stay
+    fused writer sheds its first tiles to waves of other SIMDs.  Codes and scales stay
     bit-identical to the two-launch path; the outputs agree with each other within 2e-3 and
     with the oracle within the bound."""
     monkeypatch.setenv("KVQ_CHUNK_TOKENS", "4096")
