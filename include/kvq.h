@@ -270,7 +270,11 @@ int64_t kvq_append_scratch_bytes(const kvq_append_params* p);
  * Replaces the append + attention pair of the reference's decode step,
  *   cache.append(layer, k, v)            src/engine/patch_model.py:755
  *   decode_attn_*(q, caches..., ctx)     src/engine/patch_model.py:837-957
- * with the codes and the output bit-identical to kvq_quant_append then kvq_decode_attn.
+ * with the codes and the output bit-identical to kvq_quant_append then kvq_decode_attn,
+ * except that for the per-token, KIVI and mixed row formats (the writer runs the row
+ * quantizer) a writer holding at least kShed + 3 tiles of the split (1 + 3 tiles, with the
+ * INT4 group rescue 3 + 3) hands its first kShed tiles to waves of other SIMDs: the codes
+ * stay bit-identical and the output then agrees within the attention's stated tolerance.
  * Supported for the formats the tiled kernel serves (see kvq_decode_attn), with k_new /
  * v_new of seq_new 1 sharing write_pos and naming the very code buffers and strides p
  * reads:
