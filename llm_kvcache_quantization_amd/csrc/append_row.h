@@ -159,6 +159,20 @@ __device__ inline float group_quantile(float a0, float a1, int gs, float q, int 
   return quantile_lerp(vlo, vhi, rank - (float)lo);
 }
 
+// group_max for values >= +0 (absolute values: the order of the maxima cannot change a bit)
+// with DPP instead of the LDS crossbar: xor 1 and 2 within the quad, then the half-row and
+// row mirrors (lane i with 7 - i, 15 - i), which pair lanes of the two already reduced halves
+__device__ __forceinline__ float group_absmax(float v, int gs) {
+#pragma clang fp contract(off)
+  v = fmaxf(v, dppf<0xB1>(v));                       // quad_perm [1, 0, 3, 2]
+  if (gs >= 8) v = fmaxf(v, dppf<0x4E>(v));          // quad_perm [2, 3, 0, 1]
+  if (gs >= 16) v = fmaxf(v, dppf<0x141>(v));        // row_half_mirror
+  if (gs >= 32) v = fmaxf(v, dppf<0x140>(v));        // row_mirror
+  if (gs >= 64) v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if (gs >= 128) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
 // Scale of group g for a row, before the per-format final clamp.
 //  dyn_abs: absmax of the group's fp16 values (as float)
 //  stv: the static scale of the group (ld_static)
@@ -207,6 +221,22 @@ __device__ __forceinline__ half2v load_x(const AppendDev& a, int row, int lane) 
   return *reinterpret_cast<const half2v*>(row_x(a, row) + 2 * lane);
 }
 
+// The static scale of the lane's group in append row `row` as its raw bits (fp32, or fp16 in
+// the low half; 0 without a static table), and their value.  The fused step's writer requests
+// the bits at the start of the kernel and converts them where it quantizes: converting at the
+// load (one branch per table dtype) made the compiler wait for every outstanding load there,
+// the q loads and the first cache tiles included.
+__device__ __forceinline__ uint32_t row_static_bits(const AppendDev& a, int row, int lane) {
+  if (a.st == nullptr || a.fmt == KVQ_FMT_INT4_ASYM || a.fmt == KVQ_FMT_INT4_KIVI ||
+      a.fmt == KVQ_FMT_INT8_KIVI)
+    return 0u;
+  const int64_t off = (int64_t)((row / a.S) % a.H) * a.st_sh + (int64_t)((2 * lane) / a.gs) * a.st_sg;
+  return a.st_f32 ? reinterpret_cast<const uint32_t*>(a.st)[off]
+                  : (uint32_t)reinterpret_cast<const uint16_t*>(a.st)[off];
+}
+__device__ __forceinline__ float static_value(const AppendDev& a, uint32_t bits) {
+  return a.st_f32 ? __builtin_bit_cast(float, bits) : (float)__builtin_bit_cast(half_t, (uint16_t)bits);
+}
 // the static scale of the lane's group in append row `row` (0 without a static table)
 __device__ __forceinline__ float row_static(const AppendDev& a, int row, int lane) {
 #pragma clang fp contract(off)
@@ -240,7 +270,7 @@ __device__ __forceinline__ void quant_row_bhs(const AppendDev& a, int b, int h, 
   const bool pct = a.st == nullptr && a.dq > 0.f &&
                    (fmt == KVQ_FMT_INT8_SYM || fmt == KVQ_FMT_INT4_SYM);
   const float am = pct ? group_quantile(fabsf(x0), fabsf(x1), a.gs, a.dq, lane)
-                       : group_max(fmaxf(fabsf(x0), fabsf(x1)), a.gs);
+                       : group_absmax(fmaxf(fabsf(x0), fabsf(x1)), a.gs);
   uint8_t* crow = a.codes + (int64_t)b * a.csb + (int64_t)h * a.csh + t * a.cst;
   int clipped = 0;
 
@@ -341,8 +371,9 @@ __device__ __forceinline__ void quant_row_bhs(const AppendDev& a, int b, int h, 
     }
   }
   // clipped-element count (int8_cache.py:407-419, int4_cache.py:468-485)
-  for (int o = 32; o > 0; o >>= 1) clipped += __shfl_xor(clipped, o, 64);
-  if (lane == 0 && a.status && clipped) atomicAdd(&a.status[1], clipped);
+  // (each lane clips 0, 1 or 2 values: two ballots count them on the scalar unit)
+  const int nclip = __builtin_popcountll(__ballot(clipped & 1)) + 2 * __builtin_popcountll(__ballot(clipped & 2));
+  if (lane == 0 && a.status && nclip) atomicAdd(&a.status[1], nclip);
 }
 
 template <int FMT = -1>
@@ -353,19 +384,6 @@ __device__ __forceinline__ void quant_row_x(const AppendDev& a, int row, int lan
   quant_row_bhs<FMT>(a, bh / a.H, bh % a.H, s_idx, row, lane, thr, xv, stv);
 }
 
-// group_max for values >= +0 (absolute values: the order of the maxima cannot change a bit)
-// with DPP instead of the LDS crossbar: xor 1 and 2 within the quad, then the half-row and
-// row mirrors (lane i with 7 - i, 15 - i), which pair lanes of the two already reduced halves
-__device__ __forceinline__ float group_absmax(float v, int gs) {
-#pragma clang fp contract(off)
-  v = fmaxf(v, dppf<0xB1>(v));                       // quad_perm [1, 0, 3, 2]
-  if (gs >= 8) v = fmaxf(v, dppf<0x4E>(v));          // quad_perm [2, 3, 0, 1]
-  if (gs >= 16) v = fmaxf(v, dppf<0x141>(v));        // row_half_mirror
-  if (gs >= 32) v = fmaxf(v, dppf<0x140>(v));        // row_mirror
-  if (gs >= 64) v = fmaxf(v, __shfl_xor(v, 16, 64));
-  if (gs >= 128) v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
-}
 
 // lds_top_quantile by one wave alone, without barriers: lane l holds the scales v[l + 64 r]
 // (r < R, n <= 64 R) in registers; the maximum of each step is a DPP wave reduction and its

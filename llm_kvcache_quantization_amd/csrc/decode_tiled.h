@@ -2092,15 +2092,15 @@ __device__ __forceinline__ bool rescue_side(const AppendDev& d) {
 // their static scales, and with the group rescue every new row of the append.
 struct RowPre {
   half2v k, v;
-  float sk, sv;
+  uint32_t sk, sv;  // the static scales' bits (row_static_bits)
 };
 __device__ __forceinline__ void append_row_fetch(const DecodeArgs& a, int b, int hkv, int lane,
                                                  RowPre& p) {
   const int row = b * a.ark.H + hkv;
   p.k = load_x(a.ark, row, lane);
-  p.sk = row_static(a.ark, row, lane);
+  p.sk = row_static_bits(a.ark, row, lane);
   p.v = load_x(a.arv, row, lane);
-  p.sv = row_static(a.arv, row, lane);
+  p.sv = row_static_bits(a.arv, row, lane);
 }
 // (the rescue is compiled only where it can occur: INT4_SYM K and V, RESCUE)
 // KFMT / VFMT: the sides' formats (the kernel's operand types; the host admits only appends
@@ -2117,12 +2117,12 @@ __device__ __forceinline__ void append_row_pair(const DecodeArgs& a, int b, int 
     // V side's writes cannot pass the K side's reads)
     __shared__ float rdyn_k[kRescueRows * 8], rdyn_v[kRescueRows * 8];
     if (rescue_side(a.ark)) tk = rescue_thr_rows(a.ark, lane, rk, rdyn_k);
-    quant_row_bhs<KFMT>(a.ark, b, hkv, 0, row, lane, tk, p.k, p.sk);
+    quant_row_bhs<KFMT>(a.ark, b, hkv, 0, row, lane, tk, p.k, static_value(a.ark, p.sk));
     if (rescue_side(a.arv)) tv = rescue_thr_rows(a.arv, lane, rv, rdyn_v);
   } else {
-    quant_row_bhs<KFMT>(a.ark, b, hkv, 0, row, lane, tk, p.k, p.sk);
+    quant_row_bhs<KFMT>(a.ark, b, hkv, 0, row, lane, tk, p.k, static_value(a.ark, p.sk));
   }
-  quant_row_bhs<VFMT>(a.arv, b, hkv, 0, row, lane, tv, p.v, p.sv);
+  quant_row_bhs<VFMT>(a.arv, b, hkv, 0, row, lane, tv, p.v, static_value(a.arv, p.sv));
 }
 
 __device__ __forceinline__ void append_status(const FusedAppend& f, const AppendFlags& fl) {
@@ -2522,7 +2522,19 @@ void decode_tiled_kernel(DecodeArgs a) {
   // (wt past the context: the wave may have fewer steps than store_step; the row formats'
   // writer always stores here, outside the loop)
   const bool store_now = late_write && (KF::kAppendRow || wt >= ntot || store_step <= 0);
-  if (store_now) app_store();
+  if (store_now) {
+    // with the group rescue the writer's append is a long serial chain (two threshold walks
+    // and two row quantizations, about 14 us); at raised priority its SIMD partner, running
+    // its loop meanwhile, cannot take its issue slots (int4_fused 39.2 -> 38.4 us per
+    // layer-step at config 3's shape; without the rescue the raise cost 0.3 us)
+    constexpr bool kLong = [] {
+      if constexpr (KF::kAppendRow) return KF::kRescue;
+      else return false;
+    }();
+    if constexpr (kLong) __builtin_amdgcn_s_setprio(3);
+    app_store();
+    if constexpr (kLong) __builtin_amdgcn_s_setprio(0);
+  }
 
   float4v acc[8];
 #pragma unroll
