@@ -528,9 +528,9 @@ def test_decode_per_token_scales_tiled(bits, G, B, Hq, Hkv, S, ctx, static):
     out = plan.launch().clone()
     assert torch.equal(out, plan.launch()), "repeated launches differ"
     assert_close(out, ref, f"per-token int{bits} G{G} B{B} Hq{Hq} Hkv{Hkv} S{S} static={static}")
-    if bits == 4 and not static:
+    if not static:
         # the same V scales in rows padded to G + 4 values (not dense): the kernel then gathers
-        # the V operands with per-lane dword loads instead of 16-byte loads through LDS; the
+        # the V operands with per-lane loads instead of 16-byte loads through LDS; the
         # operands, and so the bits, are the same
         vpad = torch.full((B, Hkv, S, G + 4), float("nan"), dtype=sdt, device=DEV)
         vpad[..., :G] = vsd
