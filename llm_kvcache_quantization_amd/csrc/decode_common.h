@@ -119,8 +119,14 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t x, half_t off, uint32_t s2
   const half2v o = {off, off};
   return as_u32((as_h2(x) - o) * as_h2(s2));
 }
+// b * sb + h * sh for b, h >= 0 (a (b, head) slab's offset): zero-extended 32 x 64-bit
+// products, three scalar multiplies each where the sign-extended form takes four and a shift
+// (the same bits for b, h >= 0, whatever the strides' signs)
+__device__ __forceinline__ int64_t slab_off(int64_t sb, int64_t sh, int b, int h) {
+  return (int64_t)((uint64_t)(uint32_t)b * (uint64_t)sb + (uint64_t)(uint32_t)h * (uint64_t)sh);
+}
 __device__ __forceinline__ const half_t* q_row(const DecodeArgs& a, int b, int hq) {
-  return a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh;
+  return a.q + slab_off(a.q_sb, a.q_sh, b, hq);
 }
 // q'[32 lg + i] for i < 32 (the lane group's quantisation group) with four 16-byte
 // loads issued together; q' = fp16(q * inv_tau) when inv_tau is given

@@ -185,7 +185,7 @@ __device__ __forceinline__ void residual_partial(const DecodeArgs& a, int b, int
   const half_t tau = has_tau ? a.inv_tau[hq] : (half_t)1.0f;
   const half2v q2 = *reinterpret_cast<const half2v*>(q_row(a, b, hq) + 2 * lane);
   const float q0 = (float)qscale(q2.x, tau, has_tau), q1 = (float)qscale(q2.y, tau, has_tau);
-  const int64_t off = (int64_t)b * a.rsb + (int64_t)hkv * a.rsh + 2 * lane;
+  const int64_t off = slab_off(a.rsb, a.rsh, b, hkv) + 2 * lane;
   const half_t* kr = a.res_k + off;
   const half_t* vr = a.res_v + off;
   constexpr int kRB = 16;
@@ -476,11 +476,11 @@ struct KAsymT {
   __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
     olo = lg < 2;
-    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    const uint8_t* kb = a.k.codes + slab_off(a.k.sb, a.k.sh, b, hkv);
     rk = buffer_rsrc(kb, (uint32_t)(a.cap * kRowK));
     vk = (uint32_t)(col * kRowK + 16 * lg);
     if constexpr (OUT) {
-      const half_t* ob = a.k.oval + (int64_t)b * a.k.osb + (int64_t)hkv * a.k.osh;
+      const half_t* ob = a.k.oval + slab_off(a.k.osb, a.k.osh, b, hkv);
       ro = buffer_rsrc(ob, (uint32_t)(a.cap * kRowO));
       vo = (uint32_t)((16 * (lg >> 1) + col) * kRowO + (lg & 1) * 4);
     }
@@ -630,7 +630,7 @@ struct VAsymT {
   }
 
   __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
-    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    const uint8_t* vb = a.v.codes + slab_off(a.v.sb, a.v.sh, b, hkv);
     rv = buffer_rsrc(vb, (uint32_t)(((a.cap + kTile - 1) / kTile) * kTile * (kD / 2)));
     vv = (uint32_t)lane * 32u;
   }
@@ -731,7 +731,7 @@ struct KI8T {
 
   __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    const uint8_t* kb = a.k.codes + slab_off(a.k.sb, a.k.sh, b, hkv);
     rk = buffer_rsrc(kb, (uint32_t)(a.cap * kD));
     vk = (uint32_t)(col * kD + 32 * lg);
     sf32 = a.k.scale_f32;
@@ -844,7 +844,7 @@ struct VI8RowT {
   }
   __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    const uint8_t* vb = a.v.codes + slab_off(a.v.sb, a.v.sh, b, hkv);
     rv = buffer_rsrc(vb, (uint32_t)(a.cap * kD));
     vv = (uint32_t)((4 * lg) * kD + 8 * col);
     sbits = static_scale_bits(a.v, hkv, GS_ANY ? (8 * col) >> __builtin_ctz((unsigned)a.gs) : col >> 2);
@@ -922,7 +922,7 @@ struct KKiviT : KAsymT<false> {
     in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
     in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
     in.oc = int4{-1, -1, -1, -1};
-    const int64_t o = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh + 32 * lg + 8 * (wave & 3);
+    const int64_t o = slab_off(a.k.ssb, a.k.ssh, b, hkv) + 32 * lg + 8 * (wave & 3);
     const float* ps = reinterpret_cast<const float*>(a.k.scale) + o;
     const float* pz = reinterpret_cast<const float*>(a.k.zp) + o;
     in.ks[0] = *reinterpret_cast<const float4v*>(ps);
@@ -1006,7 +1006,7 @@ struct KTokAsymT : KAsymT<false> {
   };
   __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
     KAsymT<false>::setup_addr(a, b, hkv, lane);
-    const int64_t o = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh;
+    const int64_t o = slab_off(a.k.ssb, a.k.ssh, b, hkv);
     rs = buffer_rsrc(reinterpret_cast<const float*>(a.k.scale) + o, (uint32_t)(a.cap * 4));
     rz = buffer_rsrc(reinterpret_cast<const float*>(a.k.zp) + o, (uint32_t)(a.cap * 4));
     vs = (uint32_t)(4 * (lane & 15));
@@ -1156,10 +1156,10 @@ struct VKiviRowTT {
   }
   __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    const uint8_t* vb = a.v.codes + slab_off(a.v.sb, a.v.sh, b, hkv);
     rv = buffer_rsrc(vb, (uint32_t)(a.cap * (kD / 2)));
     vv = (uint32_t)((4 * lg) * (kD / 2) + 4 * col);
-    const int64_t po = (int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh;
+    const int64_t po = slab_off(a.v.ssb, a.v.ssh, b, hkv);
     rs = buffer_rsrc(reinterpret_cast<const float*>(a.v.scale) + po, (uint32_t)(a.cap * 4));
     rz = buffer_rsrc(reinterpret_cast<const float*>(a.v.zp) + po, (uint32_t)(a.cap * 4));
     vp = (uint32_t)(4 * lg) * 4u;
@@ -1313,7 +1313,7 @@ struct KKivi8T {
   };
   __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    const uint8_t* kb = a.k.codes + slab_off(a.k.sb, a.k.sh, b, hkv);
     rk = buffer_rsrc(kb, (uint32_t)(a.cap * kD));
     vk = (uint32_t)(col * kD + 32 * lg);
   }
@@ -1323,7 +1323,7 @@ struct KKivi8T {
     in.q = *reinterpret_cast<const u32x4*>(q_row(a, b, hq) + 32 * lg + 8 * (wave & 3));
     in.tau = a.inv_tau != nullptr ? a.inv_tau[hq] : (half_t)1.0f;
     in.oc = int4{-1, -1, -1, -1};
-    const int64_t o = (int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh + 32 * lg + 8 * (wave & 3);
+    const int64_t o = slab_off(a.k.ssb, a.k.ssh, b, hkv) + 32 * lg + 8 * (wave & 3);
     const float* ps = reinterpret_cast<const float*>(a.k.scale) + o;
     const float* pz = reinterpret_cast<const float*>(a.k.zp) + o;
     in.ks[0] = *reinterpret_cast<const float4v*>(ps);
@@ -1416,7 +1416,7 @@ struct KF16T {
   };
   __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    const uint8_t* kb = a.k.codes + slab_off(a.k.sb, a.k.sh, b, hkv);
     rk = buffer_rsrc(kb, (uint32_t)(a.cap * kRow));
     vk = (uint32_t)(col * kRow + 64 * lg);
   }
@@ -1498,10 +1498,10 @@ struct VKivi8RowT {
   }
   __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    const uint8_t* vb = a.v.codes + slab_off(a.v.sb, a.v.sh, b, hkv);
     rv = buffer_rsrc(vb, (uint32_t)(a.cap * kD));
     vv = (uint32_t)((4 * lg) * kD + 8 * col);
-    const int64_t po = (int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh;
+    const int64_t po = slab_off(a.v.ssb, a.v.ssh, b, hkv);
     rs = buffer_rsrc(reinterpret_cast<const float*>(a.v.scale) + po, (uint32_t)(a.cap * 4));
     rz = buffer_rsrc(reinterpret_cast<const float*>(a.v.zp) + po, (uint32_t)(a.cap * 4));
     vp = (uint32_t)(4 * lg) * 4u;
@@ -1621,7 +1621,7 @@ struct VF16RowT {
   }
   __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    const uint8_t* vb = a.v.codes + slab_off(a.v.sb, a.v.sh, b, hkv);
     rv = buffer_rsrc(vb, (uint32_t)(a.cap * kRow));
     vv = (uint32_t)((4 * lg) * kRow + 16 * col);
   }
@@ -1695,13 +1695,13 @@ struct KTokT {
 
   __device__ void setup_addr(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* kb = a.k.codes + (int64_t)b * a.k.sb + (int64_t)hkv * a.k.sh;
+    const uint8_t* kb = a.k.codes + slab_off(a.k.sb, a.k.sh, b, hkv);
     rk = buffer_rsrc(kb, (uint32_t)(a.cap * kRow));
     vk = (uint32_t)(col * kRow + (kRow / 4) * lg);
     // the lane's first group: 32 lg / gs; with NS = 2 the next one follows (stride_g = 1)
     const int g0 = (32 * lg) >> __builtin_ctz((unsigned)a.gs);
     const char* sb = reinterpret_cast<const char*>(a.k.scale) +
-                     ((int64_t)b * a.k.ssb + (int64_t)hkv * a.k.ssh) * kEs;
+                     slab_off(a.k.ssb, a.k.ssh, b, hkv) * kEs;
     sst = (uint32_t)(a.k.sst * kEs);
     rs = buffer_rsrc(sb, scale_bytes(a.cap, a.k.sst, a.gs, kEs));
     vs = (uint32_t)(col * sst + g0 * a.k.ssg * kEs);
@@ -1854,12 +1854,12 @@ struct VTokT {
   }
   __device__ void setup(const DecodeArgs& a, int b, int hkv, int lane) {
     const int col = lane & 15, lg = lane >> 4;
-    const uint8_t* vb = a.v.codes + (int64_t)b * a.v.sb + (int64_t)hkv * a.v.sh;
+    const uint8_t* vb = a.v.codes + slab_off(a.v.sb, a.v.sh, b, hkv);
     rv = buffer_rsrc(vb, (uint32_t)(a.cap * kRow));
     vv = (uint32_t)((4 * lg) * kRow + (I4 ? 4 : 8) * col);
     const int gi = (8 * col) >> __builtin_ctz((unsigned)a.vgs);
     const char* sb = reinterpret_cast<const char*>(a.v.scale) +
-                     ((int64_t)b * a.v.ssb + (int64_t)hkv * a.v.ssh) * kEs;
+                     slab_off(a.v.ssb, a.v.ssh, b, hkv) * kEs;
     sst = (uint32_t)(a.v.sst * kEs);
     rs = buffer_rsrc(sb, scale_bytes(a.cap, a.v.sst, a.vgs, kEs));
     vs = (uint32_t)((4 * lg) * sst + gi * a.v.ssg * kEs);
@@ -2019,8 +2019,8 @@ template <class KF, class VF>
 __device__ __forceinline__ void append_fetch(const DecodeArgs& a, int b, int hkv, int lane,
                                              int4 oc, AppendIn& in) {
   const FusedAppend& f = a.app;
-  const half_t* xk = f.kx + (int64_t)b * f.ksb + (int64_t)hkv * f.ksh;
-  const half_t* xv = f.vx + (int64_t)b * f.vsb + (int64_t)hkv * f.vsh;
+  const half_t* xk = f.kx + slab_off(f.ksb, f.ksh, b, hkv);
+  const half_t* xv = f.vx + slab_off(f.vsb, f.vsh, b, hkv);
   const rsrc_t rk = buffer_rsrc(xk, kD * 2), rv = buffer_rsrc(xv, kD * 2);
   in.k2 = bload1(rk, 4u * lane, 0);
   in.v2 = bload1(rv, 4u * lane, 0);
