@@ -2271,14 +2271,17 @@ void decode_tiled_kernel(DecodeArgs a) {
   // One field of each kernel-argument line the prologue reads, so that the first batch of
   // scalar loads fetches every such line: a line first touched later costs one more round
   // trip before the first cache load (measured 0.15-0.25 us per launch).  The row formats'
-  // prologue reads most of the arguments (the append's two row sides): one dword of every
-  // 64-byte line (it touched about 20 lines one after another, 2 us per launch); so does the
-  // shared split, whose prologue reads the split's fields before the cache descriptors (1.1
-  // us per launch at config 4); the others read four lines (touching all costs them 0.2 us).
+  // prologue reads most of the arguments: one dword of every 64-byte line up to the append's
+  // two row sides (it touched about 20 lines one after another, 2 us per launch); so does
+  // the shared split, whose prologue reads the split's fields before the cache descriptors
+  // (1.1 us per launch at config 4); the others read four lines (touching all costs them
+  // 0.2 us).  The row sides (ark, arv) are read by the writer wave alone, where it uses
+  // them (touching their lines in every wave cost the shared split 0.27 us per launch).
   if constexpr (KF::kAppendRow || SHARE) {
     const uint32_t* w = reinterpret_cast<const uint32_t*>(&a);
 #pragma unroll
-    for (int i = 0; i < (int)(sizeof(DecodeArgs) / 4); i += 16) asm volatile("" ::"s"(w[i]));
+    for (int i = 0; i < (int)(__builtin_offsetof(DecodeArgs, ark) / 4); i += 16)
+      asm volatile("" ::"s"(w[i]));
   } else {
     asm volatile("" ::"s"(a.v.scale), "s"(a.ctx), "s"(a.app.kx), "s"(a.app.wpos));
   }
