@@ -2276,12 +2276,20 @@ void decode_tiled_kernel(DecodeArgs a) {
   // the shared split, whose prologue reads the split's fields before the cache descriptors
   // (1.1 us per launch at config 4); the others read four lines (touching all costs them
   // 0.2 us).  The row sides (ark, arv) are read by the writer wave alone, where it uses
-  // them (touching their lines in every wave cost the shared split 0.27 us per launch).
-  if constexpr (KF::kAppendRow || SHARE) {
+  // them (touching their lines in every wave cost the shared split 0.27 us per launch); the
+  // shared split of the other formats touches the lines before the append's and the
+  // append's first (0.15 us per launch against every line up to the row sides).
+  if constexpr (KF::kAppendRow) {
     const uint32_t* w = reinterpret_cast<const uint32_t*>(&a);
 #pragma unroll
     for (int i = 0; i < (int)(__builtin_offsetof(DecodeArgs, ark) / 4); i += 16)
       asm volatile("" ::"s"(w[i]));
+  } else if constexpr (SHARE) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&a);
+#pragma unroll
+    for (int i = 0; i < (int)(__builtin_offsetof(DecodeArgs, app) / 4); i += 16)
+      asm volatile("" ::"s"(w[i]));
+    asm volatile("" ::"s"(a.app.kx), "s"(a.app.wpos));
   } else {
     asm volatile("" ::"s"(a.v.scale), "s"(a.ctx), "s"(a.app.kx), "s"(a.app.wpos));
   }
