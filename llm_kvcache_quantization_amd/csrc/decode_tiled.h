@@ -2259,6 +2259,25 @@ __device__ WgRows share_waves(const DecodeArgs& a, int lin) {
   return wr;
 }
 
+// merge_chunks with the batch cut to 8 partials when the unit has at most 8: the loads of a
+// larger batch past the unit's partials read nothing (out of range) but are not free (a
+// 32-partial batch cost the static-INT8-K kernels 1.3 us per launch at 8 chunks per (b, kv
+// head)); the 8-partial round is the same arithmetic in the same chunk order, so the same bits.
+// The static INT8 pair with group-32 rows keeps the one 32-partial path: its launches split a
+// context into many chunks (32 at config 1), and a second path changed its code and cost it
+// 0.13 us.  Call sites take merge_chunks_n only where kMergeSplit8 holds.
+template <class KF, class VF>
+constexpr bool kMergeSplit8 = KF::kMergeBatch > 8 &&
+                              !(std::is_same_v<KF, KI8T<false>> && std::is_same_v<VF, VI8RowT<false>>);
+template <class KF, class VF>
+__device__ __forceinline__ void merge_chunks_n(const DecodeArgs& a, int b, int hkv, int nvalid,
+                                               int wave, int lane) {
+  if (nvalid <= 8)
+    merge_chunks<VF, 8>(a, b, hkv, nvalid, wave, lane);
+  else
+    merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, nvalid, wave, lane);
+}
+
 // SHARE: the instantiation for the shared split (a.share); the other one carries none of
 // its code (it cost the grid split 0.2 us per launch at the headline shape).
 // V operand types that pass their tiles through LDS (VTokT<true, true>) have kStage
@@ -2313,7 +2332,8 @@ void decode_tiled_kernel(DecodeArgs a) {
       for (uint64_t e = wr.empty; e != 0; e &= e - 1) {
         const int rb = __builtin_amdgcn_readfirstlane(__builtin_ctzll(e));
         if (VF::kResidual && a.res_n > 0) {
-          merge_chunks<VF, KF::kMergeBatch>(a, rb, eh, 0, wave, lane);
+          if constexpr (kMergeSplit8<KF, VF>) merge_chunks_n<KF, VF>(a, rb, eh, 0, wave, lane);
+          else merge_chunks<VF, KF::kMergeBatch>(a, rb, eh, 0, wave, lane);
         } else {
           for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
             a.out[(int64_t)rb * a.o_sb + (int64_t)(eh * a.n_rep + (idx >> 7)) * a.o_sh +
@@ -2505,7 +2525,8 @@ void decode_tiled_kernel(DecodeArgs a) {
     }
     if (!SHARE && ntot == 0 && wr.v0 == 0 && a.fused) {
       if (VF::kResidual && a.res_n > 0) {  // empty quantized context: the residual window alone
-        merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, 0, wave, lane);
+        if constexpr (kMergeSplit8<KF, VF>) merge_chunks_n<KF, VF>(a, b, hkv, 0, wave, lane);
+        else merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, 0, wave, lane);
       } else {  // empty context: zero rows
         for (int idx = threadIdx.x; idx < a.n_rep * kD; idx += kTW * 64)
           a.out[(int64_t)b * a.o_sb + (int64_t)(hkv * a.n_rep + (idx >> 7)) * a.o_sh +
@@ -2624,7 +2645,8 @@ void decode_tiled_kernel(DecodeArgs a) {
                    (uint32_t)(nvalid - 1);
     __syncthreads();
     if (!is_last[0]) return;
-    merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, nvalid, wave, lane);
+    if constexpr (kMergeSplit8<KF, VF>) merge_chunks_n<KF, VF>(a, b, hkv, nvalid, wave, lane);
+    else merge_chunks<VF, KF::kMergeBatch>(a, b, hkv, nvalid, wave, lane);
     if (threadIdx.x == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
@@ -2654,8 +2676,13 @@ void decode_tiled_kernel(DecodeArgs a) {
   const int l0 = sgv(is_last[0]), l1 = sgv(is_last[1]);
   if (!l0 && !l1) return;
   constexpr int kB = KF::kMergeBatch < 16 ? KF::kMergeBatch : 16;
-  merge_rows<VF, kB>(a, hkv, sgv(seg.b[l0 ? 0 : 1]), sgv(seg.n[l0 ? 0 : 1]), sgv(seg.b[1]),
-                     sgv(seg.n[1]), l0 && l1 ? 2 : 1, wave, lane);
+  const int mb0 = sgv(seg.b[l0 ? 0 : 1]), mn0 = sgv(seg.n[l0 ? 0 : 1]), mn1 = sgv(seg.n[1]);
+  const int nr = l0 && l1 ? 2 : 1;
+  // (at most 8 partials per merged row: rounds of 8, as merge_chunks_n)
+  if (kMergeSplit8<KF, VF> && kB > 8 && mn0 <= 8 && (nr == 1 || mn1 <= 8))
+    merge_rows<VF, (kB > 8 ? 8 : kB)>(a, hkv, mb0, mn0, sgv(seg.b[1]), mn1, nr, wave, lane);
+  else
+    merge_rows<VF, kB>(a, hkv, mb0, mn0, sgv(seg.b[1]), mn1, nr, wave, lane);
 }
 
 template <class KF, class VF, bool PACK8, bool SHARE, int LOOK = 1>
